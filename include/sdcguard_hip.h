@@ -1,0 +1,76 @@
+/* sdcguard_hip.h -- C ABI of libsdcguard_hip.so, the MI355X (gfx950) verification hot path of sdcguard.
+ *
+ * Plain pointers (device memory), element strides, sizes and a hipStream_t; no torch types.  Every entry
+ * point queues work on `stream` and returns at once (no host synchronisation), returning 0 on success or a
+ * negative status:
+ *   -1 SDC_EINVAL       an argument is out of range (shape, stride, null pointer)
+ *   -2 SDC_EUNSUPPORTED a case this library does not implement; the caller must not treat it as checked
+ *   -3 SDC_EWORKSPACE   the workspace is smaller than the matching *_workspace() call asked for
+ *   -4 SDC_ELAUNCH      a HIP launch error
+ * dtype: 0 = bf16, 1 = fp16.  Integer results wrap modulo 2^64 like the reference's int64 arithmetic.
+ */
+#ifndef SDCGUARD_HIP_H
+#define SDCGUARD_HIP_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- serving check of one linear layer --------------------------------------------------------------------
+ * Replaces the custom op sdcguard::check_static (serve.py:465-489) and what it runs: _serve_fast.check
+ * (_serve_fast.py:632) = check_v1/check_v3 (:265-313, :539-587), i.e. E = x @ parts then the block sums of y and
+ * the scoring of _check/_judge/_report (:102-262, :334-452); same arithmetic as serve._check_static_impl
+ * (serve.py:301-396).
+ *   x (m x k), y (m x n): element strides (sxm, sxk), (sym, syn); both of `dtype`.
+ *   parts: the three low-precision parts of the layer's block sums B2 / scale (k x 6nb, LayerChecksums.parts,
+ *     serve.py:186), element (kk, c) at parts[kk * spk + c * spc]; spk must be 1 (k-contiguous columns).
+ *     nparts must be 3.
+ *   sign_table: 128 x 128 fp32, row w-1 = the epoch-0 +-1 pattern of width w (_group.py:262-291).
+ *   scale, b2n, b2max, bsum: (nb, 2) fp32; bmax, bmax_bias: (nb,) fp32 (LayerChecksums.tensors()).
+ *   state: the layer's row of the guard's state (int64): keys at [0], [1]; with counts != 0, checks executed
+ *     at [2] and unjudged checksums at [3] (serve.py:55-65).  slot: the layer's slot (capture flag index).
+ *   cap_meta / cap_data (may be NULL): the capture buffers of serve.py:67-88; cap_flags = CAP_FLAGS,
+ *     cap_slots = CAPTURE_SLOTS, cap_stride = cap_data's row stride, cap_w = where x starts in a row.
+ *   workspace: device memory of at least sdc_check_static_workspace(m, k, n, bs) bytes.
+ *   scores_out (may be NULL): every checksum's score, (m, nb, 2) fp32, plain then signed (for tests). */
+int64_t sdc_check_static_workspace(int64_t m, int64_t k, int64_t n, int64_t bs);
+int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t sxk, const void* y, int64_t sym, int64_t syn,
+                     int64_t m, int64_t k, int64_t n, int64_t bs, const void* parts, int64_t spk, int64_t spc,
+                     int nparts, const float* sign_table, const float* scale, const float* b2n,
+                     const float* b2max, const float* bmax, const float* bmax_bias, const float* bsum,
+                     int64_t* state, int counts, int64_t slot, float z, float abs_floor, int64_t* cap_meta,
+                     float* cap_data, int64_t cap_stride, int64_t cap_w, int64_t cap_tag, int64_t cap_flags,
+                     int64_t cap_slots, void* workspace, int64_t workspace_bytes, float* scores_out,
+                     hipStream_t stream);
+
+/* Depth split the expected-side GEMM uses for an (m x k) @ (k x ncols) product (sizes the workspace). */
+int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
+
+/* ---- integer fingerprints --------------------------------------------------------------------------------
+ * sdc_fingerprint3: out[0..2] += recompute.fingerprint's three sums (recompute.py:72-116; the Triton kernel
+ *   _fingerprint.py:51-65 / fingerprint_bits :128-130) of n words of word_bytes (2: int16, 1: int8) bytes,
+ *   word positions numbered from `start`.  out must be zeroed by the caller for a fresh fingerprint.
+ * sdc_fingerprint2: out[0..1] += serve_weights.fingerprint's two sums (serve_weights.py:172-185; kernel
+ *   :194-204) of n words; kind 0 = int16, 1 = int32, 2 = uint8 (serve_weights._int_view :151-161). */
+int sdc_fingerprint3(const void* bits, int64_t n, int word_bytes, int64_t start, int64_t* out, hipStream_t stream);
+int sdc_fingerprint2(const void* bits, int64_t n, int kind, int64_t* out, hipStream_t stream);
+
+/* ---- per-kernel timing (no counterpart in the reference; for benchmarks) ------------------------------------
+ * With profiling on, every kernel launch is bracketed by two HIP events on its stream; sdc_profile_read waits for
+ * them and sums the durations of one kernel ("expected_gemm", "serve_score", "fingerprint3", ...). */
+int sdc_profile_enable(int on);
+int sdc_profile_reset(void);
+int sdc_profile_read(const char* name, double* total_ms, int64_t* launches);
+
+/* ---- self-tests ---------------------------------------------------------------------------------------------
+ * No counterpart in the reference: checks the MFMA operand layout the GEMM kernels assume.
+ * C (32 x 32 fp32) = A (32 x 16 bf16, row-major) @ B (16 x 32 bf16, column-major), one wave. */
+int sdc_mfma_layout_selftest(const void* A, const void* B, float* C, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SDCGUARD_HIP_H */

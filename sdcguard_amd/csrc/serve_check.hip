@@ -1,0 +1,322 @@
+// Serving check of one linear layer (the sdcguard::check_static op): y = x @ W^T (+ b), W's block sums known.
+//
+// Reference: serve.py:301-396 (`_check_static_impl`, the arithmetic and the state row), _serve_fast.py:102-262
+// (`_check`), :334-452 (`_judge`, `_report`: scoring order, Inf/NaN rules, unjudged counts, the capture of an
+// alarming row), :454-526 (`_sums`, `_score`).  Two launches:
+//   1. expected_gemm (expected_gemm.hip): E = x @ parts on MFMA, plus |x_row|_2^2 and |x_row|_1;
+//   2. serve_score (here): one pass over y.  A wave owns 64 (row, block) pairs; four lanes share a pair (each
+//      reads 4 x 16 bytes of the 256-byte block, in runs of 64 bytes), accumulate its four sums (plain, signed,
+//      of squares, of |values|) and add them up with two DPP steps; over four rounds each lane keeps one pair's
+//      sums, then scores it with the reference's noise model.  The workgroup's worst key goes into the layer's
+//      state row with one integer atomic maximum (only when it raises the row), counts with atomic adds.
+#include "common.h"
+#include "profile.h"
+
+int sdc_expected_launch(int dtype, const void* x, int64_t sxm, int64_t sxk, const void* parts, int64_t spk,
+                        int64_t spc, int nparts, int64_t m, int64_t k, int64_t ncols, int64_t splits, float* E,
+                        float* XN, hipStream_t stream);
+extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
+
+namespace {
+
+struct ScoreArgs {
+  const uint16_t* x; int64_t sxm, sxk;
+  const uint16_t* y; int64_t sym, syn;
+  int64_t m, k, n, nb, bs, rem, npairs;
+  const float* E; int64_t ncols; int64_t splits;
+  const float* XN;
+  const float* s_full; const float* s_last;       // sign patterns of widths bs and rem (rows of the table)
+  const float* scale; const float* b2n; const float* b2max; const float* bmax; const float* bmb; const float* bsum;
+  int64_t* state; int counts;
+  float u, h, abs_floor, l1c, zt, lim_a, lim_big, capk;
+  int64_t* capm; float* capd; int64_t cst, cw, ctag, cfo, ncap, slot;
+  int vec;
+  float* zdump;      // optional: every checksum's score, (m, nb, 2) fp32 (tests)
+};
+
+struct PairScore {
+  float z0, z1;
+  float zc, dc;
+  bool sec;
+  int unk;
+};
+
+// _serve_fast.py:334-402 (`_judge`) for one (row, block) pair, serving flavour (unjudged checksums score 0).
+__device__ __forceinline__ PairScore judge_serve(float plain, float sgn, float sq, float l1, float xn, float asum,
+                                                 float e0, float e1, float sc0, float sc1, float bs0, float bs1,
+                                                 float bmaxv, float bmbv, float b2n0, float b2n1, float b2m0,
+                                                 float b2m1, float wf, const ScoreArgs& a) {
+  const float inf = __builtin_inff();
+  const float nanv = __builtin_nanf("");
+  float exp0 = e0 * sc0 + bs0;
+  float exp1 = e1 * sc1 + bs1;
+  float bound = asum * bmaxv + bmbv;
+  float rsq = sqrtf(sq);
+  float noise = rsq * a.u;
+  float fl0 = xn * b2n0 * 1e-5f;
+  float fl1 = xn * b2n1 * 1e-5f;
+  float hl0 = asum * b2m0 * a.l1c;
+  float hl1 = asum * b2m1 * a.l1c;
+  fl0 = fminf(fabsf(fl0) < inf ? fl0 : inf, fabsf(hl0) < inf ? hl0 : inf);
+  fl1 = fminf(fabsf(fl1) < inf ? fl1 : inf, fabsf(hl1) < inf ? hl1 : inf);
+  const float bigfl = bound * (float)(1e-5 * 128.0);
+  fl0 = fl0 < inf ? fl0 : bigfl;
+  fl1 = fl1 < inf ? fl1 : bigfl;
+  float swf = sqrtf(wf);
+  float tail = a.abs_floor + swf * a.h;
+  float den0 = (noise + fl0) + tail;
+  float den1 = (noise + fl1) + tail;
+  float d0 = fabsf(exp0 - plain);
+  float d1 = fabsf(exp1 - sgn);
+  float z0 = d0 / den0;
+  float z1 = d1 / den1;
+  float worst = (l1 * (1.25f * a.u) + (1.25f * a.h * wf)) + fl0 + a.abs_floor;
+  float zw = d0 / worst * a.zt;
+  z0 = (z0 == z0 && zw == zw) ? fminf(z0, zw) : nanv;
+  float lim = bound * 1.01f;
+  bool nfin = !(noise < inf);
+  bool e_bad0 = !(fabsf(exp0) < inf);
+  bool a_bad0 = !e_bad0 && !(fabsf(plain) < inf);
+  bool big0 = nfin && !e_bad0 && !a_bad0;
+  bool nan0 = !(z0 == z0);
+  z0 = z0 == z0 ? z0 : 0.f;
+  z0 = e_bad0 ? 0.f : z0;
+  float cap = bound * a.capk + 2.0f * a.h;
+  bool imposs = !nfin && (lim < a.lim_big) && (rsq > cap * swf);
+  bool ok_a = lim < a.lim_a, ok_big = lim < a.lim_big;
+  z0 = (imposs && !e_bad0 && !a_bad0) ? inf : z0;
+  z0 = a_bad0 ? (ok_a ? inf : 0.f) : z0;
+  z0 = big0 ? (ok_big ? inf : 0.f) : z0;
+  bool e_bad1 = !(fabsf(exp1) < inf);
+  bool a_bad1 = !e_bad1 && !(fabsf(sgn) < inf);
+  bool big1 = nfin && !e_bad1 && !a_bad1;
+  bool nan1 = !(z1 == z1);
+  z1 = z1 == z1 ? z1 : 0.f;
+  z1 = e_bad1 ? 0.f : z1;
+  z1 = (imposs && !e_bad1 && !a_bad1) ? inf : z1;
+  z1 = a_bad1 ? (ok_a ? inf : 0.f) : z1;
+  z1 = big1 ? (ok_big ? inf : 0.f) : z1;
+  bool unk0 = (nan0 && !imposs && !a_bad0 && !big0) || e_bad0 || (a_bad0 && !ok_a) || (big0 && !ok_big);
+  bool unk1 = (nan1 && !imposs && !a_bad1 && !big1) || e_bad1 || (a_bad1 && !ok_a) || (big1 && !ok_big);
+  PairScore r;
+  r.z0 = z0;
+  r.z1 = z1;
+  r.sec = z1 > z0;
+  r.zc = r.sec ? z1 : z0;
+  r.dc = r.sec ? (a_bad1 ? nanv : den1) : (a_bad0 ? nanv : den0);
+  r.unk = (int)unk0 + (int)unk1;
+  return r;
+}
+
+template <int DT>
+__device__ __forceinline__ void acc8(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, const float* s, float& pl,
+                                     float& sg, float& sq, float& ab) {
+  float v[8] = {lo_of<DT>(w0), hi_of<DT>(w0), lo_of<DT>(w1), hi_of<DT>(w1),
+                lo_of<DT>(w2), hi_of<DT>(w2), lo_of<DT>(w3), hi_of<DT>(w3)};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    pl += v[e];
+    sg = fmaf(v[e], s[e], sg);
+    sq = fmaf(v[e], v[e], sq);
+    ab += fabsf(v[e]);
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void serve_score_kernel(ScoreArgs a) {
+  __shared__ int64_t red_k[4], red_d[4];
+  __shared__ int red_u[4];
+  __shared__ int64_t cap_slot;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, q = lane & 3;
+  const int64_t base = (int64_t)blockIdx.x * 256 + w * 64;
+
+  // this lane's 32 columns of a block: chunks q, q+4, q+8, q+12 of 8 columns
+  float sfull[32];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int c = 8 * (q + 4 * j) + e;
+      sfull[j * 8 + e] = c < a.bs ? a.s_full[c] : 0.f;
+    }
+
+  float my_pl = 0.f, my_sg = 0.f, my_sq = 0.f, my_ab = 0.f;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int64_t p = base + g * 16 + (lane >> 2);
+    float pl = 0.f, sg = 0.f, sq = 0.f, ab = 0.f;
+    if (p < a.npairs) {
+      const int64_t r = p / a.nb, jb = p - r * a.nb;
+      const bool last = (jb == a.nb - 1) && (a.rem > 0);
+      const int64_t wid = last ? a.rem : a.bs;
+      const uint16_t* yr = a.y + r * a.sym + jb * a.bs * a.syn;
+      if (a.vec && wid == 128) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          u32x4 v = *reinterpret_cast<const u32x4*>(yr + 8 * (q + 4 * j));
+          acc8<DT>(v.x, v.y, v.z, v.w, &sfull[j * 8], pl, sg, sq, ab);
+        }
+      } else {
+        const float* sp = last ? a.s_last : a.s_full;
+        for (int j = 0; j < 4; ++j)
+          for (int e = 0; e < 8; ++e) {
+            const int c = 8 * (q + 4 * j) + e;
+            if (c < wid) {
+              float v = half_to_f32<DT>(yr[c * a.syn]);
+              pl += v;
+              sg = fmaf(v, sp[c], sg);
+              sq = fmaf(v, v, sq);
+              ab += fabsf(v);
+            }
+          }
+      }
+    }
+    pl = quad_sum(pl); sg = quad_sum(sg); sq = quad_sum(sq); ab = quad_sum(ab);
+    if (q == g) { my_pl = pl; my_sg = sg; my_sq = sq; my_ab = ab; }
+  }
+
+  // score this lane's pair
+  const int64_t p = base + q * 16 + (lane >> 2);
+  int64_t key = 0, keyd = 0;
+  int unk = 0;
+  if (p < a.npairs) {
+    const int64_t r = p / a.nb, jb = p - r * a.nb;
+    const bool last = (jb == a.nb - 1) && (a.rem > 0);
+    const float wf = (float)(last ? a.rem : a.bs);
+    float e0 = 0.f, e1 = 0.f, asq = 0.f, asum = 0.f;
+    for (int64_t s = 0; s < a.splits; ++s) {
+      const float* Es = a.E + (s * a.m + r) * a.ncols + 2 * jb;
+      e0 += Es[0];
+      e1 += Es[1];
+      asq += a.XN[s * 2 * a.m + r];
+      asum += a.XN[s * 2 * a.m + a.m + r];
+    }
+    PairScore ps = judge_serve(my_pl, my_sg, my_sq, my_ab, sqrtf(asq), asum, e0, e1, a.scale[2 * jb],
+                               a.scale[2 * jb + 1], a.bsum[2 * jb], a.bsum[2 * jb + 1], a.bmax[jb], a.bmb[jb],
+                               a.b2n[2 * jb], a.b2n[2 * jb + 1], a.b2max[2 * jb], a.b2max[2 * jb + 1], wf, a);
+    if (a.zdump) {
+      a.zdump[2 * p] = ps.z0;
+      a.zdump[2 * p + 1] = ps.z1;
+    }
+    const int64_t zb = fbits64(fmaxf(ps.zc, 0.f));
+    const int64_t flat = p * 2 + (ps.sec ? 1 : 0);
+    key = (zb << 32) | (flat & 0xFFFFFFFFll);
+    keyd = (zb << 32) | (fbits64(ps.dc) & 0xFFFFFFFFll);
+    unk = ps.unk;
+  }
+  key = wave_max_i64(key);
+  keyd = wave_max_i64(keyd);
+  unk = wave_sum_i32(unk);
+  if (lane == 0) { red_k[w] = key; red_d[w] = keyd; red_u[w] = unk; }
+  __syncthreads();
+  int64_t* st = a.state;
+  if (t == 0) {
+    int64_t k0 = red_k[0], d0 = red_d[0];
+    int un = red_u[0];
+    for (int i = 1; i < 4; ++i) {
+      k0 = red_k[i] > k0 ? red_k[i] : k0;
+      d0 = red_d[i] > d0 ? red_d[i] : d0;
+      un += red_u[i];
+    }
+    red_k[0] = k0;
+    // most workgroups cannot raise the layer's worst score: read first, take the atomic only when it can
+    if (k0 > __atomic_load_n(st, __ATOMIC_RELAXED)) atomicMax((unsigned long long*)st, (unsigned long long)k0);
+    if (d0 > __atomic_load_n(st + 1, __ATOMIC_RELAXED)) atomicMax((unsigned long long*)(st + 1), (unsigned long long)d0);
+    if (a.counts) {
+      if (blockIdx.x == 0) atomicAdd((unsigned long long*)(st + 2), 1ull);
+      if (un > 0) atomicAdd((unsigned long long*)(st + 3), (unsigned long long)un);
+    }
+    cap_slot = -1;
+    if (a.capm) {
+      const int64_t zbits = k0 >> 32;
+      const float best = __uint_as_float((uint32_t)zbits);
+      if (best > a.zt) {
+        unsigned long long taken = atomicExch((unsigned long long*)(a.capm + a.cfo + a.slot), 1ull);
+        if (taken == 0) {
+          int64_t c = (int64_t)atomicAdd((unsigned long long*)a.capm, 1ull);
+          if (c < a.ncap) {
+            const int64_t best_i = k0 & 0xFFFFFFFFll;
+            const int64_t bi = best_i / 2, crow = bi / a.nb, cblk = bi % a.nb;
+            int64_t* rec = a.capm + 2 + c * 6;
+            rec[0] = a.ctag; rec[1] = crow; rec[2] = cblk; rec[3] = best_i; rec[4] = zbits;
+            rec[5] = __atomic_load_n(a.capm + 1, __ATOMIC_RELAXED);
+            cap_slot = c;
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (a.capm && cap_slot >= 0) {
+    const int64_t k0 = red_k[0];
+    const int64_t bi = (k0 & 0xFFFFFFFFll) / 2, crow = bi / a.nb, cblk = bi % a.nb;
+    const int64_t cwid = (cblk == a.nb - 1 && a.rem > 0) ? a.rem : a.bs;
+    float* dst = a.capd + cap_slot * a.cst;
+    for (int64_t i = t; i < cwid; i += 256) dst[i] = half_to_f32<DT>(a.y[crow * a.sym + (cblk * a.bs + i) * a.syn]);
+    for (int64_t i = t; i < a.k; i += 256) dst[a.cw + i] = half_to_f32<DT>(a.x[crow * a.sxm + i * a.sxk]);
+  }
+}
+
+}  // namespace
+
+extern "C" int64_t sdc_check_static_workspace(int64_t m, int64_t k, int64_t n, int64_t bs) {
+  if (m <= 0 || n <= 0 || bs <= 0) return 0;
+  const int64_t nb = sdc_cdiv(n, bs), ncols = 2 * nb;
+  const int64_t splits = sdc_expected_splits(m, k, ncols);
+  return (splits * m * ncols + splits * 2 * m) * (int64_t)sizeof(float) + 256;
+}
+
+extern "C" int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t sxk, const void* y, int64_t sym,
+                                int64_t syn, int64_t m, int64_t k, int64_t n, int64_t bs, const void* parts,
+                                int64_t spk, int64_t spc, int nparts, const float* sign_table, const float* scale,
+                                const float* b2n, const float* b2max, const float* bmax, const float* bmax_bias,
+                                const float* bsum, int64_t* state, int counts, int64_t slot, float z,
+                                float abs_floor, int64_t* cap_meta, float* cap_data, int64_t cap_stride,
+                                int64_t cap_w, int64_t cap_tag, int64_t cap_flags, int64_t cap_slots,
+                                void* workspace, int64_t workspace_bytes, float* scores_out, hipStream_t stream) {
+  if (m < 0 || n < 0 || k < 0) return SDC_EINVAL;
+  if (m == 0 || n == 0) return SDC_OK;                     // nothing to check, not counted (serve.py:435)
+  if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EINVAL;
+  if (bs < 1 || bs > 128) return SDC_EUNSUPPORTED;         // the sign table holds widths 1..128
+  if (k < 1) return SDC_EUNSUPPORTED;
+  if (!x || !y || !parts || !sign_table || !scale || !b2n || !b2max || !bmax || !bmax_bias || !bsum || !state)
+    return SDC_EINVAL;
+  if (m * (sdc_cdiv(n, bs)) * 2 > 0xFFFFFFFFll) return SDC_EUNSUPPORTED;   // flat index in 32 bits
+  const int64_t need = sdc_check_static_workspace(m, k, n, bs);
+  if (!workspace || workspace_bytes < need) return SDC_EWORKSPACE;
+  const int64_t nb = sdc_cdiv(n, bs), rem = n % bs, ncols = 2 * nb;
+  const int64_t splits = sdc_expected_splits(m, k, ncols);
+  float* E = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  float* XN = E + splits * m * ncols;
+  int rc = sdc_expected_launch(dtype, x, sxm, sxk, parts, spk, spc, nparts, m, k, ncols, splits, E, XN, stream);
+  if (rc != SDC_OK) return rc;
+  const double u = dtype == SDC_BF16 ? 1.0 / 256.0 : 1.0 / 2048.0;
+  const double h = dtype == SDC_BF16 ? 0.0 : 1.0 / 33554432.0;             // 2^-25
+  const double dmax = dtype == SDC_BF16 ? 3.3895313892515355e38 : 65504.0;
+  ScoreArgs a;
+  a.x = (const uint16_t*)x; a.sxm = sxm; a.sxk = sxk;
+  a.y = (const uint16_t*)y; a.sym = sym; a.syn = syn;
+  a.m = m; a.k = k; a.n = n; a.nb = nb; a.bs = bs; a.rem = rem; a.npairs = m * nb;
+  a.E = E; a.ncols = ncols; a.splits = splits; a.XN = XN;
+  a.s_full = sign_table + (bs - 1) * 128;
+  a.s_last = rem ? sign_table + (rem - 1) * 128 : a.s_full;
+  a.scale = scale; a.b2n = b2n; a.b2max = b2max; a.bmax = bmax; a.bmb = bmax_bias; a.bsum = bsum;
+  a.state = state + 0; a.counts = counts;
+  a.u = (float)u; a.h = (float)h; a.abs_floor = abs_floor;
+  a.l1c = (float)(k * 7.450580596923828e-09 > 1e-5 ? k * 7.450580596923828e-09 : 1e-5);   // checksum.py:95-104
+  a.zt = z; a.lim_a = (float)(dmax < 1e18 ? dmax : 1e18); a.lim_big = 1e18f;
+  a.capk = (float)(1.02 + (double)k * 2.384185791015625e-07);
+  a.capm = cap_meta; a.capd = cap_data; a.cst = cap_stride; a.cw = cap_w; a.ctag = cap_tag; a.cfo = cap_flags;
+  a.ncap = cap_slots; a.slot = slot;
+  a.zdump = scores_out;
+  a.vec = (syn == 1) && (sym % 8 == 0) && (bs % 8 == 0) && ((uintptr_t)y % 16 == 0);
+  if (cap_meta && (!cap_data || cap_w < bs)) return SDC_EINVAL;
+  const unsigned grid = (unsigned)sdc_cdiv(m * nb, 256);
+  SdcProf prof("serve_score", stream);
+  if (dtype == SDC_BF16)
+    hipLaunchKernelGGL(serve_score_kernel<SDC_BF16>, dim3(grid), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(serve_score_kernel<SDC_FP16>, dim3(grid), dim3(256), 0, stream, a);
+  SDC_LAUNCH_CHECK();
+  return SDC_OK;
+}

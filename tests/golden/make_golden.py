@@ -1,0 +1,271 @@
+"""Write the golden fixtures of the floating-point checks from the reference itself.
+
+Run once, in a container that has the reference checked out at /root/reference (never on a GPU box):
+
+    SDCGUARD_SIGN_SEED=1 python tests/golden/make_golden.py
+
+It imports the reference's checksum and serve modules (pure Python + torch, CPU) and records, for seeded small
+cases, the inputs and the reference's answers:
+  * signs.npz      the epoch-0 sign table of widths 1..128 and the epoch-3 table (checksum._signs at seed 1);
+  * train.npz      checksum.matmul_zscores + resolve: every checksum's score (the array the reference reduces
+                   with torch.max, recorded on the way) and the resolved (max_z, batch, row, col_block, noise);
+  * serve.npz      serve.check_static_impl: every checksum's score, the state row (keys and counts).
+Only numbers are stored (inputs as raw 16-bit words).  The integer fingerprints and the int8 check need no
+fixture: closed forms and brute force pin them (tests/test_oracle_fingerprint.py, tests/test_oracle_quant.py).
+"""
+from __future__ import annotations
+
+import math
+import os
+import sys
+
+import numpy as np
+import torch
+
+REF = os.environ.get("SDCGUARD_REFERENCE", "/root/reference/src")
+OUT = os.path.dirname(os.path.abspath(__file__))
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16).copy()
+
+
+class _MaxRecorder:
+    """Records the tensors passed to torch.max(t, 0) (the reference's reduction of every checksum's score)."""
+
+    def __init__(self):
+        self.seen = []
+        self._orig = torch.max
+
+    def __enter__(self):
+        orig = self._orig
+
+        def rec(*a, **kw):
+            if len(a) == 2 and a[1] == 0 and isinstance(a[0], torch.Tensor) and a[0].dim() == 1:
+                self.seen.append(a[0].detach().clone())
+            return orig(*a, **kw)
+
+        torch.max = rec
+        return self
+
+    def __exit__(self, *exc):
+        torch.max = self._orig
+
+
+def make_signs(cs):
+    t0 = np.zeros((128, 128), np.float32)
+    t3 = np.zeros((128, 128), np.float32)
+    for w in range(1, 129):
+        t0[w - 1, :w] = cs._signs(w, "cpu").numpy()
+        t3[w - 1, :w] = cs._signs(w, "cpu", 3).numpy()
+    np.savez_compressed(os.path.join(OUT, "signs.npz"), epoch0=t0, epoch3=t3, seed=np.int64(1))
+
+
+def _train_cases():
+    """(name, A, B, C, bias, alpha, beta, dtype) seeded cases: clean and corrupted, the shapes of _group._probe,
+    bmm, remainder blocks, alpha/beta, 2-D bias, fp16, tiny and huge outputs, NaN/Inf."""
+    g = torch.Generator().manual_seed(7)
+    cases = []
+
+    def r(*shape, dt=torch.bfloat16, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to(dt)
+
+    shapes = [(96, 80, 300, True), (70, 48, 1500, False), (70, 48, 2600, True), (64, 96, 40, False),
+              (48, 700, 300, True), (33, 130, 129, True), (5, 17, 1, False), (1, 64, 128, True)]
+    spots = [(70, 140), (5, 1300), (66, 2599), (17, 39), (40, 250), (32, 128), (4, 0), (0, 77)]
+    for dt in (torch.bfloat16, torch.float16):
+        for (m, k, n, wb), spot in zip(shapes, spots):
+            a, b = r(m, k, dt=dt), r(k, n, dt=dt, scale=1 / math.sqrt(k))
+            bias = r(n, dt=dt) if wb else None
+            c = torch.addmm(bias.float(), a.float(), b.float()).to(dt) if wb else (a.float() @ b.float()).to(dt)
+            tag = f"{str(dt)[6:]}_{m}x{k}x{n}"
+            cases.append((tag + "_clean", a, b, c, bias, 1.0, 1.0, dt))
+            bad = c.clone()
+            bad[spot] = bad[spot] + 50.0
+            cases.append((tag + "_plus50", a, b, bad, bias, 1.0, 1.0, dt))
+            bad = c.clone()
+            bad[spot] = float("nan")
+            cases.append((tag + "_nan", a, b, bad, bias, 1.0, 1.0, dt))
+    # bmm (batch 2), shared-B bmm
+    a, b = r(2, 40, 64), r(2, 64, 136, scale=0.125)
+    c = torch.bmm(a.float(), b.float()).bfloat16()
+    cases.append(("bf16_bmm_clean", a, b, c, None, 1.0, 1.0, torch.bfloat16))
+    bad = c.clone()
+    bad[1, 33, 130] += 50
+    cases.append(("bf16_bmm_plus50", a, b, bad, None, 1.0, 1.0, torch.bfloat16))
+    # alpha / beta with a 2-D bias (checksum tests: addmm with 2-D bias and scaling)
+    a, b = r(64, 128), r(128, 256, scale=1 / math.sqrt(128))
+    bias2 = r(64, 256)
+    c = torch.addmm(bias2.float(), a.float(), b.float(), beta=0.5, alpha=2.0).bfloat16()
+    cases.append(("bf16_addmm2d_clean", a, b, c, bias2, 2.0, 0.5, torch.bfloat16))
+    bad = c.clone()
+    bad[10, 32:64] = 0
+    cases.append(("bf16_addmm2d_zeroed", a, b, bad, bias2, 2.0, 0.5, torch.bfloat16))
+    # tiny outputs (no false alarm down to 1e-30) and a tiny value turned big
+    W = r(256, 256, scale=0.02)
+    for sc in (1e-18, 1e-24, 1e-30):
+        dY = r(64, 256, scale=sc)
+        dX = (dY.float() @ W.float()).bfloat16()
+        cases.append((f"bf16_tiny{sc:g}_clean", dY, W, dX, None, 1.0, 1.0, torch.bfloat16))
+    dY = r(64, 256, scale=1e-24)
+    dX = (dY.float() @ W.float()).bfloat16()
+    bad = dX.clone()
+    bad[3, 5] = 1e-3
+    cases.append(("bf16_tiny_to_big", dY, W, bad, None, 1.0, 1.0, torch.bfloat16))
+    # Inf output, an Inf input (expected side not finite: unjudged), an exponent-bit flip
+    a, b = r(32, 64), r(64, 256, scale=0.125)
+    c = (a.float() @ b.float()).bfloat16()
+    bad = c.clone()
+    bad[7, 200] = float("inf")
+    cases.append(("bf16_inf_out", a, b, bad, None, 1.0, 1.0, torch.bfloat16))
+    ainf = a.clone()
+    ainf[3, 3] = float("inf")
+    cases.append(("bf16_inf_in", ainf, b, c, None, 1.0, 1.0, torch.bfloat16))
+    bad = c.clone()
+    v = bad.view(-1)[5000:5001].view(torch.int16)
+    bad.view(-1)[5000] = (v ^ (1 << 14)).view(torch.bfloat16)[0]
+    cases.append(("bf16_bit14", a, b, bad, None, 1.0, 1.0, torch.bfloat16))
+    # fp16 overflow: huge outputs the inputs can produce (unjudged) vs. ones they cannot (a fault)
+    a16, b16 = r(16, 64, dt=torch.float16, scale=200.0), r(64, 128, dt=torch.float16, scale=20.0)
+    c16 = (a16.float() @ b16.float()).half()
+    cases.append(("fp16_overflow", a16, b16, c16, None, 1.0, 1.0, torch.float16))
+    # identical columns (B of ones): the plain sum's worst-case rule
+    a = r(32, 64)
+    b = torch.ones(64, 256, dtype=torch.bfloat16)
+    c = (a.float() @ b.float()).bfloat16()
+    cases.append(("bf16_ones_clean", a, b, c, None, 1.0, 1.0, torch.bfloat16))
+    return cases
+
+
+class _Store:
+    """Arrays stored once: identical tensors share an entry, and a tensor that differs from an earlier one of its
+    shape in a few elements (a corrupted copy of a clean output) is stored as (positions, new words) edits."""
+
+    def __init__(self):
+        self.out, self._seen, self._last = {}, {}, {}
+
+    def put(self, t: torch.Tensor) -> str:
+        b = _bits(t)
+        key = (b.shape, b.tobytes())
+        if key in self._seen:
+            return self._seen[key]
+        name = f"a{len(self._seen)}"
+        base = self._last.get(b.shape)
+        if base is not None:
+            diff = np.nonzero(self.out_full[base].reshape(-1) != b.reshape(-1))[0]
+            if diff.size <= 64:
+                self.out[name + "_base"] = np.array(base)
+                self.out[name + "_edit"] = np.stack([diff.astype(np.int64), b.reshape(-1)[diff].astype(np.int64)])
+                self._seen[key] = name
+                self.out_full[name] = b
+                return name
+        self.out[name] = b
+        self.out_full[name] = b
+        self._seen[key] = name
+        self._last[b.shape] = name
+        return name
+
+    out_full: dict = {}
+
+
+def make_train(cs):
+    st_ = _Store()
+    st_.out_full = {}
+    out = st_.out
+    names = []
+    for i, (name, a, b, c, bias, alpha, beta, dt) in enumerate(_train_cases()):
+        with _MaxRecorder() as mr:
+            st = cs.matmul_zscores(a, b, c, bias, alpha=alpha, beta=beta)
+        res = cs.resolve([st], 6.0)[0]
+        names.append(name)
+        p = f"c{i}_"
+        out[p + "ids"] = np.array([st_.put(a), st_.put(b), st_.put(c), st_.put(bias) if bias is not None else ""])
+        out[p + "shapes"] = np.array([list(a.shape) + [0] * (3 - a.dim()), list(b.shape) + [0] * (3 - b.dim()),
+                                      list(c.shape) + [0] * (3 - c.dim()),
+                                      (list(bias.shape) if bias is not None else []) + [0] * (3 - (bias.dim() if bias is not None else 0))],
+                                     np.int64)
+        out[p + "meta"] = np.array([alpha, beta, 1.0 if dt == torch.float16 else 0.0], np.float64)
+        out[p + "zs"] = np.concatenate([z.numpy().astype(np.float32) for z in mr.seen])
+        out[p + "result"] = np.array([res.max_z, -1 if res.batch is None else res.batch, res.row, res.col_block,
+                                      res.noise], np.float64)
+    out["names"] = np.array(names)
+    np.savez_compressed(os.path.join(OUT, "train.npz"), **out)
+    return len(names)
+
+
+def _serve_cases():
+    g = torch.Generator().manual_seed(11)
+    shapes = [(64, 256, 300, True), (1, 256, 1000, False), (200, 96, 40, True), (33, 130, 129, True),
+              (300, 64, 700, False), (64, 192, 1100, True), (16, 256, 512, False), (40, 128, 128, True)]
+    cases = []
+    for dt in (torch.bfloat16, torch.float16):
+        for m, k, n, wb in shapes:
+            W = (torch.randn(n, k, generator=g) / k ** 0.5).to(dt)
+            b = torch.randn(n, generator=g).to(dt) if wb else None
+            x = torch.randn(m, k, generator=g).to(dt)
+            y = torch.nn.functional.linear(x.float(), W.float(), None if b is None else b.float()).to(dt)
+            tag = f"{str(dt)[6:]}_{m}x{k}x{n}"
+            cases.append((tag + "_clean", x, W, b, y, dt))
+            rr, cc = (m * 2) // 3, (n * 3) // 5
+            bad = y.clone()
+            bad[rr, cc] = bad[rr, cc] + 50.0
+            cases.append((tag + "_plus50", x, W, b, bad, dt))
+            bad = y.clone()
+            bad[rr, cc] = float("nan")
+            cases.append((tag + "_nan", x, W, b, bad, dt))
+            bad = y.clone()
+            bad[rr, cc] = float("inf")
+            cases.append((tag + "_inf", x, W, b, bad, dt))
+    # an input that is not finite: every checksum of its row is unjudged
+    W = (torch.randn(256, 64, generator=g) / 8).bfloat16()
+    x = torch.randn(8, 64, generator=g).bfloat16()
+    y = (x.float() @ W.float().t()).bfloat16()
+    x2 = x.clone()
+    x2[2, 5] = float("inf")
+    cases.append(("bf16_inf_input", x2, W, None, y, torch.bfloat16))
+    # tiny outputs
+    W = (torch.randn(384, 128, generator=g) * 0.02).bfloat16()
+    x = (torch.randn(32, 128, generator=g) * 1e-24).bfloat16()
+    y = (x.float() @ W.float().t()).bfloat16()
+    cases.append(("bf16_tiny", x, W, None, y, torch.bfloat16))
+    return cases
+
+
+def make_serve(sv):
+    st_ = _Store()
+    st_.out_full = {}
+    out = st_.out
+    names = []
+    for i, (name, x, W, b, y, dt) in enumerate(_serve_cases()):
+        cs = sv.LayerChecksums(W, b, 128)
+        state = torch.zeros(1, sv.STATE_COLS, dtype=torch.int64)
+        with _MaxRecorder() as mr:
+            sv.check_static_impl(x, y, *cs.tensors(True), state, 0, 6.0, 1e-20)
+        names.append(name)
+        p = f"c{i}_"
+        out[p + "ids"] = np.array([st_.put(x), st_.put(W), st_.put(y), st_.put(b) if b is not None else ""])
+        out[p + "shape"] = np.array([x.shape[0], x.shape[1], W.shape[0]], np.int64)
+        out[p + "dtype"] = np.int64(1 if dt == torch.float16 else 0)
+        out[p + "zs"] = mr.seen[0].numpy().astype(np.float32)[:-1]       # (the appended 0 dropped)
+        out[p + "state"] = state[0].numpy().copy()
+    out["names"] = np.array(names)
+    np.savez_compressed(os.path.join(OUT, "serve.npz"), **out)
+    return len(names)
+
+
+def main():
+    if os.environ.get("SDCGUARD_SIGN_SEED") != "1":
+        sys.exit("run with SDCGUARD_SIGN_SEED=1")
+    sys.path.insert(0, REF)
+    from sdcguard import checksum as cs
+    from sdcguard import serve as sv
+    cs.USE_FAST = False
+    torch.set_num_threads(4)
+    make_signs(cs)
+    nt = make_train(cs)
+    ns = make_serve(sv)
+    print(f"wrote signs.npz, train.npz ({nt} cases), serve.npz ({ns} cases) to {OUT}")
+
+
+if __name__ == "__main__":
+    main()

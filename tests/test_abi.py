@@ -1,0 +1,49 @@
+"""The C-ABI library: it builds, loads without a GPU, and exports every symbol include/sdcguard_hip.h declares
+(no compute calls here)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared():
+    text = open(os.path.join(ROOT, "include", "sdcguard_hip.h")).read()
+    return sorted(set(re.findall(r"^(?:int|int64_t|void)\s+(sdc_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert "sdc_check_static" in names and "sdc_fingerprint3" in names
+
+
+def test_library_exports_every_declared_symbol():
+    from sdcguard_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in declared() if not hasattr(L, n)]
+    assert not missing, missing
+    assert set(declared()) <= set(_lib.SIGNATURES), set(declared()) - set(_lib.SIGNATURES)
+
+
+def test_workspace_sizes_are_host_only():
+    from sdcguard_amd import _lib
+    L = _lib.lib()
+    assert L.sdc_check_static_workspace(0, 10, 10, 128) == 0
+    ws = L.sdc_check_static_workspace(4096, 4096, 14336, 128)
+    s = L.sdc_expected_splits(4096, 4096, 224)
+    assert ws >= (s * 4096 * 224 + s * 2 * 4096) * 4
+
+
+def test_product_refuses_cpu_tensors():
+    """No CPU path: a check of CPU tensors raises instead of silently not running."""
+    import torch
+    from sdcguard_amd import _lib
+    from sdcguard_amd.recompute import fingerprint
+    with pytest.raises(_lib.HipLibraryError):
+        fingerprint(torch.ones(10))

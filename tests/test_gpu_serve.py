@@ -1,0 +1,178 @@
+"""Serving check on the GPU (sdc_check_static through the C ABI) against the oracle and the reference's answers.
+
+Every checksum's score is compared with the oracle's (tests/test_oracle_golden.py's tolerance: 1e-3 relative plus
+four fp32 ulps of the expected side's partial-sum bound, in noise units); special scores (inf, unjudged 0) exactly;
+the state row's counts exactly and its worst checksum's location whenever it is over the line.  Verdicts must
+agree on every fault-injected trial except inside a declared band |z - 6| < 0.3 around the line (H3: the two
+implementations add in different orders, so a block scoring 5.99 in one may score 6.01 in the other); the test
+counts those and requires them to be rare.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import serve_check
+from tests import _golden as G
+from tests.test_oracle_golden import SERVE, gemm_slack, serve_case, z_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _dt(name):
+    return torch.bfloat16 if name == "bf16" else torch.float16
+
+
+def to_dev(a: np.ndarray, dt: str) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(_dt(dt)).cuda()
+
+
+def run_gpu(x, W, b, y, dt, state=None, slot=0, cap=None, with_bias=True):
+    from sdcguard_amd.serve import STATE_COLS, LayerChecksums, check_static_impl
+    xd, Wd, yd = to_dev(x, dt), to_dev(W, dt), to_dev(y, dt)
+    bd = to_dev(b, dt) if b is not None else None
+    cs = LayerChecksums(Wd, bd, 128)
+    if state is None:
+        state = torch.zeros(1, STATE_COLS, dtype=torch.int64, device="cuda")
+    zs = torch.full((x.shape[0], cs.nb, 2), -7.0, dtype=torch.float32, device="cuda")
+    capm, capd = cap if cap is not None else (None, None)
+    check_static_impl(xd, yd, *cs.tensors(with_bias), state, slot, 6.0, 1e-20, capm, capd, 128, 2,
+                      scores_out=zs)
+    torch.cuda.synchronize()
+    return zs.cpu().numpy(), state.cpu().numpy(), cs
+
+
+def test_mfma_layout_selftest():
+    from sdcguard_amd import _lib
+    g = torch.Generator().manual_seed(3)
+    A = torch.randn(32, 16, generator=g).bfloat16()
+    B = torch.randn(16, 32, generator=g).bfloat16()
+    C = torch.zeros(32, 32, dtype=torch.float32, device="cuda")
+    Ad, Bt = A.cuda().contiguous(), B.t().contiguous().cuda()
+    _lib.check(_lib.lib().sdc_mfma_layout_selftest(Ad.data_ptr(), Bt.data_ptr(), C.data_ptr(), 0), "selftest")
+    torch.cuda.synchronize()
+    ref = A.double() @ B.double()
+    assert torch.allclose(C.cpu().double(), ref, rtol=1e-5, atol=1e-5), (C.cpu() - ref).abs().max()
+
+
+@pytest.mark.parametrize("i", range(len(G.names(SERVE))))
+def test_serving_kernel_matches_oracle_and_reference(i):
+    name = G.names(SERVE)[i]
+    x, W, b, y, dt = serve_case(i)
+    zs, st, cs = run_gpu(x, W, b, y, dt)
+    c = serve_check.layer_constants(W, b, 128, dt, seed=1)
+    o = serve_check.check_static(x, y, c, dtype=dt, seed=1)
+    ok = z_close(zs.reshape(-1), o.z.reshape(-1), gemm_slack(o.csb, o.den).reshape(-1))
+    assert ok.all(), (name, np.nonzero(~ok)[0][:5], zs.reshape(-1)[~ok][:5], o.z.reshape(-1)[~ok][:5])
+    ref = SERVE[f"c{i}_state"]
+    assert st[0, 2] == ref[2] == o.state[2] and st[0, 3] == ref[3] == o.state[3], (name, st, ref)
+    gz, gf, _ = serve_check.decode(st[0, 0], st[0, 1])
+    rz, rf, _ = serve_check.decode(ref[0], ref[1])
+    assert (gz > 6) == (rz > 6), (name, gz, rz)
+    if rz > 6:
+        assert gf // 2 == rf // 2, (name, gf, rf)
+
+
+def _layer(m, k, n, seed, dt="bf16", wstd=0.02, with_bias=False):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=g).to(_dt(dt))
+    W = (torch.randn(n, k, generator=g) * wstd).to(_dt(dt))
+    b = (torch.randn(n, generator=g) * 0.02).to(_dt(dt)) if with_bias else None
+    return x, W, b
+
+
+def _gpu_linear(x, W, b):
+    return torch.nn.functional.linear(x.cuda(), W.cuda(), None if b is None else b.cuda())
+
+
+@pytest.mark.parametrize("m,k,n,dt,bias", [(256, 1024, 2816, "bf16", False), (96, 512, 1000, "fp16", True),
+                                            (1, 4096, 14336, "bf16", False), (513, 256, 384, "bf16", True)])
+def test_bit_flip_verdicts_match_oracle(m, k, n, dt, bias):
+    """Single-bit flips in y at a 1/8 trial rate (the bf16 Llama-MLP workload's fault model, scaled down):
+    per-block verdicts and fault locations agree with the oracle on every trial."""
+    x, W, b = _layer(m, k, n, seed=m + k + n, dt=dt, with_bias=bias)
+    y = _gpu_linear(x, W, b)
+    xf, Wf = x.float().numpy(), W.float().numpy()
+    bf = None if b is None else b.float().numpy()
+    c = serve_check.layer_constants(Wf, bf, 128, dt, seed=1)
+    rng = np.random.default_rng(5)
+    band = flips = 0
+    for trial in range(16):
+        yy = y.clone()
+        if trial % 8 == 7:
+            idx = int(rng.integers(yy.numel()))
+            bit = int(rng.integers(16))
+            v = yy.view(-1)[idx:idx + 1].view(torch.int16)
+            yy.view(-1)[idx] = (v ^ torch.tensor([(1 << bit) if bit < 15 else -32768], dtype=torch.int16,
+                                                 device="cuda")).view(yy.dtype)[0]
+            flips += 1
+        yf = yy.float().cpu().numpy()
+        zs, st, _ = run_gpu(xf, Wf, bf, yf, dt)
+        o = serve_check.check_static(xf, yf, c, dtype=dt, seed=1)
+        near = np.abs(o.z - 6.0) < 0.3
+        band += int(near.sum())
+        gv, ov = zs > 6.0, o.z > 6.0
+        assert np.array_equal(gv[~near], ov[~near]), (trial, np.argwhere(gv != ov)[:4])
+        assert st[0, 2] == 1 and st[0, 3] == o.state[3]
+        oz, of, _ = serve_check.decode(o.state[0], o.state[1])
+        gz, gf, _ = serve_check.decode(st[0, 0], st[0, 1])
+        if oz > 6.3:
+            assert gz > 6 and gf // 2 == of // 2
+    assert band <= 2, band
+
+
+def test_capture_and_counts():
+    """A row over the line is captured once per layer and read (serve.py:67-88)."""
+    from sdcguard_amd.serve import CAP_FLAGS, CAPTURE_SLOTS, STATE_COLS
+    x, W, b = _layer(64, 256, 300, seed=9, with_bias=True)
+    y = _gpu_linear(x, W, b).cpu()
+    y[40, 150] += 50.0
+    capm = torch.zeros(CAP_FLAGS + 4, dtype=torch.int64, device="cuda")
+    capd = torch.zeros(CAPTURE_SLOTS + 1, 128 + 256, dtype=torch.float32, device="cuda")
+    state = torch.zeros(4, STATE_COLS, dtype=torch.int64, device="cuda")
+    xf, Wf, bf, yf = x.float().numpy(), W.float().numpy(), b.float().numpy(), y.float().numpy()
+    for _ in range(2):
+        zs, st, cs = run_gpu(xf, Wf, bf, yf, "bf16", state=state, slot=2, cap=(capm, capd))
+    assert st[2, 2] == 2                                     # two checks executed
+    z, flat, _ = serve_check.decode(st[2, 0], st[2, 1])
+    assert z > 6 and (flat // 2) // cs.nb == 40 and (flat // 2) % cs.nb == 1
+    cm = capm.cpu().numpy()
+    assert cm[0] == 1                                        # one row kept (the layer's flag stops the second)
+    rec = cm[2:2 + 6]
+    assert rec[1] == 40 and rec[2] == 1 and cm[CAP_FLAGS + 2] == 1
+    cd = capd.cpu().numpy()
+    assert np.array_equal(cd[0, :128], yf[40, 128:256])
+    assert np.array_equal(cd[0, 128:128 + 256], xf[40])
+
+
+def test_empty_batch_is_not_counted():
+    from sdcguard_amd.serve import STATE_COLS, LayerChecksums, check_static_impl
+    W = torch.randn(256, 64).bfloat16().cuda()
+    cs = LayerChecksums(W, None)
+    st = torch.zeros(1, STATE_COLS, dtype=torch.int64, device="cuda")
+    check_static_impl(torch.zeros(0, 64, dtype=torch.bfloat16, device="cuda"),
+                      torch.zeros(0, 256, dtype=torch.bfloat16, device="cuda"), *cs.tensors(), st, 0, 6.0, 1e-20)
+    torch.cuda.synchronize()
+    assert st.abs().sum().item() == 0
+
+
+def test_llama_mlp_full_size_clean_and_faulty():
+    """The bf16 Llama-MLP workload at full size (4096 x 4096 x 14336): clean scores agree with the oracle block
+    by block, and a single corrupted element is found at its (row, block)."""
+    x, W, _ = _layer(4096, 4096, 14336, seed=2024)
+    y = _gpu_linear(x, W, None)
+    xf, Wf = x.float().numpy(), W.float().numpy()
+    c = serve_check.layer_constants(Wf, None, 128, "bf16", seed=1)
+    yf = y.float().cpu().numpy()
+    zs, st, _ = run_gpu(xf, Wf, None, yf, "bf16")
+    o = serve_check.check_static(xf, yf, c, dtype="bf16", seed=1)
+    ok = z_close(zs.reshape(-1), o.z.reshape(-1), gemm_slack(o.csb, o.den).reshape(-1))
+    assert ok.all(), (np.nonzero(~ok)[0][:5], zs.reshape(-1)[~ok][:5], o.z.reshape(-1)[~ok][:5])
+    assert float(np.max(zs)) < 6.0 and int(st[0, 3]) == 0
+    yf[1234, 5678] += 8.0
+    zs, st, _ = run_gpu(xf, Wf, None, yf, "bf16")
+    z, flat, _ = serve_check.decode(st[0, 0], st[0, 1])
+    assert z > 6 and (flat // 2) // 112 == 1234 and (flat // 2) % 112 == 5678 // 128
