@@ -35,7 +35,13 @@ extern "C" {
  *   cap_meta / cap_data (may be NULL): the capture buffers of serve.py:67-88; cap_flags = CAP_FLAGS,
  *     cap_slots = CAPTURE_SLOTS, cap_stride = cap_data's row stride, cap_w = where x starts in a row.
  *   workspace: device memory of at least sdc_check_static_workspace(m, k, n, bs) bytes.
- *   scores_out (may be NULL): every checksum's score, (m, nb, 2) fp32, plain then signed (for tests). */
+ *   scores_out (may be NULL): every checksum's score, (m, nb, 2) fp32, plain then signed (for tests).
+ *   kernel: 0 or 1 = v1, the GEMM then one persistent pass over y that sums and scores every pair (fastest at
+ *     every batch size measured on MI355X); 3 = v3, the block sums of y on a side stream concurrently with the
+ *     GEMM, then a scoring pass (the reference's SDCGUARD_SERVE_KERNEL=v1|v3 switch); 4 = v3 on `stream` alone.
+ *   block_consts (may be NULL): the same per-block constants packed as (nb, 12) fp32, 16-byte aligned, per block
+ *     [scale0, scale1, bsum0, bsum1, b2n0, b2n1, b2max0, b2max1, bmax, bmax_bias, 0, 0]: three 16-byte loads
+ *     per block instead of ten scattered ones; the separate arrays are still required. */
 int64_t sdc_check_static_workspace(int64_t m, int64_t k, int64_t n, int64_t bs);
 int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t sxk, const void* y, int64_t sym, int64_t syn,
                      int64_t m, int64_t k, int64_t n, int64_t bs, const void* parts, int64_t spk, int64_t spc,
@@ -43,8 +49,8 @@ int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t sxk, const v
                      const float* b2max, const float* bmax, const float* bmax_bias, const float* bsum,
                      int64_t* state, int counts, int64_t slot, float z, float abs_floor, int64_t* cap_meta,
                      float* cap_data, int64_t cap_stride, int64_t cap_w, int64_t cap_tag, int64_t cap_flags,
-                     int64_t cap_slots, void* workspace, int64_t workspace_bytes, float* scores_out,
-                     hipStream_t stream);
+                     int64_t cap_slots, void* workspace, int64_t workspace_bytes, float* scores_out, int kernel,
+                     const float* block_consts, hipStream_t stream);
 
 /* Depth split the expected-side GEMM uses for an (m x k) @ (k x ncols) product (sizes the workspace). */
 int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
@@ -64,6 +70,9 @@ int sdc_fingerprint2(const void* bits, int64_t n, int kind, int64_t* out, hipStr
 int sdc_profile_enable(int on);
 int sdc_profile_reset(void);
 int sdc_profile_read(const char* name, double* total_ms, int64_t* launches);
+
+/* Name of the HIP error behind the last SDC_ELAUNCH returned to the calling thread. */
+const char* sdc_last_error(void);
 
 /* ---- self-tests ---------------------------------------------------------------------------------------------
  * No counterpart in the reference: checks the MFMA operand layout the GEMM kernels assume.

@@ -29,11 +29,12 @@ P, I64, I32, F32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
 SIGNATURES = {
     "sdc_check_static_workspace": (I64, [I64, I64, I64, I64]),
     "sdc_check_static": (I32, [I32, P, I64, I64, P, I64, I64, I64, I64, I64, I64, P, I64, I64, I32, P, P, P, P, P,
-                               P, P, P, I32, I64, F32, F32, P, P, I64, I64, I64, I64, I64, P, I64, P, P]),
+                               P, P, P, I32, I64, F32, F32, P, P, I64, I64, I64, I64, I64, P, I64, P, I32, P, P]),
     "sdc_expected_splits": (I64, [I64, I64, I64]),
     "sdc_fingerprint3": (I32, [P, I64, I32, I64, P, P]),
     "sdc_fingerprint2": (I32, [P, I64, I32, P, P]),
     "sdc_mfma_layout_selftest": (I32, [P, P, P, P]),
+    "sdc_last_error": (ctypes.c_char_p, []),
     "sdc_profile_enable": (I32, [I32]),
     "sdc_profile_reset": (I32, []),
     "sdc_profile_read": (I32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]),
@@ -64,7 +65,10 @@ def lib() -> ctypes.CDLL:
 
 def check(rc: int, what: str) -> None:
     if rc != SDC_OK:
-        raise HipLibraryError(f"{what}: {_NAMES.get(rc, 'error')} (status {rc})")
+        extra = ""
+        if rc == SDC_ELAUNCH:
+            extra = f": {lib().sdc_last_error().decode(errors='replace')}"
+        raise HipLibraryError(f"{what}: {_NAMES.get(rc, 'error')} (status {rc}){extra}")
 
 
 def stream_of(t: torch.Tensor) -> int:

@@ -4,8 +4,12 @@
 #include <stdint.h>
 
 #define SDC_WAVE 64
+// most depth-split planes of the expected-side GEMM (its scorers add them with unrolled loads)
+#define SDC_MAX_SPLITS 4
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -96,7 +100,17 @@ __device__ __forceinline__ int64_t fbits64(float f) { return (int64_t)(uint32_t)
 
 static inline int64_t sdc_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// The HIP error behind the last SDC_ELAUNCH of this thread (sdc_last_error()).
+void sdc_note_error(hipError_t e);
+
 #define SDC_LAUNCH_CHECK()                                      \
   do {                                                          \
-    if (hipGetLastError() != hipSuccess) return SDC_ELAUNCH;    \
+    hipError_t e_ = hipGetLastError();                          \
+    if (e_ != hipSuccess) {                                     \
+      sdc_note_error(e_);                                       \
+      return SDC_ELAUNCH;                                       \
+    }                                                           \
   } while (0)
+
+// Entry points clear errors left by earlier HIP calls of the thread, so a launch check sees only its own.
+#define SDC_CLEAR_ERRORS() (void)hipGetLastError()

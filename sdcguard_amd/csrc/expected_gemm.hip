@@ -163,7 +163,7 @@ extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols) {
   int64_t s = sdc_cdiv(512, tiles);
   const int64_t smax = k / 512 > 1 ? k / 512 : 1;
   if (s > smax) s = smax;
-  if (s > 16) s = 16;
+  if (s > SDC_MAX_SPLITS) s = SDC_MAX_SPLITS;
   if (s < 1) s = 1;
   return s;
 }

@@ -153,6 +153,7 @@ unsigned grid_for(int64_t work_items) {
 // out[3] (int64, zeroed by the caller) += fp3 of n words of word_bytes (2 or 1) bytes at bits, positions from start
 extern "C" int sdc_fingerprint3(const void* bits, int64_t n, int word_bytes, int64_t start, int64_t* out,
                                 hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
   if (n < 0 || !out || (word_bytes != 1 && word_bytes != 2)) return SDC_EINVAL;
   if (n == 0) return SDC_OK;
   if (!bits) return SDC_EINVAL;
@@ -175,6 +176,7 @@ extern "C" int sdc_fingerprint3(const void* bits, int64_t n, int word_bytes, int
 
 // out[2] (int64, zeroed by the caller) += fp2 of n words; kind 0 = int16, 1 = int32, 2 = uint8
 extern "C" int sdc_fingerprint2(const void* bits, int64_t n, int kind, int64_t* out, hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
   if (n < 0 || !out || kind < 0 || kind > 2) return SDC_EINVAL;
   if (n == 0) return SDC_OK;
   if (!bits) return SDC_EINVAL;

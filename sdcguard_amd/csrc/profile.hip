@@ -77,3 +77,12 @@ extern "C" int sdc_profile_read(const char* name, double* total_ms, int64_t* lau
   *launches = cnt;
   return SDC_OK;
 }
+
+namespace {
+thread_local hipError_t g_last = hipSuccess;
+}
+
+void sdc_note_error(hipError_t e) { g_last = e; }
+
+// name of the HIP error behind the last SDC_ELAUNCH returned to this thread
+extern "C" const char* sdc_last_error(void) { return hipGetErrorString(g_last); }

@@ -11,6 +11,7 @@
 //      state row with one integer atomic maximum (only when it raises the row), counts with atomic adds.
 #include "common.h"
 #include "profile.h"
+#include "streams.h"
 
 int sdc_expected_launch(int dtype, const void* x, int64_t sxm, int64_t sxk, const void* parts, int64_t spk,
                         int64_t spc, int nparts, int64_t m, int64_t k, int64_t ncols, int64_t splits, float* E,
@@ -32,6 +33,7 @@ struct ScoreArgs {
   int64_t* capm; float* capd; int64_t cst, cw, ctag, cfo, ncap, slot;
   int vec;
   float* zdump;      // optional: every checksum's score, (m, nb, 2) fp32 (tests)
+  const f32x4* packed;   // optional: the per-block constants as 3 float4 per block (see sdc_check_static)
 };
 
 struct PairScore {
@@ -40,6 +42,12 @@ struct PairScore {
   bool sec;
   int unk;
 };
+
+// Division and square root by the hardware's reciprocal and square-root approximations (about 1 ulp): the scores
+// only need to agree with the reference's to 1e-3 of the noise, and the special cases keep their IEEE results
+// (x / 0 = inf, 0 / 0 = NaN, inf / inf = NaN, sqrt(inf) = inf, sqrt(NaN) = NaN).
+__device__ __forceinline__ float fdiv(float a, float b) { return a * __builtin_amdgcn_rcpf(b); }
+__device__ __forceinline__ float fsqrt(float a) { return __builtin_amdgcn_sqrtf(a); }
 
 // _serve_fast.py:334-402 (`_judge`) for one (row, block) pair, serving flavour (unjudged checksums score 0).
 __device__ __forceinline__ PairScore judge_serve(float plain, float sgn, float sq, float l1, float xn, float asum,
@@ -51,7 +59,7 @@ __device__ __forceinline__ PairScore judge_serve(float plain, float sgn, float s
   float exp0 = e0 * sc0 + bs0;
   float exp1 = e1 * sc1 + bs1;
   float bound = asum * bmaxv + bmbv;
-  float rsq = sqrtf(sq);
+  float rsq = fsqrt(sq);
   float noise = rsq * a.u;
   float fl0 = xn * b2n0 * 1e-5f;
   float fl1 = xn * b2n1 * 1e-5f;
@@ -62,16 +70,16 @@ __device__ __forceinline__ PairScore judge_serve(float plain, float sgn, float s
   const float bigfl = bound * (float)(1e-5 * 128.0);
   fl0 = fl0 < inf ? fl0 : bigfl;
   fl1 = fl1 < inf ? fl1 : bigfl;
-  float swf = sqrtf(wf);
+  float swf = fsqrt(wf);
   float tail = a.abs_floor + swf * a.h;
   float den0 = (noise + fl0) + tail;
   float den1 = (noise + fl1) + tail;
   float d0 = fabsf(exp0 - plain);
   float d1 = fabsf(exp1 - sgn);
-  float z0 = d0 / den0;
-  float z1 = d1 / den1;
+  float z0 = fdiv(d0, den0);
+  float z1 = fdiv(d1, den1);
   float worst = (l1 * (1.25f * a.u) + (1.25f * a.h * wf)) + fl0 + a.abs_floor;
-  float zw = d0 / worst * a.zt;
+  float zw = fdiv(d0, worst) * a.zt;
   z0 = (z0 == z0 && zw == zw) ? fminf(z0, zw) : nanv;
   float lim = bound * 1.01f;
   bool nfin = !(noise < inf);
@@ -108,105 +116,180 @@ __device__ __forceinline__ PairScore judge_serve(float plain, float sgn, float s
   return r;
 }
 
+// Four sums of 8 elements (one 16-byte load) with packed dot products: v_dot2_f32_{bf16,f16} adds two products
+// to an fp32 accumulator, so each instruction takes two elements: plain sum (x . 1), signed sum (x . s), sum of
+// squares (x . x) and sum of |x| (|x| . 1).  `sg2` holds the four sign pairs of these eight columns.
 template <int DT>
-__device__ __forceinline__ void acc8(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, const float* s, float& pl,
-                                     float& sg, float& sq, float& ab) {
-  float v[8] = {lo_of<DT>(w0), hi_of<DT>(w0), lo_of<DT>(w1), hi_of<DT>(w1),
-                lo_of<DT>(w2), hi_of<DT>(w2), lo_of<DT>(w3), hi_of<DT>(w3)};
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    pl += v[e];
-    sg = fmaf(v[e], s[e], sg);
-    sq = fmaf(v[e], v[e], sq);
-    ab += fabsf(v[e]);
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (DT == SDC_BF16) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+  } else {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
   }
 }
 
 template <int DT>
-__global__ __launch_bounds__(256) void serve_score_kernel(ScoreArgs a) {
-  __shared__ int64_t red_k[4], red_d[4];
-  __shared__ int red_u[4];
-  __shared__ int64_t cap_slot;
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6, q = lane & 3;
-  const int64_t base = (int64_t)blockIdx.x * 256 + w * 64;
+__device__ __forceinline__ void acc8(u32x4 v, const uint32_t* sg2, float& pl, float& sg, float& sq, float& ab) {
+  constexpr uint32_t ONES = DT == SDC_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    pl = dot2<DT>(w[i], ONES, pl);
+    sg = dot2<DT>(w[i], sg2[i], sg);
+    sq = dot2<DT>(w[i], w[i], sq);
+    ab = dot2<DT>(w[i] & 0x7FFF7FFFu, ONES, ab);
+  }
+}
 
-  // this lane's 32 columns of a block: chunks q, q+4, q+8, q+12 of 8 columns
-  float sfull[32];
+// The four sums of the (row, block) pair each lane keeps: a wave reads 64 consecutive pairs starting at `base`;
+// lane l ends up with pair base + (l & 3) * 16 + (l >> 2).  Four lanes share a pair in each of four rounds; all
+// sixteen 16-byte loads are issued before any is used (256 bytes per lane in flight).  Pairs that are not full
+// 128-wide vector-loadable blocks (a narrower last block, strided y) take an element-wise path.
+template <int DT>
+__device__ __forceinline__ void pair_sums(const ScoreArgs& a, int64_t base, int lane, const uint32_t* sg2, float& my_pl,
+                                          float& my_sg, float& my_sq, float& my_ab) {
+  const int q = lane & 3;
+  bool full[4];
+  u32x4 v[4][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int g = 0; g < 4; ++g) {
+    const int64_t p = base + g * 16 + (lane >> 2);
+    full[g] = false;
+    if (p < a.npairs && a.vec) {
+      const uint32_t r = (uint32_t)p / (uint32_t)a.nb, jb = (uint32_t)p - r * (uint32_t)a.nb;
+      const bool last = (jb == a.nb - 1) && (a.rem > 0);
+      if (!last && a.bs == 128) {
+        full[g] = true;
+        const uint16_t* yr = a.y + (int64_t)r * a.sym + (int64_t)jb * 128;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int c = 8 * (q + 4 * j) + e;
-      sfull[j * 8 + e] = c < a.bs ? a.s_full[c] : 0.f;
+        for (int j = 0; j < 4; ++j)
+          v[g][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(yr + 8 * (q + 4 * j)));
+      }
     }
-
-  float my_pl = 0.f, my_sg = 0.f, my_sq = 0.f, my_ab = 0.f;
+  }
+  my_pl = my_sg = my_sq = my_ab = 0.f;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int64_t p = base + g * 16 + (lane >> 2);
     float pl = 0.f, sg = 0.f, sq = 0.f, ab = 0.f;
-    if (p < a.npairs) {
-      const int64_t r = p / a.nb, jb = p - r * a.nb;
+    if (full[g]) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc8<DT>(v[g][j], &sg2[j * 4], pl, sg, sq, ab);
+    } else if (p < a.npairs) {
+      const int64_t r = (uint32_t)p / (uint32_t)a.nb, jb = (uint32_t)p - (uint32_t)r * (uint32_t)a.nb;
       const bool last = (jb == a.nb - 1) && (a.rem > 0);
       const int64_t wid = last ? a.rem : a.bs;
       const uint16_t* yr = a.y + r * a.sym + jb * a.bs * a.syn;
-      if (a.vec && wid == 128) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          u32x4 v = *reinterpret_cast<const u32x4*>(yr + 8 * (q + 4 * j));
-          acc8<DT>(v.x, v.y, v.z, v.w, &sfull[j * 8], pl, sg, sq, ab);
-        }
-      } else {
-        const float* sp = last ? a.s_last : a.s_full;
-        for (int j = 0; j < 4; ++j)
-          for (int e = 0; e < 8; ++e) {
-            const int c = 8 * (q + 4 * j) + e;
-            if (c < wid) {
-              float v = half_to_f32<DT>(yr[c * a.syn]);
-              pl += v;
-              sg = fmaf(v, sp[c], sg);
-              sq = fmaf(v, v, sq);
-              ab += fabsf(v);
-            }
+      const float* sp = last ? a.s_last : a.s_full;
+#pragma unroll 1
+      for (int j = 0; j < 4; ++j)
+#pragma unroll 1
+        for (int e = 0; e < 8; ++e) {
+          const int c = 8 * (q + 4 * j) + e;
+          if (c < wid) {
+            float x = half_to_f32<DT>(yr[c * a.syn]);
+            pl += x;
+            sg = fmaf(x, sp[c], sg);
+            sq = fmaf(x, x, sq);
+            ab += fabsf(x);
           }
-      }
+        }
     }
     pl = quad_sum(pl); sg = quad_sum(sg); sq = quad_sum(sq); ab = quad_sum(ab);
     if (q == g) { my_pl = pl; my_sg = sg; my_sq = sq; my_ab = ab; }
   }
+}
 
-  // score this lane's pair
-  const int64_t p = base + q * 16 + (lane >> 2);
+// The signs of this lane's 32 columns of a full block (chunks q, q+4, q+8, q+12 of 8 columns) as packed pairs; a
+// table row holds 128 entries (zeros past its width), so these loads need no bounds test.
+template <int DT>
+__device__ __forceinline__ void lane_signs(const ScoreArgs& a, int q, uint32_t* sg2) {
+  constexpr uint32_t POS = DT == SDC_BF16 ? 0x3F80u : 0x3C00u, NEG = DT == SDC_BF16 ? 0xBF80u : 0xBC00u;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(a.s_full + 8 * (q + 4 * j));
+    const f32x4 s1 = *reinterpret_cast<const f32x4*>(a.s_full + 8 * (q + 4 * j) + 4);
+    sg2[j * 4 + 0] = (s0.x < 0.f ? NEG : POS) | ((s0.y < 0.f ? NEG : POS) << 16);
+    sg2[j * 4 + 1] = (s0.z < 0.f ? NEG : POS) | ((s0.w < 0.f ? NEG : POS) << 16);
+    sg2[j * 4 + 2] = (s1.x < 0.f ? NEG : POS) | ((s1.y < 0.f ? NEG : POS) << 16);
+    sg2[j * 4 + 3] = (s1.z < 0.f ? NEG : POS) | ((s1.w < 0.f ? NEG : POS) << 16);
+  }
+}
+
+// Scores this lane's pairs (NP of them: p0, p0 + 256, ...; those >= npairs are skipped) from their four sums, then
+// the workgroup's worst key into the layer's state row (one atomic maximum, only when it raises the row), the
+// counts, and the capture of a row over the line (_serve_fast.py:404-452).  Every thread of the workgroup calls it.
+struct LaneBest {
   int64_t key = 0, keyd = 0;
   int unk = 0;
-  if (p < a.npairs) {
-    const int64_t r = p / a.nb, jb = p - r * a.nb;
-    const bool last = (jb == a.nb - 1) && (a.rem > 0);
-    const float wf = (float)(last ? a.rem : a.bs);
-    float e0 = 0.f, e1 = 0.f, asq = 0.f, asum = 0.f;
-    for (int64_t s = 0; s < a.splits; ++s) {
-      const float* Es = a.E + (s * a.m + r) * a.ncols + 2 * jb;
-      e0 += Es[0];
-      e1 += Es[1];
-      asq += a.XN[s * 2 * a.m + r];
-      asum += a.XN[s * 2 * a.m + a.m + r];
+};
+
+// Scores pair p (skipped when p >= npairs) from its four sums into the lane's running worst.
+template <int DT>
+__device__ __forceinline__ void score_pair(const ScoreArgs& a, int64_t p, float pl, float sg, float sq, float ab,
+                                           LaneBest& best) {
+  if (p >= a.npairs) return;
+  const int64_t r = (uint32_t)p / (uint32_t)a.nb, jb = (uint32_t)p - (uint32_t)r * (uint32_t)a.nb;
+  const bool last = (jb == a.nb - 1) && (a.rem > 0);
+  const float wf = (float)(last ? a.rem : a.bs);
+  // the GEMM's depth-split planes (at most SDC_MAX_SPLITS): every load issued before the first add
+  const float* ep = a.E + r * a.ncols + 2 * jb;
+  const float* xp = a.XN + r;
+  const int64_t estep = a.m * a.ncols, xstep = 2 * a.m;
+  float2 ev[SDC_MAX_SPLITS];
+  float xa[SDC_MAX_SPLITS], xb[SDC_MAX_SPLITS];
+#pragma unroll
+  for (int s = 0; s < SDC_MAX_SPLITS; ++s) {
+    if (s < a.splits) {
+      ev[s] = *reinterpret_cast<const float2*>(ep + s * estep);
+      xa[s] = xp[s * xstep];
+      xb[s] = xp[s * xstep + a.m];
     }
-    PairScore ps = judge_serve(my_pl, my_sg, my_sq, my_ab, sqrtf(asq), asum, e0, e1, a.scale[2 * jb],
-                               a.scale[2 * jb + 1], a.bsum[2 * jb], a.bsum[2 * jb + 1], a.bmax[jb], a.bmb[jb],
-                               a.b2n[2 * jb], a.b2n[2 * jb + 1], a.b2max[2 * jb], a.b2max[2 * jb + 1], wf, a);
-    if (a.zdump) {
-      a.zdump[2 * p] = ps.z0;
-      a.zdump[2 * p + 1] = ps.z1;
-    }
-    const int64_t zb = fbits64(fmaxf(ps.zc, 0.f));
-    const int64_t flat = p * 2 + (ps.sec ? 1 : 0);
-    key = (zb << 32) | (flat & 0xFFFFFFFFll);
-    keyd = (zb << 32) | (fbits64(ps.dc) & 0xFFFFFFFFll);
-    unk = ps.unk;
   }
-  key = wave_max_i64(key);
-  keyd = wave_max_i64(keyd);
-  unk = wave_sum_i32(unk);
+  float e0 = ev[0].x, e1 = ev[0].y, asq = xa[0], asum = xb[0];
+#pragma unroll
+  for (int s = 1; s < SDC_MAX_SPLITS; ++s) {
+    if (s < a.splits) {
+      e0 += ev[s].x;
+      e1 += ev[s].y;
+      asq += xa[s];
+      asum += xb[s];
+    }
+  }
+  PairScore ps;
+  if (a.packed) {
+    const f32x4 c0 = a.packed[3 * jb], c1 = a.packed[3 * jb + 1], c2 = a.packed[3 * jb + 2];
+    ps = judge_serve(pl, sg, sq, ab, fsqrt(asq), asum, e0, e1, c0.x, c0.y, c0.z, c0.w, c2.x, c2.y, c1.x, c1.y,
+                     c1.z, c1.w, wf, a);
+  } else {
+    ps = judge_serve(pl, sg, sq, ab, fsqrt(asq), asum, e0, e1, a.scale[2 * jb], a.scale[2 * jb + 1],
+                     a.bsum[2 * jb], a.bsum[2 * jb + 1], a.bmax[jb], a.bmb[jb], a.b2n[2 * jb], a.b2n[2 * jb + 1],
+                     a.b2max[2 * jb], a.b2max[2 * jb + 1], wf, a);
+  }
+  if (a.zdump) {
+    a.zdump[2 * p] = ps.z0;
+    a.zdump[2 * p + 1] = ps.z1;
+  }
+  const int64_t zb = fbits64(fmaxf(ps.zc, 0.f));
+  const int64_t flat = p * 2 + (ps.sec ? 1 : 0);
+  const int64_t k1 = (zb << 32) | (flat & 0xFFFFFFFFll);
+  const int64_t d1 = (zb << 32) | (fbits64(ps.dc) & 0xFFFFFFFFll);
+  best.key = k1 > best.key ? k1 : best.key;
+  best.keyd = d1 > best.keyd ? d1 : best.keyd;
+  best.unk += ps.unk;
+}
+
+// The workgroup's worst key into the layer's state row (one atomic maximum, only when it raises the row), the
+// counts, and the capture of a row over the line (_serve_fast.py:404-452).  Every thread of the workgroup calls it.
+template <int DT>
+__device__ __forceinline__ void report_wg(const ScoreArgs& a, LaneBest best) {
+  __shared__ int64_t red_k[4], red_d[4];
+  __shared__ int red_u[4];
+  __shared__ int64_t cap_slot;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int64_t key = wave_max_i64(best.key);
+  int64_t keyd = wave_max_i64(best.keyd);
+  int unk = wave_sum_i32(best.unk);
   if (lane == 0) { red_k[w] = key; red_d[w] = keyd; red_u[w] = unk; }
   __syncthreads();
   int64_t* st = a.state;
@@ -220,8 +303,9 @@ __global__ __launch_bounds__(256) void serve_score_kernel(ScoreArgs a) {
     }
     red_k[0] = k0;
     // most workgroups cannot raise the layer's worst score: read first, take the atomic only when it can
-    if (k0 > __atomic_load_n(st, __ATOMIC_RELAXED)) atomicMax((unsigned long long*)st, (unsigned long long)k0);
-    if (d0 > __atomic_load_n(st + 1, __ATOMIC_RELAXED)) atomicMax((unsigned long long*)(st + 1), (unsigned long long)d0);
+    const int64_t s0 = __atomic_load_n(st, __ATOMIC_RELAXED), s1 = __atomic_load_n(st + 1, __ATOMIC_RELAXED);
+    if (k0 > s0) atomicMax((unsigned long long*)st, (unsigned long long)k0);
+    if (d0 > s1) atomicMax((unsigned long long*)(st + 1), (unsigned long long)d0);
     if (a.counts) {
       if (blockIdx.x == 0) atomicAdd((unsigned long long*)(st + 2), 1ull);
       if (un > 0) atomicAdd((unsigned long long*)(st + 3), (unsigned long long)un);
@@ -229,8 +313,8 @@ __global__ __launch_bounds__(256) void serve_score_kernel(ScoreArgs a) {
     cap_slot = -1;
     if (a.capm) {
       const int64_t zbits = k0 >> 32;
-      const float best = __uint_as_float((uint32_t)zbits);
-      if (best > a.zt) {
+      const float bz = __uint_as_float((uint32_t)zbits);
+      if (bz > a.zt) {
         unsigned long long taken = atomicExch((unsigned long long*)(a.capm + a.cfo + a.slot), 1ull);
         if (taken == 0) {
           int64_t c = (int64_t)atomicAdd((unsigned long long*)a.capm, 1ull);
@@ -257,13 +341,63 @@ __global__ __launch_bounds__(256) void serve_score_kernel(ScoreArgs a) {
   }
 }
 
+// v1 (one launch after the GEMM): sums and scores in the same pass over y.  Each wave walks tiles of 64 pairs
+// with a grid stride and keeps its worst key; the workgroup reports once at the end.
+template <int DT>
+__global__ __launch_bounds__(256) void serve_fused_kernel(ScoreArgs a) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, q = lane & 3;
+  uint32_t sg2[16];
+  lane_signs<DT>(a, q, sg2);
+  LaneBest best;
+  const int64_t tiles = (a.npairs + 63) / 64;
+  for (int64_t tile = (int64_t)blockIdx.x * 4 + w; tile < tiles; tile += (int64_t)gridDim.x * 4) {
+    const int64_t base = tile * 64;
+    float pl, sg, sq, ab;
+    pair_sums<DT>(a, base, lane, sg2, pl, sg, sq, ab);
+    score_pair<DT>(a, base + q * 16 + (lane >> 2), pl, sg, sq, ab, best);
+  }
+  report_wg<DT>(a, best);
+}
+
+// v3, part 1 (concurrent with the GEMM, on a side stream): the four sums of every pair, (4, npairs) fp32.  Each
+// wave walks tiles of 64 pairs with a grid stride, so a workgroup's set-up (the sign pairs) is paid once.
+template <int DT>
+__global__ __launch_bounds__(256) void serve_sums_kernel(ScoreArgs a, float* __restrict__ sums) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, q = lane & 3;
+  uint32_t sg2[16];
+  lane_signs<DT>(a, q, sg2);
+  const int64_t tiles = (a.npairs + 63) / 64;
+  for (int64_t tile = (int64_t)blockIdx.x * 4 + w; tile < tiles; tile += (int64_t)gridDim.x * 4) {
+    const int64_t base = tile * 64;
+    float pl, sg, sq, ab;
+    pair_sums<DT>(a, base, lane, sg2, pl, sg, sq, ab);
+    const int64_t p = base + q * 16 + (lane >> 2);
+    if (p < a.npairs) {
+      sums[p] = pl;
+      sums[a.npairs + p] = sg;
+      sums[2 * a.npairs + p] = sq;
+      sums[3 * a.npairs + p] = ab;
+    }
+  }
+}
+
+// v3, part 2 (after both): pairs scored with a grid stride, one report per workgroup.
+template <int DT>
+__global__ __launch_bounds__(256) void serve_pairs_kernel(ScoreArgs a, const float* __restrict__ sums) {
+  LaneBest best;
+  for (int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x; p < a.npairs; p += (int64_t)gridDim.x * 256)
+    score_pair<DT>(a, p, sums[p], sums[a.npairs + p], sums[2 * a.npairs + p], sums[3 * a.npairs + p], best);
+  report_wg<DT>(a, best);
+}
+
 }  // namespace
 
 extern "C" int64_t sdc_check_static_workspace(int64_t m, int64_t k, int64_t n, int64_t bs) {
   if (m <= 0 || n <= 0 || bs <= 0) return 0;
   const int64_t nb = sdc_cdiv(n, bs), ncols = 2 * nb;
   const int64_t splits = sdc_expected_splits(m, k, ncols);
-  return (splits * m * ncols + splits * 2 * m) * (int64_t)sizeof(float) + 256;
+  // E planes, row-norm planes, then the (4, m * nb) pair sums of the split design
+  return (splits * m * ncols + splits * 2 * m + 4 * m * nb) * (int64_t)sizeof(float) + 512;
 }
 
 extern "C" int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t sxk, const void* y, int64_t sym,
@@ -273,7 +407,9 @@ extern "C" int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t s
                                 const float* bsum, int64_t* state, int counts, int64_t slot, float z,
                                 float abs_floor, int64_t* cap_meta, float* cap_data, int64_t cap_stride,
                                 int64_t cap_w, int64_t cap_tag, int64_t cap_flags, int64_t cap_slots,
-                                void* workspace, int64_t workspace_bytes, float* scores_out, hipStream_t stream) {
+                                void* workspace, int64_t workspace_bytes, float* scores_out, int kernel,
+                                const float* block_consts, hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
   if (m < 0 || n < 0 || k < 0) return SDC_EINVAL;
   if (m == 0 || n == 0) return SDC_OK;                     // nothing to check, not counted (serve.py:435)
   if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EINVAL;
@@ -288,8 +424,9 @@ extern "C" int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t s
   const int64_t splits = sdc_expected_splits(m, k, ncols);
   float* E = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
   float* XN = E + splits * m * ncols;
-  int rc = sdc_expected_launch(dtype, x, sxm, sxk, parts, spk, spc, nparts, m, k, ncols, splits, E, XN, stream);
-  if (rc != SDC_OK) return rc;
+  float* SUMS = (float*)(((uintptr_t)(XN + splits * 2 * m) + 255) & ~(uintptr_t)255);
+  // (the fused persistent pass measured fastest at every batch size on MI355X; v3 stays available on request)
+  const bool split_design = kernel == 3 || kernel == 4;
   const double u = dtype == SDC_BF16 ? 1.0 / 256.0 : 1.0 / 2048.0;
   const double h = dtype == SDC_BF16 ? 0.0 : 1.0 / 33554432.0;             // 2^-25
   const double dmax = dtype == SDC_BF16 ? 3.3895313892515355e38 : 65504.0;
@@ -309,14 +446,48 @@ extern "C" int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t s
   a.capm = cap_meta; a.capd = cap_data; a.cst = cap_stride; a.cw = cap_w; a.ctag = cap_tag; a.cfo = cap_flags;
   a.ncap = cap_slots; a.slot = slot;
   a.zdump = scores_out;
+  a.packed = (const f32x4*)block_consts;
+  if (block_consts && ((uintptr_t)block_consts % 16)) return SDC_EINVAL;
   a.vec = (syn == 1) && (sym % 8 == 0) && (bs % 8 == 0) && ((uintptr_t)y % 16 == 0);
   if (cap_meta && (!cap_data || cap_w < bs)) return SDC_EINVAL;
-  const unsigned grid = (unsigned)sdc_cdiv(m * nb, 256);
+  // persistent grids: about four workgroups per CU (256 CUs), fewer for small batches
+  const int64_t tiles = sdc_cdiv(m * nb, 64);
+  const unsigned grid = (unsigned)(sdc_cdiv(tiles, 4) < 1024 ? sdc_cdiv(tiles, 4) : 1024);
+  if (!split_design) {
+    int rc = sdc_expected_launch(dtype, x, sxm, sxk, parts, spk, spc, nparts, m, k, ncols, splits, E, XN, stream);
+    if (rc != SDC_OK) return rc;
+    SdcProf prof("serve_fused", stream);
+    if (dtype == SDC_BF16)
+      hipLaunchKernelGGL(serve_fused_kernel<SDC_BF16>, dim3(grid), dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL(serve_fused_kernel<SDC_FP16>, dim3(grid), dim3(256), 0, stream, a);
+    SDC_LAUNCH_CHECK();
+    return SDC_OK;
+  }
+  // the block sums of y need nothing from the GEMM: they stream from HBM on a side stream while the GEMM runs
+  // (kernel 4: the same design without the fork, every launch on the caller's stream, for measurements)
+  hipStream_t side = stream;                   // (the caller's stream may be the null stream)
+  if (kernel != 4 && !(side = sdc_fork(stream))) return SDC_ELAUNCH;
+  {
+    SdcProf prof("serve_sums", side);
+    if (dtype == SDC_BF16)
+      hipLaunchKernelGGL(serve_sums_kernel<SDC_BF16>, dim3(grid), dim3(256), 0, side, a, SUMS);
+    else
+      hipLaunchKernelGGL(serve_sums_kernel<SDC_FP16>, dim3(grid), dim3(256), 0, side, a, SUMS);
+    SDC_LAUNCH_CHECK();
+  }
+  int rc = sdc_expected_launch(dtype, x, sxm, sxk, parts, spk, spc, nparts, m, k, ncols, splits, E, XN, stream);
+  if (kernel != 4) {
+    const int jc = sdc_join(stream, side);
+    if (rc == SDC_OK) rc = jc;
+  }
+  if (rc != SDC_OK) return rc;
   SdcProf prof("serve_score", stream);
+  const unsigned pgrid = (unsigned)(sdc_cdiv(m * nb, 1024) < 512 ? sdc_cdiv(m * nb, 1024) : 512);
   if (dtype == SDC_BF16)
-    hipLaunchKernelGGL(serve_score_kernel<SDC_BF16>, dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(serve_pairs_kernel<SDC_BF16>, dim3(pgrid), dim3(256), 0, stream, a, (const float*)SUMS);
   else
-    hipLaunchKernelGGL(serve_score_kernel<SDC_FP16>, dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(serve_pairs_kernel<SDC_FP16>, dim3(pgrid), dim3(256), 0, stream, a, (const float*)SUMS);
   SDC_LAUNCH_CHECK();
   return SDC_OK;
 }

@@ -15,6 +15,7 @@ so torch.compile sees one opaque call and HIP graphs capture its kernels.
 from __future__ import annotations
 
 import math
+import os
 import struct
 import threading
 import time
@@ -120,6 +121,8 @@ class LayerChecksums:
         self.width = width
         self.wsq = width.sqrt()
         self.fingerprint = self._fingerprint(W)
+        for wb in (True, False):
+            _packed_consts(*(self.tensors(wb)[i] for i in (3, 4, 5, 6, 7, 8)))
         for t in self.tensors(True) + self.tensors(False):
             _static(t)
 
@@ -201,10 +204,11 @@ def check_static_impl(x2: torch.Tensor, y2: torch.Tensor, parts: torch.Tensor, p
                       bmax: torch.Tensor, bmax_bias: torch.Tensor, bsum: torch.Tensor, wsq: torch.Tensor,
                       width: torch.Tensor, state: torch.Tensor, slot: int, z: float, abs_floor: float,
                       cap_meta: Optional[torch.Tensor] = None, cap_data: Optional[torch.Tensor] = None,
-                      cap_w: int = 0, cap_tag: int = 0, scores_out: Optional[torch.Tensor] = None) -> None:
+                      cap_w: int = 0, cap_tag: int = 0, scores_out: Optional[torch.Tensor] = None,
+                      kernel: Optional[str] = None) -> None:
     """Check y2 = x2 @ W^T (+ bias) for one layer on the GPU and fold the worst z into state[slot]; with cap_meta
     and cap_data, keep the row that alarmed (serve.py:257-270).  No host sync.  scores_out (tests): a (m, nb, 2)
-    fp32 tensor that receives every checksum's score."""
+    fp32 tensor that receives every checksum's score; kernel ("v1" | "v3") forces one design."""
     m, n = y2.shape
     if m == 0 or n == 0:
         return
@@ -239,8 +243,34 @@ def check_static_impl(x2: torch.Tensor, y2: torch.Tensor, parts: torch.Tensor, p
         row, counts, int(slot), float(z), float(abs_floor),
         cap_meta.data_ptr() if capture else None, cap_data.data_ptr() if capture else None,
         cap_data.stride(0) if capture else 0, int(cap_w), int(cap_tag), CAP_FLAGS, CAPTURE_SLOTS,
-        ws.data_ptr(), ws_bytes, None if scores_out is None else scores_out.data_ptr(), _lib.stream_of(y2))
+        ws.data_ptr(), ws_bytes, None if scores_out is None else scores_out.data_ptr(),
+        kernel_mode() if kernel is None else {"v1": 1, "v3": 3, "v3-serial": 4}[kernel],
+        _packed_consts(scale, b2n, b2max, bmax, bmax_bias, bsum).data_ptr(), _lib.stream_of(y2))
     _lib.check(rc, "sdc_check_static")
+
+
+def _packed_consts(scale, b2n, b2max, bmax, bmax_bias, bsum) -> torch.Tensor:
+    """The per-block constants as one (nb, 12) fp32 table (three 16-byte loads per block in the kernel):
+    [scale, bsum, b2n, b2max, bmax, bmax_bias, 0, 0].  Kept on the bsum tensor object (with and without the
+    bias, LayerChecksums hands different bsum tensors), so it lives exactly as long as the constants it packs."""
+    packed = getattr(bsum, "_sdc_packed", None)
+    if packed is not None and packed[1] == (scale.data_ptr(), bmax_bias.data_ptr(), b2n.data_ptr()):
+        return packed[0]
+    nb = b2n.shape[0]
+    z = torch.zeros(nb, 2, dtype=torch.float32, device=bsum.device)
+    t = torch.cat([scale.view(nb, 2), bsum.view(nb, 2), b2n.view(nb, 2), b2max.view(nb, 2),
+                   torch.stack([bmax.view(nb), bmax_bias.view(nb)], 1), z], dim=1).contiguous()
+    try:
+        bsum._sdc_packed = (t, (scale.data_ptr(), bmax_bias.data_ptr(), b2n.data_ptr()))
+    except (AttributeError, RuntimeError):
+        pass
+    return t
+
+
+def kernel_mode() -> int:
+    """0: the design by batch size; SDCGUARD_SERVE_KERNEL=v1|v3 forces one (_serve_fast.py:600-606)."""
+    v = os.environ.get("SDCGUARD_SERVE_KERNEL", "auto")
+    return {"v1": 1, "v3": 3}.get(v, 0)
 
 
 # the reference routes between its Triton and PyTorch checks here; this build has one implementation

@@ -12,7 +12,11 @@ pytestmark = pytest.mark.gpu
 
 
 def _np(t: torch.Tensor) -> np.ndarray:
-    return t.detach().cpu().contiguous().numpy()
+    """Raw values as numpy (bf16 as its int16 words: numpy has no bf16)."""
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.bfloat16:
+        t = t.view(torch.int16)
+    return t.numpy()
 
 
 def test_fp3_probe_cases_of_the_reference():

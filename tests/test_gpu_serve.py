@@ -30,7 +30,7 @@ def to_dev(a: np.ndarray, dt: str) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(_dt(dt)).cuda()
 
 
-def run_gpu(x, W, b, y, dt, state=None, slot=0, cap=None, with_bias=True):
+def run_gpu(x, W, b, y, dt, state=None, slot=0, cap=None, with_bias=True, kernel=None):
     from sdcguard_amd.serve import STATE_COLS, LayerChecksums, check_static_impl
     xd, Wd, yd = to_dev(x, dt), to_dev(W, dt), to_dev(y, dt)
     bd = to_dev(b, dt) if b is not None else None
@@ -40,7 +40,7 @@ def run_gpu(x, W, b, y, dt, state=None, slot=0, cap=None, with_bias=True):
     zs = torch.full((x.shape[0], cs.nb, 2), -7.0, dtype=torch.float32, device="cuda")
     capm, capd = cap if cap is not None else (None, None)
     check_static_impl(xd, yd, *cs.tensors(with_bias), state, slot, 6.0, 1e-20, capm, capd, 128, 2,
-                      scores_out=zs)
+                      scores_out=zs, kernel=kernel)
     torch.cuda.synchronize()
     return zs.cpu().numpy(), state.cpu().numpy(), cs
 
@@ -58,11 +58,12 @@ def test_mfma_layout_selftest():
     assert torch.allclose(C.cpu().double(), ref, rtol=1e-5, atol=1e-5), (C.cpu() - ref).abs().max()
 
 
+@pytest.mark.parametrize("kernel", ["v1", "v3"])
 @pytest.mark.parametrize("i", range(len(G.names(SERVE))))
-def test_serving_kernel_matches_oracle_and_reference(i):
+def test_serving_kernel_matches_oracle_and_reference(i, kernel):
     name = G.names(SERVE)[i]
     x, W, b, y, dt = serve_case(i)
-    zs, st, cs = run_gpu(x, W, b, y, dt)
+    zs, st, cs = run_gpu(x, W, b, y, dt, kernel=kernel)
     c = serve_check.layer_constants(W, b, 128, dt, seed=1)
     o = serve_check.check_static(x, y, c, dtype=dt, seed=1)
     ok = z_close(zs.reshape(-1), o.z.reshape(-1), gemm_slack(o.csb, o.den).reshape(-1))
@@ -124,7 +125,8 @@ def test_bit_flip_verdicts_match_oracle(m, k, n, dt, bias):
     assert band <= 2, band
 
 
-def test_capture_and_counts():
+@pytest.mark.parametrize("kernel", ["v1", "v3"])
+def test_capture_and_counts(kernel):
     """A row over the line is captured once per layer and read (serve.py:67-88)."""
     from sdcguard_amd.serve import CAP_FLAGS, CAPTURE_SLOTS, STATE_COLS
     x, W, b = _layer(64, 256, 300, seed=9, with_bias=True)
@@ -135,7 +137,7 @@ def test_capture_and_counts():
     state = torch.zeros(4, STATE_COLS, dtype=torch.int64, device="cuda")
     xf, Wf, bf, yf = x.float().numpy(), W.float().numpy(), b.float().numpy(), y.float().numpy()
     for _ in range(2):
-        zs, st, cs = run_gpu(xf, Wf, bf, yf, "bf16", state=state, slot=2, cap=(capm, capd))
+        zs, st, cs = run_gpu(xf, Wf, bf, yf, "bf16", state=state, slot=2, cap=(capm, capd), kernel=kernel)
     assert st[2, 2] == 2                                     # two checks executed
     z, flat, _ = serve_check.decode(st[2, 0], st[2, 1])
     assert z > 6 and (flat // 2) // cs.nb == 40 and (flat // 2) % cs.nb == 1
@@ -176,3 +178,20 @@ def test_llama_mlp_full_size_clean_and_faulty():
     zs, st, _ = run_gpu(xf, Wf, None, yf, "bf16")
     z, flat, _ = serve_check.decode(st[0, 0], st[0, 1])
     assert z > 6 and (flat // 2) // 112 == 1234 and (flat // 2) % 112 == 5678 // 128
+
+
+@pytest.mark.parametrize("scale", [1e-3, 3e-5, 1e-6])
+def test_fp16_subnormal_outputs_match_oracle(scale):
+    """fp16 outputs in the subnormal range (below 6.1e-5): the packed-dot block sums must keep subnormals, and the
+    noise model's half-step term (checksum.py:20-22) must score them as the oracle does."""
+    g = torch.Generator().manual_seed(12)
+    x = (torch.randn(48, 256, generator=g) * scale).half()
+    W = (torch.randn(384, 256, generator=g) * 0.05).half()
+    y = torch.nn.functional.linear(x.float(), W.float()).half()
+    xf, Wf, yf = x.float().numpy(), W.float().numpy(), y.float().numpy()
+    zs, st, _ = run_gpu(xf, Wf, None, yf, "fp16")
+    c = serve_check.layer_constants(Wf, None, 128, "fp16", seed=1)
+    o = serve_check.check_static(xf, yf, c, dtype="fp16", seed=1)
+    ok = z_close(zs.reshape(-1), o.z.reshape(-1), gemm_slack(o.csb, o.den).reshape(-1))
+    assert ok.all(), (np.nonzero(~ok)[0][:5], zs.reshape(-1)[~ok][:5], o.z.reshape(-1)[~ok][:5])
+    assert int(st[0, 3]) == int(o.state[3])
