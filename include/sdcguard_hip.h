@@ -52,6 +52,28 @@ int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t sxk, const v
                      int64_t cap_slots, void* workspace, int64_t workspace_bytes, float* scores_out, int kernel,
                      const float* block_consts, hipStream_t stream);
 
+/* ---- check of one matmul (training / one-off) -------------------------------------------------------------
+ * Replaces checksum.matmul_zscores (checksum.py:400-432, `_zscores` :435-530) and the Triton group it routes to
+ * (_group.Group.add/launch/row, _group.py:749-902): the column-block check of C = beta * bias + alpha * (A @ B)
+ * with B's block sums made on the device for this call, unjudged checksums scoring -1 (checksum.py:346-383).
+ *   A (batch_a, m, k), B (batch_b, k, n), C (batch_c, m, n): element strides per dimension; batch_a / batch_b may
+ *     be 1 (shared) or equal to batch_c (bmm); all of `dtype`.
+ *   bias_kind 0: none; 1: a vector of n (stride sbias_n); 2: a matrix (strides sbias_b, sbias_m, sbias_n; sbias_b
+ *     0 for a 2-D bias shared by the batches) -- addmm / baddbmm biases (checksum.py:471-479).
+ *   sign_table: the 128 x 128 table of the epoch in use (epoch 0: as serving; a later epoch: _group._sign_table).
+ *   result: int64[3], zeroed by the caller: the worst checksum's key (bits of z << 32 | flat index, flat =
+ *     ((batch * m + row) * nb + block) * 2 + signed), the key with its noise, and the number of checksums that
+ *     could not be judged.  Several checks may share no result row.
+ *   workspace: at least sdc_matmul_check_workspace(batch_a, batch_b, m, k, n, bs) bytes.
+ *   scores_out (may be NULL): every checksum's score, (batch_c, m, nb, 2) fp32 (tests). */
+int64_t sdc_matmul_check_workspace(int64_t batch_a, int64_t batch_b, int64_t m, int64_t k, int64_t n, int64_t bs);
+int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, int64_t batch_a,
+                     const void* B, int64_t sbb, int64_t sbk, int64_t sbn, int64_t batch_b, const void* C, int64_t scb,
+                     int64_t scm, int64_t scn, int64_t batch_c, int64_t m, int64_t k, int64_t n, int64_t bs,
+                     const void* bias, int bias_kind, int64_t sbias_b, int64_t sbias_m, int64_t sbias_n, float alpha,
+                     float beta, float z, float abs_floor, const float* sign_table, int64_t* result, void* workspace,
+                     int64_t workspace_bytes, float* scores_out, hipStream_t stream);
+
 /* Depth split the expected-side GEMM uses for an (m x k) @ (k x ncols) product (sizes the workspace). */
 int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
 

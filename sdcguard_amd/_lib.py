@@ -30,6 +30,9 @@ SIGNATURES = {
     "sdc_check_static_workspace": (I64, [I64, I64, I64, I64]),
     "sdc_check_static": (I32, [I32, P, I64, I64, P, I64, I64, I64, I64, I64, I64, P, I64, I64, I32, P, P, P, P, P,
                                P, P, P, I32, I64, F32, F32, P, P, I64, I64, I64, I64, I64, P, I64, P, I32, P, P]),
+    "sdc_matmul_check_workspace": (I64, [I64, I64, I64, I64, I64, I64]),
+    "sdc_matmul_check": (I32, [I32, P, I64, I64, I64, I64, P, I64, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, I64,
+                               I64, P, I32, I64, I64, I64, F32, F32, F32, F32, P, P, P, I64, P, P]),
     "sdc_expected_splits": (I64, [I64, I64, I64]),
     "sdc_fingerprint3": (I32, [P, I64, I32, I64, P, P]),
     "sdc_fingerprint2": (I32, [P, I64, I32, P, P]),

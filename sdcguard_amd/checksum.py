@@ -117,3 +117,137 @@ def _split3(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     mid = r.to(dtype)
     lo = (r - mid).to(dtype)
     return torch.cat([hi, mid, lo], dim=-1)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# The check of one matmul, queued on the GPU (checksum.py:400-432, :695-767 in the reference)
+
+@dataclass
+class CheckStat:
+    """A queued check: its result row on the device plus what decoding it needs (checksum.py:125-133)."""
+    result: torch.Tensor         # [3] int64: worst key (bits of z << 32 | flat), key with its noise, unjudged count
+    m: int
+    nb: int
+    batched: bool
+    z: float
+
+
+def _as3(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dim() == 3 else t.unsqueeze(0)
+
+
+def _dims3(t: torch.Tensor):
+    """(batch, batch stride, rows, cols, row stride, col stride) of a 2-D or 3-D tensor (_group.py:369-373)."""
+    if t.dim() == 3:
+        return t.shape[0], t.stride(0), t.shape[1], t.shape[2], t.stride(1), t.stride(2)
+    return 1, 0, t.shape[0], t.shape[1], t.stride(0), t.stride(1)
+
+
+def matmul_zscores(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, bias: Optional[torch.Tensor] = None, *,
+                   alpha: float = 1.0, beta: float = 1.0, block: int = 128, abs_floor: float = ABS_FLOOR,
+                   z: float = 6.0, epoch: int = 0, out: Optional[torch.Tensor] = None,
+                   scores_out: Optional[torch.Tensor] = None) -> Optional[CheckStat]:
+    """Queue the check of C = beta*bias + alpha*(A @ B) on the GPU without waiting (checksum.py:400-432).  2-D
+    (mm/addmm) or 3-D (bmm/baddbmm).  None when C's dtype isn't bf16/fp16.  `out`: a [3] int64 device tensor of
+    zeros to receive the result (a fresh one otherwise)."""
+    from . import _lib
+    if C.dtype not in UNIT_ROUNDOFF:
+        return None
+    if C.numel() == 0:
+        raise ValueError("empty output: nothing to check (callers skip these, see is_empty)")
+    _lib.require_gpu(A, B, C, bias)
+    dt = C.dtype
+    if A.shape[-1] == 0:                                   # checksum.py:386-392: one zero column
+        A = A.new_zeros(*A.shape[:-1], 1)
+        B = B.new_zeros(*B.shape[:-2], 1, B.shape[-1])
+    A = A if A.dtype == dt else A.to(dt)
+    B = B if B.dtype == dt else B.to(dt)
+    ba, sab, m, k, sam, sak = _dims3(A)
+    bb, sbb, kb, n, sbk, sbn = _dims3(B)
+    bc, scb, mc, nc, scm, scn = _dims3(C)
+    if mc != m or kb != k or nc != n:
+        raise ValueError(f"shape mismatch: A{tuple(A.shape)} B{tuple(B.shape)} C{tuple(C.shape)}")
+    nbt = max(ba, bb)
+    if bc != nbt and not (ba == 1 and bb == 1):
+        raise ValueError(f"batch mismatch: A{tuple(A.shape)} B{tuple(B.shape)} C{tuple(C.shape)}")
+    if ba == 1 and bb == 1 and bc > 1:                    # (a batched C of a 2-D product: check each batch)
+        raise ValueError("a 3-D output needs 3-D operands")
+    bs = max(1, min(block, n))
+    if bs > 128:
+        raise _lib.HipLibraryError(f"blocks up to 128 wide, not {bs}")
+    kind, b_ptr, sb_b, sb_m, sb_n = 0, None, 0, 0, 0
+    if bias is not None and beta != 0:
+        bias = bias if bias.dtype == dt else bias.to(dt)
+        if bias.dim() == 1 and bias.numel() in (1, n):
+            kind, b_ptr, sb_n = 1, bias, (0 if bias.numel() == 1 else bias.stride(0))
+        else:
+            full = torch.broadcast_to(bias, (bc, m, n)) if bias.dim() == 3 or C.dim() == 3 else \
+                torch.broadcast_to(bias, (m, n)).unsqueeze(0)
+            kind, b_ptr = 2, full
+            sb_b, sb_m, sb_n = full.stride(0) if C.dim() == 3 else 0, full.stride(1), full.stride(2)
+    if out is None:
+        out = torch.zeros(3, dtype=torch.int64, device=C.device)
+    L = _lib.lib()
+    ws_bytes = int(L.sdc_matmul_check_workspace(ba, bb, m, k, n, bs))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=C.device)
+    rc = L.sdc_matmul_check(
+        _lib.dtype_code(dt), A.data_ptr(), sab, sam, sak, ba, B.data_ptr(), sbb, sbk, sbn, bb,
+        C.data_ptr(), scb, scm, scn, bc, m, k, n, bs, None if b_ptr is None else b_ptr.data_ptr(), kind,
+        sb_b, sb_m, sb_n, float(alpha), float(beta), float(z), float(abs_floor),
+        sign_table(C.device, epoch).data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
+        None if scores_out is None else scores_out.data_ptr(), _lib.stream_of(C))
+    _lib.check(rc, "sdc_matmul_check")
+    nb = -(-n // bs)
+    return CheckStat(result=out, m=m, nb=nb, batched=C.dim() == 3, z=float(z))
+
+
+def _f32_of_bits(b: int) -> float:
+    import struct
+    return struct.unpack("<f", struct.pack("<I", b & 0xFFFFFFFF))[0]
+
+
+def resolve(stats, z: float = 6.0) -> list:
+    """Read queued checks back (one transfer per device for all of them) and decode them (checksum.py:695-725)."""
+    if not stats:
+        return []
+    rows = [None] * len(stats)
+    by_device: dict = {}
+    for i, s in enumerate(stats):
+        by_device.setdefault(s.result.device, []).append(i)
+    for idx in by_device.values():
+        host = torch.stack([stats[i].result for i in idx]).cpu().tolist()
+        for j, i in enumerate(idx):
+            rows[i] = host[j]
+    out = []
+    for s, (key, keyd, unjudged) in zip(stats, rows):
+        mz = _f32_of_bits(key >> 32)
+        flat = key & 0xFFFFFFFF
+        noise = _f32_of_bits(keyd)
+        if unjudged and mz <= z:                          # checksum.py:349-356
+            mz = UNJUDGED
+        blk = flat // 2
+        b_i, rem = divmod(blk, s.m * s.nb)
+        r_i, c_i = divmod(rem, s.nb)
+        finite = math.isfinite(mz)
+        out.append(CheckResult(ok=finite and mz <= z, max_z=mz, nonfinite=not finite,
+                               batch=b_i if s.batched else None, row=r_i, col_block=c_i, noise=noise))
+    return out
+
+
+def is_empty(C: torch.Tensor) -> bool:
+    return C.numel() == 0
+
+
+def check_matmul(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, bias: Optional[torch.Tensor] = None, *,
+                 alpha: float = 1.0, beta: float = 1.0, block: int = 128, z: float = 6.0,
+                 abs_floor: float = ABS_FLOOR, epoch: int = 0) -> Optional[CheckResult]:
+    """Check C = beta*bias + alpha*(A @ B) and answer now (checksum.py:728-760).  None if the dtype is unsupported."""
+    if is_empty(C) and C.dtype in UNIT_ROUNDOFF:
+        return CheckResult(ok=True, max_z=0.0, nonfinite=False)
+    st = matmul_zscores(A, B, C, bias, alpha=alpha, beta=beta, block=block, abs_floor=abs_floor, z=z, epoch=epoch)
+    return None if st is None else resolve([st], z)[0]
+
+
+def check_linear(x, weight, bias, y, **kw) -> Optional[CheckResult]:
+    """Check y = torch.nn.functional.linear(x, weight, bias) for any leading dims (checksum.py:763-767)."""
+    return check_matmul(x.reshape(-1, x.shape[-1]), weight.t(), y.reshape(-1, y.shape[-1]), bias, **kw)

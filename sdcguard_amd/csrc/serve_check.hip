@@ -9,7 +9,7 @@
 //      of squares, of |values|) and add them up with two DPP steps; over four rounds each lane keeps one pair's
 //      sums, then scores it with the reference's noise model.  The workgroup's worst key goes into the layer's
 //      state row with one integer atomic maximum (only when it raises the row), counts with atomic adds.
-#include "common.h"
+#include "blocksums.h"
 #include "profile.h"
 #include "streams.h"
 
@@ -21,6 +21,7 @@ extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
 namespace {
 
 struct ScoreArgs {
+  YView yv;
   const uint16_t* x; int64_t sxm, sxk;
   const uint16_t* y; int64_t sym, syn;
   int64_t m, k, n, nb, bs, rem, npairs;
@@ -42,12 +43,6 @@ struct PairScore {
   bool sec;
   int unk;
 };
-
-// Division and square root by the hardware's reciprocal and square-root approximations (about 1 ulp): the scores
-// only need to agree with the reference's to 1e-3 of the noise, and the special cases keep their IEEE results
-// (x / 0 = inf, 0 / 0 = NaN, inf / inf = NaN, sqrt(inf) = inf, sqrt(NaN) = NaN).
-__device__ __forceinline__ float fdiv(float a, float b) { return a * __builtin_amdgcn_rcpf(b); }
-__device__ __forceinline__ float fsqrt(float a) { return __builtin_amdgcn_sqrtf(a); }
 
 // _serve_fast.py:334-402 (`_judge`) for one (row, block) pair, serving flavour (unjudged checksums score 0).
 __device__ __forceinline__ PairScore judge_serve(float plain, float sgn, float sq, float l1, float xn, float asum,
@@ -114,106 +109,6 @@ __device__ __forceinline__ PairScore judge_serve(float plain, float sgn, float s
   r.dc = r.sec ? (a_bad1 ? nanv : den1) : (a_bad0 ? nanv : den0);
   r.unk = (int)unk0 + (int)unk1;
   return r;
-}
-
-// Four sums of 8 elements (one 16-byte load) with packed dot products: v_dot2_f32_{bf16,f16} adds two products
-// to an fp32 accumulator, so each instruction takes two elements: plain sum (x . 1), signed sum (x . s), sum of
-// squares (x . x) and sum of |x| (|x| . 1).  `sg2` holds the four sign pairs of these eight columns.
-template <int DT>
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  if constexpr (DT == SDC_BF16) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
-  } else {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
-  }
-}
-
-template <int DT>
-__device__ __forceinline__ void acc8(u32x4 v, const uint32_t* sg2, float& pl, float& sg, float& sq, float& ab) {
-  constexpr uint32_t ONES = DT == SDC_BF16 ? 0x3F803F80u : 0x3C003C00u;
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    pl = dot2<DT>(w[i], ONES, pl);
-    sg = dot2<DT>(w[i], sg2[i], sg);
-    sq = dot2<DT>(w[i], w[i], sq);
-    ab = dot2<DT>(w[i] & 0x7FFF7FFFu, ONES, ab);
-  }
-}
-
-// The four sums of the (row, block) pair each lane keeps: a wave reads 64 consecutive pairs starting at `base`;
-// lane l ends up with pair base + (l & 3) * 16 + (l >> 2).  Four lanes share a pair in each of four rounds; all
-// sixteen 16-byte loads are issued before any is used (256 bytes per lane in flight).  Pairs that are not full
-// 128-wide vector-loadable blocks (a narrower last block, strided y) take an element-wise path.
-template <int DT>
-__device__ __forceinline__ void pair_sums(const ScoreArgs& a, int64_t base, int lane, const uint32_t* sg2, float& my_pl,
-                                          float& my_sg, float& my_sq, float& my_ab) {
-  const int q = lane & 3;
-  bool full[4];
-  u32x4 v[4][4];
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int64_t p = base + g * 16 + (lane >> 2);
-    full[g] = false;
-    if (p < a.npairs && a.vec) {
-      const uint32_t r = (uint32_t)p / (uint32_t)a.nb, jb = (uint32_t)p - r * (uint32_t)a.nb;
-      const bool last = (jb == a.nb - 1) && (a.rem > 0);
-      if (!last && a.bs == 128) {
-        full[g] = true;
-        const uint16_t* yr = a.y + (int64_t)r * a.sym + (int64_t)jb * 128;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          v[g][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(yr + 8 * (q + 4 * j)));
-      }
-    }
-  }
-  my_pl = my_sg = my_sq = my_ab = 0.f;
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int64_t p = base + g * 16 + (lane >> 2);
-    float pl = 0.f, sg = 0.f, sq = 0.f, ab = 0.f;
-    if (full[g]) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc8<DT>(v[g][j], &sg2[j * 4], pl, sg, sq, ab);
-    } else if (p < a.npairs) {
-      const int64_t r = (uint32_t)p / (uint32_t)a.nb, jb = (uint32_t)p - (uint32_t)r * (uint32_t)a.nb;
-      const bool last = (jb == a.nb - 1) && (a.rem > 0);
-      const int64_t wid = last ? a.rem : a.bs;
-      const uint16_t* yr = a.y + r * a.sym + jb * a.bs * a.syn;
-      const float* sp = last ? a.s_last : a.s_full;
-#pragma unroll 1
-      for (int j = 0; j < 4; ++j)
-#pragma unroll 1
-        for (int e = 0; e < 8; ++e) {
-          const int c = 8 * (q + 4 * j) + e;
-          if (c < wid) {
-            float x = half_to_f32<DT>(yr[c * a.syn]);
-            pl += x;
-            sg = fmaf(x, sp[c], sg);
-            sq = fmaf(x, x, sq);
-            ab += fabsf(x);
-          }
-        }
-    }
-    pl = quad_sum(pl); sg = quad_sum(sg); sq = quad_sum(sq); ab = quad_sum(ab);
-    if (q == g) { my_pl = pl; my_sg = sg; my_sq = sq; my_ab = ab; }
-  }
-}
-
-// The signs of this lane's 32 columns of a full block (chunks q, q+4, q+8, q+12 of 8 columns) as packed pairs; a
-// table row holds 128 entries (zeros past its width), so these loads need no bounds test.
-template <int DT>
-__device__ __forceinline__ void lane_signs(const ScoreArgs& a, int q, uint32_t* sg2) {
-  constexpr uint32_t POS = DT == SDC_BF16 ? 0x3F80u : 0x3C00u, NEG = DT == SDC_BF16 ? 0xBF80u : 0xBC00u;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const f32x4 s0 = *reinterpret_cast<const f32x4*>(a.s_full + 8 * (q + 4 * j));
-    const f32x4 s1 = *reinterpret_cast<const f32x4*>(a.s_full + 8 * (q + 4 * j) + 4);
-    sg2[j * 4 + 0] = (s0.x < 0.f ? NEG : POS) | ((s0.y < 0.f ? NEG : POS) << 16);
-    sg2[j * 4 + 1] = (s0.z < 0.f ? NEG : POS) | ((s0.w < 0.f ? NEG : POS) << 16);
-    sg2[j * 4 + 2] = (s1.x < 0.f ? NEG : POS) | ((s1.y < 0.f ? NEG : POS) << 16);
-    sg2[j * 4 + 3] = (s1.z < 0.f ? NEG : POS) | ((s1.w < 0.f ? NEG : POS) << 16);
-  }
 }
 
 // Scores this lane's pairs (NP of them: p0, p0 + 256, ...; those >= npairs are skipped) from their four sums, then
@@ -347,13 +242,13 @@ template <int DT>
 __global__ __launch_bounds__(256) void serve_fused_kernel(ScoreArgs a) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, q = lane & 3;
   uint32_t sg2[16];
-  lane_signs<DT>(a, q, sg2);
+  lane_signs<DT>(a.yv, q, sg2);
   LaneBest best;
   const int64_t tiles = (a.npairs + 63) / 64;
   for (int64_t tile = (int64_t)blockIdx.x * 4 + w; tile < tiles; tile += (int64_t)gridDim.x * 4) {
     const int64_t base = tile * 64;
     float pl, sg, sq, ab;
-    pair_sums<DT>(a, base, lane, sg2, pl, sg, sq, ab);
+    pair_sums<DT>(a.yv, base, lane, sg2, pl, sg, sq, ab);
     score_pair<DT>(a, base + q * 16 + (lane >> 2), pl, sg, sq, ab, best);
   }
   report_wg<DT>(a, best);
@@ -365,12 +260,12 @@ template <int DT>
 __global__ __launch_bounds__(256) void serve_sums_kernel(ScoreArgs a, float* __restrict__ sums) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, q = lane & 3;
   uint32_t sg2[16];
-  lane_signs<DT>(a, q, sg2);
+  lane_signs<DT>(a.yv, q, sg2);
   const int64_t tiles = (a.npairs + 63) / 64;
   for (int64_t tile = (int64_t)blockIdx.x * 4 + w; tile < tiles; tile += (int64_t)gridDim.x * 4) {
     const int64_t base = tile * 64;
     float pl, sg, sq, ab;
-    pair_sums<DT>(a, base, lane, sg2, pl, sg, sq, ab);
+    pair_sums<DT>(a.yv, base, lane, sg2, pl, sg, sq, ab);
     const int64_t p = base + q * 16 + (lane >> 2);
     if (p < a.npairs) {
       sums[p] = pl;
@@ -445,10 +340,13 @@ extern "C" int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t s
   a.capk = (float)(1.02 + (double)k * 2.384185791015625e-07);
   a.capm = cap_meta; a.capd = cap_data; a.cst = cap_stride; a.cw = cap_w; a.ctag = cap_tag; a.cfo = cap_flags;
   a.ncap = cap_slots; a.slot = slot;
+  a.yv.y = a.y; a.yv.sb = 0; a.yv.sm = sym; a.yv.sn = syn; a.yv.m = m; a.yv.nb = nb; a.yv.bs = bs;
+  a.yv.rem = rem; a.yv.npairs = m * nb; a.yv.s_full = a.s_full; a.yv.s_last = a.s_last;
   a.zdump = scores_out;
   a.packed = (const f32x4*)block_consts;
   if (block_consts && ((uintptr_t)block_consts % 16)) return SDC_EINVAL;
   a.vec = (syn == 1) && (sym % 8 == 0) && (bs % 8 == 0) && ((uintptr_t)y % 16 == 0);
+  a.yv.vec = a.vec;
   if (cap_meta && (!cap_data || cap_w < bs)) return SDC_EINVAL;
   // persistent grids: about four workgroups per CU (256 CUs), fewer for small batches
   const int64_t tiles = sdc_cdiv(m * nb, 64);

@@ -1,0 +1,479 @@
+// Column-block check of one matmul C = beta * bias + alpha * (A @ B), answered on the device (the training check).
+//
+// Reference: checksum.py:435-530 (`_zscores`: the arithmetic), :349-383 (`_complete_score`, `_judge_nonfinite`:
+// the Inf/NaN rules with unjudged checksums scoring -1), _group.py:386-746 (the device version it replaces: B-side
+// stage, comparison, worst-z search).  Four launches, no host synchronisation:
+//   1. b_stage: the plain and signed block sums of every row of B (B2, fp32, stored transposed so the GEMM reads
+//      depth-contiguous columns) and, per 64-row slice, partial sums of squares / maxima of B2's columns and the
+//      largest |B| of every block;
+//   2. b_finish: those partials added up (|checksum column|_2, its largest entry, the per-column power of two that
+//      keeps fp16 parts in range, the block's largest |B|) and the bias vector's block sums;
+//   3. expected_gemm (expected_gemm.hip): E = A @ B2 from three on-the-fly parts, plus A's row norms;
+//   4. train_score: one persistent pass over C scoring every (batch, row, block) pair, worst key and unjudged count
+//      into the check's result row with atomics.
+#include "blocksums.h"
+#include "gemm.h"
+#include "profile.h"
+
+extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
+
+namespace {
+
+constexpr int BROWS = 64;          // rows of B per b_stage workgroup
+constexpr int NSTAT = 5;           // partial stats per (slice, block): sq0, sq1, max0, max1, bmax
+
+struct BStageArgs {
+  const uint16_t* B;
+  int64_t sbb, sbk, sbn;
+  int64_t k, n, nb, bs, rem, nkc;
+  const float* s_full;
+  const float* s_last;
+  float* B2T;                      // [bB][2nb][k]
+  float* part;                     // [bB][nkc][nb][NSTAT]
+  int vec;
+};
+
+__device__ __forceinline__ float nan_inf(float v) { return v == v ? fabsf(v) : __builtin_inff(); }
+
+template <int DT>
+__global__ __launch_bounds__(256) void b_stage_kernel(BStageArgs a) {
+  __shared__ float red[4][NSTAT];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, q = t & 3;
+  const int64_t kc = blockIdx.x, jb = blockIdx.y, bb = blockIdx.z;
+  const int64_t kk = kc * BROWS + (t >> 2);
+  const bool last = (jb == a.nb - 1) && (a.rem > 0);
+  const int64_t wid = last ? a.rem : a.bs;
+  const float* sp = last ? a.s_last : a.s_full;
+  float pl = 0.f, sg = 0.f, mx = 0.f;
+  if (kk < a.k) {
+    const uint16_t* row = a.B + bb * a.sbb + kk * a.sbk + jb * a.bs * a.sbn;
+    if (a.vec && wid == 128) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c0 = 8 * (q + 4 * j);
+        const u32x4 v = *reinterpret_cast<const u32x4*>(row + c0);
+        const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp + c0);
+        const f32x4 s1 = *reinterpret_cast<const f32x4*>(sp + c0 + 4);
+        const float x[8] = {lo_of<DT>(v.x), hi_of<DT>(v.x), lo_of<DT>(v.y), hi_of<DT>(v.y),
+                            lo_of<DT>(v.z), hi_of<DT>(v.z), lo_of<DT>(v.w), hi_of<DT>(v.w)};
+        const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          pl += x[e];
+          sg = fmaf(x[e], s[e], sg);
+          mx = fmaxf(mx, nan_inf(x[e]));
+        }
+      }
+    } else {
+#pragma unroll 1
+      for (int j = 0; j < 4; ++j)
+#pragma unroll 1
+        for (int e = 0; e < 8; ++e) {
+          const int c = 8 * (q + 4 * j) + e;
+          if (c < wid) {
+            const float x = half_to_f32<DT>(row[c * a.sbn]);
+            pl += x;
+            sg = fmaf(x, sp[c], sg);
+            mx = fmaxf(mx, nan_inf(x));
+          }
+        }
+    }
+  }
+  pl = quad_sum(pl);
+  sg = quad_sum(sg);
+  mx = fmaxf(mx, dpp_xor1(mx));
+  mx = fmaxf(mx, dpp_xor2(mx));
+  const bool mine = q == 0 && kk < a.k;
+  if (mine) {
+    float* col = a.B2T + (bb * 2 * a.nb + 2 * jb) * a.k;
+    col[kk] = pl;
+    col[a.k + kk] = sg;
+  }
+  // this slice's partial |column|^2, largest |entry| of both checksum columns, largest |B| of the block
+  float st[NSTAT] = {mine ? pl * pl : 0.f, mine ? sg * sg : 0.f, mine ? nan_inf(pl) : 0.f, mine ? nan_inf(sg) : 0.f,
+                     mine ? mx : 0.f};
+#pragma unroll
+  for (int i = 0; i < NSTAT; ++i) {
+    float v = st[i];
+#pragma unroll
+    for (int msk = 1; msk < 64; msk <<= 1) {
+      const float o = __shfl_xor(v, msk, 64);
+      v = i < 2 ? v + o : fmaxf(v, o);
+    }
+    if (lane == 0) red[w][i] = v;
+  }
+  __syncthreads();
+  if (t < NSTAT) {
+    float v = red[0][t];
+    for (int i = 1; i < 4; ++i) v = t < 2 ? v + red[i][t] : fmaxf(v, red[i][t]);
+    a.part[((bb * a.nkc + kc) * a.nb + jb) * NSTAT + t] = v;
+  }
+}
+
+struct BFinishArgs {
+  const float* part;
+  int64_t nkc, nb, bs, rem;
+  int fp16;
+  float* colstat;                  // [bB][2nb][3]: |column|_2, largest |entry|, power-of-two scale
+  float* bmaxf;                    // [bB][nb]
+  const uint16_t* bias;            // vector bias (n,) or null
+  int64_t sbias;
+  const float* s_full;
+  const float* s_last;
+  float* bias_out;                 // [nb][3]: plain sum, signed sum, largest |value|
+};
+
+// ceil(log2 x) as a power of two, exactly (frexp: x = f 2^e, f in [0.5, 1))
+__device__ __forceinline__ float pow2_ceil(float x) {
+  int e;
+  const float f = frexpf(x, &e);
+  return ldexpf(1.f, f == 0.5f ? e - 1 : e);
+}
+
+template <int DT>
+__global__ __launch_bounds__(64) void b_finish_kernel(BFinishArgs a) {
+  const int lane = threadIdx.x;
+  const int64_t jb = blockIdx.x, bb = blockIdx.y;
+  float st[NSTAT] = {0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int64_t kc = lane; kc < a.nkc; kc += 64) {
+    const float* p = a.part + ((bb * a.nkc + kc) * a.nb + jb) * NSTAT;
+    st[0] += p[0];
+    st[1] += p[1];
+    st[2] = fmaxf(st[2], p[2]);
+    st[3] = fmaxf(st[3], p[3]);
+    st[4] = fmaxf(st[4], p[4]);
+  }
+#pragma unroll
+  for (int i = 0; i < NSTAT; ++i)
+#pragma unroll
+    for (int msk = 1; msk < 64; msk <<= 1) {
+      const float o = __shfl_xor(st[i], msk, 64);
+      st[i] = i < 2 ? st[i] + o : fmaxf(st[i], o);
+    }
+  if (lane == 0) {
+    float* cs = a.colstat + (bb * 2 * a.nb + 2 * jb) * 3;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const float amax = st[2 + c];
+      cs[3 * c + 0] = sqrtf(st[c]);
+      cs[3 * c + 1] = amax;
+      // fp16 parts stay in range divided by a power of two (checksum._matmul_fp32); bf16 needs none
+      cs[3 * c + 2] = (a.fp16 && amax > 0.f && amax < __builtin_inff()) ? pow2_ceil(amax) : 1.f;
+    }
+    a.bmaxf[bb * a.nb + jb] = st[4];
+  }
+  if (a.bias && bb == 0) {
+    const bool last = (jb == a.nb - 1) && (a.rem > 0);
+    const int64_t wid = last ? a.rem : a.bs;
+    const float* sp = last ? a.s_last : a.s_full;
+    float pl = 0.f, sg = 0.f, mx = 0.f;
+    for (int64_t c = lane; c < wid; c += 64) {
+      const float x = half_to_f32<DT>(a.bias[(jb * a.bs + c) * a.sbias]);
+      pl += x;
+      sg = fmaf(x, sp[c], sg);
+      mx = fmaxf(mx, nan_inf(x));
+    }
+#pragma unroll
+    for (int msk = 1; msk < 64; msk <<= 1) {
+      pl += __shfl_xor(pl, msk, 64);
+      sg += __shfl_xor(sg, msk, 64);
+      mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+    }
+    if (lane == 0) {
+      a.bias_out[3 * jb] = pl;
+      a.bias_out[3 * jb + 1] = sg;
+      a.bias_out[3 * jb + 2] = mx;
+    }
+  }
+}
+
+struct TrainArgs {
+  YView cv;                        // C
+  int64_t k, splits, nbt, ncols;
+  int b_batched;                   // B (and its stats) has one entry per batch
+  int e_batched;                   // E / XN have one plane set per batch
+  const float* E;
+  const float* XN;
+  const float* colstat;
+  const float* bmaxf;
+  int bias_kind;                   // 0 none, 1 vector (block sums in bias_vec), 2 matrix (read per pair)
+  const float* bias_vec;
+  const uint16_t* bias_mat;
+  int64_t sbias_b, sbias_m, sbias_n;
+  float alpha, beta, u, h, abs_floor, l1c, zt, lim_a, capk;
+  int64_t* result;                 // [key, key of the noise, unjudged]
+  float* zdump;
+};
+
+struct TrainBest {
+  int64_t key = 0, keyd = 0;
+  int unk = 0;
+};
+
+// one checksum of checksum._zscores + _judge_nonfinite (unjudged = -1)
+__device__ __forceinline__ float judge_one(float expected, float actual, float noise, float cn, float fl, float bound,
+                                           float wf, float l1, bool plain, const TrainArgs& a, float& den) {
+  const float inf = __builtin_inff();
+  const float swf = fsqrt(wf);
+  den = (noise + fl) + (a.abs_floor + swf * a.h);
+  const float diff = fabsf(expected - actual);
+  float z = fdiv(diff, den);
+  if (plain) {
+    const float worst = ((l1 * (1.25f * a.u) + 1.25f * wf * a.h) + fl) + a.abs_floor;
+    const float zw = fdiv(diff, worst) * a.zt;
+    z = (z == z && zw == zw) ? fminf(z, zw) : __builtin_nanf("");
+  }
+  const bool e_bad = !(fabsf(expected) < inf);
+  const bool a_bad = !(fabsf(actual) < inf) && !e_bad;
+  const bool big = !(noise < inf) && !e_bad && !a_bad;
+  const float lim = bound * 1.01f;
+  z = z == z ? z : -1.f;
+  z = e_bad ? -1.f : z;
+  const float cap = bound * a.capk + 2.f * a.h;
+  const bool imposs = !e_bad && !a_bad && !big && (lim < 1e18f) && (cn > cap * swf);
+  z = imposs ? inf : z;
+  z = a_bad ? (lim < a.lim_a ? inf : -1.f) : z;
+  z = big ? (lim < 1e18f ? inf : -1.f) : z;
+  return z;
+}
+
+template <int DT>
+__device__ __forceinline__ void train_pair(const TrainArgs& a, int64_t p, float pl, float sg, float sq, float l1,
+                                           TrainBest& best) {
+  if (p >= a.cv.npairs) return;
+  int64_t bc, r, jb;
+  pair_index(a.cv, p, bc, r, jb);
+  const bool last = (jb == a.cv.nb - 1) && (a.cv.rem > 0);
+  const float wf = (float)(last ? a.cv.rem : a.cv.bs);
+  const int64_t eb = a.e_batched ? bc : 0, bbi = a.b_batched ? bc : 0;
+  const float* ep = a.E + ((eb * a.splits) * a.cv.m + r) * a.ncols + 2 * jb;
+  const float* xp = a.XN + (eb * a.splits) * 2 * a.cv.m + r;
+  const int64_t estep = a.cv.m * a.ncols, xstep = 2 * a.cv.m;
+  float2 ev[SDC_MAX_SPLITS];
+  float xa[SDC_MAX_SPLITS], xb[SDC_MAX_SPLITS];
+#pragma unroll
+  for (int s = 0; s < SDC_MAX_SPLITS; ++s)
+    if (s < a.splits) {
+      ev[s] = *reinterpret_cast<const float2*>(ep + s * estep);
+      xa[s] = xp[s * xstep];
+      xb[s] = xp[s * xstep + a.cv.m];
+    }
+  float e0 = ev[0].x, e1 = ev[0].y, asq = xa[0], asum = xb[0];
+#pragma unroll
+  for (int s = 1; s < SDC_MAX_SPLITS; ++s)
+    if (s < a.splits) {
+      e0 += ev[s].x;
+      e1 += ev[s].y;
+      asq += xa[s];
+      asum += xb[s];
+    }
+  const float* cs = a.colstat + (bbi * a.ncols + 2 * jb) * 3;
+  e0 *= cs[2];                                   // the parts were made from B2 / scale
+  e1 *= cs[5];
+  float bound = asum * a.bmaxf[bbi * a.cv.nb + jb];
+  if (a.alpha != 1.f) {
+    e0 *= a.alpha;
+    e1 *= a.alpha;
+    bound *= fabsf(a.alpha);
+  }
+  if (a.bias_kind == 1) {
+    e0 = e0 + a.bias_vec[3 * jb] * a.beta;
+    e1 = e1 + a.bias_vec[3 * jb + 1] * a.beta;
+    bound = bound + fabsf(a.beta) * a.bias_vec[3 * jb + 2];
+  } else if (a.bias_kind == 2) {
+    const uint16_t* br = a.bias_mat + bc * a.sbias_b + r * a.sbias_m + jb * a.cv.bs * a.sbias_n;
+    const float* sp = last ? a.cv.s_last : a.cv.s_full;
+    float bp = 0.f, bsg = 0.f, bmx = 0.f;
+    for (int64_t c = 0; c < (int64_t)wf; ++c) {
+      const float x = half_to_f32<DT>(br[c * a.sbias_n]);
+      bp += x;
+      bsg = fmaf(x, sp[c], bsg);
+      bmx = fmaxf(bmx, nan_inf(x));
+    }
+    e0 = e0 + bp * a.beta;
+    e1 = e1 + bsg * a.beta;
+    bound = bound + fabsf(a.beta) * bmx;
+  }
+  const float cn = fsqrt(sq);
+  const float noise = cn * a.u;
+  const float xn = fsqrt(asq), aal = fabsf(a.alpha);
+  float fl[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const float f_l2 = (xn * cs[3 * c]) * (1e-5f * aal);
+    const float f_l1 = (asum * cs[3 * c + 1]) * (a.l1c * aal);
+    const float inf = __builtin_inff();
+    float f = fminf(fabsf(f_l2) < inf ? f_l2 : inf, fabsf(f_l1) < inf ? f_l1 : inf);
+    fl[c] = f < inf ? f : bound * (float)(1e-5 * 128.0);
+  }
+  float d0, d1;
+  const float z0 = judge_one(e0, pl, noise, cn, fl[0], bound, wf, l1, true, a, d0);
+  const float z1 = judge_one(e1, sg, noise, cn, fl[1], bound, wf, l1, false, a, d1);
+  if (a.zdump) {
+    a.zdump[2 * p] = z0;
+    a.zdump[2 * p + 1] = z1;
+  }
+  best.unk += (z0 < 0.f) + (z1 < 0.f);
+  const bool sec = z1 > z0;
+  const float zc = sec ? z1 : z0;
+  const int64_t zb = fbits64(fmaxf(zc, 0.f));
+  const int64_t flat = p * 2 + (sec ? 1 : 0);
+  const int64_t k1 = (zb << 32) | (flat & 0xFFFFFFFFll);
+  const int64_t k2 = (zb << 32) | (fbits64(sec ? d1 : d0) & 0xFFFFFFFFll);
+  best.key = k1 > best.key ? k1 : best.key;
+  best.keyd = k2 > best.keyd ? k2 : best.keyd;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void train_score_kernel(TrainArgs a) {
+  __shared__ int64_t red_k[4], red_d[4];
+  __shared__ int red_u[4];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, q = lane & 3;
+  uint32_t sg2[16];
+  lane_signs<DT>(a.cv, q, sg2);
+  TrainBest best;
+  const int64_t tiles = (a.cv.npairs + 63) / 64;
+  for (int64_t tile = (int64_t)blockIdx.x * 4 + w; tile < tiles; tile += (int64_t)gridDim.x * 4) {
+    const int64_t base = tile * 64;
+    float pl, sg, sq, ab;
+    pair_sums<DT>(a.cv, base, lane, sg2, pl, sg, sq, ab);
+    train_pair<DT>(a, base + q * 16 + (lane >> 2), pl, sg, sq, ab, best);
+  }
+  int64_t key = wave_max_i64(best.key), keyd = wave_max_i64(best.keyd);
+  int unk = wave_sum_i32(best.unk);
+  if (lane == 0) { red_k[w] = key; red_d[w] = keyd; red_u[w] = unk; }
+  __syncthreads();
+  if (t == 0) {
+    int64_t k0 = red_k[0], d0 = red_d[0];
+    int un = red_u[0];
+    for (int i = 1; i < 4; ++i) {
+      k0 = red_k[i] > k0 ? red_k[i] : k0;
+      d0 = red_d[i] > d0 ? red_d[i] : d0;
+      un += red_u[i];
+    }
+    int64_t* res = a.result;
+    const int64_t s0 = __atomic_load_n(res, __ATOMIC_RELAXED), s1 = __atomic_load_n(res + 1, __ATOMIC_RELAXED);
+    if (k0 > s0) atomicMax((unsigned long long*)res, (unsigned long long)k0);
+    if (d0 > s1) atomicMax((unsigned long long*)(res + 1), (unsigned long long)d0);
+    if (un > 0) atomicAdd((unsigned long long*)(res + 2), (unsigned long long)un);
+  }
+}
+
+struct Layout {
+  int64_t nb, rem, ncols, nkc, splits, nbt;
+  int64_t off_b2t, off_part, off_col, off_bmax, off_bias, off_e, off_xn, total;
+};
+
+Layout layout(int64_t batch_a, int64_t batch_b, int64_t m, int64_t k, int64_t n, int64_t bs) {
+  Layout L{};
+  L.nb = sdc_cdiv(n, bs);
+  L.rem = n % bs;
+  L.ncols = 2 * L.nb;
+  L.nkc = sdc_cdiv(k, BROWS);
+  L.nbt = batch_a > batch_b ? batch_a : batch_b;
+  L.splits = sdc_expected_splits(m, k, L.ncols);
+  auto al = [](int64_t x) { return (x + 63) / 64 * 64; };   // floats, 256-byte aligned sections
+  int64_t o = 0;
+  L.off_b2t = o; o += al(batch_b * L.ncols * k);
+  L.off_part = o; o += al(batch_b * L.nkc * L.nb * NSTAT);
+  L.off_col = o; o += al(batch_b * L.ncols * 3);
+  L.off_bmax = o; o += al(batch_b * L.nb);
+  L.off_bias = o; o += al(3 * L.nb);
+  L.off_e = o; o += al(L.nbt * L.splits * m * L.ncols);
+  L.off_xn = o; o += al(L.nbt * L.splits * 2 * m);
+  L.total = o;
+  return L;
+}
+
+}  // namespace
+
+extern "C" int64_t sdc_matmul_check_workspace(int64_t batch_a, int64_t batch_b, int64_t m, int64_t k, int64_t n,
+                                              int64_t bs) {
+  if (m <= 0 || n <= 0 || k <= 0 || bs <= 0 || batch_a <= 0 || batch_b <= 0) return 0;
+  return layout(batch_a, batch_b, m, k, n, bs).total * (int64_t)sizeof(float) + 256;
+}
+
+extern "C" int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, int64_t batch_a,
+                                const void* B, int64_t sbb, int64_t sbk, int64_t sbn, int64_t batch_b, const void* C,
+                                int64_t scb, int64_t scm, int64_t scn, int64_t batch_c, int64_t m, int64_t k,
+                                int64_t n, int64_t bs, const void* bias, int bias_kind, int64_t sbias_b,
+                                int64_t sbias_m, int64_t sbias_n, float alpha, float beta, float z, float abs_floor,
+                                const float* sign_table, int64_t* result, void* workspace, int64_t workspace_bytes,
+                                float* scores_out, hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
+  if (m < 1 || n < 1 || k < 1 || batch_a < 1 || batch_b < 1 || batch_c < 1) return SDC_EINVAL;
+  if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EINVAL;
+  if (bs < 1 || bs > 128) return SDC_EUNSUPPORTED;
+  if (!A || !B || !C || !sign_table || !result) return SDC_EINVAL;
+  if (bias_kind < 0 || bias_kind > 2 || (bias_kind && !bias)) return SDC_EINVAL;
+  const int64_t nbt = batch_a > batch_b ? batch_a : batch_b;
+  if ((batch_a != 1 && batch_a != nbt) || (batch_b != 1 && batch_b != nbt)) return SDC_EINVAL;
+  if (batch_c != nbt && !(nbt == 1)) return SDC_EINVAL;
+  const Layout L = layout(batch_a, batch_b, m, k, n, bs);
+  if (batch_c * m * L.nb * 2 > 0xFFFFFFFFll) return SDC_EUNSUPPORTED;     // flat index in 32 bits
+  if (!workspace || workspace_bytes < L.total * (int64_t)sizeof(float) + 256) return SDC_EWORKSPACE;
+  float* ws = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  const float* s_full = sign_table + (bs - 1) * 128;
+  const float* s_last = L.rem ? sign_table + (L.rem - 1) * 128 : s_full;
+
+  BStageArgs ba{};
+  ba.B = (const uint16_t*)B; ba.sbb = sbb; ba.sbk = sbk; ba.sbn = sbn;
+  ba.k = k; ba.n = n; ba.nb = L.nb; ba.bs = bs; ba.rem = L.rem; ba.nkc = L.nkc;
+  ba.s_full = s_full; ba.s_last = s_last; ba.B2T = ws + L.off_b2t; ba.part = ws + L.off_part;
+  ba.vec = sbn == 1 && (sbk % 8 == 0) && (sbb % 8 == 0) && (bs % 8 == 0) && ((uintptr_t)B % 16 == 0);
+  {
+    SdcProf prof("b_stage", stream);
+    dim3 grid((unsigned)L.nkc, (unsigned)L.nb, (unsigned)batch_b);
+    if (dtype == SDC_BF16) hipLaunchKernelGGL(b_stage_kernel<SDC_BF16>, grid, dim3(256), 0, stream, ba);
+    else hipLaunchKernelGGL(b_stage_kernel<SDC_FP16>, grid, dim3(256), 0, stream, ba);
+    SDC_LAUNCH_CHECK();
+  }
+  BFinishArgs fa{};
+  fa.part = ws + L.off_part; fa.nkc = L.nkc; fa.nb = L.nb; fa.bs = bs; fa.rem = L.rem; fa.fp16 = dtype == SDC_FP16;
+  fa.colstat = ws + L.off_col; fa.bmaxf = ws + L.off_bmax;
+  fa.bias = bias_kind == 1 ? (const uint16_t*)bias : nullptr; fa.sbias = sbias_n;
+  fa.s_full = s_full; fa.s_last = s_last; fa.bias_out = ws + L.off_bias;
+  {
+    SdcProf prof("b_finish", stream);
+    dim3 grid((unsigned)L.nb, (unsigned)batch_b);
+    if (dtype == SDC_BF16) hipLaunchKernelGGL(b_finish_kernel<SDC_BF16>, grid, dim3(64), 0, stream, fa);
+    else hipLaunchKernelGGL(b_finish_kernel<SDC_FP16>, grid, dim3(64), 0, stream, fa);
+    SDC_LAUNCH_CHECK();
+  }
+  GemmArgs g{};
+  g.A = (const uint16_t*)A; g.sab = batch_a > 1 ? sab : 0; g.sam = sam; g.sak = sak;
+  g.B = ws + L.off_b2t; g.sbb = batch_b > 1 ? L.ncols * k : 0; g.sbc = k;
+  g.scale = ws + L.off_col + 2;      // every third float of colstat: stride 3 per column
+  g.sscb = batch_b > 1 ? L.ncols * 3 : 0;
+  g.m = m; g.k = k; g.N = L.ncols; g.splits = L.splits;
+  g.E = ws + L.off_e; g.XN = ws + L.off_xn;
+  g.scale_stride = 3;
+  int rc = sdc_gemm_launch(dtype, 1, g, nbt, stream);
+  if (rc != SDC_OK) return rc;
+
+  TrainArgs ta{};
+  ta.cv.y = (const uint16_t*)C; ta.cv.sb = scb; ta.cv.sm = scm; ta.cv.sn = scn; ta.cv.m = m; ta.cv.nb = L.nb;
+  ta.cv.bs = bs; ta.cv.rem = L.rem; ta.cv.npairs = batch_c * m * L.nb; ta.cv.s_full = s_full; ta.cv.s_last = s_last;
+  ta.cv.vec = scn == 1 && (scm % 8 == 0) && (scb % 8 == 0) && (bs % 8 == 0) && ((uintptr_t)C % 16 == 0);
+  ta.k = k; ta.splits = L.splits; ta.nbt = nbt; ta.ncols = L.ncols;
+  ta.b_batched = batch_b > 1; ta.e_batched = nbt > 1;
+  ta.E = ws + L.off_e; ta.XN = ws + L.off_xn; ta.colstat = ws + L.off_col; ta.bmaxf = ws + L.off_bmax;
+  ta.bias_kind = bias_kind; ta.bias_vec = ws + L.off_bias; ta.bias_mat = (const uint16_t*)bias;
+  ta.sbias_b = sbias_b; ta.sbias_m = sbias_m; ta.sbias_n = sbias_n;
+  ta.alpha = alpha; ta.beta = beta;
+  ta.u = dtype == SDC_BF16 ? 1.f / 256.f : 1.f / 2048.f;
+  ta.h = dtype == SDC_BF16 ? 0.f : 1.f / 33554432.f;
+  ta.abs_floor = abs_floor;
+  ta.l1c = (float)(k * 7.450580596923828e-09 > 1e-5 ? k * 7.450580596923828e-09 : 1e-5);
+  ta.zt = z;
+  ta.lim_a = dtype == SDC_BF16 ? 1e18f : 65504.f;
+  ta.capk = (float)(1.02 + (double)k * 2.384185791015625e-07);
+  ta.result = result; ta.zdump = scores_out;
+  const int64_t tiles = sdc_cdiv(ta.cv.npairs, 64);
+  const unsigned grid = (unsigned)(sdc_cdiv(tiles, 4) < 1024 ? sdc_cdiv(tiles, 4) : 1024);
+  SdcProf prof("train_score", stream);
+  if (dtype == SDC_BF16) hipLaunchKernelGGL(train_score_kernel<SDC_BF16>, dim3(grid), dim3(256), 0, stream, ta);
+  else hipLaunchKernelGGL(train_score_kernel<SDC_FP16>, dim3(grid), dim3(256), 0, stream, ta);
+  SDC_LAUNCH_CHECK();
+  return SDC_OK;
+}
