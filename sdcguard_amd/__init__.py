@@ -13,7 +13,7 @@ def __getattr__(name):
     if name in ("ServeGuard", "LayerChecksums"):
         from . import serve
         return getattr(serve, name)
-    if name in ("check_matmul", "check_linear", "matmul_zscores", "resolve"):
+    if name in ("check_matmul", "check_linear", "check_linear_rows", "matmul_zscores", "resolve"):
         from . import checksum
         return getattr(checksum, name)
     if name == "fingerprint":

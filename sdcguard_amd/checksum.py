@@ -251,3 +251,20 @@ def check_matmul(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, bias: Option
 def check_linear(x, weight, bias, y, **kw) -> Optional[CheckResult]:
     """Check y = torch.nn.functional.linear(x, weight, bias) for any leading dims (checksum.py:763-767)."""
     return check_matmul(x.reshape(-1, x.shape[-1]), weight.t(), y.reshape(-1, y.shape[-1]), bias, **kw)
+
+
+def linear_rows_operands(x, weight, bias, y):
+    """(A, B, C, bias) of the row-block check of y = linear(x, weight, bias): for every output column j and block of
+    `block` rows, sum_{i in blk} s_i y[i, j] = (sum_{i in blk} s_i x[i, :]) . weight[j, :] + (sum s_i) bias[j].  That is
+    the column-block check of y^T = weight @ x^T + bias[:, None] (the reference's own identity applied to the
+    transposed product; every operand is a strided view, nothing is copied)."""
+    x2 = x.reshape(-1, x.shape[-1])
+    y2 = y.reshape(-1, y.shape[-1])
+    b = None if bias is None else bias.reshape(-1, 1)
+    return weight, x2.t(), y2.t(), b
+
+
+def check_linear_rows(x, weight, bias, y, **kw) -> Optional[CheckResult]:
+    """Row-block check of y = torch.nn.functional.linear(x, weight, bias).  The result's `row` is the output column
+    and `col_block` the block of token rows."""
+    return check_matmul(*linear_rows_operands(x, weight, bias, y), **kw)

@@ -5,7 +5,7 @@
 
 #define SDC_WAVE 64
 // most depth-split planes of the expected-side GEMM (its scorers add them with unrolled loads)
-#define SDC_MAX_SPLITS 4
+#define SDC_MAX_SPLITS 8
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -98,7 +98,7 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
 // bits of a float as an int64 holding the unsigned 32-bit pattern
 __device__ __forceinline__ int64_t fbits64(float f) { return (int64_t)(uint32_t)__float_as_uint(f); }
 
-static inline int64_t sdc_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ static inline int64_t sdc_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // The HIP error behind the last SDC_ELAUNCH of this thread (sdc_last_error()).
 void sdc_note_error(hipError_t e);

@@ -3,27 +3,17 @@
 // The block sums B2 (k x 2nb fp32 per batch) multiply A as three low-precision parts (hi + mid + lo, whose sum is
 // B2 to ~2^-27; checksum.py:160-166, :313-343, serve.py:185-186), so A (bf16/fp16) is never widened and the
 // tensor-core products stay exact; every part accumulates into one fp32 accumulator, so E comes out summed over
-// parts.  The parts come either
-//   BSRC 0: precomputed (serving: LayerChecksums.parts, a (3 x 2nb) x k matrix stored k-contiguous per column), or
-//   BSRC 1: split on the fly from fp32 block sums B2^T (training: made by the B-side kernel for this call), after
-//           division by a per-column power of two (fp16's range; _matmul_fp32 scales the same way).
-// The same pass over A adds |a_row|_2^2 and |a_row|_1 (the noise model's row norms), in the workgroups of the
-// first column tile.
-//
-// Tiling (gfx950, wave64): a workgroup of 4 waves owns a 128-row x 64-column tile of E and a slice of the depth
-// (split-K when the tiles alone cannot fill 256 CUs: the partial results go to separate planes that the scoring
-// kernel adds).  Depth steps of 32 are staged through LDS; each wave computes a 64 x 32 sub-tile with
-// v_mfma_f32_32x32x16_{bf16,f16}: per 16-deep step 2 row fragments x 3 parts.
+// parts.  The parts are a (3 x ncols) x k matrix stored k-contiguous per column: precomputed per layer for the
+// serving check (LayerChecksums.parts), made per call by split_kernel for the training check (from the B-side
+// stage's fp32 sums, after division by a per-column power of two that keeps fp16 parts in range, as
+// checksum._matmul_fp32 scales).  The same pass over A adds |a_row|_2^2 and |a_row|_1 (the noise model's row
+// norms), in the workgroups of the first column tile.  Depth is split over workgroups when the tiles alone cannot
+// fill the 256 CUs: each split writes its own plane of E and the scoring kernels add the planes.
 #include "common.h"
 #include "gemm.h"
 #include "profile.h"
 
 namespace {
-
-constexpr int GM = 128;   // rows of E per workgroup
-constexpr int GN = 64;    // columns of E per workgroup
-constexpr int GK = 32;    // depth per LDS stage
-constexpr int LDSK = GK + 8;   // padded LDS row (elements): 80-byte rows spread the banks
 
 template <int DT>
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
@@ -108,147 +98,291 @@ __device__ __forceinline__ void norm_acc(u32x4 v, float& sq, float& ab) {
   }
 }
 
-template <int DT, int BSRC, bool VEC>
-__global__ __launch_bounds__(256) void expected_gemm_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[GM * LDSK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[3 * GN * LDSK];
+// One workgroup of 8 waves (two per SIMD, one workgroup per CU) owns a TM x TN tile of E and one depth slice.
+// WGN = 2: waves 4 x 2, tile 256 x 128 (wide checksum sets); WGN = 1: waves 8 x 1, tile 512 x 64 (narrow ones, such
+// as the 64 columns of a row-block check).  Each wave computes 64 x 64 with 2 x 2 fragments of v_mfma_f32_32x32x16
+// and, per fragment pair, the three parts of B into the same accumulator.
+//
+// Depth advances in stages of 32.  Per stage s a thread loads its 16-byte chunks of stage s + 1 into one of two
+// register sets (coalesced: 4 consecutive threads read one 64-byte row segment), the waves run the MFMAs of stage s
+// from one of two LDS buffers, the thread stores stage s + 1 into the other buffer, and one barrier ends the stage.
+// The loads are unconditional in the steady state (a guarded load makes the compiler wait for it at the end of the
+// guarded block).  LDS rows are padded to 40 elements so the 8 lanes of each ds_read_b128 phase hit distinct banks.
+// Workgroups are numbered so that each XCD (dispatch is round-robin over the eight) takes a contiguous range of
+// tiles: column tiles of one row tile, and row tiles of one depth slice, share an XCD's L2.
+constexpr int KS = 32;                 // depth per stage
+constexpr int LP = KS + 8;             // LDS row pitch (elements)
+constexpr int NT = 512;                // threads per workgroup
+
+template <int WGN>
+struct Tile {
+  static constexpr int WGM = 8 / WGN;
+  static constexpr int TM = 64 * WGM;
+  static constexpr int TN = 64 * WGN;
+  static constexpr int ACH = TM * (KS / 8);                   // 16-byte chunks of A per stage
+  static constexpr int BCH = 3 * TN * (KS / 8);               // ... of the three parts of B
+  static constexpr int NA = (ACH + NT - 1) / NT;              // per thread
+  static constexpr int NB = (BCH + NT - 1) / NT;
+  static constexpr int ROWS = TM + 3 * TN;                    // LDS rows per buffer
+};
+
+template <int DT, int WGN, bool VEC>
+__global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
+  using T = Tile<WGN>;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2][T::ROWS * LP];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int wm = w >> 1, wn = w & 1;
-  const int64_t r0 = (int64_t)blockIdx.x * GM, c0 = (int64_t)blockIdx.y * GN;
-  const int64_t batch = blockIdx.z / g.splits, split = blockIdx.z - batch * g.splits;
+  const int wm = w / WGN, wn = w % WGN;
+  const int64_t nrt = sdc_cdiv(g.m, T::TM), nct = sdc_cdiv(g.N, T::TN);
+  // XCD-aware order: block b runs on XCD b % 8; give XCD x the x-th eighth of the tiles (column tile fastest)
+  const int64_t G = (int64_t)gridDim.x, b = blockIdx.x;
+  const int64_t wid = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+  const int64_t ct = wid % nct, rt = (wid / nct) % nrt, rest = wid / (nct * nrt);
+  const int64_t split = rest % g.splits, batch = rest / g.splits;
+  const int64_t r0 = rt * T::TM, c0 = ct * T::TN;
   const int64_t kbeg = split * g.kchunk;
   const int64_t kend = kbeg + g.kchunk < g.k ? kbeg + g.kchunk : g.k;
-  const bool norms = blockIdx.y == 0;
+  const int nst = kbeg < kend ? (int)sdc_cdiv(kend - kbeg, KS) : 0;
+  const bool norms = ct == 0;
   const int64_t m = g.m, N = g.N;
-
-  // what this thread stages: two rows of A, one column of each part, 8 deep each
-  const int lr = t >> 2, lk = (t & 3) * 8;
-  const int64_t ar0 = r0 + lr, ar1 = r0 + lr + 64;
   const uint16_t* Ab = g.A + batch * g.sab;
-  const uint16_t* xa0 = Ab + (ar0 < m ? ar0 : 0) * g.sam;
-  const uint16_t* xa1 = Ab + (ar1 < m ? ar1 : 0) * g.sam;
-  const int64_t bc = c0 + lr;
-  const bool bc_ok = bc < N;
-  const int64_t bcc = bc_ok ? bc : 0;
-  float inv_scale = 1.f;
-  if constexpr (BSRC == 1) inv_scale = 1.f / g.scale[batch * g.sscb + bcc * g.scale_stride];   // (a power of two: exact)
+  const uint16_t* Pb = (const uint16_t*)g.B + batch * g.sbb;
 
-  u32x4 ra0, ra1, rb[3];
-  float sq0 = 0.f, ab0 = 0.f, sq1 = 0.f, ab1 = 0.f;
-  auto load_regs = [&](int64_t k0) {
-    ra0 = load8<VEC>(xa0, g.sak, k0 + lk, kend, ar0 < m);
-    ra1 = load8<VEC>(xa1, g.sak, k0 + lk, kend, ar1 < m);
-    if constexpr (BSRC == 0) {
-      const uint16_t* P = (const uint16_t*)g.B + batch * g.sbb;
+  // this thread's chunks: A chunk c is (row c / 4, depth 8 (c % 4)); B chunk c is (LDS row c / 4: part, column);
+  // indexes past the end repeat the last chunk (the same value is stored twice)
+  const uint16_t* asrc[T::NA];
+  int alds[T::NA], ak[T::NA];
+  bool aok[T::NA];
 #pragma unroll
-      for (int p = 0; p < 3; ++p) rb[p] = load8<VEC>(P + ((int64_t)p * N + bcc) * g.sbc, 1, k0 + lk, kend, bc_ok);
+  for (int j = 0; j < T::NA; ++j) {
+    const int c = (t + NT * j) < T::ACH ? t + NT * j : T::ACH - 1;
+    const int64_t row = r0 + c / 4;
+    aok[j] = row < m;
+    asrc[j] = Ab + (aok[j] ? row : 0) * g.sam;
+    alds[j] = (c / 4) * LP + 8 * (c % 4);
+    ak[j] = 8 * (c % 4);
+  }
+  const uint16_t* bsrc[T::NB];
+  int blds[T::NB], bk[T::NB];
+  bool bok[T::NB];
+#pragma unroll
+  for (int j = 0; j < T::NB; ++j) {
+    const int c = (t + NT * j) < T::BCH ? t + NT * j : T::BCH - 1;
+    const int cr = c / 4;                                     // 0 .. 3 TN - 1: part cr / TN, column cr % TN
+    const int64_t col = c0 + cr % T::TN;
+    bok[j] = col < N;
+    bsrc[j] = Pb + ((int64_t)(cr / T::TN) * N + (bok[j] ? col : 0)) * g.sbc;
+    blds[j] = (T::TM + cr) * LP + 8 * (c % 4);
+    bk[j] = 8 * (c % 4);
+  }
+
+  // VEC (k-contiguous operands, depth a multiple of KS): loads are unconditional and unmasked.  Rows of A past m
+  // read row 0 and columns past N read column 0; they only feed rows / columns of E that are never stored.
+  // Otherwise every element is loaded with its own bounds check and zero-filled.
+  u32x4 ra[2][T::NA], rb[2][T::NB];
+  auto load = [&](int set, int st) {
+    const int64_t k0 = kbeg + (int64_t)st * KS;
+    if constexpr (VEC) {
+#pragma unroll
+      for (int j = 0; j < T::NA; ++j) ra[set][j] = *reinterpret_cast<const u32x4*>(asrc[j] + (k0 + ak[j]));
+#pragma unroll
+      for (int j = 0; j < T::NB; ++j) rb[set][j] = *reinterpret_cast<const u32x4*>(bsrc[j] + (k0 + bk[j]));
     } else {
-      const float* Bt = (const float*)g.B + batch * g.sbb + bcc * g.sbc;
-      float v[8];
-      const int64_t kk = k0 + lk;
-      if (VEC && bc_ok && kk + 8 <= kend) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(Bt + kk);
-        const f32x4 b = *reinterpret_cast<const f32x4*>(Bt + kk + 4);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-      } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = (bc_ok && kk + i < kend) ? Bt[kk + i] : 0.f;
-      }
+      for (int j = 0; j < T::NA; ++j) ra[set][j] = load8<false>(asrc[j], g.sak, k0 + ak[j], kend, aok[j]);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] *= inv_scale;
-      split8<DT>(v, rb);
+      for (int j = 0; j < T::NB; ++j) rb[set][j] = load8<false>(bsrc[j], 1, k0 + bk[j], kend, bok[j]);
     }
   };
+  float sq[T::NA], ab[T::NA];
+#pragma unroll
+  for (int j = 0; j < T::NA; ++j) sq[j] = ab[j] = 0.f;
+  auto store = [&](int set, int buf) {
+    uint16_t* L = lds[buf];
+#pragma unroll
+    for (int j = 0; j < T::NA; ++j) {
+      *reinterpret_cast<u32x4*>(&L[alds[j]]) = ra[set][j];
+      if (norms && t + NT * j < T::ACH) norm_acc<DT>(ra[set][j], sq[j], ab[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < T::NB; ++j) *reinterpret_cast<u32x4*>(&L[blds[j]]) = rb[set][j];
+  };
 
-  f32x16 acc[2];
+  f32x16 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][n][r] = 0.f;
 
-  if (kbeg < kend) load_regs(kbeg);
-  for (int64_t k0 = kbeg; k0 < kend; k0 += GK) {
-    __syncthreads();
-    *reinterpret_cast<u32x4*>(&As[lr * LDSK + lk]) = ra0;
-    *reinterpret_cast<u32x4*>(&As[(lr + 64) * LDSK + lk]) = ra1;
+  auto compute = [&](int buf) {
+    const uint16_t* L = lds[buf];
 #pragma unroll
-    for (int p = 0; p < 3; ++p) *reinterpret_cast<u32x4*>(&Bs[(p * GN + lr) * LDSK + lk]) = rb[p];
-    if (norms) {
-      norm_acc<DT>(ra0, sq0, ab0);
-      norm_acc<DT>(ra1, sq1, ab1);
+    for (int s = 0; s < KS / 16; ++s) {
+      const int ko = 16 * s + (lane >> 5) * 8;
+      u32x4 a[2], bv[3][2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const u32x4*>(&L[(wm * 64 + 32 * i + (lane & 31)) * LP + ko]);
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+          bv[p][n] = *reinterpret_cast<const u32x4*>(&L[(T::TM + p * T::TN + wn * 64 + 32 * n + (lane & 31)) * LP + ko]);
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+          acc[0][n] = mfma32<DT>(a[0], bv[p][n], acc[0][n]);
+          acc[1][n] = mfma32<DT>(a[1], bv[p][n], acc[1][n]);
+        }
     }
+  };
+
+  // stage s: loaded into register set s % 2 during stage s - 1 ... s - 2, stored into LDS buffer s % 2 at the end of
+  // stage s - 1.  The steady-state loop loads unconditionally; the last one to three stages are peeled.
+  int st = 0;
+  if (nst > 0) {
+    load(0, 0);
+    if (nst > 1) load(1, 1);
+    store(0, 0);
     __syncthreads();
-    if (k0 + GK < kend) load_regs(k0 + GK);
-#pragma unroll
-    for (int kk = 0; kk < GK; kk += 16) {
-      const int ko = kk + (lane >> 5) * 8;
-      u32x4 a0 = *reinterpret_cast<const u32x4*>(&As[(wm * 64 + (lane & 31)) * LDSK + ko]);
-      u32x4 a1 = *reinterpret_cast<const u32x4*>(&As[(wm * 64 + 32 + (lane & 31)) * LDSK + ko]);
-#pragma unroll
-      for (int p = 0; p < 3; ++p) {
-        u32x4 b = *reinterpret_cast<const u32x4*>(&Bs[(p * GN + wn * 32 + (lane & 31)) * LDSK + ko]);
-        acc[0] = mfma32<DT>(a0, b, acc[0]);
-        acc[1] = mfma32<DT>(a1, b, acc[1]);
+    for (; st + 3 < nst; st += 2) {
+      load(0, st + 2);
+      compute(0);
+      store(1, 1);
+      __syncthreads();
+      load(1, st + 3);
+      compute(1);
+      store(0, 0);
+      __syncthreads();
+    }
+    const int left = nst - st;              // 1, 2 or 3
+    if (left == 3) load(0, st + 2);
+    compute(0);
+    if (left >= 2) {
+      store(1, 1);
+      __syncthreads();
+      compute(1);
+      if (left == 3) {
+        store(0, 0);
+        __syncthreads();
+        compute(0);
       }
     }
   }
 
   // C[i][j] of a 32x32 MFMA tile sits in lane j + 32 * ((i / 4) % 2), register (i / 8) * 4 + i % 4
   float* Es = g.E + (batch * g.splits + split) * m * N;
-  const int64_t col = c0 + wn * 32 + (lane & 31);
-  if (col < N) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+  for (int n = 0; n < 2; ++n) {
+    const int64_t col = c0 + wn * 64 + 32 * n + (lane & 31);
+    if (col < N) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = r0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < m) Es[row * N + col] = acc[i][r];
-      }
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = r0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (row < m) Es[row * N + col] = acc[i][n][r];
+        }
+    }
   }
   if (norms) {
-    sq0 = quad_sum(sq0); ab0 = quad_sum(ab0);
-    sq1 = quad_sum(sq1); ab1 = quad_sum(ab1);
-    if ((t & 3) == 0) {
-      float* xs = g.XN + (batch * g.splits + split) * 2 * m;
-      if (ar0 < m) { xs[ar0] = sq0; xs[m + ar0] = ab0; }
-      if (ar1 < m) { xs[ar1] = sq1; xs[m + ar1] = ab1; }
+    float* xs = g.XN + (batch * g.splits + split) * 2 * m;
+#pragma unroll
+    for (int j = 0; j < T::NA; ++j) {
+      float q = sq[j], a1 = ab[j];
+      q += __shfl_xor(q, 1, 64);
+      a1 += __shfl_xor(a1, 1, 64);
+      q += __shfl_xor(q, 2, 64);
+      a1 += __shfl_xor(a1, 2, 64);
+      const int c = t + NT * j;
+      const int64_t row = r0 + c / 4;
+      if ((c & 3) == 0 && c < T::ACH && row < m) {
+        xs[row] = q;
+        xs[m + row] = a1;
+      }
     }
   }
 }
 
-template <int DT, int BSRC>
-int launch_dt(GemmArgs g, bool vec, dim3 grid, hipStream_t stream) {
-  if (vec) hipLaunchKernelGGL((expected_gemm_kernel<DT, BSRC, true>), grid, dim3(256), 0, stream, g);
-  else hipLaunchKernelGGL((expected_gemm_kernel<DT, BSRC, false>), grid, dim3(256), 0, stream, g);
+template <int DT, int WGN>
+int launch_dt(GemmArgs g, bool vec, int64_t blocks, hipStream_t stream) {
+  if (vec) hipLaunchKernelGGL((expected_gemm_kernel<DT, WGN, true>), dim3((unsigned)blocks), dim3(NT), 0, stream, g);
+  else hipLaunchKernelGGL((expected_gemm_kernel<DT, WGN, false>), dim3((unsigned)blocks), dim3(NT), 0, stream, g);
   SDC_LAUNCH_CHECK();
   return SDC_OK;
 }
 
+// fp32 B2^T columns -> three parts (dtype), each column divided by its power of two first (exact)
+struct SplitArgs {
+  const float* B2T;                 // [batch][ncols][k]
+  const float* scale;               // scale[batch * sscb + col * scale_stride], or null (1)
+  int64_t sscb, scale_stride;
+  int64_t ncols, k, kp, batches;
+  uint16_t* parts;                  // [batch][3 * ncols][kp]
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void split_kernel(SplitArgs a) {
+  const int64_t nch = sdc_cdiv(a.kp, 8);
+  const int64_t total = a.batches * a.ncols * nch;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t ch = i % nch, cb = i / nch, col = cb % a.ncols, bb = cb / a.ncols;
+    const float inv = a.scale ? 1.f / a.scale[bb * a.sscb + col * a.scale_stride] : 1.f;
+    const float* src = a.B2T + cb * a.k;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t kk = 8 * ch + e;
+      v[e] = kk < a.k ? src[kk] * inv : 0.f;
+    }
+    u32x4 pr[3];
+    split8<DT>(v, pr);
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+      *reinterpret_cast<u32x4*>(a.parts + ((bb * 3 + p) * a.ncols + col) * a.kp + 8 * ch) = pr[p];
+  }
+}
+
 }  // namespace
 
-// Split of the depth so that tiles x splits fill the GPU (256 CUs, 2 workgroups each), in multiples of GK.
+// Split of the depth so that tiles x splits fill the GPU (one workgroup per CU), in multiples of the stage depth.
 extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols) {
   if (m <= 0 || k <= 0 || ncols <= 0) return 1;
-  const int64_t tiles = sdc_cdiv(m, GM) * sdc_cdiv(ncols, GN);
-  int64_t s = sdc_cdiv(512, tiles);
-  const int64_t smax = k / 512 > 1 ? k / 512 : 1;
+  const int wgn = ncols > 64 ? 2 : 1;
+  const int64_t tiles = sdc_cdiv(m, 64 * (8 / wgn)) * sdc_cdiv(ncols, 64 * wgn);
+  int64_t s = sdc_cdiv(256, tiles);
+  const int64_t smax = k / 256 > 1 ? k / 256 : 1;
   if (s > smax) s = smax;
   if (s > SDC_MAX_SPLITS) s = SDC_MAX_SPLITS;
   if (s < 1) s = 1;
   return s;
 }
 
-int sdc_gemm_launch(int dtype, int bsrc, GemmArgs g, int64_t batches, hipStream_t stream) {
+int sdc_gemm_launch(int dtype, GemmArgs g, int64_t batches, hipStream_t stream) {
   if (g.splits < 1 || g.splits > SDC_MAX_SPLITS || batches < 1) return SDC_EINVAL;
-  g.kchunk = sdc_cdiv(sdc_cdiv(g.k, g.splits), GK) * GK;
-  bool vec = g.sak == 1 && (g.k % 8 == 0) && (g.sam % 8 == 0) && (g.sab % 8 == 0) && ((uintptr_t)g.A % 16 == 0);
-  if (bsrc == 0) vec = vec && (g.sbc % 8 == 0) && (g.sbb % 8 == 0) && ((uintptr_t)g.B % 16 == 0);
-  else vec = vec && (g.sbc % 4 == 0) && (g.sbb % 4 == 0) && ((uintptr_t)g.B % 16 == 0);
-  dim3 grid((unsigned)sdc_cdiv(g.m, GM), (unsigned)sdc_cdiv(g.N, GN), (unsigned)(batches * g.splits));
+  g.kchunk = sdc_cdiv(sdc_cdiv(g.k, g.splits), KS) * KS;
+  const bool vec = g.sak == 1 && (g.k % KS == 0) && (g.sam % 8 == 0) && (g.sab % 8 == 0) &&
+                   ((uintptr_t)g.A % 16 == 0) && (g.sbc % 8 == 0) && (g.sbb % 8 == 0) && ((uintptr_t)g.B % 16 == 0);
+  const int wgn = g.N > 64 ? 2 : 1;
+  const int64_t blocks = sdc_cdiv(g.m, 64 * (8 / wgn)) * sdc_cdiv(g.N, 64 * wgn) * g.splits * batches;
+  if (blocks > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
   SdcProf prof("expected_gemm", stream);
   if (dtype == SDC_BF16)
-    return bsrc == 0 ? launch_dt<SDC_BF16, 0>(g, vec, grid, stream) : launch_dt<SDC_BF16, 1>(g, vec, grid, stream);
-  return bsrc == 0 ? launch_dt<SDC_FP16, 0>(g, vec, grid, stream) : launch_dt<SDC_FP16, 1>(g, vec, grid, stream);
+    return wgn == 2 ? launch_dt<SDC_BF16, 2>(g, vec, blocks, stream) : launch_dt<SDC_BF16, 1>(g, vec, blocks, stream);
+  return wgn == 2 ? launch_dt<SDC_FP16, 2>(g, vec, blocks, stream) : launch_dt<SDC_FP16, 1>(g, vec, blocks, stream);
+}
+
+int sdc_split_launch(int dtype, const float* B2T, const float* scale, int64_t sscb, int64_t scale_stride,
+                     int64_t ncols, int64_t k, int64_t kp, int64_t batches, uint16_t* parts, hipStream_t stream) {
+  SplitArgs a{B2T, scale, sscb, scale_stride, ncols, k, kp, batches, parts};
+  const int64_t total = batches * ncols * sdc_cdiv(kp, 8);
+  const int64_t blocks = sdc_cdiv(total, 256) < 2048 ? sdc_cdiv(total, 256) : 2048;
+  SdcProf prof("split", stream);
+  if (dtype == SDC_BF16) hipLaunchKernelGGL(split_kernel<SDC_BF16>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL(split_kernel<SDC_FP16>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  SDC_LAUNCH_CHECK();
+  return SDC_OK;
 }
 
 // The serving check's call: one batch, precomputed parts (k-contiguous columns).
@@ -260,10 +394,9 @@ int sdc_expected_launch(int dtype, const void* x, int64_t sxm, int64_t sxk, cons
   GemmArgs g{};
   g.A = (const uint16_t*)x; g.sab = 0; g.sam = sxm; g.sak = sxk;
   g.B = parts; g.sbb = 0; g.sbc = spc;
-  g.scale = nullptr; g.sscb = 0;
   g.m = m; g.k = k; g.N = ncols; g.splits = splits;
   g.E = E; g.XN = XN;
-  return sdc_gemm_launch(dtype, 0, g, 1, stream);
+  return sdc_gemm_launch(dtype, g, 1, stream);
 }
 
 // Self-test of the MFMA operand layout this file assumes: C (32 x 32) = A (32 x 16) @ B (16 x 32), bf16 in,

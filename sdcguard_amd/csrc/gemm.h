@@ -6,15 +6,17 @@
 struct GemmArgs {
   const uint16_t* A;            // bf16/fp16 rows; element (batch, row, kk) at A[batch * sab + row * sam + kk * sak]
   int64_t sab, sam, sak;
-  const void* B;                // BSRC 0: parts (3 x N columns of the dtype), BSRC 1: fp32 B2^T (N columns)
-  int64_t sbb, sbc;             // batch stride, column stride (columns are depth-contiguous)
-  const float* scale;           // BSRC 1: per-column power of two to divide by before the split, at
-  int64_t sscb;                 //   scale[batch * sscb + column * scale_stride]
-  int64_t scale_stride;
+  const void* B;                // parts: 3 x N depth-contiguous columns of the dtype, part p column c at
+  int64_t sbb, sbc;             //   B[batch * sbb + (p * N + c) * sbc + kk]
   int64_t m, k, N, kchunk, splits;
   float* E;                     // [batch][split][m][N]
   float* XN;                    // [batch][split][2][m]: sum of squares and sum of |a| of each row's depth slice
 };
 
-// E and XN for `batches` batches (grid z = batches x splits); bsrc 0 or 1 as above.
-int sdc_gemm_launch(int dtype, int bsrc, GemmArgs g, int64_t batches, hipStream_t stream);
+// E and XN for `batches` batches.
+int sdc_gemm_launch(int dtype, GemmArgs g, int64_t batches, hipStream_t stream);
+
+// parts[batch][3 * ncols][kp] from B2T[batch][ncols][k] (fp32), each column divided by
+// scale[batch * sscb + col * scale_stride] first (null: 1); depth kp >= k padded with zeros.
+int sdc_split_launch(int dtype, const float* B2T, const float* scale, int64_t sscb, int64_t scale_stride,
+                     int64_t ncols, int64_t k, int64_t kp, int64_t batches, uint16_t* parts, hipStream_t stream);

@@ -8,7 +8,7 @@
 //      largest |B| of every block;
 //   2. b_finish: those partials added up (|checksum column|_2, its largest entry, the per-column power of two that
 //      keeps fp16 parts in range, the block's largest |B|) and the bias vector's block sums;
-//   3. expected_gemm (expected_gemm.hip): E = A @ B2 from three on-the-fly parts, plus A's row norms;
+//   3. split + expected_gemm (expected_gemm.hip): B2 as three parts, E = A @ B2 on MFMA, plus A's row norms;
 //   4. train_score: one persistent pass over C scoring every (batch, row, block) pair, worst key and unjudged count
 //      into the check's result row with atomics.
 #include "blocksums.h"
@@ -108,6 +108,89 @@ __global__ __launch_bounds__(256) void b_stage_kernel(BStageArgs a) {
     for (int i = 1; i < 4; ++i) v = t < 2 ? v + red[i][t] : fmaxf(v, red[i][t]);
     a.part[((bb * a.nkc + kc) * a.nb + jb) * NSTAT + t] = v;
   }
+}
+
+// The same stage for a B whose rows are contiguous across k (sbk == 1: a weight passed as W.t(), or the activations
+// x^T of a row-block check).  A workgroup takes 256 consecutive rows of B and one block of columns: each thread reads
+// 16 bytes (8 rows of B) of one column per step, the eight column groups of a workgroup take every eighth column,
+// and LDS adds their sums.  Partial stats are written per 64-row slice, as b_stage_kernel writes them.
+template <int DT>
+__global__ __launch_bounds__(256) void b_stage_t_kernel(BStageArgs a) {
+  __shared__ float red[2][8][256 + 4];
+  __shared__ float redm[4];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int kg = t & 31, cg = t >> 5;
+  const int64_t kc = blockIdx.x, jb = blockIdx.y, bb = blockIdx.z;
+  const int64_t kk0 = kc * 256 + 8 * kg;
+  const bool last = (jb == a.nb - 1) && (a.rem > 0);
+  const int wid = (int)(last ? a.rem : a.bs);
+  const float* sp = last ? a.s_last : a.s_full;
+  float pl[8], sg[8], mx = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) pl[e] = sg[e] = 0.f;
+  const uint16_t* base = a.B + bb * a.sbb + jb * a.bs * a.sbn + kk0;
+  if (a.vec && kk0 + 8 <= a.k) {
+#pragma unroll 4
+    for (int c = cg; c < wid; c += 8) {
+      const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + c * a.sbn));
+      const float s = sp[c];
+      const float x[8] = {lo_of<DT>(v.x), hi_of<DT>(v.x), lo_of<DT>(v.y), hi_of<DT>(v.y),
+                          lo_of<DT>(v.z), hi_of<DT>(v.z), lo_of<DT>(v.w), hi_of<DT>(v.w)};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pl[e] += x[e];
+        sg[e] = fmaf(x[e], s, sg[e]);
+        mx = fmaxf(mx, nan_inf(x[e]));
+      }
+    }
+  } else if (kk0 < a.k) {
+    const int ne = a.k - kk0 < 8 ? (int)(a.k - kk0) : 8;
+#pragma unroll 1
+    for (int c = cg; c < wid; c += 8) {
+      const float s = sp[c];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (e < ne) {
+          const float x = half_to_f32<DT>(base[c * a.sbn + e]);
+          pl[e] += x;
+          sg[e] = fmaf(x, s, sg[e]);
+          mx = fmaxf(mx, nan_inf(x));
+        }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    red[0][cg][8 * kg + e] = pl[e];
+    red[1][cg][8 * kg + e] = sg[e];
+  }
+#pragma unroll
+  for (int msk = 1; msk < 64; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+  if (lane == 0) redm[w] = mx;
+  __syncthreads();
+  float P = 0.f, S = 0.f;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    P += red[0][g][t];
+    S += red[1][g][t];
+  }
+  const float bm = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
+  const int64_t kk = kc * 256 + t;
+  const bool mine = kk < a.k;
+  if (mine) {
+    float* col = a.B2T + (bb * 2 * a.nb + 2 * jb) * a.k;
+    col[kk] = P;
+    col[a.k + kk] = S;
+  }
+  float st[NSTAT] = {mine ? P * P : 0.f, mine ? S * S : 0.f, mine ? nan_inf(P) : 0.f, mine ? nan_inf(S) : 0.f, bm};
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int msk = 1; msk < 64; msk <<= 1) {
+      const float o = __shfl_xor(st[i], msk, 64);
+      st[i] = i < 2 ? st[i] + o : fmaxf(st[i], o);
+    }
+  const int64_t slice = kc * 4 + w;           // 64-row slice of this wave's rows
+  if (lane < NSTAT && slice < a.nkc) a.part[((bb * a.nkc + slice) * a.nb + jb) * NSTAT + lane] = st[lane];
 }
 
 struct BFinishArgs {
@@ -284,11 +367,22 @@ __device__ __forceinline__ void train_pair(const TrainArgs& a, int64_t p, float 
     const uint16_t* br = a.bias_mat + bc * a.sbias_b + r * a.sbias_m + jb * a.cv.bs * a.sbias_n;
     const float* sp = last ? a.cv.s_last : a.cv.s_full;
     float bp = 0.f, bsg = 0.f, bmx = 0.f;
-    for (int64_t c = 0; c < (int64_t)wf; ++c) {
-      const float x = half_to_f32<DT>(br[c * a.sbias_n]);
-      bp += x;
-      bsg = fmaf(x, sp[c], bsg);
-      bmx = fmaxf(bmx, nan_inf(x));
+    if (a.sbias_n == 0) {
+      // a bias constant along the row (a per-output bias of a row-block check): w copies of one value, whose
+      // block sums w*b and (sum of signs)*b are exact in fp32 (8-bit significands times w <= 128)
+      const float x = half_to_f32<DT>(br[0]);
+      float ss = 0.f;
+      for (int64_t c = 0; c < (int64_t)wf; ++c) ss += sp[c];
+      bp = x * wf;
+      bsg = x * ss;
+      bmx = nan_inf(x);
+    } else {
+      for (int64_t c = 0; c < (int64_t)wf; ++c) {
+        const float x = half_to_f32<DT>(br[c * a.sbias_n]);
+        bp += x;
+        bsg = fmaf(x, sp[c], bsg);
+        bmx = fmaxf(bmx, nan_inf(x));
+      }
     }
     e0 = e0 + bp * a.beta;
     e1 = e1 + bsg * a.beta;
@@ -359,9 +453,102 @@ __global__ __launch_bounds__(256) void train_score_kernel(TrainArgs a) {
   }
 }
 
+// The scoring pass for a C whose rows are contiguous across each other (scm == 1: C = y^T of a row-block check,
+// where a "row" of C is a column of y and a block of C's columns is a block of 128 rows of y).  A workgroup takes
+// 512 consecutive rows of C (8 per lane, one 16-byte load) and one block: the four waves split the block's
+// columns, each lane accumulates the four sums of its 8 rows, LDS adds the waves' sums, and every thread scores
+// two (row, block) pairs with the same arithmetic as train_score_kernel.
+template <int DT>
+__global__ __launch_bounds__(256) void train_score_t_kernel(TrainArgs a) {
+  __shared__ float red[4][4][512];
+  __shared__ int64_t red_k[4], red_d[4];
+  __shared__ int red_u[4];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t rt = blockIdx.x, jb = blockIdx.y, bc = blockIdx.z;
+  const int64_t m = a.cv.m;
+  const bool last = (jb == a.cv.nb - 1) && (a.cv.rem > 0);
+  const int wid = (int)(last ? a.cv.rem : a.cv.bs);
+  const float* sp = last ? a.cv.s_last : a.cv.s_full;
+  const int64_t r0 = rt * 512 + 8 * lane;
+  float pl[8], sg[8], sq[8], ab[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) pl[e] = sg[e] = sq[e] = ab[e] = 0.f;
+  const uint16_t* base = a.cv.y + bc * a.cv.sb + r0 + jb * a.cv.bs * a.cv.sn;
+  if (a.cv.vec && r0 + 8 <= m) {
+#pragma unroll 8
+    for (int c = w; c < wid; c += 4) {
+      const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + c * a.cv.sn));
+      const float s = sp[c];
+      const float x[8] = {lo_of<DT>(v.x), hi_of<DT>(v.x), lo_of<DT>(v.y), hi_of<DT>(v.y),
+                          lo_of<DT>(v.z), hi_of<DT>(v.z), lo_of<DT>(v.w), hi_of<DT>(v.w)};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pl[e] += x[e];
+        sg[e] = fmaf(x[e], s, sg[e]);
+        sq[e] = fmaf(x[e], x[e], sq[e]);
+        ab[e] += fabsf(x[e]);
+      }
+    }
+  } else if (r0 < m) {
+    const int ne = m - r0 < 8 ? (int)(m - r0) : 8;
+#pragma unroll 1
+    for (int c = w; c < wid; c += 4) {
+      const float s = sp[c];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (e < ne) {
+          const float x = half_to_f32<DT>(base[c * a.cv.sn + e]);
+          pl[e] += x;
+          sg[e] = fmaf(x, s, sg[e]);
+          sq[e] = fmaf(x, x, sq[e]);
+          ab[e] += fabsf(x);
+        }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    red[w][0][8 * lane + e] = pl[e];
+    red[w][1][8 * lane + e] = sg[e];
+    red[w][2][8 * lane + e] = sq[e];
+    red[w][3][8 * lane + e] = ab[e];
+  }
+  __syncthreads();
+  TrainBest best;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int i = t + 256 * h;
+    const int64_t r = rt * 512 + i;
+    if (r < m) {
+      float s4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) s4[q] = (red[0][q][i] + red[1][q][i]) + (red[2][q][i] + red[3][q][i]);
+      train_pair<DT>(a, (bc * m + r) * a.cv.nb + jb, s4[0], s4[1], s4[2], s4[3], best);
+    }
+  }
+  int64_t key = wave_max_i64(best.key), keyd = wave_max_i64(best.keyd);
+  int unk = wave_sum_i32(best.unk);
+  if (lane == 0) { red_k[w] = key; red_d[w] = keyd; red_u[w] = unk; }
+  __syncthreads();
+  if (t == 0) {
+    int64_t k0 = red_k[0], d0 = red_d[0];
+    int un = red_u[0];
+    for (int i = 1; i < 4; ++i) {
+      k0 = red_k[i] > k0 ? red_k[i] : k0;
+      d0 = red_d[i] > d0 ? red_d[i] : d0;
+      un += red_u[i];
+    }
+    int64_t* res = a.result;
+    const int64_t s0 = __atomic_load_n(res, __ATOMIC_RELAXED), s1 = __atomic_load_n(res + 1, __ATOMIC_RELAXED);
+    if (k0 > s0) atomicMax((unsigned long long*)res, (unsigned long long)k0);
+    if (d0 > s1) atomicMax((unsigned long long*)(res + 1), (unsigned long long)d0);
+    if (un > 0) atomicAdd((unsigned long long*)(res + 2), (unsigned long long)un);
+  }
+}
+
 struct Layout {
   int64_t nb, rem, ncols, nkc, splits, nbt;
-  int64_t off_b2t, off_part, off_col, off_bmax, off_bias, off_e, off_xn, total;
+  int64_t kp;                      // depth pitch of the parts (k rounded up to 8: 16-byte aligned columns)
+  int64_t off_b2t, off_part, off_col, off_bmax, off_bias, off_parts, off_e, off_xn, total;
 };
 
 Layout layout(int64_t batch_a, int64_t batch_b, int64_t m, int64_t k, int64_t n, int64_t bs) {
@@ -374,11 +561,13 @@ Layout layout(int64_t batch_a, int64_t batch_b, int64_t m, int64_t k, int64_t n,
   L.splits = sdc_expected_splits(m, k, L.ncols);
   auto al = [](int64_t x) { return (x + 63) / 64 * 64; };   // floats, 256-byte aligned sections
   int64_t o = 0;
+  L.kp = (k + 7) / 8 * 8;
   L.off_b2t = o; o += al(batch_b * L.ncols * k);
   L.off_part = o; o += al(batch_b * L.nkc * L.nb * NSTAT);
   L.off_col = o; o += al(batch_b * L.ncols * 3);
   L.off_bmax = o; o += al(batch_b * L.nb);
   L.off_bias = o; o += al(3 * L.nb);
+  L.off_parts = o; o += al((batch_b * 3 * L.ncols * L.kp + 1) / 2);      // 16-bit parts, two per float
   L.off_e = o; o += al(L.nbt * L.splits * m * L.ncols);
   L.off_xn = o; o += al(L.nbt * L.splits * 2 * m);
   L.total = o;
@@ -420,12 +609,21 @@ extern "C" int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t s
   ba.B = (const uint16_t*)B; ba.sbb = sbb; ba.sbk = sbk; ba.sbn = sbn;
   ba.k = k; ba.n = n; ba.nb = L.nb; ba.bs = bs; ba.rem = L.rem; ba.nkc = L.nkc;
   ba.s_full = s_full; ba.s_last = s_last; ba.B2T = ws + L.off_b2t; ba.part = ws + L.off_part;
-  ba.vec = sbn == 1 && (sbk % 8 == 0) && (sbb % 8 == 0) && (bs % 8 == 0) && ((uintptr_t)B % 16 == 0);
+  // B with k-contiguous rows (W.t(), x^T) is read down its columns by b_stage_t_kernel; otherwise across rows
+  const bool b_t = sbk == 1 && sbn != 1;
+  if (b_t) ba.vec = (sbn % 8 == 0) && (sbb % 8 == 0) && ((uintptr_t)B % 16 == 0);
+  else ba.vec = sbn == 1 && (sbk % 8 == 0) && (sbb % 8 == 0) && (bs % 8 == 0) && ((uintptr_t)B % 16 == 0);
   {
     SdcProf prof("b_stage", stream);
-    dim3 grid((unsigned)L.nkc, (unsigned)L.nb, (unsigned)batch_b);
-    if (dtype == SDC_BF16) hipLaunchKernelGGL(b_stage_kernel<SDC_BF16>, grid, dim3(256), 0, stream, ba);
-    else hipLaunchKernelGGL(b_stage_kernel<SDC_FP16>, grid, dim3(256), 0, stream, ba);
+    if (b_t) {
+      dim3 grid((unsigned)sdc_cdiv(k, 256), (unsigned)L.nb, (unsigned)batch_b);
+      if (dtype == SDC_BF16) hipLaunchKernelGGL(b_stage_t_kernel<SDC_BF16>, grid, dim3(256), 0, stream, ba);
+      else hipLaunchKernelGGL(b_stage_t_kernel<SDC_FP16>, grid, dim3(256), 0, stream, ba);
+    } else {
+      dim3 grid((unsigned)L.nkc, (unsigned)L.nb, (unsigned)batch_b);
+      if (dtype == SDC_BF16) hipLaunchKernelGGL(b_stage_kernel<SDC_BF16>, grid, dim3(256), 0, stream, ba);
+      else hipLaunchKernelGGL(b_stage_kernel<SDC_FP16>, grid, dim3(256), 0, stream, ba);
+    }
     SDC_LAUNCH_CHECK();
   }
   BFinishArgs fa{};
@@ -440,15 +638,17 @@ extern "C" int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t s
     else hipLaunchKernelGGL(b_finish_kernel<SDC_FP16>, grid, dim3(64), 0, stream, fa);
     SDC_LAUNCH_CHECK();
   }
+  // the three parts of B2 / scale (scale: every third float of colstat, stride 3 per column)
+  uint16_t* parts = (uint16_t*)(ws + L.off_parts);
+  int rc = sdc_split_launch(dtype, ws + L.off_b2t, ws + L.off_col + 2, L.ncols * 3, 3, L.ncols, k, L.kp, batch_b,
+                            parts, stream);
+  if (rc != SDC_OK) return rc;
   GemmArgs g{};
   g.A = (const uint16_t*)A; g.sab = batch_a > 1 ? sab : 0; g.sam = sam; g.sak = sak;
-  g.B = ws + L.off_b2t; g.sbb = batch_b > 1 ? L.ncols * k : 0; g.sbc = k;
-  g.scale = ws + L.off_col + 2;      // every third float of colstat: stride 3 per column
-  g.sscb = batch_b > 1 ? L.ncols * 3 : 0;
+  g.B = parts; g.sbb = batch_b > 1 ? 3 * L.ncols * L.kp : 0; g.sbc = L.kp;
   g.m = m; g.k = k; g.N = L.ncols; g.splits = L.splits;
   g.E = ws + L.off_e; g.XN = ws + L.off_xn;
-  g.scale_stride = 3;
-  int rc = sdc_gemm_launch(dtype, 1, g, nbt, stream);
+  rc = sdc_gemm_launch(dtype, g, nbt, stream);
   if (rc != SDC_OK) return rc;
 
   TrainArgs ta{};
@@ -469,11 +669,19 @@ extern "C" int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t s
   ta.lim_a = dtype == SDC_BF16 ? 1e18f : 65504.f;
   ta.capk = (float)(1.02 + (double)k * 2.384185791015625e-07);
   ta.result = result; ta.zdump = scores_out;
-  const int64_t tiles = sdc_cdiv(ta.cv.npairs, 64);
-  const unsigned grid = (unsigned)(sdc_cdiv(tiles, 4) < 1024 ? sdc_cdiv(tiles, 4) : 1024);
   SdcProf prof("train_score", stream);
-  if (dtype == SDC_BF16) hipLaunchKernelGGL(train_score_kernel<SDC_BF16>, dim3(grid), dim3(256), 0, stream, ta);
-  else hipLaunchKernelGGL(train_score_kernel<SDC_FP16>, dim3(grid), dim3(256), 0, stream, ta);
+  if (scm == 1 && scn != 1 && L.nb < 65536 && batch_c < 65536) {
+    // C with adjacent rows (y^T): read 512 rows at a time down each column
+    ta.cv.vec = (scn % 8 == 0) && (scb % 8 == 0) && ((uintptr_t)C % 16 == 0);
+    dim3 grid((unsigned)sdc_cdiv(m, 512), (unsigned)L.nb, (unsigned)batch_c);
+    if (dtype == SDC_BF16) hipLaunchKernelGGL(train_score_t_kernel<SDC_BF16>, grid, dim3(256), 0, stream, ta);
+    else hipLaunchKernelGGL(train_score_t_kernel<SDC_FP16>, grid, dim3(256), 0, stream, ta);
+  } else {
+    const int64_t tiles = sdc_cdiv(ta.cv.npairs, 64);
+    const unsigned grid = (unsigned)(sdc_cdiv(tiles, 4) < 1024 ? sdc_cdiv(tiles, 4) : 1024);
+    if (dtype == SDC_BF16) hipLaunchKernelGGL(train_score_kernel<SDC_BF16>, dim3(grid), dim3(256), 0, stream, ta);
+    else hipLaunchKernelGGL(train_score_kernel<SDC_FP16>, dim3(grid), dim3(256), 0, stream, ta);
+  }
   SDC_LAUNCH_CHECK();
   return SDC_OK;
 }

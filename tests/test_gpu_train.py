@@ -218,3 +218,62 @@ def test_bf16_1024_cubed_with_exponent_bit_flips():
             assert (res.row, res.col_block) == (o.row, o.col_block)
         agree += 1
     assert agree >= 62 and band <= 2
+
+
+ROW_SHAPES = [(256, 512, 1024, torch.bfloat16), (300, 264, 1000, torch.bfloat16), (130, 1024, 520, torch.float16),
+              (1, 96, 40, torch.bfloat16), (1100, 300, 37, torch.float16)]
+
+
+@pytest.mark.parametrize("T,din,dout,dtype", ROW_SHAPES)
+def test_transposed_weight_stage_matches_oracle(T, din, dout, dtype):
+    """check_linear passes B = W.t() (k-contiguous rows): the column-read stage must give the oracle's scores,
+    including k not a multiple of 8 or 256 and unaligned row strides."""
+    x, W, b, y = make_layer(T, din, dout, dtype, outliers=True, seed=T)
+    zs, res = _scores(x, W.t(), y, b)
+    o = abft.zscores(x.float().cpu().numpy(), W.t().float().cpu().numpy(), y.float().cpu().numpy(),
+                     b.float().cpu().numpy(), dtype="bf16" if dtype == torch.bfloat16 else "fp16", seed=1)
+    ok = z_close(zs.reshape(-1), o.z.reshape(-1), gemm_slack(o.csb, o.den).reshape(-1))
+    assert ok.all(), (np.nonzero(~ok)[0][:5], zs.reshape(-1)[~ok][:5], o.z.reshape(-1)[~ok][:5])
+    assert res.ok and o.ok
+
+
+@pytest.mark.parametrize("T,din,dout,dtype", ROW_SHAPES)
+def test_row_block_check_matches_oracle(T, din, dout, dtype):
+    """The row-block check (column-block check of y^T = W x^T + b[:, None]) against the oracle on the same
+    transposed operands: per-checksum z, clean verdict; then a corrupted element is located at (column, row block)."""
+    from sdcguard_amd.checksum import check_linear_rows, linear_rows_operands
+    x, W, b, y = make_layer(T, din, dout, dtype, seed=T + 1)
+    A, B, C, bias = linear_rows_operands(x, W, b, y)
+    zs, res = _scores(A, B, C, bias)
+    dt = "bf16" if dtype == torch.bfloat16 else "fp16"
+    o = abft.zscores(A.float().cpu().numpy(), B.float().cpu().numpy(), C.float().cpu().numpy(),
+                     bias.float().cpu().numpy(), dtype=dt, seed=1)
+    ok = z_close(zs.reshape(-1), o.z.reshape(-1), gemm_slack(o.csb, o.den).reshape(-1))
+    assert ok.all(), (np.nonzero(~ok)[0][:5], zs.reshape(-1)[~ok][:5], o.z.reshape(-1)[~ok][:5])
+    assert res.ok and o.ok, (res.max_z, o.max_z)
+    y2 = y.clone()
+    r, c = T // 2, dout - 1
+    y2[r, c] = y2[r, c] * 64 + 8
+    res = check_linear_rows(x, W, b, y2)
+    o = abft.check_matmul(*[t.float().cpu().numpy() for t in linear_rows_operands(x, W, b, y2)], dtype=dt, seed=1)
+    assert not res.ok and not o.ok
+    assert (res.row, res.col_block) == (c, r // 128) == (o.row, o.col_block)
+
+
+def test_row_block_check_bit_flips_4096x4096x14336():
+    """Full-size layer (x 4096x4096 N(0,1), W 14336x4096 N(0,0.02), y bf16): the row-block check is clean, and a
+    flip of a top exponent bit of y[i, j] is located at (j, i // 128); one flip per trial, 8 trials."""
+    from sdcguard_amd.checksum import check_linear_rows
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(4096, 4096, device="cuda", generator=g).bfloat16()
+    W = (torch.randn(14336, 4096, device="cuda", generator=g) * 0.02).bfloat16()
+    y = torch.nn.functional.linear(x, W)
+    res = check_linear_rows(x, W, None, y)
+    assert res.ok, res.max_z
+    rng = random.Random(5)
+    for _ in range(8):
+        i, j = rng.randrange(4096), rng.randrange(14336)
+        y2 = y.clone()
+        _flip(y2, i * 14336 + j, 14)
+        res = check_linear_rows(x, W, None, y2)
+        assert not res.ok and (res.row, res.col_block) == (j, i // 128), (i, j, res)
