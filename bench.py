@@ -1,12 +1,19 @@
-"""Benchmark of the verification hot path on one MI355X: the serving checksum check of a bf16 Llama-MLP-shaped
-linear layer (x: 4096 tokens x 4096, W: 14336 x 4096, y = x @ W^T in bf16 with fp32 accumulation).
+"""Benchmark of the verification hot path on one MI355X: both checksums of a bf16 Llama-MLP-shaped linear layer
+(x: 4096 tokens x 4096, W: 14336 x 4096, y = x @ W^T in bf16 with fp32 accumulation).
 
-A step is one check of that layer (sdc_check_static: the expected-side GEMM on MFMA + one pass over y that scores
-every (row, 128-column block) pair).  Inputs are resident in HBM; the timed loop rotates over enough copies of
-(x, y) that each step's reads miss the 256 MB Infinity Cache (a cold check, the conservative number).  Reported:
-  value         algorithmic bytes of one check (x + y + the layer's three-part block sums) / time per step, GB/s
-  roofline      the dominant kernel (the y pass) against HBM peak, from HIP events on its launch stream
-  overhead      check time / the guarded GEMM's time on the same GPU and stream, warm (the check right after its
+A step checks that layer's output once with both identities:
+  column-block  every (token row, block of 128 output columns), plain and signed: the serving check
+                (sdc_check_static: expected side x @ parts on MFMA, one pass over y that sums and scores);
+  row-block     every (output column, block of 128 token rows), plain and signed: the column-block check of
+                y^T = W x^T (sdc_matmul_check on transposed views: block sums of x, W @ those sums on MFMA, one
+                pass over y reading down its columns).
+Inputs are resident in HBM; the timed loop rotates over enough copies of (x, y) that a step's reads of x and y miss
+the 256 MB Infinity Cache (W, 117 MB, is one tensor, as served).  Reported:
+  value         algorithmic bytes of one step (x + y + the layer's parts + W: what both checks must read at least)
+                / time per step, GB/s
+  roofline      the kernel with the largest share of the step, against its bound, from HIP events recorded on its
+                launch stream; traffic from the committed rocprofv3 counter summary
+  overhead      step time / the guarded GEMM's time on the same GPU and stream, warm (the check right after its
                 GEMM, as served) and cold
   cpu_baseline  the oracle's serving check (numpy, 1 thread) on a bounded sample of the same workload
 
@@ -21,6 +28,7 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 M, K, N = 4096, 4096, 14336
 
 
@@ -37,7 +45,7 @@ def _args():
 
 def cpu_baseline(x, W, y, seconds: float):
     """The oracle's serving check on the first rows of the workload, one thread, repeated for ~`seconds`."""
-    import numpy as np
+    import numpy as np  # noqa: F401
     from threadpoolctl import threadpool_limits
 
     from oracle import serve_check
@@ -57,8 +65,8 @@ def cpu_baseline(x, W, y, seconds: float):
                 break
     gbs = nbytes * reps / el / 1e9
     return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle.serve_check.check_static (numpy) on the first {rows} of 4096 rows, {reps} repetitions "
-                      f"in {el:.1f} s; same algorithmic bytes per row as the GPU check"}
+            "sample": f"oracle.serve_check.check_static (numpy, column-block check) on the first {rows} of 4096 "
+                      f"rows, {reps} repetitions in {el:.1f} s; bytes counted as the GPU column check counts them"}
 
 
 def _traffic(kernel: str):
@@ -85,6 +93,7 @@ def main():
     import torch
     torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
     from sdcguard_amd import _lib
+    from sdcguard_amd.checksum import linear_rows_operands, matmul_zscores, resolve
     from sdcguard_amd.serve import STATE_COLS, LayerChecksums, check_static_impl
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -99,22 +108,27 @@ def main():
         ys.append(torch.nn.functional.linear(x, W))
     cs = LayerChecksums(W, None, 128)
     state = torch.zeros(1, STATE_COLS, dtype=torch.int64, device=dev)
+    row_res = torch.zeros(3, dtype=torch.int64, device=dev)
     args = cs.tensors(True)
     nb = cs.nb
-    ws_bytes = int(L.sdc_check_static_workspace(M, K, N, 128))
+    rows_ops = [linear_rows_operands(xs[i], W, None, ys[i]) for i in range(a.copies)]
     torch.cuda.synchronize()
 
     def check(i):
         check_static_impl(xs[i], ys[i], *args, state, 0, 6.0, 1e-20)
+        A, B, C, _ = rows_ops[i]
+        matmul_zscores(A, B, C, None, out=row_res)
 
     for i in range(a.warmup):
         check(i % a.copies)
     torch.cuda.synchronize()
     if int(state[0, 2].item()) != a.warmup:
         raise RuntimeError("the check did not run")
-    z_clean = float(torch.tensor([int(state[0, 0].item()) >> 32], dtype=torch.int32).view(torch.float32).item())
+    z_col = float(torch.tensor([int(state[0, 0].item()) >> 32], dtype=torch.int32).view(torch.float32).item())
+    from sdcguard_amd.checksum import CheckStat
+    r_rows = resolve([CheckStat(row_res, N, M // 128, False, 6.0)])[0]
 
-    # timed region: the check alone, cold (rotating copies)
+    # timed region: both checks, cold (rotating copies)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
@@ -124,18 +138,19 @@ def main():
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop) / a.steps
 
-    # the same loop with per-kernel HIP events on the launch stream (roofline of the dominant kernel)
+    # the same loop with per-kernel HIP events on the launch stream
+    names = ["expected_gemm", "serve_fused", "b_stage", "b_finish", "split", "train_gemm", "train_score"]
     L.sdc_profile_reset()
     L.sdc_profile_enable(1)
     for i in range(a.steps):
         check(i % a.copies)
     torch.cuda.synchronize()
     L.sdc_profile_enable(0)
-    score_ms, score_n = _lib.profile_read("serve_fused")
-    gemm_ms, gemm_n = _lib.profile_read("expected_gemm")
+    kms = {}
+    for nm in names:
+        tot, cnt = _lib.profile_read(nm)
+        kms[nm] = tot / max(cnt, 1)
     L.sdc_profile_reset()
-    score_avg = score_ms / max(score_n, 1)
-    gemm_avg = gemm_ms / max(gemm_n, 1)
 
     # guarded GEMM alone, and GEMM + check back to back (warm: y and x still in the caches, as served)
     def gemm(i):
@@ -172,13 +187,37 @@ def main():
     copy_gbs = 2 * ys[0].numel() * 2 / (start.elapsed_time(stop) / a.steps * 1e-3) / 1e9
     del buf
 
+    xb, yb, wb = M * K * 2, M * N * 2, N * K * 2
     parts_bytes = K * 6 * nb * 2
-    alg_bytes = M * K * 2 + M * N * 2 + parts_bytes
+    alg_bytes = xb + yb + parts_bytes + wb
     value = alg_bytes / (ms * 1e-3) / 1e9
-    # the y pass reads y and the expected side (E planes + row norms) and the per-block constants
-    splits = int(L.sdc_expected_splits(M, K, 2 * nb))
-    score_bytes = M * N * 2 + splits * (M * 2 * nb * 4 + 2 * M * 4)
-    score_gbs = score_bytes / (score_avg * 1e-3) / 1e9
+    s_col = int(L.sdc_expected_splits(M, K, 2 * nb))
+    s_row = int(L.sdc_expected_splits(N, K, 2 * (M // 128)))
+    # per kernel: (bound, algorithmic amount per launch, unit): bytes it must move, or MFMA flops
+    alg = {
+        "expected_gemm": ("mfma", 2.0 * M * K * 6 * nb),
+        "serve_fused": ("hbm", yb + s_col * (M * 2 * nb * 4 + 2 * M * 4)),
+        "b_stage": ("hbm", xb),
+        "train_gemm": ("hbm", wb + s_row * (N * 2 * (M // 128) * 4 + 2 * N * 4)),
+        "train_score": ("hbm", yb + s_row * (N * 2 * (M // 128) * 4 + 2 * N * 4)),
+    }
+    kern = {}
+    for nm, (bound, amount) in alg.items():
+        t = kms[nm]
+        if t <= 0:
+            raise RuntimeError(f"no timing recorded for kernel {nm}")
+        if bound == "mfma":
+            ach = amount / (t * 1e-3) / 1e12
+            kern[nm] = {"ms": round(t, 5), "bound": "mfma", "achieved": round(ach, 1), "unit": "TFLOP/s",
+                        "frac": round(ach / MFMA_BF16_PEAK_TFLOPS, 4), "algorithmic": amount}
+        else:
+            ach = amount / (t * 1e-3) / 1e9
+            kern[nm] = {"ms": round(t, 5), "bound": "hbm", "achieved": round(ach, 1), "unit": "GB/s",
+                        "frac": round(ach / HBM_PEAK_GBS, 4), "algorithmic": amount}
+    for nm in ("b_finish", "split"):
+        kern[nm] = {"ms": round(kms[nm], 5), "bound": "latency"}
+    dom = max(alg, key=lambda nm: kms[nm])
+    d = kern[dom]
     out = {
         "metric": "checksum-verify GB/s (% of HBM peak) + overhead % vs guarded GEMM, 1 GPU",
         "value": round(value, 2),
@@ -192,22 +231,20 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "serving column-block checksum check of a bf16 Llama-MLP linear layer, "
-                               "x 4096x4096, W 14336x4096 (N(0,0.02)), y = x W^T bf16 (fp32 accumulation)",
+        "config": {"workload": "column-block and row-block checksum check of a bf16 Llama-MLP linear layer, "
+                               "x 4096x4096 N(0,1), W 14336x4096 N(0,0.02), y = x W^T bf16 (fp32 accumulation)",
                    "m": M, "k": K, "n": N, "block": 128, "copies_rotated": a.copies,
                    "algorithmic_bytes": alg_bytes},
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": "serve_fused", "achieved": round(score_gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(score_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": _traffic("serve_fused"), "avg_ms": round(score_avg, 5),
-                     "algorithmic_bytes": score_bytes},
-        "kernels_ms": {"expected_gemm": round(gemm_avg, 5), "serve_fused": round(score_avg, 5)},
+        "roofline": {"kernel": dom, "bound": d["bound"], "achieved": d["achieved"],
+                     "peak": MFMA_BF16_PEAK_TFLOPS if d["bound"] == "mfma" else HBM_PEAK_GBS, "unit": d["unit"],
+                     "frac": d["frac"], "traffic": _traffic(dom), "avg_ms": d["ms"]},
+        "kernels": kern,
         "device_copy_gbs": round(copy_gbs, 1),
-        "expected_gemm_tflops": round(2 * M * K * 6 * nb / (gemm_avg * 1e-3) / 1e12, 1),
         "guarded_gemm_ms": round(gemm_ms_step, 5),
         "overhead_pct_warm": round(100.0 * (both_ms - gemm_ms_step) / gemm_ms_step, 2),
         "overhead_pct_cold": round(100.0 * ms / gemm_ms_step, 2),
-        "clean_max_z": round(z_clean, 4),
+        "clean_max_z": {"column": round(z_col, 4), "row": round(float(r_rows.max_z), 4)},
     }
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(xs[0], W, ys[0], a.cpu_seconds)

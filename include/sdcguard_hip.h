@@ -88,7 +88,8 @@ int sdc_fingerprint2(const void* bits, int64_t n, int kind, int64_t* out, hipStr
 
 /* ---- per-kernel timing (no counterpart in the reference; for benchmarks) ------------------------------------
  * With profiling on, every kernel launch is bracketed by two HIP events on its stream; sdc_profile_read waits for
- * them and sums the durations of one kernel ("expected_gemm", "serve_score", "fingerprint3", ...). */
+ * them and sums the durations of one kernel: "expected_gemm" (serving GEMM), "serve_fused", "serve_sums",
+ * "serve_score", "b_stage", "b_finish", "split", "train_gemm", "train_score", "fingerprint3", "fingerprint2". */
 int sdc_profile_enable(int on);
 int sdc_profile_reset(void);
 int sdc_profile_read(const char* name, double* total_ms, int64_t* launches);

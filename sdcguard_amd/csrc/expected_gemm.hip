@@ -272,6 +272,7 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
   }
 
   // C[i][j] of a 32x32 MFMA tile sits in lane j + 32 * ((i / 4) % 2), register (i / 8) * 4 + i % 4
+  // (transposed planes: each lane's 4 consecutive registers are 4 consecutive rows, one 16-byte store)
   float* Es = g.E + (batch * g.splits + split) * m * N;
 #pragma unroll
   for (int n = 0; n < 2; ++n) {
@@ -280,9 +281,16 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t row = r0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          if (row < m) Es[row * N + col] = acc[i][n][r];
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int64_t row = r0 + wm * 64 + i * 32 + 8 * r4 + 4 * (lane >> 5);
+          if (g.et && row + 4 <= m && (m % 4) == 0) {
+            f32x4 v = {acc[i][n][4 * r4], acc[i][n][4 * r4 + 1], acc[i][n][4 * r4 + 2], acc[i][n][4 * r4 + 3]};
+            *reinterpret_cast<f32x4*>(&Es[col * m + row]) = v;
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (row + q < m) Es[g.et ? col * m + row + q : (row + q) * N + col] = acc[i][n][4 * r4 + q];
+          }
         }
     }
   }
@@ -367,7 +375,7 @@ int sdc_gemm_launch(int dtype, GemmArgs g, int64_t batches, hipStream_t stream) 
   const int wgn = g.N > 64 ? 2 : 1;
   const int64_t blocks = sdc_cdiv(g.m, 64 * (8 / wgn)) * sdc_cdiv(g.N, 64 * wgn) * g.splits * batches;
   if (blocks > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
-  SdcProf prof("expected_gemm", stream);
+  SdcProf prof(g.prof_name ? g.prof_name : "expected_gemm", stream);
   if (dtype == SDC_BF16)
     return wgn == 2 ? launch_dt<SDC_BF16, 2>(g, vec, blocks, stream) : launch_dt<SDC_BF16, 1>(g, vec, blocks, stream);
   return wgn == 2 ? launch_dt<SDC_FP16, 2>(g, vec, blocks, stream) : launch_dt<SDC_FP16, 1>(g, vec, blocks, stream);

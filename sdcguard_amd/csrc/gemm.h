@@ -9,7 +9,9 @@ struct GemmArgs {
   const void* B;                // parts: 3 x N depth-contiguous columns of the dtype, part p column c at
   int64_t sbb, sbc;             //   B[batch * sbb + (p * N + c) * sbc + kk]
   int64_t m, k, N, kchunk, splits;
-  float* E;                     // [batch][split][m][N]
+  float* E;                     // [batch][split][m][N], or [batch][split][N][m] with et
+  int et;                       // store E transposed (column-major per plane)
+  const char* prof_name;        // name for per-kernel timing (null: "expected_gemm")
   float* XN;                    // [batch][split][2][m]: sum of squares and sum of |a| of each row's depth slice
 };
 

@@ -129,20 +129,28 @@ __global__ __launch_bounds__(256) void b_stage_t_kernel(BStageArgs a) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) pl[e] = sg[e] = 0.f;
   const uint16_t* base = a.B + bb * a.sbb + jb * a.bs * a.sbn + kk0;
-  if (a.vec && kk0 + 8 <= a.k) {
-#pragma unroll 4
-    for (int c = cg; c < wid; c += 8) {
-      const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + c * a.sbn));
-      const float s = sp[c];
-      const float x[8] = {lo_of<DT>(v.x), hi_of<DT>(v.x), lo_of<DT>(v.y), hi_of<DT>(v.y),
-                          lo_of<DT>(v.z), hi_of<DT>(v.z), lo_of<DT>(v.w), hi_of<DT>(v.w)};
+  auto add8 = [&](const u32x4 v, float s) {
+    const float x[8] = {lo_of<DT>(v.x), hi_of<DT>(v.x), lo_of<DT>(v.y), hi_of<DT>(v.y),
+                        lo_of<DT>(v.z), hi_of<DT>(v.z), lo_of<DT>(v.w), hi_of<DT>(v.w)};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pl[e] += x[e];
-        sg[e] = fmaf(x[e], s, sg[e]);
-        mx = fmaxf(mx, nan_inf(x[e]));
-      }
+    for (int e = 0; e < 8; ++e) {
+      pl[e] += x[e];
+      sg[e] = fmaf(x[e], s, sg[e]);
+      mx = fmaxf(mx, nan_inf(x[e]));
     }
+  };
+  if (a.vec && kk0 + 8 <= a.k && wid == 128) {
+    // a full block: all 16 loads of this thread in flight before the first add
+    u32x4 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + (cg + 8 * i) * a.sbn));
+#pragma unroll
+    for (int i = 0; i < 16; ++i) add8(v[i], sp[cg + 8 * i]);
+  } else if (a.vec && kk0 + 8 <= a.k) {
+#pragma unroll 4
+    for (int c = cg; c < wid; c += 8)
+      add8(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + c * a.sbn)), sp[c]);
   } else if (kk0 < a.k) {
     const int ne = a.k - kk0 < 8 ? (int)(a.k - kk0) : 8;
 #pragma unroll 1
@@ -275,6 +283,7 @@ struct TrainArgs {
   int64_t k, splits, nbt, ncols;
   int b_batched;                   // B (and its stats) has one entry per batch
   int e_batched;                   // E / XN have one plane set per batch
+  int et;                          // E planes transposed (the column-read scoring pass)
   const float* E;
   const float* XN;
   const float* colstat;
@@ -329,7 +338,9 @@ __device__ __forceinline__ void train_pair(const TrainArgs& a, int64_t p, float 
   const bool last = (jb == a.cv.nb - 1) && (a.cv.rem > 0);
   const float wf = (float)(last ? a.cv.rem : a.cv.bs);
   const int64_t eb = a.e_batched ? bc : 0, bbi = a.b_batched ? bc : 0;
-  const float* ep = a.E + ((eb * a.splits) * a.cv.m + r) * a.ncols + 2 * jb;
+  // E planes row-major ([m][ncols]: plain and signed adjacent) or transposed ([ncols][m]: adjacent rows)
+  const float* ep = a.et ? a.E + ((eb * a.splits) * a.ncols + 2 * jb) * a.cv.m + r
+                         : a.E + ((eb * a.splits) * a.cv.m + r) * a.ncols + 2 * jb;
   const float* xp = a.XN + (eb * a.splits) * 2 * a.cv.m + r;
   const int64_t estep = a.cv.m * a.ncols, xstep = 2 * a.cv.m;
   float2 ev[SDC_MAX_SPLITS];
@@ -337,7 +348,8 @@ __device__ __forceinline__ void train_pair(const TrainArgs& a, int64_t p, float 
 #pragma unroll
   for (int s = 0; s < SDC_MAX_SPLITS; ++s)
     if (s < a.splits) {
-      ev[s] = *reinterpret_cast<const float2*>(ep + s * estep);
+      if (a.et) ev[s] = make_float2(ep[s * estep], ep[s * estep + a.cv.m]);
+      else ev[s] = *reinterpret_cast<const float2*>(ep + s * estep);
       xa[s] = xp[s * xstep];
       xb[s] = xp[s * xstep + a.cv.m];
     }
@@ -648,6 +660,9 @@ extern "C" int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t s
   g.B = parts; g.sbb = batch_b > 1 ? 3 * L.ncols * L.kp : 0; g.sbc = L.kp;
   g.m = m; g.k = k; g.N = L.ncols; g.splits = L.splits;
   g.E = ws + L.off_e; g.XN = ws + L.off_xn;
+  const bool c_t = scm == 1 && scn != 1 && L.nb < 65536 && batch_c < 65536;   // C read down its columns
+  g.et = c_t;
+  g.prof_name = "train_gemm";
   rc = sdc_gemm_launch(dtype, g, nbt, stream);
   if (rc != SDC_OK) return rc;
 
@@ -670,7 +685,8 @@ extern "C" int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t s
   ta.capk = (float)(1.02 + (double)k * 2.384185791015625e-07);
   ta.result = result; ta.zdump = scores_out;
   SdcProf prof("train_score", stream);
-  if (scm == 1 && scn != 1 && L.nb < 65536 && batch_c < 65536) {
+  ta.et = c_t;
+  if (c_t) {
     // C with adjacent rows (y^T): read 512 rows at a time down each column
     ta.cv.vec = (scn % 8 == 0) && (scb % 8 == 0) && ((uintptr_t)C % 16 == 0);
     dim3 grid((unsigned)sdc_cdiv(m, 512), (unsigned)L.nb, (unsigned)batch_c);
