@@ -2,16 +2,18 @@
 
 Run once, in a container that has the reference checked out at /root/reference (never on a GPU box):
 
-    SDCGUARD_SIGN_SEED=1 python tests/golden/make_golden.py
+    SDCGUARD_SIGN_SEED=1 python tests/golden/make_golden.py [signs] [train] [serve] [quant]
 
 It imports the reference's checksum and serve modules (pure Python + torch, CPU) and records, for seeded small
 cases, the inputs and the reference's answers:
   * signs.npz      the epoch-0 sign table of widths 1..128 and the epoch-3 table (checksum._signs at seed 1);
   * train.npz      checksum.matmul_zscores + resolve: every checksum's score (the array the reference reduces
                    with torch.max, recorded on the way) and the resolved (max_z, batch, row, col_block, noise);
-  * serve.npz      serve.check_static_impl: every checksum's score, the state row (keys and counts).
-Only numbers are stored (inputs as raw 16-bit words).  The integer fingerprints and the int8 check need no
-fixture: closed forms and brute force pin them (tests/test_oracle_fingerprint.py, tests/test_oracle_quant.py).
+  * serve.npz      serve.check_static_impl: every checksum's score, the state row (keys and counts);
+  * quant.npz      modes.judge on fp8 e4m3 and int8 GEMMs (inputs from modes._inputs, results of modes.gemm's CPU
+                   path, with and without an injected fault): per-block z and wrong-block counts.
+Only numbers are stored (inputs as raw 16-bit or 8-bit words).  The integer fingerprints need no fixture: closed
+forms and brute force pin them (tests/test_oracle_fingerprint.py).
 """
 from __future__ import annotations
 
@@ -253,18 +255,75 @@ def make_serve(sv):
     return len(names)
 
 
+def make_quant(md):
+    """modes.judge on small fp8 and int8 GEMMs (the fp8 unit and products per step of an unknown GPU).  Per input
+    set: a, b, the clean result c, and for each fault (none, +small, +large, NaN, huge; int8: none, +1) the changed
+    element (row, col, value), the per-block z and the wrong-block count."""
+    out = {}
+    i = 0
+    gen = torch.Generator().manual_seed(11)
+    for mode in ("fp8", "int8"):
+        for shape in ((24, 256, 256), (9, 384, 384)):
+            for dist, scale in (md.VARIANTS[:4] if shape[0] == 24 else md.VARIANTS[:2]):
+                a, b, a64, b64 = md._inputs(mode, shape, dist, scale, gen)
+                c0 = md.gemm(mode, a, b)
+                if mode == "fp8":
+                    out[f"q{i}_a"] = a.view(torch.uint8).numpy().copy()
+                    out[f"q{i}_b"] = b.view(torch.uint8).numpy().copy()
+                else:
+                    out[f"q{i}_a"] = a.numpy().copy()
+                    out[f"q{i}_b"] = b.numpy().copy()
+                out[f"q{i}_c"] = c0.numpy().copy()
+                out[f"q{i}_name"] = np.array(f"{mode} {shape} {dist} {scale}")
+                faults = (None, "add") if mode == "int8" else (None, "add", "big", "nan", "huge")
+                for f, fault in enumerate(faults):
+                    c = c0.clone()
+                    r = int(torch.randint(0, shape[0], (1,), generator=gen))
+                    j = int(torch.randint(0, shape[2], (1,), generator=gen))
+                    if fault is None:
+                        pass
+                    elif mode == "int8":
+                        c[r, j] += 1
+                    elif fault == "add":
+                        blk = c[r, (j // 128) * 128:(j // 128 + 1) * 128].double()
+                        c[r, j] += float(blk.norm() / math.sqrt(128)) * 0.02 + 1e-3
+                    elif fault == "big":
+                        blk = c[r, (j // 128) * 128:(j // 128 + 1) * 128].double()
+                        c[r, j] += float(blk.norm() / math.sqrt(128)) * 0.5 + 1e-2
+                    elif fault == "nan":
+                        c[r, j] = float("nan")
+                    else:
+                        c[r, j] = 3e30
+                    res = md.judge(mode, a64, b64, c, nfma=16, unit=md.UNIT["fp8"]) if mode == "fp8" else \
+                        md.judge(mode, a64, b64, c)
+                    out[f"q{i}_f{f}_at"] = np.array([r, j], np.int64)
+                    out[f"q{i}_f{f}_v"] = np.array(c[r, j].item(), c0.numpy().dtype)
+                    out[f"q{i}_f{f}_z"] = res["z"].float().numpy()
+                    out[f"q{i}_f{f}_wrong"] = np.int64(res["wrong_blocks"])
+                out[f"q{i}_nf"] = np.int64(len(faults))
+                i += 1
+    np.savez_compressed(os.path.join(OUT, "quant.npz"), **out)
+    return i
+
+
 def main():
     if os.environ.get("SDCGUARD_SIGN_SEED") != "1":
         sys.exit("run with SDCGUARD_SIGN_SEED=1")
     sys.path.insert(0, REF)
     from sdcguard import checksum as cs
+    from sdcguard import modes as md
     from sdcguard import serve as sv
     cs.USE_FAST = False
     torch.set_num_threads(4)
-    make_signs(cs)
-    nt = make_train(cs)
-    ns = make_serve(sv)
-    print(f"wrote signs.npz, train.npz ({nt} cases), serve.npz ({ns} cases) to {OUT}")
+    which = sys.argv[1:] or ["signs", "train", "serve", "quant"]
+    if "signs" in which:
+        make_signs(cs)
+    if "train" in which:
+        print("train.npz:", make_train(cs), "cases")
+    if "serve" in which:
+        print("serve.npz:", make_serve(sv), "cases")
+    if "quant" in which:
+        print("quant.npz:", make_quant(md), "cases")
 
 
 if __name__ == "__main__":
