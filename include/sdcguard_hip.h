@@ -74,6 +74,27 @@ int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t
                      float beta, float z, float abs_floor, const float* sign_table, int64_t* result, void* workspace,
                      int64_t workspace_bytes, float* scores_out, hipStream_t stream);
 
+/* ---- check of one quantized GEMM ----------------------------------------------------------------------------
+ * Replaces modes.judge (modes.py:231-291) for its int8 and fp8 branches, on the device, and extends the fp8 one to
+ * per-row activation scales sa and per-column weight scales sb (C = sa_i sb_j sum_k Aq[i,k] Bq[k,j]).
+ *   kind 0 = int8 W8A8: A (m x k) int8, C (m x n) int32 (c_dtype 2); parts = the block sums of B (plain, then
+ *     signed, per block) as two base-128 int8 digits, hi then lo, (2 x 2nb) columns of k bytes at spc bytes apart
+ *     (B2 = 128 hi + lo, |lo| <= 64).  The check is exact: every differing sum is a wrong block.
+ *   kind 1 = fp8 e4m3: A (m x k) fp8 e4m3fn (k-contiguous rows), sa (m) fp32 or NULL (1), C fp32 (c_dtype 0) or
+ *     bf16 (1); parts = the three bf16 parts of B2s = sum_j w_j sb_j Bq[:,j] per checksum column (3 x 2nb columns
+ *     of k elements, spc apart); bfrob (nb) = |sb Bq|_F per block; bcol (n) = |sb_j Bq[:,j]|_2 per column;
+ *     unit = the accumulation's rounding unit (2^-14 for an fp8 tensor-core accumulation of unknown precision,
+ *     modes.acc_unit), nfma = products per accumulation step (16, modes.n_fma; 0: none).
+ *   A row stride sam, C strides (scm, scn), in elements.  sign_table: as sdc_check_static (epoch 0).
+ *   result: int64[4], zeroed by the caller: the worst block's key (bits of z << 32 | row * nb + block), the key with
+ *     its noise, the number of wrong blocks (z > z; int8: any differing sum), blocks with a non-finite sum.
+ *   workspace: at least sdc_quant_check_workspace(kind, m, k, n, bs) bytes; scores_out: (m, nb) z or NULL. */
+int64_t sdc_quant_check_workspace(int kind, int64_t m, int64_t k, int64_t n, int64_t bs);
+int sdc_quant_check(int kind, const void* A, int64_t sam, const void* parts, int64_t spc, const float* sa,
+                    const void* C, int64_t scm, int64_t scn, int c_dtype, int64_t m, int64_t k, int64_t n, int64_t bs,
+                    const float* sign_table, const float* bfrob, const float* bcol, float unit, float nfma, float z,
+                    int64_t* result, void* workspace, int64_t workspace_bytes, float* scores_out, hipStream_t stream);
+
 /* Depth split the expected-side GEMM uses for an (m x k) @ (k x ncols) product (sizes the workspace). */
 int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
 
@@ -89,7 +110,8 @@ int sdc_fingerprint2(const void* bits, int64_t n, int kind, int64_t* out, hipStr
 /* ---- per-kernel timing (no counterpart in the reference; for benchmarks) ------------------------------------
  * With profiling on, every kernel launch is bracketed by two HIP events on its stream; sdc_profile_read waits for
  * them and sums the durations of one kernel: "expected_gemm" (serving GEMM), "serve_fused", "serve_sums",
- * "serve_score", "b_stage", "b_finish", "split", "train_gemm", "train_score", "fingerprint3", "fingerprint2". */
+ * "serve_score", "b_stage", "b_finish", "split", "train_gemm", "train_score", "quant_gemm_i8", "quant_gemm_fp8",
+ * "quant_score_i8", "quant_score_fp8", "fingerprint3", "fingerprint2". */
 int sdc_profile_enable(int on);
 int sdc_profile_reset(void);
 int sdc_profile_read(const char* name, double* total_ms, int64_t* launches);

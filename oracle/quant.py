@@ -4,7 +4,8 @@ int8 W8A8 -- modes.py:231-291 (`judge`, the int8 branch): C = A @ B with int8 A 
     int32 result C.  For every row and block of 128 columns the plain sum and one sum per +-1 pattern (default: the
     process's width-128 pattern, checksum._signs) must equal A @ (the same sums of B's columns) *exactly*.  The
     reference adds them in float64, exact below 2^53; here in int64.  A narrower last block (n not a multiple of
-    128) uses the first `rem` entries of each pattern (the reference requires n % 128 == 0).
+    128; modes.judge requires n % 128 == 0) uses the pattern of its own width, as every other check of the
+    reference does (checksum._signs(width), seeded SIGN_SEED + width).
 
 fp8 e4m3 with scales -- no reference function: the reference checks fp8 GEMMs only with per-tensor scale 1
     (modes.judge, fp8 branch).  Built from its pieces: for C[i, j] = sa_i * sb_j * sum_k Aq[i, k] Bq[k, j] (fp32,
@@ -32,11 +33,15 @@ FP8_NFMA = 16                  # modes.py:70-82 (n_fma) for GPUs other than Hopp
 C1 = C2 = C3 = 1.0             # modes.py:48
 
 
-def patterns(seed: int, P: int = 1) -> np.ndarray:
-    """(1 + P, 128) +-1 weights: ones, then P patterns; P = 1 is the process's width-128 pattern (modes.py:246-249
-    default), more are drawn as modes.draw_signs would (torch randint on a generator) by the caller."""
-    w = [np.ones(BLOCK, np.int64), _signs(BLOCK, seed).astype(np.int64)]
-    return np.stack(w[:1 + P])
+def patterns(seed: int, width: int = BLOCK) -> np.ndarray:
+    """(2, width) weights: ones, then the process's +-1 pattern of that width (modes.py:246-249 default for width
+    128; checksum._signs(width) for a narrower last block)."""
+    return np.stack([np.ones(width, np.int64), _signs(width, seed).astype(np.int64)])
+
+
+def _block_w(W, wid: int, seed):
+    """The weights of a block of `wid` columns: W itself for a full block, the width's own pattern otherwise."""
+    return W[:, :wid] if wid == W.shape[1] or seed is None else patterns(seed, wid)
 
 
 def _blocks(n: int):
@@ -44,8 +49,8 @@ def _blocks(n: int):
     return nbf + (1 if rem else 0), rem
 
 
-def int8_sums(A: np.ndarray, B: np.ndarray, C: np.ndarray, W: np.ndarray):
-    """(actual, expected), each (m, nb, P+1) int64: block sums of int32 C and A @ (block sums of B)."""
+def int8_sums(A: np.ndarray, B: np.ndarray, C: np.ndarray, W: np.ndarray, seed: int = 1):
+    """(actual, expected), each (m, nb, 2) int64: block sums of int32 C and A @ (block sums of B)."""
     A = A.astype(np.int64)
     B = B.astype(np.int64)
     C = C.astype(np.int64)
@@ -57,16 +62,16 @@ def int8_sums(A: np.ndarray, B: np.ndarray, C: np.ndarray, W: np.ndarray):
     for b in range(nb):
         lo = b * BLOCK
         wid = rem if (b == nb - 1 and rem) else BLOCK
-        w = W[:, :wid]
+        w = _block_w(W, wid, seed)
         actual[:, b, :] = C[:, lo:lo + wid] @ w.T
         B2[:, b, :] = B[:, lo:lo + wid] @ w.T
     expected = (A @ B2.reshape(B.shape[0], nb * npat)).reshape(m, nb, npat)
     return actual, expected
 
 
-def int8_judge(A, B, C, W) -> dict:
+def int8_judge(A, B, C, W, seed: int = 1) -> dict:
     """modes.judge("int8", ...): wrong_blocks and the per-block verdict (m, nb) bool."""
-    actual, expected = int8_sums(A, B, C, W)
+    actual, expected = int8_sums(A, B, C, W, seed)
     bad = (actual != expected).any(axis=-1)
     return {"wrong_blocks": int(bad.sum()), "blocks": bad.size, "bad": bad, "actual": actual,
             "expected": expected}
@@ -89,7 +94,7 @@ def fp8_e4m3_values() -> np.ndarray:
 
 
 def fp8_judge(Aq, Bq, sa, sb, C, W, *, c_bf16: bool = False, unit: float = FP8_UNIT, nfma: int = FP8_NFMA,
-              z: float = 6.0) -> dict:
+              z: float = 6.0, seed: int = 1) -> dict:
     """The scaled fp8 check above: per (row, block) worst z over the checksums, after the Inf/NaN and impossible
     rules (inf).  Aq, Bq: the fp8 values as float64; sa (m,), sb (n,) float; C: the result as float64."""
     Aq = np.asarray(Aq, np.float64)
@@ -100,7 +105,6 @@ def fp8_judge(Aq, Bq, sa, sb, C, W, *, c_bf16: bool = False, unit: float = FP8_U
     m, k = Aq.shape
     n = C.shape[1]
     nb, rem = _blocks(n)
-    Wf = np.asarray(W, np.float64)
     As = Aq * sa[:, None]
     Bs = Bq * sb[None, :]
     a_norm = np.sqrt((As ** 2).sum(1))                                   # (m,)
@@ -109,10 +113,10 @@ def fp8_judge(Aq, Bq, sa, sb, C, W, *, c_bf16: bool = False, unit: float = FP8_U
     for b in range(nb):
         lo = b * BLOCK
         wid = rem if (b == nb - 1 and rem) else BLOCK
-        w = Wf[:, :wid]
+        w = np.asarray(_block_w(W, wid, seed), np.float64)
         cb = C[:, lo:lo + wid]
         with np.errstate(invalid="ignore", over="ignore"):
-            actual = cb @ w.T                                            # (m, P+1)
+            actual = cb @ w.T                                            # (m, 2)
             expected = As @ (Bs[:, lo:lo + wid] @ w.T)
             c_norm = np.sqrt((cb ** 2).sum(1))
             b_frob = math.sqrt(float((Bs[:, lo:lo + wid] ** 2).sum()))

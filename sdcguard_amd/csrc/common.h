@@ -15,8 +15,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Element kinds of the checked matmul's operands.
-enum SdcDtype { SDC_BF16 = 0, SDC_FP16 = 1 };
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+
+// Element kinds of the checked matmul's operands.  The expected-side GEMM also runs in two quantized modes:
+// SDC_FP8 (A fp8 e4m3, converted exactly to bf16 on load; bf16 parts) and SDC_I8 (A int8; int8 parts).
+enum SdcDtype { SDC_BF16 = 0, SDC_FP16 = 1, SDC_FP8 = 2, SDC_I8 = 3 };
 
 // Status codes of the C ABI.
 enum SdcStatus {

@@ -26,6 +26,37 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
   }
 }
 
+__device__ __forceinline__ f32x16 mfma32_i8(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_bit_cast(f32x16, __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a),
+                                                                          __builtin_bit_cast(i32x4, b),
+                                                                          __builtin_bit_cast(i32x16, c), 0, 0, 0));
+}
+
+// fp8 e4m3 (OCP: bias 7, no infinities, S.1111.111 NaN) -> bf16 bits, exactly: normals move their exponent
+// (e + 120) and keep 3 mantissa bits; subnormals m * 2^-9 are normal in bf16.
+__device__ __forceinline__ uint32_t e4m3_to_bf16(uint32_t b) {
+  const uint32_t s = (b & 0x80u) << 8, e = (b >> 3) & 15u, m = b & 7u;
+  if (e == 15u && m == 7u) return s | 0x7FC0u;
+  if (e != 0u) return s | ((e + 120u) << 7) | (m << 4);
+  if (m == 0u) return s;
+  const uint32_t f = __float_as_uint((float)m * 0.001953125f);         // m * 2^-9, exact
+  return s | (f >> 16);
+}
+
+// 8 fp8 values (one 8-byte word pair) -> 8 bf16 (16 bytes)
+__device__ __forceinline__ u32x4 fp8x8_to_bf16(u32x2 v) {
+  u32x4 o;
+  uint32_t* po = reinterpret_cast<uint32_t*>(&o);
+#pragma unroll
+  for (int w = 0; w < 2; ++w)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t x = v[w] >> (16 * h);
+      po[2 * w + h] = e4m3_to_bf16(x & 0xFFu) | (e4m3_to_bf16((x >> 8) & 0xFFu) << 16);
+    }
+  return o;
+}
+
 // 8 consecutive (in depth) 16-bit elements at p[kk * sk], or zeros past `lim`
 template <bool VEC>
 __device__ __forceinline__ u32x4 load8(const uint16_t* p, int64_t sk, int64_t kk, int64_t lim, bool ok) {
@@ -43,6 +74,20 @@ __device__ __forceinline__ u32x4 load8(const uint16_t* p, int64_t sk, int64_t kk
     v.w = e[6] | ((uint32_t)e[7] << 16);
     return v;
   }
+}
+
+// 8 fp8 values at p[kk * sk ...] (bounds-checked, zero past `lim`) as bf16
+__device__ __forceinline__ u32x4 load8_fp8(const uint8_t* p, int64_t sk, int64_t kk, int64_t lim, bool ok) {
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (!ok) return v;
+  uint32_t* pv = reinterpret_cast<uint32_t*>(&v);
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) {
+    const uint32_t lo = kk + i < lim ? e4m3_to_bf16(p[(kk + i) * sk]) : 0u;
+    const uint32_t hi = kk + i + 1 < lim ? e4m3_to_bf16(p[(kk + i + 1) * sk]) : 0u;
+    pv[i / 2] = lo | (hi << 16);
+  }
+  return v;
 }
 
 __device__ __forceinline__ uint32_t to_bf16_bits(float f) {
@@ -114,21 +159,29 @@ constexpr int KS = 32;                 // depth per stage
 constexpr int LP = KS + 8;             // LDS row pitch (elements)
 constexpr int NT = 512;                // threads per workgroup
 
-template <int WGN>
+template <int WGN, int NP>
 struct Tile {
   static constexpr int WGM = 8 / WGN;
   static constexpr int TM = 64 * WGM;
   static constexpr int TN = 64 * WGN;
   static constexpr int ACH = TM * (KS / 8);                   // 16-byte chunks of A per stage
-  static constexpr int BCH = 3 * TN * (KS / 8);               // ... of the three parts of B
+  static constexpr int BCH = NP * TN * (KS / 8);              // ... of the NP parts of B
   static constexpr int NA = (ACH + NT - 1) / NT;              // per thread
   static constexpr int NB = (BCH + NT - 1) / NT;
-  static constexpr int ROWS = TM + 3 * TN;                    // LDS rows per buffer
+  static constexpr int ROWS = TM + NP * TN;                   // LDS rows per buffer
 };
 
-template <int DT, int WGN, bool VEC>
+// MODE: SDC_BF16 / SDC_FP16 (A and 3 parts of that type), SDC_FP8 (A fp8 converted to bf16 on load, 3 bf16
+// parts), SDC_I8 (A int8 and 2 int8 parts: the block sums' base-128 digits, each into its own int32
+// accumulator; depth and strides are in pairs of int8 so that a 16-byte chunk is 8 "elements" as for 16-bit data,
+// and the 32x32x32 int8 MFMA takes a k-step of 16 pairs).
+template <int MODE, int WGN, bool VEC>
 __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
-  using T = Tile<WGN>;
+  constexpr int NP = MODE == SDC_I8 ? 2 : 3;                  // parts
+  constexpr int NACC = MODE == SDC_I8 ? 2 : 1;                // accumulator sets
+  constexpr int DT = MODE == SDC_FP16 ? SDC_FP16 : SDC_BF16;  // element type of the LDS tiles (16-bit modes)
+  constexpr int ESA = MODE == SDC_FP8 ? 1 : 2;                // bytes per A element in memory
+  using T = Tile<WGN, NP>;
   __shared__ __attribute__((aligned(16))) uint16_t lds[2][T::ROWS * LP];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int wm = w / WGN, wn = w % WGN;
@@ -144,12 +197,12 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
   const int nst = kbeg < kend ? (int)sdc_cdiv(kend - kbeg, KS) : 0;
   const bool norms = ct == 0;
   const int64_t m = g.m, N = g.N;
-  const uint16_t* Ab = g.A + batch * g.sab;
+  const uint8_t* Ab = (const uint8_t*)g.A + batch * g.sab * ESA;
   const uint16_t* Pb = (const uint16_t*)g.B + batch * g.sbb;
 
   // this thread's chunks: A chunk c is (row c / 4, depth 8 (c % 4)); B chunk c is (LDS row c / 4: part, column);
   // indexes past the end repeat the last chunk (the same value is stored twice)
-  const uint16_t* asrc[T::NA];
+  const uint8_t* asrc[T::NA];
   int alds[T::NA], ak[T::NA];
   bool aok[T::NA];
 #pragma unroll
@@ -157,7 +210,7 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
     const int c = (t + NT * j) < T::ACH ? t + NT * j : T::ACH - 1;
     const int64_t row = r0 + c / 4;
     aok[j] = row < m;
-    asrc[j] = Ab + (aok[j] ? row : 0) * g.sam;
+    asrc[j] = Ab + (aok[j] ? row : 0) * g.sam * ESA;
     alds[j] = (c / 4) * LP + 8 * (c % 4);
     ak[j] = 8 * (c % 4);
   }
@@ -183,12 +236,20 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
     const int64_t k0 = kbeg + (int64_t)st * KS;
     if constexpr (VEC) {
 #pragma unroll
-      for (int j = 0; j < T::NA; ++j) ra[set][j] = *reinterpret_cast<const u32x4*>(asrc[j] + (k0 + ak[j]));
+      for (int j = 0; j < T::NA; ++j) {
+        if constexpr (MODE == SDC_FP8)
+          ra[set][j] = fp8x8_to_bf16(*reinterpret_cast<const u32x2*>(asrc[j] + (k0 + ak[j])));
+        else
+          ra[set][j] = *reinterpret_cast<const u32x4*>(asrc[j] + (k0 + ak[j]) * 2);
+      }
 #pragma unroll
       for (int j = 0; j < T::NB; ++j) rb[set][j] = *reinterpret_cast<const u32x4*>(bsrc[j] + (k0 + bk[j]));
     } else {
 #pragma unroll
-      for (int j = 0; j < T::NA; ++j) ra[set][j] = load8<false>(asrc[j], g.sak, k0 + ak[j], kend, aok[j]);
+      for (int j = 0; j < T::NA; ++j) {
+        if constexpr (MODE == SDC_FP8) ra[set][j] = load8_fp8(asrc[j], g.sak, k0 + ak[j], kend, aok[j]);
+        else ra[set][j] = load8<false>((const uint16_t*)asrc[j], g.sak, k0 + ak[j], kend, aok[j]);
+      }
 #pragma unroll
       for (int j = 0; j < T::NB; ++j) rb[set][j] = load8<false>(bsrc[j], 1, k0 + bk[j], kend, bok[j]);
     }
@@ -201,39 +262,47 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < T::NA; ++j) {
       *reinterpret_cast<u32x4*>(&L[alds[j]]) = ra[set][j];
-      if (norms && t + NT * j < T::ACH) norm_acc<DT>(ra[set][j], sq[j], ab[j]);
+      if constexpr (MODE != SDC_I8)
+        if (norms && t + NT * j < T::ACH) norm_acc<DT>(ra[set][j], sq[j], ab[j]);
     }
 #pragma unroll
     for (int j = 0; j < T::NB; ++j) *reinterpret_cast<u32x4*>(&L[blds[j]]) = rb[set][j];
   };
 
-  f32x16 acc[2][2];
+  f32x16 acc[NACC][2][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int q = 0; q < NACC; ++q)
 #pragma unroll
-    for (int n = 0; n < 2; ++n)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][n][r] = 0.f;
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[q][i][n][r] = 0.f;         // (int8: the bits of integer 0)
 
   auto compute = [&](int buf) {
     const uint16_t* L = lds[buf];
 #pragma unroll
     for (int s = 0; s < KS / 16; ++s) {
       const int ko = 16 * s + (lane >> 5) * 8;
-      u32x4 a[2], bv[3][2];
+      u32x4 a[2], bv[NP][2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const u32x4*>(&L[(wm * 64 + 32 * i + (lane & 31)) * LP + ko]);
 #pragma unroll
-      for (int p = 0; p < 3; ++p)
+      for (int p = 0; p < NP; ++p)
 #pragma unroll
         for (int n = 0; n < 2; ++n)
           bv[p][n] = *reinterpret_cast<const u32x4*>(&L[(T::TM + p * T::TN + wn * 64 + 32 * n + (lane & 31)) * LP + ko]);
 #pragma unroll
-      for (int p = 0; p < 3; ++p)
+      for (int p = 0; p < NP; ++p)
 #pragma unroll
         for (int n = 0; n < 2; ++n) {
-          acc[0][n] = mfma32<DT>(a[0], bv[p][n], acc[0][n]);
-          acc[1][n] = mfma32<DT>(a[1], bv[p][n], acc[1][n]);
+          if constexpr (MODE == SDC_I8) {
+            acc[p][0][n] = mfma32_i8(a[0], bv[p][n], acc[p][0][n]);
+            acc[p][1][n] = mfma32_i8(a[1], bv[p][n], acc[p][1][n]);
+          } else {
+            acc[0][0][n] = mfma32<DT>(a[0], bv[p][n], acc[0][0][n]);
+            acc[0][1][n] = mfma32<DT>(a[1], bv[p][n], acc[0][1][n]);
+          }
         }
     }
   };
@@ -272,29 +341,34 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
   }
 
   // C[i][j] of a 32x32 MFMA tile sits in lane j + 32 * ((i / 4) % 2), register (i / 8) * 4 + i % 4
-  // (transposed planes: each lane's 4 consecutive registers are 4 consecutive rows, one 16-byte store)
-  float* Es = g.E + (batch * g.splits + split) * m * N;
+  // (transposed planes: each lane's 4 consecutive registers are 4 consecutive rows, one 16-byte store).  int8: the
+  // two digit planes of a split are adjacent planes, their values the int32 bits.
 #pragma unroll
-  for (int n = 0; n < 2; ++n) {
-    const int64_t col = c0 + wn * 64 + 32 * n + (lane & 31);
-    if (col < N) {
+  for (int pa = 0; pa < NACC; ++pa) {
+    float* Es = g.E + ((batch * g.splits + split) * NACC + pa) * m * N;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+    for (int n = 0; n < 2; ++n) {
+      const int64_t col = c0 + wn * 64 + 32 * n + (lane & 31);
+      if (col < N) {
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const int64_t row = r0 + wm * 64 + i * 32 + 8 * r4 + 4 * (lane >> 5);
-          if (g.et && row + 4 <= m && (m % 4) == 0) {
-            f32x4 v = {acc[i][n][4 * r4], acc[i][n][4 * r4 + 1], acc[i][n][4 * r4 + 2], acc[i][n][4 * r4 + 3]};
-            *reinterpret_cast<f32x4*>(&Es[col * m + row]) = v;
-          } else {
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              if (row + q < m) Es[g.et ? col * m + row + q : (row + q) * N + col] = acc[i][n][4 * r4 + q];
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const int64_t row = r0 + wm * 64 + i * 32 + 8 * r4 + 4 * (lane >> 5);
+            const f32x16& av = acc[pa][i][n];
+            if (g.et && row + 4 <= m && (m % 4) == 0) {
+              f32x4 v = {av[4 * r4], av[4 * r4 + 1], av[4 * r4 + 2], av[4 * r4 + 3]};
+              *reinterpret_cast<f32x4*>(&Es[col * m + row]) = v;
+            } else {
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                if (row + q < m) Es[g.et ? col * m + row + q : (row + q) * N + col] = av[4 * r4 + q];
+            }
           }
-        }
+      }
     }
   }
-  if (norms) {
+  if (norms && MODE != SDC_I8) {
     float* xs = g.XN + (batch * g.splits + split) * 2 * m;
 #pragma unroll
     for (int j = 0; j < T::NA; ++j) {
@@ -313,12 +387,17 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
   }
 }
 
-template <int DT, int WGN>
+template <int MODE, int WGN>
 int launch_dt(GemmArgs g, bool vec, int64_t blocks, hipStream_t stream) {
-  if (vec) hipLaunchKernelGGL((expected_gemm_kernel<DT, WGN, true>), dim3((unsigned)blocks), dim3(NT), 0, stream, g);
-  else hipLaunchKernelGGL((expected_gemm_kernel<DT, WGN, false>), dim3((unsigned)blocks), dim3(NT), 0, stream, g);
+  if (vec) hipLaunchKernelGGL((expected_gemm_kernel<MODE, WGN, true>), dim3((unsigned)blocks), dim3(NT), 0, stream, g);
+  else hipLaunchKernelGGL((expected_gemm_kernel<MODE, WGN, false>), dim3((unsigned)blocks), dim3(NT), 0, stream, g);
   SDC_LAUNCH_CHECK();
   return SDC_OK;
+}
+
+template <int MODE>
+int launch_mode(GemmArgs g, bool vec, int wgn, int64_t blocks, hipStream_t stream) {
+  return wgn == 2 ? launch_dt<MODE, 2>(g, vec, blocks, stream) : launch_dt<MODE, 1>(g, vec, blocks, stream);
 }
 
 // fp32 B2^T columns -> three parts (dtype), each column divided by its power of two first (exact)
@@ -369,16 +448,22 @@ extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols) {
 
 int sdc_gemm_launch(int dtype, GemmArgs g, int64_t batches, hipStream_t stream) {
   if (g.splits < 1 || g.splits > SDC_MAX_SPLITS || batches < 1) return SDC_EINVAL;
+  if (dtype < SDC_BF16 || dtype > SDC_I8) return SDC_EINVAL;
   g.kchunk = sdc_cdiv(sdc_cdiv(g.k, g.splits), KS) * KS;
-  const bool vec = g.sak == 1 && (g.k % KS == 0) && (g.sam % 8 == 0) && (g.sab % 8 == 0) &&
+  const int64_t ea = dtype == SDC_FP8 ? 1 : 2;                   // bytes per A element
+  const bool vec = g.sak == 1 && (g.k % KS == 0) && ((g.sam * ea) % 16 == 0) && ((g.sab * ea) % 16 == 0) &&
                    ((uintptr_t)g.A % 16 == 0) && (g.sbc % 8 == 0) && (g.sbb % 8 == 0) && ((uintptr_t)g.B % 16 == 0);
+  if (dtype == SDC_FP8 && !vec) return SDC_EUNSUPPORTED;          // fp8 A: k-contiguous, aligned rows only
   const int wgn = g.N > 64 ? 2 : 1;
   const int64_t blocks = sdc_cdiv(g.m, 64 * (8 / wgn)) * sdc_cdiv(g.N, 64 * wgn) * g.splits * batches;
   if (blocks > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
   SdcProf prof(g.prof_name ? g.prof_name : "expected_gemm", stream);
-  if (dtype == SDC_BF16)
-    return wgn == 2 ? launch_dt<SDC_BF16, 2>(g, vec, blocks, stream) : launch_dt<SDC_BF16, 1>(g, vec, blocks, stream);
-  return wgn == 2 ? launch_dt<SDC_FP16, 2>(g, vec, blocks, stream) : launch_dt<SDC_FP16, 1>(g, vec, blocks, stream);
+  switch (dtype) {
+    case SDC_BF16: return launch_mode<SDC_BF16>(g, vec, wgn, blocks, stream);
+    case SDC_FP16: return launch_mode<SDC_FP16>(g, vec, wgn, blocks, stream);
+    case SDC_FP8: return launch_mode<SDC_FP8>(g, vec, wgn, blocks, stream);
+    default: return launch_mode<SDC_I8>(g, vec, wgn, blocks, stream);
+  }
 }
 
 int sdc_split_launch(int dtype, const float* B2T, const float* scale, int64_t sscb, int64_t scale_stride,

@@ -1,0 +1,172 @@
+"""Checks of quantized GEMMs on the device: int8 W8A8 (exact) and fp8 e4m3 with per-row / per-column scales.
+
+Mirrors the reference's modes.judge (modes.py:231-291) for its "int8" and "fp8" branches -- the same checksums
+(the plain sum of every 128-column block and one signed sum per block with the process's pattern), the same exact
+int8 comparison, the same fp8 noise u (C1 |a_i| |B_blk|_F + (C2 sqrt(k) + C3 k / nfma) |C_blk|) and Inf/NaN /
+Cauchy-Schwarz rules -- and returns the same summary ({"wrong_blocks", "blocks", "worst_z", "z"}).  The fp8
+check takes the scales of a real fp8 GEMM (C = sa_i sb_j sum_k Aq[i,k] Bq[k,j], fp32 or bf16 result); with unit
+scales and an fp32 result it is modes.judge("fp8") itself.  Everything runs in libsdcguard_hip.so
+(sdc_quant_check): an MFMA GEMM for the expected side, one pass over C.
+"""
+from __future__ import annotations
+
+import struct
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from .checksum import sign_table
+
+BLOCK = 128
+ALARM = 6.0
+UNIT_FP8 = 2.0 ** -14            # modes.py:49: an fp8 accumulation of unknown precision keeps 13 bits per step
+NFMA_FP8 = 16                    # modes.py:70-82: products per step for GPUs other than Hopper / Blackwell
+_C_DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.int32: 2}
+
+
+def _block_weights(n: int, block: int, device) -> torch.Tensor:
+    """(n, 2 nb) float64: column 2b sums block b, column 2b + 1 its signed sum (the epoch-0 pattern of its width)."""
+    nb = -(-n // block)
+    tab = sign_table("cpu").double().view(128, 128)
+    w = torch.zeros(n, 2 * nb, dtype=torch.float64)
+    for b in range(nb):
+        lo, hi = b * block, min(n, (b + 1) * block)
+        w[lo:hi, 2 * b] = 1.0
+        w[lo:hi, 2 * b + 1] = tab[hi - lo - 1, :hi - lo]
+    return w.to(device)
+
+
+def _split3(x: torch.Tensor) -> torch.Tensor:
+    """fp32 -> three bf16 parts whose sum is x to ~2^-27 (checksum._split3)."""
+    hi = x.bfloat16()
+    r = x - hi.float()
+    mid = r.bfloat16()
+    lo = (r - mid.float()).bfloat16()
+    return torch.stack([hi, mid, lo])
+
+
+@dataclass
+class QuantChecksums:
+    """Per-weight constants of a quantized GEMM C = A @ B (B: k x n, the weight), made once at load time.
+
+    int8:  parts (2, 2nb, k) int8 -- the block sums' base-128 digits (B2 = 128 hi + lo, |lo| <= 64).
+    fp8:   parts (3, 2nb, k) bf16 -- B2s = sum_j w_j sb_j Bq[:, j] split in three; bfrob (nb) and bcol (n)."""
+    kind: str
+    k: int
+    n: int
+    block: int
+    parts: torch.Tensor
+    bfrob: Optional[torch.Tensor] = None
+    bcol: Optional[torch.Tensor] = None
+
+    @classmethod
+    def make(cls, B: torch.Tensor, sb: Optional[torch.Tensor] = None, block: int = BLOCK) -> "QuantChecksums":
+        if B.dim() != 2:
+            raise ValueError("B must be (k, n)")
+        k, n = B.shape
+        W = _block_weights(n, block, B.device)
+        if B.dtype == torch.int8:
+            if sb is not None:
+                raise ValueError("int8 check: no scales (the accumulator itself is checked, exactly)")
+            if k % 2:
+                raise ValueError("int8 check: k must be even")
+            B2 = B.double() @ W                                   # exact: |B2| <= 128 * 127
+            hi = torch.floor((B2 + 64) / 128)
+            lo = B2 - 128 * hi
+            parts = torch.stack([hi, lo]).to(torch.int8).transpose(1, 2).contiguous()   # (2, 2nb, k)
+            return cls("int8", k, n, block, parts)
+        if B.dtype == torch.float8_e4m3fn:
+            Bs = B.double() if sb is None else B.double() * sb.double().view(1, n)
+            B2s = (Bs @ W).float()
+            parts = _split3(B2s.t().contiguous())                  # (3, 2nb, k)
+            nb = W.shape[1] // 2
+            pad = nb * block - n
+            sq = torch.nn.functional.pad(Bs.pow(2).sum(0), (0, pad)).view(nb, block).sum(1)
+            return cls("fp8", k, n, block, parts.contiguous(), sq.sqrt().float(), Bs.pow(2).sum(0).sqrt().float())
+        raise ValueError(f"unsupported weight dtype {B.dtype} (int8 or float8_e4m3fn)")
+
+
+@dataclass
+class QuantStat:
+    """A queued quantized check: its result row on the device and what decoding it needs."""
+    result: torch.Tensor          # [4] int64
+    m: int
+    nb: int
+    kind: str
+    z: float
+    scores: Optional[torch.Tensor] = None
+
+
+def quant_zscores(A: torch.Tensor, consts: QuantChecksums, C: torch.Tensor, *, sa: Optional[torch.Tensor] = None,
+                  unit: float = UNIT_FP8, nfma: Optional[int] = NFMA_FP8, z: float = ALARM,
+                  scores_out: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                  workspace: Optional[torch.Tensor] = None) -> QuantStat:
+    """Queue the check of C against A (m x k: int8, or fp8 e4m3 with per-row scales sa) and the weight's constants,
+    without waiting."""
+    from . import _lib
+    _lib.require_gpu(A, C, consts.parts)
+    m, k = A.shape
+    if C.shape != (m, consts.n) or k != consts.k:
+        raise ValueError(f"shape mismatch: A{tuple(A.shape)} C{tuple(C.shape)} weight ({consts.k}, {consts.n})")
+    if A.stride(1) != 1:
+        A = A.contiguous()
+    kind = 0 if consts.kind == "int8" else 1
+    if kind == 0 and (A.dtype != torch.int8 or C.dtype != torch.int32):
+        raise ValueError("int8 check: A int8 and C int32")
+    if kind == 1 and (A.dtype != torch.float8_e4m3fn or C.dtype not in (torch.float32, torch.bfloat16)):
+        raise ValueError("fp8 check: A float8_e4m3fn and C float32 or bfloat16")
+    if sa is not None:
+        sa = sa.float().contiguous()
+    L = _lib.lib()
+    nb = -(-consts.n // consts.block)
+    if out is None:
+        out = torch.zeros(4, dtype=torch.int64, device=C.device)
+    need = int(L.sdc_quant_check_workspace(kind, m, k, consts.n, consts.block))
+    ws = workspace if workspace is not None and workspace.numel() >= need else \
+        torch.empty(need, dtype=torch.uint8, device=C.device)
+    tab = sign_table(C.device)
+    P = consts.parts
+    Av = A.view(torch.uint8) if kind == 1 else A
+    rc = L.sdc_quant_check(
+        kind, Av.data_ptr(), Av.stride(0), P.data_ptr(), P.stride(1), None if sa is None else sa.data_ptr(),
+        C.data_ptr(), C.stride(0), C.stride(1), _C_DTYPES[C.dtype], m, k, consts.n, consts.block, tab.data_ptr(),
+        None if consts.bfrob is None else consts.bfrob.data_ptr(), None if consts.bcol is None else consts.bcol.data_ptr(),
+        float(unit), float(nfma or 0), float(z), out.data_ptr(), ws.data_ptr(), ws.numel(),
+        None if scores_out is None else scores_out.data_ptr(), _lib.stream_of(C))
+    _lib.check(rc, "sdc_quant_check")
+    return QuantStat(out, m, nb, consts.kind, z, scores_out)
+
+
+def resolve(st: QuantStat) -> dict:
+    """modes.judge's summary of a queued check (one device-to-host copy): wrong_blocks, blocks, worst_z (None for
+    int8, as the reference reports), and the worst block's (row, block) and noise."""
+    r = [int(v) for v in st.result.cpu().tolist()]
+
+    def f32(bits: int) -> float:
+        return struct.unpack("<f", struct.pack("<I", bits & 0xFFFFFFFF))[0]
+    worst = f32(r[0] >> 32) if r[0] else 0.0
+    flat = r[0] & 0xFFFFFFFF
+    noise = f32(r[1])
+    out = {"wrong_blocks": r[2], "blocks": st.m * st.nb, "worst_z": None if st.kind == "int8" else worst,
+           "row": flat // st.nb if r[0] else None, "block": flat % st.nb if r[0] else None,
+           "noise": noise, "nonfinite_blocks": r[3]}
+    if st.scores is not None:
+        out["z"] = st.scores
+    return out
+
+
+def judge(mode: str, a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, nfma: Optional[int] = NFMA_FP8,
+          unit: Optional[float] = None, sa: Optional[torch.Tensor] = None, sb: Optional[torch.Tensor] = None,
+          z: float = ALARM) -> dict:
+    """modes.judge(mode, a, b, c) for "int8" and "fp8" on the GPU: a (m x k) and b (k x n) are the quantized
+    inputs themselves (not float64 copies), c the GEMM's result; per-block z in result["z"] (m, nb)."""
+    if mode not in ("int8", "fp8"):
+        raise ValueError("judge on the device covers the int8 and fp8 modes")
+    consts = QuantChecksums.make(b, sb)
+    m = c.shape[0]
+    nb = -(-c.shape[1] // BLOCK)
+    zs = torch.empty(m, nb, dtype=torch.float32, device=c.device)
+    st = quant_zscores(a, consts, c, sa=sa, unit=UNIT_FP8 if unit is None else unit, nfma=nfma, z=z, scores_out=zs)
+    return resolve(st)
+

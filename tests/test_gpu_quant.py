@@ -1,0 +1,175 @@
+"""The quantized checks on the GPU (sdc_quant_check through sdcguard_amd.modes) against the reference's
+modes.judge answers (tests/golden/quant.npz), the oracle (oracle/quant.py) on scaled fp8 problems, the
+reference's +-127 known answer, and the 2048 x 7168 x 4096 int8 / fp8 workloads with injected faults."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import quant
+from tests import _golden as G
+
+pytestmark = pytest.mark.gpu
+
+Q = G.load("quant.npz")
+NCASES = sum(1 for k in Q.files if k.endswith("_nf"))
+
+
+def _cases(mode):
+    return [(i, f) for i in range(NCASES) if str(Q[f"q{i}_name"]).startswith(mode)
+            for f in range(int(Q[f"q{i}_nf"]))]
+
+
+def _case(i, f):
+    a, b, c = Q[f"q{i}_a"], Q[f"q{i}_b"], Q[f"q{i}_c"].copy()
+    r, j = (int(v) for v in Q[f"q{i}_f{f}_at"])
+    c[r, j] = Q[f"q{i}_f{f}_v"]
+    return str(Q[f"q{i}_name"]), a, b, c, Q[f"q{i}_f{f}_z"], int(Q[f"q{i}_f{f}_wrong"])
+
+
+def _fp8(a_u8: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(a_u8).cuda().view(torch.float8_e4m3fn)
+
+
+@pytest.mark.parametrize("i,f", _cases("int8"))
+def test_int8_matches_reference(i, f):
+    from sdcguard_amd import modes
+    name, a, b, c, z, wrong = _case(i, f)
+    res = modes.judge("int8", torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda(), torch.from_numpy(c).cuda())
+    assert res["wrong_blocks"] == wrong, name
+    assert np.array_equal(np.isinf(res["z"].cpu().numpy()), np.isinf(z)), name
+
+
+def _slack(A, B, sa, sb, C, W):
+    """fp32 rounding of the expected side (MFMA accumulation of the three parts) in units of each block's noise."""
+    Bs = B * sb[None, :]
+    m, n = C.shape
+    nb = -(-n // 128)
+    out = np.zeros((m, nb))
+    As = A * sa[:, None]
+    for b in range(nb):
+        lo, hi = 128 * b, min(n, 128 * b + 128)
+        b2 = Bs[:, lo:hi] @ W[:, :hi - lo].T
+        out[:, b] = (np.abs(As) @ np.abs(b2)).max(axis=1)
+    return out * 2.0 ** -22
+
+
+@pytest.mark.parametrize("i,f", _cases("fp8"))
+def test_fp8_matches_reference(i, f):
+    """Unit scales, fp32 result: modes.judge('fp8', nfma=16, unit=2^-14); z within 1e-3 (plus the expected side's
+    fp32 rounding), verdicts and non-finite blocks identical."""
+    from sdcguard_amd import modes
+    name, a, b, c, z, wrong = _case(i, f)
+    res = modes.judge("fp8", _fp8(a), _fp8(b), torch.from_numpy(c).cuda(), nfma=16, unit=modes.UNIT_FP8)
+    zg = res["z"].cpu().numpy()
+    assert res["wrong_blocks"] == wrong, (name, f)
+    assert np.array_equal(np.isinf(zg), np.isinf(z)), name
+    fin = np.isfinite(z)
+    vals = quant.fp8_e4m3_values()
+    A, B = vals[a], vals[b]
+    sl = _slack(A, B, np.ones(A.shape[0]), np.ones(B.shape[1]), c, quant.patterns(1))
+    den = 2.0 ** -14 * (np.sqrt((A ** 2).sum(1))[:, None] * 1.0 + 1.0)   # a lower bound of every block's noise
+    tol = 1e-3 * np.maximum(1.0, np.abs(z)) + sl / den
+    assert (np.abs(zg[fin] - z[fin]) <= tol[fin]).all(), (name, np.abs(zg[fin] - z[fin]).max())
+
+
+def _scaled_problem(seed, m, k, n, out=torch.float32):
+    """fp8 inputs with per-row / per-column scales 10^U(-3,-1) and C = sa_i sb_j (Aq @ Bq)_ij computed in float64
+    on the GPU, rounded to `out`."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    Aq = (torch.randn(m, k, device="cuda", generator=g) * 4).clamp(-448, 448).to(torch.float8_e4m3fn)
+    Bq = (torch.randn(k, n, device="cuda", generator=g) * 4).clamp(-448, 448).to(torch.float8_e4m3fn)
+    sa = 10.0 ** (torch.rand(m, device="cuda", generator=g) * 2 - 3)
+    sb = 10.0 ** (torch.rand(n, device="cuda", generator=g) * 2 - 3)
+    C = ((Aq.double() @ Bq.double()) * sa.double()[:, None] * sb.double()[None, :]).to(out)
+    return Aq, Bq, sa.float(), sb.float(), C
+
+
+@pytest.mark.parametrize("shape", [(40, 256, 384), (7, 512, 300), (130, 1024, 1000)])
+@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
+def test_fp8_scaled_matches_oracle(shape, out):
+    from sdcguard_amd import modes
+    Aq, Bq, sa, sb, C = _scaled_problem(sum(shape), *shape, out=out)
+    res = modes.judge("fp8", Aq, Bq, C, sa=sa, sb=sb)
+    vals = quant.fp8_e4m3_values()
+    A = vals[Aq.view(torch.uint8).cpu().numpy()]
+    B = vals[Bq.view(torch.uint8).cpu().numpy()]
+    o = quant.fp8_judge(A, B, sa.double().cpu().numpy(), sb.double().cpu().numpy(), C.double().cpu().numpy(),
+                        quant.patterns(1), c_bf16=out == torch.bfloat16)
+    zg = res["z"].cpu().numpy()
+    assert res["wrong_blocks"] == o["wrong_blocks"] == 0
+    assert np.allclose(zg, o["z"], rtol=1e-3, atol=2e-3), np.abs(zg - o["z"]).max()
+
+
+def test_fp8_scaled_faults_located():
+    from sdcguard_amd import modes
+    Aq, Bq, sa, sb, C = _scaled_problem(9, 64, 512, 512)
+    consts = modes.QuantChecksums.make(Bq, sb)
+    for r, j, kind in [(3, 300, "add"), (0, 5, "nan"), (63, 130, "huge"), (10, 511, "inf")]:
+        c = C.clone()
+        blk = c[r, (j // 128) * 128:(j // 128 + 1) * 128]
+        if kind == "add":
+            c[r, j] += 0.5 * blk.pow(2).mean().sqrt()
+        else:
+            c[r, j] = {"nan": float("nan"), "huge": 1e30, "inf": float("inf")}[kind]
+        res = modes.resolve(modes.quant_zscores(Aq, consts, c, sa=sa))
+        assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (r, j // 128), (kind, res)
+
+
+def test_int8_known_answer_at_the_largest_values():
+    """Reference test_modes.py:47-64 on the GPU: +-127 everywhere at k = 1024, one output off by 1."""
+    from sdcguard_amd import modes
+    a = torch.full((64, 1024), 127, dtype=torch.int8, device="cuda")
+    b = torch.full((1024, 256), 127, dtype=torch.int8, device="cuda")
+    b[:, ::3] = -127
+    c = (a.double() @ b.double()).to(torch.int32)
+    assert int(c.abs().min()) == 16516096
+    assert modes.judge("int8", a, b, c)["wrong_blocks"] == 0
+    c[5, 200] += 1
+    res = modes.judge("int8", a, b, c)
+    assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (5, 1)
+
+
+def test_int8_2048x7168x4096_accumulator_bit_flips():
+    """The quantized config at full size: A, B uniform on [-127, 127], C the exact int32 product; clean is exact;
+    a flip of any one bit (0-30) of one int32 accumulator is exactly one wrong block, located; 8 trials."""
+    from sdcguard_amd import modes
+    g = torch.Generator(device="cuda").manual_seed(21)
+    A = torch.randint(-127, 128, (2048, 7168), device="cuda", generator=g, dtype=torch.int32).to(torch.int8)
+    B = torch.randint(-127, 128, (7168, 4096), device="cuda", generator=g, dtype=torch.int32).to(torch.int8)
+    C = (A.double() @ B.double()).to(torch.int32)
+    consts = modes.QuantChecksums.make(B)
+    res = modes.resolve(modes.quant_zscores(A, consts, C))
+    assert res["wrong_blocks"] == 0 and res["blocks"] == 2048 * 32
+    rng = np.random.default_rng(5)
+    for _ in range(8):
+        i, j, bit = int(rng.integers(2048)), int(rng.integers(4096)), int(rng.integers(31))
+        c = C.clone()
+        c[i, j] ^= (1 << bit)
+        res = modes.resolve(modes.quant_zscores(A, consts, c))
+        assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (i, j // 128), (i, j, bit, res)
+
+
+def test_fp8_2048x7168x4096_clean_and_faults():
+    """The fp8 config at full size with log-uniform scales: clean (fp32 and bf16 outputs) raises nothing; a fault in
+    the dequantized output of 4 typical outputs, or a flipped top exponent bit, is one wrong block, located."""
+    from sdcguard_amd import modes
+    Aq, Bq, sa, sb, C = _scaled_problem(33, 2048, 7168, 4096)
+    consts = modes.QuantChecksums.make(Bq, sb)
+    res = modes.resolve(modes.quant_zscores(Aq, consts, C, sa=sa))
+    assert res["wrong_blocks"] == 0 and res["worst_z"] < 1.0, res
+    res = modes.resolve(modes.quant_zscores(Aq, consts, C.bfloat16(), sa=sa))
+    assert res["wrong_blocks"] == 0 and res["worst_z"] < 1.0, res
+    rng = np.random.default_rng(6)
+    for t in range(6):
+        i, j = int(rng.integers(2048)), int(rng.integers(4096))
+        c = C.clone()
+        blk = c[i, (j // 128) * 128:(j // 128 + 1) * 128]
+        if t % 2:
+            c[i, j] += 4 * blk.pow(2).mean().sqrt()
+        else:
+            v = c[i:i + 1, j].view(torch.int32)
+            v ^= (1 << 30)
+        res = modes.resolve(modes.quant_zscores(Aq, consts, c, sa=sa))
+        assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (i, j // 128), (t, i, j, res)

@@ -81,9 +81,10 @@ def test_int8_sums_brute_force():
     c = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.int32)
     W = quant.patterns(1)
     actual, expected = quant.int8_sums(a, b, c, W)
+    W44 = quant.patterns(1, 44)                      # the last block's own pattern
     for i, blk, p in itertools.product(range(m), range(3), range(2)):
         lo, hi = 128 * blk, min(128 * blk + 128, n)
-        w = [int(W[p, j - lo]) for j in range(lo, hi)]
+        w = [int((W if hi - lo == 128 else W44)[p, j - lo]) for j in range(lo, hi)]
         act = sum(int(c[i, j]) * w[j - lo] for j in range(lo, hi))
         exp = sum(int(a[i, kk]) * sum(int(b[kk, j]) * w[j - lo] for j in range(lo, hi)) for kk in range(k))
         assert actual[i, blk, p] == act and expected[i, blk, p] == exp
