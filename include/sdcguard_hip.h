@@ -74,6 +74,24 @@ int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t
                      float beta, float z, float abs_floor, const float* sign_table, int64_t* result, void* workspace,
                      int64_t workspace_bytes, float* scores_out, hipStream_t stream);
 
+/* ---- check of a MoE grouped GEMM ----------------------------------------------------------------------------
+ * Replaces guard._grouped_checks (guard.py:102-143) + one checksum._zscores per group for torch._grouped_mm's
+ * forward layout: out (rows x n) = A (rows x k, tokens sorted by expert) @ B[g] (k x n) for the rows of group g,
+ * offs (groups, int64, on the device) the cumulative group ends.  No host synchronisation: the offsets are read on
+ * the device (rows past offs[groups-1] belong to no group and are not checked; empty groups are skipped).
+ *   B (groups, k, n): strides sbg, sbk, sbn; A strides (sam, sak); out strides (scm, scn), scn must be 1 or scm
+ *   not 1.  bias (n values, stride sbias) shared by every group, or NULL.
+ *   results: int64[groups][3], zeroed by the caller: per group the worst checksum's key (bits of z << 32 | flat,
+ *   flat = (global row * nb + block) * 2 + signed), the key with its noise, the unjudged count (as
+ *   sdc_matmul_check's result row).  workspace: sdc_grouped_check_workspace(groups, rows, k, n, bs) bytes;
+ *   scores_out (rows, nb, 2) or NULL. */
+int64_t sdc_grouped_check_workspace(int64_t groups, int64_t rows, int64_t k, int64_t n, int64_t bs);
+int sdc_grouped_check(int dtype, const void* A, int64_t sam, int64_t sak, const void* B, int64_t sbg, int64_t sbk,
+                      int64_t sbn, int64_t groups, const void* C, int64_t scm, int64_t scn, int64_t rows, int64_t k,
+                      int64_t n, int64_t bs, const int64_t* offs, const void* bias, int64_t sbias, float z,
+                      float abs_floor, const float* sign_table, int64_t* results, void* workspace,
+                      int64_t workspace_bytes, float* scores_out, hipStream_t stream);
+
 /* ---- check of one quantized GEMM ----------------------------------------------------------------------------
  * Replaces modes.judge (modes.py:231-291) for its int8 and fp8 branches, on the device, and extends the fp8 one to
  * per-row activation scales sa and per-column weight scales sb (C = sa_i sb_j sum_k Aq[i,k] Bq[k,j]).

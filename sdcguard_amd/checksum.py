@@ -268,3 +268,126 @@ def check_linear_rows(x, weight, bias, y, **kw) -> Optional[CheckResult]:
     """Row-block check of y = torch.nn.functional.linear(x, weight, bias).  The result's `row` is the output column
     and `col_block` the block of token rows."""
     return check_matmul(*linear_rows_operands(x, weight, bias, y), **kw)
+
+
+def grouped_checks(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, offs: Optional[torch.Tensor],
+                   bias: Optional[torch.Tensor] = None) -> list:
+    """guard._grouped_checks (guard.py:102-143): the (A, B, C, bias, alpha, beta) of every group of a
+    torch._grouped_mm, split on the cumulative group ends `offs` (read on the host).  2-D x 3-D: tokens grouped by
+    expert (rows of a and out); 3-D x 2-D: grouped along n; 2-D x 2-D: grouped along k (weight gradients: an empty
+    group still has an all-zero output to check); 3-D x 3-D: one batched check.  Groups whose output a shared bias
+    does not broadcast to are skipped, as the reference skips them."""
+    def shared(shape) -> Optional[bool]:
+        if bias is None:
+            return None
+        try:
+            return torch.broadcast_shapes(tuple(bias.shape), tuple(shape)) == tuple(shape)
+        except RuntimeError:
+            return False
+
+    if a.dim() == 3 and b.dim() == 3:
+        return [(a, b, out, bias, 1.0, 1.0)] if bias is None or shared(out.shape[1:]) else []
+    if offs is None:
+        return []
+    ends = [int(e) for e in offs.tolist()]
+    checks, start = [], 0
+    for i, end in enumerate(ends):
+        if end > start or (a.dim() == 2 and b.dim() == 2):
+            if a.dim() == 2 and b.dim() == 3:
+                c = (a[start:end], b[i], out[start:end])
+            elif a.dim() == 3 and b.dim() == 2:
+                c = (a[i], b[:, start:end], out[:, start:end])
+            elif a.dim() == 2 and b.dim() == 2:
+                c = (a[:, start:end], b[start:end, :], out[i])
+            else:
+                c = None
+            if c is not None and (bias is None or shared(c[2].shape)):
+                checks.append((*c, bias, 1.0, 1.0))
+        start = end
+    return checks
+
+
+@dataclass
+class GroupedStat:
+    """A queued grouped check: one result row per group on the device (worst key over the group's rows, key with its
+    noise, unjudged count) and what decoding it needs."""
+    results: torch.Tensor        # (groups, 3) int64
+    offs: torch.Tensor           # the group ends as given (device)
+    rows: int
+    nb: int
+    z: float
+
+
+def grouped_zscores(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, offs: torch.Tensor,
+                    bias: Optional[torch.Tensor] = None, *, block: int = 128, abs_floor: float = ABS_FLOOR,
+                    z: float = 6.0, scores_out: Optional[torch.Tensor] = None) -> GroupedStat:
+    """Queue the check of a MoE grouped product out = a @ b[g] for the rows of group g (a: (T, k) tokens sorted by
+    expert, b: (G, k, n), out: (T, n), offs: (G,) cumulative row ends, int32 or int64, on the device) without
+    reading offs on the host: every group's rows are checked against that group's B, as
+    check_matmul(a[start:end], b[g], out[start:end]) checks them (guard._grouped_checks + checksum._zscores)."""
+    from . import _lib
+    if a.dim() != 2 or b.dim() != 3 or out.dim() != 2:
+        raise ValueError("grouped_zscores covers the (T, k) x (G, k, n) -> (T, n) layout")
+    _lib.require_gpu(a, b, out, offs, bias)
+    dt = out.dtype
+    if dt not in UNIT_ROUNDOFF:
+        raise ValueError(f"unsupported output dtype {dt}")
+    T, k = a.shape
+    G, kb, n = b.shape
+    if kb != k or out.shape != (T, n) or offs.numel() != G:
+        raise ValueError(f"shape mismatch: a{tuple(a.shape)} b{tuple(b.shape)} out{tuple(out.shape)} offs {offs.numel()}")
+    a = a if a.dtype == dt else a.to(dt)
+    b = b if b.dtype == dt else b.to(dt)
+    if bias is not None:
+        bias = bias.reshape(-1)
+        if bias.numel() != n:
+            raise ValueError("grouped_zscores: a shared bias of n values")
+        bias = bias if bias.dtype == dt else bias.to(dt)
+    offs64 = offs.to(torch.int64).contiguous()
+    L = _lib.lib()
+    nb = -(-n // block)
+    results = torch.zeros(G, 3, dtype=torch.int64, device=out.device)
+    ws = torch.empty(int(L.sdc_grouped_check_workspace(G, T, k, n, block)), dtype=torch.uint8, device=out.device)
+    rc = L.sdc_grouped_check(_lib.dtype_code(dt), a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(), b.stride(0),
+                             b.stride(1), b.stride(2), G, out.data_ptr(), out.stride(0), out.stride(1), T, k, n, block,
+                             offs64.data_ptr(), None if bias is None else bias.data_ptr(),
+                             0 if bias is None else bias.stride(0), float(z), float(abs_floor),
+                             sign_table(out.device).data_ptr(), results.data_ptr(), ws.data_ptr(), ws.numel(),
+                             None if scores_out is None else scores_out.data_ptr(), _lib.stream_of(out))
+    _lib.check(rc, "sdc_grouped_check")
+    return GroupedStat(results, offs, T, nb, z)
+
+
+def resolve_grouped(st: GroupedStat) -> list:
+    """One CheckResult per non-empty group, in group order (the checks guard._grouped_checks makes), rows relative to
+    the group's first row as check_matmul on the group's slice reports them (two small device-to-host copies)."""
+    ends = [int(e) for e in st.offs.tolist()]
+    host = st.results.cpu().tolist()
+    out, start = [], 0
+    for g, end in enumerate(ends):
+        end = min(end, st.rows)
+        if end > start:
+            key, keyd, unjudged = host[g]
+            mz = _f32_of_bits(key >> 32)
+            if unjudged and mz <= st.z:
+                mz = UNJUDGED
+            flat = key & 0xFFFFFFFF
+            r_i, c_i = divmod(flat // 2, st.nb)
+            finite = math.isfinite(mz)
+            out.append(CheckResult(ok=finite and mz <= st.z, max_z=mz, nonfinite=not finite, batch=None,
+                                   row=(r_i - start) if key else 0, col_block=c_i, noise=_f32_of_bits(keyd)))
+        start = max(start, end)
+    return out
+
+
+def check_grouped_mm(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, offs: Optional[torch.Tensor] = None,
+                     bias: Optional[torch.Tensor] = None, **kw) -> list:
+    """Check a torch._grouped_mm result: one CheckResult per check guard._grouped_checks would make.  The MoE
+    forward layout (2-D x 3-D) runs as one device-side grouped check; the others as one check per group."""
+    if a.dim() == 2 and b.dim() == 3 and offs is not None and out.dtype in UNIT_ROUNDOFF and \
+            (bias is None or bias.numel() == out.shape[-1]):
+        return resolve_grouped(grouped_zscores(a, b, out, offs, bias, **kw))
+    res = []
+    for A, B, C, bi, al, be in grouped_checks(a, b, out, offs, bias):
+        res.append(check_matmul(A, B, C, bi, alpha=al, beta=be, **kw))
+    return res

@@ -185,20 +185,40 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2][T::ROWS * LP];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int wm = w / WGN, wn = w % WGN;
-  const int64_t nrt = sdc_cdiv(g.m, T::TM), nct = sdc_cdiv(g.N, T::TN);
+  const int64_t nrt = sdc_cdiv(g.m, T::TM) + (g.goffs ? g.ngroups : 0), nct = sdc_cdiv(g.N, T::TN);
   // XCD-aware order: block b runs on XCD b % 8; give XCD x the x-th eighth of the tiles (column tile fastest)
   const int64_t G = (int64_t)gridDim.x, b = blockIdx.x;
   const int64_t wid = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
   const int64_t ct = wid % nct, rt = (wid / nct) % nrt, rest = wid / (nct * nrt);
-  const int64_t split = rest % g.splits, batch = rest / g.splits;
-  const int64_t r0 = rt * T::TM, c0 = ct * T::TN;
+  const int64_t split = rest % g.splits;
+  int64_t batch = rest / g.splits, r0 = rt * T::TM, m = g.m;
+  if (g.goffs) {
+    // grouped rows: find the group whose row tiles contain tile rt (every thread walks the same offsets)
+    int64_t start = 0, acc = 0, grp = -1;
+    for (int64_t q = 0; q < g.ngroups; ++q) {
+      const int64_t end = g.goffs[q] < g.m ? g.goffs[q] : g.m;   // offsets past the rows are clamped
+      const int64_t nt = end > start ? sdc_cdiv(end - start, T::TM) : 0;
+      if (rt < acc + nt) {
+        grp = q;
+        r0 = start + (rt - acc) * T::TM;
+        m = end;                        // rows of this tile stop at the group's end
+        break;
+      }
+      acc += nt;
+      start = end > start ? end : start;
+    }
+    if (grp < 0) return;                // past the last tile: the whole workgroup leaves before any barrier
+    batch = grp;
+  }
+  const int64_t c0 = ct * T::TN;
   const int64_t kbeg = split * g.kchunk;
   const int64_t kend = kbeg + g.kchunk < g.k ? kbeg + g.kchunk : g.k;
   const int nst = kbeg < kend ? (int)sdc_cdiv(kend - kbeg, KS) : 0;
   const bool norms = ct == 0;
-  const int64_t m = g.m, N = g.N;
-  const uint8_t* Ab = (const uint8_t*)g.A + batch * g.sab * ESA;
+  const int64_t N = g.N, me = g.m;      // me: rows of E and XN (the global row count)
+  const uint8_t* Ab = (const uint8_t*)g.A + (g.goffs ? 0 : batch * g.sab * ESA);
   const uint16_t* Pb = (const uint16_t*)g.B + batch * g.sbb;
+  const int64_t eb = g.goffs ? 0 : batch;           // E / XN plane set
 
   // this thread's chunks: A chunk c is (row c / 4, depth 8 (c % 4)); B chunk c is (LDS row c / 4: part, column);
   // indexes past the end repeat the last chunk (the same value is stored twice)
@@ -345,7 +365,7 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
   // two digit planes of a split are adjacent planes, their values the int32 bits.
 #pragma unroll
   for (int pa = 0; pa < NACC; ++pa) {
-    float* Es = g.E + ((batch * g.splits + split) * NACC + pa) * m * N;
+    float* Es = g.E + ((eb * g.splits + split) * NACC + pa) * me * N;
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
       const int64_t col = c0 + wn * 64 + 32 * n + (lane & 31);
@@ -356,20 +376,20 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
           for (int r4 = 0; r4 < 4; ++r4) {
             const int64_t row = r0 + wm * 64 + i * 32 + 8 * r4 + 4 * (lane >> 5);
             const f32x16& av = acc[pa][i][n];
-            if (g.et && row + 4 <= m && (m % 4) == 0) {
+            if (g.et && row + 4 <= m && (me % 4) == 0 && (row % 4) == 0) {
               f32x4 v = {av[4 * r4], av[4 * r4 + 1], av[4 * r4 + 2], av[4 * r4 + 3]};
-              *reinterpret_cast<f32x4*>(&Es[col * m + row]) = v;
+              *reinterpret_cast<f32x4*>(&Es[col * me + row]) = v;
             } else {
 #pragma unroll
               for (int q = 0; q < 4; ++q)
-                if (row + q < m) Es[g.et ? col * m + row + q : (row + q) * N + col] = av[4 * r4 + q];
+                if (row + q < m) Es[g.et ? col * me + row + q : (row + q) * N + col] = av[4 * r4 + q];
             }
           }
       }
     }
   }
   if (norms && MODE != SDC_I8) {
-    float* xs = g.XN + (batch * g.splits + split) * 2 * m;
+    float* xs = g.XN + (eb * g.splits + split) * 2 * me;
 #pragma unroll
     for (int j = 0; j < T::NA; ++j) {
       float q = sq[j], a1 = ab[j];
@@ -381,7 +401,7 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
       const int64_t row = r0 + c / 4;
       if ((c & 3) == 0 && c < T::ACH && row < m) {
         xs[row] = q;
-        xs[m + row] = a1;
+        xs[me + row] = a1;
       }
     }
   }
@@ -455,7 +475,9 @@ int sdc_gemm_launch(int dtype, GemmArgs g, int64_t batches, hipStream_t stream) 
                    ((uintptr_t)g.A % 16 == 0) && (g.sbc % 8 == 0) && (g.sbb % 8 == 0) && ((uintptr_t)g.B % 16 == 0);
   if (dtype == SDC_FP8 && !vec) return SDC_EUNSUPPORTED;          // fp8 A: k-contiguous, aligned rows only
   const int wgn = g.N > 64 ? 2 : 1;
-  const int64_t blocks = sdc_cdiv(g.m, 64 * (8 / wgn)) * sdc_cdiv(g.N, 64 * wgn) * g.splits * batches;
+  const int64_t rtiles = sdc_cdiv(g.m, 64 * (8 / wgn)) + (g.goffs ? g.ngroups : 0);
+  if (g.goffs && batches != 1) return SDC_EINVAL;
+  const int64_t blocks = rtiles * sdc_cdiv(g.N, 64 * wgn) * g.splits * batches;
   if (blocks > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
   SdcProf prof(g.prof_name ? g.prof_name : "expected_gemm", stream);
   switch (dtype) {

@@ -12,6 +12,12 @@ struct GemmArgs {
   float* E;                     // [batch][split][m][N], or [batch][split][N][m] with et
   int et;                       // store E transposed (column-major per plane)
   const char* prof_name;        // name for per-kernel timing (null: "expected_gemm")
+  // Grouped rows (a MoE grouped GEMM, tokens sorted by expert): when goffs is set, row r belongs to group g with
+  // goffs[g-1] <= r < goffs[g] (cumulative ends, on the device) and is multiplied by group g's parts (batch
+  // stride sbb); row tiles never cross a group, the grid covers cdiv(m, TM) + ngroups tiles and workgroups past the
+  // last tile exit.  E and XN are indexed by the global row (batch 0).
+  const int64_t* goffs;
+  int64_t ngroups;
   float* XN;                    // [batch][split][2][m]: sum of squares and sum of |a| of each row's depth slice
 };
 

@@ -295,6 +295,8 @@ struct TrainArgs {
   float alpha, beta, u, h, abs_floor, l1c, zt, lim_a, capk;
   int64_t* result;                 // [key, key of the noise, unjudged]
   float* zdump;
+  const int64_t* goffs;            // grouped rows: cumulative group ends (device), or null
+  int64_t ngroups;
 };
 
 struct TrainBest {
@@ -331,13 +333,13 @@ __device__ __forceinline__ float judge_one(float expected, float actual, float n
 
 template <int DT>
 __device__ __forceinline__ void train_pair(const TrainArgs& a, int64_t p, float pl, float sg, float sq, float l1,
-                                           TrainBest& best) {
+                                           TrainBest& best, int64_t grp = -1) {
   if (p >= a.cv.npairs) return;
   int64_t bc, r, jb;
   pair_index(a.cv, p, bc, r, jb);
   const bool last = (jb == a.cv.nb - 1) && (a.cv.rem > 0);
   const float wf = (float)(last ? a.cv.rem : a.cv.bs);
-  const int64_t eb = a.e_batched ? bc : 0, bbi = a.b_batched ? bc : 0;
+  const int64_t eb = (a.e_batched && grp < 0) ? bc : 0, bbi = grp >= 0 ? grp : (a.b_batched ? bc : 0);
   // E planes row-major ([m][ncols]: plain and signed adjacent) or transposed ([ncols][m]: adjacent rows)
   const float* ep = a.et ? a.E + ((eb * a.splits) * a.ncols + 2 * jb) * a.cv.m + r
                          : a.E + ((eb * a.splits) * a.cv.m + r) * a.ncols + 2 * jb;
@@ -557,19 +559,75 @@ __global__ __launch_bounds__(256) void train_score_t_kernel(TrainArgs a) {
   }
 }
 
+// The scoring pass of a grouped check (rows grouped by cumulative offsets, each group with its own B): every
+// (row, block) pair is scored as train_score_kernel scores it, with the B-side statistics of its row's group, and
+// the worst key and unjudged count go to that group's result row.  Rows past the last offset belong to no group and
+// are not scored.  A wave's 64 pairs usually share one group: then one set of atomics per wave, else one per lane.
+__device__ __forceinline__ int64_t group_of(const int64_t* offs, int64_t ng, int64_t r) {
+  int64_t lo = 0, hi = ng;                        // first q with offs[q] > r (offsets are non-decreasing)
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (offs[mid] > r) hi = mid;
+    else lo = mid + 1;
+  }
+  return lo < ng ? lo : -1;
+}
+
+__device__ __forceinline__ void flush_group(int64_t* res, const TrainBest& b) {
+  if (b.key > __atomic_load_n(res, __ATOMIC_RELAXED)) atomicMax((unsigned long long*)res, (unsigned long long)b.key);
+  if (b.keyd > __atomic_load_n(res + 1, __ATOMIC_RELAXED))
+    atomicMax((unsigned long long*)(res + 1), (unsigned long long)b.keyd);
+  if (b.unk > 0) atomicAdd((unsigned long long*)(res + 2), (unsigned long long)b.unk);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void grouped_score_kernel(TrainArgs a) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, q = lane & 3;
+  uint32_t sg2[16];
+  lane_signs<DT>(a.cv, q, sg2);
+  const int64_t tiles = (a.cv.npairs + 63) / 64;
+  for (int64_t tile = (int64_t)blockIdx.x * 4 + w; tile < tiles; tile += (int64_t)gridDim.x * 4) {
+    const int64_t base = tile * 64;
+    float pl, sg, sq, ab;
+    pair_sums<DT>(a.cv, base, lane, sg2, pl, sg, sq, ab);
+    const int64_t p = base + q * 16 + (lane >> 2);
+    const int64_t pc = p < a.cv.npairs ? p : a.cv.npairs - 1;
+    const int64_t grp = group_of(a.goffs, a.ngroups, pc / a.cv.nb);
+    TrainBest tb;
+    if (grp >= 0) train_pair<DT>(a, p, pl, sg, sq, ab, tb, grp);
+    const int64_t last = base + 63 < a.cv.npairs ? base + 63 : a.cv.npairs - 1;
+    const int64_t g0 = group_of(a.goffs, a.ngroups, base / a.cv.nb);
+    const int64_t g1 = group_of(a.goffs, a.ngroups, last / a.cv.nb);
+    if (g0 == g1) {
+      if (g0 >= 0) {
+        const int64_t key = wave_max_i64(tb.key), keyd = wave_max_i64(tb.keyd);
+        const int unk = wave_sum_i32(tb.unk);
+        if (lane == 0) {
+          TrainBest w1;
+          w1.key = key; w1.keyd = keyd; w1.unk = unk;
+          flush_group(a.result + 3 * g0, w1);
+        }
+      }
+    } else if (grp >= 0) {
+      flush_group(a.result + 3 * grp, tb);
+    }
+  }
+}
+
 struct Layout {
   int64_t nb, rem, ncols, nkc, splits, nbt;
   int64_t kp;                      // depth pitch of the parts (k rounded up to 8: 16-byte aligned columns)
   int64_t off_b2t, off_part, off_col, off_bmax, off_bias, off_parts, off_e, off_xn, total;
 };
 
-Layout layout(int64_t batch_a, int64_t batch_b, int64_t m, int64_t k, int64_t n, int64_t bs) {
+// grouped: B has batch_b groups but A, C, E and XN are one tall matrix (rows grouped by offsets)
+Layout layout(int64_t batch_a, int64_t batch_b, int64_t m, int64_t k, int64_t n, int64_t bs, bool grouped = false) {
   Layout L{};
   L.nb = sdc_cdiv(n, bs);
   L.rem = n % bs;
   L.ncols = 2 * L.nb;
   L.nkc = sdc_cdiv(k, BROWS);
-  L.nbt = batch_a > batch_b ? batch_a : batch_b;
+  L.nbt = grouped ? 1 : (batch_a > batch_b ? batch_a : batch_b);
   L.splits = sdc_expected_splits(m, k, L.ncols);
   auto al = [](int64_t x) { return (x + 63) / 64 * 64; };   // floats, 256-byte aligned sections
   int64_t o = 0;
@@ -594,23 +652,18 @@ extern "C" int64_t sdc_matmul_check_workspace(int64_t batch_a, int64_t batch_b, 
   return layout(batch_a, batch_b, m, k, n, bs).total * (int64_t)sizeof(float) + 256;
 }
 
-extern "C" int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, int64_t batch_a,
-                                const void* B, int64_t sbb, int64_t sbk, int64_t sbn, int64_t batch_b, const void* C,
-                                int64_t scb, int64_t scm, int64_t scn, int64_t batch_c, int64_t m, int64_t k,
-                                int64_t n, int64_t bs, const void* bias, int bias_kind, int64_t sbias_b,
-                                int64_t sbias_m, int64_t sbias_n, float alpha, float beta, float z, float abs_floor,
-                                const float* sign_table, int64_t* result, void* workspace, int64_t workspace_bytes,
-                                float* scores_out, hipStream_t stream) {
-  SDC_CLEAR_ERRORS();
-  if (m < 1 || n < 1 || k < 1 || batch_a < 1 || batch_b < 1 || batch_c < 1) return SDC_EINVAL;
-  if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EINVAL;
-  if (bs < 1 || bs > 128) return SDC_EUNSUPPORTED;
-  if (!A || !B || !C || !sign_table || !result) return SDC_EINVAL;
-  if (bias_kind < 0 || bias_kind > 2 || (bias_kind && !bias)) return SDC_EINVAL;
-  const int64_t nbt = batch_a > batch_b ? batch_a : batch_b;
-  if ((batch_a != 1 && batch_a != nbt) || (batch_b != 1 && batch_b != nbt)) return SDC_EINVAL;
-  if (batch_c != nbt && !(nbt == 1)) return SDC_EINVAL;
-  const Layout L = layout(batch_a, batch_b, m, k, n, bs);
+namespace {
+
+// The check of sdc_matmul_check, or (goffs set) of sdc_grouped_check: batch_b groups of B over one tall A / C.
+int run_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, int64_t batch_a, const void* B,
+              int64_t sbb, int64_t sbk, int64_t sbn, int64_t batch_b, const void* C, int64_t scb, int64_t scm,
+              int64_t scn, int64_t batch_c, int64_t m, int64_t k, int64_t n, int64_t bs, const void* bias,
+              int bias_kind, int64_t sbias_b, int64_t sbias_m, int64_t sbias_n, float alpha, float beta, float z,
+              float abs_floor, const float* sign_table, int64_t* result, void* workspace, int64_t workspace_bytes,
+              float* scores_out, const int64_t* goffs, hipStream_t stream) {
+  const bool grouped = goffs != nullptr;
+  const int64_t nbt = grouped ? 1 : (batch_a > batch_b ? batch_a : batch_b);
+  const Layout L = layout(batch_a, batch_b, m, k, n, bs, grouped);
   if (batch_c * m * L.nb * 2 > 0xFFFFFFFFll) return SDC_EUNSUPPORTED;     // flat index in 32 bits
   if (!workspace || workspace_bytes < L.total * (int64_t)sizeof(float) + 256) return SDC_EWORKSPACE;
   float* ws = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
@@ -660,9 +713,10 @@ extern "C" int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t s
   g.B = parts; g.sbb = batch_b > 1 ? 3 * L.ncols * L.kp : 0; g.sbc = L.kp;
   g.m = m; g.k = k; g.N = L.ncols; g.splits = L.splits;
   g.E = ws + L.off_e; g.XN = ws + L.off_xn;
-  const bool c_t = scm == 1 && scn != 1 && L.nb < 65536 && batch_c < 65536;   // C read down its columns
+  const bool c_t = !grouped && scm == 1 && scn != 1 && L.nb < 65536 && batch_c < 65536;   // C read down columns
   g.et = c_t;
   g.prof_name = "train_gemm";
+  g.goffs = goffs; g.ngroups = grouped ? batch_b : 0;
   rc = sdc_gemm_launch(dtype, g, nbt, stream);
   if (rc != SDC_OK) return rc;
 
@@ -684,9 +738,15 @@ extern "C" int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t s
   ta.lim_a = dtype == SDC_BF16 ? 1e18f : 65504.f;
   ta.capk = (float)(1.02 + (double)k * 2.384185791015625e-07);
   ta.result = result; ta.zdump = scores_out;
+  ta.goffs = goffs; ta.ngroups = grouped ? batch_b : 0;
   SdcProf prof("train_score", stream);
   ta.et = c_t;
-  if (c_t) {
+  if (grouped) {
+    const int64_t tiles = sdc_cdiv(ta.cv.npairs, 64);
+    const unsigned grid = (unsigned)(sdc_cdiv(tiles, 4) < 1024 ? sdc_cdiv(tiles, 4) : 1024);
+    if (dtype == SDC_BF16) hipLaunchKernelGGL(grouped_score_kernel<SDC_BF16>, dim3(grid), dim3(256), 0, stream, ta);
+    else hipLaunchKernelGGL(grouped_score_kernel<SDC_FP16>, dim3(grid), dim3(256), 0, stream, ta);
+  } else if (c_t) {
     // C with adjacent rows (y^T): read 512 rows at a time down each column
     ta.cv.vec = (scn % 8 == 0) && (scb % 8 == 0) && ((uintptr_t)C % 16 == 0);
     dim3 grid((unsigned)sdc_cdiv(m, 512), (unsigned)L.nb, (unsigned)batch_c);
@@ -700,4 +760,48 @@ extern "C" int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t s
   }
   SDC_LAUNCH_CHECK();
   return SDC_OK;
+}
+
+}  // namespace
+
+extern "C" int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, int64_t batch_a,
+                                const void* B, int64_t sbb, int64_t sbk, int64_t sbn, int64_t batch_b, const void* C,
+                                int64_t scb, int64_t scm, int64_t scn, int64_t batch_c, int64_t m, int64_t k,
+                                int64_t n, int64_t bs, const void* bias, int bias_kind, int64_t sbias_b,
+                                int64_t sbias_m, int64_t sbias_n, float alpha, float beta, float z, float abs_floor,
+                                const float* sign_table, int64_t* result, void* workspace, int64_t workspace_bytes,
+                                float* scores_out, hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
+  if (m < 1 || n < 1 || k < 1 || batch_a < 1 || batch_b < 1 || batch_c < 1) return SDC_EINVAL;
+  if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EINVAL;
+  if (bs < 1 || bs > 128) return SDC_EUNSUPPORTED;
+  if (!A || !B || !C || !sign_table || !result) return SDC_EINVAL;
+  if (bias_kind < 0 || bias_kind > 2 || (bias_kind && !bias)) return SDC_EINVAL;
+  const int64_t nbt = batch_a > batch_b ? batch_a : batch_b;
+  if ((batch_a != 1 && batch_a != nbt) || (batch_b != 1 && batch_b != nbt)) return SDC_EINVAL;
+  if (batch_c != nbt && !(nbt == 1)) return SDC_EINVAL;
+  return run_check(dtype, A, sab, sam, sak, batch_a, B, sbb, sbk, sbn, batch_b, C, scb, scm, scn, batch_c, m, k, n, bs,
+                   bias, bias_kind, sbias_b, sbias_m, sbias_n, alpha, beta, z, abs_floor, sign_table, result, workspace,
+                   workspace_bytes, scores_out, nullptr, stream);
+}
+
+extern "C" int64_t sdc_grouped_check_workspace(int64_t groups, int64_t rows, int64_t k, int64_t n, int64_t bs) {
+  if (groups <= 0 || rows <= 0 || n <= 0 || k <= 0 || bs <= 0) return 0;
+  return layout(1, groups, rows, k, n, bs, true).total * (int64_t)sizeof(float) + 256;
+}
+
+extern "C" int sdc_grouped_check(int dtype, const void* A, int64_t sam, int64_t sak, const void* B, int64_t sbg,
+                                 int64_t sbk, int64_t sbn, int64_t groups, const void* C, int64_t scm, int64_t scn,
+                                 int64_t rows, int64_t k, int64_t n, int64_t bs, const int64_t* offs, const void* bias,
+                                 int64_t sbias, float z, float abs_floor, const float* sign_table, int64_t* results,
+                                 void* workspace, int64_t workspace_bytes, float* scores_out, hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
+  if (rows < 1 || n < 1 || k < 1 || groups < 1) return SDC_EINVAL;
+  if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EINVAL;
+  if (bs < 1 || bs > 128) return SDC_EUNSUPPORTED;
+  if (!A || !B || !C || !offs || !sign_table || !results) return SDC_EINVAL;
+  if (scn != 1 && scm == 1) return SDC_EUNSUPPORTED;          // the grouped pass reads C along its rows
+  return run_check(dtype, A, 0, sam, sak, 1, B, sbg, sbk, sbn, groups, C, 0, scm, scn, 1, rows, k, n, bs, bias,
+                   bias ? 1 : 0, 0, 0, sbias, 1.f, 1.f, z, abs_floor, sign_table, results, workspace,
+                   workspace_bytes, scores_out, offs, stream);
 }

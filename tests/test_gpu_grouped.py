@@ -1,0 +1,133 @@
+"""The MoE grouped-GEMM check (sdc_grouped_check through checksum.grouped_zscores / check_grouped_mm) against the
+oracle per group (each group is checked as check_matmul(a[start:end], b[g], out[start:end]), guard.py:102-143),
+the other torch._grouped_mm layouts through per-group checks, and the 4096-token top-8 / 64-expert workload with
+Zipf(1.1) expert loads and one corrupted expert tile."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import abft
+from tests.test_oracle_golden import gemm_slack, z_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _grouped(sizes, k, n, dtype=torch.bfloat16, seed=0, w_scale=None):
+    g = torch.Generator().manual_seed(seed)
+    T = sum(sizes)
+    a = torch.randn(T, k, generator=g).to(dtype).cuda()
+    b = (torch.randn(len(sizes), k, n, generator=g) * (w_scale or 1 / math.sqrt(k))).to(dtype).cuda()
+    offs = torch.tensor(np.cumsum(sizes), dtype=torch.int32).cuda()
+    out = torch.empty(T, n, dtype=dtype, device="cuda")
+    s = 0
+    for e, c in enumerate(sizes):
+        if c:
+            out[s:s + c] = (a[s:s + c].float() @ b[e].float()).to(dtype)
+        s += c
+    return a, b, out, offs
+
+
+@pytest.mark.parametrize("sizes,k,n", [([0, 37, 130, 1, 200], 256, 300), ([513, 0, 0, 700], 512, 128),
+                                       ([5] * 20, 96, 40)])
+def test_grouped_scores_match_oracle_per_group(sizes, k, n):
+    from sdcguard_amd.checksum import grouped_zscores, resolve_grouped
+    a, b, out, offs = _grouped(sizes, k, n, seed=len(sizes))
+    nb = -(-n // min(128, n))
+    zs = torch.full((sum(sizes), nb, 2), -7.0, device="cuda")
+    res = resolve_grouped(grouped_zscores(a, b, out, offs, scores_out=zs))
+    zs = zs.cpu().numpy()
+    s, j = 0, 0
+    for e, c in enumerate(sizes):
+        if c:
+            o = abft.zscores(a[s:s + c].float().cpu().numpy(), b[e].float().cpu().numpy(),
+                             out[s:s + c].float().cpu().numpy(), seed=1)
+            got = zs[s:s + c].reshape(-1)
+            ok = z_close(got, o.z.reshape(-1), gemm_slack(o.csb, o.den).reshape(-1))
+            assert ok.all(), (e, np.nonzero(~ok)[0][:5], got[~ok][:5], o.z.reshape(-1)[~ok][:5])
+            assert res[j].ok == o.ok
+            j += 1
+        s += c
+    assert j == len(res)
+
+
+def test_grouped_fault_located_in_its_group():
+    from sdcguard_amd.checksum import check_grouped_mm
+    sizes = [64, 0, 300, 17, 129]
+    a, b, out, offs = _grouped(sizes, 256, 384, seed=3)
+    assert all(r.ok for r in check_grouped_mm(a, b, out, offs))
+    bad = out.clone()
+    bad[64 + 200, 130:140] += 4.0                # group 2 (the second non-empty group), local row 200, block 1
+    res = check_grouped_mm(a, b, bad, offs)
+    flags = [not r.ok for r in res]
+    assert flags == [False, True, False, False]
+    assert (res[1].row, res[1].col_block) == (200, 1)
+    past = torch.cat([out, out[:3]])             # rows past offs[-1] belong to no group
+    past[-2] = float("nan")
+    a2 = torch.cat([a, a[:3]])
+    assert all(r.ok for r in check_grouped_mm(a2, b, past, offs))
+
+
+def test_other_grouped_layouts_match_per_group_checks():
+    """3-D x 2-D (grouped along n), 2-D x 2-D (grouped along k, empty group = an all-zero output) and 3-D x 3-D run
+    one check per group, as guard._grouped_checks splits them."""
+    from sdcguard_amd.checksum import check_grouped_mm, check_matmul
+    g = torch.Generator().manual_seed(4)
+    A3 = torch.randn(3, 32, 64, generator=g).bfloat16().cuda()
+    B2 = (torch.randn(64, 200, generator=g) / 8).bfloat16().cuda()
+    offs_n = torch.tensor([50, 50, 200], dtype=torch.int32).cuda()
+    out = torch.zeros(32, 200, dtype=torch.bfloat16, device="cuda")
+    out[:, :50] = (A3[0].float() @ B2[:, :50].float()).bfloat16()
+    out[:, 50:200] = (A3[2].float() @ B2[:, 50:].float()).bfloat16()
+    res = check_grouped_mm(A3, B2, out, offs_n)
+    assert len(res) == 2 and all(r.ok for r in res)
+    A2 = torch.randn(16, 90, generator=g).bfloat16().cuda()
+    Bk = torch.randn(90, 24, generator=g).bfloat16().cuda()
+    offs_k = torch.tensor([40, 40, 90], dtype=torch.int32).cuda()
+    outk = torch.stack([(A2[:, :40].float() @ Bk[:40].float()).bfloat16(), torch.zeros(16, 24).bfloat16().cuda(),
+                        (A2[:, 40:].float() @ Bk[40:].float()).bfloat16()])
+    res = check_grouped_mm(A2, Bk, outk, offs_k)
+    assert len(res) == 3 and all(r.ok for r in res)
+    outk[1, 3, 5] = 1.0                          # an empty group's output must be all zeros
+    assert [r.ok for r in check_grouped_mm(A2, Bk, outk, offs_k)] == [True, False, True]
+    Bb = torch.randn(3, 64, 40, generator=g).bfloat16().cuda()
+    outb = torch.bmm(A3, Bb)
+    assert check_grouped_mm(A3, Bb, outb, None)[0].ok == check_matmul(A3, Bb, outb).ok is True
+
+
+def _zipf_counts(tokens, experts, topk, s, gen):
+    p = torch.tensor([1.0 / (r + 1) ** s for r in range(experts)], dtype=torch.float64)
+    picks = torch.multinomial(p.expand(tokens, experts), topk, replacement=False, generator=gen)
+    return torch.bincount(picks.reshape(-1), minlength=experts).tolist()
+
+
+def test_moe_4096_tokens_top8_64_experts():
+    """4096 tokens x top-8 over 64 experts with Zipf(1.1) loads, K = 2048, N = 1408, bf16: clean raises nothing;
+    one corrupted 128 x 128 tile of one expert's output flags that expert (and only it), at the tile's block;
+    6 trials."""
+    from sdcguard_amd.checksum import check_grouped_mm, grouped_zscores, resolve_grouped
+    gen = torch.Generator().manual_seed(7)
+    sizes = _zipf_counts(4096, 64, 8, 1.1, gen)
+    assert sum(sizes) == 32768
+    a, b, out, offs = _grouped(sizes, 2048, 1408, seed=8, w_scale=0.02)
+    res = check_grouped_mm(a, b, out, offs)
+    assert len(res) == sum(1 for c in sizes if c) and all(r.ok for r in res), max(r.max_z for r in res)
+    starts = np.concatenate([[0], np.cumsum(sizes)[:-1]])
+    nonempty = [e for e, c in enumerate(sizes) if c]
+    rng = np.random.default_rng(9)
+    for _ in range(6):
+        e = int(rng.choice([x for x in nonempty if sizes[x] >= 1]))
+        r0 = int(starts[e]) + int(rng.integers(0, max(1, sizes[e] - 127))) if sizes[e] > 128 else int(starts[e])
+        rows = min(128, sizes[e])
+        blk = int(rng.integers(0, 11))
+        bad = out.clone()
+        bad[r0:r0 + rows, blk * 128:(blk + 1) * 128] = torch.randn(rows, 128, device="cuda").bfloat16()
+        st = grouped_zscores(a, b, bad, offs)
+        res = resolve_grouped(st)
+        flagged = [nonempty[i] for i, r in enumerate(res) if not r.ok]
+        assert flagged == [e], (e, flagged)
+        r = res[nonempty.index(e)]
+        assert r.col_block == blk and 0 <= r.row < sizes[e]
