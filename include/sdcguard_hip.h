@@ -125,6 +125,14 @@ int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
 int sdc_fingerprint3(const void* bits, int64_t n, int word_bytes, int64_t start, int64_t* out, hipStream_t stream);
 int sdc_fingerprint2(const void* bits, int64_t n, int kind, int64_t* out, hipStream_t stream);
 
+/* ---- paged-KV block fingerprints (no counterpart function in the reference; each block's value is
+ * recompute.fingerprint of the block's bytes as a tensor of its own, recompute.py:72-116, words numbered from 0) --
+ * out[i][0..2] (int64, zeroed by the caller) += the fingerprint of block ids[i] of a cache of nblocks blocks of
+ * `words` 16-bit words each, block b at cache + b * block_bytes; ids == NULL: entry i is block i (n = nblocks).
+ * An entry whose id is negative or >= nblocks is left unchanged (a block-table walk passes the table's rows). */
+int sdc_kv_fingerprint(const void* cache, int64_t nblocks, int64_t block_bytes, int64_t words, const int64_t* ids,
+                       int64_t n, int64_t* out, hipStream_t stream);
+
 /* ---- per-kernel timing (no counterpart in the reference; for benchmarks) ------------------------------------
  * With profiling on, every kernel launch is bracketed by two HIP events on its stream; sdc_profile_read waits for
  * them and sums the durations of one kernel: "expected_gemm" (serving GEMM), "serve_fused", "serve_sums",

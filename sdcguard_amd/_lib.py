@@ -42,6 +42,7 @@ SIGNATURES = {
                               P, P, I64, P, P]),
     "sdc_fingerprint3": (I32, [P, I64, I32, I64, P, P]),
     "sdc_fingerprint2": (I32, [P, I64, I32, P, P]),
+    "sdc_kv_fingerprint": (I32, [P, I64, I64, I64, P, I64, P, P]),
     "sdc_mfma_layout_selftest": (I32, [P, P, P, P]),
     "sdc_last_error": (ctypes.c_char_p, []),
     "sdc_profile_enable": (I32, [I32]),

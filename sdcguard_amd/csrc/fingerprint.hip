@@ -148,6 +148,87 @@ unsigned grid_for(int64_t work_items) {
   return (unsigned)g;
 }
 
+
+// Paged-KV block fingerprints: fp3 of every block of a paged cache, each block's words numbered from 0 (what
+// recompute.fingerprint gives the block as a tensor of its own).  The weights depend only on the position in the
+// block, so a workgroup owns one slice of KV_SLICE positions of every block it visits (16 words per thread) and
+// keeps their weights in registers while it streams blocks; per block the three sums use one 64-bit and one
+// 32-bit multiply-add per weight (b w = b lo_s + 2^32 b hi' mod 2^64, with lo_s the signed low half of w and
+// hi' its high half plus the low half's sign bit), then a wave and workgroup reduction and three 64-bit atomics.
+constexpr int KV_WPT = 16;                       // words per thread
+constexpr int KV_SLICE = 256 * KV_WPT;           // positions per workgroup slice
+
+struct KvArgs {
+  const uint8_t* cache;
+  int64_t block_bytes, words, nblocks;           // nblocks: valid block ids are 0 .. nblocks - 1
+  const int64_t* ids;                            // block of entry i (null: entry i is block i); < 0: no block
+  int64_t n;
+  int64_t* out;                                  // [n][3]
+  int vec;
+};
+
+__global__ __launch_bounds__(256) void kv_fp3_kernel(KvArgs a) {
+  __shared__ int64_t red[4][3];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t p0 = (int64_t)blockIdx.x * KV_SLICE + (int64_t)t * KV_WPT;
+  int32_t w1l[KV_WPT], w2l[KV_WPT];
+  uint32_t w1h[KV_WPT], w2h[KV_WPT];
+#pragma unroll
+  for (int e = 0; e < KV_WPT; ++e) {
+    const uint64_t z = fp3_z((uint64_t)(p0 + e));
+    const uint64_t q1 = z | 1ull, q2 = (z ^ (z >> 32)) | 1ull;
+    w1l[e] = (int32_t)(uint32_t)q1;
+    w2l[e] = (int32_t)(uint32_t)q2;
+    w1h[e] = (uint32_t)(q1 >> 32) + ((uint32_t)q1 >> 31);
+    w2h[e] = (uint32_t)(q2 >> 32) + ((uint32_t)q2 >> 31);
+  }
+  const int nw = p0 >= a.words ? 0 : (a.words - p0 < KV_WPT ? (int)(a.words - p0) : KV_WPT);
+  for (int64_t i = blockIdx.y; i < a.n; i += gridDim.y) {
+    const int64_t blk = a.ids ? a.ids[i] : i;
+    if (blk < 0 || blk >= a.nblocks) continue;                  // (uniform over the workgroup)
+    const uint8_t* src = a.cache + blk * a.block_bytes + p0 * 2;
+    int32_t b[KV_WPT];
+    if (a.vec && nw == KV_WPT) {
+      const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+      const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        b[2 * j] = (int16_t)(v0[j] & 0xFFFFu);
+        b[2 * j + 1] = (int16_t)(v0[j] >> 16);
+        b[8 + 2 * j] = (int16_t)(v1[j] & 0xFFFFu);
+        b[8 + 2 * j + 1] = (int16_t)(v1[j] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < KV_WPT; ++e) b[e] = e < nw ? (int16_t)(src[2 * e] | (src[2 * e + 1] << 8)) : 0;
+    }
+    int64_t s0 = 0, l1 = 0, l2 = 0;
+    uint32_t h1 = 0, h2 = 0;
+#pragma unroll
+    for (int e = 0; e < KV_WPT; ++e) {
+      s0 += b[e];
+      l1 += (int64_t)b[e] * (int64_t)w1l[e];
+      l2 += (int64_t)b[e] * (int64_t)w2l[e];
+      h1 += (uint32_t)b[e] * w1h[e];
+      h2 += (uint32_t)b[e] * w2h[e];
+    }
+    int64_t v[3] = {s0, (int64_t)((uint64_t)l1 + ((uint64_t)h1 << 32)), (int64_t)((uint64_t)l2 + ((uint64_t)h2 << 32))};
+#pragma unroll
+    for (int c = 0; c < 3; ++c) v[c] = wave_sum_i64(v[c]);
+    if (lane == 0) {
+      red[w][0] = v[0];
+      red[w][1] = v[1];
+      red[w][2] = v[2];
+    }
+    __syncthreads();
+    if (t < 3) {
+      const uint64_t sum = (uint64_t)red[0][t] + (uint64_t)red[1][t] + (uint64_t)red[2][t] + (uint64_t)red[3][t];
+      atomicAdd((unsigned long long*)(a.out + 3 * i + t), (unsigned long long)sum);
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace
 
 // out[3] (int64, zeroed by the caller) += fp3 of n words of word_bytes (2 or 1) bytes at bits, positions from start
@@ -187,6 +268,26 @@ extern "C" int sdc_fingerprint2(const void* bits, int64_t n, int kind, int64_t* 
   if (kind == 0) hipLaunchKernelGGL(fp2_kernel<0>, dim3(g), dim3(256), 0, stream, X, n, out);
   else if (kind == 1) hipLaunchKernelGGL(fp2_kernel<1>, dim3(g), dim3(256), 0, stream, X, n, out);
   else hipLaunchKernelGGL(fp2_kernel<2>, dim3(g), dim3(256), 0, stream, X, n, out);
+  SDC_LAUNCH_CHECK();
+  return SDC_OK;
+}
+
+// out[i][0..2] (int64, zeroed by the caller) += fp3 of block ids[i] (or block i) of a paged cache of int16 words:
+// block b holds `words` words at cache + b * block_bytes, its positions numbered from 0.  Entries whose id is
+// negative or >= nblocks are left as they are.
+extern "C" int sdc_kv_fingerprint(const void* cache, int64_t nblocks, int64_t block_bytes, int64_t words,
+                                  const int64_t* ids, int64_t n, int64_t* out, hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
+  if (!cache || !out || nblocks < 1 || words < 1 || n < 0 || block_bytes < words * 2) return SDC_EINVAL;
+  if (n == 0) return SDC_OK;
+  KvArgs a{(const uint8_t*)cache, block_bytes, words, nblocks, ids, n, out,
+           (block_bytes % 16 == 0) && ((uintptr_t)cache % 16 == 0)};
+  const int64_t slices = sdc_cdiv(words, KV_SLICE);
+  int64_t gy = sdc_cdiv(2048, slices);
+  if (gy > n) gy = n;
+  if (gy > 65535) gy = 65535;
+  SdcProf prof("kv_fingerprint", stream);
+  hipLaunchKernelGGL(kv_fp3_kernel, dim3((unsigned)slices, (unsigned)gy), dim3(256), 0, stream, a);
   SDC_LAUNCH_CHECK();
   return SDC_OK;
 }

@@ -1,0 +1,112 @@
+"""Paged-KV block fingerprints (sdc_kv_fingerprint through sdcguard_amd.kv) bit-exact against the oracle (fp3 of
+each block's words from 0, the value recompute.fingerprint gives the block on its own) and against this library's
+own whole-tensor fingerprint per block; the ledger check catches stale / reused blocks and K/V bit flips; the
+28-layer x 4096-block Qwen3-0.6B-like cache with 64 sequences of 512-2048 tokens."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fingerprint as F
+
+pytestmark = pytest.mark.gpu
+
+
+def _cache(nblocks, hkv=8, n=16, d=128, seed=0):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return torch.randn(nblocks, hkv, n, 2 * d, device="cuda", generator=g).bfloat16()
+
+
+def test_block_fingerprints_bit_exact():
+    from sdcguard_amd.kv import block_fingerprints
+    from sdcguard_amd.recompute import fingerprint
+    cache = _cache(37, hkv=2, n=16, d=64)
+    fp = block_fingerprints(cache).cpu().numpy()
+    ref = F.kv_block_fp3(cache.view(torch.int16).cpu().numpy())
+    assert np.array_equal(fp, ref)
+    for b in (0, 5, 36):
+        assert np.array_equal(fp[b], fingerprint(cache[b]).cpu().numpy())
+    ids = torch.tensor([3, -1, 3, 36, 40, 0], device="cuda")
+    fi = block_fingerprints(cache, ids).cpu().numpy()
+    assert np.array_equal(fi[[0, 2, 3, 5]], ref[[3, 3, 36, 0]])
+    assert not fi[[1, 4]].any()                              # no block: zeros
+
+
+def test_odd_sized_and_strided_blocks():
+    """Blocks whose word count is not a multiple of the per-thread slice, and blocks padded apart in memory."""
+    from sdcguard_amd.kv import block_fingerprints
+    g = torch.Generator(device="cuda").manual_seed(1)
+    base = torch.randn(9, 3, 1000, device="cuda", generator=g).bfloat16()
+    cache = base[:, :, :777]                                 # block b at stride 3000 words, 2331 words... per row gap
+    blocks = torch.stack([cache[b].contiguous() for b in range(9)])
+    fp = block_fingerprints(blocks).cpu().numpy()
+    ref = F.kv_block_fp3(blocks.view(torch.int16).cpu().numpy())
+    assert np.array_equal(fp, ref)
+    padded = base[:, :2]                                     # each block 2000 contiguous words, 3000 apart
+    fp2 = block_fingerprints(padded).cpu().numpy()
+    ref2 = F.kv_block_fp3(padded.contiguous().view(torch.int16).cpu().numpy())
+    assert np.array_equal(fp2, ref2)
+
+
+def test_ledger_catches_stale_blocks_and_bit_flips():
+    from sdcguard_amd.kv import KVLedger
+    cache = _cache(64, hkv=4, n=16, d=64, seed=2)
+    g = torch.Generator().manual_seed(3)
+    bt = torch.randint(0, 64, (6, 10), generator=g).cuda()
+    bt[2, 7:] = -1
+    led = KVLedger(cache, 6, 10)
+    led.record(bt)
+    assert led.verify(bt).read()["mismatched"] == 0
+    stale = bt.clone()
+    stale[4, 3] = (bt[4, 3] + 1) % 64                        # the table points at another block
+    r = led.verify(stale).read()
+    assert r["entries"] == [(4, 3)] or (bt == stale[4, 3]).sum() > 0
+    assert (4, 3) in r["entries"]
+    blk = int(bt[1, 5])
+    v = cache[blk, 2, 7, 100:101].view(torch.int16)
+    v ^= 1 << 3                                              # one bit of one value of one block
+    r = led.verify(bt).read()
+    want = sorted(tuple(x) for x in (bt == blk).nonzero().cpu().tolist())
+    assert sorted(r["entries"]) == want and r["mismatched"] == len(want)
+
+
+def test_qwen3_like_cache_28_layers_4096_blocks():
+    """28 layers x 4096 blocks of [8 KV heads, 16 tokens, 2 x 128] bf16 N(0,1) (7.5 GB); 64 sequences of U[512,
+    2048] tokens whose block-table entries are drawn from the 4096 blocks with replacement (about 80 blocks a
+    sequence: pages are shared); every fingerprint of a sample of 512 (layer, block) pairs is bit-exact against the
+    oracle; the ledger flags a stale entry and a flipped bit, exactly where they are."""
+    from sdcguard_amd.kv import KVLedger, block_fingerprints
+    layers, nblk = 28, 4096
+    g = torch.Generator(device="cuda").manual_seed(11)
+    cache = torch.empty(layers * nblk, 8, 16, 256, dtype=torch.bfloat16, device="cuda")
+    for lay in range(layers):
+        cache[lay * nblk:(lay + 1) * nblk] = torch.randn(nblk, 8, 16, 256, device="cuda", generator=g).bfloat16()
+    fp = block_fingerprints(cache)
+    rng = np.random.default_rng(12)
+    sample = rng.choice(layers * nblk, 512, replace=False)
+    sub = cache[torch.from_numpy(sample).cuda()].view(torch.int16).cpu().numpy()
+    ref = F.kv_block_fp3_c(sub, threads=8) if F.c_lib() is not None else F.kv_block_fp3(sub)
+    assert np.array_equal(fp[torch.from_numpy(sample).cuda()].cpu().numpy(), ref)
+    lens = rng.integers(512, 2049, 64)
+    W = int(-(-lens.max() // 16))
+    bt = torch.full((64, W), -1, dtype=torch.int64)
+    for r, L in enumerate(lens):
+        nb = int(-(-L // 16))
+        bt[r, :nb] = torch.from_numpy(rng.integers(0, nblk, nb))
+    bt = bt.cuda()
+    layer = 17
+    lc = cache[layer * nblk:(layer + 1) * nblk]
+    led = KVLedger(lc, 64, W)
+    led.record(bt)
+    assert led.verify(bt).read()["mismatched"] == 0
+    stale = bt.clone()
+    stale[40, 10] = (int(bt[40, 10]) + 1234) % nblk
+    r = led.verify(stale).read()
+    assert (40, 10) in r["entries"]
+    blk = int(bt[7, 3])
+    v = lc[blk, 5, 9, 200:201].view(torch.int16)
+    v ^= 1 << 14
+    r = led.verify(bt).read()
+    want = sorted(tuple(x) for x in (bt == blk).nonzero().cpu().tolist())
+    assert sorted(r["entries"]) == want
