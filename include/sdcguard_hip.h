@@ -133,6 +133,35 @@ int sdc_fingerprint2(const void* bits, int64_t n, int kind, int64_t* out, hipStr
 int sdc_kv_fingerprint(const void* cache, int64_t nblocks, int64_t block_bytes, int64_t words, const int64_t* ids,
                        int64_t n, int64_t* out, hipStream_t stream);
 
+/* ---- sampled attention recompute from a paged KV cache, and the sampled tokens' KV-write check ------------
+ * Replaces serve_attn.attn_check_triton (serve_attn.py:574-602) and its two kernels _attn_part / _attn_judge
+ * (:335-571); the arithmetic of attn_check_torch (:165-280).  One launch, no host synchronisation.
+ *   q, o (T, Hq, D): element strides (sqt, sqh), last dimension contiguous; dtype 0 = bf16, 1 = fp16 (the KV
+ *     cache, key and val are of the same dtype).
+ *   kv (NB, Hkv, N, 2D): K in [.., :D], V in [.., D:2D], element strides (skb, skh, skn, skd).
+ *   key, val (T, Hkv, D): the keys and values the layer wrote this call, strides (skt, skh2), (svt, svh), last
+ *     dimension contiguous; slots (SN,) int64: vLLM's slot_mapping.  Only read when has_write != 0.
+ *   qsl (R + 1) int32 query_start_loc, seq_lens (R) int32, bt (R, W) int32 block table with row stride sbt.
+ *   state: the layer's 18-column int64 row (serve_attn.py:87-89) at state + slot * 18; ctrl int64[2] =
+ *     (step, active): the call checks only when active != 0 and step % nl == idx.
+ *   capm (slots, 12) int32, capq / capo (slots, capw) fp32: the capture of the first sample over `line`; capkv
+ *     (caprows, 2, capw) in the cache's dtype + capkvm int32[4]: the keys and values it attended (keep_kv), or NULL.
+ *   samples: (token, head) pairs recomputed per call (SAMPLES = 4 in the reference; more reuse its picking rule).
+ *   workspace: sdc_attn_check_workspace(samples, W * N, D) bytes, ZEROED before its first use (per-sample
+ *     counters, which every call leaves at zero again); may be NULL when sdc_attn_splits(samples, W * N) == 1.
+ *   scores_out (may be NULL): each judged sample's per-dimension scores, (samples, D) fp32 (tests). */
+int64_t sdc_attn_splits(int64_t samples, int64_t max_keys);
+int64_t sdc_attn_check_workspace(int64_t samples, int64_t max_keys, int64_t head_size);
+int sdc_attn_check(int dtype, const void* q, int64_t sqt, int64_t sqh, const void* o, int64_t sot, int64_t soh,
+                   int64_t T, int64_t Hq, int64_t D, const void* kv, int64_t skb, int64_t skh, int64_t skn,
+                   int64_t skd, int64_t NB, int64_t Hkv, int64_t N, const void* key, int64_t skt, int64_t skh2,
+                   const void* val, int64_t svt, int64_t svh, const int32_t* qsl, const int32_t* seq_lens, int64_t R,
+                   const int32_t* bt, int64_t sbt, int64_t W, const int64_t* slots, int64_t SN, int64_t* state,
+                   int64_t slot, const int64_t* ctrl, int64_t nl, int64_t idx, float scale, int64_t left, float line,
+                   int32_t* capm, float* capq, float* capo, int64_t capw, void* capkv, int32_t* capkvm,
+                   int64_t caprows, int samples, void* workspace, int64_t workspace_bytes, int has_write,
+                   int keep_kv, float* scores_out, hipStream_t stream);
+
 /* ---- per-kernel timing (no counterpart in the reference; for benchmarks) ------------------------------------
  * With profiling on, every kernel launch is bracketed by two HIP events on its stream; sdc_profile_read waits for
  * them and sums the durations of one kernel: "expected_gemm" (serving GEMM), "serve_fused", "serve_sums",

@@ -1,0 +1,284 @@
+"""Sampled attention recompute from a paged KV cache, and the check of the sampled tokens' own KV writes.
+
+The check of serve_attn.py (reference): at a checked call, SAMPLES (token, head) outputs of one attention layer are
+recomputed in fp32 from the query row and the request's keys and values, read from the paged KV cache through the
+block table (block bt[r, t // block_size], slot t % block_size), and scored against the first-order rounding bound
+of a correct FlashAttention / Triton backend (serve_attn.py:14-36); the sampled token's own KV write is compared bit
+for bit with the cache slot the block table gives its position.  The GPU work is one launch of the library's
+`sdc_attn_check` (csrc/attn_check.hip); there is no CPU implementation of the check.
+
+Kept as in the reference, because they are its state format and its sample choice: the constants below, the
+18-column state row and its column order, the 12-column capture row, the packed keys (score bits << 32 | value),
+and the sample-picking rule (sample_python).
+"""
+from __future__ import annotations
+
+import bisect
+import ctypes
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+ATTN_Z = 4.0              # the line (serve_attn.py:73)
+MIN_LINE = 1.5
+SAMPLES = 4               # (token, head) pairs per checked call
+CAP_ROWS = 65536          # most keys and values kept for an alarming sample
+LOG_R = 17
+MAX_REQUESTS = (1 << (LOG_R - 1)) - 1
+M32 = 0xFFFFFFFF
+S31 = 0x7FFFFFFF
+PICK_A, PICK_B, PICK_C = 1000003, 7919, 104729
+TWO22, TWO21, TWO23 = 2.0 ** -22, 2.0 ** -21, 2.0 ** -23
+COLS = 18
+(C_ZT, C_ZH, C_ZD, C_ZO, C_ZR, C_ZS, C_ZP, C_CALLS, C_SAMPLES, C_SKIP, C_UNJ, C_BADBLK, C_KEYS, C_WN, C_WBAD,
+ C_WSLOT, C_WLAST, C_WWHERE) = range(COLS)
+CAPM = 12
+CM_CLAIM, CM_ROW, CM_HEAD, CM_REQ, CM_POS, CM_SL, CM_LO, CM_STEP, CM_Z, CM_KEPT, CM_DIM, CM_HK = range(CAPM)
+W_CONTENT, W_SLOT = 1, 2
+
+
+def f32_of_bits(bits: int) -> float:
+    return float(torch.tensor([int(bits) & M32], dtype=torch.int64).to(torch.int32).view(torch.float32).item())
+
+
+def dtype_consts(dtype: torch.dtype) -> tuple:
+    """(unit roundoff, output spacing) of the outputs' dtype (serve_norm.py:69-77)."""
+    if dtype == torch.float16:
+        return 2.0 ** -11, 2.0 ** -24
+    return 2.0 ** -8, 1e-37
+
+
+def p_spacing(dtype: torch.dtype) -> float:
+    """Half the subnormal spacing of P's dtype, or fp32's smallest normal (serve_attn.py:106-109)."""
+    return 2.0 ** -25 if dtype == torch.float16 else 2.0 ** -126
+
+
+def bound_consts(dtype: torch.dtype, head_size: int) -> tuple:
+    """(u, output spacing, P spacing, q.k accumulation coefficient) for outputs in dtype (serve_attn.py:115-118)."""
+    u, sp = dtype_consts(dtype)
+    return u, sp, p_spacing(dtype), (head_size + 8) * TWO23
+
+
+def sample_python(step: int, idx: int, nl: int, j: int, qsl: list, seq_lens: list, rows: int,
+                  heads: int) -> Optional[dict]:
+    """The (token row, request, position, seq_len, query head) sample j of layer idx of nl takes at a step, or None
+    (serve_attn.py:130-157; the kernel takes the same)."""
+    nreq = len(seq_lens)
+    ntok = min(int(qsl[nreq]), rows)
+    if ntok <= 0:
+        return None
+    h = (step // nl) * PICK_A + j * PICK_B + idx * PICK_C
+    if j % 2 == 0:
+        pk = h % (ntok * heads)
+        i = pk // heads
+    else:
+        nreal = bisect.bisect_left(qsl, ntok, 0, nreq + 1)      # requests that hold a token of the step
+        if nreal <= 0:
+            return None
+        pk = h % (nreal * heads)
+        i = int(qsl[pk // heads + 1]) - 1
+    r = bisect.bisect_left(qsl, i + 1, 0, nreq + 1) - 1
+    q0, q1, sl = int(qsl[r]), int(qsl[r + 1]), int(seq_lens[r])
+    pos = sl - (q1 - q0) + (i - q0)
+    if not (0 <= i < rows and q1 > q0 and sl > 0 and 0 <= pos < sl):
+        return None
+    return {"row": i, "request": r, "position": pos, "seq_len": sl, "head": pk % heads}
+
+
+def _pow2(x: int) -> int:
+    return 1 << (max(1, int(x)) - 1).bit_length()
+
+
+def workspace_bytes(samples: int, max_keys: int, head_size: int) -> int:
+    return int(_lib.lib().sdc_attn_check_workspace(samples, max_keys, head_size))
+
+
+def buffers(device, slots: int, width: int, cap_rows: int, kv_dtype, samples: int = SAMPLES) -> dict:
+    """The buffers the checks of `slots` layers write on one device, allocated once (fixed addresses, so calls can
+    be captured in HIP graphs); the workspace is sized for any context length (serve_attn.py:667-678)."""
+    bd = _pow2(width)
+    ws = workspace_bytes(samples, 1 << 40, width)
+    return {"state": torch.zeros(slots, COLS, dtype=torch.int64, device=device),
+            "capm": torch.zeros(slots, CAPM, dtype=torch.int32, device=device),
+            "capq": torch.zeros(slots, bd, dtype=torch.float32, device=device),
+            "capo": torch.zeros(slots, bd, dtype=torch.float32, device=device),
+            "capkv": torch.zeros(max(1, cap_rows), 2, bd, dtype=kv_dtype, device=device),
+            "capkvm": torch.zeros(4, dtype=torch.int32, device=device),
+            "ws": torch.zeros(max(ws, 1), dtype=torch.uint8, device=device),
+            "ctrl": torch.zeros(2, dtype=torch.int64, device=device),
+            "samples": samples}
+
+
+def _index32(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.int32 else t.to(torch.int32)
+
+
+def attn_check(q, o, kv, key, val, qsl, seq_lens, bt, slots, state, slot, ctrl, nl, idx, scale, left, line, capm,
+               capq, capo, capkv, capkvm, ws, has_write, keep_kv, samples: int = SAMPLES,
+               scores_out: Optional[torch.Tensor] = None) -> None:
+    """One check of a call (serve_attn.attn_check_triton's arguments): q, o [T, Hq, D], kv [blocks, Hkv, N, 2D],
+    key / val [T, Hkv, D], vLLM's query_start_loc, seq_lens, block_table and slot_mapping; state, capm, capq, capo,
+    capkv, capkvm, ws and ctrl from buffers().  Queues one kernel on the current stream; never synchronises."""
+    _lib.require_gpu(q, o, kv, state)
+    T, Hq, D = q.shape
+    NB, Hkv, N = kv.shape[0], kv.shape[1], kv.shape[2]
+    R, W = seq_lens.shape[0], bt.shape[1]
+    if q.stride(-1) != 1 or o.stride(-1) != 1 or o.shape != q.shape:
+        raise ValueError("q and o must be [T, Hq, D] with the last dimension contiguous")
+    if kv.shape[3] != 2 * D or kv.dtype != q.dtype or o.dtype != q.dtype:
+        raise ValueError("a KV cache layout the check does not read: [blocks, Hkv, block_size, 2 * head_size] in "
+                         "the queries' dtype")
+    if R > MAX_REQUESTS:
+        raise ValueError(f"{R} requests in a step: the kernel takes at most {MAX_REQUESTS}")
+    if not 0 <= int(slot) < state.shape[0] or state.shape[1] != COLS or ctrl.numel() < 2:
+        raise ValueError("slot outside the state rows, or buffers not made by buffers()")
+    if capm is not None and (capm.shape[0] <= int(slot) or capm.shape[1] != CAPM or capq.shape[0] <= int(slot) or
+                             capo.shape != capq.shape or capq.shape[1] < D):
+        raise ValueError("capture buffers too small for this slot or head size")
+    if capkv is not None and (capkv.dim() != 3 or capkv.shape[1] != 2 or
+                              (capq is not None and capkv.shape[2] != capq.shape[1])):
+        raise ValueError("capkv must be [rows, 2, width] with the width of capq")
+    qsl, seq_lens, bt = _index32(qsl), _index32(seq_lens), _index32(bt)
+    if bt.stride(1) != 1:
+        bt = bt.contiguous()
+    if has_write:
+        if key.stride(-1) != 1 or val.stride(-1) != 1:
+            raise ValueError("key and val must have a contiguous last dimension")
+        if slots.dtype != torch.int64:
+            slots = slots.to(torch.int64)
+        kk, vv, sl_ = key, val, slots
+    else:
+        kk, vv, sl_ = None, None, None
+    keep = bool(keep_kv) and capkv is not None and capkv.dtype == kv.dtype and capkv.shape[-1] >= D
+    cap_rows = capkv.shape[0] if keep else 0
+    L = _lib.lib()
+    rc = L.sdc_attn_check(
+        _lib.dtype_code(q.dtype), q.data_ptr(), q.stride(0), q.stride(1), o.data_ptr(), o.stride(0), o.stride(1),
+        T, Hq, D, kv.data_ptr(), kv.stride(0), kv.stride(1), kv.stride(2), kv.stride(3), NB, Hkv, N,
+        _lib.ptr(kk), kk.stride(0) if kk is not None else 0, kk.stride(1) if kk is not None else 0,
+        _lib.ptr(vv), vv.stride(0) if vv is not None else 0, vv.stride(1) if vv is not None else 0,
+        qsl.data_ptr(), seq_lens.data_ptr(), R, bt.data_ptr(), bt.stride(0), W,
+        _lib.ptr(sl_), sl_.shape[0] if sl_ is not None else 0,
+        state.data_ptr(), int(slot), ctrl.data_ptr(), int(nl), int(idx), float(scale), int(left), float(line),
+        _lib.ptr(capm), _lib.ptr(capq), _lib.ptr(capo), capq.shape[1] if capq is not None else 0,
+        _lib.ptr(capkv) if keep else None, _lib.ptr(capkvm) if keep else None, cap_rows, int(samples),
+        _lib.ptr(ws), ws.numel() * ws.element_size() if ws is not None else 0, 1 if has_write else 0,
+        1 if keep else 0, _lib.ptr(scores_out), _lib.stream_of(q))
+    _lib.check(rc, "sdc_attn_check")
+
+
+attn_check_triton = attn_check     # the reference's name for the device check
+
+
+def run_case(c: dict, b: dict, *, step=0, nl=1, idx=0, slot=0, line=ATTN_Z, left=-1, has_write=True,
+             keep_kv=True, active=True, scores_out=None) -> None:
+    """One check of the call c (make_case) with the buffers b (buffers), at a step (serve_attn.py:681-690)."""
+    b["ctrl"][0] = step
+    b["ctrl"][1] = 1 if active else 0
+    attn_check(c["q"], c["o"], c["kv"], c["key"], c["val"], c["qsl"], c["seq_lens"], c["bt"], c["slots"],
+               b["state"], slot, b["ctrl"], nl, idx, c["scale"], left, line, b["capm"], b["capq"], b["capo"],
+               b["capkv"], b["capkvm"], b["ws"], has_write, keep_kv, samples=b.get("samples", SAMPLES),
+               scores_out=scores_out)
+
+
+def make_case(device, dtype, *, D=64, Hq=4, Hkv=2, N=16, NB=12, lens=((5, 1), (37, 9), (0, 0)), seed=0,
+              padded_rows=3) -> dict:
+    """A small paged-attention call with the outputs of a correct backend (float64 attention rounded to dtype):
+    requests (seq_len, query_len), (0, 0) a graph-padding request, padded_rows rows past the real tokens; block
+    ids drawn without repeats (serve_attn.py:621-664 builds the same kind of call)."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    R = len(lens)
+    qlens = [ql for _, ql in lens]
+    T = sum(qlens) + padded_rows
+    W = max(1, max(-(-sl // N) for sl, _ in lens))
+    order = torch.randperm(NB, generator=g)
+    bt = torch.zeros(R, W, dtype=torch.int32)
+    used = 0
+    for r, (sl, _) in enumerate(lens):
+        nblk = -(-sl // N)
+        bt[r, :nblk] = order[(torch.arange(nblk) + used) % NB].to(torch.int32)
+        used += nblk
+    kv = (torch.randn(NB, Hkv, N, 2 * D, generator=g) * 0.8).to(dtype)
+    q = (torch.randn(T, Hq, D, generator=g) * 0.5).to(dtype)
+    qsl = torch.zeros(R + 1, dtype=torch.int32)
+    qsl[1:] = torch.tensor(qlens, dtype=torch.int32).cumsum(0)
+    sls = torch.tensor([sl for sl, _ in lens], dtype=torch.int32)
+    slots = torch.full((T,), -1, dtype=torch.int64)
+    key = torch.zeros(T, Hkv, D, dtype=dtype)
+    val = torch.zeros(T, Hkv, D, dtype=dtype)
+    o = torch.zeros(T, Hq, D, dtype=dtype)
+    kv64 = kv.double()
+    for r, (sl, ql) in enumerate(lens):
+        if ql == 0:
+            continue
+        t = torch.arange(sl)
+        rows = kv64[bt[r, t // N].long(), :, t % N]                 # [sl, Hkv, 2D]
+        for jj in range(ql):
+            i = int(qsl[r]) + jj
+            pos = sl - ql + jj
+            blk, off = int(bt[r, pos // N]), pos % N
+            slots[i] = blk * N + off
+            key[i] = kv[blk, :, off, :D]
+            val[i] = kv[blk, :, off, D:]
+            ks = rows[:pos + 1]                                      # [pos+1, Hkv, 2D]
+            for hq in range(Hq):
+                hk = hq // (Hq // Hkv)
+                s = ks[:, hk, :D] @ q[i, hq].double() * D ** -0.5
+                o[i, hq] = (torch.softmax(s, 0) @ ks[:, hk, D:]).to(dtype)
+    return {"q": q.to(device), "o": o.to(device), "kv": kv.to(device), "key": key.to(device), "val": val.to(device),
+            "qsl": qsl.to(device), "seq_lens": sls.to(device), "bt": bt.to(device), "slots": slots.to(device),
+            "scale": D ** -0.5}
+
+
+def recheck(q_row: torch.Tensor, o_row: torch.Tensor, k_rows: torch.Tensor, v_rows: torch.Tensor, scale: float,
+            dtype: torch.dtype, line: float = ATTN_Z) -> dict:
+    """An alarming sample's recompute in float64 from the keys and values it attended (kept exactly by the check),
+    with the same bound: the host-side confirmation an alert carries (serve_attn.py:764-798).  It runs on the
+    captured rows after the read-back, not in the check."""
+    D = q_row.shape[-1]
+    q, o = q_row.double().cpu(), o_row.double().cpu()
+    K, V = k_rows.double().cpu(), v_rows.double().cpu()
+    u, sig_o, hsig_p, g_qk = bound_consts(dtype, D)
+    s = (K @ q) * scale
+    mx = s.max()
+    p = torch.exp(s - mx)
+    tot = p.sum()
+    ref = (p @ V) / tot
+    Va = V.abs()
+    e = g_qk * scale * (K.abs() @ q.abs()) + TWO22 * s.abs() + TWO21
+    bound = (2 * u + (K.shape[0] / 16 + 32) * TWO22 + TWO22 * abs(float(mx))) * ((p @ Va) / tot + ref.abs()) + \
+        ((p * e) @ Va + ref.abs() * (p * e).sum()) / tot + hsig_p * Va.sum(0) / tot + sig_o
+    z = torch.nan_to_num((o - ref).abs() / bound, nan=math.inf, posinf=math.inf)
+    worst = float(z.max()) if z.numel() else 0.0
+    over = int((z > line).sum())
+    out = {"worst_score": worst, "outputs_over_line": over, "outputs": int(o.numel()), "keys": int(K.shape[0])}
+    if not torch.isfinite(ref).all():
+        return {**out, "verdict": "not_judged", "why": "the kept keys or values are not finite"}
+    if z.numel():
+        d = int(z.argmax())
+        out.update(dim=d, output=float(o[d]), expected=float(ref[d]))
+    if over:
+        return {**out, "verdict": "output_wrong",
+                "why": f"{over} of {o.numel()} values of the kept output are more than {line:g} times the rounding "
+                       "bound from attention recomputed in float64 from its query and the keys and values it "
+                       "attended"}
+    return {**out, "verdict": "output_agrees",
+            "why": "the float64 recompute of the kept sample agrees with its output: the GPU's check disagreed"}
+
+
+def decode_state(row) -> dict:
+    """The 18-column state row of one layer as a dict (the reference's AttnChecks._report reads the same)."""
+    k = [int(v) for v in (row.tolist() if hasattr(row, "tolist") else row)]
+    return {"max_z": f32_of_bits(k[C_ZT] >> 32), "row": k[C_ZT] & M32, "head": k[C_ZH] & M32,
+            "dim": k[C_ZD] & M32, "output": f32_of_bits(k[C_ZO]), "expected": f32_of_bits(k[C_ZR]),
+            "step": k[C_ZS] & M32, "position": k[C_ZP] & M32, "calls": k[C_CALLS], "samples": k[C_SAMPLES],
+            "skipped": k[C_SKIP], "unjudged": k[C_UNJ], "bad_blocks": k[C_BADBLK], "keys": k[C_KEYS],
+            "writes_checked": k[C_WN], "writes_wrong": k[C_WBAD], "slots_wrong": k[C_WSLOT],
+            "write_last": k[C_WLAST], "write_where": k[C_WWHERE]}
+
+
+__all__ = ["ATTN_Z", "SAMPLES", "COLS", "CAPM", "bound_consts", "sample_python", "buffers", "attn_check",
+           "attn_check_triton", "run_case", "make_case", "recheck", "decode_state", "workspace_bytes"]

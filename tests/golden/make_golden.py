@@ -11,7 +11,11 @@ cases, the inputs and the reference's answers:
                    with torch.max, recorded on the way) and the resolved (max_z, batch, row, col_block, noise);
   * serve.npz      serve.check_static_impl: every checksum's score, the state row (keys and counts);
   * quant.npz      modes.judge on fp8 e4m3 and int8 GEMMs (inputs from modes._inputs, results of modes.gemm's CPU
-                   path, with and without an injected fault): per-block z and wrong-block counts.
+                   path, with and without an injected fault): per-block z and wrong-block counts;
+  * attn.npz       serve_attn.attn_check_torch on make_case calls (shapes, request mixes, a sliding window, wrong
+                   outputs, wrong KV writes and slots, block ids outside the cache, non-finite values, padding)
+                   over several steps: every sample's per-dimension scores, the 18-column state row and the
+                   capture row; sample_python's picks on a grid of batches; recheck on kept samples.
 Only numbers are stored (inputs as raw 16-bit or 8-bit words).  The integer fingerprints need no fixture: closed
 forms and brute force pin them (tests/test_oracle_fingerprint.py).
 """
@@ -306,6 +310,155 @@ def make_quant(md):
     return i
 
 
+class _NanToNumRecorder:
+    """Records the per-dimension score vectors the reference's attention check passes through torch.nan_to_num (one
+    call per sample, valid or not)."""
+
+    def __init__(self):
+        self.seen = []
+        self._orig = torch.nan_to_num
+
+    def __enter__(self):
+        orig = self._orig
+
+        def rec(t, *a, **kw):
+            r = orig(t, *a, **kw)
+            self.seen.append(r.detach().clone())
+            return r
+
+        torch.nan_to_num = rec
+        return self
+
+    def __exit__(self, *exc):
+        torch.nan_to_num = self._orig
+
+
+def _attn_cases(sa):
+    """(name, case, left, runs) cases built with the reference's make_case (serve_attn.py:621-664): shapes, request
+    mixes, a sliding window, and the faults its tests use (a wrong output, a wrong KV write, a block id outside the
+    cache, a write to another slot, non-finite outputs and keys).  runs: (step, nl, idx, active) calls."""
+    out = []
+    steps = [(s, 1, 0, True) for s in range(6)]
+    turns = [(s, 3, 1, True) for s in range(5)] + [(4, 1, 0, False)]
+    lens_mix = ((70, 1), (21, 6), (3, 3), (0, 0))
+    for dt in (torch.bfloat16, torch.float16):
+        tag = "bf16" if dt == torch.bfloat16 else "fp16"
+        for D, Hq, Hkv in ((64, 4, 2), (128, 2, 1), (128, 16, 8)):
+            base = sa.make_case("cpu", dt, D=D, Hq=Hq, Hkv=Hkv, lens=lens_mix, seed=D + Hq)
+            out.append((f"{tag}_D{D}_H{Hq}x{Hkv}_clean", base, -1, steps + turns))
+            wrong = dict(base, o=base["o"].clone())
+            wrong["o"][:, 1 % Hq, 5] = wrong["o"][:, 1 % Hq, 5].float() * 3 + 1
+            out.append((f"{tag}_D{D}_H{Hq}x{Hkv}_wrong", wrong, -1, steps))
+            if D == 64:
+                badw = dict(base, key=base["key"].clone())
+                badw["key"][:, 0, 3] = badw["key"][:, 0, 3].float() + 1
+                out.append((f"{tag}_D{D}_badwrite", badw, -1, steps))
+                badv = dict(base, val=base["val"].clone())
+                badv["val"][:, Hkv - 1, D - 2] = badv["val"][:, Hkv - 1, D - 2].float() * -1 + 0.5
+                out.append((f"{tag}_D{D}_badvalue", badv, -1, steps))
+                badblk = dict(base, bt=base["bt"].clone())
+                badblk["bt"][0, 1] = 10 ** 6
+                out.append((f"{tag}_D{D}_badblock", badblk, -1, steps))
+                negblk = dict(base, bt=base["bt"].clone())
+                negblk["bt"][1, 0] = -1
+                out.append((f"{tag}_D{D}_negblock", negblk, -1, steps))
+                badslot = dict(base, slots=base["slots"].clone())
+                badslot["slots"][:] = torch.where(badslot["slots"] >= 0, (badslot["slots"] + 1) % (12 * 16),
+                                                  badslot["slots"])
+                out.append((f"{tag}_D{D}_badslot", badslot, -1, steps))
+                nano = dict(base, o=base["o"].clone())
+                nano["o"][:, :, 7] = float("nan")
+                out.append((f"{tag}_D{D}_nan_out", nano, -1, steps))
+                infk = dict(base, kv=base["kv"].clone())
+                infk["kv"][:, :, :, 9] = float("inf")
+                out.append((f"{tag}_D{D}_inf_key", infk, -1, steps))
+                out.append((f"{tag}_D{D}_window20", base, 20, steps))
+        long_ = sa.make_case("cpu", dt, D=128, Hq=8, Hkv=2, NB=40, lens=((300, 1), (129, 1), (17, 4), (0, 0)),
+                             seed=5, padded_rows=2)
+        out.append((f"{tag}_long_clean", long_, -1, steps))
+        lw = dict(long_, o=long_["o"].clone())
+        lw["o"][:, 3, 100] = lw["o"][:, 3, 100].float() + 0.25
+        out.append((f"{tag}_long_wrong", lw, -1, steps))
+        out.append((f"{tag}_long_window7", long_, 7, steps[:3]))
+        pad = sa.make_case("cpu", dt, D=64, Hq=2, Hkv=1, NB=4, lens=((0, 0), (0, 0)), seed=6, padded_rows=3)
+        out.append((f"{tag}_all_padding", pad, -1, steps[:2]))
+    return out
+
+
+def make_attn(sa):
+    """serve_attn.attn_check_torch on make_case calls over several steps, each from fresh buffers: every sample's
+    per-dimension scores, the 18-column state row, the capture row and its q / o rows; sample_python's picks on a
+    grid; recheck on kept samples."""
+    st_ = _Store()
+    st_.out_full = {}
+    out = st_.out
+    names = []
+    for ci, (name, c, left, runs) in enumerate(_attn_cases(sa)):
+        p = f"c{ci}_"
+        D = c["q"].shape[-1]
+        out[p + "ids"] = np.array([st_.put(c[k]) for k in ("q", "o", "kv", "key", "val")])
+        out[p + "shape_q"] = np.array(c["q"].shape, np.int64)
+        out[p + "shape_kv"] = np.array(c["kv"].shape, np.int64)
+        out[p + "dtype"] = np.int64(1 if c["q"].dtype == torch.float16 else 0)
+        out[p + "qsl"] = c["qsl"].numpy().astype(np.int64)
+        out[p + "seq_lens"] = c["seq_lens"].numpy().astype(np.int64)
+        out[p + "bt"] = c["bt"].numpy().astype(np.int64)
+        out[p + "slots"] = c["slots"].numpy().astype(np.int64)
+        out[p + "scale"] = np.float64(c["scale"])
+        out[p + "left"] = np.int64(left)
+        out[p + "runs"] = np.array([[s, nl, idx, int(a)] for s, nl, idx, a in runs], np.int64)
+        for ri, (step, nl, idx, active) in enumerate(runs):
+            b = sa.buffers("cpu", 1, D, 128, c["q"].dtype)
+            with _NanToNumRecorder() as rec:
+                sa.run_case(sa.attn_check_torch, c, b, step=step, nl=nl, idx=idx, left=left, active=active)
+            q = f"{p}r{ri}_"
+            out[q + "state"] = b["state"][0].numpy().copy()
+            out[q + "capm"] = b["capm"][0].numpy().astype(np.int64)
+            out[q + "capq"] = b["capq"][0, :D].numpy().copy()
+            out[q + "capo"] = b["capo"][0, :D].numpy().copy()
+            out[q + "z"] = torch.stack([z.float() for z in rec.seen]).numpy()
+        names.append(name)
+    out["names"] = np.array(names)
+    # sample_python on a grid of batches (every kind of request mix, padding rows and requests)
+    grid = []
+    batches = [([0, 1, 7, 10, 10], [70, 21, 3, 0], 12, 4), ([0, 1, 2, 3, 4], [512, 900, 1500, 2047], 4, 16),
+               ([0, 5, 5, 6], [5, 0, 40], 9, 8), ([0, 0], [0], 3, 2), ([0, 3], [3], 3, 2),
+               ([0, 1, 2], [10, 20], 5, 32)]
+    for bi, (qsl, sls, rows, heads) in enumerate(batches):
+        for step in range(0, 41, 3):
+            for nl, idx in ((1, 0), (3, 2), (28, 5)):
+                for j in range(8):
+                    s = sa.sample_python(step, idx, nl, j, qsl, sls, rows, heads)
+                    v = [-1] * 5 if s is None else [s["row"], s["request"], s["position"], s["seq_len"], s["head"]]
+                    grid.append([bi, step, nl, idx, j, *v])
+    out["pick_grid"] = np.array(grid, np.int64)
+    for bi, (qsl, sls, rows, heads) in enumerate(batches):
+        out[f"pick_b{bi}"] = np.array([*qsl, -7, *sls, -7, rows, heads], np.int64)
+    # recheck (float64) on rows of the long case, right and wrong
+    c = sa.make_case("cpu", torch.bfloat16, D=128, Hq=8, Hkv=2, NB=40, lens=((300, 1), (129, 1)), seed=9)
+    g = torch.Generator().manual_seed(3)
+    for ri in range(4):
+        r = ri % 2
+        pos = int(c["seq_lens"][r]) - 1
+        i = int(c["qsl"][r + 1]) - 1
+        hq = ri * 2 + 1
+        N = c["kv"].shape[2]
+        rows = torch.stack([c["kv"][int(c["bt"][r, t // N]), hq // 4, t % N] for t in range(pos + 1)])
+        o_row = c["o"][i, hq].float().clone()
+        if ri >= 2:
+            o_row[int(torch.randint(0, 128, (1,), generator=g))] += 0.5 * (ri - 1)
+        res = sa.recheck(c["q"][i, hq], o_row, rows[:, :128], rows[:, 128:], c["scale"], torch.bfloat16)
+        out[f"rc{ri}_q"] = _bits(c["q"][i, hq])
+        out[f"rc{ri}_o"] = o_row.numpy().copy()
+        out[f"rc{ri}_kv"] = _bits(rows)
+        out[f"rc{ri}_scale"] = np.float64(c["scale"])
+        out[f"rc{ri}_res"] = np.array([res["worst_score"], res["outputs_over_line"], res.get("dim", -1),
+                                       res.get("output", 0.0), res.get("expected", 0.0),
+                                       1.0 if res["verdict"] == "output_wrong" else 0.0])
+    np.savez_compressed(os.path.join(OUT, "attn.npz"), **out)
+    return len(names)
+
+
 def main():
     if os.environ.get("SDCGUARD_SIGN_SEED") != "1":
         sys.exit("run with SDCGUARD_SIGN_SEED=1")
@@ -315,7 +468,10 @@ def main():
     from sdcguard import serve as sv
     cs.USE_FAST = False
     torch.set_num_threads(4)
-    which = sys.argv[1:] or ["signs", "train", "serve", "quant"]
+    which = sys.argv[1:] or ["signs", "train", "serve", "quant", "attn"]
+    if "attn" in which:
+        from sdcguard import serve_attn as sa
+        print("attn.npz:", make_attn(sa), "cases")
     if "signs" in which:
         make_signs(cs)
     if "train" in which:

@@ -47,3 +47,23 @@ def test_product_refuses_cpu_tensors():
     from sdcguard_amd.recompute import fingerprint
     with pytest.raises(_lib.HipLibraryError):
         fingerprint(torch.ones(10))
+
+
+def _param_counts():
+    """Number of parameters of every sdc_ function the header declares."""
+    text = open(os.path.join(ROOT, "include", "sdcguard_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"^(?:int|int64_t|void|const char\*)\s+(sdc_\w+)\s*\(([^)]*)\)\s*;", text, re.M):
+        params = [p for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+        out[m.group(1)] = len(params)
+    return out
+
+
+def test_ctypes_signatures_take_as_many_arguments_as_the_header_declares():
+    from sdcguard_amd import _lib
+    counts = _param_counts()
+    assert counts, "no declarations parsed"
+    for name, n in counts.items():
+        assert name in _lib.SIGNATURES, name
+        assert len(_lib.SIGNATURES[name][1]) == n, (name, len(_lib.SIGNATURES[name][1]), n)
