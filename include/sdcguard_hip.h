@@ -146,9 +146,12 @@ int sdc_kv_fingerprint(const void* cache, int64_t nblocks, int64_t block_bytes, 
  *     (step, active): the call checks only when active != 0 and step % nl == idx.
  *   capm (slots, 12) int32, capq / capo (slots, capw) fp32: the capture of the first sample over `line`; capkv
  *     (caprows, 2, capw) in the cache's dtype + capkvm int32[4]: the keys and values it attended (keep_kv), or NULL.
- *   samples: (token, head) pairs recomputed per call (SAMPLES = 4 in the reference; more reuse its picking rule).
- *   workspace: sdc_attn_check_workspace(samples, W * N, D) bytes, ZEROED before its first use (per-sample
- *     counters, which every call leaves at zero again); may be NULL when sdc_attn_splits(samples, W * N) == 1.
+ *   samples: (token, head) pairs recomputed per call, 1..1024 (SAMPLES = 4 in the reference; more reuse its
+ *     picking rule).
+ *   workspace: sdc_attn_check_workspace(samples, W * N, D) bytes, ZEROED before its first use: its first 4 KiB
+ *     hold per-sample counters at fixed places, which every call leaves at zero again, so one buffer serves calls
+ *     of any sample count and context length; may be NULL when sdc_attn_splits(samples, W * N) == 1.  Calls that
+ *     share a workspace must not overlap (one stream).
  *   scores_out (may be NULL): each judged sample's per-dimension scores, (samples, D) fp32 (tests). */
 int64_t sdc_attn_splits(int64_t samples, int64_t max_keys);
 int64_t sdc_attn_check_workspace(int64_t samples, int64_t max_keys, int64_t head_size);

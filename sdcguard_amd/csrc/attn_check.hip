@@ -574,10 +574,16 @@ int64_t pad_dim(int64_t D) { return D <= 64 ? 64 : D <= 128 ? 128 : 256; }
 
 }  // namespace
 
-// Workgroups per sample: enough that a long context spreads over the chip, at least ~256 keys each.
+// Workspace layout: per-sample counters first, at a fixed place (COUNTER_BYTES: up to MAX_SAMPLES samples), so a
+// buffer reused with another sample or split count still finds them at zero; then one record per workgroup.
+constexpr int64_t MAX_SAMPLES = 1024;
+constexpr int64_t COUNTER_BYTES = MAX_SAMPLES * (int64_t)sizeof(int32_t);
+
+// Workgroups per sample: enough that a long context spreads over the chip (about 256 keys each), at most 64, and
+// at most 1024 workgroups in all.
 extern "C" int64_t sdc_attn_splits(int64_t samples, int64_t max_keys) {
   if (samples <= 0 || max_keys <= 0) return 1;
-  const int64_t cap = std::max<int64_t>(1, sdc_cdiv(1024, samples));   // about 1024 workgroups in all at most
+  const int64_t cap = std::max<int64_t>(1, 1024 / samples);
   const int64_t s = std::min<int64_t>(sdc_cdiv(max_keys, 256), cap);
   return std::max<int64_t>(1, std::min<int64_t>(s, 64));
 }
@@ -586,27 +592,30 @@ extern "C" int64_t sdc_attn_check_workspace(int64_t samples, int64_t max_keys, i
   if (samples <= 0 || head_size <= 0) return 0;
   const int64_t nsplit = sdc_attn_splits(samples, max_keys);
   const int64_t dp = pad_dim(head_size);
-  return 256 + samples * nsplit * (4 + 4 * dp) * (int64_t)sizeof(float) + samples * (int64_t)sizeof(int32_t);
+  return 256 + COUNTER_BYTES + samples * nsplit * (4 + 4 * dp) * (int64_t)sizeof(float);
 }
 
-extern "C" int sdc_attn_check(int dtype, const void* q, int64_t sqt, int64_t sqh, const void* o, int64_t sot,
-                              int64_t soh, int64_t T, int64_t Hq, int64_t D, const void* kv, int64_t skb,
-                              int64_t skh, int64_t skn, int64_t skd, int64_t NB, int64_t Hkv, int64_t N,
-                              const void* key, int64_t skt, int64_t skh2, const void* val, int64_t svt,
-                              int64_t svh, const int32_t* qsl, const int32_t* seq_lens, int64_t R,
-                              const int32_t* bt, int64_t sbt, int64_t W, const int64_t* slots, int64_t SN,
-                              int64_t* state, int64_t slot, const int64_t* ctrl, int64_t nl, int64_t idx,
-                              float scale, int64_t left, float line, int32_t* capm, float* capq, float* capo,
-                              int64_t capw, void* capkv, int32_t* capkvm, int64_t caprows, int samples,
-                              void* workspace, int64_t workspace_bytes, int has_write, int keep_kv,
-                              float* scores_out, hipStream_t stream) {
-  SDC_CLEAR_ERRORS();
+#define SDC_ATTN_PARAMS                                                                                          \
+  int dtype, const void *q, int64_t sqt, int64_t sqh, const void *o, int64_t sot, int64_t soh, int64_t T,          \
+      int64_t Hq, int64_t D, const void *kv, int64_t skb, int64_t skh, int64_t skn, int64_t skd, int64_t NB,       \
+      int64_t Hkv, int64_t N, const void *key, int64_t skt, int64_t skh2, const void *val, int64_t svt,            \
+      int64_t svh, const int32_t *qsl, const int32_t *seq_lens, int64_t R, const int32_t *bt, int64_t sbt,         \
+      int64_t W, const int64_t *slots, int64_t SN, int64_t *state, int64_t slot, const int64_t *ctrl, int64_t nl,  \
+      int64_t idx, float scale, int64_t left, float line, int32_t *capm, float *capq, float *capo, int64_t capw,   \
+      void *capkv, int32_t *capkvm, int64_t caprows, int samples
+#define SDC_ATTN_ARGS                                                                                            \
+  dtype, q, sqt, sqh, o, sot, soh, T, Hq, D, kv, skb, skh, skn, skd, NB, Hkv, N, key, skt, skh2, val, svt, svh,    \
+      qsl, seq_lens, R, bt, sbt, W, slots, SN, state, slot, ctrl, nl, idx, scale, left, line, capm, capq, capo,    \
+      capw, capkv, capkvm, caprows, samples
+
+static int attn_check_impl(SDC_ATTN_PARAMS, void* workspace, int64_t workspace_bytes, int has_write, int keep_kv,
+                           float* scores_out, hipStream_t stream) {
   if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EINVAL;
   if (T <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || N <= 0 || R <= 0 || W <= 0 || NB <= 0) return SDC_EINVAL;
   if (Hq % Hkv != 0) return SDC_EINVAL;
   if (D > 256) return SDC_EUNSUPPORTED;                       // serve_attn.why_not: head sizes up to 256
   if (R > 65535) return SDC_EUNSUPPORTED;                     // MAX_REQUESTS (serve_attn.py:80)
-  if (samples < 1 || samples > 65536 || nl < 1 || idx < 0) return SDC_EINVAL;
+  if (samples < 1 || samples > MAX_SAMPLES || nl < 1 || idx < 0) return SDC_EINVAL;
   if (!q || !o || !kv || !qsl || !seq_lens || !bt || !state || !ctrl) return SDC_EINVAL;
   if (has_write && (!key || !val || !slots || SN < 0)) return SDC_EINVAL;
   if (capm && (!capq || !capo || capw < D)) return SDC_EINVAL;
@@ -619,9 +628,9 @@ extern "C" int sdc_attn_check(int dtype, const void* q, int64_t sqt, int64_t sqh
   a.q = (const uint16_t*)q; a.o = (const uint16_t*)o; a.kv = (const uint16_t*)kv;
   a.key = (const uint16_t*)key; a.val = (const uint16_t*)val;
   a.qsl = qsl; a.seqlens = seq_lens; a.bt = bt; a.slots = slots; a.ctrl = ctrl;
-  float* ws = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
-  a.ws = ws;
-  a.cnt = workspace ? (int32_t*)(ws + samples * nsplit * (4 + 4 * dp)) : nullptr;
+  char* wsb = (char*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  a.cnt = workspace ? (int32_t*)wsb : nullptr;
+  a.ws = workspace ? (float*)(wsb + COUNTER_BYTES) : nullptr;
   a.zdump = scores_out;
   a.state = state; a.capm = capm; a.capq = capq; a.capo = capo; a.capkv = (uint16_t*)capkv; a.capkvm = capkvm;
   a.T = T; a.R = R; a.W = W; a.NB = NB; a.N = N; a.Hq = Hq; a.GQ = Hq / Hkv; a.Hkv = Hkv; a.D = D;
@@ -650,4 +659,10 @@ extern "C" int sdc_attn_check(int dtype, const void* q, int64_t sqt, int64_t sqh
     launch_dt<SDC_FP16>(a, (int)dp, vec, grid, stream);
   SDC_LAUNCH_CHECK();
   return SDC_OK;
+}
+
+extern "C" int sdc_attn_check(SDC_ATTN_PARAMS, void* workspace, int64_t workspace_bytes, int has_write, int keep_kv,
+                              float* scores_out, hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
+  return attn_check_impl(SDC_ATTN_ARGS, workspace, workspace_bytes, has_write, keep_kv, scores_out, stream);
 }

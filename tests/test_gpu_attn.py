@@ -136,6 +136,35 @@ def test_matches_the_oracle_on_long_contexts(dtype, lens, samples, D, heads):
     print(f"max relative |dz| vs the oracle {worst:.2e}")
 
 
+def test_one_workspace_serves_calls_of_any_context_length_and_sample_count():
+    """A buffer reused by calls whose split counts and sample counts differ (the per-sample counters sit at fixed
+    places and every call leaves them at zero): each call's state equals a call on fresh buffers."""
+    from sdcguard_amd import serve_attn as SA
+    cases = [SA.make_case(DEV, torch.bfloat16, D=128, Hq=4, Hkv=2, NB=nb, lens=lens, seed=i)
+             for i, (nb, lens) in enumerate([(300, ((4000, 1), (700, 1))), (8, ((60, 1), (30, 2))),
+                                              (120, ((1800, 1), (33, 1)))])]
+    for c in cases:
+        c["left"] = -1
+        c["o"][:, 1, 9] += 0.75
+    shared = SA.buffers(DEV, 1, 128, 64, torch.bfloat16, samples=32)
+    for rep in range(2):
+        for ci, c in enumerate(cases):
+            for samples in (4, 32, 8):
+                shared["state"].zero_()
+                shared["capm"].zero_()
+                shared["samples"] = samples
+                SA.run_case(c, shared, step=rep * 5 + ci, keep_kv=False)
+                fresh = SA.buffers(DEV, 1, 128, 64, torch.bfloat16, samples=samples)
+                SA.run_case(c, fresh, step=rep * 5 + ci, keep_kv=False)
+                torch.cuda.synchronize()
+                assert torch.equal(shared["state"], fresh["state"]), (rep, ci, samples)
+                assert int(shared["state"][0, OA.C_CALLS]) == 1
+                assert int(shared["state"][0, OA.C_SAMPLES] + shared["state"][0, OA.C_SKIP] +
+                           shared["state"][0, OA.C_UNJ] + shared["state"][0, OA.C_BADBLK]) == samples
+    ws = shared["ws"]
+    assert int(ws[:4096].view(torch.int32).abs().sum()) == 0          # the counters are back at zero
+
+
 def test_keeps_the_attended_keys_and_the_recheck_confirms():
     from sdcguard_amd import serve_attn as SA
     c = SA.make_case(DEV, torch.bfloat16, D=128, Hq=4, Hkv=2, NB=30, lens=((300, 1), (90, 1)), seed=3)
