@@ -165,6 +165,24 @@ int sdc_attn_check(int dtype, const void* q, int64_t sqt, int64_t sqh, const voi
                    int64_t caprows, int samples, void* workspace, int64_t workspace_bytes, int has_write,
                    int keep_kv, float* scores_out, hipStream_t stream);
 
+/* sdc_attn_check without a workspace argument: it allocates nothing.  No counterpart in the reference; it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments and results as sdc_attn_check minus workspace / workspace_bytes.  Its workspace
+ * is a static device array of SDC_ATTN_SCRATCH_BYTES per GPU, held from the first call on that GPU (which must be
+ * the current device) until the process ends; a call that would need more returns SDC_EWORKSPACE (none does within
+ * the limits above: samples x splits <= 1024, head size <= 256).  All calls on one GPU share that array: calls
+ * that overlap in time on one GPU (several streams or host threads) race and must not be made. */
+#define SDC_ATTN_SCRATCH_BYTES 4456448
+int sdc_attn_check_noalloc(int dtype, const void* q, int64_t sqt, int64_t sqh, const void* o, int64_t sot,
+                           int64_t soh, int64_t T, int64_t Hq, int64_t D, const void* kv, int64_t skb, int64_t skh,
+                           int64_t skn, int64_t skd, int64_t NB, int64_t Hkv, int64_t N, const void* key, int64_t skt,
+                           int64_t skh2, const void* val, int64_t svt, int64_t svh, const int32_t* qsl,
+                           const int32_t* seq_lens, int64_t R, const int32_t* bt, int64_t sbt, int64_t W,
+                           const int64_t* slots, int64_t SN, int64_t* state, int64_t slot, const int64_t* ctrl,
+                           int64_t nl, int64_t idx, float scale, int64_t left, float line, int32_t* capm,
+                           float* capq, float* capo, int64_t capw, void* capkv, int32_t* capkvm, int64_t caprows,
+                           int samples, int has_write, int keep_kv, float* scores_out, hipStream_t stream);
+
 /* ---- per-kernel timing (no counterpart in the reference; for benchmarks) ------------------------------------
  * With profiling on, every kernel launch is bracketed by two HIP events on its stream; sdc_profile_read waits for
  * them and sums the durations of one kernel: "expected_gemm" (serving GEMM), "serve_fused", "serve_sums",

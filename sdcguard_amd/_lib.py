@@ -48,6 +48,9 @@ SIGNATURES = {
     "sdc_attn_check": (I32, [I32, P, I64, I64, P, I64, I64, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, I64,
                              P, I64, I64, P, I64, I64, P, P, I64, P, I64, I64, P, I64, P, I64, P, I64, I64, F32,
                              I64, F32, P, P, P, I64, P, P, I64, I32, P, I64, I32, I32, P, P]),
+    "sdc_attn_check_noalloc": (I32, [I32, P, I64, I64, P, I64, I64, I64, I64, I64, P, I64, I64, I64, I64, I64, I64,
+                                     I64, P, I64, I64, P, I64, I64, P, P, I64, P, I64, I64, P, I64, P, I64, P, I64,
+                                     I64, F32, I64, F32, P, P, P, I64, P, P, I64, I32, I32, I32, P, P]),
     "sdc_mfma_layout_selftest": (I32, [P, P, P, P]),
     "sdc_last_error": (ctypes.c_char_p, []),
     "sdc_profile_enable": (I32, [I32]),

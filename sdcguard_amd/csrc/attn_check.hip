@@ -15,6 +15,8 @@
 // log-sum-exp rescale, scores the sample against the first-order rounding bound and updates the layer's state row
 // with atomics.  With one split per sample the workgroup judges directly.
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "common.h"
 #include "profile.h"
@@ -665,4 +667,68 @@ extern "C" int sdc_attn_check(SDC_ATTN_PARAMS, void* workspace, int64_t workspac
                               float* scores_out, hipStream_t stream) {
   SDC_CLEAR_ERRORS();
   return attn_check_impl(SDC_ATTN_ARGS, workspace, workspace_bytes, has_write, keep_kv, scores_out, stream);
+}
+
+// ---- the same check without a workspace argument, for callers that cannot allocate -------------------------------
+// The workspace lives in `scratch`, a static device array: each GPU the library runs on holds its own copy until the
+// process ends.  SCRATCH_BYTES covers every call the check accepts (at most 1024 sample x split records of a head
+// size up to 256, plus the counters).  Its counters are cleared once per device, at the first call there, by a fill
+// kernel on the caller's stream (no memset node, so the call can be captured in a graph); every call leaves them at
+// zero again.  Calls on one GPU share the array: calls that overlap in time (other streams, other host threads)
+// race and must not be made.
+constexpr int64_t SCRATCH_BYTES = 4456448;        // 4.25 MiB
+static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::atomic<void*> g_scratch[MAX_DEVICES];
+std::mutex g_scratch_mu;
+
+__global__ void clear_counters_kernel(int32_t* cnt, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    cnt[i] = 0;
+}
+
+// The device address of this device's scratch array (set up at the first call on the device, which must be the
+// current device), or an error status.
+static int scratch_of_current_device(void** out, hipStream_t stream) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    sdc_note_error(e);
+    return SDC_ELAUNCH;
+  }
+  if (dev < 0 || dev >= MAX_DEVICES) return SDC_EUNSUPPORTED;
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) {
+        sdc_note_error(e != hipSuccess ? e : hipErrorInvalidSymbol);
+        return SDC_ELAUNCH;
+      }
+      hipLaunchKernelGGL(clear_counters_kernel, dim3(4), dim3(256), 0, stream, (int32_t*)p,
+                         COUNTER_BYTES / (int64_t)sizeof(int32_t));
+      e = hipGetLastError();
+      if (e != hipSuccess) {
+        sdc_note_error(e);
+        return SDC_ELAUNCH;
+      }
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return SDC_OK;
+}
+
+extern "C" int sdc_attn_check_noalloc(SDC_ATTN_PARAMS, int has_write, int keep_kv, float* scores_out,
+                                      hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
+  if (samples < 1 || samples > MAX_SAMPLES || D <= 0 || W <= 0 || N <= 0) return SDC_EINVAL;
+  if (sdc_attn_check_workspace(samples, W * N, D) > SCRATCH_BYTES) return SDC_EWORKSPACE;
+  void* ws = nullptr;
+  const int rc = scratch_of_current_device(&ws, stream);
+  if (rc != SDC_OK) return rc;
+  return attn_check_impl(SDC_ATTN_ARGS, ws, SCRATCH_BYTES, has_write, keep_kv, scores_out, stream);
 }

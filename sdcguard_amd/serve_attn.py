@@ -116,12 +116,9 @@ def _index32(t: torch.Tensor) -> torch.Tensor:
     return t if t.dtype == torch.int32 else t.to(torch.int32)
 
 
-def attn_check(q, o, kv, key, val, qsl, seq_lens, bt, slots, state, slot, ctrl, nl, idx, scale, left, line, capm,
-               capq, capo, capkv, capkvm, ws, has_write, keep_kv, samples: int = SAMPLES,
-               scores_out: Optional[torch.Tensor] = None) -> None:
-    """One check of a call (serve_attn.attn_check_triton's arguments): q, o [T, Hq, D], kv [blocks, Hkv, N, 2D],
-    key / val [T, Hkv, D], vLLM's query_start_loc, seq_lens, block_table and slot_mapping; state, capm, capq, capo,
-    capkv, capkvm, ws and ctrl from buffers().  Queues one kernel on the current stream; never synchronises."""
+def _call_args(q, o, kv, key, val, qsl, seq_lens, bt, slots, state, slot, ctrl, nl, idx, scale, left, line, capm,
+               capq, capo, capkv, capkvm, has_write, keep_kv, samples):
+    """The C-ABI arguments of one check, up to and including `samples` (sdc_attn_check's order), and the flags."""
     _lib.require_gpu(q, o, kv, state)
     T, Hq, D = q.shape
     NB, Hkv, N = kv.shape[0], kv.shape[1], kv.shape[2]
@@ -154,20 +151,51 @@ def attn_check(q, o, kv, key, val, qsl, seq_lens, bt, slots, state, slot, ctrl, 
         kk, vv, sl_ = None, None, None
     keep = bool(keep_kv) and capkv is not None and capkv.dtype == kv.dtype and capkv.shape[-1] >= D
     cap_rows = capkv.shape[0] if keep else 0
-    L = _lib.lib()
-    rc = L.sdc_attn_check(
-        _lib.dtype_code(q.dtype), q.data_ptr(), q.stride(0), q.stride(1), o.data_ptr(), o.stride(0), o.stride(1),
-        T, Hq, D, kv.data_ptr(), kv.stride(0), kv.stride(1), kv.stride(2), kv.stride(3), NB, Hkv, N,
-        _lib.ptr(kk), kk.stride(0) if kk is not None else 0, kk.stride(1) if kk is not None else 0,
-        _lib.ptr(vv), vv.stride(0) if vv is not None else 0, vv.stride(1) if vv is not None else 0,
-        qsl.data_ptr(), seq_lens.data_ptr(), R, bt.data_ptr(), bt.stride(0), W,
-        _lib.ptr(sl_), sl_.shape[0] if sl_ is not None else 0,
-        state.data_ptr(), int(slot), ctrl.data_ptr(), int(nl), int(idx), float(scale), int(left), float(line),
-        _lib.ptr(capm), _lib.ptr(capq), _lib.ptr(capo), capq.shape[1] if capq is not None else 0,
-        _lib.ptr(capkv) if keep else None, _lib.ptr(capkvm) if keep else None, cap_rows, int(samples),
-        _lib.ptr(ws), ws.numel() * ws.element_size() if ws is not None else 0, 1 if has_write else 0,
-        1 if keep else 0, _lib.ptr(scores_out), _lib.stream_of(q))
+    args = (_lib.dtype_code(q.dtype), q.data_ptr(), q.stride(0), q.stride(1), o.data_ptr(), o.stride(0), o.stride(1),
+            T, Hq, D, kv.data_ptr(), kv.stride(0), kv.stride(1), kv.stride(2), kv.stride(3), NB, Hkv, N,
+            _lib.ptr(kk), kk.stride(0) if kk is not None else 0, kk.stride(1) if kk is not None else 0,
+            _lib.ptr(vv), vv.stride(0) if vv is not None else 0, vv.stride(1) if vv is not None else 0,
+            qsl.data_ptr(), seq_lens.data_ptr(), R, bt.data_ptr(), bt.stride(0), W,
+            _lib.ptr(sl_), sl_.shape[0] if sl_ is not None else 0,
+            state.data_ptr(), int(slot), ctrl.data_ptr(), int(nl), int(idx), float(scale), int(left), float(line),
+            _lib.ptr(capm), _lib.ptr(capq), _lib.ptr(capo), capq.shape[1] if capq is not None else 0,
+            _lib.ptr(capkv) if keep else None, _lib.ptr(capkvm) if keep else None, cap_rows, int(samples))
+    # the index tensors converted above must live until the kernel has read them: the caller's stream orders them
+    return args, (1 if has_write else 0), (1 if keep else 0), (qsl, seq_lens, bt, sl_)
+
+
+def attn_check(q, o, kv, key, val, qsl, seq_lens, bt, slots, state, slot, ctrl, nl, idx, scale, left, line, capm,
+               capq, capo, capkv, capkvm, ws, has_write, keep_kv, samples: int = SAMPLES,
+               scores_out: Optional[torch.Tensor] = None) -> None:
+    """One check of a call (serve_attn.attn_check_triton's arguments): q, o [T, Hq, D], kv [blocks, Hkv, N, 2D],
+    key / val [T, Hkv, D], vLLM's query_start_loc, seq_lens, block_table and slot_mapping; state, capm, capq, capo,
+    capkv, capkvm, ws and ctrl from buffers().  Queues one kernel on the current stream; never synchronises."""
+    args, hw, keep, _held = _call_args(q, o, kv, key, val, qsl, seq_lens, bt, slots, state, slot, ctrl, nl, idx,
+                                       scale, left, line, capm, capq, capo, capkv, capkvm, has_write, keep_kv,
+                                       samples)
+    rc = _lib.lib().sdc_attn_check(*args, _lib.ptr(ws), ws.numel() * ws.element_size() if ws is not None else 0,
+                                   hw, keep, _lib.ptr(scores_out), _lib.stream_of(q))
     _lib.check(rc, "sdc_attn_check")
+
+
+SCRATCH_BYTES = 4456448      # the static workspace of attn_check_noalloc on each GPU (SDC_ATTN_SCRATCH_BYTES)
+
+
+def attn_check_noalloc(q, o, kv, key, val, qsl, seq_lens, bt, slots, state, slot, ctrl, nl, idx, scale, left, line,
+                       capm, capq, capo, capkv, capkvm, has_write, keep_kv, samples: int = SAMPLES,
+                       scores_out: Optional[torch.Tensor] = None) -> None:
+    """attn_check without a workspace: the library uses a static device array of SCRATCH_BYTES on q's GPU, so the
+    call allocates nothing (for graph capture and serving loops that cannot allocate).  Calls that overlap in time
+    on one GPU share that array and must not be made."""
+    with torch.cuda.device(q.device):
+        args, hw, keep, _held = _call_args(q, o, kv, key, val, qsl, seq_lens, bt, slots, state, slot, ctrl, nl, idx,
+                                           scale, left, line, capm, capq, capo, capkv, capkvm, has_write, keep_kv,
+                                           samples)
+        rc = _lib.lib().sdc_attn_check_noalloc(*args, hw, keep, _lib.ptr(scores_out), _lib.stream_of(q))
+    if rc == _lib.SDC_EWORKSPACE:
+        raise _lib.HipLibraryError(f"sdc_attn_check_noalloc: the call needs more than the {SCRATCH_BYTES} bytes of "
+                                   "static workspace (use attn_check with a workspace)")
+    _lib.check(rc, "sdc_attn_check_noalloc")
 
 
 attn_check_triton = attn_check     # the reference's name for the device check
