@@ -74,6 +74,27 @@ int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t
                      float beta, float z, float abs_floor, const float* sign_table, int64_t* result, void* workspace,
                      int64_t workspace_bytes, float* scores_out, hipStream_t stream);
 
+/* ---- both block checksums of one linear layer, one pass over y (no counterpart function in the reference) --------
+ * y = x @ W^T (+ bias): the column-block check of sdc_check_static (the serving check, serve.py:301-396) and the
+ * row-block check of sdc_matmul_check on the transposed views (W, x^T, y^T, bias[:, None]; checksum.py:435-530),
+ * with the same scores, keys and counts, from one read of y.
+ *   x (m x k) row stride sxm, W (n x k) row stride swn, y (m x n) row stride sym: bf16 (dtype 0; fp16 returns
+ *     SDC_EUNSUPPORTED), k- / n-contiguous; x and y with 16-byte aligned rows and n a multiple of 8 (otherwise
+ *     SDC_EUNSUPPORTED: the caller runs the two checks separately).  Blocks are 128 wide.
+ *   bias (n) or NULL; parts / spc / block_consts: the layer's constants as for sdc_check_static (k-contiguous
+ *     columns spc elements apart; block_consts required); sign_table: the epoch-0 128 x 128 table.
+ *   state: int64[4] of the column check (sdc_check_static's row, counts on); row_result: int64[3] of the row check
+ *     (sdc_matmul_check's result row; flat index ((column * mb + row block) * 2 + signed), mb = ceil(m / 128)).
+ *   workspace: sdc_linear_check_workspace(m, k, n) bytes.  col_scores (m, nb, 2) / row_scores (n, mb, 2): every
+ *     checksum's score, or NULL.  flags bit 0: run the column check's GEMM on a side stream, concurrently with the
+ *     row check's x pass and GEMM. */
+int64_t sdc_linear_check_workspace(int64_t m, int64_t k, int64_t n);
+int sdc_linear_check(int dtype, const void* x, int64_t sxm, const void* W, int64_t swn, const void* y, int64_t sym,
+                     const void* bias, int64_t m, int64_t k, int64_t n, const void* parts, int64_t spc,
+                     const float* block_consts, const float* sign_table, int64_t* state, int64_t* row_result,
+                     float z, float abs_floor, void* workspace, int64_t workspace_bytes, float* col_scores,
+                     float* row_scores, int flags, hipStream_t stream);
+
 /* ---- check of a MoE grouped GEMM ----------------------------------------------------------------------------
  * Replaces guard._grouped_checks (guard.py:102-143) + one checksum._zscores per group for torch._grouped_mm's
  * forward layout: out (rows x n) = A (rows x k, tokens sorted by expert) @ B[g] (k x n) for the rows of group g,

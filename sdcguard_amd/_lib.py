@@ -34,6 +34,9 @@ SIGNATURES = {
     "sdc_matmul_check": (I32, [I32, P, I64, I64, I64, I64, P, I64, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, I64,
                                I64, P, I32, I64, I64, I64, F32, F32, F32, F32, P, P, P, I64, P, P]),
     "sdc_expected_splits": (I64, [I64, I64, I64]),
+    "sdc_linear_check_workspace": (I64, [I64, I64, I64]),
+    "sdc_linear_check": (I32, [I32, P, I64, P, I64, P, I64, P, I64, I64, I64, P, I64, P, P, P, P, F32, F32, P, I64,
+                               P, P, I32, P]),
     "sdc_grouped_check_workspace": (I64, [I64, I64, I64, I64, I64]),
     "sdc_grouped_check": (I32, [I32, P, I64, I64, P, I64, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, P, P, I64,
                                 F32, F32, P, P, P, I64, P, P]),
@@ -118,3 +121,22 @@ def profile_read(name: str):
 
 def ptr(t) -> int:
     return 0 if t is None else t.data_ptr()
+
+
+_WS: dict = {}
+_WS_LOCK = threading.Lock()
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A device workspace of at least `nbytes`, kept per (device, current stream) and grown when a call needs more,
+    so steady-state calls allocate nothing (and a HIP-graph capture after a warm-up call reuses the same buffer).
+    Calls on one stream are ordered, so they may share it; another stream gets its own."""
+    dev = torch.device(device)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(),
+           torch.cuda.current_stream(dev).cuda_stream)
+    with _WS_LOCK:
+        buf = _WS.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
+            _WS[key] = buf
+        return buf

@@ -1,0 +1,573 @@
+// Both block checksums of one linear layer y = x @ W^T (+ b), with one pass over y.
+//
+// Column-block check (the serving check, serve.py:301-396 / _serve_fast.py:102-526): for every row i of y and
+// block of 128 output columns, sum_j y_ij against x_i . B2 (B2: the layer's block sums of W, three parts, made once
+// per layer), scored as the serving check scores it (unjudged checksums count, score 0).
+// Row-block check (the north star's row side; the column-block check of y^T = W x^T, checksum.py:435-530 on
+// transposed operands): for every column j and block of 128 rows, sum_i y_ij against W_j . (sum_i x_i), scored as
+// the training check scores it (unjudged checksums score -1).
+//
+// Four launches, no host synchronisation:
+//   1. xstage: the plain and signed sums of every 128-row block of x, split into three bf16 parts (the B operand
+//      of the row check's GEMM), and per 256-deep chunk partial statistics of those sums and of |x|;
+//   2. the row check's GEMM E_row = W @ (x block sums) on MFMA, plus W's row norms (expected_gemm.hip);
+//   3. the column check's GEMM E_col = x @ B2 on MFMA, plus x's row norms -- independent of 1 and 2, so it can
+//      run on a side stream concurrently with them;
+//   4. ypass: one read of y.  A workgroup owns a 128 x 128 tile (one row block by one column block): every thread
+//      reads 8 rows x 8 columns (eight 16-byte loads, all in flight), adds the four sums (plain, signed, squares,
+//      |values|) of its rows with packed dot products and those of its columns by pairing two rows' values of a
+//      column into one packed operand; the 16 lanes sharing the rows add theirs with DPP steps, the column partials
+//      go through LDS; then two waves score the tile's 128 (row, column block) pairs and two its 128 (column,
+//      row block) pairs, and the workgroup's worst keys go to the two result rows with one atomic maximum each.
+#include <algorithm>
+
+#include "blocksums.h"
+#include "gemm.h"
+#include "judge.h"
+#include "profile.h"
+#include "streams.h"
+
+extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
+int sdc_gemm_launch(int dtype, GemmArgs g, int64_t batches, hipStream_t stream);
+
+namespace {
+
+constexpr int BS = 128;            // block width of both checks
+constexpr int XK = 256;            // depth per xstage workgroup
+constexpr int NXS = 5;             // partial stats per (depth chunk, row block): sq0, sq1, max0, max1, max|x|
+
+__device__ __forceinline__ float nan_abs(float v) { return v == v ? fabsf(v) : __builtin_inff(); }
+
+__device__ __forceinline__ uint16_t bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// ---------------------------------------------------------------------------------------- 1. x block sums
+struct XStageArgs {
+  const uint16_t* x;
+  int64_t sxm, m, k, kp, mb, rem;
+  const float* s_full;             // sign pattern of a full row block (128), and of the last (rem) one
+  const float* s_last;
+  uint16_t* parts;                 // [3][2 mb][kp] bf16: hi, mid, lo of (plain, signed) per row block
+  float* stats;                    // [nkc][mb][NXS]
+};
+
+// One workgroup: one row block (128 rows) by 256 consecutive depths.  Thread t reads depths 8 (t % 32) .. +8 of
+// rows t / 32 + 8 i (i < 16): sixteen 16-byte loads, a wave covering two rows of 512 contiguous bytes each; LDS
+// adds the eight row groups; thread t then owns depth t: its two sums become three bf16 parts (checksum._split3),
+// stored k-contiguous per checksum column.
+__global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
+  __shared__ float red[2][8][XK + 4];
+  __shared__ float wst[4][NXS];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int dc = t & 31, rg = t >> 5;
+  const int64_t kc = blockIdx.x, ib = blockIdx.y;
+  const int64_t k0 = kc * XK + 8 * dc;
+  const int wid = (int)((ib == a.mb - 1 && a.rem > 0) ? a.rem : BS);
+  const float* sp = (ib == a.mb - 1 && a.rem > 0) ? a.s_last : a.s_full;
+  const uint16_t* base = a.x + (ib * BS) * a.sxm + k0;
+  float pl[8], sg[8], mx = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) pl[e] = sg[e] = 0.f;
+  if (k0 + 8 <= a.k) {
+    // a full block loads unconditionally (a guarded load would make the compiler wait for it inside the guard);
+    // rows past a narrower last block read row 0 of the block and are weighted 0
+    u32x4 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = rg + 8 * i;
+      v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + (r < wid ? r : 0) * a.sxm));
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = rg + 8 * i;
+      const float s = sp[r];                      // (0 past the pattern's width)
+      if (r >= wid) v[i] = u32x4{0u, 0u, 0u, 0u};
+      const float xv[8] = {bf16_lo(v[i].x), bf16_hi(v[i].x), bf16_lo(v[i].y), bf16_hi(v[i].y),
+                           bf16_lo(v[i].z), bf16_hi(v[i].z), bf16_lo(v[i].w), bf16_hi(v[i].w)};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pl[e] += xv[e];
+        sg[e] = fmaf(xv[e], s, sg[e]);
+        mx = fmaxf(mx, nan_abs(xv[e]));
+      }
+    }
+  } else if (k0 < a.k) {
+    const int ne = (int)(a.k - k0);
+#pragma unroll 1
+    for (int i = 0; i < 16; ++i) {
+      const int r = rg + 8 * i;
+      if (r >= wid) continue;
+      const float s = sp[r];
+      for (int e = 0; e < ne; ++e) {
+        const float xv = bf16_lo(base[r * a.sxm + e]);
+        pl[e] += xv;
+        sg[e] = fmaf(xv, s, sg[e]);
+        mx = fmaxf(mx, nan_abs(xv));
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    red[0][rg][8 * dc + e] = pl[e];
+    red[1][rg][8 * dc + e] = sg[e];
+  }
+#pragma unroll
+  for (int msk = 1; msk < 64; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+  __syncthreads();
+  float P = 0.f, S = 0.f;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    P += red[0][g][t];
+    S += red[1][g][t];
+  }
+  const int64_t kk = kc * XK + t;
+  const bool mine = kk < a.k;
+  if (kk < a.kp) {
+    // three parts of each sum (hi + mid + lo reproduces it to ~2^-27); depths past k are zero
+    const float v2[2] = {mine ? P : 0.f, mine ? S : 0.f};
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const uint16_t h = bf16_rne(v2[c]);
+      const float r1 = v2[c] - bf16_lo(h);
+      const uint16_t md = bf16_rne(r1);
+      const uint16_t lo = bf16_rne(r1 - bf16_lo(md));
+      const int64_t col = 2 * ib + c;
+      a.parts[(0 * 2 * a.mb + col) * a.kp + kk] = h;
+      a.parts[(1 * 2 * a.mb + col) * a.kp + kk] = md;
+      a.parts[(2 * 2 * a.mb + col) * a.kp + kk] = lo;
+    }
+  }
+  float st[4] = {mine ? P * P : 0.f, mine ? S * S : 0.f, mine ? nan_abs(P) : 0.f, mine ? nan_abs(S) : 0.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int msk = 1; msk < 64; msk <<= 1) {
+      const float o = __shfl_xor(st[i], msk, 64);
+      st[i] = i < 2 ? st[i] + o : fmaxf(st[i], o);
+    }
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wst[w][i] = st[i];
+    wst[w][4] = mx;
+  }
+  __syncthreads();
+  if (t < NXS) {
+    float v = wst[0][t];
+    for (int i = 1; i < 4; ++i) v = t < 2 ? v + wst[i][t] : fmaxf(v, wst[i][t]);
+    a.stats[(kc * a.mb + ib) * NXS + t] = v;
+  }
+}
+
+// --------------------------------------------------------------------------------------------- 4. the y pass
+struct YArgs {
+  const uint16_t* y;
+  int64_t sym, m, n, k, nb, mb, rem_n, rem_m;
+  const float* sign_table;         // 128 x 128, row w - 1 = the pattern of width w
+  // column-block check (serving flavour)
+  const float* Ecol;               // [scol][2 nb][m] (transposed planes)
+  const float* XN;                 // [scol][2][m]: |x_i|_2^2, |x_i|_1
+  int64_t scol;
+  const f32x4* consts;             // (nb, 12) packed per-block constants of the layer
+  int64_t* state;                  // int64[4]: key, key with noise, checks, unjudged
+  float* zcol;                     // (m, nb, 2) scores or null
+  // row-block check (training flavour)
+  const float* Erow;               // [srow][2 mb][n]
+  const float* WN;                 // [srow][2][n]
+  int64_t srow;
+  const float* xstats;             // [nkc][mb][NXS]
+  int64_t nkc;
+  const uint16_t* bias;            // (n) or null
+  int64_t* result;                 // int64[3]: key, key with noise, unjudged
+  float* zrow;                     // (n, mb, 2) scores or null
+  // constants of both noise models
+  float u, h, abs_floor, l1c, zt, lim_a, lim_big, capk;
+};
+
+template <int DT>
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_xor1(v);
+  v += dpp_xor2(v);
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // half mirror
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));  // row mirror
+  return v;
+}
+
+struct Best {
+  int64_t key = 0, keyd = 0;
+  int unk = 0;
+};
+
+__device__ __forceinline__ void keep_best(Best& b, float zc, bool sec, float dc, int64_t p) {
+  const int64_t zb = fbits64(fmaxf(zc, 0.f));
+  const int64_t k1 = (zb << 32) | ((p * 2 + (sec ? 1 : 0)) & 0xFFFFFFFFll);
+  const int64_t k2 = (zb << 32) | (fbits64(dc) & 0xFFFFFFFFll);
+  b.key = k1 > b.key ? k1 : b.key;
+  b.keyd = k2 > b.keyd ? k2 : b.keyd;
+}
+
+// Signs of a pattern as packed pairs of 16-bit +-1 (entries past the width read as +1: they only ever meet zeros)
+template <int DT>
+__device__ __forceinline__ uint32_t pack_signs(float s0, float s1) {
+  constexpr uint32_t ONE = DT == SDC_BF16 ? 0x3F80u : 0x3C00u;
+  return (ONE | ((__float_as_uint(s0) >> 16) & 0x8000u)) | ((ONE << 16) | (__float_as_uint(s1) & 0x80000000u));
+}
+
+
+// The tile of one workgroup: 128 rows (one row block) x 128 columns (one column block).  Thread t = 16 rg + cg owns
+// rows 8 rg .. 8 rg + 7 and columns 8 cg .. 8 cg + 7 (each load instruction of a wave reads 4 rows x 256
+// contiguous bytes).  Waves 0 and 1 score the tile's 128 column-block pairs (one row each), waves 2 and 3 its 128
+// row-block pairs (one column each); what that scoring needs is loaded at the start, so its latency passes under
+// the arithmetic.
+template <int DT>
+__global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
+  __shared__ f32x4 colp[BS][17];                // column partials [column][row group, rotated], padded
+  __shared__ f32x4 rows[BS];                    // the tile's row sums
+  __shared__ float rstat[NXS];                  // the row block's B-side statistics
+  __shared__ float xpart[256];
+  __shared__ float rsign;                       // the row block's pattern sum (for the bias)
+  __shared__ int64_t red_k[4], red_d[4];
+  __shared__ int red_u[4];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int rg = t >> 4, cg = t & 15;
+  const int jb = blockIdx.x, ib = blockIdx.y;
+  const int r0 = ib * BS, c0 = jb * BS;
+  const int wr = (int)((ib == a.mb - 1 && a.rem_m > 0) ? a.rem_m : BS);     // rows in this tile
+  const int wc = (int)((jb == a.nb - 1 && a.rem_n > 0) ? a.rem_n : BS);     // columns in this tile
+  const int m = (int)a.m, n = (int)a.n;
+
+  // ---- loads: y (eight 16-byte pieces, unconditional on a full tile), then what this lane's scoring needs
+  u32x4 v[8];
+  if (wr == BS && wc == BS) {
+    const uint16_t* p0 = a.y + (int64_t)(r0 + 8 * rg) * a.sym + c0 + 8 * cg;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p0 + i * a.sym));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 8 * rg + i;
+      v[i] = (r < wr && 8 * cg < wc)
+          ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.y + (int64_t)(r0 + r) * a.sym + c0 + 8 * cg))
+          : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  // waves 0, 1: column-block pair of row R; waves 2, 3: row-block pair of column J
+  const bool colside = w < 2;
+  const int R = r0 + 64 * w + lane, J = c0 + 64 * (w - 2) + lane;
+  const float* ebase;
+  const float* nbase;
+  int64_t estride, pstride, nstride, splits;
+  if (colside) {
+    const int Rc = R < m ? R : m - 1;
+    ebase = a.Ecol + (int64_t)(2 * jb) * a.m + Rc; estride = a.m; pstride = 2 * a.nb * a.m;
+    nbase = a.XN + Rc; nstride = a.m; splits = a.scol;
+  } else {
+    const int Jc = J < n ? J : n - 1;
+    ebase = a.Erow + (int64_t)(2 * ib) * a.n + Jc; estride = a.n; pstride = 2 * a.mb * a.n;
+    nbase = a.WN + Jc; nstride = a.n; splits = a.srow;
+  }
+  float ev[SDC_MAX_SPLITS][4];
+#pragma unroll
+  for (int s = 0; s < SDC_MAX_SPLITS; ++s) {
+    const int64_t sc = s < splits ? s : 0;
+    ev[s][0] = ebase[sc * pstride];
+    ev[s][1] = ebase[sc * pstride + estride];
+    ev[s][2] = nbase[sc * 2 * nstride];
+    ev[s][3] = nbase[sc * 2 * nstride + nstride];
+  }
+  const float bj = (!colside && a.bias) ? half_to_f32<DT>(a.bias[J < n ? J : n - 1]) : 0.f;
+
+  // the row block's statistics: the depth chunks' partials, loaded in parallel and added in LDS
+  const int nst = (int)a.nkc * NXS;
+  constexpr int XCH = 255;                     // partials per round: a multiple of NXS
+  for (int base = 0; base < nst; base += XCH) {
+    if (t < XCH && base + t < nst) {
+      const int i = base + t;
+      xpart[t] = a.xstats[((int64_t)(i / NXS) * a.mb + ib) * NXS + i % NXS];
+    }
+    __syncthreads();
+    if (t < NXS) {
+      float acc = base == 0 ? 0.f : rstat[t];        // (sums of squares, and maxima of values >= 0)
+      const int cnt = nst - base < XCH ? nst - base : XCH;
+      for (int j = t; j < cnt; j += NXS) acc = t < 2 ? acc + xpart[j] : fmaxf(acc, xpart[j]);
+      rstat[t] = acc;
+    }
+    __syncthreads();
+  }
+
+  // ---- signs: this thread's 8 columns of the column block's pattern, its 8 rows of the row block's pattern
+  const float* spc = a.sign_table + (wc - 1) * 128;
+  const float* spr = a.sign_table + (wr - 1) * 128;
+  uint32_t scol2[4], srow2[4];
+  {
+    const f32x4 ca = *reinterpret_cast<const f32x4*>(spc + 8 * cg);
+    const f32x4 cb = *reinterpret_cast<const f32x4*>(spc + 8 * cg + 4);
+    const f32x4 ra = *reinterpret_cast<const f32x4*>(spr + 8 * rg);
+    const f32x4 rb = *reinterpret_cast<const f32x4*>(spr + 8 * rg + 4);
+    scol2[0] = pack_signs<DT>(ca.x, ca.y); scol2[1] = pack_signs<DT>(ca.z, ca.w);
+    scol2[2] = pack_signs<DT>(cb.x, cb.y); scol2[3] = pack_signs<DT>(cb.z, cb.w);
+    srow2[0] = pack_signs<DT>(ra.x, ra.y); srow2[1] = pack_signs<DT>(ra.z, ra.w);
+    srow2[2] = pack_signs<DT>(rb.x, rb.y); srow2[3] = pack_signs<DT>(rb.z, rb.w);
+  }
+  if (w == 0) {
+    const float ss = wave_sum_f32(spr[lane] + spr[lane + 64]);
+    if (lane == 0) rsign = ss;
+  }
+  constexpr uint32_t ONES = DT == SDC_BF16 ? 0x3F803F80u : 0x3C003C00u;
+
+  // ---- row direction: four sums of each of the eight rows over this thread's eight columns
+  float rs[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t ww[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+    float pl = 0.f, sg = 0.f, sq = 0.f, ab = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      pl = dot2<DT>(ww[q], ONES, pl);
+      sg = dot2<DT>(ww[q], scol2[q], sg);
+      sq = dot2<DT>(ww[q], ww[q], sq);
+      ab = dot2<DT>(ww[q] & 0x7FFF7FFFu, ONES, ab);
+    }
+    rs[i][0] = pl; rs[i][1] = sg; rs[i][2] = sq; rs[i][3] = ab;
+  }
+  // ---- column direction: two rows' values of one column packed into one operand
+  float cs[8][4];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) cs[e][0] = cs[e][1] = cs[e][2] = cs[e][3] = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) {
+    const uint32_t w0[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+    const uint32_t w1[4] = {v[i + 1].x, v[i + 1].y, v[i + 1].z, v[i + 1].w};
+    const uint32_t sr = srow2[i / 2];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t plo = __builtin_amdgcn_perm(w1[q], w0[q], 0x05040100u);     // column 2q of rows i, i + 1
+      const uint32_t phi = __builtin_amdgcn_perm(w1[q], w0[q], 0x07060302u);     // column 2q + 1
+      cs[2 * q][0] = dot2<DT>(plo, ONES, cs[2 * q][0]);
+      cs[2 * q][1] = dot2<DT>(plo, sr, cs[2 * q][1]);
+      cs[2 * q][2] = dot2<DT>(plo, plo, cs[2 * q][2]);
+      cs[2 * q][3] = dot2<DT>(plo & 0x7FFF7FFFu, ONES, cs[2 * q][3]);
+      cs[2 * q + 1][0] = dot2<DT>(phi, ONES, cs[2 * q + 1][0]);
+      cs[2 * q + 1][1] = dot2<DT>(phi, sr, cs[2 * q + 1][1]);
+      cs[2 * q + 1][2] = dot2<DT>(phi, phi, cs[2 * q + 1][2]);
+      cs[2 * q + 1][3] = dot2<DT>(phi & 0x7FFF7FFFu, ONES, cs[2 * q + 1][3]);
+    }
+  }
+  // column partials into LDS, the row-group slot rotated by the column group so the eight lanes of a write phase
+  // (columns 8 apart) fall in different banks; the reader adds all 16 slots
+#pragma unroll
+  for (int e = 0; e < 8; ++e) colp[8 * cg + e][(rg + cg) & 15] = f32x4{cs[e][0], cs[e][1], cs[e][2], cs[e][3]};
+  // the 16 lanes of a row group add their row sums; lane cg < 8 keeps row 8 rg + cg
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    f32x4 r;
+    r.x = row16_sum<DT>(rs[i][0]);
+    r.y = row16_sum<DT>(rs[i][1]);
+    r.z = row16_sum<DT>(rs[i][2]);
+    r.w = row16_sum<DT>(rs[i][3]);
+    if (cg == i) rows[8 * rg + i] = r;
+  }
+  __syncthreads();
+
+  // ---- scoring
+  float e0 = ev[0][0], e1 = ev[0][1], asq = ev[0][2], asum = ev[0][3];
+#pragma unroll
+  for (int s = 1; s < SDC_MAX_SPLITS; ++s)
+    if (s < splits) {
+      e0 += ev[s][0];
+      e1 += ev[s][1];
+      asq += ev[s][2];
+      asum += ev[s][3];
+    }
+  Best best;
+  if (colside) {
+    // column-block check of row R, block jb (serving flavour)
+    const int rr = 64 * w + lane;
+    if (rr < wr) {
+      const f32x4 s4 = rows[rr];
+      const f32x4 q0 = a.consts[3 * jb], q1 = a.consts[3 * jb + 1], q2 = a.consts[3 * jb + 2];
+      const PairScore ps = judge_serve(s4.x, s4.y, s4.z, s4.w, fsqrt(asq), asum, e0, e1, q0.x, q0.y, q0.z, q0.w,
+                                       q2.x, q2.y, q1.x, q1.y, q1.z, q1.w, (float)wc, a);
+      const int64_t p = (int64_t)R * a.nb + jb;
+      if (a.zcol) {
+        a.zcol[2 * p] = ps.z0;
+        a.zcol[2 * p + 1] = ps.z1;
+      }
+      keep_best(best, ps.zc, ps.sec, ps.dc, p);
+      best.unk += ps.unk;
+    }
+  } else {
+    // row-block check of column J, row block ib (training flavour, y^T = W x^T + b)
+    const int cc = 64 * (w - 2) + lane;
+    if (cc < wc) {
+      float pl = 0.f, sg = 0.f, sq = 0.f, ab = 0.f;
+#pragma unroll
+      for (int g = 0; g < 16; ++g) {
+        const f32x4 q = colp[cc][g];
+        pl += q.x; sg += q.y; sq += q.z; ab += q.w;
+      }
+      const float wf = (float)wr;
+      float bound = asum * rstat[4];
+      if (a.bias) {
+        // a bias constant along the block: w copies of b_j, whose sums w b_j and (sum of signs) b_j are exact
+        e0 = e0 + bj * wf;
+        e1 = e1 + bj * rsign;
+        bound = bound + nan_abs(bj);
+      }
+      const float cn = fsqrt(sq), noise = cn * a.u, xn = fsqrt(asq);
+      const float inf = __builtin_inff();
+      const float nrm[2] = {fsqrt(rstat[0]), fsqrt(rstat[1])};
+      float fl[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const float f_l2 = (xn * nrm[c]) * 1e-5f;
+        const float f_l1 = (asum * rstat[2 + c]) * a.l1c;
+        const float f = fminf(fabsf(f_l2) < inf ? f_l2 : inf, fabsf(f_l1) < inf ? f_l1 : inf);
+        fl[c] = f < inf ? f : bound * (float)(1e-5 * 128.0);
+      }
+      float d0, d1;
+      const float z0 = judge_one(e0, pl, noise, cn, fl[0], bound, wf, ab, true, a, d0);
+      const float z1 = judge_one(e1, sg, noise, cn, fl[1], bound, wf, ab, false, a, d1);
+      const int64_t p = (int64_t)J * a.mb + ib;
+      if (a.zrow) {
+        a.zrow[2 * p] = z0;
+        a.zrow[2 * p + 1] = z1;
+      }
+      best.unk += (z0 < 0.f) + (z1 < 0.f);
+      const bool sec = z1 > z0;
+      keep_best(best, sec ? z1 : z0, sec, sec ? d1 : d0, p);
+    }
+  }
+  const int64_t key = wave_max_i64(best.key), keyd = wave_max_i64(best.keyd);
+  const int unk = wave_sum_i32(best.unk);
+  if (lane == 0) {
+    red_k[w] = key;
+    red_d[w] = keyd;
+    red_u[w] = unk;
+  }
+  __syncthreads();
+  if (t == 0 || t == 64) {
+    // thread 0: the column check (waves 0, 1); thread 64: the row check (waves 2, 3)
+    const int w0 = t == 0 ? 0 : 2;
+    const int64_t k0 = red_k[w0] > red_k[w0 + 1] ? red_k[w0] : red_k[w0 + 1];
+    const int64_t d0 = red_d[w0] > red_d[w0 + 1] ? red_d[w0] : red_d[w0 + 1];
+    const int un = red_u[w0] + red_u[w0 + 1];
+    int64_t* res = t == 0 ? a.state : a.result;
+    if (k0 > __atomic_load_n(res, __ATOMIC_RELAXED)) atomicMax((unsigned long long*)res, (unsigned long long)k0);
+    if (d0 > __atomic_load_n(res + 1, __ATOMIC_RELAXED))
+      atomicMax((unsigned long long*)(res + 1), (unsigned long long)d0);
+    if (t == 0) {
+      if (blockIdx.x == 0 && blockIdx.y == 0) atomicAdd((unsigned long long*)(res + 2), 1ull);
+      if (un > 0) atomicAdd((unsigned long long*)(res + 3), (unsigned long long)un);
+    } else if (un > 0) {
+      atomicAdd((unsigned long long*)(res + 2), (unsigned long long)un);
+    }
+  }
+}
+
+struct Layout {
+  int64_t nb, mb, rem_n, rem_m, nkc, kp, scol, srow;
+  int64_t off_parts, off_stats, off_erow, off_wn, off_ecol, off_xn, total;   // in floats
+};
+
+Layout layout(int64_t m, int64_t k, int64_t n) {
+  Layout L{};
+  L.nb = sdc_cdiv(n, BS);
+  L.mb = sdc_cdiv(m, BS);
+  L.rem_n = n % BS;
+  L.rem_m = m % BS;
+  L.nkc = sdc_cdiv(k, XK);
+  L.kp = (k + 7) / 8 * 8;
+  L.scol = sdc_expected_splits(m, k, 2 * L.nb);
+  L.srow = sdc_expected_splits(n, k, 2 * L.mb);
+  auto al = [](int64_t x) { return (x + 63) / 64 * 64; };
+  int64_t o = 0;
+  L.off_parts = o; o += al((3 * 2 * L.mb * L.kp + 1) / 2);
+  L.off_stats = o; o += al(L.nkc * L.mb * NXS);
+  L.off_erow = o; o += al(L.srow * 2 * L.mb * n);
+  L.off_wn = o; o += al(L.srow * 2 * n);
+  L.off_ecol = o; o += al(L.scol * 2 * L.nb * m);
+  L.off_xn = o; o += al(L.scol * 2 * m);
+  L.total = o;
+  return L;
+}
+
+}  // namespace
+
+extern "C" int64_t sdc_linear_check_workspace(int64_t m, int64_t k, int64_t n) {
+  if (m <= 0 || k <= 0 || n <= 0) return 0;
+  return layout(m, k, n).total * (int64_t)sizeof(float) + 256;
+}
+
+extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const void* W, int64_t swn, const void* y,
+                                int64_t sym, const void* bias, int64_t m, int64_t k, int64_t n, const void* parts,
+                                int64_t spc, const float* block_consts, const float* sign_table, int64_t* state,
+                                int64_t* row_result, float z, float abs_floor, void* workspace,
+                                int64_t workspace_bytes, float* col_scores, float* row_scores, int flags,
+                                hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
+  if (m < 1 || n < 1 || k < 1) return SDC_EINVAL;
+  if (dtype != SDC_BF16) return SDC_EUNSUPPORTED;               // (fp16: the separate checks)
+  if (!x || !W || !y || !parts || !block_consts || !sign_table || !state || !row_result) return SDC_EINVAL;
+  if (n % 8 || sym % 8 || sxm % 8 || ((uintptr_t)y | (uintptr_t)x | (uintptr_t)block_consts) % 16)
+    return SDC_EUNSUPPORTED;                                    // x and y are read in 16-byte pieces
+  const Layout L = layout(m, k, n);
+  if (m * L.nb * 2 > 0xFFFFFFFFll || n * L.mb * 2 > 0xFFFFFFFFll) return SDC_EUNSUPPORTED;
+  if (!workspace || workspace_bytes < L.total * (int64_t)sizeof(float) + 256) return SDC_EWORKSPACE;
+  float* ws = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  const float* s_full = sign_table + (BS - 1) * 128;
+  const bool concurrent = (flags & 1) != 0;
+
+  // 3. (side stream when asked) the column check's GEMM: E_col = x @ B2 parts, x's row norms
+  hipStream_t side = stream;
+  if (concurrent && !(side = sdc_fork(stream))) return SDC_ELAUNCH;
+  GemmArgs gc{};
+  gc.A = (const uint16_t*)x; gc.sab = 0; gc.sam = sxm; gc.sak = 1;
+  gc.B = parts; gc.sbb = 0; gc.sbc = spc;
+  gc.m = m; gc.k = k; gc.N = 2 * L.nb; gc.splits = L.scol;
+  gc.E = ws + L.off_ecol; gc.XN = ws + L.off_xn; gc.et = 1;
+  gc.prof_name = "col_gemm";
+  int rc = sdc_gemm_launch(SDC_BF16, gc, 1, side);
+  if (rc != SDC_OK) return rc;
+
+  // 1. the block sums of x (as three parts) and their statistics
+  XStageArgs xa{};
+  xa.x = (const uint16_t*)x; xa.sxm = sxm; xa.m = m; xa.k = k; xa.kp = L.kp; xa.mb = L.mb; xa.rem = L.rem_m;
+  xa.s_full = s_full; xa.s_last = L.rem_m ? sign_table + (L.rem_m - 1) * 128 : s_full;
+  xa.parts = (uint16_t*)(ws + L.off_parts); xa.stats = ws + L.off_stats;
+  {
+    SdcProf prof("xstage", stream);
+    hipLaunchKernelGGL(xstage_kernel, dim3((unsigned)L.nkc, (unsigned)L.mb), dim3(256), 0, stream, xa);
+    SDC_LAUNCH_CHECK();
+  }
+  // 2. the row check's GEMM: E_row = W @ (x block sums), W's row norms
+  GemmArgs gr{};
+  gr.A = (const uint16_t*)W; gr.sab = 0; gr.sam = swn; gr.sak = 1;
+  gr.B = ws + L.off_parts; gr.sbb = 0; gr.sbc = L.kp;
+  gr.m = n; gr.k = k; gr.N = 2 * L.mb; gr.splits = L.srow;
+  gr.E = ws + L.off_erow; gr.XN = ws + L.off_wn; gr.et = 1;
+  gr.prof_name = "row_gemm";
+  rc = sdc_gemm_launch(SDC_BF16, gr, 1, stream);
+  if (rc != SDC_OK) return rc;
+  if (concurrent && (rc = sdc_join(stream, side)) != SDC_OK) return rc;
+
+  // 4. one pass over y: both checks
+  YArgs ya{};
+  ya.y = (const uint16_t*)y; ya.sym = sym; ya.m = m; ya.n = n; ya.k = k; ya.nb = L.nb; ya.mb = L.mb;
+  ya.rem_n = L.rem_n; ya.rem_m = L.rem_m; ya.sign_table = sign_table;
+  ya.Ecol = ws + L.off_ecol; ya.XN = ws + L.off_xn; ya.scol = L.scol; ya.consts = (const f32x4*)block_consts;
+  ya.state = state; ya.zcol = col_scores;
+  ya.Erow = ws + L.off_erow; ya.WN = ws + L.off_wn; ya.srow = gr.splits; ya.xstats = ws + L.off_stats;
+  ya.nkc = L.nkc; ya.bias = (const uint16_t*)bias; ya.result = row_result; ya.zrow = row_scores;
+  ya.u = 1.f / 256.f; ya.h = 0.f; ya.abs_floor = abs_floor;
+  ya.l1c = (float)(k * 7.450580596923828e-09 > 1e-5 ? k * 7.450580596923828e-09 : 1e-5);   // checksum.py:95-104
+  ya.zt = z; ya.lim_a = 1e18f; ya.lim_big = 1e18f;
+  ya.capk = (float)(1.02 + (double)k * 2.384185791015625e-07);
+  SdcProf prof("ypass", stream);
+  hipLaunchKernelGGL(ypass_kernel<SDC_BF16>, dim3((unsigned)L.nb, (unsigned)L.mb), dim3(256), 0, stream, ya);
+  SDC_LAUNCH_CHECK();
+  return SDC_OK;
+}

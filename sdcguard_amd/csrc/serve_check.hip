@@ -10,6 +10,7 @@
 //      sums, then scores it with the reference's noise model.  The workgroup's worst key goes into the layer's
 //      state row with one integer atomic maximum (only when it raises the row), counts with atomic adds.
 #include "blocksums.h"
+#include "judge.h"
 #include "profile.h"
 #include "streams.h"
 
@@ -36,80 +37,6 @@ struct ScoreArgs {
   float* zdump;      // optional: every checksum's score, (m, nb, 2) fp32 (tests)
   const f32x4* packed;   // optional: the per-block constants as 3 float4 per block (see sdc_check_static)
 };
-
-struct PairScore {
-  float z0, z1;
-  float zc, dc;
-  bool sec;
-  int unk;
-};
-
-// _serve_fast.py:334-402 (`_judge`) for one (row, block) pair, serving flavour (unjudged checksums score 0).
-__device__ __forceinline__ PairScore judge_serve(float plain, float sgn, float sq, float l1, float xn, float asum,
-                                                 float e0, float e1, float sc0, float sc1, float bs0, float bs1,
-                                                 float bmaxv, float bmbv, float b2n0, float b2n1, float b2m0,
-                                                 float b2m1, float wf, const ScoreArgs& a) {
-  const float inf = __builtin_inff();
-  const float nanv = __builtin_nanf("");
-  float exp0 = e0 * sc0 + bs0;
-  float exp1 = e1 * sc1 + bs1;
-  float bound = asum * bmaxv + bmbv;
-  float rsq = fsqrt(sq);
-  float noise = rsq * a.u;
-  float fl0 = xn * b2n0 * 1e-5f;
-  float fl1 = xn * b2n1 * 1e-5f;
-  float hl0 = asum * b2m0 * a.l1c;
-  float hl1 = asum * b2m1 * a.l1c;
-  fl0 = fminf(fabsf(fl0) < inf ? fl0 : inf, fabsf(hl0) < inf ? hl0 : inf);
-  fl1 = fminf(fabsf(fl1) < inf ? fl1 : inf, fabsf(hl1) < inf ? hl1 : inf);
-  const float bigfl = bound * (float)(1e-5 * 128.0);
-  fl0 = fl0 < inf ? fl0 : bigfl;
-  fl1 = fl1 < inf ? fl1 : bigfl;
-  float swf = fsqrt(wf);
-  float tail = a.abs_floor + swf * a.h;
-  float den0 = (noise + fl0) + tail;
-  float den1 = (noise + fl1) + tail;
-  float d0 = fabsf(exp0 - plain);
-  float d1 = fabsf(exp1 - sgn);
-  float z0 = fdiv(d0, den0);
-  float z1 = fdiv(d1, den1);
-  float worst = (l1 * (1.25f * a.u) + (1.25f * a.h * wf)) + fl0 + a.abs_floor;
-  float zw = fdiv(d0, worst) * a.zt;
-  z0 = (z0 == z0 && zw == zw) ? fminf(z0, zw) : nanv;
-  float lim = bound * 1.01f;
-  bool nfin = !(noise < inf);
-  bool e_bad0 = !(fabsf(exp0) < inf);
-  bool a_bad0 = !e_bad0 && !(fabsf(plain) < inf);
-  bool big0 = nfin && !e_bad0 && !a_bad0;
-  bool nan0 = !(z0 == z0);
-  z0 = z0 == z0 ? z0 : 0.f;
-  z0 = e_bad0 ? 0.f : z0;
-  float cap = bound * a.capk + 2.0f * a.h;
-  bool imposs = !nfin && (lim < a.lim_big) && (rsq > cap * swf);
-  bool ok_a = lim < a.lim_a, ok_big = lim < a.lim_big;
-  z0 = (imposs && !e_bad0 && !a_bad0) ? inf : z0;
-  z0 = a_bad0 ? (ok_a ? inf : 0.f) : z0;
-  z0 = big0 ? (ok_big ? inf : 0.f) : z0;
-  bool e_bad1 = !(fabsf(exp1) < inf);
-  bool a_bad1 = !e_bad1 && !(fabsf(sgn) < inf);
-  bool big1 = nfin && !e_bad1 && !a_bad1;
-  bool nan1 = !(z1 == z1);
-  z1 = z1 == z1 ? z1 : 0.f;
-  z1 = e_bad1 ? 0.f : z1;
-  z1 = (imposs && !e_bad1 && !a_bad1) ? inf : z1;
-  z1 = a_bad1 ? (ok_a ? inf : 0.f) : z1;
-  z1 = big1 ? (ok_big ? inf : 0.f) : z1;
-  bool unk0 = (nan0 && !imposs && !a_bad0 && !big0) || e_bad0 || (a_bad0 && !ok_a) || (big0 && !ok_big);
-  bool unk1 = (nan1 && !imposs && !a_bad1 && !big1) || e_bad1 || (a_bad1 && !ok_a) || (big1 && !ok_big);
-  PairScore r;
-  r.z0 = z0;
-  r.z1 = z1;
-  r.sec = z1 > z0;
-  r.zc = r.sec ? z1 : z0;
-  r.dc = r.sec ? (a_bad1 ? nanv : den1) : (a_bad0 ? nanv : den0);
-  r.unk = (int)unk0 + (int)unk1;
-  return r;
-}
 
 // Scores this lane's pairs (NP of them: p0, p0 + 256, ...; those >= npairs are skipped) from their four sums, then
 // the workgroup's worst key into the layer's state row (one atomic maximum, only when it raises the row), the

@@ -12,6 +12,7 @@
 //   4. train_score: one persistent pass over C scoring every (batch, row, block) pair, worst key and unjudged count
 //      into the check's result row with atomics.
 #include "blocksums.h"
+#include "judge.h"
 #include "gemm.h"
 #include "profile.h"
 
@@ -303,33 +304,6 @@ struct TrainBest {
   int64_t key = 0, keyd = 0;
   int unk = 0;
 };
-
-// one checksum of checksum._zscores + _judge_nonfinite (unjudged = -1)
-__device__ __forceinline__ float judge_one(float expected, float actual, float noise, float cn, float fl, float bound,
-                                           float wf, float l1, bool plain, const TrainArgs& a, float& den) {
-  const float inf = __builtin_inff();
-  const float swf = fsqrt(wf);
-  den = (noise + fl) + (a.abs_floor + swf * a.h);
-  const float diff = fabsf(expected - actual);
-  float z = fdiv(diff, den);
-  if (plain) {
-    const float worst = ((l1 * (1.25f * a.u) + 1.25f * wf * a.h) + fl) + a.abs_floor;
-    const float zw = fdiv(diff, worst) * a.zt;
-    z = (z == z && zw == zw) ? fminf(z, zw) : __builtin_nanf("");
-  }
-  const bool e_bad = !(fabsf(expected) < inf);
-  const bool a_bad = !(fabsf(actual) < inf) && !e_bad;
-  const bool big = !(noise < inf) && !e_bad && !a_bad;
-  const float lim = bound * 1.01f;
-  z = z == z ? z : -1.f;
-  z = e_bad ? -1.f : z;
-  const float cap = bound * a.capk + 2.f * a.h;
-  const bool imposs = !e_bad && !a_bad && !big && (lim < 1e18f) && (cn > cap * swf);
-  z = imposs ? inf : z;
-  z = a_bad ? (lim < a.lim_a ? inf : -1.f) : z;
-  z = big ? (lim < 1e18f ? inf : -1.f) : z;
-  return z;
-}
 
 template <int DT>
 __device__ __forceinline__ void train_pair(const TrainArgs& a, int64_t p, float pl, float sg, float sq, float l1,

@@ -1,0 +1,137 @@
+"""Both block checksums of a linear layer from one pass over y (sdc_linear_check, through the C ABI).
+
+Every checksum's score is compared with the oracle's (the serving check for the column blocks, the training check
+of y^T = W x^T + b[:, None] for the row blocks; tolerance of tests/test_oracle_golden.py) and with the two separate
+entry points (sdc_check_static, sdc_matmul_check on the transposed views); counts exactly; the located fault
+exactly.  At the full 4096 x 4096 x 14336 layer, single-bit flips of y: the verdicts of both checks agree with the
+separate checks' on every flip outside the band |z - 6| < 0.3, and the band count is reported."""
+from __future__ import annotations
+
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import abft, serve_check
+from tests.test_oracle_golden import gemm_slack, z_close
+
+pytestmark = pytest.mark.gpu
+
+
+def make(m, k, n, with_bias, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(m, k, device="cuda", generator=g).bfloat16()
+    W = (torch.randn(n, k, device="cuda", generator=g) * 0.02).bfloat16()
+    b = (torch.randn(n, device="cuda", generator=g) * 0.1).bfloat16() if with_bias else None
+    y = torch.nn.functional.linear(x.float(), W.float(), None if b is None else b.float()).bfloat16()
+    return x, W, b, y
+
+
+def fused(x, W, b, y, cs, concurrent=True):
+    from sdcguard_amd.linear import check_linear_both
+    m, n = y.shape
+    mb, nb = -(-m // 128), -(-n // 128)
+    zc = torch.full((m, nb, 2), -7.0, device="cuda")
+    zr = torch.full((n, mb, 2), -7.0, device="cuda")
+    st, rr = check_linear_both(x, W, b, y, cs, col_scores=zc, row_scores=zr, concurrent=concurrent)
+    torch.cuda.synchronize()
+    return zc.cpu().numpy(), zr.cpu().numpy(), st.cpu().numpy(), rr.cpu().numpy()
+
+
+def separate(x, W, b, y, cs):
+    from sdcguard_amd.checksum import linear_rows_operands, matmul_zscores
+    from sdcguard_amd.serve import STATE_COLS, check_static_impl
+    m, n = y.shape
+    mb, nb = -(-m // 128), -(-n // 128)
+    zc = torch.full((m, nb, 2), -7.0, device="cuda")
+    zr = torch.full((1, n, mb, 2), -7.0, device="cuda")
+    st = torch.zeros(1, STATE_COLS, dtype=torch.int64, device="cuda")
+    check_static_impl(x, y, *cs.tensors(True), st, 0, 6.0, 1e-20, scores_out=zc)
+    rr = torch.zeros(3, dtype=torch.int64, device="cuda")
+    matmul_zscores(*linear_rows_operands(x, W, b, y), out=rr, scores_out=zr)
+    torch.cuda.synchronize()
+    return zc.cpu().numpy(), zr.cpu().numpy()[0], st.cpu().numpy()[0], rr.cpu().numpy()
+
+
+def zmax(key) -> float:
+    return float(np.array([int(key) >> 32], np.uint32).view(np.float32)[0])
+
+
+SHAPES = [(512, 640, 1000, True), (300, 256, 136, False), (129, 1032, 264, True), (1024, 4096, 1408, True),
+          (256, 4104, 512, False), (100, 1030, 264, True)]        # (the last: x rows not 16-byte aligned)
+
+
+@pytest.mark.parametrize("m,k,n,with_bias", SHAPES)
+@pytest.mark.parametrize("concurrent", [True, False])
+def test_both_checks_match_the_oracle_and_the_separate_checks(m, k, n, with_bias, concurrent):
+    from sdcguard_amd.checksum import linear_rows_operands
+    from sdcguard_amd.serve import LayerChecksums
+    x, W, b, y = make(m, k, n, with_bias, seed=m + k + n)
+    y[m // 3, n // 2] = y[m // 3, n // 2].float() * 64 + 8                 # one corrupted element
+    cs = LayerChecksums(W, b, 128)
+    zc, zr, st, rr = fused(x, W, b, y, cs, concurrent)
+    zc2, zr2, st2, rr2 = separate(x, W, b, y, cs)
+    # against the two separate entry points: the same scores (only the order of fp32 additions differs)
+    assert z_close(zc.reshape(-1), zc2.reshape(-1)).all()
+    assert z_close(zr.reshape(-1), zr2.reshape(-1)).all()
+    assert st[2] == 1 and st[3] == st2[3] and rr[2] == rr2[2]
+    # against the oracle
+    f = lambda t: t.float().cpu().numpy()                                    # noqa: E731
+    c = serve_check.layer_constants(f(W), None if b is None else f(b), 128, "bf16", seed=1)
+    o = serve_check.check_static(f(x), f(y), c, dtype="bf16", seed=1)
+    ok = z_close(zc.reshape(-1), o.z.reshape(-1), gemm_slack(o.csb, o.den).reshape(-1))
+    assert ok.all(), (np.nonzero(~ok)[0][:5], zc.reshape(-1)[~ok][:5], o.z.reshape(-1)[~ok][:5])
+    A, B, C, bias = linear_rows_operands(x, W, b, y)
+    orow = abft.zscores(f(A), f(B), f(C), None if bias is None else f(bias), dtype="bf16", seed=1)
+    ok = z_close(zr.reshape(-1), orow.z.reshape(-1), gemm_slack(orow.csb, orow.den).reshape(-1))
+    assert ok.all(), (np.nonzero(~ok)[0][:5], zr.reshape(-1)[~ok][:5], orow.z.reshape(-1)[~ok][:5])
+    # the fault, located by both checks as the separate checks and the oracle locate it
+    fc, fr = int(st[0]) & 0xFFFFFFFF, int(rr[0]) & 0xFFFFFFFF
+    nb, mb = -(-n // 128), -(-m // 128)
+    assert zmax(st[0]) > 6 and (fc // 2) == (m // 3) * nb + (n // 2) // 128
+    assert zmax(rr[0]) > 6 and (fr // 2) == (n // 2) * mb + (m // 3) // 128
+    assert (fc // 2, fr // 2) == ((int(st2[0]) & 0xFFFFFFFF) // 2, (int(rr2[0]) & 0xFFFFFFFF) // 2)
+    dz = max(float(np.nanmax(np.abs(np.where(np.isfinite(zc2), zc - zc2, 0)))),
+             float(np.nanmax(np.abs(np.where(np.isfinite(zr2), zr - zr2, 0)))))
+    print(f"{m}x{k}x{n}: max |dz| against the separate checks {dz:.2e}")
+
+
+def _flip(y: torch.Tensor, flat: int, bit: int) -> None:
+    v = y.view(-1)[flat:flat + 1].view(torch.int16)
+    y.view(-1)[flat] = (v ^ (1 << bit)).view(torch.bfloat16)[0]
+
+
+def test_full_size_layer_single_bit_flips():
+    """x 4096x4096 N(0,1), W 14336x4096 N(0,0.02), y = x W^T in bf16: clean, then 16 trials each flipping one random
+    bit (exponent or mantissa) of one random element of y.  Both verdicts agree with the separate checks outside the
+    band |z - 6| < 0.3; a flagged flip is located at the same place."""
+    from sdcguard_amd.serve import LayerChecksums
+    x, W, b, y = make(4096, 4096, 14336, False, seed=3)
+    cs = LayerChecksums(W, None, 128)
+    zc, zr, st, rr = fused(x, W, None, y, cs)
+    assert zmax(st[0]) < 6 and zmax(rr[0]) < 6, (zmax(st[0]), zmax(rr[0]))
+    rng = random.Random(11)
+    band = agree = flagged = 0
+    worst_dz = 0.0
+    for trial in range(16):
+        i, j, bit = rng.randrange(4096), rng.randrange(14336), rng.randrange(0, 15)
+        y2 = y.clone()
+        _flip(y2, i * 14336 + j, bit)
+        zc, zr, st, rr = fused(x, W, None, y2, cs)
+        zc2, zr2, st2, rr2 = separate(x, W, None, y2, cs)
+        worst_dz = max(worst_dz, float(np.abs(zc[i, j // 128] - zc2[i, j // 128]).max()),
+                       float(np.abs(zr[j, i // 128] - zr2[j, i // 128]).max()))
+        for got, want, loc in ((st, st2, (i * 112 + j // 128)), (rr, rr2, (j * 32 + i // 128))):
+            zg, zw = zmax(got[0]), zmax(want[0])
+            if abs(zw - 6.0) < 0.3 or abs(zg - 6.0) < 0.3:
+                band += 1
+                continue
+            assert (zg > 6) == (zw > 6), (trial, bit, zg, zw)
+            agree += 1
+            if zg > 6:
+                flagged += 1
+                assert (int(got[0]) & 0xFFFFFFFF) // 2 == loc, (trial, bit)
+    print(f"16 single-bit flips x 2 checks: {agree} verdicts agree, {band} in the band, {flagged} flagged; "
+          f"max |dz| at the flipped blocks {worst_dz:.2e}")
+    assert band <= 2
