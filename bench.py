@@ -1,35 +1,50 @@
-"""Benchmark of the verification hot path on one MI355X: both checksums of a bf16 Llama-MLP-shaped linear layer
-(x: 4096 tokens x 4096, W: 14336 x 4096, y = x @ W^T in bf16 with fp32 accumulation).
+"""Benchmark of the verification hot path on one MI355X.
 
-A step checks that layer's output once with both identities:
-  column-block  every (token row, block of 128 output columns), plain and signed: the serving check
-                (sdc_check_static: expected side x @ parts on MFMA, one pass over y that sums and scores);
-  row-block     every (output column, block of 128 token rows), plain and signed: the column-block check of
-                y^T = W x^T (sdc_matmul_check on transposed views: block sums of x, W @ those sums on MFMA, one
-                pass over y reading down its columns).
-Inputs are resident in HBM; the timed loop rotates over enough copies of (x, y) that a step's reads of x and y miss
-the 256 MB Infinity Cache (W, 117 MB, is one tensor, as served).  Reported:
-  value         algorithmic bytes of one step (x + y + the layer's parts + W: what both checks must read at least)
-                / time per step, GB/s
-  roofline      the kernel with the largest share of the step, against its bound, from HIP events recorded on its
-                launch stream; traffic from the committed rocprofv3 counter summary
-  overhead      step time / the guarded GEMM's time on the same GPU and stream, warm (the check right after its
-                GEMM, as served) and cold
-  cpu_baseline  the oracle's serving check (numpy, 1 thread) on a bounded sample of the same workload
+The headline line (the one JSON line printed) is the bf16 Llama-MLP-shaped linear layer checked with both block
+checksums:  x 4096 tokens x 4096, W 14336 x 4096, y = x W^T in bf16 with fp32 accumulation.  A step is one
+sdc_linear_check call (column-block check against the layer's precomputed block sums, row-block check of
+y^T = W x^T, one pass over y for both).  Inputs are resident in HBM; the timed loop rotates over enough copies of
+(x, y) that a step's reads of them miss the 256 MB Infinity Cache (W, 117 MB, is one tensor, as served).
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+  value         algorithmic bytes of one step / time per step, GB/s: x + y + W + the layer's block-sum parts
+                (33.55 + 117.44 + 117.44 + 5.51 = 273.94 MB), what the two checks must read at least
+  roofline      the kernel with the largest share of the step, against its bound: algorithmic bytes (or MFMA
+                flops) per launch / its average launch time from HIP events recorded on its launch stream;
+                traffic = HBM bytes per launch from the committed rocprofv3 counter summary of the same workload
+  overhead      the check after its GEMM (warm: x and y still in the caches, as served) and alone (cold), against
+                the guarded GEMM's time on the same GPU and stream
+  cpu_baseline  the torch restatement of the check (both block checks, fp32 on every host core) on the same
+                workload at full size, median of >= 5 runs
+
+"more" holds one line per other workload, each with its own value, roofline and cpu_baseline:
+  fp8_mlp_4096x4096x14336   fp8 e4m3 linear layer with per-token / per-channel scales, bf16 output, column check
+  int8_2048x7168x4096       int8 W8A8 GEMM, exact int32 check
+  fp8_2048x7168x4096        fp8 e4m3 GEMM with scales 10^U(-3,-1), bf16 output
+  moe_4096x8of64_2048x1408  MoE grouped GEMM: 4096 tokens, top-8 of 64 experts (Zipf 1.1), bf16
+  kv_fingerprint_28x4096    fingerprints of every block of a 28-layer x 4096-block paged KV cache (7.52 GB)
+  attn_recompute_28x64      sampled attention recompute: one decode step of 64 sequences over 28 layers, 16
+                            sampled (row, head) pairs a layer
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--only NAME] [--no-cpu]
+    python bench.py --summarize DIR [DIR ...]     # rocprofv3 csv output -> the text summary kept in profiles/
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import platform
+import re
+import statistics
 import sys
 import time
 
 HBM_PEAK_GBS = 8000.0
-MFMA_BF16_PEAK_TFLOPS = 2500.0
-M, K, N = 4096, 4096, 14336
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp8": 5000.0, "int8": 5000.0}
+HERE = os.path.dirname(os.path.abspath(__file__))
+METRIC = "checksum-verify GB/s (% of HBM peak) + overhead % vs guarded GEMM, 1 GPU"
 
 
 def _args():
@@ -38,217 +53,696 @@ def _args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--copies", type=int, default=4)
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--only", default=None, help="run one workload and print its line alone")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="time budget of each CPU baseline")
+    p.add_argument("--summarize", nargs="+", default=None, help="rocprofv3 output directories to summarize")
     return p.parse_args()
 
 
-def cpu_baseline(x, W, y, seconds: float):
-    """The oracle's serving check on the first rows of the workload, one thread, repeated for ~`seconds`."""
-    import numpy as np  # noqa: F401
-    from threadpoolctl import threadpool_limits
+# ---------------------------------------------------------------------------------------------------------------
+# rocprofv3 summaries (profiles/*.txt are written by --summarize and read back for the traffic figure)
 
-    from oracle import serve_check
-    rows = 512
-    xs = x[:rows].float().cpu().numpy()
-    ys = y[:rows].float().cpu().numpy()
-    c = serve_check.layer_constants(W.float().cpu().numpy(), None, 128, "bf16", seed=int(os.environ.get(
-        "SDCGUARD_SIGN_SEED", "1")))
-    nbytes = rows * K * 2 + rows * N * 2 + K * 6 * (N // 128) * 2
-    reps, t0 = 0, time.perf_counter()
-    with threadpool_limits(limits=1):
-        while True:
-            serve_check.check_static(xs, ys, c, dtype="bf16")
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= seconds:
-                break
-    gbs = nbytes * reps / el / 1e9
-    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle.serve_check.check_static (numpy, column-block check) on the first {rows} of 4096 "
-                      f"rows, {reps} repetitions in {el:.1f} s; bytes counted as the GPU column check counts them"}
+def _csv_rows(d: str, suffix: str):
+    rows = []
+    for f in sorted(glob.glob(os.path.join(d, "**", f"*{suffix}"), recursive=True)):
+        with open(f, newline="") as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
 
 
-def _traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed counter summary (rocprofv3 --pmc FETCH_SIZE and
-    WRITE_SIZE, each scaled by what the counter reads for a device copy of known size), or None without one."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.txt")
+def summarize(dirs) -> str:
+    """Kernel-trace statistics and per-dispatch HBM bytes of each kernel from rocprofv3 csv output.  Read bytes are
+    32 TCC_EA0_RDREQ_32B + 64 TCC_EA0_RDREQ_64B + 128 TCC_EA0_RDREQ_128B (each request counted at its size), write
+    bytes 32 (TCC_EA0_WRREQ - TCC_EA0_WRREQ_64B) + 64 TCC_EA0_WRREQ_64B; counters are summed over the L2 channels."""
+    out = []
+    keep = lambda name: "at::native" not in name and "at::cuda" not in name     # noqa: E731  (torch's own kernels)
+    for d in dirs:
+        stats = [r for r in _csv_rows(d, "kernel_stats.csv") if keep(r["Name"])]
+        if stats:
+            out.append(f"# kernel trace ({os.path.basename(os.path.normpath(d))})")
+            out.append("stats\tname\tcalls\tavg_us\tmin_us\tmax_us\tpct")
+            for r in sorted(stats, key=lambda r: -float(r["TotalDurationNs"])):
+                out.append("stats\t{}\t{}\t{:.2f}\t{:.2f}\t{:.2f}\t{:.1f}".format(
+                    r["Name"], r["Calls"], float(r["AverageNs"]) / 1e3, float(r["MinNs"]) / 1e3,
+                    float(r["MaxNs"]) / 1e3, float(r["Percentage"])))
+    per = {}
+    for d in dirs:
+        for r in _csv_rows(d, "counter_collection.csv"):
+            key = r["Kernel_Name"]
+            if not keep(key):
+                continue
+            per.setdefault(key, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    if per:
+        out.append("# HBM bytes per dispatch (averages over the dispatches of each kernel)")
+        out.append("traffic\tname\tdispatches\tread_bytes\twrite_bytes")
+        for name, c in per.items():
+            def avg(n):
+                v = c.get(n)
+                return sum(v) / len(v) if v else None
+            r32, r64, r128 = avg("TCC_EA0_RDREQ_32B_sum"), avg("TCC_EA0_RDREQ_64B_sum"), avg("TCC_EA0_RDREQ_128B_sum")
+            w, w64 = avg("TCC_EA0_WRREQ_sum"), avg("TCC_EA0_WRREQ_64B_sum")
+            rd = None if r32 is None else 32 * r32 + 64 * (r64 or 0) + 128 * (r128 or 0)
+            wr = None if w is None else 32 * (w - (w64 or 0)) + 64 * (w64 or 0)
+            n = max(len(v) for v in c.values())
+            out.append(f"traffic\t{name}\t{n}\t{'' if rd is None else int(rd)}\t{'' if wr is None else int(wr)}")
+    return "\n".join(out)
+
+
+def _profile_table(workload: str):
+    """{kernel name: (read bytes, write bytes)} from profiles/<workload>.txt, or {} without one."""
+    path = os.path.join(HERE, "profiles", f"{workload}.txt")
+    t = {}
     try:
         with open(path) as f:
             for line in f:
-                p = line.split()
-                if len(p) == 3 and p[0] == "traffic_bytes" and p[1] == kernel:
-                    return int(float(p[2]))
+                p = line.rstrip("\n").split("\t")
+                if len(p) == 5 and p[0] == "traffic" and p[2] != "dispatches":
+                    t[p[1]] = (float(p[3]) if p[3] else None, float(p[4]) if p[4] else None)
     except OSError:
         pass
-    return None
+    return t
+
+
+def _traffic(workload: str, pattern: str):
+    """HBM bytes (read + write) per launch of the kernels matching `pattern`, from the committed summary."""
+    hits = [v for k, v in _profile_table(workload).items() if re.search(pattern, k)]
+    if not hits or any(r is None or w is None for r, w in hits):
+        return None
+    return int(sum(r + w for r, w in hits) / len(hits))
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# measurement helpers
+
+class Ctx:
+    def __init__(self, a):
+        import torch
+        from sdcguard_amd import _lib
+        self.a, self.torch, self._lib = a, torch, _lib
+        self.L = _lib.lib()
+        self.dev = torch.device("cuda", 0)
+        torch.cuda.set_device(self.dev)
+
+    def loop_ms(self, fn, steps: int) -> float:
+        """Milliseconds per call of fn(i) over `steps` calls, HIP events on the current stream, synchronized on
+        both sides."""
+        torch = self.torch
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for i in range(steps):
+            fn(i)
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / steps
+
+    def kernel_ms(self, fn, steps: int, names) -> dict:
+        """Average launch duration (ms) of each named library kernel over `steps` calls of fn(i): the library
+        brackets every launch with HIP events on the stream it launches on."""
+        self.L.sdc_profile_reset()
+        self.L.sdc_profile_enable(1)
+        for i in range(steps):
+            fn(i)
+        self.torch.cuda.synchronize()
+        self.L.sdc_profile_enable(0)
+        out = {}
+        for nm in names:
+            tot, cnt = self._lib.profile_read(nm)
+            out[nm] = (tot / cnt if cnt else 0.0, cnt)
+        self.L.sdc_profile_reset()
+        return out
+
+
+def _roof(kernels: dict, amounts: dict, workload: str, patterns: dict, steps: int):
+    """Per-kernel roofline entries and the dominant kernel's `roofline` object.  amounts: name -> (bound, amount
+    per launch, dtype for an MFMA bound); kernels: name -> (avg ms, launches)."""
+    ent = {}
+    for nm, (bound, amount, dt) in amounts.items():
+        ms, cnt = kernels[nm]
+        if cnt == 0 or ms <= 0:
+            raise RuntimeError(f"no timing recorded for kernel {nm}")
+        if bound == "mfma":
+            ach = amount / (ms * 1e-3) / 1e12
+            peak, unit = MFMA_PEAK_TFLOPS[dt], "TFLOP/s"
+        else:
+            ach = amount / (ms * 1e-3) / 1e9
+            peak, unit = HBM_PEAK_GBS, "GB/s"
+        ent[nm] = {"avg_us": round(ms * 1e3, 2), "launches_per_step": round(cnt / steps, 3), "bound": bound,
+                   "algorithmic": amount, "achieved": round(ach, 1), "peak": peak, "unit": unit,
+                   "frac": round(ach / peak, 4), "traffic": _traffic(workload, patterns[nm]) if nm in patterns else None}
+    dom = max(ent, key=lambda nm: kernels[nm][0] * kernels[nm][1])
+    d = ent[dom]
+    roof = {"kernel": dom, "bound": d["bound"], "achieved": d["achieved"], "peak": d["peak"], "unit": d["unit"],
+            "frac": d["frac"], "traffic": d["traffic"], "algorithmic": d["algorithmic"], "avg_us": d["avg_us"],
+            "profile": f"profiles/{workload}.txt"}
+    return ent, roof
+
+
+def _cpu_info() -> dict:
+    import torch
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "torch": torch.__version__}
+
+
+def _cpu_median(fn, seconds: float, min_runs: int = 5, max_runs: int = 50):
+    """Median seconds of fn() over at least `min_runs` runs, more while `seconds` last."""
+    times = []
+    t0 = time.perf_counter()
+    while len(times) < min_runs or (time.perf_counter() - t0 < seconds and len(times) < max_runs):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return statistics.median(times), len(times)
+
+
+def _cpu_threads() -> int:
+    import torch
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    torch.set_num_threads(n)
+    return n
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# workloads
+
+def bench_bf16_mlp(ctx: Ctx) -> dict:
+    torch, a = ctx.torch, ctx.a
+    from sdcguard_amd.linear import check_linear_both, resolve_both
+    from sdcguard_amd.serve import LayerChecksums
+    M, K, N = 4096, 4096, 14336
+    name = "bf16_mlp_4096x4096x14336"
+    g = torch.Generator(device=ctx.dev).manual_seed(0)
+    W = (torch.randn(N, K, device=ctx.dev, generator=g) * 0.02).bfloat16()
+    xs = [torch.randn(M, K, device=ctx.dev, generator=g).bfloat16() for _ in range(a.copies)]
+    ys = [torch.nn.functional.linear(x, W) for x in xs]
+    cs = LayerChecksums(W, None, 128)
+    nb, mb = cs.nb, M // 128
+    state = torch.zeros(4, dtype=torch.int64, device=ctx.dev)
+    rows = torch.zeros(3, dtype=torch.int64, device=ctx.dev)
+
+    def check(i):
+        check_linear_both(xs[i % a.copies], W, None, ys[i % a.copies], cs, state=state, row_result=rows,
+                          concurrent=False)
+
+    for i in range(a.warmup):
+        check(i)
+    torch.cuda.synchronize()
+    if int(state[2].item()) != a.warmup:
+        raise RuntimeError(f"the check did not run: {int(state[2].item())} calls counted of {a.warmup}")
+    col, row = resolve_both(state, rows, M, N)
+    ms = ctx.loop_ms(check, a.steps)
+    names = ("xstage", "col_gemm", "row_gemm", "ypass")
+    km = ctx.kernel_ms(check, a.steps, names)
+
+    def gemm(i):
+        torch.mm(xs[i % a.copies], W.t(), out=ys[i % a.copies])
+
+    for i in range(3):
+        gemm(i)
+    gemm_ms = ctx.loop_ms(gemm, a.steps)
+
+    def both(i):
+        gemm(i)
+        check(i)
+    both_ms = ctx.loop_ms(both, a.steps)
+    buf = torch.empty_like(ys[0])
+    copy_ms = ctx.loop_ms(lambda i: buf.copy_(ys[i % a.copies]), a.steps)
+    del buf
+    xb, yb, wb, pb = M * K * 2, M * N * 2, N * K * 2, K * 6 * nb * 2
+    alg = xb + yb + wb + pb
+    amounts = {"xstage": ("hbm", xb, None), "row_gemm": ("hbm", wb, None),
+               "col_gemm": ("mfma", 2.0 * M * K * 6 * nb, "bf16"), "ypass": ("hbm", yb, None)}
+    patterns = {"xstage": r"xstage_kernel", "ypass": r"ypass_kernel",
+                "row_gemm": r"expected_gemm_kernel<0, 1", "col_gemm": r"expected_gemm_kernel<0, 2"}
+    ent, roof = _roof(km, amounts, name, patterns, a.steps)
+    value = alg / (ms * 1e-3) / 1e9
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "both block checksums (column-block against the layer's block sums, row-block of "
+                               "y^T = W x^T) of a bf16 Llama-MLP linear layer, x 4096x4096 N(0,1), W 14336x4096 "
+                               "N(0,0.02), y = x W^T bf16 (fp32 accumulation), block 128",
+                   "name": name, "m": M, "k": K, "n": N, "block": 128, "copies_rotated": a.copies,
+                   "algorithmic_bytes": alg},
+        "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "roofline": roof, "kernels": ent,
+        "device_copy_gbs": round(2 * yb / (copy_ms * 1e-3) / 1e9, 1),
+        "guarded_gemm_ms": round(gemm_ms, 5),
+        "overhead_pct_warm": round(100.0 * (both_ms - gemm_ms) / gemm_ms, 2),
+        "overhead_pct_cold": round(100.0 * ms / gemm_ms, 2),
+        "clean_max_z": {"column": round(col.max_z, 4), "row": round(row.max_z, 4)},
+    }
+    if not a.no_cpu:
+        out["cpu_baseline"] = cpu_linear(xs[0], W, ys[0], alg, a.cpu_seconds)
+    return out
+
+
+def cpu_linear(x, W, y, alg: int, seconds: float) -> dict:
+    """The torch restatement of both block checks (oracle.torch_check) on the full layer, every host core."""
+    from oracle import torch_check
+    cores = _cpu_threads()
+    xc, Wc, yc = x.cpu(), W.cpu(), y.cpu()
+    med, runs = _cpu_median(lambda: torch_check.linear_both(xc, Wc, None, yc), seconds)
+    return {"value": round(alg / med / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "median_s": round(med, 4), "runs": runs, **_cpu_info(),
+            "sample": "oracle.torch_check.linear_both (the reference's checksum._zscores in torch, fp32, on the CPU) "
+                      "over the whole 4096x4096x14336 layer: column-block and row-block checks, block sums of W "
+                      "made in the call as the reference's CPU path makes them; GB/s over the same 273.94 MB"}
+
+
+def _fp8_problem(ctx, seed, m, k, n, copies):
+    torch = ctx.torch
+    g = torch.Generator(device=ctx.dev).manual_seed(seed)
+    Bq = (torch.randn(k, n, device=ctx.dev, generator=g) * 4).clamp(-448, 448).to(torch.float8_e4m3fn)
+    sb = (10.0 ** (torch.rand(n, device=ctx.dev, generator=g) * 2 - 3)).float()
+    As, sas, Cs = [], [], []
+    for _ in range(copies):
+        Aq = (torch.randn(m, k, device=ctx.dev, generator=g) * 4).clamp(-448, 448).to(torch.float8_e4m3fn)
+        sa = (10.0 ** (torch.rand(m, device=ctx.dev, generator=g) * 2 - 3)).float()
+        C = ((Aq.float() @ Bq.float()) * sa[:, None] * sb[None, :]).bfloat16()
+        As.append(Aq)
+        sas.append(sa)
+        Cs.append(C)
+    return Bq, sb, As, sas, Cs
+
+
+def bench_quant(ctx: Ctx, kind: str, m: int, k: int, n: int, name: str, seed: int) -> dict:
+    torch, a = ctx.torch, ctx.a
+    from sdcguard_amd import modes
+    copies = a.copies
+    if kind == "int8":
+        g = torch.Generator(device=ctx.dev).manual_seed(seed)
+        B = torch.randint(-127, 128, (k, n), device=ctx.dev, generator=g, dtype=torch.int32).to(torch.int8)
+        As = [torch.randint(-127, 128, (m, k), device=ctx.dev, generator=g, dtype=torch.int32).to(torch.int8)
+              for _ in range(copies)]
+        Cs = [(A.double() @ B.double()).to(torch.int32) for A in As]
+        sas, sb = [None] * copies, None
+        consts = modes.QuantChecksums.make(B)
+    else:
+        B, sb, As, sas, Cs = _fp8_problem(ctx, seed, m, k, n, copies)
+        consts = modes.QuantChecksums.make(B, sb)
+    nb = -(-n // 128)
+    res = torch.zeros(4, dtype=torch.int64, device=ctx.dev)
+
+    def check(i):
+        modes.quant_zscores(As[i % copies], consts, Cs[i % copies], sa=sas[i % copies], out=res)
+
+    for i in range(a.warmup):
+        check(i)
+    torch.cuda.synchronize()
+    st = modes.resolve(modes.QuantStat(res, m, nb, consts.kind, 6.0))
+    if st["wrong_blocks"] != 0:
+        raise RuntimeError(f"{name}: the clean workload raised {st['wrong_blocks']} blocks")
+    ms = ctx.loop_ms(check, a.steps)
+    gname, sname = ("quant_gemm_i8", "quant_score_i8") if kind == "int8" else ("quant_gemm_fp8", "quant_score_fp8")
+    km = ctx.kernel_ms(check, a.steps, (gname, sname))
+    ab = m * k
+    cb = Cs[0].numel() * Cs[0].element_size()
+    pb = consts.parts.numel() * consts.parts.element_size()
+    sc = 0 if kind == "int8" else 4 * m
+    alg = ab + cb + pb + sc
+    amounts = {gname: ("mfma", 2.0 * m * k * consts.parts.shape[0] * consts.parts.shape[1], kind),
+               sname: ("hbm", cb, None)}
+    patterns = {gname: r"expected_gemm_kernel<" + ("3" if kind == "int8" else "2"), sname: r"quant_score"}
+    ent, roof = _roof(km, amounts, name, patterns, a.steps)
+    value = alg / (ms * 1e-3) / 1e9
+    gemm_ms = None
+    try:
+        if kind == "int8":
+            def gemm(i):
+                torch._int_mm(As[i % copies], B)
+        else:
+            Bt = B.t().contiguous().t()
+
+            def gemm(i):
+                torch._scaled_mm(As[i % copies], Bt, scale_a=sas[i % copies].view(-1, 1),
+                                 scale_b=sb.view(1, -1), out_dtype=torch.bfloat16)
+        for i in range(3):
+            gemm(i)
+        gemm_ms = ctx.loop_ms(gemm, a.steps)
+        both_ms = ctx.loop_ms(lambda i: (gemm(i), check(i)), a.steps)
+    except (RuntimeError, TypeError) as e:                          # no library GEMM for this layout here
+        gemm_err = str(e).splitlines()[0][:160]
+    out = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "ms_per_step": round(ms, 5),
+           "dtype": kind, "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+           "config": {"workload": f"{kind} GEMM {m}x{k}x{n} column-block check" +
+                      (" (exact int32)" if kind == "int8" else ", per-token / per-channel scales 10^U(-3,-1), "
+                                                                 "bf16 output"),
+                      "name": name, "m": m, "k": k, "n": n, "algorithmic_bytes": alg},
+           "roofline": roof, "kernels": ent,
+           "guarded_gemm_ms": None if gemm_ms is None else round(gemm_ms, 5),
+           "overhead_pct_warm": None if gemm_ms is None else round(100.0 * (both_ms - gemm_ms) / gemm_ms, 2),
+           "overhead_pct_cold": None if gemm_ms is None else round(100.0 * ms / gemm_ms, 2)}
+    if gemm_ms is None:
+        out["guarded_gemm_note"] = gemm_err
+    if not a.no_cpu:
+        out["cpu_baseline"] = cpu_quant(kind, As[0], B, sas[0], sb, Cs[0], alg, a.cpu_seconds)
+    return out
+
+
+def cpu_quant(kind, A, B, sa, sb, C, alg: int, seconds: float) -> dict:
+    """The oracle's quantized check (numpy, float64 / int64 BLAS on every host core) on a sample of rows."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import quant
+    cores = _cpu_threads()
+    m = A.shape[0]
+    rows = min(m, 512)
+    W = quant.patterns(1)
+    if kind == "int8":
+        Ac, Bc, Cc = A[:rows].cpu().numpy(), B.cpu().numpy(), C[:rows].cpu().numpy()
+        fn = lambda: quant.int8_judge(Ac, Bc, Cc, W)                         # noqa: E731
+    else:
+        vals = quant.fp8_e4m3_values()
+        Ac = vals[A[:rows].view(__import__("torch").uint8).cpu().numpy()]
+        Bc = vals[B.view(__import__("torch").uint8).cpu().numpy()]
+        sac, sbc = sa[:rows].double().cpu().numpy(), sb.double().cpu().numpy()
+        Cc = C[:rows].double().cpu().numpy()
+        fn = lambda: quant.fp8_judge(Ac, Bc, sac, sbc, Cc, W, c_bf16=True)  # noqa: E731
+    with threadpool_limits(limits=cores):
+        med, runs = _cpu_median(fn, seconds)
+    k, n = B.shape
+    sample_bytes = rows * k * A.element_size() + rows * n * C.element_size() + (alg - m * k * A.element_size() -
+                                                                               m * n * C.element_size())
+    del np
+    return {"value": round(sample_bytes / med / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "median_s": round(med, 4), "runs": runs, **_cpu_info(),
+            "sample": f"oracle.quant.{kind}_judge (numpy) on the first {rows} of {m} rows (block sums of B made in "
+                      f"the call); GB/s over the sample's algorithmic bytes"}
+
+
+def bench_moe(ctx: Ctx) -> dict:
+    torch, a = ctx.torch, ctx.a
+    from sdcguard_amd.checksum import grouped_zscores, resolve_grouped
+    name = "moe_4096x8of64_2048x1408"
+    T0, E, TOPK, K, N = 4096, 64, 8, 2048, 1408
+    gen = torch.Generator().manual_seed(7)
+    p = torch.tensor([1.0 / (r + 1) ** 1.1 for r in range(E)], dtype=torch.float64)
+    picks = torch.multinomial(p.expand(T0, E), TOPK, replacement=False, generator=gen)
+    sizes = torch.bincount(picks.reshape(-1), minlength=E)
+    T = int(sizes.sum())
+    g = torch.Generator(device=ctx.dev).manual_seed(8)
+    A = torch.randn(T, K, device=ctx.dev, generator=g).bfloat16()
+    Bw = (torch.randn(E, K, N, device=ctx.dev, generator=g) * 0.02).bfloat16()
+    offs = torch.cumsum(sizes, 0).to(torch.int32).to(ctx.dev)
+    out = torch.empty(T, N, dtype=torch.bfloat16, device=ctx.dev)
+    s = 0
+    for e, c in enumerate(sizes.tolist()):
+        if c:
+            out[s:s + c] = (A[s:s + c].float() @ Bw[e].float()).bfloat16()
+        s += c
+
+    def check(i):
+        grouped_zscores(A, Bw, out, offs)
+
+    for i in range(a.warmup):
+        check(i)
+    res = resolve_grouped(grouped_zscores(A, Bw, out, offs))
+    if not all(r.ok for r in res):
+        raise RuntimeError(f"{name}: the clean workload raised")
+    ms = ctx.loop_ms(check, a.steps)
+    names = ("b_stage", "b_finish", "split", "train_gemm", "train_score")
+    km = ctx.kernel_ms(check, a.steps, names)
+    nb = -(-N // 128)
+    ab, cb, b2 = T * K * 2, T * N * 2, E * K * 2 * nb * 4
+    alg = ab + cb + b2
+    amounts = {"b_stage": ("hbm", E * K * N * 2, None), "train_gemm": ("mfma", 2.0 * T * K * 6 * nb, "bf16"),
+               "train_score": ("hbm", cb, None)}
+    patterns = {"b_stage": r"b_stage", "train_gemm": r"expected_gemm_kernel<0", "train_score": r"score"}
+    ent, roof = _roof(km, amounts, name, patterns, a.steps)
+    value = alg / (ms * 1e-3) / 1e9
+    gemm_ms = None
+    try:
+        def gemm(i):
+            torch._grouped_mm(A, Bw, offs=offs, out_dtype=torch.bfloat16)
+        for i in range(3):
+            gemm(i)
+        gemm_ms = ctx.loop_ms(gemm, a.steps)
+        both_ms = ctx.loop_ms(lambda i: (gemm(i), check(i)), a.steps)
+    except (RuntimeError, TypeError, AttributeError) as e:
+        gemm_err = str(e).splitlines()[0][:160]
+    line = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "ms_per_step": round(ms, 5), "dtype": "bf16",
+            "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+            "config": {"workload": "MoE grouped-GEMM column-block check, 4096 tokens x top-8 of 64 experts (Zipf "
+                                   "1.1 loads), expert weights 2048x1408 bf16, per-expert block sums made in the call",
+                       "name": name, "rows": T, "k": K, "n": N, "experts": E, "algorithmic_bytes": alg},
+            "roofline": roof, "kernels": ent,
+            "guarded_gemm_ms": None if gemm_ms is None else round(gemm_ms, 5),
+            "overhead_pct_warm": None if gemm_ms is None else round(100.0 * (both_ms - gemm_ms) / gemm_ms, 2),
+            "overhead_pct_cold": None if gemm_ms is None else round(100.0 * ms / gemm_ms, 2)}
+    if gemm_ms is None:
+        line["guarded_gemm_note"] = gemm_err
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_moe(A, Bw, out, sizes.tolist(), alg, a.cpu_seconds)
+    return line
+
+
+def cpu_moe(A, Bw, out, sizes, alg, seconds) -> dict:
+    """The torch restatement of the column-block check, expert by expert, every host core."""
+    from oracle import torch_check
+    cores = _cpu_threads()
+    Ac, Bc, Oc = A.cpu(), Bw.cpu(), out.cpu()
+
+    def run():
+        s = 0
+        for e, c in enumerate(sizes):
+            if c:
+                torch_check.zscores(Ac[s:s + c], Bc[e], Oc[s:s + c])
+            s += c
+    med, runs = _cpu_median(run, seconds)
+    return {"value": round(alg / med / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "median_s": round(med, 4), "runs": runs, **_cpu_info(),
+            "sample": "oracle.torch_check.zscores per expert over the whole grouped product (64 experts)"}
+
+
+def _kv_cache(ctx, layers=28, nblk=4096):
+    torch = ctx.torch
+    g = torch.Generator(device=ctx.dev).manual_seed(55)
+    kv = torch.empty(layers, nblk, 8, 16, 256, dtype=torch.bfloat16, device=ctx.dev)
+    for lay in range(layers):
+        kv[lay].normal_(generator=g)
+    return kv
+
+
+def bench_kv(ctx: Ctx, kv) -> dict:
+    torch, a = ctx.torch, ctx.a
+    from sdcguard_amd.kv import block_fingerprints
+    name = "kv_fingerprint_28x4096"
+    cache = kv.view(-1, 8, 16, 256)
+    fp = torch.zeros(cache.shape[0], 3, dtype=torch.int64, device=ctx.dev)
+    steps = max(5, a.steps // 5)
+
+    def run(i):
+        block_fingerprints(cache, out=fp)
+
+    for i in range(2):
+        run(i)
+    ms = ctx.loop_ms(run, steps)
+    km = ctx.kernel_ms(run, steps, ("kv_fingerprint",))
+    alg = cache.numel() * 2
+    ent, roof = _roof(km, {"kv_fingerprint": ("hbm", alg, None)}, name, {"kv_fingerprint": r"kv_fp"}, steps)
+    value = alg / (ms * 1e-3) / 1e9
+    line = {"metric": "KV block fingerprint GB/s (% of HBM peak), 1 GPU", "value": round(value, 2), "unit": "GB/s",
+            "ms_per_step": round(ms, 5), "dtype": "u16", "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+            "config": {"workload": "fingerprints (sums of the 16-bit words, weighted twice, mod 2^64) of every "
+                                   "block of a 28-layer x 4096-block paged KV cache, blocks [8 heads, 16 tokens, "
+                                   "2 x 128] bf16", "name": name, "blocks": cache.shape[0],
+                       "block_bytes": cache[0].numel() * 2, "algorithmic_bytes": alg},
+            "roofline": roof, "kernels": ent}
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_kv(cache, a.cpu_seconds)
+    return line
+
+
+def cpu_kv(cache, seconds) -> dict:
+    """The oracle's C fingerprint (oracle/fingerprint.c, one thread per core) on a sample of blocks."""
+    import numpy as np
+
+    from oracle import fingerprint as F
+    cores = _cpu_threads()
+    nb = 2048
+    sub = cache[:nb].view(__import__("torch").int16).cpu().numpy()
+    if F.c_lib() is None:
+        return {"value": None, "unit": "GB/s", "cores": 0, "kind": "port", "sample": "oracle C library not built"}
+    med, runs = _cpu_median(lambda: F.kv_block_fp3_c(sub, threads=cores), seconds)
+    del np
+    return {"value": round(sub.nbytes / med / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "median_s": round(med, 4), "runs": runs, **_cpu_info(),
+            "sample": f"oracle.fingerprint.kv_block_fp3_c (C, {cores} threads) on {nb} of the "
+                      f"{cache.shape[0]} blocks ({sub.nbytes / 1e6:.0f} MB)"}
+
+
+def bench_attn(ctx: Ctx, kv) -> dict:
+    torch, a = ctx.torch, ctx.a
+    from sdcguard_amd import serve_attn as SA
+    name = "attn_recompute_28x64"
+    L_, NBLK, HKV, NTOK, D, HQ, NSEQ = kv.shape[0], kv.shape[1], 8, 16, 128, 16, 64
+    samples = 16
+    gc = torch.Generator().manual_seed(56)
+    lens = torch.randint(512, 2049, (NSEQ,), generator=gc)
+    Wt = 2048 // NTOK
+    bt = torch.zeros(NSEQ, Wt, dtype=torch.int32)
+    for r in range(NSEQ):
+        nbk = -(-int(lens[r]) // NTOK)
+        bt[r, :nbk] = torch.randperm(NBLK, generator=gc)[:nbk].to(torch.int32)
+    q = (torch.randn(L_, NSEQ, HQ, D, generator=gc) * 0.5).bfloat16().to(ctx.dev)
+    qsl = torch.arange(NSEQ + 1, dtype=torch.int32, device=ctx.dev)
+    pos = lens - 1
+    blk_of = bt[torch.arange(NSEQ), (pos // NTOK).long()]
+    slots = (blk_of.long() * NTOK + pos % NTOK).to(ctx.dev)
+    lens_d, bt_d = lens.to(torch.int32).to(ctx.dev), bt.to(ctx.dev)
+    live = torch.arange(Wt * NTOK, device=ctx.dev)[None, :] < lens_d[:, None]
+    outs, keys, vals = [], [], []
+    for layer in range(L_):
+        kv_l = kv[layer]
+        rows = kv_l[bt_d.long()].permute(0, 1, 3, 2, 4).reshape(NSEQ, Wt * NTOK, HKV, 2 * D).float()
+        Kt, Vt = rows[..., :D].permute(0, 2, 1, 3).contiguous(), rows[..., D:].permute(0, 2, 1, 3).contiguous()
+        qf = q[layer].float().view(NSEQ, HKV, HQ // HKV, D)
+        s = torch.matmul(qf, Kt.transpose(-1, -2).contiguous()) * D ** -0.5           # [seq, hkv, g, keys]
+        s = s.masked_fill(~live[:, None, None, :], float("-inf"))
+        o = torch.matmul(torch.softmax(s, -1), Vt).reshape(NSEQ, HQ, D).bfloat16()
+        outs.append(o)
+        keys.append(kv_l[blk_of.long().to(ctx.dev), :, (pos % NTOK).long().to(ctx.dev), :D].contiguous())
+        vals.append(kv_l[blk_of.long().to(ctx.dev), :, (pos % NTOK).long().to(ctx.dev), D:].contiguous())
+        del rows, Kt, Vt, s
+    bufs = SA.buffers(ctx.dev, L_, D, 64, torch.bfloat16, samples=samples)
+    scale = D ** -0.5
+
+    def step(i):
+        bufs["ctrl"][0] = 1000 + i
+        for layer in range(L_):
+            SA.attn_check(q[layer], outs[layer], kv[layer], keys[layer], vals[layer], qsl, lens_d, bt_d, slots,
+                          bufs["state"], layer, bufs["ctrl"], 1, 0, scale, -1, SA.ATTN_Z, bufs["capm"],
+                          bufs["capq"], bufs["capo"], None, None, bufs["ws"], True, False, samples=samples)
+
+    bufs["ctrl"][1] = 1
+    steps = max(5, a.steps // 5)
+    for i in range(2):
+        step(i)
+    torch.cuda.synchronize()
+    rep = [SA.decode_state(bufs["state"][l_].cpu()) for l_ in range(L_)]
+    worst = max(r["max_z"] for r in rep)
+    if not worst < SA.ATTN_Z or any(r["writes_wrong"] or r["bad_blocks"] for r in rep):
+        raise RuntimeError(f"{name}: the clean decode step raised (z {worst})")
+    ms = ctx.loop_ms(step, steps)
+    km = ctx.kernel_ms(step, steps, ("attn_check",))
+    # every layer call is live (one check per layer per step) and samples the same (row, head) pairs at a step.
+    # bytes: the K and V rows of every distinct sampled (request, kv head), per layer, averaged over the timed steps
+    ql, ll = qsl.cpu().tolist(), lens.tolist()
+    tot = 0
+    for i in range(steps):
+        for layer in range(L_):
+            seen = set()
+            for j in range(samples):
+                p_ = SA.sample_python(1000 + i, 0, 1, j, ql, ll, NSEQ, HQ)
+                if p_:
+                    seen.add((p_["request"], p_["head"] // (HQ // HKV)))
+            tot += sum(ll[r] * D * 2 * 2 for r, _ in seen)
+    alg_step = tot / steps
+    ent, roof = _roof(km, {"attn_check": ("hbm", alg_step / L_, None)}, name,
+                      {"attn_check": r"attn_check_kernel"}, steps)
+    line = {"metric": "sampled attention recompute GB/s of sampled K/V rows, 1 GPU",
+            "value": round(alg_step / (ms * 1e-3) / 1e9, 2), "unit": "GB/s", "ms_per_step": round(ms, 5),
+            "us_per_layer_call": round(ms * 1e3 / L_, 2), "dtype": "bf16",
+            "config": {"workload": "one decode step of 64 sequences (512-2048 tokens) over 28 layers of a paged "
+                                   "bf16 KV cache (4096 blocks a layer, [8 heads, 16 tokens, 2 x 128]): each layer's "
+                                   "check recomputes 16 sampled (row, head) attentions and checks the step's KV write",
+                       "name": name, "layers": L_, "samples_per_layer": samples,
+                       "algorithmic_bytes_per_step": int(alg_step)},
+            "roofline": roof, "kernels": ent, "clean_max_z": round(worst, 4)}
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_attn(kv, q, outs, keys, vals, qsl, lens, bt, slots, L_, samples, alg_step,
+                                        a.cpu_seconds)
+    return line
+
+
+def cpu_attn(kv, q, outs, keys, vals, qsl, lens, bt, slots, L_, samples, alg_step, seconds) -> dict:
+    """The oracle's attention check (numpy) of one layer call at a time, on the blocks its samples can read."""
+    import numpy as np
+    import torch
+
+    from oracle import attn as OA
+    cores = _cpu_threads()
+    layer = 3
+    kv_l = kv[layer]
+    ids = sorted({int(v) for r in range(bt.shape[0]) for v in bt[r].tolist()})
+    remap = torch.zeros(kv.shape[1], dtype=torch.int32)
+    remap[torch.tensor(ids)] = torch.arange(len(ids), dtype=torch.int32)
+    bt_c = remap[bt.long()].numpy()
+    sl = slots.cpu()
+    sl_c = (remap[(sl // 16)].long() * 16 + sl % 16).numpy()
+    w = kv_l[torch.tensor(ids, device=kv.device)].view(torch.int16).cpu().numpy().view(np.uint16)
+    kv_c = (w.astype(np.uint32) << 16).view(np.float32)
+    f = lambda t: t.float().cpu().numpy()                                   # noqa: E731
+    args = (f(q[layer]), f(outs[layer]), kv_c, f(keys[layer]), f(vals[layer]), qsl.cpu().numpy(), lens.numpy(),
+            bt_c, sl_c)
+    med, runs = _cpu_median(lambda: OA.check(*args, step=1000, scale=128 ** -0.5, samples=samples), seconds)
+    return {"value": round(alg_step / L_ / med / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "median_s": round(med, 4), "runs": runs, **_cpu_info(),
+            "sample": "oracle.attn.check (numpy) of one layer's call (16 samples) over the blocks the step's "
+                      "sequences hold; GB/s over a layer's average sampled K/V bytes"}
+
+
+WORKLOADS = ("bf16_mlp_4096x4096x14336", "fp8_mlp_4096x4096x14336", "int8_2048x7168x4096", "fp8_2048x7168x4096",
+             "moe_4096x8of64_2048x1408", "kv_fingerprint_28x4096", "attn_recompute_28x64")
+
+
+def run(ctx: Ctx, name: str, kv_holder: dict) -> dict:
+    if name == "bf16_mlp_4096x4096x14336":
+        return bench_bf16_mlp(ctx)
+    if name == "fp8_mlp_4096x4096x14336":
+        return bench_quant(ctx, "fp8", 4096, 4096, 14336, name, seed=21)
+    if name == "int8_2048x7168x4096":
+        return bench_quant(ctx, "int8", 2048, 7168, 4096, name, seed=22)
+    if name == "fp8_2048x7168x4096":
+        return bench_quant(ctx, "fp8", 2048, 7168, 4096, name, seed=23)
+    if name == "moe_4096x8of64_2048x1408":
+        return bench_moe(ctx)
+    if "kv" not in kv_holder:
+        kv_holder["kv"] = _kv_cache(ctx)
+    if name == "kv_fingerprint_28x4096":
+        return bench_kv(ctx, kv_holder["kv"])
+    if name == "attn_recompute_28x64":
+        return bench_attn(ctx, kv_holder["kv"])
+    raise SystemExit(f"unknown workload {name}; one of {', '.join(WORKLOADS)}")
 
 
 def main():
     a = _args()
+    if a.summarize:
+        print(summarize(a.summarize))
+        return
     if a.gpus != 1:
-        print(f"bench.py measures one GPU: this build runs the check on a single MI355X (asked for {a.gpus}); "
-              "the multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
+        print(f"bench.py measures one GPU (asked for {a.gpus}): the checks are independent per GPU shard, and "
+              "their multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
         sys.exit(2)
-    import torch
-    torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
-    from sdcguard_amd import _lib
-    from sdcguard_amd.checksum import linear_rows_operands, matmul_zscores, resolve
-    from sdcguard_amd.serve import STATE_COLS, LayerChecksums, check_static_impl
-    dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    L = _lib.lib()
-
-    g = torch.Generator(device=dev).manual_seed(0)
-    W = (torch.randn(N, K, device=dev, generator=g) * 0.02).bfloat16()
-    xs, ys = [], []
-    for _ in range(a.copies):
-        x = torch.randn(M, K, device=dev, generator=g).bfloat16()
-        xs.append(x)
-        ys.append(torch.nn.functional.linear(x, W))
-    cs = LayerChecksums(W, None, 128)
-    state = torch.zeros(1, STATE_COLS, dtype=torch.int64, device=dev)
-    row_res = torch.zeros(3, dtype=torch.int64, device=dev)
-    args = cs.tensors(True)
-    nb = cs.nb
-    rows_ops = [linear_rows_operands(xs[i], W, None, ys[i]) for i in range(a.copies)]
-    torch.cuda.synchronize()
-
-    def check(i):
-        check_static_impl(xs[i], ys[i], *args, state, 0, 6.0, 1e-20)
-        A, B, C, _ = rows_ops[i]
-        matmul_zscores(A, B, C, None, out=row_res)
-
-    for i in range(a.warmup):
-        check(i % a.copies)
-    torch.cuda.synchronize()
-    if int(state[0, 2].item()) != a.warmup:
-        raise RuntimeError("the check did not run")
-    z_col = float(torch.tensor([int(state[0, 0].item()) >> 32], dtype=torch.int32).view(torch.float32).item())
-    from sdcguard_amd.checksum import CheckStat
-    r_rows = resolve([CheckStat(row_res, N, M // 128, False, 6.0)])[0]
-
-    # timed region: both checks, cold (rotating copies)
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for i in range(a.steps):
-        check(i % a.copies)
-    stop.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / a.steps
-
-    # the same loop with per-kernel HIP events on the launch stream
-    names = ["expected_gemm", "serve_fused", "b_stage", "b_finish", "split", "train_gemm", "train_score"]
-    L.sdc_profile_reset()
-    L.sdc_profile_enable(1)
-    for i in range(a.steps):
-        check(i % a.copies)
-    torch.cuda.synchronize()
-    L.sdc_profile_enable(0)
-    kms = {}
-    for nm in names:
-        tot, cnt = _lib.profile_read(nm)
-        kms[nm] = tot / max(cnt, 1)
-    L.sdc_profile_reset()
-
-    # guarded GEMM alone, and GEMM + check back to back (warm: y and x still in the caches, as served)
-    def gemm(i):
-        return torch.mm(xs[i], W.t(), out=ys[i])
-
-    for i in range(3):
-        gemm(i % a.copies)
-    torch.cuda.synchronize()
-    start.record()
-    for i in range(a.steps):
-        gemm(i % a.copies)
-    stop.record()
-    torch.cuda.synchronize()
-    gemm_ms_step = start.elapsed_time(stop) / a.steps
-    start.record()
-    for i in range(a.steps):
-        gemm(i % a.copies)
-        check(i % a.copies)
-    stop.record()
-    torch.cuda.synchronize()
-    both_ms = start.elapsed_time(stop) / a.steps
-
-    # a plain device copy of y (read + write of a known size): the achievable-bandwidth yardstick, and the kernel
-    # whose FETCH_SIZE / WRITE_SIZE calibrate the counters for the traffic figure
-    buf = torch.empty_like(ys[0])
-    for i in range(3):
-        buf.copy_(ys[i % a.copies])
-    torch.cuda.synchronize()
-    start.record()
-    for i in range(a.steps):
-        buf.copy_(ys[i % a.copies])
-    stop.record()
-    torch.cuda.synchronize()
-    copy_gbs = 2 * ys[0].numel() * 2 / (start.elapsed_time(stop) / a.steps * 1e-3) / 1e9
-    del buf
-
-    xb, yb, wb = M * K * 2, M * N * 2, N * K * 2
-    parts_bytes = K * 6 * nb * 2
-    alg_bytes = xb + yb + parts_bytes + wb
-    value = alg_bytes / (ms * 1e-3) / 1e9
-    s_col = int(L.sdc_expected_splits(M, K, 2 * nb))
-    s_row = int(L.sdc_expected_splits(N, K, 2 * (M // 128)))
-    # per kernel: (bound, algorithmic amount per launch, unit): bytes it must move, or MFMA flops
-    alg = {
-        "expected_gemm": ("mfma", 2.0 * M * K * 6 * nb),
-        "serve_fused": ("hbm", yb + s_col * (M * 2 * nb * 4 + 2 * M * 4)),
-        "b_stage": ("hbm", xb),
-        "train_gemm": ("hbm", wb + s_row * (N * 2 * (M // 128) * 4 + 2 * N * 4)),
-        "train_score": ("hbm", yb + s_row * (N * 2 * (M // 128) * 4 + 2 * N * 4)),
-    }
-    kern = {}
-    for nm, (bound, amount) in alg.items():
-        t = kms[nm]
-        if t <= 0:
-            raise RuntimeError(f"no timing recorded for kernel {nm}")
-        if bound == "mfma":
-            ach = amount / (t * 1e-3) / 1e12
-            kern[nm] = {"ms": round(t, 5), "bound": "mfma", "achieved": round(ach, 1), "unit": "TFLOP/s",
-                        "frac": round(ach / MFMA_BF16_PEAK_TFLOPS, 4), "algorithmic": amount}
-        else:
-            ach = amount / (t * 1e-3) / 1e9
-            kern[nm] = {"ms": round(t, 5), "bound": "hbm", "achieved": round(ach, 1), "unit": "GB/s",
-                        "frac": round(ach / HBM_PEAK_GBS, 4), "algorithmic": amount}
-    for nm in ("b_finish", "split"):
-        kern[nm] = {"ms": round(kms[nm], 5), "bound": "latency"}
-    dom = max(alg, key=lambda nm: kms[nm])
-    d = kern[dom]
-    out = {
-        "metric": "checksum-verify GB/s (% of HBM peak) + overhead % vs guarded GEMM, 1 GPU",
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": a.steps,
-        "warmup": a.warmup,
-        "ms_per_step": round(ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": {"workload": "column-block and row-block checksum check of a bf16 Llama-MLP linear layer, "
-                               "x 4096x4096 N(0,1), W 14336x4096 N(0,0.02), y = x W^T bf16 (fp32 accumulation)",
-                   "m": M, "k": K, "n": N, "block": 128, "copies_rotated": a.copies,
-                   "algorithmic_bytes": alg_bytes},
-        "hbm_frac": round(value / HBM_PEAK_GBS, 4),
-        "roofline": {"kernel": dom, "bound": d["bound"], "achieved": d["achieved"],
-                     "peak": MFMA_BF16_PEAK_TFLOPS if d["bound"] == "mfma" else HBM_PEAK_GBS, "unit": d["unit"],
-                     "frac": d["frac"], "traffic": _traffic(dom), "avg_ms": d["ms"]},
-        "kernels": kern,
-        "device_copy_gbs": round(copy_gbs, 1),
-        "guarded_gemm_ms": round(gemm_ms_step, 5),
-        "overhead_pct_warm": round(100.0 * (both_ms - gemm_ms_step) / gemm_ms_step, 2),
-        "overhead_pct_cold": round(100.0 * ms / gemm_ms_step, 2),
-        "clean_max_z": {"column": round(z_col, 4), "row": round(float(r_rows.max_z), 4)},
-    }
-    if not a.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(xs[0], W, ys[0], a.cpu_seconds)
-    print(json.dumps(out))
+    ctx = Ctx(a)
+    ctx.torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
+    kv_holder: dict = {}
+    if a.only:
+        line = run(ctx, a.only, kv_holder)
+        line.setdefault("n_gpus", 1)
+        print(json.dumps(line))
+        return
+    main_line = run(ctx, WORKLOADS[0], kv_holder)
+    more = []
+    for nm in WORKLOADS[1:]:
+        print(f"# {nm}", file=sys.stderr, flush=True)
+        more.append(run(ctx, nm, kv_holder))
+        ctx.torch.cuda.empty_cache()
+    main_line["more"] = more
+    print(json.dumps(main_line))
 
 
 if __name__ == "__main__":

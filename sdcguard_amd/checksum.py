@@ -189,7 +189,7 @@ def matmul_zscores(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, bias: Opti
         out = torch.zeros(3, dtype=torch.int64, device=C.device)
     L = _lib.lib()
     ws_bytes = int(L.sdc_matmul_check_workspace(ba, bb, m, k, n, bs))
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=C.device)
+    ws = _lib.workspace(C.device, ws_bytes)
     rc = L.sdc_matmul_check(
         _lib.dtype_code(dt), A.data_ptr(), sab, sam, sak, ba, B.data_ptr(), sbb, sbk, sbn, bb,
         C.data_ptr(), scb, scm, scn, bc, m, k, n, bs, None if b_ptr is None else b_ptr.data_ptr(), kind,
@@ -347,7 +347,7 @@ def grouped_zscores(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, offs: t
     L = _lib.lib()
     nb = -(-n // block)
     results = torch.zeros(G, 3, dtype=torch.int64, device=out.device)
-    ws = torch.empty(int(L.sdc_grouped_check_workspace(G, T, k, n, block)), dtype=torch.uint8, device=out.device)
+    ws = _lib.workspace(out.device, int(L.sdc_grouped_check_workspace(G, T, k, n, block)))
     rc = L.sdc_grouped_check(_lib.dtype_code(dt), a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(), b.stride(0),
                              b.stride(1), b.stride(2), G, out.data_ptr(), out.stride(0), out.stride(1), T, k, n, block,
                              offs64.data_ptr(), None if bias is None else bias.data_ptr(),

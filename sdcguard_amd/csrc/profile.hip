@@ -3,6 +3,7 @@
 // When enabled (sdc_profile_enable(1)), every kernel launch of the library is bracketed by two events on its own
 // stream; sdc_profile_read() waits for them and returns the summed duration and the launch count of one kernel
 // name.  The events come from a pool created on first use, so nothing is allocated per launch once warm.
+#include <atomic>
 #include <mutex>
 #include <string.h>
 #include <string>
@@ -17,7 +18,7 @@ struct Rec {
   hipEvent_t a, b;
 };
 std::mutex g_mu;
-bool g_on = false;
+std::atomic<bool> g_on{false};     // read without the lock: a launch with profiling off costs one relaxed load
 std::vector<Rec> g_recs;
 std::vector<hipEvent_t> g_pool;
 size_t g_used = 0;
@@ -33,8 +34,9 @@ hipEvent_t take() {
 }  // namespace
 
 SdcProf::SdcProf(const char* name, hipStream_t stream) : name_(name), stream_(stream), b_(nullptr) {
+  if (!g_on.load(std::memory_order_relaxed)) return;
   std::lock_guard<std::mutex> lk(g_mu);
-  if (!g_on) return;
+  if (!g_on.load(std::memory_order_relaxed)) return;
   hipEvent_t a = take(), b = take();
   if (!a || !b) return;
   hipEventRecord(a, stream_);
@@ -48,7 +50,7 @@ SdcProf::~SdcProf() {
 
 extern "C" int sdc_profile_enable(int on) {
   std::lock_guard<std::mutex> lk(g_mu);
-  g_on = on != 0;
+  g_on.store(on != 0, std::memory_order_relaxed);
   return SDC_OK;
 }
 

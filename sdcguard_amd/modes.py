@@ -123,8 +123,7 @@ def quant_zscores(A: torch.Tensor, consts: QuantChecksums, C: torch.Tensor, *, s
     if out is None:
         out = torch.zeros(4, dtype=torch.int64, device=C.device)
     need = int(L.sdc_quant_check_workspace(kind, m, k, consts.n, consts.block))
-    ws = workspace if workspace is not None and workspace.numel() >= need else \
-        torch.empty(need, dtype=torch.uint8, device=C.device)
+    ws = workspace if workspace is not None and workspace.numel() >= need else _lib.workspace(C.device, need)
     tab = sign_table(C.device)
     P = consts.parts
     Av = A.view(torch.uint8) if kind == 1 else A

@@ -234,7 +234,7 @@ def check_static_impl(x2: torch.Tensor, y2: torch.Tensor, parts: torch.Tensor, p
             raise ValueError("layer constants must be contiguous fp32 tensors")
     L = _lib.lib()
     ws_bytes = int(L.sdc_check_static_workspace(m, k, n, bs))
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=y2.device)
+    ws = _lib.workspace(y2.device, ws_bytes)
     row = state.data_ptr() + slot * state.stride(0) * state.element_size()
     rc = L.sdc_check_static(
         _lib.dtype_code(dt), x2.data_ptr(), x2.stride(0), x2.stride(1), y2.data_ptr(), y2.stride(0), y2.stride(1),
