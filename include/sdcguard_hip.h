@@ -113,6 +113,21 @@ int sdc_grouped_check(int dtype, const void* A, int64_t sam, int64_t sak, const 
                       float abs_floor, const float* sign_table, int64_t* results, void* workspace,
                       int64_t workspace_bytes, float* scores_out, hipStream_t stream);
 
+/* ---- per-layer constants of the serving check -------------------------------------------------------------
+ * Replaces LayerChecksums._initialize (serve.py:149-211): built on the device from W (n x k, row stride swn, rows
+ * k-contiguous) and an optional bias (n values at stride sbias, NULL: none), blocks of bs <= 128 output rows.
+ *   parts: the three 16-bit parts (hi, mid, lo) of B2 / scale, B2 = the plain and signed block sums of W's rows
+ *     (k x 2nb fp32), as (3 x 2nb) columns of parts_pitch = k rounded up to 8 elements (zero padded), part p of
+ *     column c at parts[(p * 2nb + c) * parts_pitch]: the layout sdc_check_static and sdc_linear_check read.
+ *   consts_bias, consts_plain: fp32 [nb][12] per block (the scoring pass's table), with and without the bias:
+ *     scale (plain, signed), bias block sums (2), |B2 column|_2 (2), max |B2| (2), max |W| of the block,
+ *     max |bias| of the block, 0, 0.
+ *   sign_table: as sdc_check_static.  workspace: sdc_layer_constants_workspace(n, k, bs) bytes. */
+int64_t sdc_layer_constants_workspace(int64_t n, int64_t k, int64_t bs);
+int sdc_layer_constants(int dtype, const void* W, int64_t swn, int64_t n, int64_t k, int64_t bs, const void* bias,
+                        int64_t sbias, const float* sign_table, void* parts, int64_t parts_pitch, float* consts_bias,
+                        float* consts_plain, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 /* ---- check of one quantized GEMM ----------------------------------------------------------------------------
  * Replaces modes.judge (modes.py:231-291) for its int8 and fp8 branches, on the device, and extends the fp8 one to
  * per-row activation scales sa and per-column weight scales sb (C = sa_i sb_j sum_k Aq[i,k] Bq[k,j]).

@@ -270,41 +270,46 @@ def check_linear_rows(x, weight, bias, y, **kw) -> Optional[CheckResult]:
     return check_matmul(*linear_rows_operands(x, weight, bias, y), **kw)
 
 
+def _bias_fits(bias: Optional[torch.Tensor], shape) -> bool:
+    """A shared bias applies to a group's output when it broadcasts to exactly that shape."""
+    if bias is None:
+        return True
+    try:
+        return tuple(torch.broadcast_shapes(tuple(bias.shape), tuple(shape))) == tuple(shape)
+    except RuntimeError:
+        return False
+
+
+# how a torch._grouped_mm layout (a.dim(), b.dim()) splits into per-group products: group g, its rows or columns
+# [lo, hi) -> (A, B, C); and whether an empty group still has an output to check (grouped along k: out[g] is zeros)
+_GROUP_SLICES = {
+    (2, 3): (lambda a, b, out, g, lo, hi: (a[lo:hi], b[g], out[lo:hi]), False),          # tokens by expert
+    (3, 2): (lambda a, b, out, g, lo, hi: (a[g], b[:, lo:hi], out[:, lo:hi]), False),    # grouped along n
+    (2, 2): (lambda a, b, out, g, lo, hi: (a[:, lo:hi], b[lo:hi, :], out[g]), True),     # grouped along k
+}
+
+
 def grouped_checks(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, offs: Optional[torch.Tensor],
                    bias: Optional[torch.Tensor] = None) -> list:
-    """guard._grouped_checks (guard.py:102-143): the (A, B, C, bias, alpha, beta) of every group of a
-    torch._grouped_mm, split on the cumulative group ends `offs` (read on the host).  2-D x 3-D: tokens grouped by
-    expert (rows of a and out); 3-D x 2-D: grouped along n; 2-D x 2-D: grouped along k (weight gradients: an empty
-    group still has an all-zero output to check); 3-D x 3-D: one batched check.  Groups whose output a shared bias
-    does not broadcast to are skipped, as the reference skips them."""
-    def shared(shape) -> Optional[bool]:
-        if bias is None:
-            return None
-        try:
-            return torch.broadcast_shapes(tuple(bias.shape), tuple(shape)) == tuple(shape)
-        except RuntimeError:
-            return False
-
+    """The (A, B, C, bias, alpha, beta) checks of a torch._grouped_mm result, as the reference's guard splits one
+    (guard.py:102-143): groups cut at the cumulative ends `offs` (read on the host), a 3-D x 3-D product as one
+    batched check, and no check for a group whose output the shared bias does not broadcast to."""
     if a.dim() == 3 and b.dim() == 3:
-        return [(a, b, out, bias, 1.0, 1.0)] if bias is None or shared(out.shape[1:]) else []
-    if offs is None:
+        return [(a, b, out, bias, 1.0, 1.0)] if _bias_fits(bias, out.shape[1:]) else []
+    layout = _GROUP_SLICES.get((a.dim(), b.dim()))
+    if layout is None or offs is None:
         return []
-    ends = [int(e) for e in offs.tolist()]
-    checks, start = [], 0
-    for i, end in enumerate(ends):
-        if end > start or (a.dim() == 2 and b.dim() == 2):
-            if a.dim() == 2 and b.dim() == 3:
-                c = (a[start:end], b[i], out[start:end])
-            elif a.dim() == 3 and b.dim() == 2:
-                c = (a[i], b[:, start:end], out[:, start:end])
-            elif a.dim() == 2 and b.dim() == 2:
-                c = (a[:, start:end], b[start:end, :], out[i])
-            else:
-                c = None
-            if c is not None and (bias is None or shared(c[2].shape)):
-                checks.append((*c, bias, 1.0, 1.0))
-        start = end
-    return checks
+    cut, keep_empty = layout
+    bounds = [0] + [int(e) for e in offs.tolist()]
+    found = []
+    for g in range(len(bounds) - 1):
+        lo, hi = bounds[g], bounds[g + 1]
+        if hi <= lo and not keep_empty:
+            continue
+        A, B, C = cut(a, b, out, g, lo, max(lo, hi))
+        if _bias_fits(bias, C.shape):
+            found.append((A, B, C, bias, 1.0, 1.0))
+    return found
 
 
 @dataclass
@@ -312,7 +317,7 @@ class GroupedStat:
     """A queued grouped check: one result row per group on the device (worst key over the group's rows, key with its
     noise, unjudged count) and what decoding it needs."""
     results: torch.Tensor        # (groups, 3) int64
-    offs: torch.Tensor           # the group ends as given (device)
+    offs: torch.Tensor           # the group ends as the kernels read them (clamped, non-decreasing; device)
     rows: int
     nb: int
     z: float
@@ -320,7 +325,7 @@ class GroupedStat:
 
 def grouped_zscores(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, offs: torch.Tensor,
                     bias: Optional[torch.Tensor] = None, *, block: int = 128, abs_floor: float = ABS_FLOOR,
-                    z: float = 6.0, scores_out: Optional[torch.Tensor] = None) -> GroupedStat:
+                    z: float = 6.0, epoch: int = 0, scores_out: Optional[torch.Tensor] = None) -> GroupedStat:
     """Queue the check of a MoE grouped product out = a @ b[g] for the rows of group g (a: (T, k) tokens sorted by
     expert, b: (G, k, n), out: (T, n), offs: (G,) cumulative row ends, int32 or int64, on the device) without
     reading offs on the host: every group's rows are checked against that group's B, as
@@ -343,7 +348,10 @@ def grouped_zscores(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, offs: t
         if bias.numel() != n:
             raise ValueError("grouped_zscores: a shared bias of n values")
         bias = bias if bias.dtype == dt else bias.to(dt)
-    offs64 = offs.to(torch.int64).contiguous()
+    # the ends as both kernels read them: clamped to the rows and made non-decreasing (a running maximum), so the
+    # GEMM's tile walk and the scoring pass's row-to-group search agree whatever offs holds; a private copy, so a
+    # routing buffer reused before resolve_grouped does not change how the results decode
+    offs64 = torch.cummax(offs.reshape(-1).to(torch.int64).clamp(0, T), 0).values.contiguous()
     L = _lib.lib()
     nb = -(-n // block)
     results = torch.zeros(G, 3, dtype=torch.int64, device=out.device)
@@ -352,10 +360,10 @@ def grouped_zscores(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, offs: t
                              b.stride(1), b.stride(2), G, out.data_ptr(), out.stride(0), out.stride(1), T, k, n, block,
                              offs64.data_ptr(), None if bias is None else bias.data_ptr(),
                              0 if bias is None else bias.stride(0), float(z), float(abs_floor),
-                             sign_table(out.device).data_ptr(), results.data_ptr(), ws.data_ptr(), ws.numel(),
+                             sign_table(out.device, epoch).data_ptr(), results.data_ptr(), ws.data_ptr(), ws.numel(),
                              None if scores_out is None else scores_out.data_ptr(), _lib.stream_of(out))
     _lib.check(rc, "sdc_grouped_check")
-    return GroupedStat(results, offs, T, nb, z)
+    return GroupedStat(results, offs64, T, nb, z)
 
 
 def resolve_grouped(st: GroupedStat) -> list:
@@ -384,8 +392,9 @@ def check_grouped_mm(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, offs: 
                      bias: Optional[torch.Tensor] = None, **kw) -> list:
     """Check a torch._grouped_mm result: one CheckResult per check guard._grouped_checks would make.  The MoE
     forward layout (2-D x 3-D) runs as one device-side grouped check; the others as one check per group."""
+    device_path = {"block", "abs_floor", "z", "epoch", "scores_out"}
     if a.dim() == 2 and b.dim() == 3 and offs is not None and out.dtype in UNIT_ROUNDOFF and \
-            (bias is None or bias.numel() == out.shape[-1]):
+            (bias is None or bias.numel() == out.shape[-1]) and set(kw) <= device_path:
         return resolve_grouped(grouped_zscores(a, b, out, offs, bias, **kw))
     res = []
     for A, B, C, bi, al, be in grouped_checks(a, b, out, offs, bias):

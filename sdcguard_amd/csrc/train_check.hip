@@ -779,3 +779,101 @@ extern "C" int sdc_grouped_check(int dtype, const void* A, int64_t sam, int64_t 
                    bias ? 1 : 0, 0, 0, sbias, 1.f, 1.f, z, abs_floor, sign_table, results, workspace,
                    workspace_bytes, scores_out, offs, stream);
 }
+
+// ---------------------------------------------------------------------------------------------------------------
+// Per-layer constants of the serving check, built on the device from W (n x k, rows k-contiguous) and an optional
+// bias: the B-side stage of the training check run on B = W^T (block sums B2 over 128 output rows of W, their
+// column norms and maxima, each block's largest |W|, the bias's block sums), the split of B2 into three parts
+// (k-major, depth pitch kp = k rounded up to 8), and one table of per-block constants for the check's scoring pass,
+// with and without the bias.
+
+namespace {
+
+struct PackArgs {
+  const float* colstat;            // [2nb][3]: |B2 column|_2, largest |entry|, power-of-two scale
+  const float* bmaxf;              // [nb]
+  const float* bias3;              // [nb][3] or null
+  int64_t nb;
+  float* with_bias;                // [nb][12]
+  float* without_bias;             // [nb][12]
+};
+
+// row of a block: scale(plain, signed), bias sums(plain, signed), |B2|_2(2), max |B2|(2), max |W|, max |bias|, 0, 0
+__global__ __launch_bounds__(256) void pack_consts_kernel(PackArgs a) {
+  for (int64_t jb = (int64_t)blockIdx.x * 256 + threadIdx.x; jb < a.nb; jb += (int64_t)gridDim.x * 256) {
+    const float* c = a.colstat + 6 * jb;
+    float row[12] = {c[2], c[5], 0.f, 0.f, c[0], c[3], c[1], c[4], a.bmaxf[jb], 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 12; ++i) a.without_bias[12 * jb + i] = row[i];
+    if (a.bias3) {
+      row[2] = a.bias3[3 * jb];
+      row[3] = a.bias3[3 * jb + 1];
+      row[9] = a.bias3[3 * jb + 2];
+    }
+#pragma unroll
+    for (int i = 0; i < 12; ++i) a.with_bias[12 * jb + i] = row[i];
+  }
+}
+
+}  // namespace
+
+extern "C" int64_t sdc_layer_constants_workspace(int64_t n, int64_t k, int64_t bs) {
+  if (n <= 0 || k <= 0 || bs <= 0) return 0;
+  return layout(1, 1, 1, k, n, bs).total * (int64_t)sizeof(float) + 256;
+}
+
+extern "C" int sdc_layer_constants(int dtype, const void* W, int64_t swn, int64_t n, int64_t k, int64_t bs,
+                                   const void* bias, int64_t sbias, const float* sign_table, void* parts,
+                                   int64_t parts_pitch, float* consts_bias, float* consts_plain, void* workspace,
+                                   int64_t workspace_bytes, hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
+  if (n < 1 || k < 1 || swn < k) return SDC_EINVAL;
+  if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EINVAL;
+  if (bs < 1 || bs > 128) return SDC_EUNSUPPORTED;
+  if (!W || !sign_table || !parts || !consts_bias || !consts_plain) return SDC_EINVAL;
+  const Layout L = layout(1, 1, 1, k, n, bs);
+  if (parts_pitch != L.kp) return SDC_EINVAL;
+  if (!workspace || workspace_bytes < L.total * (int64_t)sizeof(float) + 256) return SDC_EWORKSPACE;
+  float* ws = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  const float* s_full = sign_table + (bs - 1) * 128;
+  const float* s_last = L.rem ? sign_table + (L.rem - 1) * 128 : s_full;
+
+  BStageArgs ba{};
+  ba.B = (const uint16_t*)W; ba.sbb = 0; ba.sbk = 1; ba.sbn = swn;      // B = W^T: B[kk][j] = W[j][kk]
+  ba.k = k; ba.n = n; ba.nb = L.nb; ba.bs = bs; ba.rem = L.rem; ba.nkc = L.nkc;
+  ba.s_full = s_full; ba.s_last = s_last; ba.B2T = ws + L.off_b2t; ba.part = ws + L.off_part;
+  {
+    SdcProf prof("b_stage", stream);
+    if (swn != 1) {
+      ba.vec = (swn % 8 == 0) && ((uintptr_t)W % 16 == 0);
+      dim3 grid((unsigned)sdc_cdiv(k, 256), (unsigned)L.nb, 1u);
+      if (dtype == SDC_BF16) hipLaunchKernelGGL(b_stage_t_kernel<SDC_BF16>, grid, dim3(256), 0, stream, ba);
+      else hipLaunchKernelGGL(b_stage_t_kernel<SDC_FP16>, grid, dim3(256), 0, stream, ba);
+    } else {                                                            // k == 1: W^T is one contiguous row
+      ba.vec = (bs % 8 == 0) && ((uintptr_t)W % 16 == 0);
+      dim3 grid((unsigned)L.nkc, (unsigned)L.nb, 1u);
+      if (dtype == SDC_BF16) hipLaunchKernelGGL(b_stage_kernel<SDC_BF16>, grid, dim3(256), 0, stream, ba);
+      else hipLaunchKernelGGL(b_stage_kernel<SDC_FP16>, grid, dim3(256), 0, stream, ba);
+    }
+    SDC_LAUNCH_CHECK();
+  }
+  BFinishArgs fa{};
+  fa.part = ws + L.off_part; fa.nkc = L.nkc; fa.nb = L.nb; fa.bs = bs; fa.rem = L.rem; fa.fp16 = dtype == SDC_FP16;
+  fa.colstat = ws + L.off_col; fa.bmaxf = ws + L.off_bmax;
+  fa.bias = (const uint16_t*)bias; fa.sbias = sbias;
+  fa.s_full = s_full; fa.s_last = s_last; fa.bias_out = ws + L.off_bias;
+  {
+    SdcProf prof("b_finish", stream);
+    if (dtype == SDC_BF16) hipLaunchKernelGGL(b_finish_kernel<SDC_BF16>, dim3((unsigned)L.nb, 1u), dim3(64), 0, stream, fa);
+    else hipLaunchKernelGGL(b_finish_kernel<SDC_FP16>, dim3((unsigned)L.nb, 1u), dim3(64), 0, stream, fa);
+    SDC_LAUNCH_CHECK();
+  }
+  int rc = sdc_split_launch(dtype, ws + L.off_b2t, ws + L.off_col + 2, L.ncols * 3, 3, L.ncols, k, L.kp, 1,
+                            (uint16_t*)parts, stream);
+  if (rc != SDC_OK) return rc;
+  PackArgs pa{ws + L.off_col, ws + L.off_bmax, bias ? ws + L.off_bias : nullptr, L.nb, consts_bias, consts_plain};
+  const unsigned grid = (unsigned)(sdc_cdiv(L.nb, 256) < 1024 ? sdc_cdiv(L.nb, 256) : 1024);
+  hipLaunchKernelGGL(pack_consts_kernel, dim3(grid), dim3(256), 0, stream, pa);
+  SDC_LAUNCH_CHECK();
+  return SDC_OK;
+}

@@ -71,9 +71,15 @@ class QuantChecksums:
                 raise ValueError("int8 check: no scales (the accumulator itself is checked, exactly)")
             if k % 2:
                 raise ValueError("int8 check: k must be even")
-            B2 = B.double() @ W                                   # exact: |B2| <= 128 * 127
-            hi = torch.floor((B2 + 64) / 128)
+            B2 = B.double() @ W                                   # exact: |B2| <= 128 * 128 = 16384
+            # two base-128 digits, B2 = 128 hi + lo with hi in [-128, 127]: |lo| <= 64 except for sums in
+            # [16320, 16383] (-128 entries laid against the sign pattern), whose lo takes 64..127.  +16384 would
+            # need a width-128 pattern of all -1 entries; it is refused rather than wrapped
+            hi = torch.floor((B2 + 64) / 128).clamp(-128, 127)
             lo = B2 - 128 * hi
+            if bool((lo.abs() > 127).any()):
+                raise ValueError("int8 check: a block sum of 16384 (every entry -128 against the sign pattern) does "
+                                 "not split into two int8 digits")
             parts = torch.stack([hi, lo]).to(torch.int8).transpose(1, 2).contiguous()   # (2, 2nb, k)
             return cls("int8", k, n, block, parts)
         if B.dtype == torch.float8_e4m3fn:

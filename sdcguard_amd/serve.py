@@ -1,16 +1,16 @@
 """Serving check: every bf16/fp16 linear layer on every forward pass (reference: serve.py).
 
-Weights do not change while a model serves, so each layer's block sums are computed once (LayerChecksums) and
-every forward pass only reads the layer's input x and output y again:
+Weights do not change while a model serves, so each layer's block sums are computed once (LayerChecksums, built on
+the GPU by sdc_layer_constants) and every forward pass only reads the layer's input x and output y again:
 
     expected = x @ (block sums of W)       MFMA, three low-precision parts of the fp32 sums
     actual   = block sums of y             one pass over y
     z        = |expected - actual| / rounding noise,  fault above z (default 6)
 
-The work runs in libsdcguard_hip.so (sdc_check_static), two launches per layer, no host synchronisation; the
-worst score goes into a per-layer int64 state row with atomic maxima and is read back asynchronously by
-ServeGuard.poll().  The custom op sdcguard::check_static keeps the reference's argument list (serve.py:465-489),
-so torch.compile sees one opaque call and HIP graphs capture its kernels.
+The work runs in libsdcguard_hip.so (sdc_check_static), no host synchronisation; the worst score goes into a
+per-layer int64 state row with atomic maxima and is read back asynchronously by ServeGuard.poll().  The custom op
+sdcguard::check_static keeps the reference's argument list (serve.py:465-489), so torch.compile sees one opaque call
+and HIP graphs capture its kernels.
 """
 from __future__ import annotations
 
@@ -25,7 +25,7 @@ from typing import Callable, Optional
 import torch
 
 from . import _lib
-from .checksum import ABS_FLOOR, UNIT_ROUNDOFF, _signs, sign_table
+from .checksum import ABS_FLOOR, UNIT_ROUNDOFF, sign_table
 
 # serve.py:55-89: the state row and the capture buffers
 STATE_COLS = 4
@@ -38,125 +38,105 @@ EPOCH_SHIFT = 32
 STEP_MASK = (1 << 32) - 1
 OP_SCHEMA = 2
 
-_PHI = (math.sqrt(5.0) - 1.0) / 2.0
+_GOLDEN = 0.5 * (math.sqrt(5.0) - 1.0)
 
 
 def select_layer(i: int, share: float, offset: int = 0) -> bool:
-    """Golden-ratio spread of a checked share of layers (serve.py:104-116)."""
+    """Whether the i-th eligible layer is among a `share` of layers spread evenly by the golden-ratio sequence,
+    shifted by `offset` shares (serve.py:104-116: the same selection, so both pick the same layers)."""
     if share >= 1.0:
         return True
     if share <= 0.0:
         return False
-    return ((i * _PHI) % 1.0 - offset * share) % 1.0 < share
+    return ((i * _GOLDEN) % 1.0 - offset * share) % 1.0 < share
 
 
-def _static(t: torch.Tensor) -> None:
-    try:
-        torch._dynamo.mark_static_address(t)
-    except Exception:  # noqa: BLE001
-        pass
+def _pin_address(t: torch.Tensor) -> None:
+    """Tell torch.compile that t keeps its address (buffers the check writes across calls and graph replays)."""
+    mark = getattr(getattr(torch, "_dynamo", None), "mark_static_address", None)
+    if mark is not None:
+        try:
+            mark(t)
+        except (RuntimeError, TypeError, ValueError):
+            pass
+
+
+def _pattern_pair(width: int, dtype: torch.dtype, dev) -> torch.Tensor:
+    """(width, 2): a column of ones and the signed checksum's pattern of that block width, in `dtype`."""
+    s = sign_table(dev).view(128, 128)[width - 1, :width]
+    return torch.stack([torch.ones_like(s), s], dim=1).to(dtype)
 
 
 class LayerChecksums:
-    """Everything the check needs about one weight matrix W (n outputs x k inputs), computed once
-    (serve.py:140-244).  `parts` is the (k x 6nb) matrix of the three low-precision parts of B2 / scale, stored
-    k-contiguous per column (a transposed view of a (6nb x k) tensor): the layout the MFMA kernel reads."""
+    """Everything the check needs about one weight matrix W (n outputs x k inputs), computed once on the GPU
+    (sdc_layer_constants; the reference builds the same quantities in serve.py:149-211).
+
+    parts      (k, 6nb) view, k-contiguous columns: the three low-precision parts of B2 / scale, B2 the plain and
+               signed sums of each block of `block` rows of W (fp32), the layout the check's MFMA kernel reads
+    scale, b2n, b2max, bsum        (nb, 2) fp32; bmax, bmax_bias (nb,) fp32; width, wsq (nb,)
+    pair_full, pair_rem            (bs, 2) / (rem, 2) ones and signs in W's dtype (the op's interface)
+    fingerprint                    int64[3] of W's bits (recompute.fingerprint), to notice a rewritten weight
+    tensors(with_bias)             the op's arguments after x2 and y2, in the reference's order"""
 
     def __init__(self, weight: torch.Tensor, bias: Optional[torch.Tensor], block: int = 128):
-        with torch.autocast(device_type=weight.device.type, enabled=False), torch.no_grad():
-            self._initialize(weight, bias, block)
-
-    def _initialize(self, weight: torch.Tensor, bias: Optional[torch.Tensor], block: int) -> None:
+        from .recompute import fingerprint
         W = weight.detach()
+        if W.dim() != 2:
+            raise ValueError("the serving check takes a 2-D weight (n outputs x k inputs)")
+        if W.dtype not in UNIT_ROUNDOFF:
+            raise ValueError(f"the serving check takes bf16 and fp16 weights, not {W.dtype}")
+        _lib.require_gpu(W)
+        if W.stride(1) != 1:
+            W = W.contiguous()
         n, k = W.shape
         dt, dev = W.dtype, W.device
-        if dt not in UNIT_ROUNDOFF:
-            raise ValueError(f"the serving check takes bf16 and fp16 weights, not {dt}")
-        bs = max(1, min(block, n))
-        nbf, rem = n // bs, n % bs
-        nb = nbf + (1 if rem else 0)
-        self.n, self.k, self.nb, self.bs, self.nbf, self.rem, self.dtype = n, k, nb, bs, nbf, rem, dt
+        bs = max(1, min(int(block), n))
+        self.n, self.k, self.bs, self.dtype = n, k, bs, dt
+        self.nbf, self.rem = divmod(n, bs)
+        self.nb = nb = self.nbf + (1 if self.rem else 0)
         self.has_bias = bias is not None
-        self.pair_full = self._pair(bs, dt, dev)
-        self.pair_rem = self._pair(rem, dt, dev) if rem else self.pair_full
-        Wf = W.float()
-        cols = []
-        if nbf:
-            Wb = Wf[:nbf * bs].view(nbf, bs, k)
-            cols.append(torch.einsum("bjk,jc->kbc", Wb, self._pair(bs, torch.float32, dev)).reshape(k, 2 * nbf))
-        if rem:
-            cols.append(torch.einsum("jk,jc->kc", Wf[nbf * bs:], self._pair(rem, torch.float32, dev)))
-        B2 = torch.cat(cols, dim=1).contiguous()                                # (k, 2nb) fp32
-        del Wf
-        self.b2n = torch.linalg.vector_norm(B2, dim=0).view(nb, 2)
-        self.b2max = torch.linalg.vector_norm(B2, ord=float("inf"), dim=0).view(nb, 2)
-        if dt == torch.float16:
-            amax = B2.abs().amax(dim=0)
-            ok = torch.isfinite(amax) & (amax > 0)
-            scale = torch.where(ok, torch.exp2(torch.ceil(torch.log2(amax.clamp_min(1e-30)))), 1.0)
-        else:
-            scale = torch.ones(2 * nb, device=dev, dtype=torch.float32)
-        self.scale = scale.view(nb, 2)
-        # (6nb, k) contiguous: part p of column c is row p * 2nb + c; `parts` is its (k, 6nb) transpose
-        self.parts = _split3_kmajor(B2 / scale, dt)
-        rows_max = W.float().abs().amax(dim=1)
-        self.bmax = self._block_reduce(rows_max, nbf, bs, rem)
+        b = None
         if bias is not None:
-            bf = bias.detach().float()
-            bp = []
-            if nbf:
-                bp.append(bf[:nbf * bs].view(nbf, bs) @ self._pair(bs, torch.float32, dev))
-            if rem:
-                bp.append((bf[nbf * bs:] @ self._pair(rem, torch.float32, dev)).view(1, 2))
-            self.bsum = torch.cat(bp, dim=0)
-            self.bmax_bias = self._block_reduce(bf.abs(), nbf, bs, rem)
-        else:
-            self.bsum = torch.zeros(nb, 2, device=dev, dtype=torch.float32)
-            self.bmax_bias = torch.zeros(nb, device=dev, dtype=torch.float32)
-        self._z1 = torch.zeros(nb, device=dev, dtype=torch.float32)
-        self._z2 = torch.zeros(nb, 2, device=dev, dtype=torch.float32)
-        width = torch.full((nb,), float(bs), device=dev, dtype=torch.float32)
-        if rem:
-            width[-1] = float(rem)
-        self.width = width
-        self.wsq = width.sqrt()
-        self.fingerprint = self._fingerprint(W)
-        for wb in (True, False):
-            _packed_consts(*(self.tensors(wb)[i] for i in (3, 4, 5, 6, 7, 8)))
-        for t in self.tensors(True) + self.tensors(False):
-            _static(t)
-
-    @staticmethod
-    def _pair(width: int, dtype: torch.dtype, dev) -> torch.Tensor:
-        s = _signs(width, dev)
-        return torch.stack([torch.ones_like(s), s], dim=1).to(dtype)
-
-    @staticmethod
-    def _block_reduce(v: torch.Tensor, nbf: int, bs: int, rem: int) -> torch.Tensor:
-        out = []
-        if nbf:
-            out.append(v[:nbf * bs].view(nbf, bs).amax(dim=1))
-        if rem:
-            out.append(v[nbf * bs:].amax().view(1))
-        return torch.cat(out)
-
-    @staticmethod
-    def _fingerprint(W: torch.Tensor) -> torch.Tensor:
-        """serve.py:226-237: sums of the weights' raw bits, plain and weighted by position mod 65521."""
-        bits = W.contiguous().view(-1).view(torch.int16 if W.element_size() == 2 else torch.int32)
-        tot = torch.zeros(2, dtype=torch.int64, device=W.device)
-        chunk = 1 << 24
-        for i in range(0, bits.numel(), chunk):
-            b = bits[i:i + chunk].to(torch.int64)
-            pos = torch.arange(i, i + b.numel(), device=W.device, dtype=torch.int64) % 65521 + 1
-            tot += torch.stack([b.sum(), (b * pos).sum()])
-        return tot
+            b = bias.detach().reshape(-1)
+            if b.numel() != n:
+                raise ValueError(f"bias of {b.numel()} values for {n} outputs")
+            b = b if b.dtype == dt else b.to(dt)
+        kp = -(-k // 8) * 8
+        L = _lib.lib()
+        with torch.no_grad():
+            store = torch.empty(6 * nb, kp, dtype=dt, device=dev)
+            table = torch.empty(2, nb, 12, dtype=torch.float32, device=dev)
+            ws = _lib.workspace(dev, int(L.sdc_layer_constants_workspace(n, k, bs)))
+            rc = L.sdc_layer_constants(_lib.dtype_code(dt), W.data_ptr(), W.stride(0), n, k, bs, _lib.ptr(b),
+                                       b.stride(0) if b is not None else 0, sign_table(dev).data_ptr(),
+                                       store.data_ptr(), kp, table[0].data_ptr(), table[1].data_ptr(),
+                                       ws.data_ptr(), ws.numel(), _lib.stream_of(W))
+            _lib.check(rc, "sdc_layer_constants")
+        self.parts = store[:, :k].t()
+        cols = table[0]
+        self.scale, self.bsum = cols[:, 0:2].contiguous(), cols[:, 2:4].contiguous()
+        self.b2n, self.b2max = cols[:, 4:6].contiguous(), cols[:, 6:8].contiguous()
+        self.bmax, self.bmax_bias = cols[:, 8].contiguous(), cols[:, 9].contiguous()
+        self._nobias = (torch.zeros(nb, device=dev), torch.zeros(nb, 2, device=dev))
+        self.width = torch.full((nb,), float(bs), device=dev)
+        if self.rem:
+            self.width[-1] = float(self.rem)
+        self.wsq = self.width.sqrt()
+        self.pair_full = _pattern_pair(bs, dt, dev)
+        self.pair_rem = _pattern_pair(self.rem, dt, dev) if self.rem else self.pair_full
+        self.fingerprint = fingerprint(W)
+        # the scoring pass reads one (nb, 12) table per variant: hand the built ones to _packed_consts
+        self.bsum._sdc_packed = (table[0], (self.scale.data_ptr(), self.bmax_bias.data_ptr(), self.b2n.data_ptr()))
+        self._nobias[1]._sdc_packed = (table[1], (self.scale.data_ptr(), self._nobias[0].data_ptr(),
+                                                  self.b2n.data_ptr()))
+        for t in self.tensors(True) + self._nobias:
+            _pin_address(t)
 
     def tensors(self, with_bias: bool = True):
-        """Arguments of the check op after x2 and y2 (serve.py:239-244)."""
-        bmb, bs = (self.bmax_bias, self.bsum) if with_bias else (self._z1, self._z2)
-        return (self.parts, self.pair_full, self.pair_rem, self.scale, self.b2n, self.b2max, self.bmax, bmb, bs,
-                self.wsq, self.width)
+        """Arguments of the check op after x2 and y2 (the reference's order, serve.py:239-244)."""
+        bmax_bias, bsum = (self.bmax_bias, self.bsum) if with_bias else self._nobias
+        return (self.parts, self.pair_full, self.pair_rem, self.scale, self.b2n, self.b2max, self.bmax, bmax_bias,
+                bsum, self.wsq, self.width)
 
 
 def _split3_kmajor(B2: torch.Tensor, dt: torch.dtype) -> torch.Tensor:
@@ -278,18 +258,15 @@ check_static_any = check_static_impl
 
 
 def decode_state(rows: torch.Tensor):
-    """(z, flat index, noise) per row of a state tensor on the CPU (serve.py:399-404)."""
-    zs = (rows[:, 0] >> 32).to(torch.int32).view(torch.float32).tolist()
-    flats = (rows[:, 0] & 0xFFFFFFFF).tolist()
-    nzs = (rows[:, 1] & 0xFFFFFFFF).to(torch.int32).view(torch.float32).tolist()
-    return list(zip(zs, flats, nzs))
+    """(z, flat index, noise) of every state row (the reference's decode_state, serve.py:399-404)."""
+    return [decode(a, b) for a, b in rows[:, :2].detach().to("cpu").tolist()]
 
 
 def decode_counts(rows: torch.Tensor):
-    """(checks executed, unjudged checksums) per row (serve.py:407-412)."""
+    """(checks executed, unjudged checksums) of every state row (serve.py:407-412); zeros for rows without them."""
     if rows.dim() != 2 or rows.shape[1] < STATE_COLS:
-        return [(0, 0)] * rows.shape[0]
-    return list(zip(rows[:, COL_CHECKS].tolist(), rows[:, COL_UNJUDGED].tolist()))
+        return [(0, 0) for _ in range(rows.shape[0])]
+    return [(int(r[COL_CHECKS]), int(r[COL_UNJUDGED])) for r in rows.detach().to("cpu").tolist()]
 
 
 def decode(key_i: int, key_d: int, *counts: int):
@@ -343,9 +320,72 @@ class SDCEvent:
     extra: dict = field(default_factory=dict)
 
 
+class _DeviceRows:
+    """What a guard keeps on one device: the int64 state rows of its layers, the capture area (flags and the rows
+    kept for a recheck), and the snapshot of the state on its way to the host."""
+
+    def __init__(self, device: torch.device, rows: int, kmax: int, cap_w: int):
+        self.device = device
+        self.state = torch.zeros(rows, STATE_COLS, dtype=torch.int64, device=device)
+        self.cap_meta = torch.zeros(CAP_FLAGS + rows, dtype=torch.int64, device=device)
+        self.cap_data = torch.zeros(CAPTURE_SLOTS + 1, cap_w + kmax, dtype=torch.float32, device=device)
+        self.in_flight = None            # (pinned host copy, event recorded after the copy)
+        self.epoch = 0
+        for t in (self.state, self.cap_meta, self.cap_data):
+            _pin_address(t)
+
+    def fits(self, rows: int, kmax: int, cap_w: int) -> bool:
+        return self.state.shape[0] >= rows and self.cap_data.shape[1] >= cap_w + kmax
+
+    def enlarged(self, rows: int, kmax: int, cap_w: int) -> "_DeviceRows":
+        """A bigger copy (room for twice the layers, depth rounded up to 1024) keeping what this one holds."""
+        new = _DeviceRows(self.device, max(rows, 2 * self.state.shape[0]), -(-max(kmax, 1) // 1024) * 1024, cap_w)
+        new.state[:self.state.shape[0]] = self.state
+        new.cap_meta[:CAP_FLAGS + self.state.shape[0]] = self.cap_meta
+        new.cap_data[:, :self.cap_data.shape[1]] = self.cap_data
+        new.epoch = self.epoch
+        return new
+
+    def take(self, n: int, wait: bool):
+        """Start copying the first n state rows to the host, then clear them and open a new capture epoch, in stream
+        order on the current stream.  wait: return the host rows; else return None and keep them in flight."""
+        stream = torch.cuda.current_stream(self.device)
+        if wait:
+            host = self.state[:n].to("cpu")
+        else:
+            host = torch.empty((n, STATE_COLS), dtype=torch.int64, pin_memory=True)
+            host.copy_(self.state[:n], non_blocking=True)
+        self.state[:n].zero_()
+        self.epoch += 1
+        self.cap_meta[1:2].add_(1 << EPOCH_SHIFT)
+        self.cap_meta[CAP_FLAGS:CAP_FLAGS + n].zero_()
+        if wait:
+            return host
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        self.in_flight = (host, ev)
+        return None
+
+    def landed(self, block: bool):
+        """The host rows of the snapshot in flight once they have arrived (block: wait for them), else None."""
+        if self.in_flight is None:
+            return None
+        host, ev = self.in_flight
+        if block:
+            ev.synchronize()
+        elif not ev.query():
+            return None
+        self.in_flight = None
+        return host
+
+
 class ServeGuard:
-    """Always-on checks for inference (serve.py:548-).  attach(model) checks every bf16/fp16 nn.Linear; poll()
-    reads the per-layer state back (asynchronously unless wait=True) and returns alerts."""
+    """Always-on checks for inference (the reference's serve.ServeGuard, serve.py:548-1170, for its checksum leg).
+
+    attach(model) checks every bf16/fp16 nn.Linear through a forward hook (the layer's own forward runs unchanged);
+    poll() reads the per-layer worst scores back without stalling the GPU and returns the alerts; detach() removes
+    the hooks.  check(slot, x, y) / op_args(slot) serve callers that run the layer themselves (a vLLM linear
+    method)."""
 
     def __init__(self, z: float = 6.0, block: int = 128, abs_floor: float = ABS_FLOOR,
                  on_alert: Optional[Callable[[SDCEvent], None]] = None):
@@ -357,12 +397,9 @@ class ServeGuard:
         self.z, self.block, self.abs_floor = z, int(block), abs_floor
         self.on_alert = on_alert
         self.enabled = True
-        self.layers: list = []
-        self._state: dict = {}
-        self._cap: dict = {}
+        self.layers: list = []                 # per slot: name, module, cs, device, hook handle
+        self._rows: dict = {}                  # device -> _DeviceRows
         self._cap_w = max(128, int(block))
-        self._host: dict = {}
-        self._epoch: dict = {}
         self.worst_seen: dict = {}
         self.checks_seen: dict = {}
         self.unjudged_seen: dict = {}
@@ -371,221 +408,187 @@ class ServeGuard:
         self.stats = {"layers": 0, "skipped_layers": 0, "polls": 0, "alerts": 0, "checks_executed": 0,
                       "unjudged_checksums": 0}
 
-    # ---------------------------------------------------------------- setup
+    # ---------------------------------------------------------------- layers
+    @staticmethod
+    def _why_not(mod: torch.nn.Module) -> Optional[str]:
+        if getattr(mod, "_sdcguard_slot", None):
+            return "already checked by another ServeGuard"
+        w = getattr(mod, "weight", None)
+        if not torch.is_tensor(w) or w.dtype not in UNIT_ROUNDOFF or w.numel() == 0:
+            return f"{getattr(w, 'dtype', None)} weights or no weights: not checked"
+        if not w.is_cuda:
+            return "weights not on a GPU: not checked"
+        if "forward" in mod.__dict__ or type(mod).forward is not torch.nn.Linear.forward:
+            return "forward replaced: its output need not be x W^T + b, not checked"
+        return None
+
     def attach(self, model: torch.nn.Module, share: float = 1.0, offset: int = 0) -> "ServeGuard":
-        i = 0
+        """Check every eligible nn.Linear of `model` (a golden-ratio spread `share` of them)."""
+        eligible = 0
         for name, mod in model.named_modules():
             if not isinstance(mod, torch.nn.Linear):
                 continue
             label = name or type(mod).__name__
-            if getattr(mod, "_sdcguard_slot", None):
-                self.unsupported[label] = "already checked by another ServeGuard"
+            why = self._why_not(mod)
+            if why is not None:
+                self.unsupported[label] = why
+                self.stats["skipped_layers"] += why != "already checked by another ServeGuard"
                 continue
-            if mod.weight.dtype not in UNIT_ROUNDOFF or mod.weight.numel() == 0:
-                self.unsupported[label] = f"{mod.weight.dtype} weights or no weights: not checked"
-                self.stats["skipped_layers"] += 1
-                continue
-            if type(mod).forward is not torch.nn.Linear.forward or "forward" in mod.__dict__:
-                self.unsupported[label] = "forward replaced: not checked"
-                self.stats["skipped_layers"] += 1
-                continue
-            take = select_layer(i, share, offset)
-            i += 1
-            if not take:
+            chosen = select_layer(eligible, share, offset)
+            eligible += 1
+            if not chosen:
                 self.stats["skipped_layers"] += 1
                 continue
             slot = self.add_layer(mod, label)
-            mod.forward = self._make_forward(mod)
-            self.layers[slot]["took_over"] = True
+            self.layers[slot]["hook"] = mod.register_forward_hook(self._hook(slot))
         return self
 
     def add_layer(self, mod: torch.nn.Module, name: str, weight: Optional[torch.Tensor] = None,
                   bias: Optional[torch.Tensor] = None) -> int:
+        """Register a layer (its constants are built now) and return its slot; no hook is installed."""
         w = mod.weight if weight is None else weight
         b = getattr(mod, "bias", None) if bias is None else bias
         with torch.inference_mode(False), torch.no_grad():
             cs = LayerChecksums(w, b, self.block)
-            slot = len(self.layers)
-            if not name or any(lay["name"] == name for lay in self.layers):
-                name = f"{name or type(mod).__name__}#{slot + 1}"
-            self.layers.append({"name": name, "module": mod, "cs": cs, "device": w.device})
-            mod._sdcguard_slot = slot + 1
-            mod._sdcguard_name = name
-            self._grow(w.device)
+        slot = len(self.layers)
+        taken = {lay["name"] for lay in self.layers}
+        if not name or name in taken:
+            name = f"{name or type(mod).__name__}#{slot + 1}"
+        self.layers.append({"name": name, "module": mod, "cs": cs, "device": w.device, "hook": None})
+        mod._sdcguard_slot = slot + 1
+        mod._sdcguard_name = name
+        kmax = max(lay["cs"].k for lay in self.layers if lay["device"] == w.device)
+        rows = self._rows.get(w.device)
+        if rows is None:
+            self._rows[w.device] = _DeviceRows(w.device, 4096, -(-max(kmax, 8192) // 1024) * 1024, self._cap_w)
+        elif not rows.fits(slot + 1, kmax, self._cap_w):
+            self._rows[w.device] = rows.enlarged(slot + 1, kmax, self._cap_w)
         self.stats["layers"] += 1
         return slot
 
-    def _grow(self, device: torch.device) -> None:
-        n = len(self.layers)
-        kmax = max([lay["cs"].k for lay in self.layers if lay["device"] == device] or [1])
-        st = self._state.get(device)
-        if st is None or st.shape[0] < n:
-            new = torch.zeros(max(4096, 2 * n), STATE_COLS, device=device, dtype=torch.int64)
-            if st is not None:
-                new[:st.shape[0]] = st
-            _static(new)
-            self._state[device] = new
-        st = self._state[device]
-        cm, cd = self._cap.get(device, (None, None))
-        if cm is None or cm.numel() < CAP_FLAGS + st.shape[0]:
-            new = torch.zeros(CAP_FLAGS + st.shape[0], device=device, dtype=torch.int64)
-            if cm is not None:
-                new[:cm.numel()] = cm
-            cm = new
-        if cd is None or cd.shape[1] < self._cap_w + kmax:
-            new = torch.zeros(CAPTURE_SLOTS + 1, self._cap_w + max(8192, -(-kmax // 1024) * 1024), device=device,
-                              dtype=torch.float32)
-            if cd is not None:
-                new[:, :cd.shape[1]] = cd
-            cd = new
-        self._cap[device] = (cm, cd)
+    def _hook(self, slot: int):
+        cs = self.layers[slot]["cs"]
+
+        def after_forward(mod, args, out):
+            if not self.enabled or not args or not torch.is_tensor(out) or out.dtype != cs.dtype:
+                return None
+            x = args[0]
+            if not torch.is_tensor(x) or x.numel() == 0 or x.shape[-1] != cs.k or out.shape[-1] != cs.n:
+                return None
+            run = _op() if torch.compiler.is_compiling() else check_static_impl
+            run(x.reshape(-1, cs.k), out.reshape(-1, cs.n), *self.op_args(slot, True))
+            return None
+
+        return after_forward
 
     def state(self, device) -> torch.Tensor:
         device = torch.device(device)
         if device.type == "cuda" and device.index is None:
             device = torch.device("cuda", torch.cuda.current_device())
-        return self._state[device]
+        return self._rows[device].state
 
     def op_args(self, slot: int, with_bias: bool = True) -> tuple:
+        """The op's arguments after x2 and y2 for layer `slot` (constants, state, slot, z, floor, capture area)."""
         lay = self.layers[slot]
-        cm, cd = self._cap[lay["device"]]
-        tag = (slot + 1) * 2 + (1 if with_bias and lay["cs"].has_bias else 0)
-        return (*lay["cs"].tensors(with_bias), self._state[lay["device"]], slot, float(self.z), float(self.abs_floor),
-                cm, cd, self._cap_w, tag)
+        r = self._rows[lay["device"]]
+        tag = 2 * (slot + 1) + int(with_bias and lay["cs"].has_bias)
+        return (*lay["cs"].tensors(with_bias), r.state, slot, self.z, float(self.abs_floor), r.cap_meta, r.cap_data,
+                self._cap_w, tag)
 
     def check(self, slot: int, x: torch.Tensor, y: torch.Tensor, with_bias: bool = True) -> None:
-        """Queue the check of layer `slot` for input x and output y (any leading dims)."""
-        if not self.enabled:
-            return
+        """Queue the check of layer `slot` for its input x and output y (any leading dims); no host sync."""
         cs = self.layers[slot]["cs"]
-        if y.dtype not in UNIT_ROUNDOFF or x.shape[-1] != cs.k or y.shape[-1] != cs.n:
+        if not self.enabled or y.dtype not in UNIT_ROUNDOFF or x.shape[-1] != cs.k or y.shape[-1] != cs.n:
             return
         check_static_impl(x.reshape(-1, cs.k), y.reshape(-1, cs.n), *self.op_args(slot, with_bias))
 
-    def _make_forward(self, mod: torch.nn.Linear):
-        guard, slot = self, mod._sdcguard_slot - 1
-        cs = self.layers[slot]["cs"]
-        op = _op()
-
-        def forward(x):
-            b = mod.bias
-            fused = b is None or x.dim() <= 2 or (x.is_contiguous() and b.dim() == 1 and b.is_contiguous())
-            y = torch.nn.functional.linear(x, mod.weight, b if fused else None)
-            if guard.enabled and x.numel() > 0 and y.dtype == cs.dtype:
-                args = guard.op_args(slot, fused and b is not None)
-                call = op if torch.compiler.is_compiling() else check_static_impl
-                call(x.reshape(-1, cs.k), y.reshape(-1, cs.n), *args)
-            return y if fused else y + b
-
-        return forward
-
     def read_slot(self, slot: int):
-        st = self._state[self.layers[slot]["device"]]
-        return decode_state(st[slot:slot + 1].detach().to("cpu"))[0]
+        """(z, flat index, noise) of one layer's state row now (waits for the GPU)."""
+        lay = self.layers[slot]
+        return decode_state(self._rows[lay["device"]].state[slot:slot + 1])[0]
+
+    def verify_weights(self) -> list:
+        """Names of the layers whose weights no longer hold the bits their constants were built from."""
+        from .recompute import fingerprint
+        return [lay["name"] for lay in self.layers
+                if not torch.equal(fingerprint(lay["module"].weight), lay["cs"].fingerprint)]
 
     # ---------------------------------------------------------------- results
     def poll(self, wait: bool = False) -> list:
-        """Alerts since the last poll.  Without wait it never stalls: it starts a copy of the state and reports
-        the previous copy once it has arrived (serve.py:1090-1129)."""
+        """Alerts since the last poll.  Without wait it never stalls the host: it reports the snapshot started by
+        the previous poll once that has arrived and starts the next one."""
         self.stats["polls"] += 1
+        n = len(self.layers)
         events = []
-        for dev, st in self._state.items():
-            n = len(self.layers)
+        for dev, rows in self._rows.items():
+            done = rows.landed(block=wait)
+            if done is not None:
+                events += self._report(dev, done)
             if wait:
-                pending = self._host.pop(dev, None)
-                if pending is not None:
-                    pending[1].synchronize()
-                    events += self._report(dev, pending[0])
-                host = st[:n].detach().to("cpu", copy=True)
-                st[:n].zero_()
-                self._next_epoch(dev, n)
-                events += self._report(dev, host)
-                continue
-            pending = self._host.get(dev)
-            if pending is not None and pending[1].query():
-                events += self._report(dev, pending[0])
-                self._host.pop(dev, None)
-                pending = None
-            if pending is None:
-                buf = torch.empty((n, STATE_COLS), dtype=st.dtype, pin_memory=True)
-                buf.copy_(st[:n], non_blocking=True)
-                st[:n].zero_()
-                self._next_epoch(dev, n)
-                ev = torch.cuda.Event()
-                ev.record(torch.cuda.current_stream(dev))
-                self._host[dev] = (buf, ev)
+                events += self._report(dev, rows.take(n, wait=True))
+            elif rows.in_flight is None:
+                rows.take(n, wait=False)
         return events
-
-    def _next_epoch(self, dev, n: int) -> None:
-        cap = self._cap.get(dev)
-        if cap is not None:
-            cap[0][1:2].add_(1 << EPOCH_SHIFT)
-            cap[0][CAP_FLAGS:CAP_FLAGS + n].zero_()
-        self._epoch[dev] = self._epoch.get(dev, 0) + 1
 
     def mark_step(self, step: int, rows: Optional[int] = None) -> None:
+        """Stamp the capture area with the serving step (kept rows carry it)."""
         step = int(step) & STEP_MASK
-        for dev in set(self._state) | set(self._cap):
-            cap = self._cap.get(dev)
-            if cap is not None:
-                cap[0][1:2].fill_((self._epoch.get(dev, 0) << EPOCH_SHIFT) | step)
+        for r in self._rows.values():
+            r.cap_meta[1:2].fill_((r.epoch << EPOCH_SHIFT) | step)
 
     def _report(self, dev, host: torch.Tensor) -> list:
-        events = []
-        rows = decode_state(host)
+        out = []
+        keys = decode_state(host)
         counts = decode_counts(host)
-        slots = [i for i, lay in enumerate(self.layers) if lay["device"] == dev and i < host.shape[0]]
-        for slot in slots:
-            name = self.layers[slot]["name"]
-            z, flat, nz = rows[slot]
-            checks, unj = counts[slot]
+        for slot, lay in enumerate(self.layers):
+            if lay["device"] != dev or slot >= host.shape[0]:
+                continue
+            name, cs = lay["name"], lay["cs"]
+            z, flat, noise = keys[slot]
+            checks, unjudged = counts[slot]
             self.checks_seen[name] = self.checks_seen.get(name, 0) + checks
-            self.unjudged_seen[name] = self.unjudged_seen.get(name, 0) + unj
+            self.unjudged_seen[name] = self.unjudged_seen.get(name, 0) + unjudged
             self.stats["checks_executed"] += checks
-            self.stats["unjudged_checksums"] += unj
+            self.stats["unjudged_checksums"] += unjudged
             self.worst_seen[name] = max(self.worst_seen.get(name, 0.0), z)
-            if z > self.z:
-                cs = self.layers[slot]["cs"]
-                bi = flat // 2
-                ev = SDCEvent(detector="serve_checksum", layer=name, z=z, row=bi // cs.nb, col_block=bi % cs.nb,
-                              noise=nz, nonfinite=not math.isfinite(z) or nz != nz,
-                              extra={"checksum": "signed" if flat % 2 else "plain"})
-                events.append(ev)
-                self.events.append(ev)
-                self.stats["alerts"] += 1
-                if self.on_alert is not None:
-                    self.on_alert(ev)
-        return events
+            if not z > self.z:
+                continue
+            blk = flat >> 1
+            ev = SDCEvent(detector="serve_checksum", layer=name, z=z, row=blk // cs.nb, col_block=blk % cs.nb,
+                          noise=noise, nonfinite=not math.isfinite(z) or noise != noise,
+                          extra={"checksum": "signed" if flat & 1 else "plain"})
+            out.append(ev)
+            self.events.append(ev)
+            self.stats["alerts"] += 1
+            if self.on_alert is not None:
+                self.on_alert(ev)
+        return out
 
     def captured(self, dev) -> list:
-        """(record, y block, x row) of every row the capture buffer kept on a device (waits for the GPU)."""
-        cm, cd = self._cap[torch.device(dev)]
-        head = cm[:CAP_FLAGS].cpu()
-        n = min(int(head[0]), CAPTURE_SLOTS)
-        recs = head[CAP_HEAD:CAP_FLAGS].view(CAPTURE_SLOTS + 1, CAP_REC)[:n].tolist()
-        data = cd[:n].cpu()
+        """(record, y block, x row) of every row kept on a device in the current epoch (waits for the GPU)."""
+        r = self._rows[torch.device(dev)]
+        meta = r.cap_meta[:CAP_FLAGS].to("cpu")
+        kept = min(int(meta[0]), CAPTURE_SLOTS)
+        recs = meta[CAP_HEAD:CAP_HEAD + kept * CAP_REC].view(kept, CAP_REC).tolist()
+        data = r.cap_data[:kept].to("cpu")
         out = []
-        for i, r in enumerate(recs):
-            slot = r[0] // 2 - 1
-            cs = self.layers[slot]["cs"]
-            width = cs.bs if r[2] < cs.nbf else cs.rem
-            out.append((r, data[i, :width], data[i, self._cap_w:self._cap_w + cs.k]))
+        for i, rec in enumerate(recs):
+            cs = self.layers[rec[0] // 2 - 1]["cs"]
+            width = cs.bs if rec[2] < cs.nbf else cs.rem
+            out.append((rec, data[i, :width], data[i, self._cap_w:self._cap_w + cs.k]))
         return out
 
     def detach(self) -> None:
+        """Final poll (waits), then remove the hooks and forget the layers."""
         try:
             if self.layers:
                 self.poll(wait=True)
         finally:
             for lay in self.layers:
-                mod = lay["module"]
-                if lay.get("took_over"):
-                    mod.__dict__.pop("forward", None)
-                mod.__dict__.pop("_sdcguard_slot", None)
-                mod.__dict__.pop("_sdcguard_name", None)
+                if lay.get("hook") is not None:
+                    lay["hook"].remove()
+                for attr in ("_sdcguard_slot", "_sdcguard_name"):
+                    lay["module"].__dict__.pop(attr, None)
             self.layers.clear()
-            self._state.clear()
-            self._host.clear()
-            self._cap.clear()
+            self._rows.clear()
             self.stats["layers"] = 0
-

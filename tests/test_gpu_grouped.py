@@ -131,3 +131,20 @@ def test_moe_4096_tokens_top8_64_experts():
         assert flagged == [e], (e, flagged)
         r = res[nonempty.index(e)]
         assert r.col_block == blk and 0 <= r.row < sizes[e]
+
+
+def test_offsets_out_of_order_and_past_the_rows_decode_consistently():
+    """Offsets are read as the clamped running maximum (both kernels and the decoder): a decreasing entry is an empty
+    group and an entry past the rows is the rows; the results match the per-group checks of those slices, and the
+    epoch keyword reaches the device path."""
+    from sdcguard_amd.checksum import check_grouped_mm, check_matmul, grouped_zscores, resolve_grouped
+    a, b, out, _ = _grouped([40, 30, 50], 128, 136, seed=21)
+    offs = torch.tensor([70, 40, 500], dtype=torch.int32, device="cuda")   # as ends: 70, 70 (empty), 120 (rows)
+    res = resolve_grouped(grouped_zscores(a, b, out, offs))
+    want = [check_matmul(a[0:70], b[0], out[0:70]), check_matmul(a[70:120], b[2], out[70:120])]
+    assert [r.ok for r in res] == [w.ok for w in want]
+    assert [round(r.max_z, 3) for r in res] == pytest.approx([round(w.max_z, 3) for w in want], abs=0.05)
+    offs[0] = 0                                                              # the caller reuses its buffer
+    torch.cuda.synchronize()
+    r2 = check_grouped_mm(a, b, out, torch.tensor([40, 70, 120], device="cuda"), epoch=3)
+    assert len(r2) == 3

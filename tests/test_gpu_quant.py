@@ -173,3 +173,29 @@ def test_fp8_2048x7168x4096_clean_and_faults():
             v ^= (1 << 30)
         res = modes.resolve(modes.quant_zscores(Aq, consts, c, sa=sa))
         assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (i, j // 128), (t, i, j, res)
+
+
+def test_int8_weights_at_minus_128():
+    """int8 weights may hold -128: a block laid against the sign pattern (127 where it is +1, -128 where it is -1)
+    has signed sums near 16384, whose high digit would be 128; the split keeps it at 127 and the check stays exact.
+    The plain sum of a block of -128 entries, -16384, splits as (-128, 0)."""
+    from sdcguard_amd import modes
+    from sdcguard_amd.checksum import sign_table
+    s = sign_table("cpu").view(128, 128)[127].to(torch.int32)              # the width-128 pattern
+    g = torch.Generator(device="cuda").manual_seed(14)
+    B = torch.randint(-127, 128, (512, 256), device="cuda", generator=g, dtype=torch.int32)
+    B[:, 128:] = torch.where(s[None, :].cuda() > 0, torch.full_like(B[:, 128:], 127), -128)
+    B[0, 128] = -127 if s[0] < 0 else 126                                  # 16383 at most in that block
+    B = B.to(torch.int8)
+    A = torch.randint(-127, 128, (64, 512), device="cuda", generator=g, dtype=torch.int32).to(torch.int8)
+    C = (A.double() @ B.double()).to(torch.int32)
+    consts = modes.QuantChecksums.make(B)
+    assert modes.resolve(modes.quant_zscores(A, consts, C))["wrong_blocks"] == 0
+    c = C.clone()
+    c[9, 200] += 1
+    res = modes.resolve(modes.quant_zscores(A, consts, c))
+    assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (9, 1)
+    low = torch.full((128, 256), -128, dtype=torch.int8, device="cuda")
+    A2 = A[:, :128].contiguous()
+    C2 = (A2.double() @ low.double()).to(torch.int32)
+    assert modes.resolve(modes.quant_zscores(A2, modes.QuantChecksums.make(low), C2))["wrong_blocks"] == 0
