@@ -260,7 +260,7 @@ def bench_bf16_mlp(ctx: Ctx) -> dict:
         raise RuntimeError(f"the check did not run: {int(state[2].item())} calls counted of {a.warmup}")
     col, row = resolve_both(state, rows, M, N)
     ms = ctx.loop_ms(check, a.steps)
-    names = ("xstage", "col_gemm", "row_gemm", "ypass")
+    names = ("xstage", "xfinish", "col_gemm", "row_gemm", "ypass")
     km = ctx.kernel_ms(check, a.steps, names)
 
     def gemm(i):
@@ -284,6 +284,8 @@ def bench_bf16_mlp(ctx: Ctx) -> dict:
     patterns = {"xstage": r"xstage_kernel", "ypass": r"ypass_kernel",
                 "row_gemm": r"expected_gemm_kernel<0, 1", "col_gemm": r"expected_gemm_kernel<0, 2"}
     ent, roof = _roof(km, amounts, name, patterns, a.steps)
+    ent["xfinish"] = {"avg_us": round(km["xfinish"][0] * 1e3, 2), "launches_per_step": km["xfinish"][1] / a.steps,
+                      "bound": "latency"}
     value = alg / (ms * 1e-3) / 1e9
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,

@@ -81,19 +81,20 @@ int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t
  *   x (m x k) row stride sxm, W (n x k) row stride swn, y (m x n) row stride sym: bf16 (dtype 0; fp16 returns
  *     SDC_EUNSUPPORTED), k- / n-contiguous; x and y with 16-byte aligned rows and n a multiple of 8 (otherwise
  *     SDC_EUNSUPPORTED: the caller runs the two checks separately).  Blocks are 128 wide.
- *   bias (n) or NULL; parts / spc / block_consts: the layer's constants as for sdc_check_static (k-contiguous
- *     columns spc elements apart; block_consts required); sign_table: the epoch-0 128 x 128 table.
+ *   bias (n) or NULL; parts / spc / block_consts / w_norms: the layer's constants from sdc_layer_constants
+ *     (k-contiguous part columns spc elements apart, the (nb, 12) block table, W's row norms [2][n]);
+ *     sign_table: the epoch-0 128 x 128 table.
  *   state: int64[4] of the column check (sdc_check_static's row, counts on); row_result: int64[3] of the row check
  *     (sdc_matmul_check's result row; flat index ((column * mb + row block) * 2 + signed), mb = ceil(m / 128)).
- *   workspace: sdc_linear_check_workspace(m, k, n) bytes.  col_scores (m, nb, 2) / row_scores (n, mb, 2): every
- *     checksum's score, or NULL.  flags bit 0: run the column check's GEMM on a side stream, concurrently with the
- *     row check's x pass and GEMM. */
+ *   workspace: sdc_linear_check_workspace(m, k, n) bytes.
+ *   col_scores (m, nb, 2) / row_scores (n, mb, 2): every checksum's score, or NULL.  flags bit 0: run the column
+ *     check's GEMM on a side stream, concurrently with the row check's x pass and GEMM. */
 int64_t sdc_linear_check_workspace(int64_t m, int64_t k, int64_t n);
 int sdc_linear_check(int dtype, const void* x, int64_t sxm, const void* W, int64_t swn, const void* y, int64_t sym,
                      const void* bias, int64_t m, int64_t k, int64_t n, const void* parts, int64_t spc,
-                     const float* block_consts, const float* sign_table, int64_t* state, int64_t* row_result,
-                     float z, float abs_floor, void* workspace, int64_t workspace_bytes, float* col_scores,
-                     float* row_scores, int flags, hipStream_t stream);
+                     const float* block_consts, const float* w_norms, const float* sign_table, int64_t* state,
+                     int64_t* row_result, float z, float abs_floor, void* workspace, int64_t workspace_bytes,
+                     float* col_scores, float* row_scores, int flags, hipStream_t stream);
 
 /* ---- check of a MoE grouped GEMM ----------------------------------------------------------------------------
  * Replaces guard._grouped_checks (guard.py:102-143) + one checksum._zscores per group for torch._grouped_mm's
@@ -122,11 +123,14 @@ int sdc_grouped_check(int dtype, const void* A, int64_t sam, int64_t sak, const 
  *   consts_bias, consts_plain: fp32 [nb][12] per block (the scoring pass's table), with and without the bias:
  *     scale (plain, signed), bias block sums (2), |B2 column|_2 (2), max |B2| (2), max |W| of the block,
  *     max |bias| of the block, 0, 0.
+ *   row_norms: fp32 [2][n], |w_j|_2^2 then |w_j|_1 of every row j of W (what sdc_linear_check's row-block check
+ *     takes as w_norms), or NULL.
  *   sign_table: as sdc_check_static.  workspace: sdc_layer_constants_workspace(n, k, bs) bytes. */
 int64_t sdc_layer_constants_workspace(int64_t n, int64_t k, int64_t bs);
 int sdc_layer_constants(int dtype, const void* W, int64_t swn, int64_t n, int64_t k, int64_t bs, const void* bias,
                         int64_t sbias, const float* sign_table, void* parts, int64_t parts_pitch, float* consts_bias,
-                        float* consts_plain, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+                        float* consts_plain, float* row_norms, void* workspace, int64_t workspace_bytes,
+                        hipStream_t stream);
 
 /* ---- check of one quantized GEMM ----------------------------------------------------------------------------
  * Replaces modes.judge (modes.py:231-291) for its int8 and fp8 branches, on the device, and extends the fp8 one to

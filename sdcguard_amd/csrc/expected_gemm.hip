@@ -189,9 +189,20 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
   // XCD-aware order: block b runs on XCD b % 8; give XCD x the x-th eighth of the tiles (column tile fastest)
   const int64_t G = (int64_t)gridDim.x, b = blockIdx.x;
   const int64_t wid = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
-  const int64_t ct = wid % nct, rt = (wid / nct) % nrt, rest = wid / (nct * nrt);
-  const int64_t split = rest % g.splits;
-  int64_t batch = rest / g.splits, r0 = rt * T::TM, m = g.m;
+  int64_t ct, rt, split, batch;
+  if (g.rows_per_xcd) {
+    split = wid % g.splits;
+    ct = (wid / g.splits) % nct;
+    rt = (wid / (g.splits * nct)) % nrt;
+    batch = wid / (g.splits * nct * nrt);
+  } else {
+    ct = wid % nct;
+    rt = (wid / nct) % nrt;
+    const int64_t rest = wid / (nct * nrt);
+    split = rest % g.splits;
+    batch = rest / g.splits;
+  }
+  int64_t r0 = rt * T::TM, m = g.m;
   if (g.goffs) {
     // grouped rows: find the group whose row tiles contain tile rt (every thread walks the same offsets)
     int64_t start = 0, acc = 0, grp = -1;
@@ -214,7 +225,7 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
   const int64_t kbeg = split * g.kchunk;
   const int64_t kend = kbeg + g.kchunk < g.k ? kbeg + g.kchunk : g.k;
   const int nst = kbeg < kend ? (int)sdc_cdiv(kend - kbeg, KS) : 0;
-  const bool norms = ct == 0;
+  const bool norms = ct == 0 && g.XN != nullptr;      // (a caller with the row norms already passes no XN)
   const int64_t N = g.N, me = g.m;      // me: rows of E and XN (the global row count)
   const uint8_t* Ab = (const uint8_t*)g.A + (g.goffs ? 0 : batch * g.sab * ESA);
   const uint16_t* Pb = (const uint16_t*)g.B + batch * g.sbb;

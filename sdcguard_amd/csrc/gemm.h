@@ -19,6 +19,10 @@ struct GemmArgs {
   const int64_t* goffs;
   int64_t ngroups;
   float* XN;                    // [batch][split][2][m]: sum of squares and sum of |a| of each row's depth slice
+  // 0: each XCD takes one depth slice of every row tile (its slice of the parts stays in its L2); 1: each XCD
+  // takes every depth slice of some row tiles (its rows' 128-byte lines stay in its L2 between the two stages that
+  // read their halves: for a tall A read once, whose parts fit one L2 whole)
+  int rows_per_xcd;
 };
 
 // E and XN for `batches` batches.

@@ -7,13 +7,16 @@
 // transposed operands): for every column j and block of 128 rows, sum_i y_ij against W_j . (sum_i x_i), scored as
 // the training check scores it (unjudged checksums score -1).
 //
-// Four launches, no host synchronisation:
+// Five launches, no host synchronisation:
 //   1. xstage: the plain and signed sums of every 128-row block of x, split into three bf16 parts (the B operand
-//      of the row check's GEMM), and per 256-deep chunk partial statistics of those sums and of |x|;
-//   2. the row check's GEMM E_row = W @ (x block sums) on MFMA, plus W's row norms (expected_gemm.hip);
-//   3. the column check's GEMM E_col = x @ B2 on MFMA, plus x's row norms -- independent of 1 and 2, so it can
-//      run on a side stream concurrently with them;
-//   4. ypass: one read of y.  A workgroup owns a 128 x 128 tile (one row block by one column block): every thread
+//      of the row check's GEMM), and per 256-deep chunk partials of those sums' statistics and of x's row norms;
+//   2. xfinish: those partials added up in chunk order (the column check's |x_i|_2^2 and |x_i|_1, the row blocks'
+//      statistics and sign-pattern sums);
+//   3. the row check's GEMM E_row = W @ (x block sums) on MFMA (expected_gemm.hip; W's row norms are the layer's,
+//      made once by sdc_layer_constants);
+//   4. the column check's GEMM E_col = x @ B2 on MFMA -- independent of 1 to 3, so it can run on a side stream
+//      concurrently with them;
+//   5. ypass: one read of y.  A workgroup owns a 128 x 128 tile (one row block by one column block): every thread
 //      reads 8 rows x 8 columns (eight 16-byte loads, all in flight), adds the four sums (plain, signed, squares,
 //      |values|) of its rows with packed dot products and those of its columns by pairing two rows' values of a
 //      column into one packed operand; the 16 lanes sharing the rows add theirs with DPP steps, the column partials
@@ -35,6 +38,7 @@ namespace {
 constexpr int BS = 128;            // block width of both checks
 constexpr int XK = 256;            // depth per xstage workgroup
 constexpr int NXS = 5;             // partial stats per (depth chunk, row block): sq0, sq1, max0, max1, max|x|
+constexpr int RST = 8;             // final stats per row block: the NXS above, then the sum of its sign pattern
 
 __device__ __forceinline__ float nan_abs(float v) { return v == v ? fabsf(v) : __builtin_inff(); }
 
@@ -48,19 +52,25 @@ __device__ __forceinline__ uint16_t bf16_rne(float f) {
 // ---------------------------------------------------------------------------------------- 1. x block sums
 struct XStageArgs {
   const uint16_t* x;
-  int64_t sxm, m, k, kp, mb, rem;
+  int64_t sxm, m, k, kp, mb, rem, nkc;
   const float* s_full;             // sign pattern of a full row block (128), and of the last (rem) one
   const float* s_last;
   uint16_t* parts;                 // [3][2 mb][kp] bf16: hi, mid, lo of (plain, signed) per row block
-  float* stats;                    // [nkc][mb][NXS]
+  float* stats;                    // [nkc][mb][NXS] partial statistics of the sums, per depth chunk
+  float* xnp;                      // [nkc][2][m] partial |x_i|_2^2, |x_i|_1 per depth chunk
+  float* xn;                       // [2][m] |x_i|_2^2, |x_i|_1 (the column check's A norms)
+  float* rstat;                    // [mb][RST]: sq0, sq1, max0, max1, max |x|, sum of the block's pattern
 };
 
 // One workgroup: one row block (128 rows) by 256 consecutive depths.  Thread t reads depths 8 (t % 32) .. +8 of
-// rows t / 32 + 8 i (i < 16): sixteen 16-byte loads, a wave covering two rows of 512 contiguous bytes each; LDS
-// adds the eight row groups; thread t then owns depth t: its two sums become three bf16 parts (checksum._split3),
-// stored k-contiguous per checksum column.
+// rows t / 32 + 8 i (i < 16): sixteen 16-byte loads, a wave covering two rows of 512 contiguous bytes each.  LDS
+// adds the eight row groups' depth sums; thread t then owns depth t: its two sums become three bf16 parts
+// (checksum._split3), stored k-contiguous per checksum column.  The same registers give each row's |x|_2^2 and
+// |x|_1 over the 256 depths (packed dot products; LDS adds the 32 lanes of a row), written per depth chunk for
+// xfinish_kernel to add up.
 __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
   __shared__ float red[2][8][XK + 4];
+  __shared__ float nrm[2][BS][33];
   __shared__ float wst[4][NXS];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int dc = t & 31, rg = t >> 5;
@@ -69,9 +79,12 @@ __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
   const int wid = (int)((ib == a.mb - 1 && a.rem > 0) ? a.rem : BS);
   const float* sp = (ib == a.mb - 1 && a.rem > 0) ? a.s_last : a.s_full;
   const uint16_t* base = a.x + (ib * BS) * a.sxm + k0;
-  float pl[8], sg[8], mx = 0.f;
+  constexpr uint32_t ONES = 0x3F803F80u;
+  float pl[8], sg[8], mx = 0.f, rsq[16], rab[16];
 #pragma unroll
   for (int e = 0; e < 8; ++e) pl[e] = sg[e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) rsq[i] = rab[i] = 0.f;
   if (k0 + 8 <= a.k) {
     // a full block loads unconditionally (a guarded load would make the compiler wait for it inside the guard);
     // rows past a narrower last block read row 0 of the block and are weighted 0
@@ -86,13 +99,17 @@ __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
       const int r = rg + 8 * i;
       const float s = sp[r];                      // (0 past the pattern's width)
       if (r >= wid) v[i] = u32x4{0u, 0u, 0u, 0u};
-      const float xv[8] = {bf16_lo(v[i].x), bf16_hi(v[i].x), bf16_lo(v[i].y), bf16_hi(v[i].y),
-                           bf16_lo(v[i].z), bf16_hi(v[i].z), bf16_lo(v[i].w), bf16_hi(v[i].w)};
+      const uint32_t ww[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pl[e] += xv[e];
-        sg[e] = fmaf(xv[e], s, sg[e]);
-        mx = fmaxf(mx, nan_abs(xv[e]));
+      for (int q = 0; q < 4; ++q) {
+        rsq[i] = dot2<SDC_BF16>(ww[q], ww[q], rsq[i]);
+        rab[i] = dot2<SDC_BF16>(ww[q] & 0x7FFF7FFFu, ONES, rab[i]);
+        const float x0 = bf16_lo(ww[q]), x1 = bf16_hi(ww[q]);
+        pl[2 * q] += x0;
+        pl[2 * q + 1] += x1;
+        sg[2 * q] = fmaf(x0, s, sg[2 * q]);
+        sg[2 * q + 1] = fmaf(x1, s, sg[2 * q + 1]);
+        mx = fmaxf(mx, fmaxf(nan_abs(x0), nan_abs(x1)));
       }
     }
   } else if (k0 < a.k) {
@@ -107,6 +124,8 @@ __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
         pl[e] += xv;
         sg[e] = fmaf(xv, s, sg[e]);
         mx = fmaxf(mx, nan_abs(xv));
+        rsq[i] = fmaf(xv, xv, rsq[i]);
+        rab[i] += fabsf(xv);
       }
     }
   }
@@ -116,6 +135,11 @@ __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
     red[1][rg][8 * dc + e] = sg[e];
   }
 #pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    nrm[0][rg + 8 * i][dc] = rsq[i];
+    nrm[1][rg + 8 * i][dc] = rab[i];
+  }
+#pragma unroll
   for (int msk = 1; msk < 64; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
   __syncthreads();
   float P = 0.f, S = 0.f;
@@ -123,6 +147,15 @@ __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
   for (int g = 0; g < 8; ++g) {
     P += red[0][g][t];
     S += red[1][g][t];
+  }
+  {
+    // this chunk's partial norm of row t / 2 (t % 2: squares, |values|), lanes in depth order
+    const int r = t >> 1, c = t & 1;
+    float acc = 0.f;
+#pragma unroll
+    for (int d = 0; d < 32; ++d) acc += nrm[c][r][d];
+    const int64_t row = ib * BS + r;
+    if (r < wid) a.xnp[(kc * 2 + c) * a.m + row] = acc;
   }
   const int64_t kk = kc * XK + t;
   const bool mine = kk < a.k;
@@ -162,6 +195,46 @@ __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
   }
 }
 
+// The depth chunks' partials of one row block added up in chunk order (so the result is the same on every run):
+// the rows' |x|_2^2 and |x|_1 (thread t: row t / 2, t % 2 the statistic), the block sums' statistics (wave 1), the
+// sum of the block's sign pattern (wave 2).
+__global__ __launch_bounds__(256) void xfinish_kernel(XStageArgs a) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t ib = blockIdx.x;
+  const int wid = (int)((ib == a.mb - 1 && a.rem > 0) ? a.rem : BS);
+  const float* sp = (ib == a.mb - 1 && a.rem > 0) ? a.s_last : a.s_full;
+  {
+    const int r = t >> 1, c = t & 1;
+    const int64_t row = ib * BS + (r < wid ? r : 0);
+    float acc = 0.f;
+    for (int64_t q0 = 0; q0 < a.nkc; q0 += 8) {
+      float p[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p[j] = a.xnp[((q0 + j < a.nkc ? q0 + j : a.nkc - 1) * 2 + c) * a.m + row];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (q0 + j < a.nkc) acc += p[j];
+    }
+    if (r < wid) a.xn[c * a.m + row] = acc;
+  }
+  if (w == 1) {
+    const int i = lane < NXS ? lane : 0;
+    float v = 0.f;
+    for (int64_t q0 = 0; q0 < a.nkc; q0 += 8) {
+      float p[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p[j] = a.stats[((q0 + j < a.nkc ? q0 + j : a.nkc - 1) * a.mb + ib) * NXS + i];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (q0 + j < a.nkc) v = i < 2 ? v + p[j] : fmaxf(v, p[j]);
+    }
+    if (lane < NXS) a.rstat[ib * RST + lane] = v;
+  } else if (w == 2) {
+    const float ss = wave_sum_f32((lane < wid ? sp[lane] : 0.f) + (lane + 64 < wid ? sp[lane + 64] : 0.f));
+    if (lane == 0) a.rstat[ib * RST + NXS] = ss;
+  }
+}
+
 // --------------------------------------------------------------------------------------------- 4. the y pass
 struct YArgs {
   const uint16_t* y;
@@ -169,17 +242,16 @@ struct YArgs {
   const float* sign_table;         // 128 x 128, row w - 1 = the pattern of width w
   // column-block check (serving flavour)
   const float* Ecol;               // [scol][2 nb][m] (transposed planes)
-  const float* XN;                 // [scol][2][m]: |x_i|_2^2, |x_i|_1
+  const float* xn;                 // [2][m]: |x_i|_2^2, |x_i|_1
   int64_t scol;
   const f32x4* consts;             // (nb, 12) packed per-block constants of the layer
   int64_t* state;                  // int64[4]: key, key with noise, checks, unjudged
   float* zcol;                     // (m, nb, 2) scores or null
   // row-block check (training flavour)
   const float* Erow;               // [srow][2 mb][n]
-  const float* WN;                 // [srow][2][n]
+  const float* wn;                 // [2][n]: |w_j|_2^2, |w_j|_1
   int64_t srow;
-  const float* xstats;             // [nkc][mb][NXS]
-  int64_t nkc;
+  const float* rstat;              // [mb][RST]: the row blocks' statistics (xstage)
   const uint16_t* bias;            // (n) or null
   int64_t* result;                 // int64[3]: key, key with noise, unjudged
   float* zrow;                     // (n, mb, 2) scores or null
@@ -226,9 +298,6 @@ template <int DT>
 __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
   __shared__ f32x4 colp[BS][17];                // column partials [column][row group, rotated], padded
   __shared__ f32x4 rows[BS];                    // the tile's row sums
-  __shared__ float rstat[NXS];                  // the row block's B-side statistics
-  __shared__ float xpart[256];
-  __shared__ float rsign;                       // the row block's pattern sum (for the bias)
   __shared__ int64_t red_k[4], red_d[4];
   __shared__ int red_u[4];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
@@ -263,40 +332,26 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
   if (colside) {
     const int Rc = R < m ? R : m - 1;
     ebase = a.Ecol + (int64_t)(2 * jb) * a.m + Rc; estride = a.m; pstride = 2 * a.nb * a.m;
-    nbase = a.XN + Rc; nstride = a.m; splits = a.scol;
+    nbase = a.xn + Rc; nstride = a.m; splits = a.scol;
   } else {
     const int Jc = J < n ? J : n - 1;
     ebase = a.Erow + (int64_t)(2 * ib) * a.n + Jc; estride = a.n; pstride = 2 * a.mb * a.n;
-    nbase = a.WN + Jc; nstride = a.n; splits = a.srow;
+    nbase = a.wn + Jc; nstride = a.n; splits = a.srow;
   }
-  float ev[SDC_MAX_SPLITS][4];
+  float ev[SDC_MAX_SPLITS][2];
 #pragma unroll
   for (int s = 0; s < SDC_MAX_SPLITS; ++s) {
     const int64_t sc = s < splits ? s : 0;
     ev[s][0] = ebase[sc * pstride];
     ev[s][1] = ebase[sc * pstride + estride];
-    ev[s][2] = nbase[sc * 2 * nstride];
-    ev[s][3] = nbase[sc * 2 * nstride + nstride];
   }
+  const float asq = nbase[0], asum = nbase[nstride];
   const float bj = (!colside && a.bias) ? half_to_f32<DT>(a.bias[J < n ? J : n - 1]) : 0.f;
-
-  // the row block's statistics: the depth chunks' partials, loaded in parallel and added in LDS
-  const int nst = (int)a.nkc * NXS;
-  constexpr int XCH = 255;                     // partials per round: a multiple of NXS
-  for (int base = 0; base < nst; base += XCH) {
-    if (t < XCH && base + t < nst) {
-      const int i = base + t;
-      xpart[t] = a.xstats[((int64_t)(i / NXS) * a.mb + ib) * NXS + i % NXS];
-    }
-    __syncthreads();
-    if (t < NXS) {
-      float acc = base == 0 ? 0.f : rstat[t];        // (sums of squares, and maxima of values >= 0)
-      const int cnt = nst - base < XCH ? nst - base : XCH;
-      for (int j = t; j < cnt; j += NXS) acc = t < 2 ? acc + xpart[j] : fmaxf(acc, xpart[j]);
-      rstat[t] = acc;
-    }
-    __syncthreads();
-  }
+  // the row block's statistics (complete: xstage's last chunk added them up) and the sum of its pattern
+  const f32x4 rst0 = *reinterpret_cast<const f32x4*>(a.rstat + (int64_t)ib * RST);
+  const f32x4 rst1 = *reinterpret_cast<const f32x4*>(a.rstat + (int64_t)ib * RST + 4);
+  const float rstat[NXS] = {rst0.x, rst0.y, rst0.z, rst0.w, rst1.x};
+  const float rsign = rst1.y;
 
   // ---- signs: this thread's 8 columns of the column block's pattern, its 8 rows of the row block's pattern
   const float* spc = a.sign_table + (wc - 1) * 128;
@@ -311,10 +366,6 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
     scol2[2] = pack_signs<DT>(cb.x, cb.y); scol2[3] = pack_signs<DT>(cb.z, cb.w);
     srow2[0] = pack_signs<DT>(ra.x, ra.y); srow2[1] = pack_signs<DT>(ra.z, ra.w);
     srow2[2] = pack_signs<DT>(rb.x, rb.y); srow2[3] = pack_signs<DT>(rb.z, rb.w);
-  }
-  if (w == 0) {
-    const float ss = wave_sum_f32(spr[lane] + spr[lane + 64]);
-    if (lane == 0) rsign = ss;
   }
   constexpr uint32_t ONES = DT == SDC_BF16 ? 0x3F803F80u : 0x3C003C00u;
 
@@ -373,14 +424,12 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
   __syncthreads();
 
   // ---- scoring
-  float e0 = ev[0][0], e1 = ev[0][1], asq = ev[0][2], asum = ev[0][3];
+  float e0 = ev[0][0], e1 = ev[0][1];
 #pragma unroll
   for (int s = 1; s < SDC_MAX_SPLITS; ++s)
     if (s < splits) {
       e0 += ev[s][0];
       e1 += ev[s][1];
-      asq += ev[s][2];
-      asum += ev[s][3];
     }
   Best best;
   if (colside) {
@@ -470,7 +519,7 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
 
 struct Layout {
   int64_t nb, mb, rem_n, rem_m, nkc, kp, scol, srow;
-  int64_t off_parts, off_stats, off_erow, off_wn, off_ecol, off_xn, total;   // in floats
+  int64_t off_parts, off_stats, off_xnp, off_xn, off_rstat, off_erow, off_ecol, total;   // in floats
 };
 
 Layout layout(int64_t m, int64_t k, int64_t n) {
@@ -487,10 +536,11 @@ Layout layout(int64_t m, int64_t k, int64_t n) {
   int64_t o = 0;
   L.off_parts = o; o += al((3 * 2 * L.mb * L.kp + 1) / 2);
   L.off_stats = o; o += al(L.nkc * L.mb * NXS);
+  L.off_xnp = o; o += al(L.nkc * 2 * m);
+  L.off_xn = o; o += al(2 * m);
+  L.off_rstat = o; o += al(L.mb * RST);
   L.off_erow = o; o += al(L.srow * 2 * L.mb * n);
-  L.off_wn = o; o += al(L.srow * 2 * n);
   L.off_ecol = o; o += al(L.scol * 2 * L.nb * m);
-  L.off_xn = o; o += al(L.scol * 2 * m);
   L.total = o;
   return L;
 }
@@ -504,14 +554,15 @@ extern "C" int64_t sdc_linear_check_workspace(int64_t m, int64_t k, int64_t n) {
 
 extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const void* W, int64_t swn, const void* y,
                                 int64_t sym, const void* bias, int64_t m, int64_t k, int64_t n, const void* parts,
-                                int64_t spc, const float* block_consts, const float* sign_table, int64_t* state,
-                                int64_t* row_result, float z, float abs_floor, void* workspace,
+                                int64_t spc, const float* block_consts, const float* w_norms, const float* sign_table,
+                                int64_t* state, int64_t* row_result, float z, float abs_floor, void* workspace,
                                 int64_t workspace_bytes, float* col_scores, float* row_scores, int flags,
                                 hipStream_t stream) {
   SDC_CLEAR_ERRORS();
   if (m < 1 || n < 1 || k < 1) return SDC_EINVAL;
   if (dtype != SDC_BF16) return SDC_EUNSUPPORTED;               // (fp16: the separate checks)
-  if (!x || !W || !y || !parts || !block_consts || !sign_table || !state || !row_result) return SDC_EINVAL;
+  if (!x || !W || !y || !parts || !block_consts || !w_norms || !sign_table || !state || !row_result)
+    return SDC_EINVAL;
   if (n % 8 || sym % 8 || sxm % 8 || ((uintptr_t)y | (uintptr_t)x | (uintptr_t)block_consts) % 16)
     return SDC_EUNSUPPORTED;                                    // x and y are read in 16-byte pieces
   const Layout L = layout(m, k, n);
@@ -521,34 +572,42 @@ extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const voi
   const float* s_full = sign_table + (BS - 1) * 128;
   const bool concurrent = (flags & 1) != 0;
 
-  // 3. (side stream when asked) the column check's GEMM: E_col = x @ B2 parts, x's row norms
+  // 3. (side stream when asked) the column check's GEMM: E_col = x @ B2 parts (x's row norms come from xstage)
   hipStream_t side = stream;
   if (concurrent && !(side = sdc_fork(stream))) return SDC_ELAUNCH;
   GemmArgs gc{};
   gc.A = (const uint16_t*)x; gc.sab = 0; gc.sam = sxm; gc.sak = 1;
   gc.B = parts; gc.sbb = 0; gc.sbc = spc;
   gc.m = m; gc.k = k; gc.N = 2 * L.nb; gc.splits = L.scol;
-  gc.E = ws + L.off_ecol; gc.XN = ws + L.off_xn; gc.et = 1;
+  gc.E = ws + L.off_ecol; gc.XN = nullptr; gc.et = 1;
   gc.prof_name = "col_gemm";
   int rc = sdc_gemm_launch(SDC_BF16, gc, 1, side);
   if (rc != SDC_OK) return rc;
 
-  // 1. the block sums of x (as three parts) and their statistics
+  // 1. the block sums of x (as three parts), their statistics and x's row norms
   XStageArgs xa{};
   xa.x = (const uint16_t*)x; xa.sxm = sxm; xa.m = m; xa.k = k; xa.kp = L.kp; xa.mb = L.mb; xa.rem = L.rem_m;
+  xa.nkc = L.nkc;
   xa.s_full = s_full; xa.s_last = L.rem_m ? sign_table + (L.rem_m - 1) * 128 : s_full;
-  xa.parts = (uint16_t*)(ws + L.off_parts); xa.stats = ws + L.off_stats;
+  xa.parts = (uint16_t*)(ws + L.off_parts); xa.stats = ws + L.off_stats; xa.xnp = ws + L.off_xnp;
+  xa.xn = ws + L.off_xn; xa.rstat = ws + L.off_rstat;
   {
     SdcProf prof("xstage", stream);
     hipLaunchKernelGGL(xstage_kernel, dim3((unsigned)L.nkc, (unsigned)L.mb), dim3(256), 0, stream, xa);
     SDC_LAUNCH_CHECK();
   }
-  // 2. the row check's GEMM: E_row = W @ (x block sums), W's row norms
+  {
+    SdcProf prof("xfinish", stream);
+    hipLaunchKernelGGL(xfinish_kernel, dim3((unsigned)L.mb), dim3(256), 0, stream, xa);
+    SDC_LAUNCH_CHECK();
+  }
+  // 2. the row check's GEMM: E_row = W @ (x block sums), each XCD taking every depth slice of its rows (W's row
+  //    norms are the layer's, made once)
   GemmArgs gr{};
   gr.A = (const uint16_t*)W; gr.sab = 0; gr.sam = swn; gr.sak = 1;
   gr.B = ws + L.off_parts; gr.sbb = 0; gr.sbc = L.kp;
   gr.m = n; gr.k = k; gr.N = 2 * L.mb; gr.splits = L.srow;
-  gr.E = ws + L.off_erow; gr.XN = ws + L.off_wn; gr.et = 1;
+  gr.E = ws + L.off_erow; gr.XN = nullptr; gr.et = 1; gr.rows_per_xcd = 1;
   gr.prof_name = "row_gemm";
   rc = sdc_gemm_launch(SDC_BF16, gr, 1, stream);
   if (rc != SDC_OK) return rc;
@@ -558,10 +617,10 @@ extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const voi
   YArgs ya{};
   ya.y = (const uint16_t*)y; ya.sym = sym; ya.m = m; ya.n = n; ya.k = k; ya.nb = L.nb; ya.mb = L.mb;
   ya.rem_n = L.rem_n; ya.rem_m = L.rem_m; ya.sign_table = sign_table;
-  ya.Ecol = ws + L.off_ecol; ya.XN = ws + L.off_xn; ya.scol = L.scol; ya.consts = (const f32x4*)block_consts;
+  ya.Ecol = ws + L.off_ecol; ya.xn = ws + L.off_xn; ya.scol = L.scol; ya.consts = (const f32x4*)block_consts;
   ya.state = state; ya.zcol = col_scores;
-  ya.Erow = ws + L.off_erow; ya.WN = ws + L.off_wn; ya.srow = gr.splits; ya.xstats = ws + L.off_stats;
-  ya.nkc = L.nkc; ya.bias = (const uint16_t*)bias; ya.result = row_result; ya.zrow = row_scores;
+  ya.Erow = ws + L.off_erow; ya.wn = w_norms; ya.srow = gr.splits; ya.rstat = ws + L.off_rstat;
+  ya.bias = (const uint16_t*)bias; ya.result = row_result; ya.zrow = row_scores;
   ya.u = 1.f / 256.f; ya.h = 0.f; ya.abs_floor = abs_floor;
   ya.l1c = (float)(k * 7.450580596923828e-09 > 1e-5 ? k * 7.450580596923828e-09 : 1e-5);   // checksum.py:95-104
   ya.zt = z; ya.lim_a = 1e18f; ya.lim_big = 1e18f;

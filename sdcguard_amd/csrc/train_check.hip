@@ -798,6 +798,46 @@ struct PackArgs {
   float* without_bias;             // [nb][12]
 };
 
+// |w|_2^2 and |w|_1 of every row of W (the row-block check's noise model takes them per row of its A = W): one
+// wave per row, 16-byte pieces across the row, fp32 sums
+template <int DT>
+__global__ __launch_bounds__(256) void row_norms_kernel(const uint16_t* W, int64_t swn, int64_t n, int64_t k,
+                                                        int vec, float* out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= n) return;                                   // whole waves leave; no barrier follows
+  const uint16_t* p = W + row * swn;
+  float sq = 0.f, ab = 0.f;
+  int64_t kk = 0;
+  if (vec) {
+    for (; kk + 512 <= k; kk += 512) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(p + kk + 8 * lane);
+      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float a = lo_of<DT>(w4[q]), b = hi_of<DT>(w4[q]);
+        sq = fmaf(a, a, sq);
+        sq = fmaf(b, b, sq);
+        ab += fabsf(a) + fabsf(b);
+      }
+    }
+  }
+  for (int64_t e = kk + lane; e < k; e += 64) {
+    const float a = half_to_f32<DT>(p[e]);
+    sq = fmaf(a, a, sq);
+    ab += fabsf(a);
+  }
+#pragma unroll
+  for (int msk = 1; msk < 64; msk <<= 1) {
+    sq += __shfl_xor(sq, msk, 64);
+    ab += __shfl_xor(ab, msk, 64);
+  }
+  if (lane == 0) {
+    out[row] = sq;
+    out[n + row] = ab;
+  }
+}
+
 // row of a block: scale(plain, signed), bias sums(plain, signed), |B2|_2(2), max |B2|(2), max |W|, max |bias|, 0, 0
 __global__ __launch_bounds__(256) void pack_consts_kernel(PackArgs a) {
   for (int64_t jb = (int64_t)blockIdx.x * 256 + threadIdx.x; jb < a.nb; jb += (int64_t)gridDim.x * 256) {
@@ -824,8 +864,8 @@ extern "C" int64_t sdc_layer_constants_workspace(int64_t n, int64_t k, int64_t b
 
 extern "C" int sdc_layer_constants(int dtype, const void* W, int64_t swn, int64_t n, int64_t k, int64_t bs,
                                    const void* bias, int64_t sbias, const float* sign_table, void* parts,
-                                   int64_t parts_pitch, float* consts_bias, float* consts_plain, void* workspace,
-                                   int64_t workspace_bytes, hipStream_t stream) {
+                                   int64_t parts_pitch, float* consts_bias, float* consts_plain, float* row_norms,
+                                   void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   SDC_CLEAR_ERRORS();
   if (n < 1 || k < 1 || swn < k) return SDC_EINVAL;
   if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EINVAL;
@@ -875,5 +915,16 @@ extern "C" int sdc_layer_constants(int dtype, const void* W, int64_t swn, int64_
   const unsigned grid = (unsigned)(sdc_cdiv(L.nb, 256) < 1024 ? sdc_cdiv(L.nb, 256) : 1024);
   hipLaunchKernelGGL(pack_consts_kernel, dim3(grid), dim3(256), 0, stream, pa);
   SDC_LAUNCH_CHECK();
+  if (row_norms) {
+    const int vec = (swn % 8 == 0) && ((uintptr_t)W % 16 == 0);
+    const dim3 g4((unsigned)sdc_cdiv(n, 4));
+    if (dtype == SDC_BF16)
+      hipLaunchKernelGGL(row_norms_kernel<SDC_BF16>, g4, dim3(256), 0, stream, (const uint16_t*)W, swn, n, k, vec,
+                         row_norms);
+    else
+      hipLaunchKernelGGL(row_norms_kernel<SDC_FP16>, g4, dim3(256), 0, stream, (const uint16_t*)W, swn, n, k, vec,
+                         row_norms);
+    SDC_LAUNCH_CHECK();
+  }
   return SDC_OK;
 }

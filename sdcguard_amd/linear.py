@@ -52,14 +52,18 @@ def check_linear_both(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torc
     parts, scale, b2n, b2max, bmax, bmax_bias, bsum = t[0], t[3], t[4], t[5], t[6], t[7], t[8]
     P = _kmajor_parts(parts, scale, cs.nb, y2.dtype)
     packed = _packed_consts(scale, b2n, b2max, bmax, bmax_bias, bsum)
+    wn = getattr(cs, "wnorm", None)
+    if wn is None or wn.shape != (2, n):
+        raise ValueError("the layer's checksums carry no row norms of W (LayerChecksums makes them)")
     L = _lib.lib()
     nbytes = int(L.sdc_linear_check_workspace(m, k, n))
     ws = _lib.workspace(dev, nbytes)
     rc = L.sdc_linear_check(
         _lib.DT_BF16, x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0), y2.data_ptr(), y2.stride(0),
-        _lib.ptr(bias), m, k, n, P.data_ptr(), P.stride(1), packed.data_ptr(), sign_table(dev).data_ptr(),
-        state.data_ptr(), row_result.data_ptr(), float(z), float(abs_floor), ws.data_ptr(), ws.numel(),
-        _lib.ptr(col_scores), _lib.ptr(row_scores), 1 if concurrent else 0, _lib.stream_of(y2))
+        _lib.ptr(bias), m, k, n, P.data_ptr(), P.stride(1), packed.data_ptr(), wn.data_ptr(),
+        sign_table(dev).data_ptr(), state.data_ptr(), row_result.data_ptr(), float(z), float(abs_floor),
+        ws.data_ptr(), ws.numel(), _lib.ptr(col_scores), _lib.ptr(row_scores), 1 if concurrent else 0,
+        _lib.stream_of(y2))
     if rc == _lib.SDC_EUNSUPPORTED:
         # a layout the one-pass kernels do not read (rows not 16-byte aligned): the two checks, one after the other
         _separately(x2, weight, bias, y2, cs, z, abs_floor, state, row_result, col_scores, row_scores)

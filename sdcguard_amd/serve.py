@@ -74,6 +74,7 @@ class LayerChecksums:
     parts      (k, 6nb) view, k-contiguous columns: the three low-precision parts of B2 / scale, B2 the plain and
                signed sums of each block of `block` rows of W (fp32), the layout the check's MFMA kernel reads
     scale, b2n, b2max, bsum        (nb, 2) fp32; bmax, bmax_bias (nb,) fp32; width, wsq (nb,)
+    wnorm                          (2, n) fp32: |w_j|_2^2 and |w_j|_1 of every row (the row-block check's A norms)
     pair_full, pair_rem            (bs, 2) / (rem, 2) ones and signs in W's dtype (the op's interface)
     fingerprint                    int64[3] of W's bits (recompute.fingerprint), to notice a rewritten weight
     tensors(with_bias)             the op's arguments after x2 and y2, in the reference's order"""
@@ -106,11 +107,12 @@ class LayerChecksums:
         with torch.no_grad():
             store = torch.empty(6 * nb, kp, dtype=dt, device=dev)
             table = torch.empty(2, nb, 12, dtype=torch.float32, device=dev)
+            self.wnorm = torch.empty(2, n, dtype=torch.float32, device=dev)
             ws = _lib.workspace(dev, int(L.sdc_layer_constants_workspace(n, k, bs)))
             rc = L.sdc_layer_constants(_lib.dtype_code(dt), W.data_ptr(), W.stride(0), n, k, bs, _lib.ptr(b),
                                        b.stride(0) if b is not None else 0, sign_table(dev).data_ptr(),
                                        store.data_ptr(), kp, table[0].data_ptr(), table[1].data_ptr(),
-                                       ws.data_ptr(), ws.numel(), _lib.stream_of(W))
+                                       self.wnorm.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(W))
             _lib.check(rc, "sdc_layer_constants")
         self.parts = store[:, :k].t()
         cols = table[0]
