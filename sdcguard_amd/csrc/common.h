@@ -6,6 +6,9 @@
 #define SDC_WAVE 64
 // most depth-split planes of the expected-side GEMM (its scorers add them with unrolled loads)
 #define SDC_MAX_SPLITS 8
+// depth splits the expected-side GEMM accepts (consumers that hold every split's value in registers take at most
+// SDC_MAX_SPLITS; the quantized checks, whose GEMMs can be short in rows, loop over up to this many)
+#define SDC_MAX_GEMM_SPLITS 32
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));

@@ -43,17 +43,16 @@ __device__ __forceinline__ uint32_t e4m3_to_bf16(uint32_t b) {
   return s | (f >> 16);
 }
 
-// 8 fp8 values (one 8-byte word pair) -> 8 bf16 (16 bytes)
+// 8 fp8 values (one 8-byte word pair) -> 8 bf16 (16 bytes): gfx950's scaled pair conversion with scale 1, which is
+// exact (every e4m3 value is a bf16 value; 0x7F / 0xFF become NaN), two bytes of a word per instruction
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u32x4 fp8x8_to_bf16(u32x2 v) {
   u32x4 o;
-  uint32_t* po = reinterpret_cast<uint32_t*>(&o);
 #pragma unroll
-  for (int w = 0; w < 2; ++w)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t x = v[w] >> (16 * h);
-      po[2 * w + h] = e4m3_to_bf16(x & 0xFFu) | (e4m3_to_bf16((x >> 8) & 0xFFu) << 16);
-    }
+  for (int w = 0; w < 2; ++w) {
+    o[2 * w] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[w], 1.0f, false));
+    o[2 * w + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[w], 1.0f, true));
+  }
   return o;
 }
 
@@ -478,7 +477,7 @@ extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols) {
 }
 
 int sdc_gemm_launch(int dtype, GemmArgs g, int64_t batches, hipStream_t stream) {
-  if (g.splits < 1 || g.splits > SDC_MAX_SPLITS || batches < 1) return SDC_EINVAL;
+  if (g.splits < 1 || g.splits > SDC_MAX_GEMM_SPLITS || batches < 1) return SDC_EINVAL;
   if (dtype < SDC_BF16 || dtype > SDC_I8) return SDC_EINVAL;
   g.kchunk = sdc_cdiv(sdc_cdiv(g.k, g.splits), KS) * KS;
   const int64_t ea = dtype == SDC_FP8 ? 1 : 2;                   // bytes per A element

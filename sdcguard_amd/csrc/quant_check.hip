@@ -8,8 +8,9 @@
 //               this is modes.judge("fp8") itself.
 // Two launches, no host synchronisation: the expected side on MFMA (expected_gemm.hip: int8 A with the block
 // sums' two base-128 digits, or fp8 A widened exactly to bf16 with the three bf16 parts of the scaled block sums),
-// then one persistent pass over C: 16 lanes per (row, block) pair, 8 elements per lane, the sums in int64 or fp64,
-// one verdict per pair, a wave / workgroup reduction and one set of atomics per workgroup.
+// then one pass over C: for blocks of 128 and rows read in 16-byte pieces, the tile pass (quant_tile_kernel:
+// 64 rows x one block per workgroup, sums in int64 or fp32 across 16 lanes, one lane per pair judging); otherwise
+// a persistent pass with 16 lanes per (row, block) pair, the sums in int64 or fp64.
 #include "common.h"
 #include "gemm.h"
 #include "profile.h"
@@ -101,14 +102,13 @@ __device__ __forceinline__ void load8c(const QuantArgs& a, int64_t r, int64_t c0
 __device__ __forceinline__ float judge_fp8(const QuantArgs& a, int64_t r, int64_t jb, double pl, double sg,
                                            double sq, bool imposs, float& noise_out) {
   double e0 = 0.0, e1 = 0.0, asq = 0.0;
-#pragma unroll
-  for (int s = 0; s < SDC_MAX_SPLITS; ++s)
-    if (s < a.splits) {
-      const float* ep = a.E + (s * a.m + r) * a.ncols + 2 * jb;
-      e0 += (double)ep[0];
-      e1 += (double)ep[1];
-      asq += (double)a.XN[s * 2 * a.m + r];
-    }
+#pragma unroll 4
+  for (int s = 0; s < a.splits; ++s) {
+    const float* ep = a.E + (s * a.m + r) * a.ncols + 2 * jb;
+    e0 += (double)ep[0];
+    e1 += (double)ep[1];
+    asq += (double)a.XN[s * 2 * a.m + r];
+  }
   const double sa = a.sa ? (double)a.sa[r] : 1.0;
   e0 *= sa;
   e1 *= sa;
@@ -162,14 +162,13 @@ __global__ __launch_bounds__(256) void quant_score_kernel(QuantArgs a) {
       }
       if (live && e == 0) {
         int64_t e0 = 0, e1 = 0;
-#pragma unroll
-        for (int s = 0; s < SDC_MAX_SPLITS; ++s)
-          if (s < a.splits) {
-            const int32_t* hi = reinterpret_cast<const int32_t*>(a.E) + ((s * 2) * a.m + r) * a.ncols + 2 * jb;
-            const int32_t* lo = hi + a.m * a.ncols;
-            e0 += 128 * (int64_t)hi[0] + (int64_t)lo[0];
-            e1 += 128 * (int64_t)hi[1] + (int64_t)lo[1];
-          }
+#pragma unroll 4
+        for (int s = 0; s < a.splits; ++s) {
+          const int32_t* hi = reinterpret_cast<const int32_t*>(a.E) + ((s * 2) * a.m + r) * a.ncols + 2 * jb;
+          const int32_t* lo = hi + a.m * a.ncols;
+          e0 += 128 * (int64_t)hi[0] + (int64_t)lo[0];
+          e1 += 128 * (int64_t)hi[1] + (int64_t)lo[1];
+        }
         const bool bad = e0 != pl || e1 != sg;
         const float z = bad ? __builtin_inff() : 0.f;
         if (a.zdump) a.zdump[p] = z;
@@ -198,9 +197,8 @@ __global__ __launch_bounds__(256) void quant_score_kernel(QuantArgs a) {
       // Cauchy-Schwarz per output: |c_ij| > 2 |sa_i Aq_i| |sb_j Bq_j|
       if (live) {
         double asq = 0.0;
-#pragma unroll
-        for (int s = 0; s < SDC_MAX_SPLITS; ++s)
-          if (s < a.splits) asq += (double)a.XN[s * 2 * a.m + r];
+#pragma unroll 4
+        for (int s = 0; s < a.splits; ++s) asq += (double)a.XN[s * 2 * a.m + r];
         const double an = (a.sa ? (double)a.sa[r] : 1.0) * sqrt(asq);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -246,6 +244,224 @@ __global__ __launch_bounds__(256) void quant_score_kernel(QuantArgs a) {
   }
 }
 
+// The tile pass (blocks of 128 columns, C read along rows in 16-byte pieces): one workgroup owns 64 rows x one
+// column block.  Thread t = 16 rg + cg reads rows 4 rg .. 4 rg + 3, columns 8 cg .. 8 cg + 7 (a wave's load covers
+// 4 rows x a whole block); its partial sums of each row go to the row's 16 lanes by DPP steps, and to LDS.  Wave 0
+// prepares the rows' norms (fp8: |sa_i Aq_i| for the Cauchy-Schwarz rule, which every element checks) and then
+// judges the 64 pairs, one lane each, reading the expected sums from transposed planes (consecutive rows).
+__device__ __forceinline__ float sum16(float v) {
+  v += dpp_xor1(v);
+  v += dpp_xor2(v);
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // half mirror
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));  // row mirror
+  return v;
+}
+
+__device__ __forceinline__ int64_t sum16_i64(int64_t v) {
+#pragma unroll
+  for (int msk = 1; msk < 16; msk <<= 1) v += shfl_xor_i64(v, msk);
+  return v;
+}
+
+template <int KIND, int CT>
+__global__ __launch_bounds__(256) void quant_tile_kernel(QuantArgs a) {
+  constexpr int ES = CT == C_BF16 ? 2 : 4;                  // bytes per C element
+  constexpr int NL = 8 * ES / 16;                           // 16-byte loads per row piece (1 or 2)
+  __shared__ float an_s[64];                                // fp8: 2 |sa_i Aq_i| per row (the rule's limit)
+  __shared__ float imp_s[64];                               // fp8: lanes of the row that broke the rule
+  __shared__ float srow[64][4];                             // fp8: plain, signed, squares, |sa_i Aq_i|
+  __shared__ int64_t irow[64][2];                           // int8: plain, signed
+  __shared__ int64_t red_k[4], red_d[4];
+  __shared__ int red_w[4], red_n[4];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int rg = t >> 4, cg = t & 15;
+  const int64_t jb = blockIdx.x, r0 = (int64_t)blockIdx.y * 64;
+  const int64_t c0 = jb * 128 + 8 * cg;
+  // C: 4 rows x 8 columns, clamped to row m - 1 (rows past m are never judged); the last block's columns past n
+  // are masked at use
+  u32x4 v[4][NL];
+  const uint8_t* base = (const uint8_t*)a.C;
+  const int64_t cl = c0 + 8 <= a.n ? c0 : a.n - 8;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t r = r0 + 4 * rg + i < a.m ? r0 + 4 * rg + i : a.m - 1;
+#pragma unroll
+    for (int l = 0; l < NL; ++l)
+      v[i][l] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + (r * a.scm + cl) * ES + 16 * l));
+  }
+  const int wid = (int)((jb == a.nb - 1 && a.rem > 0) ? a.rem : 128);
+  const float* sp = wid == 128 ? a.s_full : a.s_last;
+  float sgn[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sgn[e] = 8 * cg + e < wid ? sp[8 * cg + e] : 0.f;
+  const bool on = 8 * cg < wid;                              // this thread's columns exist (a whole piece or none)
+  // wave 0: the expected sums and (fp8) the row norms of its lane's row
+  const int64_t rr = r0 + lane < a.m ? r0 + lane : a.m - 1;
+  double e0 = 0.0, e1 = 0.0;
+  int64_t i0 = 0, i1 = 0;
+  if (w == 0) {
+    if constexpr (KIND == 0) {
+      const int32_t* E = reinterpret_cast<const int32_t*>(a.E);
+#pragma unroll 4
+      for (int s = 0; s < a.splits; ++s) {
+        const int32_t* hi = E + ((int64_t)(2 * s) * a.ncols + 2 * jb) * a.m + rr;
+        const int32_t* lo = E + ((int64_t)(2 * s + 1) * a.ncols + 2 * jb) * a.m + rr;
+        i0 += 128 * (int64_t)hi[0] + (int64_t)lo[0];
+        i1 += 128 * (int64_t)hi[a.m] + (int64_t)lo[a.m];
+      }
+    } else {
+      double asq = 0.0;
+#pragma unroll 4
+      for (int s = 0; s < a.splits; ++s) {
+        const float* ep = a.E + ((int64_t)s * a.ncols + 2 * jb) * a.m + rr;
+        e0 += (double)ep[0];
+        e1 += (double)ep[a.m];
+        asq += (double)a.XN[s * 2 * a.m + rr];
+      }
+      const double sa = a.sa ? (double)a.sa[rr] : 1.0;
+      e0 *= sa;
+      e1 *= sa;
+      const double an = sa * sqrt(asq);
+      an_s[lane] = (float)(2.0 * an);
+      srow[lane][3] = (float)an;                             // |sa_i Aq_i| for the noise (e0, e1 stay in registers)
+    }
+  }
+  __syncthreads();
+  if constexpr (KIND == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int64_t pl = 0, sg = 0;
+      if (on) {
+#pragma unroll
+        for (int l = 0; l < NL; ++l)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int e = 4 * l + q;
+            const int64_t x = (int64_t)(int32_t)v[i][l][q];
+            pl += x;
+            sg += sgn[e] > 0.f ? x : (sgn[e] < 0.f ? -x : 0);
+          }
+      }
+      pl = sum16_i64(pl);
+      sg = sum16_i64(sg);
+      if (cg == 0) {
+        irow[4 * rg + i][0] = pl;
+        irow[4 * rg + i][1] = sg;
+      }
+    }
+  } else {
+    float bc[8];
+    {
+      const int64_t cc = on ? c0 : 0;
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(a.bcol + cc);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(a.bcol + cc + 4);
+      bc[0] = b0.x; bc[1] = b0.y; bc[2] = b0.z; bc[3] = b0.w; bc[4] = b1.x; bc[5] = b1.y; bc[6] = b1.z; bc[7] = b1.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x[8];
+      if constexpr (CT == C_BF16) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          x[2 * q] = bf16_lo(v[i][0][q]);
+          x[2 * q + 1] = bf16_hi(v[i][0][q]);
+        }
+      } else {
+#pragma unroll
+        for (int l = 0; l < 2; ++l)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) x[4 * l + q] = __uint_as_float(v[i][l][q]);
+      }
+      const float lim = an_s[4 * rg + i];
+      float pl = 0.f, sg = 0.f, sq = 0.f;
+      bool imp = false;
+      if (on) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          pl += x[e];
+          sg = fmaf(x[e], sgn[e], sg);
+          sq = fmaf(x[e], x[e], sq);
+          imp = imp || (fabsf(x[e]) > lim * bc[e]);
+        }
+      }
+      pl = sum16(pl);
+      sg = sum16(sg);
+      sq = sum16(sq);
+      float fi = imp ? 1.f : 0.f;
+      fi += dpp_xor1(fi);
+      fi += dpp_xor2(fi);
+      fi += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(fi), 0x141, 0xF, 0xF, false));
+      fi += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(fi), 0x140, 0xF, 0xF, false));
+      if (cg == 0) {
+        srow[4 * rg + i][0] = pl;
+        srow[4 * rg + i][1] = sg;
+        srow[4 * rg + i][2] = sq;
+        imp_s[4 * rg + i] = fi;
+      }
+    }
+  }
+  __syncthreads();
+  QBest best;
+  if (w == 0 && r0 + lane < a.m) {
+    const int64_t p = (r0 + lane) * a.nb + jb;
+    if constexpr (KIND == 0) {
+      const bool bad = i0 != irow[lane][0] || i1 != irow[lane][1];
+      const float z = bad ? __builtin_inff() : 0.f;
+      if (a.zdump) a.zdump[p] = z;
+      if (bad) {
+        best.wrong = 1;
+        best.key = ((int64_t)__float_as_uint(z) << 32) | (p & 0xFFFFFFFFll);
+        best.keyd = best.key;
+      }
+    } else {
+      const double pl = srow[lane][0], sg = srow[lane][1], sq = srow[lane][2];
+      const bool imposs = imp_s[lane] > 0.f;
+      const double a_norm = srow[lane][3];
+      const double c_norm = sqrt(sq);
+      double noise = (double)a.unit * (a_norm * (double)a.bfrob[jb] + (double)a.per_out * c_norm);
+      if (a.c_bf16) noise += 0.00390625 * c_norm;
+      noise += 1e-300;
+      const double zd = fmax(fabs(e0 - pl), fabs(e1 - sg)) / noise;
+      const bool fin = isfinite(pl) && isfinite(sg);
+      const bool bad = !fin || imposs || !isfinite(noise) || isnan(zd);
+      const float z = bad ? __builtin_inff() : (float)zd;
+      if (a.zdump) a.zdump[p] = z;
+      best.wrong = z > a.zt;
+      best.nonfin = !fin;
+      const int64_t zb = (int64_t)__float_as_uint(fmaxf(z, 0.f));
+      best.key = (zb << 32) | (p & 0xFFFFFFFFll);
+      best.keyd = (zb << 32) | (int64_t)__float_as_uint((float)noise);
+    }
+  }
+  if (w == 0) {
+    const int64_t key = wave_max_i64(best.key), keyd = wave_max_i64(best.keyd);
+    const int wr = wave_sum_i32(best.wrong), nf = wave_sum_i32(best.nonfin);
+    if (lane == 0) {
+      int64_t* res = a.result;
+      if (key > __atomic_load_n(res, __ATOMIC_RELAXED)) atomicMax((unsigned long long*)res, (unsigned long long)key);
+      if (keyd > __atomic_load_n(res + 1, __ATOMIC_RELAXED))
+        atomicMax((unsigned long long*)(res + 1), (unsigned long long)keyd);
+      if (wr > 0) atomicAdd((unsigned long long*)(res + 2), (unsigned long long)wr);
+      if (nf > 0) atomicAdd((unsigned long long*)(res + 3), (unsigned long long)nf);
+    }
+  }
+}
+
+// Depth splits of the quantized checks' GEMM: sdc_expected_splits' (tiles x splits covering the 256 CUs, at most
+// SDC_MAX_SPLITS planes), except that an fp8 GEMM of few row tiles (2048 tokens make four) takes up to
+// SDC_MAX_GEMM_SPLITS splits of at least 128 depths: its planes are small, and MFMA work is its cost.  (int8 keeps
+// the planes few: each split writes two digit planes the scoring pass reads back.)
+int64_t quant_splits(int kind, int64_t m, int64_t k, int64_t ncols) {
+  const int wgn = ncols > 64 ? 2 : 1;
+  const int64_t tiles = sdc_cdiv(m, 64 * (8 / wgn)) * sdc_cdiv(ncols, 64 * wgn);
+  if (kind == 0 || tiles > 8) return sdc_expected_splits(m, k, ncols);
+  int64_t s = sdc_cdiv(256, tiles);
+  const int64_t smax = k / 128 > 1 ? k / 128 : 1;
+  if (s > smax) s = smax;
+  if (s > SDC_MAX_GEMM_SPLITS) s = SDC_MAX_GEMM_SPLITS;
+  return s < 1 ? 1 : s;
+}
+
 struct QLayout {
   int64_t nb, rem, ncols, splits, nacc, off_e, off_xn, total;
 };
@@ -256,7 +472,7 @@ QLayout qlayout(int kind, int64_t m, int64_t k, int64_t n, int64_t bs) {
   L.rem = n % bs;
   L.ncols = 2 * L.nb;
   L.nacc = kind == 0 ? 2 : 1;
-  L.splits = sdc_expected_splits(m, kind == 0 ? k / 2 : k, L.ncols);
+  L.splits = quant_splits(kind, m, kind == 0 ? k / 2 : k, L.ncols);
   auto al = [](int64_t x) { return (x + 63) / 64 * 64; };
   int64_t o = 0;
   L.off_e = o; o += al(L.splits * L.nacc * m * L.ncols);
@@ -299,7 +515,11 @@ extern "C" int sdc_quant_check(int kind, const void* A, int64_t sam, const void*
   const float* s_full = sign_table + (bs - 1) * 128;
   const float* s_last = L.rem ? sign_table + (L.rem - 1) * 128 : s_full;
 
+  const int es = c_dtype == C_BF16 ? 2 : 4;
+  const bool vec = scn == 1 && ((scm * es) % 16 == 0) && ((bs * es) % 16 == 0) && ((uintptr_t)C % 16 == 0);
+  const bool tiles = vec && bs == 128 && n % 8 == 0 && sdc_cdiv(m, 64) <= 65535;   // the tile pass (transposed E)
   GemmArgs g{};
+  g.et = tiles ? 1 : 0;
   g.A = (const uint16_t*)A;
   g.sab = 0;
   g.sam = kind == 0 ? sam / 2 : sam;
@@ -314,8 +534,7 @@ extern "C" int sdc_quant_check(int kind, const void* A, int64_t sam, const void*
   QuantArgs qa{};
   qa.C = C; qa.scm = scm; qa.scn = scn;
   qa.m = m; qa.n = n; qa.nb = L.nb; qa.bs = bs; qa.rem = L.rem; qa.npairs = m * L.nb;
-  const int es = c_dtype == C_BF16 ? 2 : 4;
-  qa.vec = scn == 1 && ((scm * es) % 16 == 0) && ((bs * es) % 16 == 0) && ((uintptr_t)C % 16 == 0);
+  qa.vec = vec;
   qa.s_full = s_full; qa.s_last = s_last;
   qa.E = ws + L.off_e; qa.XN = ws + L.off_xn; qa.splits = L.splits; qa.ncols = L.ncols;
   qa.sa = sa; qa.bfrob = bfrob; qa.bcol = bcol;
@@ -324,12 +543,19 @@ extern "C" int sdc_quant_check(int kind, const void* A, int64_t sam, const void*
   qa.zt = z;
   qa.c_bf16 = c_dtype == C_BF16;
   qa.result = result; qa.zdump = scores_out;
-  const int64_t groups = sdc_cdiv(qa.npairs, 4);
-  const unsigned grid = (unsigned)(sdc_cdiv(groups, 4) < 2048 ? sdc_cdiv(groups, 4) : 2048);
   SdcProf prof(kind == 0 ? "quant_score_i8" : "quant_score_fp8", stream);
-  if (kind == 0) launch_score<0, C_I32>(qa, grid, stream);
-  else if (c_dtype == C_F32) launch_score<1, C_F32>(qa, grid, stream);
-  else launch_score<1, C_BF16>(qa, grid, stream);
+  if (tiles) {
+    const dim3 grid((unsigned)L.nb, (unsigned)sdc_cdiv(m, 64));
+    if (kind == 0) hipLaunchKernelGGL((quant_tile_kernel<0, C_I32>), grid, dim3(256), 0, stream, qa);
+    else if (c_dtype == C_F32) hipLaunchKernelGGL((quant_tile_kernel<1, C_F32>), grid, dim3(256), 0, stream, qa);
+    else hipLaunchKernelGGL((quant_tile_kernel<1, C_BF16>), grid, dim3(256), 0, stream, qa);
+  } else {
+    const int64_t groups = sdc_cdiv(qa.npairs, 4);
+    const unsigned grid = (unsigned)(sdc_cdiv(groups, 4) < 2048 ? sdc_cdiv(groups, 4) : 2048);
+    if (kind == 0) launch_score<0, C_I32>(qa, grid, stream);
+    else if (c_dtype == C_F32) launch_score<1, C_F32>(qa, grid, stream);
+    else launch_score<1, C_BF16>(qa, grid, stream);
+  }
   SDC_LAUNCH_CHECK();
   return SDC_OK;
 }
