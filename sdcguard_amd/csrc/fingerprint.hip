@@ -151,12 +151,17 @@ unsigned grid_for(int64_t work_items) {
 
 // Paged-KV block fingerprints: fp3 of every block of a paged cache, each block's words numbered from 0 (what
 // recompute.fingerprint gives the block as a tensor of its own).  The weights depend only on the position in the
-// block, so a workgroup owns one slice of KV_SLICE positions of every block it visits (16 words per thread) and
-// keeps their weights in registers while it streams blocks; per block the three sums use one 64-bit and one
-// 32-bit multiply-add per weight (b w = b lo_s + 2^32 b hi' mod 2^64, with lo_s the signed low half of w and
-// hi' its high half plus the low half's sign bit), then a wave and workgroup reduction and three 64-bit atomics.
-constexpr int KV_WPT = 16;                       // words per thread
-constexpr int KV_SLICE = 256 * KV_WPT;           // positions per workgroup slice
+// block, so a wave owns one slice of KV_SLICE positions (16 words per lane) of every block it visits and keeps its
+// weights in registers while it streams blocks.  The products run on packed 16-bit dot products
+// (v_dot2c_i32_i16, two words per instruction): with w = lo + 2^32 hi (lo the signed low half, hi the high half
+// plus lo's sign bit), b w mod 2^64 = b lo + 2^32 (b hi mod 2^32), where lo is taken as three balanced 12-bit
+// digits (b times a digit summed over 16 words stays exact in 32 bits) and hi as two balanced 16-bit digits whose
+// sums may wrap (only hi's value mod 2^32 counts).  Each wave adds its lanes' sums (DPP steps, then two shuffles)
+// and three of its lanes add them into the block's three outputs with 64-bit atomics (wrapping, so the result does
+// not depend on the order).  Four blocks are in flight per wave.
+constexpr int KV_WPT = 16;                       // words per lane
+constexpr int KV_SLICE = 64 * KV_WPT;            // positions per wave slice
+constexpr int KV_UNROLL = 4;                     // blocks in flight per wave
 
 struct KvArgs {
   const uint8_t* cache;
@@ -167,65 +172,129 @@ struct KvArgs {
   int vec;
 };
 
-__global__ __launch_bounds__(256) void kv_fp3_kernel(KvArgs a) {
-  __shared__ int64_t red[4][3];
+typedef short short2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ int dot16(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, a), __builtin_bit_cast(short2_t, b), c, false);
+}
+
+// the balanced digit of v in base 2^bits (in [-2^(bits-1), 2^(bits-1))), as the low 16 bits of a word
+__device__ __forceinline__ int32_t bdigit(int64_t v, int bits) {
+  const int64_t h = 1ll << (bits - 1);
+  return (int32_t)(((v + h) & ((1ll << bits) - 1)) - h);
+}
+
+// a weight's five digits at position p: three of lo (12 bits each), two of hi (16 bits)
+__device__ __forceinline__ void weight_digits(uint64_t w, int32_t* d) {
+  const int64_t lo = (int32_t)(uint32_t)w;
+  const uint32_t hi = (uint32_t)(w >> 32) + ((uint32_t)w >> 31);
+  d[0] = bdigit(lo, 12);
+  const int64_t r1 = (lo - d[0]) >> 12;
+  d[1] = bdigit(r1, 12);
+  d[2] = (int32_t)((r1 - d[1]) >> 12);
+  d[3] = bdigit((int64_t)hi, 16);
+  d[4] = (int16_t)(uint16_t)(((uint32_t)hi - (uint32_t)d[3]) >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack16(int32_t a, int32_t b) {
+  return ((uint32_t)a & 0xFFFFu) | ((uint32_t)b << 16);
+}
+
+// v plus its DPP partner's value (64-bit wrapping)
+template <int CTL>
+__device__ __forceinline__ uint64_t dpp_add_u64(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTL, 0xF, 0xF, false);
+  const uint32_t hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTL, 0xF, 0xF, false);
+  return v + (((uint64_t)hi << 32) | lo);
+}
+
+// sum over the wave, 64-bit wrapping: four DPP steps inside each row of 16 lanes (quad xor 1, quad xor 2, half-row
+// mirror, row mirror; no LDS), then two shuffles across rows
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+  v = dpp_add_u64<0xB1>(v);
+  v = dpp_add_u64<0x4E>(v);
+  v = dpp_add_u64<0x141>(v);
+  v = dpp_add_u64<0x140>(v);
+  v += (uint64_t)shfl_xor_i64((int64_t)v, 16);
+  v += (uint64_t)shfl_xor_i64((int64_t)v, 32);
+  return v;
+}
+
+constexpr int KV_WAVES = 4;                      // waves per workgroup: KV_WAVES slices of one block range
+
+__global__ __launch_bounds__(64 * KV_WAVES) void kv_fp3_kernel(KvArgs a) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int64_t p0 = (int64_t)blockIdx.x * KV_SLICE + (int64_t)t * KV_WPT;
-  int32_t w1l[KV_WPT], w2l[KV_WPT];
-  uint32_t w1h[KV_WPT], w2h[KV_WPT];
+  const int64_t p0 = ((int64_t)blockIdx.x * KV_WAVES + w) * KV_SLICE + (int64_t)lane * KV_WPT;
+  // dg[j][c][d]: word pair j (positions p0 + 2j, 2j + 1), weight c, digit d, packed for the dot products
+  uint32_t dg[KV_WPT / 2][2][5];
 #pragma unroll
-  for (int e = 0; e < KV_WPT; ++e) {
-    const uint64_t z = fp3_z((uint64_t)(p0 + e));
-    const uint64_t q1 = z | 1ull, q2 = (z ^ (z >> 32)) | 1ull;
-    w1l[e] = (int32_t)(uint32_t)q1;
-    w2l[e] = (int32_t)(uint32_t)q2;
-    w1h[e] = (uint32_t)(q1 >> 32) + ((uint32_t)q1 >> 31);
-    w2h[e] = (uint32_t)(q2 >> 32) + ((uint32_t)q2 >> 31);
+  for (int j = 0; j < KV_WPT / 2; ++j) {
+    int32_t e0[2][5], e1[2][5];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint64_t z = fp3_z((uint64_t)(p0 + 2 * j + h));
+      weight_digits(z | 1ull, h ? e1[0] : e0[0]);
+      weight_digits((z ^ (z >> 32)) | 1ull, h ? e1[1] : e0[1]);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int d = 0; d < 5; ++d) dg[j][c][d] = pack16(e0[c][d], e1[c][d]);
   }
   const int nw = p0 >= a.words ? 0 : (a.words - p0 < KV_WPT ? (int)(a.words - p0) : KV_WPT);
-  for (int64_t i = blockIdx.y; i < a.n; i += gridDim.y) {
-    const int64_t blk = a.ids ? a.ids[i] : i;
-    if (blk < 0 || blk >= a.nblocks) continue;                  // (uniform over the workgroup)
-    const uint8_t* src = a.cache + blk * a.block_bytes + p0 * 2;
-    int32_t b[KV_WPT];
-    if (a.vec && nw == KV_WPT) {
-      const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-      const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16));
+  const bool full = a.vec && nw == KV_WPT;
+  for (int64_t i0 = blockIdx.y; i0 < a.n; i0 += (int64_t)gridDim.y * KV_UNROLL) {
+    uint32_t b[KV_UNROLL][KV_WPT / 2];
+    bool live[KV_UNROLL];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        b[2 * j] = (int16_t)(v0[j] & 0xFFFFu);
-        b[2 * j + 1] = (int16_t)(v0[j] >> 16);
-        b[8 + 2 * j] = (int16_t)(v1[j] & 0xFFFFu);
-        b[8 + 2 * j + 1] = (int16_t)(v1[j] >> 16);
+    for (int u = 0; u < KV_UNROLL; ++u) {
+      const int64_t i = i0 + (int64_t)u * gridDim.y;
+      const int64_t blk = i < a.n ? (a.ids ? a.ids[i] : i) : -1;
+      live[u] = blk >= 0 && blk < a.nblocks;
+      const uint8_t* src = a.cache + (live[u] ? blk : 0) * a.block_bytes + (nw ? p0 : 0) * 2;
+      if (full) {
+        const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+        const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          b[u][q] = v0[q];
+          b[u][4 + q] = v1[q];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < KV_WPT / 2; ++j) {
+          const uint32_t lo = 2 * j < nw ? (uint32_t)(src[4 * j] | (src[4 * j + 1] << 8)) : 0u;
+          const uint32_t hi = 2 * j + 1 < nw ? (uint32_t)(src[4 * j + 2] | (src[4 * j + 3] << 8)) : 0u;
+          b[u][j] = lo | (hi << 16);
+        }
       }
-    } else {
+    }
 #pragma unroll
-      for (int e = 0; e < KV_WPT; ++e) b[e] = e < nw ? (int16_t)(src[2 * e] | (src[2 * e + 1] << 8)) : 0;
-    }
-    int64_t s0 = 0, l1 = 0, l2 = 0;
-    uint32_t h1 = 0, h2 = 0;
+    for (int u = 0; u < KV_UNROLL; ++u) {
+      int s0 = 0, A[2][3] = {{0, 0, 0}, {0, 0, 0}}, H[2][2] = {{0, 0}, {0, 0}};
 #pragma unroll
-    for (int e = 0; e < KV_WPT; ++e) {
-      s0 += b[e];
-      l1 += (int64_t)b[e] * (int64_t)w1l[e];
-      l2 += (int64_t)b[e] * (int64_t)w2l[e];
-      h1 += (uint32_t)b[e] * w1h[e];
-      h2 += (uint32_t)b[e] * w2h[e];
-    }
-    int64_t v[3] = {s0, (int64_t)((uint64_t)l1 + ((uint64_t)h1 << 32)), (int64_t)((uint64_t)l2 + ((uint64_t)h2 << 32))};
+      for (int j = 0; j < KV_WPT / 2; ++j) {
+        s0 = dot16(b[u][j], 0x00010001u, s0);
 #pragma unroll
-    for (int c = 0; c < 3; ++c) v[c] = wave_sum_i64(v[c]);
-    if (lane == 0) {
-      red[w][0] = v[0];
-      red[w][1] = v[1];
-      red[w][2] = v[2];
+        for (int c = 0; c < 2; ++c) {
+#pragma unroll
+          for (int d = 0; d < 3; ++d) A[c][d] = dot16(b[u][j], dg[j][c][d], A[c][d]);
+#pragma unroll
+          for (int d = 0; d < 2; ++d) H[c][d] = dot16(b[u][j], dg[j][c][3 + d], H[c][d]);
+        }
+      }
+      uint64_t v[3];
+      v[0] = (uint64_t)(int64_t)wave_sum_i32(s0);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int64_t low = (int64_t)A[c][0] + ((int64_t)A[c][1] << 12) + ((int64_t)A[c][2] << 24);
+        const uint32_t high = (uint32_t)H[c][0] + ((uint32_t)H[c][1] << 16);
+        v[1 + c] = wave_sum_u64((uint64_t)low + ((uint64_t)high << 32));
+      }
+      const int64_t i = i0 + (int64_t)u * gridDim.y;
+      if (lane < 3 && live[u])
+        atomicAdd((unsigned long long*)(a.out + 3 * i + lane), (unsigned long long)v[lane == 0 ? 0 : (lane == 1 ? 1 : 2)]);
     }
-    __syncthreads();
-    if (t < 3) {
-      const uint64_t sum = (uint64_t)red[0][t] + (uint64_t)red[1][t] + (uint64_t)red[2][t] + (uint64_t)red[3][t];
-      atomicAdd((unsigned long long*)(a.out + 3 * i + t), (unsigned long long)sum);
-    }
-    __syncthreads();
   }
 }
 
@@ -282,12 +351,12 @@ extern "C" int sdc_kv_fingerprint(const void* cache, int64_t nblocks, int64_t bl
   if (n == 0) return SDC_OK;
   KvArgs a{(const uint8_t*)cache, block_bytes, words, nblocks, ids, n, out,
            (block_bytes % 16 == 0) && ((uintptr_t)cache % 16 == 0)};
-  const int64_t slices = sdc_cdiv(words, KV_SLICE);
-  int64_t gy = sdc_cdiv(2048, slices);
-  if (gy > n) gy = n;
+  const int64_t gx = sdc_cdiv(sdc_cdiv(words, KV_SLICE), KV_WAVES);      // workgroups of KV_WAVES wave slices
+  int64_t gy = sdc_cdiv(2048, gx);
+  if (gy > sdc_cdiv(n, KV_UNROLL)) gy = sdc_cdiv(n, KV_UNROLL);
   if (gy > 65535) gy = 65535;
   SdcProf prof("kv_fingerprint", stream);
-  hipLaunchKernelGGL(kv_fp3_kernel, dim3((unsigned)slices, (unsigned)gy), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(kv_fp3_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(64 * KV_WAVES), 0, stream, a);
   SDC_LAUNCH_CHECK();
   return SDC_OK;
 }
