@@ -1,0 +1,305 @@
+"""Training-side checks: Group, check_now and SDCGuard (reference: _group.py:749-917, guard.py:788-1971).
+
+Group gathers the checks of one step on one device and dtype: add() queues a check's GPU work at once
+(sdc_matmul_check: the block sums of B, the expected side on MFMA, one scoring pass over C that leaves the check's
+worst key in a device row); launch() collects every check's row into one device tensor; a single device-to-host copy
+per flush then reads them all, and row() decodes one.  check_now() is one check answered right away.
+
+SDCGuard checks the nn.Linear layers of a model while a step is active (protect() + at_step()): each layer's
+forward product y = x W^T + b, its input gradient dx = dy W and its weight gradient dW = dy^T x, on a share of
+them (sample_rate), queued without host synchronisation and read back by flush() (every `every` steps, at
+max_pending queued checks, or when called).  Alerts become SDCEvent records, call on_alert, and raise SDCError with
+raise_on_alert.  The reference's other routes (a dispatch mode over every operator, DTensor shards, fp32
+accumulators, recompute and replica checks) are not part of this path.
+"""
+from __future__ import annotations
+
+import contextlib
+import math
+import random
+import threading
+import time
+from dataclasses import dataclass, field
+from typing import Callable, Optional
+
+import torch
+
+from .checksum import ABS_FLOOR, UNIT_ROUNDOFF, CheckResult, _f32_of_bits, matmul_zscores
+
+UNJUDGED = -1.0
+
+
+class Group:
+    """The checks of one step on one device in one dtype (the reference's _group.Group interface)."""
+
+    CHUNK = 256                         # result rows allocated at a time
+
+    def __init__(self, device, dtype: torch.dtype, block: int = 128, abs_floor: float = ABS_FLOOR,
+                 z: float = 6.0, epoch: int = 0):
+        if dtype not in UNIT_ROUNDOFF:
+            raise ValueError(f"checks take bf16 / fp16 outputs, not {dtype}")
+        self.device, self.dtype, self.block = torch.device(device), dtype, int(block)
+        self.abs_floor, self.z, self.epoch = float(abs_floor), float(z), int(epoch)
+        self.meta: list = []            # per check: (rows m, blocks nb, batched)
+        self._rows: list = []           # (CHUNK, 3) int64 result blocks on the device
+        self.result: Optional[torch.Tensor] = None
+
+    def __len__(self) -> int:
+        return len(self.meta)
+
+    def _slot(self) -> torch.Tensor:
+        i = len(self.meta)
+        if i // self.CHUNK >= len(self._rows):
+            self._rows.append(torch.zeros(self.CHUNK, 3, dtype=torch.int64, device=self.device))
+        return self._rows[i // self.CHUNK][i % self.CHUNK]
+
+    def add(self, A, B, C, bias, alpha: float, beta: float) -> int:
+        """Check C = beta * bias + alpha * (A @ B): the GPU work is queued now.  Returns the check's index."""
+        if C.dtype != self.dtype:
+            raise ValueError(f"this group checks {self.dtype} outputs, not {C.dtype}")
+        st = matmul_zscores(A, B, C, bias, alpha=alpha, beta=beta, block=self.block, abs_floor=self.abs_floor,
+                            z=self.z, epoch=self.epoch, out=self._slot())
+        self.meta.append((st.m, st.nb, st.batched))
+        return len(self.meta) - 1
+
+    def launch(self) -> None:
+        """Every check's result row in one device tensor (checks, 3); never waits for the GPU."""
+        n = len(self.meta)
+        self.result = torch.cat(self._rows)[:n] if n else torch.zeros(0, 3, dtype=torch.int64, device=self.device)
+
+    def row(self, idx: int, r) -> tuple:
+        """Decode read-back row r (key, key with noise, unjudged) of check idx: (max_z, batch, row, col_block,
+        noise); an incomplete check (unjudged checksums) that does not alarm reads -1, never clean."""
+        m, nb, _batched = self.meta[idx]
+        key, keyd, unjudged = (int(v) for v in r)
+        z = _f32_of_bits(key >> 32)
+        if unjudged and z <= self.z:
+            z = UNJUDGED
+        b_i, rem = divmod((key & 0xFFFFFFFF) // 2, m * nb)
+        row, col_block = divmod(rem, nb)
+        return z, b_i, row, col_block, _f32_of_bits(keyd)
+
+
+def check_now(A, B, C, bias=None, alpha=1.0, beta=1.0, block=128, abs_floor=1e-20, z=6.0, epoch=0) -> tuple:
+    """One check answered right away: (max_z, batch, row, col_block, noise)."""
+    g = Group(C.device, C.dtype, block, abs_floor, z, epoch=epoch)
+    g.add(A, B, C, bias, alpha, beta)
+    g.launch()
+    return g.row(0, g.result[0].tolist())
+
+
+class SDCError(RuntimeError):
+    """Raised by flush() when a check alarms and raise_on_alert is set."""
+
+
+@dataclass
+class SDCEvent:
+    """One alert of the training guard."""
+    detector: str
+    layer: str
+    z: float
+    step: Optional[int] = None
+    row: Optional[int] = None
+    col_block: Optional[int] = None
+    noise: Optional[float] = None
+    nonfinite: bool = False
+    time: float = field(default_factory=time.time)
+    extra: dict = field(default_factory=dict)
+
+
+def _plain_linear(mod: torch.nn.Module) -> bool:
+    return isinstance(mod, torch.nn.Linear) and type(mod).forward is torch.nn.Linear.forward and \
+        "forward" not in mod.__dict__
+
+
+class SDCGuard:
+    """Checksums the matmuls of a model's linear layers on sampled steps (the reference's SDCGuard, protect() mode).
+
+        guard = SDCGuard().protect(model)
+        for step, batch in enumerate(data):
+            with guard.at_step(step):
+                loss = model(batch).sum()
+                loss.backward()
+        guard.flush()
+    """
+
+    def __init__(self, sample_rate: float = 1.0, block: int = 128, z: float = 6.0,
+                 on_alert: Optional[Callable[[SDCEvent], None]] = None, raise_on_alert: bool = False,
+                 abs_floor: Optional[float] = None, every: int = 10, max_pending: int = 4096,
+                 fresh_signs: bool = True, seed: int = 0):
+        if not 0.0 <= sample_rate <= 1.0:
+            raise ValueError("sample_rate is a share in [0, 1]")
+        self.sample_rate, self.block, self.z = float(sample_rate), int(block), float(z)
+        self.on_alert, self.raise_on_alert = on_alert, raise_on_alert
+        self.abs_floor = ABS_FLOOR if abs_floor is None else float(abs_floor)
+        self.every, self.max_pending, self.fresh_signs = int(every), int(max_pending), fresh_signs
+        self._rng = random.Random(seed)
+        self._lock = threading.RLock()
+        self._hooks: list = []
+        self._protected: list = []
+        self._active = False
+        self.step: Optional[int] = None
+        self._epoch = 0
+        self._groups: dict = {}             # (device, dtype) -> Group of the open checks
+        self._wctx: dict = {}               # id(layer) -> what its weight-gradient check needs, this step
+        self._pending: list = []            # (group, index, layer, pass, step)
+        self.events: list = []
+        self.results: list = []
+        self.stats = {"layers": 0, "matmuls_seen": 0, "checks": 0, "alerts": 0, "skipped_dtype": 0, "flushes": 0}
+
+    # ------------------------------------------------------------------------------------------- protect
+    def protect(self, model: torch.nn.Module) -> "SDCGuard":
+        """Check the forward product and both gradient products of every plain nn.Linear of `model`."""
+        for name, mod in model.named_modules():
+            if not _plain_linear(mod) or mod in self._protected:
+                continue
+            label = name or type(mod).__name__
+            self._protected.append(mod)
+            self._hooks.append(mod.register_forward_hook(self._after_forward(label)))
+            self._hooks.append(mod.register_full_backward_hook(self._after_backward(label)))
+            self.stats["layers"] += 1
+        return self
+
+    def unprotect(self) -> None:
+        for h in self._hooks:
+            h.remove()
+        self._hooks.clear()
+        self._protected.clear()
+
+    def _sampled(self) -> bool:
+        return self.sample_rate >= 1.0 or self._rng.random() < self.sample_rate
+
+    def _after_forward(self, label: str):
+        def hook(mod, args, y):
+            if not self._active or not args or not torch.is_tensor(y):
+                return None
+            x = args[0]
+            self.stats["matmuls_seen"] += 1
+            if self._sampled():
+                x2, y2 = x.reshape(-1, x.shape[-1]), y.reshape(-1, y.shape[-1])
+                self._queue(label, "forward", x2, mod.weight.t(), y2, mod.bias)
+            w = mod.weight
+            if y.requires_grad and w.requires_grad:
+                # the weight-gradient check needs x and dy; a layer used twice in a step gets the sum of two
+                # products as its weight gradient, which one (x, dy) pair does not check: it is left out
+                prev = self._wctx.get(id(mod))
+                if prev is not None:
+                    prev["shared"] = True
+                    return None
+                ctx = {"x": x.detach()}
+                self._wctx[id(mod)] = ctx
+                y.register_hook(lambda g, ctx=ctx: ctx.__setitem__("dy", g))
+                ctx["whook"] = w.register_hook(lambda gw, ctx=ctx: self._weight_grad(label, ctx, gw))
+            return None
+        return hook
+
+    def _weight_grad(self, label: str, ctx: dict, gw: torch.Tensor):
+        h = ctx.pop("whook", None)
+        if h is not None:
+            h.remove()
+        dy = ctx.get("dy")
+        if dy is None or ctx.get("shared") or not self._active:
+            return None
+        self.stats["matmuls_seen"] += 1
+        if self._sampled():
+            dy2 = dy.reshape(-1, dy.shape[-1])
+            x2 = ctx["x"].reshape(-1, ctx["x"].shape[-1])
+            self._queue(label, "weight grad", dy2.t().contiguous(), x2, gw, None)
+        return None
+
+    def _after_backward(self, label: str):
+        def hook(mod, grad_input, grad_output):
+            if not self._active or not grad_input or grad_input[0] is None or grad_output[0] is None:
+                return None
+            self.stats["matmuls_seen"] += 1
+            if self._sampled():
+                gx, gy = grad_input[0], grad_output[0]
+                self._queue(label, "input grad", gy.reshape(-1, gy.shape[-1]), mod.weight,
+                            gx.reshape(-1, gx.shape[-1]), None)
+            return None
+        return hook
+
+    def _queue(self, layer: str, where: str, A, B, C, bias) -> None:
+        """Queue one check of C = A @ B (+ bias): its GPU work starts now; the result is read at the flush."""
+        if C.dtype not in UNIT_ROUNDOFF or not C.is_cuda:
+            self.stats["skipped_dtype"] += 1
+            return
+        if C.numel() == 0:
+            return
+        with self._lock:
+            key = (C.device, C.dtype)
+            g = self._groups.get(key)
+            if g is None:
+                g = self._groups[key] = Group(C.device, C.dtype, self.block, self.abs_floor, self.z, self._epoch)
+            i = g.add(A, B, C, bias, 1.0, 1.0)
+            self._pending.append((g, i, layer, where, self.step))
+            self.stats["checks"] += 1
+
+    # ------------------------------------------------------------------------------------------- steps
+    @contextlib.contextmanager
+    def at_step(self, step: int):
+        """Check the protected layers' matmuls of this step (a nested call does nothing: the outer step counts)."""
+        if self._active:
+            yield self
+            return
+        self.step = int(step)
+        if self.fresh_signs:
+            self._epoch = self.step + 1        # a new signed-checksum pattern every checked step
+        self._active = True
+        try:
+            yield self
+        finally:
+            self._active = False
+            for ctx in self._wctx.values():          # (a forward whose backward did not run this step)
+                h = ctx.pop("whook", None)
+                if h is not None:
+                    h.remove()
+            self._wctx.clear()
+            with self._lock:
+                self._groups = {}                    # the next step's checks use its own sign pattern
+            if len(self._pending) >= self.max_pending or (self.every > 0 and self.step % self.every == 0):
+                self.flush()
+
+    def flush(self) -> list:
+        """Read every queued check back (one device-to-host copy per device), record the results and raise alerts.
+        Returns their CheckResults in queue order."""
+        with self._lock:
+            pending, self._pending = self._pending, []
+            groups = {id(g): g for g, *_ in pending}
+            self._groups = {}
+        if not pending:
+            return []
+        self.stats["flushes"] += 1
+        by_dev: dict = {}
+        for g in groups.values():
+            g.launch()
+            by_dev.setdefault(g.device, []).append(g)
+        rows = {}
+        for gs in by_dev.values():
+            back = torch.cat([g.result for g in gs]).cpu().tolist()
+            i = 0
+            for g in gs:
+                rows[id(g)] = back[i:i + len(g)]
+                i += len(g)
+        out, alerts = [], []
+        for g, i, layer, where, step in pending:
+            z, b_i, r_i, c_i, noise = g.row(i, rows[id(g)][i])
+            finite = math.isfinite(z)
+            res = CheckResult(ok=finite and z <= self.z, max_z=z, nonfinite=not finite, batch=None, row=r_i,
+                              col_block=c_i, noise=noise)
+            out.append(res)
+            if not res.ok:
+                ev = SDCEvent(detector="checksum", layer=layer, z=z, step=step, row=r_i, col_block=c_i, noise=noise,
+                              nonfinite=not finite, extra={"pass": where})
+                alerts.append(ev)
+        self.results.extend(out)
+        for ev in alerts:
+            self.events.append(ev)
+            self.stats["alerts"] += 1
+            if self.on_alert is not None:
+                self.on_alert(ev)
+        if alerts and self.raise_on_alert:
+            a = alerts[0]
+            raise SDCError(f"silent data corruption suspected: {a.layer} ({a.extra['pass']}) at step {a.step}, "
+                           f"z = {a.z:.3g}, row {a.row}, column block {a.col_block}")
+        return out

@@ -468,6 +468,17 @@ class ServeGuard:
         self.stats["layers"] += 1
         return slot
 
+    def replace_layer(self, slot: int, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> int:
+        """New constants for layer `slot` after its weights were reloaded; the slot and its state row stay."""
+        lay = self.layers[slot]
+        with torch.inference_mode(False), torch.no_grad():
+            lay["cs"] = LayerChecksums(weight, bias, self.block)
+        rows = self._rows[lay["device"]]
+        kmax = max(x["cs"].k for x in self.layers if x["device"] == lay["device"])
+        if not rows.fits(len(self.layers), kmax, self._cap_w):
+            self._rows[lay["device"]] = rows.enlarged(len(self.layers), kmax, self._cap_w)
+        return slot
+
     def _hook(self, slot: int):
         cs = self.layers[slot]["cs"]
 

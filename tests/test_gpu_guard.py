@@ -1,0 +1,96 @@
+"""Training-side API on the GPU: Group / check_now against check_matmul, and SDCGuard.protect + at_step + flush
+on a small bf16 MLP (forward, input-gradient and weight-gradient products of every linear layer), with a corrupted
+layer output caught, located and raised, and sampling."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _ab(m, k, n, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    A = torch.randn(m, k, device="cuda", generator=g).bfloat16()
+    B = (torch.randn(k, n, device="cuda", generator=g) * 0.05).bfloat16()
+    return A, B, (A.float() @ B.float()).bfloat16()
+
+
+def test_check_now_and_group_match_check_matmul():
+    from sdcguard_amd.checksum import check_matmul
+    from sdcguard_amd.guard import Group, check_now
+    A, B, C = _ab(200, 320, 300, 1)
+    z, b, r, cb, noise = check_now(A, B, C)
+    ref = check_matmul(A, B, C)
+    assert ref.ok and z == pytest.approx(ref.max_z, rel=1e-6) and noise > 0
+    C[77, 150] += 2.0
+    z, b, r, cb, noise = check_now(A, B, C)
+    assert z > 6 and (r, cb) == (77, 1)
+    g = Group(C.device, C.dtype)
+    shapes = [(64, 128, 130), (33, 256, 257), (128, 64, 128)]
+    mats = [_ab(*s, seed=i) for i, s in enumerate(shapes)]
+    mats[1][2][5, 256] += 1.0                                  # the narrow last block of the second check
+    idx = [g.add(a, bb, c, None, 1.0, 1.0) for a, bb, c in mats]
+    g.launch()
+    rows = g.result.cpu().tolist()
+    got = [g.row(i, rows[i]) for i in idx]
+    want = [check_matmul(a, bb, c) for a, bb, c in mats]
+    assert [x[0] > 6 for x in got] == [not w.ok for w in want] == [False, True, False]
+    assert got[1][2:4] == (5, 2)
+
+
+def _mlp(seed=0):
+    torch.manual_seed(seed)
+    return torch.nn.Sequential(torch.nn.Linear(256, 512), torch.nn.GELU(), torch.nn.Linear(512, 192)).to(
+        "cuda", torch.bfloat16)
+
+
+def test_protect_checks_forward_and_both_gradients():
+    from sdcguard_amd.guard import SDCGuard
+    m = _mlp()
+    g = SDCGuard(every=0).protect(m)
+    x = torch.randn(96, 256, device="cuda").bfloat16()
+    for step in range(2):
+        with g.at_step(step):
+            m(x).float().pow(2).mean().backward()
+    res = g.flush()
+    # per step: 2 forward, 1 input gradient (the first layer's input needs none), 2 weight gradients
+    assert len(res) == 10 and all(r.ok for r in res), [r.max_z for r in res]
+    assert g.stats["checks"] == 10 and g.stats["alerts"] == 0
+    assert max(r.max_z for r in res) > 0
+
+
+def test_corrupted_output_is_caught_and_raised():
+    from sdcguard_amd.guard import SDCError, SDCGuard
+    m = _mlp(seed=1)
+
+    def corrupt(mod, args, y):
+        y = y.clone()
+        y[10, 70] += 8.0
+        return y
+
+    m[2].register_forward_hook(corrupt)                        # runs before the guard's hook
+    seen = []
+    g = SDCGuard(every=0, raise_on_alert=True, on_alert=seen.append).protect(m)
+    x = torch.randn(64, 256, device="cuda").bfloat16()
+    with g.at_step(5):
+        with torch.no_grad():
+            m(x)
+    with pytest.raises(SDCError, match="2 \\(forward\\) at step 5"):
+        g.flush()
+    assert len(seen) == 1 and (seen[0].row, seen[0].col_block) == (10, 0) and seen[0].z > 6
+
+
+def test_sampling_and_steps_outside_the_guard():
+    from sdcguard_amd.guard import SDCGuard
+    m = _mlp(seed=2)
+    x = torch.randn(32, 256, device="cuda").bfloat16()
+    g = SDCGuard(sample_rate=0.0, every=0).protect(m)
+    with g.at_step(0):
+        m(x).sum().backward()
+    assert g.flush() == [] and g.stats["matmuls_seen"] == 5
+    g2 = SDCGuard(every=0).protect(torch.nn.Sequential(*[mm for mm in m]))
+    m(x).sum().backward()                                      # no step active: nothing queued
+    assert g2.flush() == []
+    g.unprotect()
+    g2.unprotect()
