@@ -226,8 +226,9 @@ int sdc_attn_check_noalloc(int dtype, const void* q, int64_t sqt, int64_t sqh, c
 /* ---- per-kernel timing (no counterpart in the reference; for benchmarks) ------------------------------------
  * With profiling on, every kernel launch is bracketed by two HIP events on its stream; sdc_profile_read waits for
  * them and sums the durations of one kernel: "expected_gemm" (serving GEMM), "serve_fused", "serve_sums",
- * "serve_score", "b_stage", "b_finish", "split", "train_gemm", "train_score", "quant_gemm_i8", "quant_gemm_fp8",
- * "quant_score_i8", "quant_score_fp8", "fingerprint3", "fingerprint2". */
+ * "serve_score", "b_stage", "b_finish", "split", "train_gemm", "train_score" (also the grouped check's),
+ * "col_gemm", "xstage", "xfinish", "row_gemm", "ypass" (sdc_linear_check), "quant_gemm_i8", "quant_gemm_fp8",
+ * "quant_score_i8", "quant_score_fp8", "fingerprint3", "fingerprint2", "kv_fingerprint", "attn_check". */
 int sdc_profile_enable(int on);
 int sdc_profile_reset(void);
 int sdc_profile_read(const char* name, double* total_ms, int64_t* launches);
