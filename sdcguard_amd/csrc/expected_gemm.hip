@@ -147,16 +147,33 @@ __device__ __forceinline__ void norm_acc(u32x4 v, float& sq, float& ab) {
 // as the 64 columns of a row-block check).  Each wave computes 64 x 64 with 2 x 2 fragments of v_mfma_f32_32x32x16
 // and, per fragment pair, the three parts of B into the same accumulator.
 //
-// Depth advances in stages of 32.  Per stage s a thread loads its 16-byte chunks of stage s + 1 into one of two
-// register sets (coalesced: 4 consecutive threads read one 64-byte row segment), the waves run the MFMAs of stage s
-// from one of two LDS buffers, the thread stores stage s + 1 into the other buffer, and one barrier ends the stage.
-// The loads are unconditional in the steady state (a guarded load makes the compiler wait for it at the end of the
-// guarded block).  LDS rows are padded to 40 elements so the 8 lanes of each ds_read_b128 phase hit distinct banks.
+// Depth advances in stages of 32 (two MFMA steps of 16) through three LDS buffers.  In stage s a wave reads the
+// fragments of step s.1 while the MFMAs of step s.0 run, then those of step (s + 1).0 while the MFMAs of s.1 run, so
+// LDS reads overlap the matrix cores inside every wave; it then stores stage s + 2 (loaded from global memory one
+// stage earlier) into the third buffer, issues the loads of stage s + 3, and one barrier ends the stage.  A buffer
+// is rewritten only after the barrier that follows every wave's last read of it.  Loads and stores are
+// unconditional (a guarded load makes the compiler wait for it at the end of the guarded block): past the last stage
+// they repeat the last stage's data into a buffer nobody reads again.
+// LDS rows hold 32 elements (64 bytes, four 16-byte chunks); chunk q of row r sits at position q ^ ((r / 2) % 4),
+// so the eight lanes of each ds_read_b128 phase (eight consecutive rows, one chunk) and of each ds_write_b128 phase
+// (two rows, four chunks each) hit 32 distinct banks.
 // Workgroups are numbered so that each XCD (dispatch is round-robin over the eight) takes a contiguous range of
 // tiles: column tiles of one row tile, and row tiles of one depth slice, share an XCD's L2.
 constexpr int KS = 32;                 // depth per stage
-constexpr int LP = KS + 8;             // LDS row pitch (elements)
 constexpr int NT = 512;                // threads per workgroup
+constexpr int NBUF = 3;                // LDS buffers
+
+__device__ __forceinline__ int lds_at(int row, int chunk) { return row * KS + 8 * (chunk ^ ((row >> 1) & 3)); }
+
+// s_waitcnt immediate that waits until at most n vector memory operations are outstanding (other counters free)
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+// 16 bytes per lane from global memory straight into LDS: lane L's bytes land at lds + 16 L (lds wave-uniform)
+__device__ __forceinline__ void lds_load16(const uint8_t* g, uint16_t* lds) {
+  __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g), lds, 16, 0, 0);
+}
+
+// ... until no LDS or scalar-memory operation is outstanding
+constexpr int lgkmcnt0_imm() { return 15 | (3 << 14) | (7 << 4); }
 
 template <int WGN, int NP>
 struct Tile {
@@ -174,14 +191,14 @@ struct Tile {
 // parts), SDC_I8 (A int8 and 2 int8 parts: the block sums' base-128 digits, each into its own int32
 // accumulator; depth and strides are in pairs of int8 so that a 16-byte chunk is 8 "elements" as for 16-bit data,
 // and the 32x32x32 int8 MFMA takes a k-step of 16 pairs).
-template <int MODE, int WGN, bool VEC>
+template <int MODE, int WGN, bool VEC, bool DIRECT>
 __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
   constexpr int NP = MODE == SDC_I8 ? 2 : 3;                  // parts
   constexpr int NACC = MODE == SDC_I8 ? 2 : 1;                // accumulator sets
   constexpr int DT = MODE == SDC_FP16 ? SDC_FP16 : SDC_BF16;  // element type of the LDS tiles (16-bit modes)
   constexpr int ESA = MODE == SDC_FP8 ? 1 : 2;                // bytes per A element in memory
   using T = Tile<WGN, NP>;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2][T::ROWS * LP];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[NBUF][T::ROWS * KS];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int wm = w / WGN, wn = w % WGN;
   const int64_t nrt = sdc_cdiv(g.m, T::TM) + (g.goffs ? g.ngroups : 0), nct = sdc_cdiv(g.N, T::TN);
@@ -241,7 +258,7 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
     const int64_t row = r0 + c / 4;
     aok[j] = row < m;
     asrc[j] = Ab + (aok[j] ? row : 0) * g.sam * ESA;
-    alds[j] = (c / 4) * LP + 8 * (c % 4);
+    alds[j] = lds_at(c / 4, c % 4);
     ak[j] = 8 * (c % 4);
   }
   const uint16_t* bsrc[T::NB];
@@ -254,49 +271,50 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
     const int64_t col = c0 + cr % T::TN;
     bok[j] = col < N;
     bsrc[j] = Pb + ((int64_t)(cr / T::TN) * N + (bok[j] ? col : 0)) * g.sbc;
-    blds[j] = (T::TM + cr) * LP + 8 * (c % 4);
+    blds[j] = lds_at(T::TM + cr, c % 4);
     bk[j] = 8 * (c % 4);
   }
 
   // VEC (k-contiguous operands, depth a multiple of KS): loads are unconditional and unmasked.  Rows of A past m
   // read row 0 and columns past N read column 0; they only feed rows / columns of E that are never stored.
   // Otherwise every element is loaded with its own bounds check and zero-filled.
-  u32x4 ra[2][T::NA], rb[2][T::NB];
-  auto load = [&](int set, int st) {
+  u32x4 ra[T::NA], rb[T::NB];
+  auto load = [&](int st) {
     const int64_t k0 = kbeg + (int64_t)st * KS;
     if constexpr (VEC) {
 #pragma unroll
       for (int j = 0; j < T::NA; ++j) {
         if constexpr (MODE == SDC_FP8)
-          ra[set][j] = fp8x8_to_bf16(*reinterpret_cast<const u32x2*>(asrc[j] + (k0 + ak[j])));
+          ra[j] = fp8x8_to_bf16(*reinterpret_cast<const u32x2*>(asrc[j] + (k0 + ak[j])));
         else
-          ra[set][j] = *reinterpret_cast<const u32x4*>(asrc[j] + (k0 + ak[j]) * 2);
+          ra[j] = *reinterpret_cast<const u32x4*>(asrc[j] + (k0 + ak[j]) * 2);
       }
 #pragma unroll
-      for (int j = 0; j < T::NB; ++j) rb[set][j] = *reinterpret_cast<const u32x4*>(bsrc[j] + (k0 + bk[j]));
+      for (int j = 0; j < T::NB; ++j) rb[j] = *reinterpret_cast<const u32x4*>(bsrc[j] + (k0 + bk[j]));
     } else {
 #pragma unroll
       for (int j = 0; j < T::NA; ++j) {
-        if constexpr (MODE == SDC_FP8) ra[set][j] = load8_fp8(asrc[j], g.sak, k0 + ak[j], kend, aok[j]);
-        else ra[set][j] = load8<false>((const uint16_t*)asrc[j], g.sak, k0 + ak[j], kend, aok[j]);
+        if constexpr (MODE == SDC_FP8) ra[j] = load8_fp8(asrc[j], g.sak, k0 + ak[j], kend, aok[j]);
+        else ra[j] = load8<false>((const uint16_t*)asrc[j], g.sak, k0 + ak[j], kend, aok[j]);
       }
 #pragma unroll
-      for (int j = 0; j < T::NB; ++j) rb[set][j] = load8<false>(bsrc[j], 1, k0 + bk[j], kend, bok[j]);
+      for (int j = 0; j < T::NB; ++j) rb[j] = load8<false>(bsrc[j], 1, k0 + bk[j], kend, bok[j]);
     }
   };
   float sq[T::NA], ab[T::NA];
 #pragma unroll
   for (int j = 0; j < T::NA; ++j) sq[j] = ab[j] = 0.f;
-  auto store = [&](int set, int buf) {
+  // counted: this store holds a stage of the slice (not a repeat past the last one), so its A rows add to the norms
+  auto store = [&](int buf, bool counted) {
     uint16_t* L = lds[buf];
 #pragma unroll
     for (int j = 0; j < T::NA; ++j) {
-      *reinterpret_cast<u32x4*>(&L[alds[j]]) = ra[set][j];
+      *reinterpret_cast<u32x4*>(&L[alds[j]]) = ra[j];
       if constexpr (MODE != SDC_I8)
-        if (norms && t + NT * j < T::ACH) norm_acc<DT>(ra[set][j], sq[j], ab[j]);
+        if (norms && counted && t + NT * j < T::ACH) norm_acc<DT>(ra[j], sq[j], ab[j]);
     }
 #pragma unroll
-    for (int j = 0; j < T::NB; ++j) *reinterpret_cast<u32x4*>(&L[blds[j]]) = rb[set][j];
+    for (int j = 0; j < T::NB; ++j) *reinterpret_cast<u32x4*>(&L[blds[j]]) = rb[j];
   };
 
   f32x16 acc[NACC][2][2];
@@ -309,63 +327,128 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[q][i][n][r] = 0.f;         // (int8: the bits of integer 0)
 
-  auto compute = [&](int buf) {
+  // the fragments of one MFMA step (16 deep): A rows of this wave, B columns of the NP parts
+  struct Frag {
+    u32x4 a[2], b[NP][2];
+  };
+  auto read = [&](Frag& f, int buf, int step) {
     const uint16_t* L = lds[buf];
+    const int q = 2 * step + (lane >> 5);
 #pragma unroll
-    for (int s = 0; s < KS / 16; ++s) {
-      const int ko = 16 * s + (lane >> 5) * 8;
-      u32x4 a[2], bv[NP][2];
+    for (int i = 0; i < 2; ++i) f.a[i] = *reinterpret_cast<const u32x4*>(&L[lds_at(wm * 64 + 32 * i + (lane & 31), q)]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const u32x4*>(&L[(wm * 64 + 32 * i + (lane & 31)) * LP + ko]);
+    for (int p = 0; p < NP; ++p)
 #pragma unroll
-      for (int p = 0; p < NP; ++p)
+      for (int n = 0; n < 2; ++n)
+        f.b[p][n] = *reinterpret_cast<const u32x4*>(&L[lds_at(T::TM + p * T::TN + wn * 64 + 32 * n + (lane & 31), q)]);
+  };
+  auto mma = [&](const Frag& f) {
 #pragma unroll
-        for (int n = 0; n < 2; ++n)
-          bv[p][n] = *reinterpret_cast<const u32x4*>(&L[(T::TM + p * T::TN + wn * 64 + 32 * n + (lane & 31)) * LP + ko]);
+    for (int p = 0; p < NP; ++p)
 #pragma unroll
-      for (int p = 0; p < NP; ++p)
-#pragma unroll
-        for (int n = 0; n < 2; ++n) {
-          if constexpr (MODE == SDC_I8) {
-            acc[p][0][n] = mfma32_i8(a[0], bv[p][n], acc[p][0][n]);
-            acc[p][1][n] = mfma32_i8(a[1], bv[p][n], acc[p][1][n]);
-          } else {
-            acc[0][0][n] = mfma32<DT>(a[0], bv[p][n], acc[0][0][n]);
-            acc[0][1][n] = mfma32<DT>(a[1], bv[p][n], acc[0][1][n]);
-          }
+      for (int n = 0; n < 2; ++n) {
+        if constexpr (MODE == SDC_I8) {
+          acc[p][0][n] = mfma32_i8(f.a[0], f.b[p][n], acc[p][0][n]);
+          acc[p][1][n] = mfma32_i8(f.a[1], f.b[p][n], acc[p][1][n]);
+        } else {
+          acc[0][0][n] = mfma32<DT>(f.a[0], f.b[p][n], acc[0][0][n]);
+          acc[0][1][n] = mfma32<DT>(f.a[1], f.b[p][n], acc[0][1][n]);
         }
-    }
+      }
   };
 
-  // stage s: loaded into register set s % 2 during stage s - 1 ... s - 2, stored into LDS buffer s % 2 at the end of
-  // stage s - 1.  The steady-state loop loads unconditionally; the last one to three stages are peeled.
-  int st = 0;
-  if (nst > 0) {
-    load(0, 0);
-    if (nst > 1) load(1, 1);
-    store(0, 0);
-    __syncthreads();
-    for (; st + 3 < nst; st += 2) {
-      load(0, st + 2);
-      compute(0);
-      store(1, 1);
-      __syncthreads();
-      load(1, st + 3);
-      compute(1);
-      store(0, 0);
-      __syncthreads();
+  if constexpr (DIRECT) {
+    // Global memory straight into LDS (global_load_lds_dwordx4): one instruction of a wave fills 16 consecutive
+    // tile rows, lane L the 16 bytes at position L % 4 of row L / 4, i.e. the chunk that the swizzle puts there.
+    // The tile's ROWS / 16 instructions per stage are dealt round-robin to the 8 waves (indexes past the end repeat
+    // the last one: the same bytes written twice).  Stage s + 3 is loaded during stage s into the buffer of stage
+    // s, after the barrier in the middle of stage s that follows every wave's last read of it; the wait before that
+    // barrier leaves only stage s + 2 in flight, so stage s + 1 is complete when its first fragments are read.
+    constexpr int NI = T::ROWS / 16;                           // load instructions per stage
+    constexpr int NIW = (NI + 7) / 8;                           // per wave
+    const uint8_t* src[NIW];
+    int dst[NIW];
+#pragma unroll
+    for (int j = 0; j < NIW; ++j) {
+      const int I = (w + 8 * j) < NI ? w + 8 * j : NI - 1;
+      const int R = 16 * I + lane / 4, P = lane % 4;
+      const int q = P ^ ((R >> 1) & 3);
+      dst[j] = 16 * I * KS;
+      if (R < T::TM) {
+        const int64_t row = r0 + R;
+        src[j] = Ab + (row < m ? row : 0) * g.sam * 2 + 16 * q;
+      } else {
+        const int cr = R - T::TM;
+        const int64_t col = c0 + cr % T::TN;
+        src[j] = reinterpret_cast<const uint8_t*>(Pb + ((int64_t)(cr / T::TN) * N + (col < N ? col : 0)) * g.sbc) + 16 * q;
+      }
     }
-    const int left = nst - st;              // 1, 2 or 3
-    if (left == 3) load(0, st + 2);
-    compute(0);
-    if (left >= 2) {
-      store(1, 1);
+    auto issue = [&](int st, int buf) {
+      const int64_t off = (kbeg + (int64_t)st * KS) * 2;
+#pragma unroll
+      for (int j = 0; j < NIW; ++j)
+        lds_load16(src[j] + off, &lds[buf][dst[j]]);
+    };
+    if (nst > 0) {
+      const int last = nst - 1;
+      issue(0, 0);
+      issue(1 < last ? 1 : last, 1);
+      issue(2 < last ? 2 : last, 2);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NIW));        // stage 0 in LDS (stages 1, 2 may be in flight)
       __syncthreads();
-      compute(1);
-      if (left == 3) {
-        store(0, 0);
+      Frag fx, fy;
+      read(fx, 0, 0);
+      // (the reads of fx complete under the MFMAs that follow them; waiting for them at the end of a stage, where
+      // it costs nothing, keeps the compiler from waiting for the next fragments too at the top of the loop)
+      __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+      int b0 = 0, b1 = 1;                                      // buffers of stages s, s + 1
+      for (int s = 0; s < nst; ++s) {
+        read(fy, b0, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(fx);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(NIW));          // stage s + 1 in LDS (stage s + 2 may be in flight)
         __syncthreads();
-        compute(0);
+        issue(s + 3 < last ? s + 3 : last, b0);
+        read(fx, b1, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(fy);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+        b0 = b1;
+        b1 = b1 == NBUF - 1 ? 0 : b1 + 1;
+      }
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));              // no load into LDS outlives the workgroup
+    }
+  } else {
+    if (nst > 0) {
+      const int last = nst - 1;
+      load(0);
+      store(0, true);
+      load(1 < last ? 1 : last);
+      store(1, nst > 1);
+      __syncthreads();
+      Frag fx, fy;
+      read(fx, 0, 0);
+      load(2 < last ? 2 : last);
+      int b0 = 0, b1 = 1, b2 = 2;                       // buffers of stages s, s + 1, s + 2
+      for (int s = 0; s < nst; ++s) {
+        // (the scheduling barriers keep each group of reads ahead of the MFMAs it overlaps)
+        read(fy, b0, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(fx);
+        __builtin_amdgcn_sched_barrier(0);
+        read(fx, b1, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(fy);
+        __builtin_amdgcn_sched_barrier(0);
+        store(b2, s + 2 < nst);
+        load(s + 3 < last ? s + 3 : last);
+        __syncthreads();
+        const int bt = b0;
+        b0 = b1;
+        b1 = b2;
+        b2 = bt;
       }
     }
   }
@@ -419,8 +502,18 @@ __global__ __launch_bounds__(NT) void expected_gemm_kernel(GemmArgs g) {
 
 template <int MODE, int WGN>
 int launch_dt(GemmArgs g, bool vec, int64_t blocks, hipStream_t stream) {
-  if (vec) hipLaunchKernelGGL((expected_gemm_kernel<MODE, WGN, true>), dim3((unsigned)blocks), dim3(NT), 0, stream, g);
-  else hipLaunchKernelGGL((expected_gemm_kernel<MODE, WGN, false>), dim3((unsigned)blocks), dim3(NT), 0, stream, g);
+  // straight-to-LDS loads for k-contiguous 16-bit (or int8 pair) operands when no row norms are asked for
+  bool direct = false;
+  if constexpr (MODE != SDC_FP8) {
+    if (vec && g.XN == nullptr) {
+      hipLaunchKernelGGL((expected_gemm_kernel<MODE, WGN, true, true>), dim3((unsigned)blocks), dim3(NT), 0, stream, g);
+      direct = true;
+    }
+  }
+  if (direct) {
+  } else if (vec)
+    hipLaunchKernelGGL((expected_gemm_kernel<MODE, WGN, true, false>), dim3((unsigned)blocks), dim3(NT), 0, stream, g);
+  else hipLaunchKernelGGL((expected_gemm_kernel<MODE, WGN, false, false>), dim3((unsigned)blocks), dim3(NT), 0, stream, g);
   SDC_LAUNCH_CHECK();
   return SDC_OK;
 }
