@@ -3,18 +3,18 @@
 // Column-block check (the serving check, serve.py:301-396 / _serve_fast.py:102-526): for every row i of y and
 // block of 128 output columns, sum_j y_ij against x_i . B2 (B2: the layer's block sums of W, three parts, made once
 // per layer), scored as the serving check scores it (unjudged checksums count, score 0).
-// Row-block check (the north star's row side; the column-block check of y^T = W x^T, checksum.py:435-530 on
+// Row-block check (the column-block check of y^T = W x^T, checksum.py:435-530 on
 // transposed operands): for every column j and block of 128 rows, sum_i y_ij against W_j . (sum_i x_i), scored as
 // the training check scores it (unjudged checksums score -1).
 //
 // Five launches, no host synchronisation:
 //   1. xstage: the plain and signed sums of every 128-row block of x, split into three bf16 parts (the B operand
 //      of the row check's GEMM), and per 256-deep chunk partials of those sums' statistics and of x's row norms;
-//   2. xfinish: those partials added up in chunk order (the column check's |x_i|_2^2 and |x_i|_1, the row blocks'
-//      statistics and sign-pattern sums);
+//   2. xfinish, on a side stream beside 3: those partials added up in chunk order (the column check's |x_i|_2^2 and
+//      |x_i|_1, the row blocks' statistics and sign-pattern sums);
 //   3. the row check's GEMM E_row = W @ (x block sums) on MFMA (expected_gemm.hip; W's row norms are the layer's,
 //      made once by sdc_layer_constants);
-//   4. the column check's GEMM E_col = x @ B2 on MFMA -- independent of 1 to 3, so it can run on a side stream
+//   4. the column check's GEMM E_col = x @ B2 on MFMA -- independent of 1 to 3, so it can run on the side stream
 //      concurrently with them;
 //   5. ypass: one read of y.  A workgroup owns a 128 x 128 tile (one row block by one column block): every thread
 //      reads 8 rows x 8 columns (eight 16-byte loads, all in flight), adds the four sums (plain, signed, squares,
@@ -596,12 +596,15 @@ extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const voi
     hipLaunchKernelGGL(xstage_kernel, dim3((unsigned)L.nkc, (unsigned)L.mb), dim3(256), 0, stream, xa);
     SDC_LAUNCH_CHECK();
   }
+  // 2. xfinish on the side stream, beside the row check's GEMM (whose 8-row-tile grid leaves CUs free)
+  hipStream_t fin = sdc_fork(stream);
+  if (!fin) return SDC_ELAUNCH;
   {
-    SdcProf prof("xfinish", stream);
-    hipLaunchKernelGGL(xfinish_kernel, dim3((unsigned)L.mb), dim3(256), 0, stream, xa);
+    SdcProf prof("xfinish", fin);
+    hipLaunchKernelGGL(xfinish_kernel, dim3((unsigned)L.mb), dim3(256), 0, fin, xa);
     SDC_LAUNCH_CHECK();
   }
-  // 2. the row check's GEMM: E_row = W @ (x block sums), each XCD taking every depth slice of its rows (W's row
+  // 3. the row check's GEMM: E_row = W @ (x block sums), each XCD taking every depth slice of its rows (W's row
   //    norms are the layer's, made once)
   GemmArgs gr{};
   gr.A = (const uint16_t*)W; gr.sab = 0; gr.sam = swn; gr.sak = 1;
@@ -611,7 +614,7 @@ extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const voi
   gr.prof_name = "row_gemm";
   rc = sdc_gemm_launch(SDC_BF16, gr, 1, stream);
   if (rc != SDC_OK) return rc;
-  if (concurrent && (rc = sdc_join(stream, side)) != SDC_OK) return rc;
+  if ((rc = sdc_join(stream, fin)) != SDC_OK) return rc;     // (the side stream also holds the concurrent GEMM)
 
   // 4. one pass over y: both checks
   YArgs ya{};
