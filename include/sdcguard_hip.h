@@ -74,6 +74,27 @@ int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t
                      float beta, float z, float abs_floor, const float* sign_table, int64_t* result, void* workspace,
                      int64_t workspace_bytes, float* scores_out, hipStream_t stream);
 
+/* ---- precise check of one matmul with an fp32 output (the accumulator itself) ------------------------------
+ * Replaces checksum.matmul_zscores_acc / _acc_zscores / check_matmul_acc (checksum.py:537-692): the column-block check
+ * of C = beta * bias + alpha * (A @ B) for bf16/fp16 A and B (dtype) and an fp32 C that was not rounded to 16 bits.
+ * Both sides of every checksum are float64 (block sums of B and of C, A @ B2); the noise is the fp32 accumulation's
+ * rounding u (C1 sqrt(k) |alpha| |a_row|_2 |B_block|_F + (C2 sqrt(k) + C3 k / nfma + sqrt(width)) |C_block|_2),
+ * u = 2^-24, C1 = 0.6, C2 = C3 = 1; Inf/NaN judged as checksum._judge_nonfinite with fp32 outputs.
+ *   A, B, C, batches, strides, bs (<= 128), sign_table, result, scores_out: as sdc_matmul_check (C fp32; batch_a and
+ *     batch_b are 1 or batch_c).  nfma: products per tensor-core truncation step (0: none).
+ *   bias_kind: 0 none, 1 vector of n (stride sbias_n), 2 matrix (strides sbias_b, sbias_m, sbias_n); + 4 when the
+ *     bias is fp32 (otherwise of dtype).  k >= 1 (a product with k = 0 is checked as one zero column).
+ *   workspace: at least sdc_matmul_check_acc_workspace(batch_a, batch_b, batch_c, m, k, n, bs) bytes. */
+int64_t sdc_matmul_check_acc_workspace(int64_t batch_a, int64_t batch_b, int64_t batch_c, int64_t m, int64_t k,
+                                       int64_t n, int64_t bs);
+int sdc_matmul_check_acc(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, int64_t batch_a,
+                         const void* B, int64_t sbb, int64_t sbk, int64_t sbn, int64_t batch_b, const float* C,
+                         int64_t scb, int64_t scm, int64_t scn, int64_t batch_c, int64_t m, int64_t k, int64_t n,
+                         int64_t bs, const void* bias, int bias_kind, int64_t sbias_b, int64_t sbias_m,
+                         int64_t sbias_n, float alpha, float beta, float nfma, float z, float abs_floor,
+                         const float* sign_table, int64_t* result, void* workspace, int64_t workspace_bytes,
+                         float* scores_out, hipStream_t stream);
+
 /* ---- both block checksums of one linear layer, one pass over y (no counterpart function in the reference) --------
  * y = x @ W^T (+ bias): the column-block check of sdc_check_static (the serving check, serve.py:301-396) and the
  * row-block check of sdc_matmul_check on the transposed views (W, x^T, y^T, bias[:, None]; checksum.py:435-530),
@@ -228,7 +249,8 @@ int sdc_attn_check_noalloc(int dtype, const void* q, int64_t sqt, int64_t sqh, c
  * them and sums the durations of one kernel: "expected_gemm" (serving GEMM), "serve_fused", "serve_sums",
  * "serve_score", "b_stage", "b_finish", "split", "train_gemm", "train_score" (also the grouped check's),
  * "col_gemm", "xstage", "xfinish", "row_gemm", "ypass" (sdc_linear_check), "quant_gemm_i8", "quant_gemm_fp8",
- * "quant_score_i8", "quant_score_fp8", "fingerprint3", "fingerprint2", "kv_fingerprint", "attn_check". */
+ * "quant_score_i8", "quant_score_fp8", "fingerprint3", "fingerprint2", "kv_fingerprint", "attn_check", "acc_bsums",
+ * "acc_finish", "acc_anorm", "acc_gemm", "acc_score" (sdc_matmul_check_acc). */
 int sdc_profile_enable(int on);
 int sdc_profile_reset(void);
 int sdc_profile_read(const char* name, double* total_ms, int64_t* launches);

@@ -33,6 +33,9 @@ SIGNATURES = {
     "sdc_matmul_check_workspace": (I64, [I64, I64, I64, I64, I64, I64]),
     "sdc_matmul_check": (I32, [I32, P, I64, I64, I64, I64, P, I64, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, I64,
                                I64, P, I32, I64, I64, I64, F32, F32, F32, F32, P, P, P, I64, P, P]),
+    "sdc_matmul_check_acc_workspace": (I64, [I64, I64, I64, I64, I64, I64, I64]),
+    "sdc_matmul_check_acc": (I32, [I32, P, I64, I64, I64, I64, P, I64, I64, I64, I64, P, I64, I64, I64, I64, I64, I64,
+                                   I64, I64, P, I32, I64, I64, I64, F32, F32, F32, F32, F32, P, P, P, I64, P, P]),
     "sdc_expected_splits": (I64, [I64, I64, I64]),
     "sdc_linear_check_workspace": (I64, [I64, I64, I64]),
     "sdc_linear_check": (I32, [I32, P, I64, P, I64, P, I64, P, I64, I64, I64, P, I64, P, P, P, P, P, F32, F32, P,

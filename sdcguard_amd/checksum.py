@@ -201,6 +201,83 @@ def matmul_zscores(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, bias: Opti
     return CheckStat(result=out, m=m, nb=nb, batched=C.dim() == 3, z=float(z))
 
 
+# The precise check of an fp32 output (checksum.py:537-563): u = 2^-24 and the noise model's constants.
+ACC_UNIT = 2.0 ** -24
+ACC_C1, ACC_C2, ACC_C3 = 0.6, 1.0, 1.0
+
+
+def acc_supported(A: torch.Tensor, C: torch.Tensor) -> bool:
+    """The precise check takes an fp32 C of bf16/fp16 operands (checksum.py:563-564)."""
+    return C.dtype == torch.float32 and A.dtype in UNIT_ROUNDOFF
+
+
+def matmul_zscores_acc(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, bias: Optional[torch.Tensor] = None, *,
+                       alpha: float = 1.0, beta: float = 1.0, block: int = 128, abs_floor: float = ABS_FLOOR,
+                       z: float = 6.0, nfma: Optional[int] = None, epoch: int = 0,
+                       out: Optional[torch.Tensor] = None,
+                       scores_out: Optional[torch.Tensor] = None) -> Optional[CheckStat]:
+    """Queue the precise check of C = beta*bias + alpha*(A @ B), C the fp32 result (not rounded), A and B bf16/fp16
+    (checksum.py:587-607): float64 checksums against the fp32 accumulation's rounding.  Same result row and read-back
+    as matmul_zscores (resolve() decodes both).  None if the dtypes don't fit.  nfma: tensor-core products per
+    truncation step (None: no tensor cores)."""
+    from . import _lib
+    if not acc_supported(A, C):
+        return None
+    if C.numel() == 0:
+        raise ValueError("empty output: nothing to check (callers skip these, see is_empty)")
+    _lib.require_gpu(A, B, C, bias)
+    dt = A.dtype
+    if A.shape[-1] == 0:                                   # checksum.py:386-392: one zero column
+        A = A.new_zeros(*A.shape[:-1], 1)
+        B = B.new_zeros(*B.shape[:-2], 1, B.shape[-1])
+    B = B if B.dtype == dt else B.to(dt)
+    ba, sab, m, k, sam, sak = _dims3(A)
+    bb, sbb, kb, n, sbk, sbn = _dims3(B)
+    bc, scb, mc, nc, scm, scn = _dims3(C)
+    if mc != m or kb != k or nc != n:
+        raise ValueError(f"shape mismatch: A{tuple(A.shape)} B{tuple(B.shape)} C{tuple(C.shape)}")
+    if ba not in (1, bc) or bb not in (1, bc) or (bc > 1 and ba == 1 and bb == 1):
+        raise ValueError(f"batch mismatch: A{tuple(A.shape)} B{tuple(B.shape)} C{tuple(C.shape)}")
+    bs = max(1, min(block, n))
+    if bs > 128:
+        raise _lib.HipLibraryError(f"blocks up to 128 wide, not {bs}")
+    kind, b_ptr, sb_b, sb_m, sb_n = 0, None, 0, 0, 0
+    if bias is not None and beta != 0:
+        if bias.dtype not in (dt, torch.float32):
+            bias = bias.float()
+        if bias.dim() == 1 and bias.numel() in (1, n):
+            kind, b_ptr, sb_n = 1, bias, (0 if bias.numel() == 1 else bias.stride(0))
+        else:
+            full = torch.broadcast_to(bias, (bc, m, n)) if bias.dim() == 3 or C.dim() == 3 else \
+                torch.broadcast_to(bias, (m, n)).unsqueeze(0)
+            kind, b_ptr = 2, full
+            sb_b, sb_m, sb_n = full.stride(0) if C.dim() == 3 else 0, full.stride(1), full.stride(2)
+        if b_ptr.dtype == torch.float32:
+            kind |= 4
+    if out is None:
+        out = torch.zeros(3, dtype=torch.int64, device=C.device)
+    L = _lib.lib()
+    ws_bytes = int(L.sdc_matmul_check_acc_workspace(ba, bb, bc, m, k, n, bs))
+    ws = _lib.workspace(C.device, ws_bytes)
+    rc = L.sdc_matmul_check_acc(
+        _lib.dtype_code(dt), A.data_ptr(), sab, sam, sak, ba, B.data_ptr(), sbb, sbk, sbn, bb,
+        C.data_ptr(), scb, scm, scn, bc, m, k, n, bs, None if b_ptr is None else b_ptr.data_ptr(), kind,
+        sb_b, sb_m, sb_n, float(alpha), float(beta), float(nfma or 0), float(z), float(abs_floor),
+        sign_table(C.device, epoch).data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
+        None if scores_out is None else scores_out.data_ptr(), _lib.stream_of(C))
+    _lib.check(rc, "sdc_matmul_check_acc")
+    nb = -(-n // bs)
+    return CheckStat(result=out, m=m, nb=nb, batched=C.dim() == 3, z=float(z))
+
+
+def check_matmul_acc(A, B, C, bias=None, *, z: float = 6.0, nfma: Optional[int] = None, **kw) -> Optional[CheckResult]:
+    """matmul_zscores_acc, answered now (checksum.py:689-694).  None if the dtypes don't fit."""
+    if C.numel() == 0 and acc_supported(A, C):
+        return CheckResult(ok=True, max_z=0.0, nonfinite=False)
+    st = matmul_zscores_acc(A, B, C, bias, z=z, nfma=nfma, **kw)
+    return None if st is None else resolve([st], z)[0]
+
+
 def _f32_of_bits(b: int) -> float:
     import struct
     return struct.unpack("<f", struct.pack("<I", b & 0xFFFFFFFF))[0]

@@ -33,3 +33,8 @@ def as_f32(w: np.ndarray, dtype: str) -> np.ndarray:
 
 def names(f):
     return [str(n) for n in f["names"]]
+
+
+def f32_words(w: np.ndarray) -> np.ndarray:
+    """float32 values stored as pairs of 16-bit words (low word first)."""
+    return np.ascontiguousarray(w.astype(np.uint16)).reshape(-1).view(np.uint32).view(np.float32)

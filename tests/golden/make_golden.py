@@ -9,6 +9,7 @@ cases, the inputs and the reference's answers:
   * signs.npz      the epoch-0 sign table of widths 1..128 and the epoch-3 table (checksum._signs at seed 1);
   * train.npz      checksum.matmul_zscores + resolve: every checksum's score (the array the reference reduces
                    with torch.max, recorded on the way) and the resolved (max_z, batch, row, col_block, noise);
+  * acc.npz        checksum.matmul_zscores_acc + resolve (the precise check of an fp32 output): the same records;
   * serve.npz      serve.check_static_impl: every checksum's score, the state row (keys and counts);
   * quant.npz      modes.judge on fp8 e4m3 and int8 GEMMs (inputs from modes._inputs, results of modes.gemm's CPU
                    path, with and without an injected fault): per-block z and wrong-block counts;
@@ -196,6 +197,93 @@ def make_train(cs):
                                       res.noise], np.float64)
     out["names"] = np.array(names)
     np.savez_compressed(os.path.join(OUT, "train.npz"), **out)
+    return len(names)
+
+
+def _acc_cases():
+    """Small products with an fp32 output: (name, A, B, C, bias, alpha, beta, nfma, epoch)."""
+    g = torch.Generator().manual_seed(11)
+
+    def r(*shape, dt=torch.bfloat16, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to(dt)
+
+    cases = []
+    for dt, tag in ((torch.bfloat16, "bf16"), (torch.float16, "fp16")):
+        a, b = r(16, 256, dt=dt), r(256, 256, dt=dt, scale=0.05)
+        c = a.float() @ b.float()
+        cases.append((f"{tag}_clean", a, b, c, None, 1.0, 1.0, None, 0))
+        cases.append((f"{tag}_clean_nfma16", a, b, c, None, 1.0, 1.0, 16, 0))
+        bad = c.clone()
+        bad[5, 77] = bad[5, 77] * (1 + 2.0 ** -10)
+        cases.append((f"{tag}_rel_2e-10", a, b, bad, None, 1.0, 1.0, None, 0))
+    a, b = r(24, 512), r(512, 300, scale=0.02)
+    c = a.float() @ b.float()
+    cases.append(("bf16_remainder_300", a, b, c, None, 1.0, 1.0, None, 0))
+    bad = c.clone()
+    bad[7, 290] += 0.01
+    cases.append(("bf16_remainder_fault", a, b, bad, None, 1.0, 1.0, None, 0))
+    a, b = r(3, 8, 64), r(3, 64, 200)
+    cases.append(("bf16_bmm", a, b, a.float() @ b.float(), None, 1.0, 1.0, None, 0))
+    b1 = r(64, 200)
+    cases.append(("bf16_shared_b", a, b1, a.float() @ b1.float(), None, 1.0, 1.0, None, 0))
+    a, b = r(12, 128), r(128, 384, scale=0.1)
+    bias = r(384)
+    c = 0.5 * (a.float() @ b.float()) + 2.0 * bias.float()
+    cases.append(("bf16_bias_vec_alpha_beta", a, b, c, bias, 0.5, 2.0, None, 0))
+    bm = r(12, 384)
+    cases.append(("bf16_bias_mat", a, b, a.float() @ b.float() + bm.float(), bm, 1.0, 1.0, None, 0))
+    cases.append(("bf16_epoch3", a, b, a.float() @ b.float(), None, 1.0, 1.0, None, 3))
+    a, b = r(8, 2048), r(2048, 256, scale=0.02)
+    c = a.float() @ b.float()
+    cases.append(("bf16_k2048", a, b, c, None, 1.0, 1.0, 16, 0))
+    for what, val in (("nan", float("nan")), ("inf", float("inf")), ("plus1", None)):
+        bad = c.clone()
+        bad[3, 130] = val if val is not None else bad[3, 130] + 1.0
+        cases.append((f"bf16_{what}", a, b, bad, None, 1.0, 1.0, None, 0))
+    from sdcguard import checksum as cs_
+    s0 = cs_._signs(128, "cpu", 0)
+    j = next(j for j in range(1, 128) if s0[j] == s0[0])
+    bad = c.clone()
+    bad[2, 0], bad[2, j] = 1e18, -1e18
+    cases.append(("bf16_huge_cancel", a, b, bad, None, 1.0, 1.0, None, 0))
+    an = a.clone()
+    an[1] = float("nan")
+    cases.append(("bf16_nan_row_unjudged", an, b, an.float() @ b.float(), None, 1.0, 1.0, None, 0))
+    a0, b0 = r(4, 0), r(0, 256)
+    cases.append(("bf16_k0", a0, b0, torch.zeros(4, 256), None, 1.0, 1.0, None, 0))
+    for scale in (0.0, 1e-24):
+        at = torch.full((3, 8), scale, dtype=torch.bfloat16)
+        bt = torch.ones(8, 260, dtype=torch.bfloat16)
+        cases.append((f"bf16_tiny_{scale:g}", at, bt, at.float() @ bt.float(), None, 1.0, 1.0, None, 0))
+    return cases
+
+
+def make_acc(cs):
+    st_ = _Store()
+    st_.out_full = {}
+    out = st_.out
+    names = []
+    for i, (name, a, b, c, bias, alpha, beta, nfma, epoch) in enumerate(_acc_cases()):
+        with _MaxRecorder() as mr:
+            st = cs.matmul_zscores_acc(a, b, c, bias, alpha=alpha, beta=beta, nfma=nfma, epoch=epoch)
+        res = cs.resolve([st], 6.0)[0]
+        names.append(name)
+        p = f"c{i}_"
+        out[p + "ids"] = np.array([st_.put(a), st_.put(b), st_.put(c.view(torch.int32).view(torch.int16)),
+                                   st_.put(bias) if bias is not None else ""])
+        out[p + "shapes"] = np.array([list(a.shape) + [0] * (3 - a.dim()), list(b.shape) + [0] * (3 - b.dim()),
+                                      list(c.shape) + [0] * (3 - c.dim()),
+                                      (list(bias.shape) if bias is not None else []) + [0] * (3 - (bias.dim() if bias is not None else 0))],
+                                     np.int64)
+        out[p + "meta"] = np.array([alpha, beta, 1.0 if a.dtype == torch.float16 else 0.0, nfma or 0, epoch],
+                                   np.float64)
+        out[p + "zs"] = np.concatenate([z.numpy().astype(np.float32) for z in mr.seen])
+        out[p + "result"] = np.array([res.max_z, -1 if res.batch is None else res.batch,
+                                      -1 if res.row is None else res.row,
+                                      -1 if res.col_block is None else res.col_block,
+                                      float("nan") if res.noise is None else res.noise], np.float64)
+    out["names"] = np.array(names)
+    np.savez_compressed(os.path.join(OUT, "acc.npz"), **out)
     return len(names)
 
 
@@ -468,7 +556,7 @@ def main():
     from sdcguard import serve as sv
     cs.USE_FAST = False
     torch.set_num_threads(4)
-    which = sys.argv[1:] or ["signs", "train", "serve", "quant", "attn"]
+    which = sys.argv[1:] or ["signs", "train", "acc", "serve", "quant", "attn"]
     if "attn" in which:
         from sdcguard import serve_attn as sa
         print("attn.npz:", make_attn(sa), "cases")
@@ -476,6 +564,8 @@ def main():
         make_signs(cs)
     if "train" in which:
         print("train.npz:", make_train(cs), "cases")
+    if "acc" in which:
+        print("acc.npz:", make_acc(cs), "cases")
     if "serve" in which:
         print("serve.npz:", make_serve(sv), "cases")
     if "quant" in which:
