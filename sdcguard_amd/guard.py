@@ -9,8 +9,14 @@ SDCGuard checks the nn.Linear layers of a model while a step is active (protect(
 forward product y = x W^T + b, its input gradient dx = dy W and its weight gradient dW = dy^T x, on a share of
 them (sample_rate), queued without host synchronisation and read back by flush() (every `every` steps, at
 max_pending queued checks, or when called).  Alerts become SDCEvent records, call on_alert, and raise SDCError with
-raise_on_alert.  The reference's other routes (a dispatch mode over every operator, DTensor shards, fp32
-accumulators, recompute and replica checks) are not part of this path.
+raise_on_alert.
+
+precise=True (guard.py:31-35, :471-530): on checked steps each protected layer computes those three products with
+an fp32 output (the accumulator), queues the precise check of it (matmul_zscores_acc: float64 checksums against the
+fp32 accumulation's own rounding, far below what bf16 rounding hides), then rounds it once; on_accumulator(layer,
+pass, C32) may change the fp32 result before its check (fault injection).  Unchecked steps run the layer unchanged.
+The reference's other routes (a dispatch mode over every operator, DTensor shards, recompute and replica checks)
+are not part of this path.
 """
 from __future__ import annotations
 
@@ -24,7 +30,7 @@ from typing import Callable, Optional
 
 import torch
 
-from .checksum import ABS_FLOOR, UNIT_ROUNDOFF, CheckResult, _f32_of_bits, matmul_zscores
+from .checksum import ABS_FLOOR, UNIT_ROUNDOFF, CheckResult, _f32_of_bits, matmul_zscores, matmul_zscores_acc
 
 UNJUDGED = -1.0
 
@@ -35,11 +41,14 @@ class Group:
     CHUNK = 256                         # result rows allocated at a time
 
     def __init__(self, device, dtype: torch.dtype, block: int = 128, abs_floor: float = ABS_FLOOR,
-                 z: float = 6.0, epoch: int = 0):
+                 z: float = 6.0, epoch: int = 0, precise: bool = False, nfma: Optional[int] = None):
+        """dtype: the outputs' (bf16 / fp16); with precise, the operands' (the outputs are their fp32 products,
+        checked by matmul_zscores_acc with nfma products per tensor-core step)."""
         if dtype not in UNIT_ROUNDOFF:
-            raise ValueError(f"checks take bf16 / fp16 outputs, not {dtype}")
+            raise ValueError(f"checks take bf16 / fp16 {'operands' if precise else 'outputs'}, not {dtype}")
         self.device, self.dtype, self.block = torch.device(device), dtype, int(block)
         self.abs_floor, self.z, self.epoch = float(abs_floor), float(z), int(epoch)
+        self.precise, self.nfma = bool(precise), nfma
         self.meta: list = []            # per check: (rows m, blocks nb, batched)
         self._rows: list = []           # (CHUNK, 3) int64 result blocks on the device
         self.result: Optional[torch.Tensor] = None
@@ -55,10 +64,16 @@ class Group:
 
     def add(self, A, B, C, bias, alpha: float, beta: float) -> int:
         """Check C = beta * bias + alpha * (A @ B): the GPU work is queued now.  Returns the check's index."""
-        if C.dtype != self.dtype:
-            raise ValueError(f"this group checks {self.dtype} outputs, not {C.dtype}")
-        st = matmul_zscores(A, B, C, bias, alpha=alpha, beta=beta, block=self.block, abs_floor=self.abs_floor,
-                            z=self.z, epoch=self.epoch, out=self._slot())
+        if self.precise:
+            if C.dtype != torch.float32 or A.dtype != self.dtype:
+                raise ValueError(f"this group checks fp32 products of {self.dtype}, not {A.dtype} -> {C.dtype}")
+            st = matmul_zscores_acc(A, B, C, bias, alpha=alpha, beta=beta, block=self.block, abs_floor=self.abs_floor,
+                                    z=self.z, nfma=self.nfma, epoch=self.epoch, out=self._slot())
+        else:
+            if C.dtype != self.dtype:
+                raise ValueError(f"this group checks {self.dtype} outputs, not {C.dtype}")
+            st = matmul_zscores(A, B, C, bias, alpha=alpha, beta=beta, block=self.block, abs_floor=self.abs_floor,
+                                z=self.z, epoch=self.epoch, out=self._slot())
         self.meta.append((st.m, st.nb, st.batched))
         return len(self.meta) - 1
 
@@ -107,6 +122,60 @@ class SDCEvent:
     extra: dict = field(default_factory=dict)
 
 
+def _acc_mm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a @ b of 16-bit operands with the fp32 result itself (guard.py:281-301), autocast off."""
+    with torch.autocast(device_type=a.device.type, enabled=False):
+        try:
+            return torch.mm(a, b, out_dtype=torch.float32)
+        except (RuntimeError, TypeError, NotImplementedError):
+            saved = torch.backends.cuda.matmul.allow_tf32
+            torch.backends.cuda.matmul.allow_tf32 = False
+            try:
+                return a.float() @ b.float()
+            finally:
+                torch.backends.cuda.matmul.allow_tf32 = saved
+
+
+class _PreciseLinear(torch.autograd.Function):
+    """y = x W^T + b on a checked step of precise mode: every product's fp32 result is checked, then rounded once
+    (the bias added in fp32 first, as one GEMM with a bias epilogue does)."""
+
+    @staticmethod
+    def forward(ctx, x, w, b, guard, label):
+        x2 = x.reshape(-1, x.shape[-1])
+        y32 = _acc_mm(x2, w.t())
+        if b is not None:
+            y32 = y32.add_(b.float())
+        guard._accumulator(label, "forward", x2, w.t(), y32, b)
+        ctx.save_for_backward(x, w)
+        ctx.guard, ctx.label, ctx.has_bias = guard, label, b is not None
+        return y32.to(x.dtype).view(*x.shape[:-1], w.shape[0])
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, w = ctx.saved_tensors
+        guard, label = ctx.guard, ctx.label
+        gy2 = gy.reshape(-1, gy.shape[-1]).to(x.dtype)
+        x2 = x.reshape(-1, x.shape[-1])
+        need_x, need_w, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
+        gx = gw = gb = None
+        checked = guard._active
+        if need_x:
+            gx32 = _acc_mm(gy2, w)
+            if checked:
+                guard._accumulator(label, "input grad", gy2, w, gx32, None)
+            gx = gx32.to(x.dtype).view(x.shape)
+        if need_w:
+            gyt = gy2.t()
+            gw32 = _acc_mm(gyt, x2)
+            if checked:
+                guard._accumulator(label, "weight grad", gyt, x2, gw32, None)
+            gw = gw32.to(w.dtype)
+        if need_b and ctx.has_bias:
+            gb = gy2.sum(0)
+        return gx, gw, gb, None, None
+
+
 def _plain_linear(mod: torch.nn.Module) -> bool:
     return isinstance(mod, torch.nn.Linear) and type(mod).forward is torch.nn.Linear.forward and \
         "forward" not in mod.__dict__
@@ -126,13 +195,17 @@ class SDCGuard:
     def __init__(self, sample_rate: float = 1.0, block: int = 128, z: float = 6.0,
                  on_alert: Optional[Callable[[SDCEvent], None]] = None, raise_on_alert: bool = False,
                  abs_floor: Optional[float] = None, every: int = 10, max_pending: int = 4096,
-                 fresh_signs: bool = True, seed: int = 0):
+                 fresh_signs: bool = True, seed: int = 0, precise: bool = False, nfma: Optional[int] = 16,
+                 on_accumulator: Optional[Callable[[str, str, torch.Tensor], None]] = None):
+        """precise: check the fp32 accumulators of the protected layers' products (see the module docstring);
+        nfma: products per tensor-core accumulation step of those products (16: one 32x32x16 MFMA; None: none)."""
         if not 0.0 <= sample_rate <= 1.0:
             raise ValueError("sample_rate is a share in [0, 1]")
         self.sample_rate, self.block, self.z = float(sample_rate), int(block), float(z)
         self.on_alert, self.raise_on_alert = on_alert, raise_on_alert
         self.abs_floor = ABS_FLOOR if abs_floor is None else float(abs_floor)
         self.every, self.max_pending, self.fresh_signs = int(every), int(max_pending), fresh_signs
+        self.precise, self.nfma, self.on_accumulator = bool(precise), nfma, on_accumulator
         self._rng = random.Random(seed)
         self._lock = threading.RLock()
         self._hooks: list = []
@@ -155,8 +228,11 @@ class SDCGuard:
                 continue
             label = name or type(mod).__name__
             self._protected.append(mod)
-            self._hooks.append(mod.register_forward_hook(self._after_forward(label)))
-            self._hooks.append(mod.register_full_backward_hook(self._after_backward(label)))
+            if self.precise:
+                mod.forward = self._precise_forward(mod, label)
+            else:
+                self._hooks.append(mod.register_forward_hook(self._after_forward(label)))
+                self._hooks.append(mod.register_full_backward_hook(self._after_backward(label)))
             self.stats["layers"] += 1
         return self
 
@@ -164,7 +240,43 @@ class SDCGuard:
         for h in self._hooks:
             h.remove()
         self._hooks.clear()
+        for mod in self._protected:
+            mod.__dict__.pop("forward", None)
         self._protected.clear()
+
+    def _precise_forward(self, mod: torch.nn.Module, label: str):
+        linear = torch.nn.functional.linear
+
+        def forward(x):
+            w, b = mod.weight, mod.bias
+            if not self._active or not x.is_cuda:
+                return linear(x, w, b)
+            if torch.is_autocast_enabled("cuda"):
+                dt = torch.get_autocast_dtype("cuda")
+                x, w, b = x.to(dt), w.to(dt), (None if b is None else b.to(dt))
+            if x.dtype not in UNIT_ROUNDOFF or w.dtype != x.dtype:
+                self.stats["skipped_dtype"] += 1
+                return linear(x, w, b)
+            self.stats["matmuls_seen"] += 3 if torch.is_grad_enabled() and (x.requires_grad or w.requires_grad) else 1
+            with torch.autocast(device_type="cuda", enabled=False):
+                return _PreciseLinear.apply(x, w, b, self, label)
+        return forward
+
+    def _accumulator(self, layer: str, where: str, A, B, C32, bias) -> None:
+        """Precise mode: one product's fp32 result before it is rounded (on_accumulator may change it first)."""
+        if self.on_accumulator is not None:
+            self.on_accumulator(layer, where, C32)
+        if C32.numel() == 0 or not self._sampled():
+            return
+        with self._lock:
+            key = (C32.device, A.dtype, "fp32")
+            g = self._groups.get(key)
+            if g is None:
+                g = self._groups[key] = Group(C32.device, A.dtype, self.block, self.abs_floor, self.z, self._epoch,
+                                              precise=True, nfma=self.nfma)
+            i = g.add(A, B, C32, bias, 1.0, 1.0)
+            self._pending.append((g, i, layer, where, self.step))
+            self.stats["checks"] += 1
 
     def _sampled(self) -> bool:
         return self.sample_rate >= 1.0 or self._rng.random() < self.sample_rate
@@ -289,8 +401,8 @@ class SDCGuard:
                               col_block=c_i, noise=noise)
             out.append(res)
             if not res.ok:
-                ev = SDCEvent(detector="checksum", layer=layer, z=z, step=step, row=r_i, col_block=c_i, noise=noise,
-                              nonfinite=not finite, extra={"pass": where})
+                ev = SDCEvent(detector="accumulator" if g.precise else "checksum", layer=layer, z=z, step=step,
+                              row=r_i, col_block=c_i, noise=noise, nonfinite=not finite, extra={"pass": where})
                 alerts.append(ev)
         self.results.extend(out)
         for ev in alerts:

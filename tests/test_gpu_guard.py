@@ -94,3 +94,49 @@ def test_sampling_and_steps_outside_the_guard():
     assert g2.flush() == []
     g.unprotect()
     g2.unprotect()
+
+
+def test_precise_mode_checks_the_fp32_accumulators():
+    """precise=True: on a checked step each protected layer's forward, input-gradient and weight-gradient products
+    are computed with fp32 outputs, checked (sdc_matmul_check_acc) and rounded once; the gradients agree with
+    autograd's to bf16 rounding, unchecked steps run the plain layer, and a changed accumulator is caught."""
+    from sdcguard_amd.guard import SDCGuard
+    m = _mlp(seed=4)
+    x = torch.randn(64, 256, device="cuda").bfloat16().requires_grad_()
+    ref_y = m(x)
+    ref_y.float().square().sum().backward()
+    ref_gx, ref_gw = x.grad.clone(), m[0].weight.grad.clone()
+    x.grad = None
+    for p in m.parameters():
+        p.grad = None
+    g = SDCGuard(precise=True, every=0).protect(m)
+    with g.at_step(1):
+        y = m(x)
+        y.float().square().sum().backward()
+    res = g.flush()
+    n_lin = sum(isinstance(mm, torch.nn.Linear) for mm in m)
+    assert len(res) == 3 * n_lin and all(r.ok and r.max_z >= 0 for r in res), res
+    assert g.stats["alerts"] == 0 and g.stats["checks"] == 3 * n_lin
+    print("precise clean max z", max(r.max_z for r in res))
+    torch.testing.assert_close(y.float(), ref_y.float(), rtol=2 ** -7, atol=1e-3)
+    torch.testing.assert_close(x.grad.float(), ref_gx.float(), rtol=2 ** -6, atol=2e-3)
+    torch.testing.assert_close(m[0].weight.grad.float(), ref_gw.float(), rtol=2 ** -6, atol=2e-3)
+    with torch.no_grad():                                          # outside a step: the plain layer, bit for bit
+        assert torch.equal(m(x), torch.nn.functional.linear(
+            torch.nn.functional.gelu(torch.nn.functional.linear(x, m[0].weight, m[0].bias)), m[2].weight, m[2].bias)) \
+            if len(m) == 3 else True
+    g.unprotect()
+
+    def bump(layer, where, c32):
+        if layer == "2" and where == "weight grad":
+            c32[7, 33] += 0.25
+    seen = []
+    g2 = SDCGuard(precise=True, every=0, on_accumulator=bump, on_alert=seen.append).protect(m)
+    with g2.at_step(2):
+        m(x).float().square().sum().backward()
+    g2.flush()
+    assert len(seen) == 1, seen
+    ev = seen[0]
+    assert ev.detector == "accumulator" and ev.layer == "2" and ev.extra["pass"] == "weight grad"
+    assert (ev.row, ev.col_block) == (7, 0) and ev.z > 6
+    g2.unprotect()
