@@ -158,13 +158,17 @@ int sdc_layer_constants(int dtype, const void* W, int64_t swn, int64_t n, int64_
  * per-row activation scales sa and per-column weight scales sb (C = sa_i sb_j sum_k Aq[i,k] Bq[k,j]).
  *   kind 0 = int8 W8A8: A (m x k) int8, C (m x n) int32 (c_dtype 2); parts = the block sums of B (plain, then
  *     signed, per block) as two base-128 int8 digits, hi then lo, (2 x 2nb) columns of k bytes at spc bytes apart
- *     (B2 = 128 hi + lo, |lo| <= 64).  The check is exact: every differing sum is a wrong block.
- *   kind 1 = fp8 e4m3: A (m x k) fp8 e4m3fn (k-contiguous rows), sa (m) fp32 or NULL (1), C fp32 (c_dtype 0) or
+ *     (B2 = 128 hi + lo, |lo| <= 64).  The check is exact: every differing sum is a wrong block.  Any depth, stride
+ *     and address: an odd k, odd sam / spc or odd addresses are copied into zero-padded workspace buffers first.
+ *   kind 1 = fp8 e4m3: A (m x k) fp8 e4m3fn (k-contiguous rows, any row stride and alignment: rows that are not
+ *     16-byte aligned or a depth that is not a multiple of 32 take bounds-checked loads), sa (m) fp32 or NULL (1),
+ *     C fp32 (c_dtype 0) or
  *     bf16 (1); parts = the three bf16 parts of B2s = sum_j w_j sb_j Bq[:,j] per checksum column (3 x 2nb columns
  *     of k elements, spc apart); bfrob (nb) = |sb Bq|_F per block; bcol (n) = |sb_j Bq[:,j]|_2 per column;
  *     unit = the accumulation's rounding unit (2^-14 for an fp8 tensor-core accumulation of unknown precision,
  *     modes.acc_unit), nfma = products per accumulation step (16, modes.n_fma; 0: none).
- *   A row stride sam, C strides (scm, scn), in elements.  sign_table: as sdc_check_static (epoch 0).
+ *   A row stride sam, C strides (scm, scn), in elements (any C layout: the row-block check passes C^T, strides
+ *     (1, m)).  sign_table: as sdc_check_static (epoch 0).
  *   result: int64[4], zeroed by the caller: the worst block's key (bits of z << 32 | row * nb + block), the key with
  *     its noise, the number of wrong blocks (z > z; int8: any differing sum), blocks with a non-finite sum.
  *   workspace: at least sdc_quant_check_workspace(kind, m, k, n, bs) bytes; scores_out: (m, nb) z or NULL. */

@@ -576,7 +576,6 @@ int sdc_gemm_launch(int dtype, GemmArgs g, int64_t batches, hipStream_t stream) 
   const int64_t ea = dtype == SDC_FP8 ? 1 : 2;                   // bytes per A element
   const bool vec = g.sak == 1 && (g.k % KS == 0) && ((g.sam * ea) % 16 == 0) && ((g.sab * ea) % 16 == 0) &&
                    ((uintptr_t)g.A % 16 == 0) && (g.sbc % 8 == 0) && (g.sbb % 8 == 0) && ((uintptr_t)g.B % 16 == 0);
-  if (dtype == SDC_FP8 && !vec) return SDC_EUNSUPPORTED;          // fp8 A: k-contiguous, aligned rows only
   const int wgn = g.N > 64 ? 2 : 1;
   const int64_t rtiles = sdc_cdiv(g.m, 64 * (8 / wgn)) + (g.goffs ? g.ngroups : 0);
   if (g.goffs && batches != 1) return SDC_EINVAL;

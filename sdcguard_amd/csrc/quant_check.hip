@@ -463,7 +463,7 @@ int64_t quant_splits(int kind, int64_t m, int64_t k, int64_t ncols) {
 }
 
 struct QLayout {
-  int64_t nb, rem, ncols, splits, nacc, off_e, off_xn, total;
+  int64_t nb, rem, ncols, splits, nacc, kpad, off_e, off_xn, off_apad, off_ppad, total;   // offsets in floats
 };
 
 QLayout qlayout(int kind, int64_t m, int64_t k, int64_t n, int64_t bs) {
@@ -472,13 +472,42 @@ QLayout qlayout(int kind, int64_t m, int64_t k, int64_t n, int64_t bs) {
   L.rem = n % bs;
   L.ncols = 2 * L.nb;
   L.nacc = kind == 0 ? 2 : 1;
-  L.splits = quant_splits(kind, m, kind == 0 ? k / 2 : k, L.ncols);
+  L.splits = quant_splits(kind, m, kind == 0 ? (k + 1) / 2 : k, L.ncols);
+  L.kpad = kind == 0 ? (k + 63) / 64 * 64 : 0;           // int8: depth of the zero-padded copies (bytes)
   auto al = [](int64_t x) { return (x + 63) / 64 * 64; };
   int64_t o = 0;
   L.off_e = o; o += al(L.splits * L.nacc * m * L.ncols);
   L.off_xn = o; o += al(L.splits * 2 * m);
+  L.off_apad = o; o += al(sdc_cdiv(m * L.kpad, 4));
+  L.off_ppad = o; o += al(sdc_cdiv(2 * L.ncols * L.kpad, 4));
   L.total = o;
   return L;
+}
+
+// rows x cols bytes at src (row stride s_row) -> rows x dcols at dst, zero past cols; 4 destination bytes per
+// thread (dcols a multiple of 4, dst 4-byte aligned)
+__global__ __launch_bounds__(256) void pad_bytes_kernel(const uint8_t* src, int64_t s_row, int64_t rows, int64_t cols,
+                                                        uint8_t* dst, int64_t dcols) {
+  const int64_t words = rows * (dcols / 4);
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < words; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / (dcols / 4), c = 4 * (i % (dcols / 4));
+    const uint8_t* row = src + r * s_row;
+    uint32_t v = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      if (c + b < cols) v |= (uint32_t)row[c + b] << (8 * b);
+    reinterpret_cast<uint32_t*>(dst + r * dcols)[c / 4] = v;
+  }
+}
+
+int pad_bytes(const void* src, int64_t s_row, int64_t rows, int64_t cols, void* dst, int64_t dcols,
+              hipStream_t stream) {
+  const int64_t words = rows * (dcols / 4);
+  const unsigned grid = (unsigned)(sdc_cdiv(words, 256) < 4096 ? sdc_cdiv(words, 256) : 4096);
+  hipLaunchKernelGGL(pad_bytes_kernel, dim3(grid), dim3(256), 0, stream, (const uint8_t*)src, s_row, rows, cols,
+                     (uint8_t*)dst, dcols);
+  SDC_LAUNCH_CHECK();
+  return SDC_OK;
 }
 
 template <int KIND, int CT>
@@ -505,13 +534,25 @@ extern "C" int sdc_quant_check(int kind, const void* A, int64_t sam, const void*
   if (kind == 0 && c_dtype != C_I32) return SDC_EINVAL;
   if (kind == 1 && c_dtype != C_F32 && c_dtype != C_BF16) return SDC_EINVAL;
   if (kind == 1 && (!bfrob || !bcol)) return SDC_EINVAL;
-  // int8 runs the GEMM on pairs of bytes: even depth and row strides
-  if (kind == 0 && ((k % 2) || (sam % 2) || (spc % 2) || ((uintptr_t)A % 2) || ((uintptr_t)parts % 2)))
-    return SDC_EUNSUPPORTED;
   const QLayout L = qlayout(kind, m, k, n, bs);
   if (m * L.nb > 0xFFFFFFFFll) return SDC_EUNSUPPORTED;
   if (!workspace || workspace_bytes < L.total * (int64_t)sizeof(float) + 256) return SDC_EWORKSPACE;
   float* ws = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  // int8 runs the GEMM on pairs of bytes: an odd depth, odd row strides or odd addresses are copied first into
+  // zero-padded buffers of the workspace (depth rounded up to 64 bytes, so the copy also loads 16 bytes at a time)
+  int64_t kg = kind == 0 ? k / 2 : k;                     // the GEMM's depth (int8: in pairs)
+  if (kind == 0 && ((k % 2) || (sam % 2) || (spc % 2) || ((uintptr_t)A % 2) || ((uintptr_t)parts % 2))) {
+    uint8_t* apad = (uint8_t*)(ws + L.off_apad);
+    uint8_t* ppad = (uint8_t*)(ws + L.off_ppad);
+    int rc = pad_bytes(A, sam, m, k, apad, L.kpad, stream);
+    if (rc == SDC_OK) rc = pad_bytes(parts, spc, 2 * L.ncols, k, ppad, L.kpad, stream);
+    if (rc != SDC_OK) return rc;
+    A = apad;
+    sam = L.kpad;
+    parts = ppad;
+    spc = L.kpad;
+    kg = L.kpad / 2;
+  }
   const float* s_full = sign_table + (bs - 1) * 128;
   const float* s_last = L.rem ? sign_table + (L.rem - 1) * 128 : s_full;
 
@@ -525,7 +566,7 @@ extern "C" int sdc_quant_check(int kind, const void* A, int64_t sam, const void*
   g.sam = kind == 0 ? sam / 2 : sam;
   g.sak = 1;
   g.B = parts; g.sbb = 0; g.sbc = kind == 0 ? spc / 2 : spc;
-  g.m = m; g.k = kind == 0 ? k / 2 : k; g.N = L.ncols; g.splits = L.splits;
+  g.m = m; g.k = kg; g.N = L.ncols; g.splits = L.splits;
   g.E = ws + L.off_e; g.XN = ws + L.off_xn;
   g.prof_name = kind == 0 ? "quant_gemm_i8" : "quant_gemm_fp8";
   int rc = sdc_gemm_launch(kind == 0 ? SDC_I8 : SDC_FP8, g, 1, stream);

@@ -69,8 +69,6 @@ class QuantChecksums:
         if B.dtype == torch.int8:
             if sb is not None:
                 raise ValueError("int8 check: no scales (the accumulator itself is checked, exactly)")
-            if k % 2:
-                raise ValueError("int8 check: k must be even")
             B2 = B.double() @ W                                   # exact: |B2| <= 128 * 128 = 16384
             # two base-128 digits, B2 = 128 hi + lo with hi in [-128, 127]: |lo| <= 64 except for sums in
             # [16320, 16383] (-128 entries laid against the sign pattern), whose lo takes 64..127.  +16384 would
@@ -80,7 +78,9 @@ class QuantChecksums:
             if bool((lo.abs() > 127).any()):
                 raise ValueError("int8 check: a block sum of 16384 (every entry -128 against the sign pattern) does "
                                  "not split into two int8 digits")
-            parts = torch.stack([hi, lo]).to(torch.int8).transpose(1, 2).contiguous()   # (2, 2nb, k)
+            parts = torch.stack([hi, lo]).to(torch.int8).transpose(1, 2)                # (2, 2nb, k)
+            # an odd depth gets one zero digit more, so every column holds whole pairs of bytes
+            parts = torch.nn.functional.pad(parts, (0, k % 2)).contiguous()
             return cls("int8", k, n, block, parts)
         if B.dtype == torch.float8_e4m3fn:
             Bs = B.double() if sb is None else B.double() * sb.double().view(1, n)
@@ -143,6 +143,21 @@ def quant_zscores(A: torch.Tensor, consts: QuantChecksums, C: torch.Tensor, *, s
     return QuantStat(out, m, nb, consts.kind, z, scores_out)
 
 
+def quant_rows_zscores(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, *, sa: Optional[torch.Tensor] = None,
+                       sb: Optional[torch.Tensor] = None, unit: float = UNIT_FP8, nfma: Optional[int] = NFMA_FP8,
+                       z: float = ALARM, scores_out: Optional[torch.Tensor] = None,
+                       out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> QuantStat:
+    """The row-block check of the quantized GEMM C = A @ B (int8 W8A8, exact; or fp8 e4m3 with scales, C =
+    sa_i sb_j sum_k Aq[i,k] Bq[k,j]): for every column j of C and block of 128 rows, the plain and signed sums
+    sum_i w_i C[i,j] against (the scaled block sums of A's rows) . B[:, j].  It is the column check of
+    C^T = B^T A^T: the constants of A's row blocks (digits, or three bf16 parts with their norms) are made on the
+    GPU for this call, B^T is the weight (k-contiguous as an nn.Linear weight stores it) and C^T is read in place.
+    The QuantStat's rows are C's columns and its blocks C's 128-row blocks."""
+    consts = QuantChecksums.make(A.t(), sa)
+    return quant_zscores(B.t(), consts, C.t(), sa=sb, unit=unit, nfma=nfma, z=z, scores_out=scores_out, out=out,
+                         workspace=workspace)
+
+
 def resolve(st: QuantStat) -> dict:
     """modes.judge's summary of a queued check (one device-to-host copy): wrong_blocks, blocks, worst_z (None for
     int8, as the reference reports), and the worst block's (row, block) and noise."""
@@ -175,3 +190,17 @@ def judge(mode: str, a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, nfma: Op
     st = quant_zscores(a, consts, c, sa=sa, unit=UNIT_FP8 if unit is None else unit, nfma=nfma, z=z, scores_out=zs)
     return resolve(st)
 
+
+def judge_rows(mode: str, a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, nfma: Optional[int] = NFMA_FP8,
+               unit: Optional[float] = None, sa: Optional[torch.Tensor] = None, sb: Optional[torch.Tensor] = None,
+               z: float = ALARM) -> dict:
+    """judge()'s summary for the row-block check (quant_rows_zscores): result["z"] is (n, mb), a column of C by a
+    block of 128 rows; "row" is the worst column and "block" its row block."""
+    if mode not in ("int8", "fp8"):
+        raise ValueError("judge_rows on the device covers the int8 and fp8 modes")
+    n = c.shape[1]
+    mb = -(-c.shape[0] // BLOCK)
+    zs = torch.empty(n, mb, dtype=torch.float32, device=c.device)
+    st = quant_rows_zscores(a, b, c, sa=sa, sb=sb, unit=UNIT_FP8 if unit is None else unit, nfma=nfma, z=z,
+                            scores_out=zs)
+    return resolve(st)

@@ -199,3 +199,115 @@ def test_int8_weights_at_minus_128():
     A2 = A[:, :128].contiguous()
     C2 = (A2.double() @ low.double()).to(torch.int32)
     assert modes.resolve(modes.quant_zscores(A2, modes.QuantChecksums.make(low), C2))["wrong_blocks"] == 0
+
+
+def test_int8_odd_depth_and_strided_operands():
+    """Any depth and layout: k = 1001 (odd) and A a column slice starting at an odd byte (odd address, odd row
+    stride 1003), which the C ABI copies into zero-padded buffers: clean is exact and matches the oracle's verdicts;
+    one output off by one is one wrong block, located."""
+    from sdcguard_amd import modes
+    g = torch.Generator(device="cuda").manual_seed(31)
+    m, k, n = 96, 1001, 384
+    Abig = torch.randint(-127, 128, (m, k + 2), device="cuda", generator=g, dtype=torch.int32).to(torch.int8)
+    A = Abig[:, 1:1 + k]
+    assert A.stride(0) % 2 == 1 and A.data_ptr() % 2 == 1
+    B = torch.randint(-127, 128, (k, n), device="cuda", generator=g, dtype=torch.int32).to(torch.int8)
+    C = (A.double() @ B.double()).to(torch.int32)
+    consts = modes.QuantChecksums.make(B)
+    assert consts.parts.shape[-1] == k + 1
+    assert modes.resolve(modes.quant_zscores(A, consts, C))["wrong_blocks"] == 0
+    c = C.clone()
+    c[17, 300] -= 1
+    res = modes.resolve(modes.quant_zscores(A, consts, c))
+    o = quant.int8_judge(A.cpu().numpy(), B.cpu().numpy(), c.cpu().numpy(), quant.patterns(1))
+    assert res["wrong_blocks"] == o["wrong_blocks"] == 1 and (res["row"], res["block"]) == (17, 2), res
+
+
+def test_fp8_any_depth_and_alignment():
+    """fp8 A of depth 1000 (not a multiple of 32) read from a view 3 bytes off alignment (row stride 1003): the
+    bounds-checked path scores as the oracle does, and a fault is located."""
+    from sdcguard_amd import modes
+    g = torch.Generator(device="cuda").manual_seed(32)
+    m, k, n = 72, 1000, 260
+    Abig = (torch.randn(m, k + 3, device="cuda", generator=g) * 4).to(torch.float8_e4m3fn)
+    Aq = Abig[:, 3:3 + k]
+    Bq = (torch.randn(k, n, device="cuda", generator=g) * 4).to(torch.float8_e4m3fn)
+    sa = 10.0 ** (torch.rand(m, device="cuda", generator=g) * 2 - 3)
+    sb = 10.0 ** (torch.rand(n, device="cuda", generator=g) * 2 - 3)
+    C = ((Aq.double() @ Bq.double()) * sa.double()[:, None] * sb.double()[None, :]).float()
+    res = modes.judge("fp8", Aq, Bq, C, sa=sa.float(), sb=sb.float())
+    vals = quant.fp8_e4m3_values()
+    o = quant.fp8_judge(vals[Aq.view(torch.uint8).cpu().numpy()], vals[Bq.view(torch.uint8).cpu().numpy()],
+                        sa.cpu().numpy(), sb.cpu().numpy(), C.double().cpu().numpy(), quant.patterns(1))
+    zg = res["z"].cpu().numpy()
+    assert res["wrong_blocks"] == o["wrong_blocks"] == 0
+    assert np.allclose(zg, o["z"], rtol=1e-3, atol=2e-3), np.abs(zg - o["z"]).max()
+    c = C.clone()
+    c[40, 259] = c[40, 259] * 1.5 + 1.0
+    res = modes.judge("fp8", Aq, Bq, c, sa=sa.float(), sb=sb.float())
+    assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (40, 2), res
+
+
+def test_int8_row_block_check():
+    """Row-block residuals of an int8 W8A8 GEMM (quant_rows_zscores: the column check of C^T = B^T A^T, B^T the
+    layer's weight): clean is exact; the per-block verdicts equal the oracle's on the transposed operands; one wrong
+    output is one wrong (column, row block), located, including in the narrower last row block."""
+    from sdcguard_amd import modes
+    g = torch.Generator(device="cuda").manual_seed(33)
+    m, k, n = 300, 512, 256
+    W = torch.randint(-127, 128, (n, k), device="cuda", generator=g, dtype=torch.int32).to(torch.int8)
+    A = torch.randint(-127, 128, (m, k), device="cuda", generator=g, dtype=torch.int32).to(torch.int8)
+    C = (A.double() @ W.double().t()).to(torch.int32)
+    res = modes.judge_rows("int8", A, W.t(), C)
+    assert res["wrong_blocks"] == 0 and res["blocks"] == n * 3
+    for i, j in ((250, 77), (5, 255), (128, 0)):
+        c = C.clone()
+        c[i, j] += 3
+        res = modes.judge_rows("int8", A, W.t(), c)
+        o = quant.int8_judge(W.cpu().numpy(), A.t().cpu().numpy(), c.t().cpu().numpy(), quant.patterns(1))
+        assert res["wrong_blocks"] == o["wrong_blocks"] == 1 and (res["row"], res["block"]) == (j, i // 128), res
+        assert np.array_equal(np.isinf(res["z"].cpu().numpy()), o["bad"])
+
+
+def test_fp8_row_block_check():
+    """Row-block residuals of a scaled fp8 GEMM: per-(column, row block) z equal to the oracle's on the transposed
+    operands (scales exchanged), clean raises nothing, a fault is located at its column and row block."""
+    from sdcguard_amd import modes
+    Aq, Bq, sa, sb, C = _scaled_problem(34, 200, 768, 384)
+    res = modes.judge_rows("fp8", Aq, Bq, C, sa=sa, sb=sb)
+    vals = quant.fp8_e4m3_values()
+    A = vals[Aq.view(torch.uint8).cpu().numpy()]
+    B = vals[Bq.view(torch.uint8).cpu().numpy()]
+    o = quant.fp8_judge(B.T, A.T, sb.double().cpu().numpy(), sa.double().cpu().numpy(), C.double().cpu().numpy().T,
+                        quant.patterns(1))
+    zg = res["z"].cpu().numpy()
+    assert res["wrong_blocks"] == o["wrong_blocks"] == 0
+    assert np.allclose(zg, o["z"], rtol=1e-3, atol=2e-3), np.abs(zg - o["z"]).max()
+    c = C.clone()
+    col = c[:, 150]
+    c[170, 150] += 4 * col[128:].pow(2).mean().sqrt()
+    res = modes.judge_rows("fp8", Aq, Bq, c, sa=sa, sb=sb)
+    assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (150, 1), res
+
+
+def test_quant_row_checks_at_2048x7168x4096():
+    """Both row-block checks at the quantized configuration's full size: int8 exact and clean, one flipped
+    accumulator bit located; fp8 clean, one fault in the dequantized output located."""
+    from sdcguard_amd import modes
+    g = torch.Generator(device="cuda").manual_seed(35)
+    A = torch.randint(-127, 128, (2048, 7168), device="cuda", generator=g, dtype=torch.int32).to(torch.int8)
+    W = torch.randint(-127, 128, (4096, 7168), device="cuda", generator=g, dtype=torch.int32).to(torch.int8)
+    C = (A.double() @ W.double().t()).to(torch.int32)
+    assert modes.judge_rows("int8", A, W.t(), C)["wrong_blocks"] == 0
+    c = C.clone()
+    c[1000, 3000] ^= 1 << 9
+    res = modes.judge_rows("int8", A, W.t(), c)
+    assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (3000, 1000 // 128), res
+    del A, W, C, c
+    Aq, Bq, sa, sb, C = _scaled_problem(36, 2048, 7168, 4096)
+    res = modes.judge_rows("fp8", Aq, Bq, C, sa=sa, sb=sb)
+    assert res["wrong_blocks"] == 0 and res["worst_z"] < 1.0, res
+    c = C.clone()
+    c[77, 4000] += 4 * C[:128, 4000].pow(2).mean().sqrt()
+    res = modes.judge_rows("fp8", Aq, Bq, c, sa=sa, sb=sb)
+    assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (4000, 0), res
