@@ -193,10 +193,12 @@ int sdc_fingerprint2(const void* bits, int64_t n, int kind, int64_t* out, hipStr
 /* ---- paged-KV block fingerprints (no counterpart function in the reference; each block's value is
  * recompute.fingerprint of the block's bytes as a tensor of its own, recompute.py:72-116, words numbered from 0) --
  * out[i][0..2] (int64, zeroed by the caller) += the fingerprint of block ids[i] of a cache of nblocks blocks of
- * `words` 16-bit words each, block b at cache + b * block_bytes; ids == NULL: entry i is block i (n = nblocks).
- * An entry whose id is negative or >= nblocks is left unchanged (a block-table walk passes the table's rows). */
-int sdc_kv_fingerprint(const void* cache, int64_t nblocks, int64_t block_bytes, int64_t words, const int64_t* ids,
-                       int64_t n, int64_t* out, hipStream_t stream);
+ * `words` words each, block b at cache + b * block_bytes; word_bytes 2: int16 words (16-bit and wider element
+ * dtypes), 1: int8 words (1-byte element dtypes such as fp8 caches, recompute.py:86-87); ids == NULL: entry i is
+ * block i (n = nblocks).  An entry whose id is negative or >= nblocks is left unchanged (a block-table walk passes
+ * the table's rows). */
+int sdc_kv_fingerprint(const void* cache, int64_t nblocks, int64_t block_bytes, int64_t words, int word_bytes,
+                       const int64_t* ids, int64_t n, int64_t* out, hipStream_t stream);
 
 /* ---- sampled attention recompute from a paged KV cache, and the sampled tokens' KV-write check ------------
  * Replaces serve_attn.attn_check_triton (serve_attn.py:574-602) and its two kernels _attn_part / _attn_judge

@@ -50,7 +50,7 @@ SIGNATURES = {
                               P, P, I64, P, P]),
     "sdc_fingerprint3": (I32, [P, I64, I32, I64, P, P]),
     "sdc_fingerprint2": (I32, [P, I64, I32, P, P]),
-    "sdc_kv_fingerprint": (I32, [P, I64, I64, I64, P, I64, P, P]),
+    "sdc_kv_fingerprint": (I32, [P, I64, I64, I64, I32, P, I64, P, P]),
     "sdc_attn_splits": (I64, [I64, I64]),
     "sdc_attn_check_workspace": (I64, [I64, I64, I64]),
     "sdc_attn_check": (I32, [I32, P, I64, I64, P, I64, I64, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, I64,

@@ -159,6 +159,9 @@ unsigned grid_for(int64_t work_items) {
 // sums may wrap (only hi's value mod 2^32 counts).  Each wave adds its lanes' sums (DPP steps, then two shuffles)
 // and three of its lanes add them into the block's three outputs with 64-bit atomics (wrapping, so the result does
 // not depend on the order).  Four blocks are in flight per wave.
+// A cache of 1-byte elements has int8 words (recompute.py:86-87): a lane's 16 words are one 16-byte load; each
+// byte is taken as u = v + 128 (its sign bit flipped), zero-extended into a 16-bit lane of the same dot products,
+// and the lane subtracts 128 times the sum of its positions' weights (made once, mod 2^64) from its sums.
 constexpr int KV_WPT = 16;                       // words per lane
 constexpr int KV_SLICE = 64 * KV_WPT;            // positions per wave slice
 constexpr int KV_UNROLL = 4;                     // blocks in flight per wave
@@ -222,6 +225,7 @@ __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
 
 constexpr int KV_WAVES = 4;                      // waves per workgroup: KV_WAVES slices of one block range
 
+template <int WB>
 __global__ __launch_bounds__(64 * KV_WAVES) void kv_fp3_kernel(KvArgs a) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t p0 = ((int64_t)blockIdx.x * KV_WAVES + w) * KV_SLICE + (int64_t)lane * KV_WPT;
@@ -243,6 +247,15 @@ __global__ __launch_bounds__(64 * KV_WAVES) void kv_fp3_kernel(KvArgs a) {
   }
   const int nw = p0 >= a.words ? 0 : (a.words - p0 < KV_WPT ? (int)(a.words - p0) : KV_WPT);
   const bool full = a.vec && nw == KV_WPT;
+  // 1-byte words: 128 x the sums of this lane's weights over its positions (the offset of u = v + 128)
+  uint64_t corr[2] = {0ull, 0ull};
+  if constexpr (WB == 1) {
+    for (int j = 0; j < nw; ++j) {
+      const uint64_t z = fp3_z((uint64_t)(p0 + j));
+      corr[0] += (z | 1ull) << 7;
+      corr[1] += ((z ^ (z >> 32)) | 1ull) << 7;
+    }
+  }
   for (int64_t i0 = blockIdx.y; i0 < a.n; i0 += (int64_t)gridDim.y * KV_UNROLL) {
     uint32_t b[KV_UNROLL][KV_WPT / 2];
     bool live[KV_UNROLL];
@@ -251,21 +264,40 @@ __global__ __launch_bounds__(64 * KV_WAVES) void kv_fp3_kernel(KvArgs a) {
       const int64_t i = i0 + (int64_t)u * gridDim.y;
       const int64_t blk = i < a.n ? (a.ids ? a.ids[i] : i) : -1;
       live[u] = blk >= 0 && blk < a.nblocks;
-      const uint8_t* src = a.cache + (live[u] ? blk : 0) * a.block_bytes + (nw ? p0 : 0) * 2;
-      if (full) {
-        const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-        const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16));
+      const uint8_t* src = a.cache + (live[u] ? blk : 0) * a.block_bytes + (nw ? p0 : 0) * WB;
+      if constexpr (WB == 2) {
+        if (full) {
+          const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+          const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16));
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          b[u][q] = v0[q];
-          b[u][4 + q] = v1[q];
+          for (int q = 0; q < 4; ++q) {
+            b[u][q] = v0[q];
+            b[u][4 + q] = v1[q];
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < KV_WPT / 2; ++j) {
+            const uint32_t lo = 2 * j < nw ? (uint32_t)(src[4 * j] | (src[4 * j + 1] << 8)) : 0u;
+            const uint32_t hi = 2 * j + 1 < nw ? (uint32_t)(src[4 * j + 2] | (src[4 * j + 3] << 8)) : 0u;
+            b[u][j] = lo | (hi << 16);
+          }
         }
       } else {
+        if (full) {
+          const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
 #pragma unroll
-        for (int j = 0; j < KV_WPT / 2; ++j) {
-          const uint32_t lo = 2 * j < nw ? (uint32_t)(src[4 * j] | (src[4 * j + 1] << 8)) : 0u;
-          const uint32_t hi = 2 * j + 1 < nw ? (uint32_t)(src[4 * j + 2] | (src[4 * j + 3] << 8)) : 0u;
-          b[u][j] = lo | (hi << 16);
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t x = v0[q] ^ 0x80808080u;                 // u = v + 128 in every byte
+            b[u][2 * q] = __builtin_amdgcn_perm(0u, x, 0x0C010C00u);       // bytes 0, 1 -> two 16-bit lanes
+            b[u][2 * q + 1] = __builtin_amdgcn_perm(0u, x, 0x0C030C02u);   // bytes 2, 3
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < KV_WPT / 2; ++j) {
+            const uint32_t lo = 2 * j < nw ? (uint32_t)(src[2 * j] ^ 0x80u) : 0u;
+            const uint32_t hi = 2 * j + 1 < nw ? (uint32_t)(src[2 * j + 1] ^ 0x80u) : 0u;
+            b[u][j] = lo | (hi << 16);
+          }
         }
       }
     }
@@ -284,12 +316,13 @@ __global__ __launch_bounds__(64 * KV_WAVES) void kv_fp3_kernel(KvArgs a) {
         }
       }
       uint64_t v[3];
+      if constexpr (WB == 1) s0 -= 128 * nw;
       v[0] = (uint64_t)(int64_t)wave_sum_i32(s0);
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const int64_t low = (int64_t)A[c][0] + ((int64_t)A[c][1] << 12) + ((int64_t)A[c][2] << 24);
         const uint32_t high = (uint32_t)H[c][0] + ((uint32_t)H[c][1] << 16);
-        v[1 + c] = wave_sum_u64((uint64_t)low + ((uint64_t)high << 32));
+        v[1 + c] = wave_sum_u64((uint64_t)low + ((uint64_t)high << 32) - corr[c]);
       }
       const int64_t i = i0 + (int64_t)u * gridDim.y;
       if (lane < 3 && live[u])
@@ -341,13 +374,14 @@ extern "C" int sdc_fingerprint2(const void* bits, int64_t n, int kind, int64_t* 
   return SDC_OK;
 }
 
-// out[i][0..2] (int64, zeroed by the caller) += fp3 of block ids[i] (or block i) of a paged cache of int16 words:
-// block b holds `words` words at cache + b * block_bytes, its positions numbered from 0.  Entries whose id is
-// negative or >= nblocks are left as they are.
+// out[i][0..2] (int64, zeroed by the caller) += fp3 of block ids[i] (or block i) of a paged cache of int16 words
+// (word_bytes 2) or int8 words (1): block b holds `words` words at cache + b * block_bytes, its positions numbered
+// from 0.  Entries whose id is negative or >= nblocks are left as they are.
 extern "C" int sdc_kv_fingerprint(const void* cache, int64_t nblocks, int64_t block_bytes, int64_t words,
-                                  const int64_t* ids, int64_t n, int64_t* out, hipStream_t stream) {
+                                  int word_bytes, const int64_t* ids, int64_t n, int64_t* out, hipStream_t stream) {
   SDC_CLEAR_ERRORS();
-  if (!cache || !out || nblocks < 1 || words < 1 || n < 0 || block_bytes < words * 2) return SDC_EINVAL;
+  if (word_bytes != 1 && word_bytes != 2) return SDC_EINVAL;
+  if (!cache || !out || nblocks < 1 || words < 1 || n < 0 || block_bytes < words * word_bytes) return SDC_EINVAL;
   if (n == 0) return SDC_OK;
   KvArgs a{(const uint8_t*)cache, block_bytes, words, nblocks, ids, n, out,
            (block_bytes % 16 == 0) && ((uintptr_t)cache % 16 == 0)};
@@ -356,7 +390,10 @@ extern "C" int sdc_kv_fingerprint(const void* cache, int64_t nblocks, int64_t bl
   if (gy > sdc_cdiv(n, KV_UNROLL)) gy = sdc_cdiv(n, KV_UNROLL);
   if (gy > 65535) gy = 65535;
   SdcProf prof("kv_fingerprint", stream);
-  hipLaunchKernelGGL(kv_fp3_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(64 * KV_WAVES), 0, stream, a);
+  if (word_bytes == 2)
+    hipLaunchKernelGGL(kv_fp3_kernel<2>, dim3((unsigned)gx, (unsigned)gy), dim3(64 * KV_WAVES), 0, stream, a);
+  else
+    hipLaunchKernelGGL(kv_fp3_kernel<1>, dim3((unsigned)gx, (unsigned)gy), dim3(64 * KV_WAVES), 0, stream, a);
   SDC_LAUNCH_CHECK();
   return SDC_OK;
 }

@@ -2,7 +2,8 @@
 references still hold what was recorded for them.
 
 A block's fingerprint is recompute.fingerprint of the block as a tensor of its own (recompute.py:72-116: the sums
-(b, b w1, b w2) mod 2^64 over its 16-bit words b, positions numbered from 0 within the block), so it is bit-exact
+(b, b w1, b w2) mod 2^64 over its 16-bit words b -- 8-bit ones for a cache of 1-byte elements such as fp8,
+recompute.py:86-87 -- positions numbered from 0 within the block), so it is bit-exact
 against the reference's fingerprint of the same bytes.  It runs in libsdcguard_hip.so (sdc_kv_fingerprint), either
 over every block of a cache or walking a block table (one entry per logical block; negative entries are unused).
 
@@ -21,8 +22,6 @@ import torch
 def _blocks_view(cache: torch.Tensor) -> torch.Tensor:
     if cache.dim() < 2:
         raise ValueError("a paged cache has its blocks on dimension 0")
-    if cache.element_size() != 2:
-        raise ValueError("16-bit KV caches (bf16 / fp16) only")
     if not cache[0].is_contiguous():
         raise ValueError("each block must be contiguous")
     return cache
@@ -36,7 +35,9 @@ def block_fingerprints(cache: torch.Tensor, ids: Optional[torch.Tensor] = None,
     cache = _blocks_view(cache)
     _lib.require_gpu(cache, ids)
     nblocks = cache.shape[0]
-    words = cache[0].numel()
+    es = cache.element_size()
+    wb = 2 if es % 2 == 0 else 1                          # recompute.py:86-87: int16 words, int8 for 1-byte dtypes
+    words = cache[0].numel() * es // wb
     if ids is not None:
         ids = ids.reshape(-1).to(torch.int64).contiguous()
     n = nblocks if ids is None else ids.numel()
@@ -44,7 +45,7 @@ def block_fingerprints(cache: torch.Tensor, ids: Optional[torch.Tensor] = None,
         out = torch.zeros(n, 3, dtype=torch.int64, device=cache.device)
     elif out.shape != (n, 3) or out.dtype != torch.int64:
         raise ValueError("out must be (n, 3) int64 zeros")
-    rc = _lib.lib().sdc_kv_fingerprint(cache.data_ptr(), nblocks, cache.stride(0) * 2, words,
+    rc = _lib.lib().sdc_kv_fingerprint(cache.data_ptr(), nblocks, cache.stride(0) * es, words, wb,
                                         None if ids is None else ids.data_ptr(), n, out.data_ptr(),
                                         _lib.stream_of(cache))
     _lib.check(rc, "sdc_kv_fingerprint")

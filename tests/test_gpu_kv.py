@@ -71,6 +71,38 @@ def test_ledger_catches_stale_blocks_and_bit_flips():
     assert sorted(r["entries"]) == want and r["mismatched"] == len(want)
 
 
+def test_fp8_cache_block_fingerprints_bit_exact():
+    """A cache of 1-byte elements (fp8 e4m3 keys and values) has int8 words (recompute.py:86-87): every block is
+    bit-exact against the oracle and against this library's fingerprint of the block on its own, also with blocks
+    whose byte count is not a multiple of a lane's 16 bytes and blocks 1 byte off alignment; a flipped bit changes
+    its block's fingerprint only; the ledger over an fp8 cache flags a stale entry."""
+    from sdcguard_amd.kv import KVLedger, block_fingerprints
+    from sdcguard_amd.recompute import fingerprint
+    g = torch.Generator(device="cuda").manual_seed(11)
+    cache = (torch.randn(29, 4, 16, 128, device="cuda", generator=g) * 8).to(torch.float8_e4m3fn)
+    fp = block_fingerprints(cache).cpu().numpy()
+    ref = F.kv_block_fp3(cache.view(torch.int8).cpu().numpy())
+    assert np.array_equal(fp, ref)
+    for b in (0, 13, 28):
+        assert np.array_equal(fp[b], fingerprint(cache[b]).cpu().numpy())
+    base = (torch.randn(13, 2000, device="cuda", generator=g) * 8).to(torch.float8_e4m3fn)
+    for view in (base[:, :777], base[:, 1:778], base[:, 3:2000]):
+        got = block_fingerprints(view).cpu().numpy()
+        want = F.kv_block_fp3(view.contiguous().view(torch.int8).cpu().numpy())
+        assert np.array_equal(got, want), view.shape
+    c2 = cache.clone()
+    c2.view(torch.uint8)[3, 1, 5, 7] ^= 0x10
+    fp2 = block_fingerprints(c2).cpu().numpy()
+    assert (fp2 != fp).any(axis=1).nonzero()[0].tolist() == [3]
+    bt = torch.tensor([[0, 5, 9, -1], [3, 3, 28, 7]], device="cuda")
+    led = KVLedger(cache, 2, 4)
+    led.record(bt)
+    assert led.verify(bt).read()["mismatched"] == 0
+    stale = bt.clone()
+    stale[1, 2] = 27
+    assert led.verify(stale).read()["entries"] == [(1, 2)]
+
+
 def test_qwen3_like_cache_28_layers_4096_blocks():
     """28 layers x 4096 blocks of [8 KV heads, 16 tokens, 2 x 128] bf16 N(0,1) (7.5 GB); 64 sequences of U[512,
     2048] tokens whose block-table entries are drawn from the 4096 blocks with replacement (about 80 blocks a
