@@ -95,6 +95,45 @@ int sdc_matmul_check_acc(int dtype, const void* A, int64_t sab, int64_t sam, int
                          const float* sign_table, int64_t* result, void* workspace, int64_t workspace_bytes,
                          float* scores_out, hipStream_t stream);
 
+/* ---- the precise check scored from the fused GEMM's block statistics ----------------------------------------
+ * Replaces fused.zscores_from_stats (fused.py:181-235): the check of sdc_matmul_check_acc for C = A @ B + bias (2-D,
+ * alpha = beta = 1) with C's plain, signed, squared and absolute block sums read from stats ((m, nb, 4) float64,
+ * strides sst_m, sst_b in doubles, as sdc_fused_mm writes them) instead of C.  bias: a vector of n (of dtype, or fp32
+ * with bias_f32) or null.  Blocks of 128 columns (one of n when n < 128).  k >= 1.  workspace: at least
+ * sdc_matmul_check_acc_workspace(1, 1, 1, m, k, n, 128) bytes. */
+int sdc_matmul_check_acc_stats(int dtype, const void* A, int64_t sam, int64_t sak, const void* B, int64_t sbk,
+                               int64_t sbn, const double* stats, int64_t sst_m, int64_t sst_b, int64_t m, int64_t k,
+                               int64_t n, const void* bias, int bias_f32, float nfma, float z, float abs_floor,
+                               const float* sign_table, int64_t* result, void* workspace, int64_t workspace_bytes,
+                               float* scores_out, hipStream_t stream);
+
+/* ---- a linear layer's matmul with its precise check fused in ------------------------------------------------
+ * Replace fused.fused_mm (fused.py:116-170) and fused.fused_mm_checked (fused.py:462-546).  C = A @ B + bias, A (m, k)
+ * and B (k, n) of dtype (bf16/fp16) with any strides (B is typically a weight's transpose), C (m, n) of dtype with
+ * row stride scm and unit column stride, computed on MFMA with fp32 accumulation and rounded once (bias, a vector
+ * of n of dtype or fp32 with bias_f32, added in fp32 first).  inject != 0 adds inj_v to the accumulator at
+ * (inj_m, inj_n) before rounding (fault-injection experiments).  m, n >= 1, k >= 0 (k = 0: C is the bias).
+ * Operands that are not depth-contiguous with 16-byte aligned rows, or whose k is not a multiple of 32, are copied
+ * into the workspace first.  workspace: at least sdc_fused_mm_workspace(...) bytes (0 is possible for sdc_fused_mm).
+ *   sdc_fused_mm: also stats ((m, ceil(n / 128), 4) float64, contiguous): per row and block of 128 columns the
+ *     plain sum, signed sum (the block width's pattern from sign_table), sum of squares and sum of absolute values
+ *     of the fp32 accumulator before rounding; sdc_matmul_check_acc_stats scores them.
+ *   sdc_fused_mm_checked: the check scored in the kernel (no float64 on the expected side): A times three 16-bit
+ *     parts of each block sum of B on MFMA, summed with compensation; precise mode's noise model plus the expected
+ *     side's rounding (C1 sqrt(32) u |a_row| |block sums|_2 + 4 u |expected|); result, scores_out ((m, nb, 2) or
+ *     null) as sdc_matmul_check; expected_out ((m, nb, 2) float64 or null) receives the expected sides. */
+int64_t sdc_fused_mm_workspace(const void* A, int64_t sam, int64_t sak, const void* B, int64_t sbk, int64_t sbn,
+                               int64_t m, int64_t k, int64_t n, int checked);
+int sdc_fused_mm(int dtype, const void* A, int64_t sam, int64_t sak, const void* B, int64_t sbk, int64_t sbn,
+                 int64_t m, int64_t k, int64_t n, const void* bias, int bias_f32, const float* sign_table, void* C,
+                 int64_t scm, double* stats, int64_t inj_m, int64_t inj_n, float inj_v, int inject, void* workspace,
+                 int64_t workspace_bytes, hipStream_t stream);
+int sdc_fused_mm_checked(int dtype, const void* A, int64_t sam, int64_t sak, const void* B, int64_t sbk,
+                         int64_t sbn, int64_t m, int64_t k, int64_t n, const void* bias, int bias_f32,
+                         const float* sign_table, void* C, int64_t scm, float nfma, float z, float abs_floor,
+                         int64_t* result, float* scores_out, double* expected_out, int64_t inj_m, int64_t inj_n,
+                         float inj_v, int inject, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 /* ---- both block checksums of one linear layer, one pass over y (no counterpart function in the reference) --------
  * y = x @ W^T (+ bias): the column-block check of sdc_check_static (the serving check, serve.py:301-396) and the
  * row-block check of sdc_matmul_check on the transposed views (W, x^T, y^T, bias[:, None]; checksum.py:435-530),
@@ -256,7 +295,8 @@ int sdc_attn_check_noalloc(int dtype, const void* q, int64_t sqt, int64_t sqh, c
  * "serve_score", "b_stage", "b_finish", "split", "train_gemm", "train_score" (also the grouped check's),
  * "col_gemm", "xstage", "xfinish", "row_gemm", "ypass" (sdc_linear_check), "quant_gemm_i8", "quant_gemm_fp8",
  * "quant_score_i8", "quant_score_fp8", "fingerprint3", "fingerprint2", "kv_fingerprint", "attn_check", "acc_bsums",
- * "acc_finish", "acc_anorm", "acc_gemm", "acc_score" (sdc_matmul_check_acc). */
+ * "acc_finish", "acc_anorm", "acc_gemm", "acc_score" (sdc_matmul_check_acc, sdc_matmul_check_acc_stats),
+ * "fused_pack", "fused_side", "fused_mm", "fused_mm_checked" (sdc_fused_mm, sdc_fused_mm_checked). */
 int sdc_profile_enable(int on);
 int sdc_profile_reset(void);
 int sdc_profile_read(const char* name, double* total_ms, int64_t* launches);

@@ -36,6 +36,13 @@ SIGNATURES = {
     "sdc_matmul_check_acc_workspace": (I64, [I64, I64, I64, I64, I64, I64, I64]),
     "sdc_matmul_check_acc": (I32, [I32, P, I64, I64, I64, I64, P, I64, I64, I64, I64, P, I64, I64, I64, I64, I64, I64,
                                    I64, I64, P, I32, I64, I64, I64, F32, F32, F32, F32, F32, P, P, P, I64, P, P]),
+    "sdc_matmul_check_acc_stats": (I32, [I32, P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, I64, P, I32, F32, F32,
+                                         F32, P, P, P, I64, P, P]),
+    "sdc_fused_mm_workspace": (I64, [P, I64, I64, P, I64, I64, I64, I64, I64, I32]),
+    "sdc_fused_mm": (I32, [I32, P, I64, I64, P, I64, I64, I64, I64, I64, P, I32, P, P, I64, P, I64, I64, F32, I32, P,
+                           I64, P]),
+    "sdc_fused_mm_checked": (I32, [I32, P, I64, I64, P, I64, I64, I64, I64, I64, P, I32, P, P, I64, F32, F32, F32, P, P,
+                                   P, I64, I64, F32, I32, P, I64, P]),
     "sdc_expected_splits": (I64, [I64, I64, I64]),
     "sdc_linear_check_workspace": (I64, [I64, I64, I64]),
     "sdc_linear_check": (I32, [I32, P, I64, P, I64, P, I64, P, I64, I64, I64, P, I64, P, P, P, P, P, F32, F32, P,

@@ -16,6 +16,9 @@
 //      the GPU (each split its own plane, added by the scorer);
 //   5. acc_score: one pass over C, 16 lanes per (batch, row, block): fp64 plain and signed sums, |C_block|_2 and
 //      |C_block|_1 (fp32), then one lane scores the pair; worst keys and the unjudged count go to the result row.
+// sdc_matmul_check_acc_stats scores the same check from the block statistics the fused GEMM leaves instead of C
+// (fused.py:181-235, `zscores_from_stats`: 2-D, bias vector, alpha = beta = 1; |C_block|_2 is the square root of
+// the float64 sum of squares).
 #include "common.h"
 #include "profile.h"
 
@@ -76,6 +79,8 @@ struct AccArgs {
   double* E;                       // [splits][batch_c][m][2 nb]
   int64_t* result;
   float* scores;                   // (batch_c, m, nb, 2) or null
+  const double* stats;             // instead of C: (m, nb, 4) plain, signed, squared, absolute block sums of C
+  int64_t sst_m, sst_b;            //   (row and block strides, in doubles)
 };
 
 __device__ __forceinline__ int64_t bwidth(const AccArgs& a, int64_t jb) {
@@ -306,7 +311,16 @@ __global__ __launch_bounds__(256) void acc_score_kernel(AccArgs a) {
   const int64_t cbase = bc * a.scb + row * a.scm + jb * a.bs * a.scn;
   double pl = 0.0, sg = 0.0, bpl = 0.0, bsg = 0.0;
   float sq = 0.f, l1 = 0.f, bmx = 0.f;
-  if (live) {
+  double sqd = 0.0;
+  if (live && a.stats) {                    // the fused kernel's block statistics (fused.py:205-207)
+    if (c16 == 0) {
+      const double* st = a.stats + row * a.sst_m + jb * a.sst_b;
+      pl = st[0];
+      sg = st[1];
+      sqd = st[2];
+      l1 = (float)st[3];
+    }
+  } else if (live) {
     if (a.scn == 1 && wid == 128 && ((uintptr_t)(a.C + cbase) & 15) == 0) {
       const f32x4 v0 = *reinterpret_cast<const f32x4*>(a.C + cbase + 8 * c16);
       const f32x4 v1 = *reinterpret_cast<const f32x4*>(a.C + cbase + 8 * c16 + 4);
@@ -330,7 +344,7 @@ __global__ __launch_bounds__(256) void acc_score_kernel(AccArgs a) {
         l1 += fabsf(x);
       }
     }
-    if (a.bias_kind == 2) {
+    if (a.bias_kind == 2 && !a.stats) {
       const int64_t bb0 = bc * a.sbias_b + row * a.sbias_m + jb * a.bs * a.sbias_n;
       for (int64_t c = c16; c < wid; c += 16) {
         const float v = bias_at(a, DT, bb0 + c * a.sbias_n);
@@ -379,7 +393,8 @@ __global__ __launch_bounds__(256) void acc_score_kernel(AccArgs a) {
       bound = bound + (float)fabs(a.beta) * bmx;
     }
     const float wf = (float)wid;
-    const float cn = sqrtf(sq);
+    // from statistics: sqrt of the float64 sum of squares (a NaN stays NaN), rounded to fp32
+    const float cn = a.stats ? (float)sqrt(sqd < 0.0 ? 0.0 : sqd) : sqrtf(sq);
     const float per_out_u = (float)((ACC_C2 * sqrt((double)a.k) + ACC_C3 * a.steps + sqrt((double)wid)) * ACC_U);
     float prod = (anorm * bfrob) * (float)(ACC_C1 * sqrt((double)a.k) * fabs(a.alpha) * ACC_U);
     prod = fabsf(prod) < __builtin_inff() ? prod : bound * (float)(ACC_U * 128.0);
@@ -495,6 +510,37 @@ extern "C" int64_t sdc_matmul_check_acc_workspace(int64_t batch_a, int64_t batch
                                                   int64_t k, int64_t n, int64_t bs) {
   if (batch_a < 1 || batch_b < 1 || batch_c < 1 || m < 1 || k < 1 || n < 1 || bs < 1) return 0;
   return acc_layout(batch_a, batch_b, batch_c, m, k, n, bs < 128 ? bs : 128).total + 256;
+}
+
+extern "C" int sdc_matmul_check_acc_stats(int dtype, const void* A, int64_t sam, int64_t sak, const void* B,
+                                          int64_t sbk, int64_t sbn, const double* stats, int64_t sst_m,
+                                          int64_t sst_b, int64_t m, int64_t k, int64_t n, const void* bias,
+                                          int bias_f32, float nfma, float z, float abs_floor,
+                                          const float* sign_table, int64_t* result, void* workspace,
+                                          int64_t workspace_bytes, float* scores_out, hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
+  if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EUNSUPPORTED;
+  if (!A || !B || !stats || !sign_table || !result) return SDC_EINVAL;
+  if (m < 1 || k < 1 || n < 1) return SDC_EINVAL;
+  const int64_t bw = n < 128 ? n : 128;
+  const AccLayout L = acc_layout(1, 1, 1, m, k, n, bw);
+  if (m * L.nb * 2 > 0xFFFFFFFFll) return SDC_EUNSUPPORTED;
+  if (!workspace || workspace_bytes < L.total + 256) return SDC_EWORKSPACE;
+  uint8_t* ws = (uint8_t*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  AccArgs a{};
+  a.A = A; a.sab = 0; a.sam = sam; a.sak = sak; a.batch_a = 1;
+  a.B = B; a.sbb = 0; a.sbk = sbk; a.sbn = sbn; a.batch_b = 1;
+  a.C = nullptr; a.batch_c = 1;
+  a.stats = stats; a.sst_m = sst_m; a.sst_b = sst_b;
+  a.m = m; a.k = k; a.n = n; a.bs = bw; a.nb = L.nb; a.rem = n % bw; a.nslice = L.nslice;
+  a.splits = L.splits; a.kchunk = L.kchunk;
+  a.bias = bias; a.bias_kind = bias ? 1 : 0; a.bias_f32 = bias_f32; a.sbias_n = 1;
+  a.alpha = 1.0; a.beta = 1.0; a.steps = nfma > 0.f ? (double)k / (double)nfma : 0.0;
+  a.z = z; a.abs_floor = abs_floor; a.sign_table = sign_table;
+  a.B2T = (double*)(ws + L.off_b2); a.part = (float*)(ws + L.off_part); a.bstat = (float*)(ws + L.off_bstat);
+  a.bsum = (double*)(ws + L.off_bsum); a.bmax = (float*)(ws + L.off_bmax); a.an = (float*)(ws + L.off_an);
+  a.E = (double*)(ws + L.off_e); a.result = result; a.scores = scores_out;
+  return dtype == SDC_BF16 ? acc_run<SDC_BF16>(a, L, 1, stream) : acc_run<SDC_FP16>(a, L, 1, stream);
 }
 
 extern "C" int sdc_matmul_check_acc(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, int64_t batch_a,

@@ -11,20 +11,12 @@
 // fill the 256 CUs: each split writes its own plane of E and the scoring kernels add the planes.
 #include "common.h"
 #include "gemm.h"
+#include "mfma_pipe.h"
 #include "profile.h"
 
 namespace {
 
-template <int DT>
-__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
-  if constexpr (DT == SDC_BF16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                   0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
-                                                  0, 0, 0);
-  }
-}
+using sdc_pipe::mfma32;
 
 __device__ __forceinline__ f32x16 mfma32_i8(u32x4 a, u32x4 b, f32x16 c) {
   return __builtin_bit_cast(f32x16, __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a),
@@ -159,21 +151,13 @@ __device__ __forceinline__ void norm_acc(u32x4 v, float& sq, float& ab) {
 // (two rows, four chunks each) hit 32 distinct banks.
 // Workgroups are numbered so that each XCD (dispatch is round-robin over the eight) takes a contiguous range of
 // tiles: column tiles of one row tile, and row tiles of one depth slice, share an XCD's L2.
-constexpr int KS = 32;                 // depth per stage
+using sdc_pipe::KS;                    // depth per stage
+using sdc_pipe::lds_at;
+using sdc_pipe::lds_load16;
+using sdc_pipe::lgkmcnt0_imm;
+using sdc_pipe::vmcnt_imm;
 constexpr int NT = 512;                // threads per workgroup
 constexpr int NBUF = 3;                // LDS buffers
-
-__device__ __forceinline__ int lds_at(int row, int chunk) { return row * KS + 8 * (chunk ^ ((row >> 1) & 3)); }
-
-// s_waitcnt immediate that waits until at most n vector memory operations are outstanding (other counters free)
-constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-// 16 bytes per lane from global memory straight into LDS: lane L's bytes land at lds + 16 L (lds wave-uniform)
-__device__ __forceinline__ void lds_load16(const uint8_t* g, uint16_t* lds) {
-  __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g), lds, 16, 0, 0);
-}
-
-// ... until no LDS or scalar-memory operation is outstanding
-constexpr int lgkmcnt0_imm() { return 15 | (3 << 14) | (7 << 4); }
 
 template <int WGN, int NP>
 struct Tile {

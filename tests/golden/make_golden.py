@@ -13,6 +13,9 @@ cases, the inputs and the reference's answers:
   * serve.npz      serve.check_static_impl: every checksum's score, the state row (keys and counts);
   * quant.npz      modes.judge on fp8 e4m3 and int8 GEMMs (inputs from modes._inputs, results of modes.gemm's CPU
                    path, with and without an injected fault): per-block z and wrong-block counts;
+  * fused.npz      fused.fused_mm (output words, float64 block statistics), fused.zscores_from_stats on them (clean,
+                   faults added to the accumulator, epoch 3, nfma) and fused.fused_mm_checked (scored in the kernel),
+                   run in Triton's CPU interpreter (TRITON_INTERPRET=1 in the environment);
   * attn.npz       serve_attn.attn_check_torch on make_case calls (shapes, request mixes, a sliding window, wrong
                    outputs, wrong KV writes and slots, block ids outside the cache, non-finite values, padding)
                    over several steps: every sample's per-dimension scores, the 18-column state row and the
@@ -287,6 +290,123 @@ def make_acc(cs):
     return len(names)
 
 
+def _fused_operands(m, k, n, dtype, bias, layout, seed):
+    """A (m, k), B (k, n), bias: a linear layer's forward (B = w.t(), w stored (n, k)), a plain B, or a weight
+    gradient's A = gy.t() (gy stored (k, m))."""
+    g = torch.Generator().manual_seed(seed)
+    A = torch.randn(m, k, generator=g).to(dtype)
+    B = (torch.randn(k, n, generator=g) / max(k, 1) ** 0.5).to(dtype)
+    if layout == "w.t()":
+        B = B.t().contiguous().t()
+    elif layout == "gy.t()":
+        A = A.t().contiguous().t()
+    b = (torch.randn(n, generator=g) * 0.5).to(dtype) if bias else None
+    return A, B, b
+
+
+FUSED_LAYOUTS = ("plain", "w.t()", "gy.t()")
+FUSED_SHAPES = [(16, 96, 200, True, "w.t()"), (33, 64, 128, False, "plain"), (8, 40, 77, True, "w.t()"),
+                (5, 256, 300, True, "gy.t()"), (70, 130, 129, False, "w.t()"), (1, 32, 256, True, "plain"),
+                (300, 64, 520, True, "w.t()")]
+
+
+def make_fused(fused, cs):
+    """fused.fused_mm (output words and float64 block statistics), fused.zscores_from_stats on those statistics
+    (clean, faults added to the accumulator, another epoch's pattern, nfma) and fused.fused_mm_checked (the fp32
+    self-check scored in the kernel), all in Triton's CPU interpreter."""
+    st_ = _Store()
+    st_.out_full = {}
+    out = st_.out
+    names = []
+
+    def rec(name, kind, A, B, b, layout, nfma=None, epoch=0, inject=None, stats=None, **res):
+        i = len(names)
+        names.append(name)
+        p = f"c{i}_"
+        out[p + "ids"] = np.array([st_.put(A.contiguous()), st_.put(B.contiguous()),
+                                   st_.put(b) if b is not None else ""])
+        iv = inject if inject is not None else (-1, -1, 0.0)
+        out[p + "meta"] = np.array([1.0 if A.dtype == torch.float16 else 0.0, FUSED_LAYOUTS.index(layout),
+                                    nfma or 0, epoch, iv[0], iv[1], iv[2], {"fm": 0, "zs": 1, "chk": 2}[kind]],
+                                   np.float64)
+        out[p + "shape"] = np.array([A.shape[0], A.shape[1], B.shape[1]], np.int64)
+        if stats is not None:
+            out[p + "stats"] = stats.numpy()
+        for key, val in res.items():
+            out[p + key] = val
+
+    def resolved(st, seen):
+        r = cs.resolve([st], 6.0)[0]
+        zs = np.concatenate([z.numpy().astype(np.float32) for z in seen]) if seen else np.zeros(0, np.float32)
+        row = np.array([r.max_z, -1 if r.row is None else r.row, -1 if r.col_block is None else r.col_block,
+                        float("nan") if r.noise is None else r.noise], np.float64)
+        return zs, row
+
+    for dtype in (torch.bfloat16, torch.float16):
+        tag = "bf16" if dtype == torch.bfloat16 else "fp16"
+        for i, (m, k, n, bias, layout) in enumerate(FUSED_SHAPES):
+            A, B, b = _fused_operands(m, k, n, dtype, bias, layout, i)
+            base = f"{tag}_{m}x{k}x{n}_{layout}"
+            C, stats = fused.fused_mm(A, B, b)
+            rec(base + "_fm", "fm", A, B, b, layout, stats=stats, C=_bits(C))
+            with _MaxRecorder() as mr:
+                st = fused.zscores_from_stats(A, B, stats, b)
+            zs, row = resolved(st, mr.seen)
+            rec(base + "_zs", "zs", A, B, b, layout, stats=stats, zs=zs, result=row)
+            row_i, col_i = m // 2, n - 1
+            for delta in (1.0, 1e-2, float("inf"), float("nan")):
+                inj = (row_i, col_i, delta) if math.isfinite(delta) else (0, 0, delta)
+                _, st2 = fused.fused_mm(A, B, b, inject=inj)
+                with _MaxRecorder() as mr:
+                    st = fused.zscores_from_stats(A, B, st2, b)
+                zs, row = resolved(st, mr.seen)
+                rec(base + f"_zs_inj{delta:g}", "zs", A, B, b, layout, inject=inj, stats=st2, zs=zs, result=row)
+            A2, B2, b2 = _fused_operands(m, k, n, dtype, bias, layout, 100 + i)
+            with _MaxRecorder() as mr:
+                C2, st = fused.fused_mm_checked(A2, B2, b2)
+            zs, row = resolved(st, mr.seen)
+            rec(base + "_chk", "chk", A2, B2, b2, layout, C=_bits(C2), zs=zs, result=row)
+            typical = float(C2.float().abs().median()) or 1.0
+            inj = (m - 1, n - 1, 0.01 * typical)
+            with _MaxRecorder() as mr:
+                _, st = fused.fused_mm_checked(A2, B2, b2, inject=inj)
+            zs, row = resolved(st, mr.seen)
+            rec(base + "_chk_inj", "chk", A2, B2, b2, layout, inject=inj, zs=zs, result=row)
+    # another epoch's pattern and the tensor-core step count, on one bf16 case
+    A, B, b = _fused_operands(32, 128, 256, torch.bfloat16, True, "w.t()", 99)
+    _, st3 = fused.fused_mm(A, B, b, epoch=3)
+    with _MaxRecorder() as mr:
+        st = fused.zscores_from_stats(A, B, st3, b, epoch=3, nfma=16)
+    zs, row = resolved(st, mr.seen)
+    rec("bf16_epoch3_nfma16_zs", "zs", A, B, b, "w.t()", nfma=16, epoch=3, stats=st3, zs=zs, result=row)
+    with _MaxRecorder() as mr:
+        _, st = fused.fused_mm_checked(A, B, b, epoch=3, nfma=16)
+    zs, row = resolved(st, mr.seen)
+    rec("bf16_epoch3_nfma16_chk", "chk", A, B, b, "w.t()", nfma=16, epoch=3, zs=zs, result=row)
+    # self-check: an Inf the inputs cannot produce, and an Inf input (unjudged)
+    with _MaxRecorder() as mr:
+        _, st = fused.fused_mm_checked(A, B, b, inject=(5, 7, float("inf")))
+    zs, row = resolved(st, mr.seen)
+    rec("bf16_chk_inf_acc", "chk", A, B, b, "w.t()", inject=(5, 7, float("inf")), zs=zs, result=row)
+    A2 = A.clone()
+    A2[3, 4] = float("inf")
+    with _MaxRecorder() as mr:
+        _, st = fused.fused_mm_checked(A2, B, b)
+    zs, row = resolved(st, mr.seen)
+    rec("bf16_chk_inf_input", "chk", A2, B, b, "w.t()", zs=zs, result=row)
+    # fp16 weights whose block sums exceed fp16's range (the parts are scaled by a power of two)
+    g = torch.Generator().manual_seed(0)
+    A = torch.randn(16, 64, generator=g).half()
+    B = (torch.rand(64, 256, generator=g) * 900 + 100).half()
+    with _MaxRecorder() as mr:
+        C, st = fused.fused_mm_checked(A, B)
+    zs, row = resolved(st, mr.seen)
+    rec("fp16_large_block_sums_chk", "chk", A, B, None, "plain", C=_bits(C), zs=zs, result=row)
+    out["names"] = np.array(names)
+    np.savez_compressed(os.path.join(OUT, "fused.npz"), **out)
+    return len(names)
+
+
 def _serve_cases():
     g = torch.Generator().manual_seed(11)
     shapes = [(64, 256, 300, True), (1, 256, 1000, False), (200, 96, 40, True), (33, 130, 129, True),
@@ -556,7 +676,12 @@ def main():
     from sdcguard import serve as sv
     cs.USE_FAST = False
     torch.set_num_threads(4)
-    which = sys.argv[1:] or ["signs", "train", "acc", "serve", "quant", "attn"]
+    which = sys.argv[1:] or ["signs", "train", "acc", "serve", "quant", "attn", "fused"]
+    if "fused" in which:
+        if os.environ.get("TRITON_INTERPRET") != "1":
+            sys.exit("fused.npz runs the reference's Triton kernels in the CPU interpreter: set TRITON_INTERPRET=1")
+        from sdcguard import fused
+        print("fused.npz:", make_fused(fused, cs), "cases")
     if "attn" in which:
         from sdcguard import serve_attn as sa
         print("attn.npz:", make_attn(sa), "cases")
