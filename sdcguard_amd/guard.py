@@ -15,6 +15,11 @@ precise=True (guard.py:31-35, :471-530): on checked steps each protected layer c
 an fp32 output (the accumulator), queues the precise check of it (matmul_zscores_acc: float64 checksums against the
 fp32 accumulation's own rounding, far below what bf16 rounding hides), then rounds it once; on_accumulator(layer,
 pass, C32) may change the fp32 result before its check (fault injection).  Unchecked steps run the layer unchanged.
+precise="fused" (guard.py:1209-1270): the same products come from the library's fused GEMM, whose epilogue checks
+the fp32 accumulator before rounding it (fused.fused_mm_checked; fused_mm + zscores_from_stats with
+SDCGUARD_FUSED_FP64=1), so no fp32 product is written or read back; fused_inject(layer, pass, (m, n)) -> (row, col,
+value) or None adds a fault to one accumulator element (experiments).  A product the fused kernel refuses switches
+the guard to precise=True from then on (stats["fused_fallbacks"], fused_why).
 The reference's other routes (a dispatch mode over every operator, DTensor shards, recompute and replica checks)
 are not part of this path.
 """
@@ -22,6 +27,7 @@ from __future__ import annotations
 
 import contextlib
 import math
+import os
 import random
 import threading
 import time
@@ -49,6 +55,7 @@ class Group:
         self.device, self.dtype, self.block = torch.device(device), dtype, int(block)
         self.abs_floor, self.z, self.epoch = float(abs_floor), float(z), int(epoch)
         self.precise, self.nfma = bool(precise), nfma
+        self.fused = False              # checks queued by add_fused (the fused GEMM's own)
         self.meta: list = []            # per check: (rows m, blocks nb, batched)
         self._rows: list = []           # (CHUNK, 3) int64 result blocks on the device
         self.result: Optional[torch.Tensor] = None
@@ -76,6 +83,24 @@ class Group:
                                 z=self.z, epoch=self.epoch, out=self._slot())
         self.meta.append((st.m, st.nb, st.batched))
         return len(self.meta) - 1
+
+    def add_fused(self, A, B, bias, inject=None, fp64: bool = False):
+        """C = A @ B + bias from the fused GEMM with the check of its fp32 accumulator queued here (fused.py);
+        fp64: statistics scored in float64 (zscores_from_stats) instead of the kernel's own fp32 self-check.
+        Returns (C rounded to A's dtype, the check's index)."""
+        from . import fused as _fused
+        if A.dtype != self.dtype:
+            raise ValueError(f"this group checks products of {self.dtype}, not {A.dtype}")
+        if fp64:
+            C, stats = _fused.fused_mm(A, B, bias, epoch=self.epoch, inject=inject)
+            st = _fused.zscores_from_stats(A, B, stats, bias, z=self.z, nfma=self.nfma, epoch=self.epoch,
+                                           abs_floor=self.abs_floor, out=self._slot())
+        else:
+            C, st = _fused.fused_mm_checked(A, B, bias, z=self.z, nfma=self.nfma, epoch=self.epoch,
+                                            abs_floor=self.abs_floor, inject=inject, out=self._slot())
+        self.fused = True
+        self.meta.append((st.m, st.nb, False))
+        return C, len(self.meta) - 1
 
     def launch(self) -> None:
         """Every check's result row in one device tensor (checks, 3); never waits for the GPU."""
@@ -143,13 +168,16 @@ class _PreciseLinear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w, b, guard, label):
         x2 = x.reshape(-1, x.shape[-1])
-        y32 = _acc_mm(x2, w.t())
-        if b is not None:
-            y32 = y32.add_(b.float())
-        guard._accumulator(label, "forward", x2, w.t(), y32, b)
         ctx.save_for_backward(x, w)
         ctx.guard, ctx.label, ctx.has_bias = guard, label, b is not None
-        return y32.to(x.dtype).view(*x.shape[:-1], w.shape[0])
+        y = guard._fused(label, "forward", x2, w.t(), b)
+        if y is None:
+            y32 = _acc_mm(x2, w.t())
+            if b is not None:
+                y32 = y32.add_(b.float())
+            guard._accumulator(label, "forward", x2, w.t(), y32, b)
+            y = y32.to(x.dtype)
+        return y.view(*x.shape[:-1], w.shape[0])
 
     @staticmethod
     def backward(ctx, gy):
@@ -161,16 +189,22 @@ class _PreciseLinear(torch.autograd.Function):
         gx = gw = gb = None
         checked = guard._active
         if need_x:
-            gx32 = _acc_mm(gy2, w)
-            if checked:
-                guard._accumulator(label, "input grad", gy2, w, gx32, None)
-            gx = gx32.to(x.dtype).view(x.shape)
+            gx = guard._fused(label, "input grad", gy2, w, None) if checked else None
+            if gx is None:
+                gx32 = _acc_mm(gy2, w)
+                if checked:
+                    guard._accumulator(label, "input grad", gy2, w, gx32, None)
+                gx = gx32.to(x.dtype)
+            gx = gx.view(x.shape)
         if need_w:
             gyt = gy2.t()
-            gw32 = _acc_mm(gyt, x2)
-            if checked:
-                guard._accumulator(label, "weight grad", gyt, x2, gw32, None)
-            gw = gw32.to(w.dtype)
+            gw = guard._fused(label, "weight grad", gyt, x2, None) if checked else None
+            if gw is None:
+                gw32 = _acc_mm(gyt, x2)
+                if checked:
+                    guard._accumulator(label, "weight grad", gyt, x2, gw32, None)
+                gw = gw32
+            gw = gw.to(w.dtype)
         if need_b and ctx.has_bias:
             gb = gy2.sum(0)
         return gx, gw, gb, None, None
@@ -195,17 +229,23 @@ class SDCGuard:
     def __init__(self, sample_rate: float = 1.0, block: int = 128, z: float = 6.0,
                  on_alert: Optional[Callable[[SDCEvent], None]] = None, raise_on_alert: bool = False,
                  abs_floor: Optional[float] = None, every: int = 10, max_pending: int = 4096,
-                 fresh_signs: bool = True, seed: int = 0, precise: bool = False, nfma: Optional[int] = 16,
+                 fresh_signs: bool = True, seed: int = 0, precise=False, nfma: Optional[int] = 16,
                  on_accumulator: Optional[Callable[[str, str, torch.Tensor], None]] = None):
-        """precise: check the fp32 accumulators of the protected layers' products (see the module docstring);
-        nfma: products per tensor-core accumulation step of those products (16: one 32x32x16 MFMA; None: none)."""
+        """precise: True or "fused", check the fp32 accumulators of the protected layers' products (see the module
+        docstring); nfma: products per tensor-core accumulation step of those products (16: one 32x32x16 MFMA;
+        None: none)."""
         if not 0.0 <= sample_rate <= 1.0:
             raise ValueError("sample_rate is a share in [0, 1]")
+        if precise not in (False, True, "fused"):
+            raise ValueError(f"precise is False, True or 'fused', not {precise!r}")
         self.sample_rate, self.block, self.z = float(sample_rate), int(block), float(z)
         self.on_alert, self.raise_on_alert = on_alert, raise_on_alert
         self.abs_floor = ABS_FLOOR if abs_floor is None else float(abs_floor)
         self.every, self.max_pending, self.fresh_signs = int(every), int(max_pending), fresh_signs
-        self.precise, self.nfma, self.on_accumulator = bool(precise), nfma, on_accumulator
+        self.precise, self.nfma, self.on_accumulator = precise, nfma, on_accumulator
+        self.fused_inject: Optional[Callable] = None      # precise="fused": (layer, pass, (m, n)) -> fault or None
+        self._fused_off = False                           # the fused kernel refused a product: precise=True now
+        self.fused_why: Optional[str] = None
         self._rng = random.Random(seed)
         self._lock = threading.RLock()
         self._hooks: list = []
@@ -219,6 +259,8 @@ class SDCGuard:
         self.events: list = []
         self.results: list = []
         self.stats = {"layers": 0, "matmuls_seen": 0, "checks": 0, "alerts": 0, "skipped_dtype": 0, "flushes": 0}
+        if precise == "fused":
+            self.stats.update(checked_fused=0, fused_fallbacks=0)
 
     # ------------------------------------------------------------------------------------------- protect
     def protect(self, model: torch.nn.Module) -> "SDCGuard":
@@ -257,10 +299,45 @@ class SDCGuard:
             if x.dtype not in UNIT_ROUNDOFF or w.dtype != x.dtype:
                 self.stats["skipped_dtype"] += 1
                 return linear(x, w, b)
-            self.stats["matmuls_seen"] += 3 if torch.is_grad_enabled() and (x.requires_grad or w.requires_grad) else 1
+            grads = torch.is_grad_enabled()              # the forward, and each gradient product backward will run
+            self.stats["matmuls_seen"] += 1 + int(grads and x.requires_grad) + int(grads and w.requires_grad)
             with torch.autocast(device_type="cuda", enabled=False):
                 return _PreciseLinear.apply(x, w, b, self, label)
         return forward
+
+    def _fused(self, layer: str, where: str, A, B, bias):
+        """precise="fused": A @ B (+ bias) from the fused GEMM with its check queued, or None where the fused
+        kernel does not take it (the caller computes the fp32 product and checks it as precise=True does).  A product
+        left out by sample_rate is the ordinary matmul, unchecked."""
+        if self.precise != "fused" or self._fused_off or not A.is_cuda:
+            return None
+        if A.shape[0] == 0 or A.shape[1] == 0 or B.shape[1] == 0:
+            return None
+        if not self._sampled():
+            C = A @ B.to(A.dtype)
+            return C if bias is None else C.add_(bias.to(C.dtype))
+        inj = self.fused_inject(layer, where, (A.shape[0], B.shape[1])) if self.fused_inject is not None else None
+        from ._lib import HipLibraryError
+        with self._lock:
+            key = (A.device, A.dtype, "fused")
+            g = self._groups.get(key)
+            if g is None:
+                g = self._groups[key] = Group(A.device, A.dtype, self.block, self.abs_floor, self.z, self._epoch,
+                                              precise=True, nfma=self.nfma)
+            try:
+                C, i = g.add_fused(A, B, bias, inject=inj, fp64=os.environ.get("SDCGUARD_FUSED_FP64") == "1")
+            except HipLibraryError as e:
+                self._fused_off = True
+                self.stats["fused_fallbacks"] += 1
+                self.fused_why = f"{layer} ({where}): {e}"
+                import warnings
+                warnings.warn(f"the fused precise check refused a product, precise=True takes over: {self.fused_why}",
+                              RuntimeWarning, stacklevel=2)
+                return None
+            self._pending.append((g, i, layer, where, self.step))
+            self.stats["checks"] += 1
+            self.stats["checked_fused"] += 1
+        return C
 
     def _accumulator(self, layer: str, where: str, A, B, C32, bias) -> None:
         """Precise mode: one product's fp32 result before it is rounded (on_accumulator may change it first)."""
@@ -401,8 +478,11 @@ class SDCGuard:
                               col_block=c_i, noise=noise)
             out.append(res)
             if not res.ok:
+                extra = {"pass": where}
+                if g.fused:
+                    extra["dtype"] = f"float32 accumulator of {g.dtype} (fused)"
                 ev = SDCEvent(detector="accumulator" if g.precise else "checksum", layer=layer, z=z, step=step,
-                              row=r_i, col_block=c_i, noise=noise, nonfinite=not finite, extra={"pass": where})
+                              row=r_i, col_block=c_i, noise=noise, nonfinite=not finite, extra=extra)
                 alerts.append(ev)
         self.results.extend(out)
         for ev in alerts:

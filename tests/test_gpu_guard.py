@@ -140,3 +140,60 @@ def test_precise_mode_checks_the_fp32_accumulators():
     assert ev.detector == "accumulator" and ev.layer == "2" and ev.extra["pass"] == "weight grad"
     assert (ev.row, ev.col_block) == (7, 0) and ev.z > 6
     g2.unprotect()
+
+
+def test_precise_fused_mode_matches_precise_mode():
+    """precise="fused" (_fused_compare.py:112-165): every linear product of a checked step goes through the fused
+    GEMM's self-check; losses and gradients agree with precise=True's, both clean; a fault added to one weight
+    gradient's accumulator raises one alert, named; with sample_rate the products left out run unchecked."""
+    from sdcguard_amd.guard import SDCGuard
+
+    def model():
+        torch.manual_seed(0)
+        return torch.nn.Sequential(torch.nn.Linear(256, 384), torch.nn.GELU(), torch.nn.Linear(384, 256)).cuda()
+
+    def step(net, g, seed, step_no):
+        torch.manual_seed(seed)
+        x = torch.randn(48, 256, device="cuda")
+        with g.at_step(step_no):
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                loss = net(x).float().pow(2).mean()
+            loss.backward()
+        grads = [p.grad.clone() for p in net.parameters()]
+        net.zero_grad()
+        return loss.detach(), grads
+
+    net_p, net_f = model(), model()
+    gp = SDCGuard(every=0, precise=True).protect(net_p)
+    gf = SDCGuard(every=0, precise="fused").protect(net_f)
+    for s in range(2):
+        lp, grp = step(net_p, gp, s, s)
+        lf, grf = step(net_f, gf, s, s)
+        assert torch.allclose(lp, lf, rtol=1e-3), (lp, lf)
+        for a, c in zip(grp, grf):
+            assert (a - c).abs().max() <= 2.0 ** -6 * a.abs().max()
+    rf, rp = gf.flush(), gp.flush()
+    print("fused guard stats:", gf.stats, "max z", max(r.max_z for r in rf))
+    assert gf.stats["checked_fused"] == gf.stats["checks"] == 10 and gf.stats["alerts"] == 0
+    assert gf.stats["fused_fallbacks"] == 0 and all(r.ok and r.max_z >= 0 for r in rf)
+    assert gp.stats["alerts"] == 0 and len(rp) == 10
+
+    hits = []
+    gf.on_alert = hits.append
+    gf.fused_inject = lambda name, pass_, shape: (3, 5, 0.05) if (name, pass_) == ("2", "weight grad") else None
+    step(net_f, gf, 7, 2)
+    gf.fused_inject = None
+    gf.flush()
+    assert len(hits) == 1, hits
+    ev = hits[0]
+    assert ev.layer == "2" and ev.extra["pass"] == "weight grad" and "fused" in ev.extra["dtype"]
+    assert (ev.row, ev.col_block) == (3, 0) and ev.z > 6
+    gp.unprotect()
+    gf.unprotect()
+
+    net_s = model()
+    g_s = SDCGuard(every=0, precise="fused", sample_rate=0.5, seed=1).protect(net_s)
+    step(net_s, g_s, 3, 0)
+    g_s.flush()
+    assert 0 < g_s.stats["checked_fused"] < g_s.stats["matmuls_seen"] == 5 and g_s.stats["alerts"] == 0, g_s.stats
+    g_s.unprotect()
