@@ -134,6 +134,28 @@ int sdc_fused_mm_checked(int dtype, const void* A, int64_t sam, int64_t sak, con
                          int64_t* result, float* scores_out, double* expected_out, int64_t inj_m, int64_t inj_n,
                          float inj_v, int inject, void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
+/* ---- the check of a serving layer's FP8 input quantization ---------------------------------------------------
+ * Replaces serve_fp8.quant_check_torch (serve_fp8.py:79-178): did the FP8 codes xq the GEMM got, and their scale(s)
+ * xs, come from this step's real rows of x by the layer's recipe (0 static: xs[0] against static_ref[0] when given;
+ * 1 dynamic per tensor: max |x| over the real rows / 448 against xs[0], noting a scale equal to the maximum over
+ * every row; 2 dynamic per token: each sampled row's max |x| / 448, capped by scale_ub[0] when given and at least
+ * 1 / (448 * 512), against xs[row])?  Two rows sampled per call ((step * 7919 + j * 104729) % rows) are quantized
+ * as the layer's kernels do (x / scale per token, x * (1 / scale) otherwise, clamped to +-448, E4M3 rounded to
+ * nearest even) and compared with xq in code order: two or more steps apart is wrong, one step is counted.
+ *   dtype: of x, 0 bf16, 1 fp16, 4 fp32; x (m, k) strides sxm, sxk; xq (mq >= m, k) uint8 codes, strides sqm, sqk;
+ *   xs: xs_n fp32 scales, stride sxs (per token: indexed by row).  rows_buf[0] * mult (clamped to m): the step's
+ *   real rows (0: nothing judged); stepbuf[0]: the step; mult: input rows per token.
+ *   state_row: the layer's 8 int64 counters (calls, wrong scales, scales from outside rows, sampled rows with wrong
+ *   values, values one step off, last finding (step & 0x7FFFFFFF) << 32 | kind << 24 | row, worst scale ratio bits,
+ *   static scale changed), added to.  workspace: sdc_fp8_quant_check_workspace(m) bytes (used by recipe 1).  No
+ *   host synchronisation, no memory set: the call can be captured in a graph. */
+int64_t sdc_fp8_quant_check_workspace(int64_t m);
+int sdc_fp8_quant_check(int dtype, const void* x, int64_t sxm, int64_t sxk, int64_t m, int64_t k, const uint8_t* xq,
+                        int64_t sqm, int64_t sqk, int64_t mq, const float* xs, int64_t xs_n, int64_t sxs, int recipe,
+                        const float* scale_ub, const float* static_ref, const int64_t* rows_buf,
+                        const int64_t* stepbuf, int64_t mult, int64_t* state_row, void* workspace,
+                        int64_t workspace_bytes, hipStream_t stream);
+
 /* ---- both block checksums of one linear layer, one pass over y (no counterpart function in the reference) --------
  * y = x @ W^T (+ bias): the column-block check of sdc_check_static (the serving check, serve.py:301-396) and the
  * row-block check of sdc_matmul_check on the transposed views (W, x^T, y^T, bias[:, None]; checksum.py:435-530),
@@ -296,7 +318,8 @@ int sdc_attn_check_noalloc(int dtype, const void* q, int64_t sqt, int64_t sqh, c
  * "col_gemm", "xstage", "xfinish", "row_gemm", "ypass" (sdc_linear_check), "quant_gemm_i8", "quant_gemm_fp8",
  * "quant_score_i8", "quant_score_fp8", "fingerprint3", "fingerprint2", "kv_fingerprint", "attn_check", "acc_bsums",
  * "acc_finish", "acc_anorm", "acc_gemm", "acc_score" (sdc_matmul_check_acc, sdc_matmul_check_acc_stats),
- * "fused_pack", "fused_side", "fused_mm", "fused_mm_checked" (sdc_fused_mm, sdc_fused_mm_checked). */
+ * "fused_pack", "fused_side", "fused_mm", "fused_mm_checked" (sdc_fused_mm, sdc_fused_mm_checked), "fp8q_amax",
+ * "fp8q_judge" (sdc_fp8_quant_check). */
 int sdc_profile_enable(int on);
 int sdc_profile_reset(void);
 int sdc_profile_read(const char* name, double* total_ms, int64_t* launches);

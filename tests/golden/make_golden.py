@@ -16,6 +16,9 @@ cases, the inputs and the reference's answers:
   * fused.npz      fused.fused_mm (output words, float64 block statistics), fused.zscores_from_stats on them (clean,
                    faults added to the accumulator, epoch 3, nfma) and fused.fused_mm_checked (scored in the kernel),
                    run in Triton's CPU interpreter (TRITON_INTERPRET=1 in the environment);
+  * fp8.npz        serve_fp8.quant_check_torch (the FP8 quantization check): each recipe clean, scales taken over
+                   padding rows or otherwise wrong, codes one, two and three steps off, a static scale changed,
+                   non-finite inputs, an unarmed step, MoE rows per token; the state row after each case's calls;
   * attn.npz       serve_attn.attn_check_torch on make_case calls (shapes, request mixes, a sliding window, wrong
                    outputs, wrong KV writes and slots, block ids outside the cache, non-finite values, padding)
                    over several steps: every sample's per-dimension scores, the 18-column state row and the
@@ -407,6 +410,90 @@ def make_fused(fused, cs):
     return len(names)
 
 
+def _fp8_cases(sf):
+    """serve_fp8.quant_check_torch calls: (name, x2, xq codes, xs, recipe, scale_ub, static_ref, real rows, steps,
+    mult); each case's calls (one per step) add into one state row."""
+    g = torch.Generator().manual_seed(5)
+    out = []
+    for dt, tag in ((torch.bfloat16, "bf16"), (torch.float16, "fp16"), (torch.float32, "fp32")):
+        m, pad, k = 24, 8, 96
+        x = (torch.randn(m + pad, k, generator=g) * 3).to(dt)
+        x[m:] *= 20                                   # padding rows left by an earlier, larger request
+        real = 19
+        st = torch.tensor([17], dtype=torch.int64)
+        rows = sf.sample_rows(st, torch.tensor([real]))
+        # per tensor
+        ok_s = (x[:real].float().abs().amax() / 448.0).reshape(1)
+        xq = sf.quantize(x, ok_s, False)
+        out.append((f"{tag}_tensor_clean", x, xq, ok_s, 1, None, None, real, [17], 1))
+        out.append((f"{tag}_tensor_not_armed", x, xq, ok_s, 1, None, None, 0, [17], 1))
+        pad_s = (x.float().abs().amax() / 448.0).reshape(1)
+        out.append((f"{tag}_tensor_from_padding", x, sf.quantize(x, pad_s, False), pad_s, 1, None, None, real, [17],
+                    1))
+        out.append((f"{tag}_tensor_scale_wrong", x, sf.quantize(x, ok_s * 1.1, False), ok_s * 1.1, 1, None, None, real,
+                    [17], 1))
+        out.append((f"{tag}_tensor_rows_all", x, sf.quantize(x, pad_s, False), pad_s, 1, None, None, m + pad, [17], 1))
+        for d, what in ((1, "one_step"), (2, "two_steps"), (-3, "three_steps_down")):
+            bad = xq.clone()
+            r = int(rows[1])
+            bad[r, 5] = (bad[r, 5].to(torch.int32) + d).clamp(0, 126).to(torch.uint8) if bad[r, 5] < 0x80 else \
+                (bad[r, 5].to(torch.int32) - d).clamp(0x80, 0xFE).to(torch.uint8)
+            out.append((f"{tag}_tensor_values_{what}", x, bad, ok_s, 1, None, None, real, [17], 1))
+        # per token
+        tok = (x.float().abs().amax(-1, keepdim=True) / 448.0).clamp(min=sf.MIN_SCALE)
+        xqt = sf.quantize(x, tok, True)
+        out.append((f"{tag}_token_clean", x, xqt, tok, 2, None, None, real, [17, 18, 2 ** 32 + 5], 1))
+        badt = tok.clone()
+        badt[int(rows[0])] *= 1.5
+        out.append((f"{tag}_token_scale_wrong", x, sf.quantize(x, badt, True), badt, 2, None, None, real, [17], 1))
+        ub = torch.tensor([0.5 * float(x[:real].float().abs().max())])
+        tub = (torch.minimum(x.float().abs().amax(-1, keepdim=True), ub) / 448.0).clamp(min=sf.MIN_SCALE)
+        out.append((f"{tag}_token_ub", x, sf.quantize(x, tub, True), tub, 2, ub, None, real, [17, 21], 1))
+        out.append((f"{tag}_token_ub_missing", x, sf.quantize(x, tub, True), tub, 2, None, None, real, [17], 1))
+        out.append((f"{tag}_token_moe_mult2", x, xqt, tok, 2, None, None, 9, [33, 34], 2))
+        # static
+        s0 = torch.tensor([0.02])
+        xqs = sf.quantize(x, s0, False)
+        out.append((f"{tag}_static_clean", x, xqs, s0, 0, None, s0.clone(), real, [17], 1))
+        out.append((f"{tag}_static_changed", x, xqs, s0, 0, None, torch.tensor([0.021]), real, [17, 40], 1))
+        out.append((f"{tag}_static_no_ref", x, xqs, s0, 0, None, None, real, [17], 1))
+        # non-finite input in a sampled row
+        xn = x.clone()
+        xn[int(rows[0]), 7] = float("nan")
+        out.append((f"{tag}_tensor_nan_input", xn, xq, ok_s, 1, None, None, real, [17], 1))
+        xi = x.clone()
+        xi[int(rows[0]), 9] = float("inf")
+        out.append((f"{tag}_token_inf_input", xi, sf.quantize(xi, tok, True), tok, 2, None, None, real, [17], 1))
+    return out
+
+
+def make_fp8(sf):
+    """serve_fp8.quant_check_torch: each case's state row after its calls."""
+    st_ = _Store()
+    st_.out_full = {}
+    out = st_.out
+    names = []
+    for i, (name, x, xq, xs, recipe, ub, sref, real, steps, mult) in enumerate(_fp8_cases(sf)):
+        state = torch.zeros(1, sf.COLS, dtype=torch.int64)
+        rows_buf = torch.tensor([real], dtype=torch.int64)
+        for stp in steps:
+            sf.quant_check_torch(x, xq, xs, recipe, ub, sref, rows_buf, torch.tensor([stp], dtype=torch.int64),
+                                 state, 0, mult)
+        names.append(name)
+        p = f"c{i}_"
+        out[p + "ids"] = np.array([st_.put(x), st_.put(xq.view(torch.int8).to(torch.int16))])
+        dtc = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 4}[x.dtype]
+        out[p + "meta"] = np.array([dtc, recipe, real, mult, x.shape[0], x.shape[1], xq.shape[0]], np.int64)
+        out[p + "steps"] = np.array(steps, np.int64)
+        out[p + "xs"] = xs.float().reshape(-1).numpy()
+        out[p + "ub"] = np.array([] if ub is None else ub.float().reshape(-1).tolist(), np.float32)
+        out[p + "sref"] = np.array([] if sref is None else sref.float().reshape(-1).tolist(), np.float32)
+        out[p + "state"] = state[0].numpy()
+    out["names"] = np.array(names)
+    np.savez_compressed(os.path.join(OUT, "fp8.npz"), **out)
+    return len(names)
+
+
 def _serve_cases():
     g = torch.Generator().manual_seed(11)
     shapes = [(64, 256, 300, True), (1, 256, 1000, False), (200, 96, 40, True), (33, 130, 129, True),
@@ -676,7 +763,10 @@ def main():
     from sdcguard import serve as sv
     cs.USE_FAST = False
     torch.set_num_threads(4)
-    which = sys.argv[1:] or ["signs", "train", "acc", "serve", "quant", "attn", "fused"]
+    which = sys.argv[1:] or ["signs", "train", "acc", "serve", "quant", "attn", "fused", "fp8"]
+    if "fp8" in which:
+        from sdcguard import serve_fp8 as sf
+        print("fp8.npz:", make_fp8(sf), "cases")
     if "fused" in which:
         if os.environ.get("TRITON_INTERPRET") != "1":
             sys.exit("fused.npz runs the reference's Triton kernels in the CPU interpreter: set TRITON_INTERPRET=1")
