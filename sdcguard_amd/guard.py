@@ -230,10 +230,11 @@ class SDCGuard:
                  on_alert: Optional[Callable[[SDCEvent], None]] = None, raise_on_alert: bool = False,
                  abs_floor: Optional[float] = None, every: int = 10, max_pending: int = 4096,
                  fresh_signs: bool = True, seed: int = 0, precise=False, nfma: Optional[int] = 16,
-                 on_accumulator: Optional[Callable[[str, str, torch.Tensor], None]] = None):
+                 on_accumulator: Optional[Callable[[str, str, torch.Tensor], None]] = None, recompute: bool = False):
         """precise: True or "fused", check the fp32 accumulators of the protected layers' products (see the module
         docstring); nfma: products per tensor-core accumulation step of those products (16: one 32x32x16 MFMA;
-        None: none)."""
+        None: none); recompute: also compare each activation-checkpointed block's recompute with its forward run
+        (recompute.RecomputeCheck, installed by protect() and flushed with the checks)."""
         if not 0.0 <= sample_rate <= 1.0:
             raise ValueError("sample_rate is a share in [0, 1]")
         if precise not in (False, True, "fused"):
@@ -246,6 +247,10 @@ class SDCGuard:
         self.fused_inject: Optional[Callable] = None      # precise="fused": (layer, pass, (m, n)) -> fault or None
         self._fused_off = False                           # the fused kernel refused a product: precise=True now
         self.fused_why: Optional[str] = None
+        self.recompute = None
+        if recompute:
+            from .recompute import RecomputeCheck
+            self.recompute = RecomputeCheck(on_alert=self._recompute_alert)
         self._rng = random.Random(seed)
         self._lock = threading.RLock()
         self._hooks: list = []
@@ -263,8 +268,17 @@ class SDCGuard:
             self.stats.update(checked_fused=0, fused_fallbacks=0)
 
     # ------------------------------------------------------------------------------------------- protect
+    def _recompute_alert(self, ev) -> None:
+        rec = SDCEvent(detector="recompute", layer=ev.layer, z=ev.z, step=self.step, extra=dict(ev.extra))
+        self.events.append(rec)
+        self.stats["alerts"] += 1
+        if self.on_alert is not None:
+            self.on_alert(rec)
+
     def protect(self, model: torch.nn.Module) -> "SDCGuard":
         """Check the forward product and both gradient products of every plain nn.Linear of `model`."""
+        if self.recompute is not None:
+            self.recompute.install(model)
         for name, mod in model.named_modules():
             if not _plain_linear(mod) or mod in self._protected:
                 continue
@@ -279,6 +293,8 @@ class SDCGuard:
         return self
 
     def unprotect(self) -> None:
+        if self.recompute is not None:
+            self.recompute.uninstall()
         for h in self._hooks:
             h.remove()
         self._hooks.clear()
@@ -452,6 +468,9 @@ class SDCGuard:
     def flush(self) -> list:
         """Read every queued check back (one device-to-host copy per device), record the results and raise alerts.
         Returns their CheckResults in queue order."""
+        if self.recompute is not None:
+            self.recompute.step = self.step
+            self.recompute.flush()
         with self._lock:
             pending, self._pending = self._pending, []
             groups = {id(g): g for g, *_ in pending}

@@ -407,6 +407,8 @@ class ServeGuard:
         self.unjudged_seen: dict = {}
         self.events: list = []
         self.unsupported: dict = {}
+        self._scan = None                      # the weight scan (weight_scan())
+        self._marked_step: Optional[int] = None
         self.stats = {"layers": 0, "skipped_layers": 0, "polls": 0, "alerts": 0, "checks_executed": 0,
                       "unjudged_checksums": 0}
 
@@ -541,10 +543,22 @@ class ServeGuard:
                 events += self._report(dev, rows.take(n, wait=True))
             elif rows.in_flight is None:
                 rows.take(n, wait=False)
+        if self._scan is not None:
+            events += self._scan.poll(wait)
         return events
+
+    def weight_scan(self, budget_mb: Optional[float] = None, **kw):
+        """The scheduled weight scan of this guard's layers (serve_weights.WeightScan), created on the first call:
+        each poll() fingerprints the next layers' tensors, up to budget_mb, and compares them with their references."""
+        if self._scan is None:
+            from .serve_weights import DEFAULT_BUDGET_MB, WeightScan
+            self._scan = WeightScan(self, DEFAULT_BUDGET_MB if budget_mb is None else budget_mb, **kw)
+            self._scan.sync()
+        return self._scan
 
     def mark_step(self, step: int, rows: Optional[int] = None) -> None:
         """Stamp the capture area with the serving step (kept rows carry it)."""
+        self._marked_step = int(step)
         step = int(step) & STEP_MASK
         for r in self._rows.values():
             r.cap_meta[1:2].fill_((r.epoch << EPOCH_SHIFT) | step)
@@ -604,4 +618,5 @@ class ServeGuard:
                     lay["module"].__dict__.pop(attr, None)
             self.layers.clear()
             self._rows.clear()
+            self._scan = None
             self.stats["layers"] = 0

@@ -19,6 +19,7 @@ cases, the inputs and the reference's answers:
   * fp8.npz        serve_fp8.quant_check_torch (the FP8 quantization check): each recipe clean, scales taken over
                    padding rows or otherwise wrong, codes one, two and three steps off, a static scale changed,
                    non-finite inputs, an unarmed step, MoE rows per token; the state row after each case's calls;
+  * weights.npz    serve_weights.model_digest and fingerprint of a small model with 1, 2, 4 and 8-byte parameters;
   * attn.npz       serve_attn.attn_check_torch on make_case calls (shapes, request mixes, a sliding window, wrong
                    outputs, wrong KV writes and slots, block ids outside the cache, non-finite values, padding)
                    over several steps: every sample's per-dimension scores, the 18-column state row and the
@@ -494,6 +495,35 @@ def make_fp8(sf):
     return len(names)
 
 
+def digest_model():
+    """A small model with parameters of every element size the fingerprint takes (2, 4 and 8 bytes, and 1 byte
+    for an int8 parameter), as (name, tensor) in a fixed order."""
+    g = torch.Generator().manual_seed(9)
+    return [("a.weight", (torch.randn(96, 64, generator=g)).bfloat16()),
+            ("a.bias", torch.randn(96, generator=g).bfloat16()),
+            ("b.weight", torch.randn(33, 96, generator=g).half()),
+            ("c.scale", torch.randn(7, 5, generator=g)),
+            ("d.table", torch.randn(4, 3, generator=g).double()),
+            ("e.q", torch.randint(-128, 128, (40, 8), generator=g, dtype=torch.int8))]
+
+
+def make_weights(sw):
+    """serve_weights.model_digest and fingerprint of digest_model()'s parameters (the PyTorch version, CPU)."""
+    params = digest_model()
+    model = torch.nn.Module()
+    for name, t in params:
+        mod_name, attr = name.split(".")
+        if not hasattr(model, mod_name):
+            model.add_module(mod_name, torch.nn.Module())
+        getattr(model, mod_name).register_parameter(attr, torch.nn.Parameter(t, requires_grad=False))
+    out = {"digest": np.array(sw.model_digest(model)), "names": np.array([n for n, _ in params])}
+    for name, t in params:
+        out["fp_" + name] = sw.fingerprint(t).numpy()
+        out["bits_" + name] = t.contiguous().view(-1).view(torch.uint8).numpy()
+    np.savez_compressed(os.path.join(OUT, "weights.npz"), **out)
+    return len(params)
+
+
 def _serve_cases():
     g = torch.Generator().manual_seed(11)
     shapes = [(64, 256, 300, True), (1, 256, 1000, False), (200, 96, 40, True), (33, 130, 129, True),
@@ -763,7 +793,10 @@ def main():
     from sdcguard import serve as sv
     cs.USE_FAST = False
     torch.set_num_threads(4)
-    which = sys.argv[1:] or ["signs", "train", "acc", "serve", "quant", "attn", "fused", "fp8"]
+    which = sys.argv[1:] or ["signs", "train", "acc", "serve", "quant", "attn", "fused", "fp8", "weights"]
+    if "weights" in which:
+        from sdcguard import serve_weights as sw
+        print("weights.npz:", make_weights(sw), "parameters")
     if "fp8" in which:
         from sdcguard import serve_fp8 as sf
         print("fp8.npz:", make_fp8(sf), "cases")
