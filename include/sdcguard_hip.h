@@ -156,6 +156,31 @@ int sdc_fp8_quant_check(int dtype, const void* x, int64_t sxm, int64_t sxk, int6
                         const int64_t* stepbuf, int64_t mult, int64_t* state_row, void* workspace,
                         int64_t workspace_bytes, hipStream_t stream);
 
+/* ---- the sampled recompute of a fused MoE layer ---------------------------------------------------------------
+ * Replaces serve_moe.moe_check_torch / moe_check_triton (serve_moe.py:127-506): when the step in stepbuf[0] (low 32
+ * bits; the step's real rows above them, 0 unknown) modulo nlayers is this layer's index, recompute SAMPLES = 2 rows
+ * ((step / nlayers * 7919 + j * 104729) % rows) of y = sum_k g_k W2_e (act(W13_e[:I] x) * W13_e[I:] x) with the
+ * fused kernel's roundings (dtype: 0 bf16, 1 fp16, of x, out and the weights) and score each output against
+ * u |r| + 4u max_k |c_k| + u sqrt(sum_k g_k^2 sum_i (W2_ni h_i)^2) + max |g W2| s + spacing (u, spacing, fmax: the
+ * dtype's unit roundoff, subnormal spacing and largest value); also count the known real rows whose expert ids are
+ * all or partly -1.  Otherwise nothing is computed.
+ *   x, out (m, H) row strides sx, so; gw (m, K) routing weights (gdtype 0 bf16, 1 fp16, 4 fp32); ids (m, K) int32;
+ *   w13 (E, 2I, H) strides s13e, s13n; w2 (E, H, I) strides s2e, s2n; expert_map (global -> local expert) or null;
+ *   act 0 SiLU, 1 GELU; routed_first: the routing weight multiplies the first matmul's result.  H <= 8192.
+ *   state_row: the layer's 11 int64 (worst keys z << 32 | row, column, output bits, recompute bits, step; active
+ *   calls; rows checked; unjudged outputs; real rows unrouted, partly routed; (step << 32) | last such row + 1).
+ *   cap_meta (claimed, row, step, z bits), cap_x, cap_y (H floats), cap_ids (K int64), cap_g (K floats): the first
+ *   sampled row over `line`.  scores_out: (2, H) fp32 or null.  workspace: sdc_moe_check_workspace(H, I, K) bytes.
+ *   No host synchronisation, no memory set. */
+int64_t sdc_moe_check_workspace(int64_t H, int64_t I, int64_t K);
+int sdc_moe_check(int dtype, const void* x, int64_t sx, const void* out, int64_t so, const void* gw, int gdtype,
+                  const int32_t* ids, const void* w13, int64_t s13e, int64_t s13n, const void* w2, int64_t s2e,
+                  int64_t s2n, const int32_t* expert_map, int64_t m, int64_t H, int64_t I, int64_t K, int act,
+                  int routed_first, const int64_t* stepbuf, int64_t nlayers, int64_t index, float u, float spacing,
+                  float fmax, float line, int64_t* state_row, int32_t* cap_meta, float* cap_x, float* cap_y,
+                  int64_t* cap_ids, float* cap_g, float* scores_out, void* workspace, int64_t workspace_bytes,
+                  hipStream_t stream);
+
 /* ---- both block checksums of one linear layer, one pass over y (no counterpart function in the reference) --------
  * y = x @ W^T (+ bias): the column-block check of sdc_check_static (the serving check, serve.py:301-396) and the
  * row-block check of sdc_matmul_check on the transposed views (W, x^T, y^T, bias[:, None]; checksum.py:435-530),
@@ -319,7 +344,7 @@ int sdc_attn_check_noalloc(int dtype, const void* q, int64_t sqt, int64_t sqh, c
  * "quant_score_i8", "quant_score_fp8", "fingerprint3", "fingerprint2", "kv_fingerprint", "attn_check", "acc_bsums",
  * "acc_finish", "acc_anorm", "acc_gemm", "acc_score" (sdc_matmul_check_acc, sdc_matmul_check_acc_stats),
  * "fused_pack", "fused_side", "fused_mm", "fused_mm_checked" (sdc_fused_mm, sdc_fused_mm_checked), "fp8q_amax",
- * "fp8q_judge" (sdc_fp8_quant_check). */
+ * "fp8q_judge" (sdc_fp8_quant_check), "moe_up", "moe_act", "moe_down", "moe_compare" (sdc_moe_check). */
 int sdc_profile_enable(int on);
 int sdc_profile_reset(void);
 int sdc_profile_read(const char* name, double* total_ms, int64_t* launches);

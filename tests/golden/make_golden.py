@@ -20,6 +20,8 @@ cases, the inputs and the reference's answers:
                    padding rows or otherwise wrong, codes one, two and three steps off, a static scale changed,
                    non-finite inputs, an unarmed step, MoE rows per token; the state row after each case's calls;
   * weights.npz    serve_weights.model_digest and fingerprint of a small model with 1, 2, 4 and 8-byte parameters;
+  * moe.npz        serve_moe.moe_check_torch (the sampled fused-MoE recompute): the state row and the kept row after
+                   one call on the reference's verification scenarios and a larger routed-first case;
   * attn.npz       serve_attn.attn_check_torch on make_case calls (shapes, request mixes, a sliding window, wrong
                    outputs, wrong KV writes and slots, block ids outside the cache, non-finite values, padding)
                    over several steps: every sample's per-dimension scores, the 18-column state row and the
@@ -524,6 +526,95 @@ def make_weights(sw):
     return len(params)
 
 
+def make_moe(sm):
+    """serve_moe.moe_check_torch: the state row and the kept row after one call, on the reference's own verification
+    scenarios (serve_moe.py:524-598: clean, a wrong output, an expert map with a missing expert, an inactive step,
+    a padding row, garbage past the step's real rows, a real row unrouted or partly routed), for SiLU and GELU in bf16
+    and SiLU in fp16, plus a larger routed-first case with a wrong routing weight and a NaN output."""
+    st_ = _Store()
+    st_.out_full = {}
+    out = st_.out
+    names = []
+
+    def rec(name, x, y, g, ids, w13, w2, emap, act, rf, raw, nl, idx):
+        m, H = x.shape
+        k = ids.shape[1]
+        state = torch.zeros(1, sm.COLS, dtype=torch.int64)
+        cm = torch.zeros(1, sm.CAP_COLS, dtype=torch.int32)
+        cx, cy = torch.zeros(1, H), torch.zeros(1, H)
+        ci, cg = torch.zeros(1, max(k, 8), dtype=torch.int64), torch.zeros(1, max(k, 8))
+        sb = torch.full((1,), raw, dtype=torch.int64)
+        sm.moe_check_torch(x, y, g, ids, w13, w2, emap, act, rf, state, 0, sb, nl, idx, cm, cx, cy, ci, cg, sm.MOE_Z)
+        i = len(names)
+        names.append(name)
+        p = f"c{i}_"
+        out[p + "ids"] = np.array([st_.put(x), st_.put(y), st_.put(w13), st_.put(w2)])
+        out[p + "topk"] = ids.numpy().astype(np.int32)
+        out[p + "g"] = g.float().numpy()
+        out[p + "emap"] = np.array([] if emap is None else emap.tolist(), np.int32)
+        out[p + "meta"] = np.array([1 if x.dtype == torch.float16 else 0, act, int(rf), raw, nl, idx,
+                                    int(emap is not None)], np.int64)
+        out[p + "state"] = state[0].numpy()
+        out[p + "cap"] = cm[0].numpy().astype(np.int64)
+        out[p + "cap_x"], out[p + "cap_y"] = cx[0].numpy(), cy[0].numpy()
+        out[p + "cap_ids"], out[p + "cap_g"] = ci[0, :k].numpy(), cg[0, :k].numpy()
+
+    for dtype, act, tag in ((torch.bfloat16, 0, "bf16_silu"), (torch.bfloat16, 1, "bf16_gelu"),
+                            (torch.float16, 0, "fp16_silu")):
+        gen = torch.Generator().manual_seed(0)
+        E, H, I, K, M = 6, 192, 96, 3, 5
+        w13 = (torch.randn(E, 2 * I, H, generator=gen) * 0.05).to(dtype)
+        w2 = (torch.randn(E, H, I, generator=gen) * 0.05).to(dtype)
+        x = torch.randn(M, H, generator=gen).to(dtype)
+        g, ids = torch.topk(torch.softmax(torch.randn(M, E, generator=gen), -1), K, -1)
+        ids = ids.to(torch.int32)
+        emap = torch.tensor([0, 1, -1, 2, 3, 4], dtype=torch.int32)
+        w13m, w2m = w13[:5].contiguous(), w2[:5].contiguous()
+        ids_pad = ids.clone()
+        ids_pad[M - 1] = -1
+        ids_part = ids.clone()
+        ids_part[1, 0] = -1
+        for case in ("clean", "wrong", "map", "inactive", "padding", "real_rows", "unrouted_real", "partial_real"):
+            step = 3 if case != "inactive" else 4
+            given = {"real_rows": 3, "unrouted_real": M, "partial_real": M}.get(case)
+            raw = sm.pack_step(step, given)
+            use_map = case == "map"
+            cids = ids_pad if case in ("padding", "unrouted_real") else ids_part if case == "partial_real" else ids
+            y = sm._reference_layer(x, cids, g, w13m if use_map else w13, w2m if use_map else w2,
+                                    emap if use_map else None, act, dtype)
+            if case == "wrong":
+                rows = sm.sample_rows(torch.tensor(step), M, "cpu", 4)
+                y[int(rows[0]), 17] = y[int(rows[0]), 17] * 4 + 1
+            elif case in ("padding", "unrouted_real"):
+                y[M - 1] = 1000.0
+            elif case == "real_rows":
+                y[3:] = 1000.0
+            rec(f"{tag}_{case}", x, y, g, cids, w13m if use_map else w13, w2m if use_map else w2,
+                emap if use_map else None, act, False, raw, 4, 3)
+    # larger, routing weight applied on the input
+    gen = torch.Generator().manual_seed(1)
+    E, H, I, K, M = 8, 256, 128, 4, 40
+    w13 = (torch.randn(E, 2 * I, H, generator=gen) * 0.04).bfloat16()
+    w2 = (torch.randn(E, H, I, generator=gen) * 0.04).bfloat16()
+    x = torch.randn(M, H, generator=gen).bfloat16()
+    g, ids = torch.topk(torch.softmax(torch.randn(M, E, generator=gen), -1), K, -1)
+    ids = ids.to(torch.int32)
+    y = sm.recompute(x, ids, g, w13, w2, None, 0, True, torch.bfloat16)[0].to(torch.bfloat16)
+    raw = sm.pack_step(10, 33)
+    rows = sm.sample_rows(torch.tensor(10), torch.tensor(33), "cpu", 2)
+    rec("bf16_routed_first_clean", x, y, g, ids, w13, w2, None, 0, True, raw, 2, 0)
+    g2 = g.clone()
+    g2[int(rows[1]), 2] *= 1.25
+    y2 = sm.recompute(x, ids, g2, w13, w2, None, 0, True, torch.bfloat16)[0].to(torch.bfloat16)
+    rec("bf16_routed_first_wrong_weight", x, y2, g, ids, w13, w2, None, 0, True, raw, 2, 0)
+    y3 = y.clone()
+    y3[int(rows[0]), 100] = float("nan")
+    rec("bf16_routed_first_nan_output", x, y3, g, ids, w13, w2, None, 0, True, raw, 2, 0)
+    out["names"] = np.array(names)
+    np.savez_compressed(os.path.join(OUT, "moe.npz"), **out)
+    return len(names)
+
+
 def _serve_cases():
     g = torch.Generator().manual_seed(11)
     shapes = [(64, 256, 300, True), (1, 256, 1000, False), (200, 96, 40, True), (33, 130, 129, True),
@@ -793,7 +884,10 @@ def main():
     from sdcguard import serve as sv
     cs.USE_FAST = False
     torch.set_num_threads(4)
-    which = sys.argv[1:] or ["signs", "train", "acc", "serve", "quant", "attn", "fused", "fp8", "weights"]
+    which = sys.argv[1:] or ["signs", "train", "acc", "serve", "quant", "attn", "fused", "fp8", "weights", "moe"]
+    if "moe" in which:
+        from sdcguard import serve_moe as sm
+        print("moe.npz:", make_moe(sm), "cases")
     if "weights" in which:
         from sdcguard import serve_weights as sw
         print("weights.npz:", make_weights(sw), "parameters")
