@@ -408,6 +408,8 @@ class ServeGuard:
         self.events: list = []
         self.unsupported: dict = {}
         self._scan = None                      # the weight scan (weight_scan())
+        self._fp8 = None                       # FP8 quantization checks (fp8_checks())
+        self._moe = None                       # fused MoE checks (moe_checks())
         self._marked_step: Optional[int] = None
         self.stats = {"layers": 0, "skipped_layers": 0, "polls": 0, "alerts": 0, "checks_executed": 0,
                       "unjudged_checksums": 0}
@@ -543,9 +545,36 @@ class ServeGuard:
                 events += self._report(dev, rows.take(n, wait=True))
             elif rows.in_flight is None:
                 rows.take(n, wait=False)
+        if self._fp8 is not None:
+            events += self._fp8.poll(wait)
+        if self._moe is not None and self._moe.finalized:
+            events += self._moe.poll(wait)
         if self._scan is not None:
             events += self._scan.poll(wait)
         return events
+
+    def fp8_checks(self):
+        """The FP8 input-quantization checks of this guard's FP8 layers (serve_fp8.Fp8Checks), created on first use;
+        mark_step / end_step / poll reach them through the guard."""
+        if self._fp8 is None:
+            from .serve_fp8 import Fp8Checks
+            self._fp8 = Fp8Checks(self)
+        return self._fp8
+
+    def moe_checks(self, line: Optional[float] = None):
+        """The sampled recompute checks of fused MoE layers (serve_moe.MoEChecks), created on first use: add() the
+        layers, finalize() before capture; mark_step / end_step / poll reach them through the guard."""
+        if self._moe is None:
+            from .serve_moe import MOE_Z, MoEChecks
+            self._moe = MoEChecks(self, MOE_Z if line is None else line)
+        return self._moe
+
+    def end_step(self) -> None:
+        """After a model step's work is queued (the FP8 and MoE checks stop judging until the next mark_step)."""
+        if self._fp8 is not None:
+            self._fp8.end_step()
+        if self._moe is not None:
+            self._moe.end_step()
 
     def weight_scan(self, budget_mb: Optional[float] = None, **kw):
         """The scheduled weight scan of this guard's layers (serve_weights.WeightScan), created on the first call:
@@ -559,6 +588,10 @@ class ServeGuard:
     def mark_step(self, step: int, rows: Optional[int] = None) -> None:
         """Stamp the capture area with the serving step (kept rows carry it)."""
         self._marked_step = int(step)
+        if self._fp8 is not None:
+            self._fp8.mark_step(step, rows)
+        if self._moe is not None:
+            self._moe.mark_step(step, rows)
         step = int(step) & STEP_MASK
         for r in self._rows.values():
             r.cap_meta[1:2].fill_((r.epoch << EPOCH_SHIFT) | step)
@@ -616,6 +649,10 @@ class ServeGuard:
                     lay["hook"].remove()
                 for attr in ("_sdcguard_slot", "_sdcguard_name"):
                     lay["module"].__dict__.pop(attr, None)
+            for sub in (self._fp8, self._moe):
+                if sub is not None:
+                    sub.detach()
+            self._fp8 = self._moe = None
             self.layers.clear()
             self._rows.clear()
             self._scan = None

@@ -228,3 +228,33 @@ def test_moechecks_flow_alerts_and_capture():
         st.zero_()
     mc.end_step()
     mc.detach()
+
+
+def test_serveguard_reaches_fp8_and_moe_checks():
+    """ServeGuard.fp8_checks() / moe_checks(): mark_step, end_step and poll of the guard reach both."""
+    from sdcguard_amd import serve_fp8 as sf
+    from sdcguard_amd import serve_moe as sm
+    from sdcguard_amd.serve import ServeGuard
+    from tests.test_gpu_fp8 import _Quant
+    seen = []
+    g = ServeGuard(on_alert=seen.append)
+    L = _FusedMoE(seed=3)
+    mc = g.moe_checks()
+    assert mc.add(L, "experts") == 0 and mc.finalize() == 1
+    lin = torch.nn.Linear(64, 64)
+    a = g.fp8_checks().add(lin, "fp8", _Quant(), None, torch.device("cuda", 0))
+    gen = torch.Generator().manual_seed(1)
+    x = torch.randn(16, 512, generator=gen).bfloat16().cuda()
+    gw, ids, y = L.run(x, gen)
+    xf = torch.randn(16, 64, device="cuda").bfloat16()
+    s_ok = (xf.float().abs().amax() / 448.0).reshape(1)
+    g.mark_step(4, 16)
+    sf.check_call(a, xf, sf.quantize(xf, s_ok * 1.5, False), s_ok * 1.5)      # a wrong per-tensor scale
+    bad = y.clone()
+    bad[om.sample_rows(4, 16, 1)[0]] += 1.0                                   # a wrong expert output
+    sm.check_call(L._sdcguard_moe, x, gw, ids, bad)
+    g.end_step()
+    ev = g.poll(wait=True)
+    assert sorted(e.detector for e in ev) == ["serve_fp8", "serve_moe"], ev
+    assert len(seen) == 2
+    g.detach()
