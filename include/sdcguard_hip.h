@@ -190,16 +190,24 @@ int sdc_moe_check(int dtype, const void* x, int64_t sx, const void* out, int64_t
  *     SDC_EUNSUPPORTED: the caller runs the two checks separately).  Blocks are 128 wide.
  *   bias (n) or NULL; parts / spc / block_consts / w_norms: the layer's constants from sdc_layer_constants
  *     (k-contiguous part columns spc elements apart, the (nb, 12) block table, W's row norms [2][n]);
- *     sign_table: the epoch-0 128 x 128 table.
+ *     parts_frag: the same parts in fragment order (sdc_parts_fragments, made once per layer), or NULL (then, when
+ *     k is a multiple of 256, each call makes them in the workspace); sign_table: the epoch-0 128 x 128 table.
  *   state: int64[4] of the column check (sdc_check_static's row, counts on); row_result: int64[3] of the row check
  *     (sdc_matmul_check's result row; flat index ((column * mb + row block) * 2 + signed), mb = ceil(m / 128)).
  *   workspace: sdc_linear_check_workspace(m, k, n) bytes.
  *   col_scores (m, nb, 2) / row_scores (n, mb, 2): every checksum's score, or NULL.  flags bit 0: run the column
  *     check's GEMM on a side stream, concurrently with the row check's x pass and GEMM. */
 int64_t sdc_linear_check_workspace(int64_t m, int64_t k, int64_t n);
+/* The layer's three part planes in the fragment order the register-streamed expected-side GEMM reads (no
+ * counterpart in the reference; a layout of this library): for depth step s (16 deep), part p and 32-column
+ * fragment f, 1024 contiguous bytes, lane l's 16 bytes = part p, column 32 f + l % 32, depths
+ * 64 (s / 4) + 32 (l / 32) + 8 (s % 4) .. + 7.  parts as sdc_linear_check's (N = 2 nb columns of pitch spc), k a
+ * multiple of 64; out: sdc_parts_fragments_bytes(N, k) bytes, 16-byte aligned. */
+int64_t sdc_parts_fragments_bytes(int64_t N, int64_t k);
+int sdc_parts_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out, hipStream_t stream);
 int sdc_linear_check(int dtype, const void* x, int64_t sxm, const void* W, int64_t swn, const void* y, int64_t sym,
                      const void* bias, int64_t m, int64_t k, int64_t n, const void* parts, int64_t spc,
-                     const float* block_consts, const float* w_norms, const float* sign_table, int64_t* state,
+                     const void* parts_frag, const float* block_consts, const float* w_norms, const float* sign_table, int64_t* state,
                      int64_t* row_result, float z, float abs_floor, void* workspace, int64_t workspace_bytes,
                      float* col_scores, float* row_scores, int flags, hipStream_t stream);
 

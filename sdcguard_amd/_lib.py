@@ -51,8 +51,10 @@ SIGNATURES = {
                             P, I64, I64, F32, F32, F32, F32, P, P, P, P, P, P, P, P, I64, P]),
     "sdc_expected_splits": (I64, [I64, I64, I64]),
     "sdc_linear_check_workspace": (I64, [I64, I64, I64]),
-    "sdc_linear_check": (I32, [I32, P, I64, P, I64, P, I64, P, I64, I64, I64, P, I64, P, P, P, P, P, F32, F32, P,
-                               I64, P, P, I32, P]),
+    "sdc_linear_check": (I32, [I32, P, I64, P, I64, P, I64, P, I64, I64, I64, P, I64, P, P, P, P, P, P, F32, F32,
+                               P, I64, P, P, I32, P]),
+    "sdc_parts_fragments_bytes": (I64, [I64, I64]),
+    "sdc_parts_fragments": (I32, [P, I64, I64, I64, P, P]),
     "sdc_grouped_check_workspace": (I64, [I64, I64, I64, I64, I64]),
     "sdc_grouped_check": (I32, [I32, P, I64, I64, P, I64, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, P, P, I64,
                                 F32, F32, P, P, P, I64, P, P]),

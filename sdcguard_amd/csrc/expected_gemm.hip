@@ -538,7 +538,267 @@ __global__ __launch_bounds__(256) void split_kernel(SplitArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------- register-streamed GEMM
+// E = A @ (three parts of the block sums) with no depth split across workgroups.  A workgroup of 4 waves owns a
+// 64 x 64 tile of E (64 rows of A, 64 checksum columns) over the whole depth; wave q takes the q-th quarter of the
+// 64-deep segments, and the waves never wait for each other until the end.
+//
+// Depth order inside a segment: lane l (row or column l % 32, half h = l / 32) takes the 16-byte pieces 4 h + j
+// (j = 0 .. 3) of its 128-byte row segment, and step j multiplies depths {8 j .. 8 j + 7} u {32 + 8 j .. 32 + 8 j
+// + 7} -- the same ones in A and B -- so the four steps cover the segment.
+// A (the operand read once from HBM) goes through a ring of LDS buffers private to the wave, filled by
+// global_load_lds two segments ahead: each of the 8 instructions of a segment reads 8 rows x 128 bytes (whole
+// lines: HBM streams those at twice the rate of the MFMA lane order's 32-byte pieces), lane L the piece
+// (L % 8) ^ (L / 8) of row L / 8, landing at 16 L; so the fragment reads (8 lanes of a phase: 8 rows, one piece)
+// hit 8 different 16-byte bank groups.  B comes in fragment order (sdc_parts_fragments): the fragment of (step,
+// part, 32 columns) is 1024 contiguous bytes, lane l's 16 at 16 l; loaded straight into registers RB steps ahead.
+// (Measured on MI355X: the loop is bound by the vector memory path mixing A's HBM misses with B's cache hits, not
+// by the matrix cores; more waves, a deeper B ring or staggered depth orders did not speed it up.)
+// Every wave has the same number of segments (the depth is a multiple of 256).  The four waves' accumulators meet
+// in LDS and are added in wave (depth) order, so E is the same on every run; one plane, stored transposed
+// (E[col][row]).
+constexpr int RS_WAVES = 4;
+constexpr int RS_KMULT = 64 * RS_WAVES;       // depth granularity of the register-streamed GEMM
+constexpr int RS_RB = 4;                      // B's ring (steps); 8 measured no faster
+constexpr int RS_SEGB = 64 * 128;             // bytes of A per wave and segment (64 rows x 128 bytes)
+
+template <int DT, int RB>
+__global__ __launch_bounds__(64 * RS_WAVES, 1) void rs_gemm_kernel(GemmArgs g) {
+  constexpr int TRF = 2, TCF = 2, TR = 64, TC = 64, NG = TRF * TCF * 4;   // f32x4 groups of a wave's accumulators
+  constexpr int SPB = RB / 4;                                   // segments per loop iteration (B's ring: RB steps)
+  constexpr int ABUF = SPB + 2;                                 // A's ring: ABUF - 1 segments ahead
+  __shared__ __attribute__((aligned(16))) uint8_t smem[RS_WAVES * ABUF * RS_SEGB];
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int r = lane & 31, h = lane >> 5;
+  const int64_t N = g.N, m = g.m;
+  const int64_t nct = sdc_cdiv(N, TC), ncf = sdc_cdiv(N, 32);
+  // XCD-aware order: block b runs on XCD b % 8; XCD x takes the x-th eighth of the tiles, column tiles fastest (the
+  // column tiles of one row tile share their rows of A in that XCD's L2)
+  const int64_t G = (int64_t)gridDim.x, b = blockIdx.x;
+  const int64_t wid = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+  const int64_t ct = wid % nct, rt = wid / nct;
+  const int64_t r0 = rt * TR, c0 = ct * TC;
+  const int per = (int)(g.k / 64) / RS_WAVES;                   // segments per wave (the depth is a multiple of 256)
+  const int seg0 = w * per;
+  uint8_t* const abuf = smem + w * ABUF * RS_SEGB;
+  // fragment reads: frag i, step j -> row R = 32 i + r, piece 4 h + j -> slot 8 (R % 8) + ((4 h + j) ^ (R % 8)) of
+  // block R / 8
+  int ard[TRF][4];
+#pragma unroll
+  for (int i = 0; i < TRF; ++i)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int R = 32 * i + r, rr = R & 7;
+      ard[i][jj] = (R >> 3) * 1024 + 16 * (8 * rr + ((4 * h + jj) ^ rr));
+    }
+  // fragment (step s, part p, column fragment f) at B + ((s * 3 + p) * ncf + f) * 512 elements; column fragments
+  // past the last are replaced by the last one (their columns of E are never stored)
+  const uint16_t* bq = (const uint16_t*)g.B + (int64_t)(4 * seg0) * 3 * ncf * 512 + 8 * lane;
+  int bf[TCF];
+#pragma unroll
+  for (int n = 0; n < TCF; ++n) {
+    const int64_t f = c0 / 32 + n;
+    bf[n] = (int)((f < ncf ? f : ncf - 1) * 512);
+  }
+  const int64_t bstep = 3 * ncf * 512;                          // elements per step of B
+  const int lastseg = per - 1;
+  const int last = 4 * per - 1;
+  // A's loads: instruction I (0 .. 7) of a segment, lane L: row 8 I + L / 8 (rows past m read row m - 1; they only
+  // feed rows of E that are never stored), piece (L % 8) ^ (L / 8)
+  const uint8_t* aptr[8];
+#pragma unroll
+  for (int I = 0; I < 8; ++I) {
+    const int64_t row = r0 + 8 * I + (lane >> 3);
+    const int pc = (lane & 7) ^ (lane >> 3);
+    aptr[I] = (const uint8_t*)g.A + ((row < m ? row : m - 1) * g.sam + 64 * (int64_t)seg0) * 2 + 16 * pc;
+  }
+
+  u32x4 rb[RB][3][TCF];
+  // two of the 8 instructions of segment sg of A (into its ring buffer)
+  auto issue_a2 = [&](int sg, int I0) {
+    const int s2 = sg < lastseg ? sg : lastseg;
+    uint8_t* dst = abuf + (sg % ABUF) * RS_SEGB;
+#pragma unroll
+    for (int I = I0; I < I0 + 2; ++I) sdc_pipe::lds_load16(aptr[I] + 128 * (int64_t)s2, (uint16_t*)(dst + 1024 * I));
+  };
+  // B's loads and A's fragment reads are written out (global_load_dwordx4, ds_read_b128) and every wait is explicit:
+  // left to the compiler, a read of the LDS ring waits for all loads into LDS (it cannot tell the buffers apart) and
+  // the loop head waits for every load in flight.  Each B register is loaded in place ("+v": the register keeps its
+  // value's place across the loop) and passes through the s_waitcnt that covers its load ("+v" again) before an
+  // MFMA reads it.  smem is the kernel's only LDS object, so its LDS address is the low 32 bits of its generic
+  // address.
+  auto issue_b = [&](int slot, int st) {
+    const uint16_t* q = bq + (int64_t)(st < last ? st : last) * bstep;
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+      for (int n = 0; n < TCF; ++n)
+        asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(rb[slot][p][n]) : "v"(q + p * ncf * 512 + bf[n]));
+  };
+  const uint32_t lds0 = (uint32_t)(uintptr_t)abuf;
+  f32x16 acc[TRF][TCF];
+#pragma unroll
+  for (int i = 0; i < TRF; ++i)
+#pragma unroll
+    for (int n = 0; n < TCF; ++n)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][n][e] = 0.f;
+#pragma unroll
+  for (int q = 0; q < RB; ++q)
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+      for (int n = 0; n < TCF; ++n) rb[q][p][n] = u32x4{0u, 0u, 0u, 0u};
+  if (per > 0) {
+    // every step issues 3 TCF loads of B (RB steps ahead), then two of the 8 instructions of the segment ABUF - 1
+    // ahead of A; the prologue issues them as the steps before the first would.  So when step st begins, the loads
+    // issued after B(st) are the two of A in its step and the 3 TCF + 2 of each of the RB - 1 steps between: a
+    // constant, 8 RB - 6; the last loads of the step's segment of A were issued more than RB steps earlier.
+    for (int sgv = 0; sgv < ABUF - 1 - SPB; ++sgv)
+#pragma unroll
+      for (int I = 0; I < 8; I += 2) issue_a2(sgv, I);
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      issue_b(q, q);
+      issue_a2(q / 4 + ABUF - 1 - SPB, 2 * (q % 4));
+    }
+    for (int sg = 0; sg < per; sg += SPB) {
+#pragma unroll
+      for (int u = 0; u < SPB; ++u) {
+        const uint32_t L = lds0 + (uint32_t)(((sg + u) % ABUF) * RS_SEGB);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int q = 4 * u + jj;                            // B's slot of this step
+          static_assert(TCF == 2 && 8 * RB - 6 <= 63, "6 + 2 loads per step, at most 63 in flight");
+          asm volatile("s_waitcnt vmcnt(%6)"
+                       : "+v"(rb[q][0][0]), "+v"(rb[q][0][1]), "+v"(rb[q][1][0]), "+v"(rb[q][1][1]),
+                         "+v"(rb[q][2][0]), "+v"(rb[q][2][1])
+                       : "n"(8 * RB - 6));
+          u32x4 a0, a1;
+          asm volatile("ds_read_b128 %0, %1" : "=v"(a0) : "v"(L + (uint32_t)ard[0][jj]));
+          asm volatile("ds_read_b128 %0, %1" : "=v"(a1) : "v"(L + (uint32_t)ard[1][jj]));
+          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a0), "+v"(a1));
+          const u32x4 a[TRF] = {a0, a1};
+#pragma unroll
+          for (int p = 0; p < 3; ++p)
+#pragma unroll
+            for (int i = 0; i < TRF; ++i)
+#pragma unroll
+              for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<DT>(a[i], rb[q][p][n], acc[i][n]);
+          __builtin_amdgcn_sched_barrier(0);
+          issue_b(q, 4 * (sg + u) + jj + RB);
+          issue_a2(sg + u + ABUF - 1, 2 * jj);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    // every load done before the loop's registers are reused (the last steps' B loads land in registers nothing
+    // reads again) and before the workgroup's LDS is
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(rb[0][0][0]), "+v"(rb[0][0][1]), "+v"(rb[0][1][0]), "+v"(rb[0][1][1]), "+v"(rb[0][2][0]),
+                   "+v"(rb[0][2][1]));
+#pragma unroll
+    for (int q = 1; q < RB; ++q)
+      asm volatile("" : "+v"(rb[q][0][0]), "+v"(rb[q][0][1]), "+v"(rb[q][1][0]), "+v"(rb[q][1][1]), "+v"(rb[q][2][0]),
+                   "+v"(rb[q][2][1]));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __syncthreads();                                             // (the epilogue's LDS overlaps other waves' A)
+  // the waves' accumulators, added in wave order; group (i, n, r4) of a lane holds rows 8 r4 + 4 h .. + 3 of
+  // fragment row i, column l % 32 of fragment column n
+  f32x4* red = reinterpret_cast<f32x4*>(smem);                  // [RS_WAVES][NG][64]
+#pragma unroll
+  for (int i = 0; i < TRF; ++i)
+#pragma unroll
+    for (int n = 0; n < TCF; ++n)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        red[(w * NG + (i * TCF + n) * 4 + r4) * 64 + lane] =
+            f32x4{acc[i][n][4 * r4], acc[i][n][4 * r4 + 1], acc[i][n][4 * r4 + 2], acc[i][n][4 * r4 + 3]};
+  __syncthreads();
+  const int64_t me = g.m;
+#pragma unroll
+  for (int gq = 0; gq < NG / RS_WAVES; ++gq) {
+    const int gi = w * (NG / RS_WAVES) + gq;
+    f32x4 v = red[gi * 64 + lane];
+#pragma unroll
+    for (int q = 1; q < RS_WAVES; ++q) v += red[(q * NG + gi) * 64 + lane];
+    const int i = gi / (4 * TCF), n = (gi / 4) % TCF, r4 = gi % 4;
+    const int64_t row = r0 + 32 * i + 8 * r4 + 4 * h;
+    const int64_t col = c0 + 32 * n + r;
+    if (col < N) {
+      float* Ec = g.E + col * me;
+      if (row + 4 <= m && (me % 4) == 0) {
+        *reinterpret_cast<f32x4*>(Ec + row) = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (row + e < m) Ec[row + e] = v[e];
+      }
+    }
+  }
+}
+
+// Parts [3][N][kp] (k-contiguous per column, column stride spc) -> fragment order for rs_gemm_kernel: element e of
+// lane l of fragment (step s, part p, column fragment f) is part p, column 32 f + l % 32 (zero past N), depth
+// 64 (s / 4) + 32 (l / 32) + 8 (s % 4) + e.  One thread per 16-byte piece.
+__global__ __launch_bounds__(256) void parts_frag_kernel(const uint16_t* parts, int64_t spc, int64_t N, int64_t k,
+                                                         uint16_t* out) {
+  const int64_t ncf = sdc_cdiv(N, 32), nst = k / 16;
+  const int64_t total = nst * 3 * ncf * 64;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int lane = (int)(i % 64);
+    const int64_t fr = i / 64, f = fr % ncf, p = (fr / ncf) % 3, s = fr / (3 * ncf);
+    const int64_t col = 32 * f + lane % 32;
+    const int64_t kk = 64 * (s / 4) + 32 * (lane / 32) + 8 * (s % 4);
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (col < N) v = *reinterpret_cast<const u32x4*>(parts + (p * N + col) * spc + kk);
+    *reinterpret_cast<u32x4*>(out + i * 8) = v;
+  }
+}
+
 }  // namespace
+
+// The register-streamed GEMM applies to k-contiguous 16-bit A with depth a multiple of 256 and 16-byte rows, B in
+// fragment order (sdc_parts_fragments): one plane of E (transposed), 64 x 64 tiles.  Returns SDC_EUNSUPPORTED
+// otherwise.
+int sdc_rs_gemm_launch(int dtype, GemmArgs g, hipStream_t stream) {
+  if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EUNSUPPORTED;
+  if (g.sak != 1 || g.k % RS_KMULT || g.k < RS_KMULT || g.sam % 8 || ((uintptr_t)g.A | (uintptr_t)g.B) % 16 ||
+      !g.et || g.goffs)
+    return SDC_EUNSUPPORTED;
+  if (g.m < 1 || g.N < 1) return SDC_EINVAL;
+  const int64_t tiles = sdc_cdiv(g.m, 64) * sdc_cdiv(g.N, 64);
+  if (tiles > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
+  SdcProf prof(g.prof_name ? g.prof_name : "expected_gemm", stream);
+  const dim3 grid((unsigned)tiles), block(64 * RS_WAVES);
+  if (dtype == SDC_BF16) hipLaunchKernelGGL((rs_gemm_kernel<SDC_BF16, RS_RB>), grid, block, 0, stream, g);
+  else hipLaunchKernelGGL((rs_gemm_kernel<SDC_FP16, RS_RB>), grid, block, 0, stream, g);
+  SDC_LAUNCH_CHECK();
+  return SDC_OK;
+}
+
+// Bytes of the fragment-ordered copy of 3 x N 16-bit parts of depth k (k a multiple of 64).
+extern "C" int64_t sdc_parts_fragments_bytes(int64_t N, int64_t k) {
+  if (N < 1 || k < 64 || k % 64) return 0;
+  return 3 * sdc_cdiv(N, 32) * 32 * k * 2;
+}
+
+// 3 x N parts [3][N][spc] (16-bit, k-contiguous per column) -> fragment order for the register-streamed GEMM.
+extern "C" int sdc_parts_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out,
+                                   hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
+  if (!parts || !out || N < 1 || k < 64 || k % 64 || spc % 8 || spc < k || ((uintptr_t)parts | (uintptr_t)out) % 16)
+    return SDC_EINVAL;
+  const int64_t total = (k / 16) * 3 * sdc_cdiv(N, 32) * 64;
+  const int64_t blocks = sdc_cdiv(total, 256) < 4096 ? sdc_cdiv(total, 256) : 4096;
+  SdcProf prof("parts_frag", stream);
+  hipLaunchKernelGGL(parts_frag_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint16_t*)parts, spc, N, k,
+                     (uint16_t*)out);
+  SDC_LAUNCH_CHECK();
+  return SDC_OK;
+}
 
 // Split of the depth so that tiles x splits fill the GPU (one workgroup per CU), in multiples of the stage depth.
 extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols) {

@@ -32,10 +32,14 @@
 
 extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
 int sdc_gemm_launch(int dtype, GemmArgs g, int64_t batches, hipStream_t stream);
+int sdc_rs_gemm_launch(int dtype, GemmArgs g, hipStream_t stream);
+extern "C" int64_t sdc_parts_fragments_bytes(int64_t N, int64_t k);
+extern "C" int sdc_parts_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out, hipStream_t stream);
 
 namespace {
 
 constexpr int BS = 128;            // block width of both checks
+constexpr int RS_K = 256;          // depth multiple of the register-streamed GEMM (expected_gemm.hip)
 constexpr int XK = 256;            // depth per xstage workgroup
 constexpr int NXS = 5;             // partial stats per (depth chunk, row block): sq0, sq1, max0, max1, max|x|
 constexpr int RST = 8;             // final stats per row block: the NXS above, then the sum of its sign pattern
@@ -53,6 +57,8 @@ __device__ __forceinline__ uint16_t bf16_rne(float f) {
 struct XStageArgs {
   const uint16_t* x;
   int64_t sxm, m, k, kp, mb, rem, nkc;
+  int frag;                        // parts in the register-streamed GEMM's fragment order (else [3][2 mb][kp])
+  int64_t ncf;                     // (fragment order) 32-column fragments of the 2 mb checksum columns
   const float* s_full;             // sign pattern of a full row block (128), and of the last (rem) one
   const float* s_last;
   uint16_t* parts;                 // [3][2 mb][kp] bf16: hi, mid, lo of (plain, signed) per row block
@@ -169,9 +175,20 @@ __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
       const uint16_t md = bf16_rne(r1);
       const uint16_t lo = bf16_rne(r1 - bf16_lo(md));
       const int64_t col = 2 * ib + c;
-      a.parts[(0 * 2 * a.mb + col) * a.kp + kk] = h;
-      a.parts[(1 * 2 * a.mb + col) * a.kp + kk] = md;
-      a.parts[(2 * 2 * a.mb + col) * a.kp + kk] = lo;
+      if (a.frag) {
+        // element e of lane l of fragment (step s, part p, column fragment f): column 32 f + l % 32, depth
+        // 64 (s / 4) + 32 (l / 32) + 8 (s % 4) + e
+        const int64_t st = 4 * (kk >> 6) + ((kk & 31) >> 3);
+        const int64_t ln = (col & 31) + 32 * ((kk & 63) >> 5);
+        const int64_t base = (st * 3 * a.ncf + (col >> 5)) * 512 + ln * 8 + (kk & 7);
+        a.parts[base] = h;
+        a.parts[base + a.ncf * 512] = md;
+        a.parts[base + 2 * a.ncf * 512] = lo;
+      } else {
+        a.parts[(0 * 2 * a.mb + col) * a.kp + kk] = h;
+        a.parts[(1 * 2 * a.mb + col) * a.kp + kk] = md;
+        a.parts[(2 * 2 * a.mb + col) * a.kp + kk] = lo;
+      }
     }
   }
   float st[4] = {mine ? P * P : 0.f, mine ? S * S : 0.f, mine ? nan_abs(P) : 0.f, mine ? nan_abs(S) : 0.f};
@@ -294,7 +311,8 @@ __device__ __forceinline__ uint32_t pack_signs(float s0, float s1) {
 // contiguous bytes).  Waves 0 and 1 score the tile's 128 column-block pairs (one row each), waves 2 and 3 its 128
 // row-block pairs (one column each); what that scoring needs is loaded at the start, so its latency passes under
 // the arithmetic.
-template <int DT>
+// ONE: both checks' E come as one plane each (the register-streamed GEMMs), else up to SDC_MAX_SPLITS planes to add
+template <int DT, bool ONE>
 __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
   __shared__ f32x4 colp[BS][17];                // column partials [column][row group, rotated], padded
   __shared__ f32x4 rows[BS];                    // the tile's row sums
@@ -338,9 +356,10 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
     ebase = a.Erow + (int64_t)(2 * ib) * a.n + Jc; estride = a.n; pstride = 2 * a.mb * a.n;
     nbase = a.wn + Jc; nstride = a.n; splits = a.srow;
   }
-  float ev[SDC_MAX_SPLITS][2];
+  constexpr int NSPL = ONE ? 1 : SDC_MAX_SPLITS;
+  float ev[NSPL][2];
 #pragma unroll
-  for (int s = 0; s < SDC_MAX_SPLITS; ++s) {
+  for (int s = 0; s < NSPL; ++s) {
     const int64_t sc = s < splits ? s : 0;
     ev[s][0] = ebase[sc * pstride];
     ev[s][1] = ebase[sc * pstride + estride];
@@ -426,7 +445,7 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
   // ---- scoring
   float e0 = ev[0][0], e1 = ev[0][1];
 #pragma unroll
-  for (int s = 1; s < SDC_MAX_SPLITS; ++s)
+  for (int s = 1; s < NSPL; ++s)
     if (s < splits) {
       e0 += ev[s][0];
       e1 += ev[s][1];
@@ -519,7 +538,8 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
 
 struct Layout {
   int64_t nb, mb, rem_n, rem_m, nkc, kp, scol, srow;
-  int64_t off_parts, off_stats, off_xnp, off_xn, off_rstat, off_erow, off_ecol, total;   // in floats
+  bool rs_col, rs_row;
+  int64_t off_parts, off_stats, off_xnp, off_xn, off_rstat, off_erow, off_ecol, off_fcol, total;   // in floats
 };
 
 Layout layout(int64_t m, int64_t k, int64_t n) {
@@ -530,17 +550,25 @@ Layout layout(int64_t m, int64_t k, int64_t n) {
   L.rem_m = m % BS;
   L.nkc = sdc_cdiv(k, XK);
   L.kp = (k + 7) / 8 * 8;
-  L.scol = sdc_expected_splits(m, k, 2 * L.nb);
-  L.srow = sdc_expected_splits(n, k, 2 * L.mb);
+  // one plane from the register-streamed GEMM where the depth allows it and its tiles fill the GPU (64 of them
+  // at least), else depth splits of the staged GEMM
+  L.rs_col = k % RS_K == 0 && sdc_cdiv(m, 64) * sdc_cdiv(2 * L.nb, 64) >= 64;
+  L.rs_row = k % RS_K == 0 && sdc_cdiv(n, 64) * sdc_cdiv(2 * L.mb, 64) >= 64;
+  L.scol = L.rs_col ? 1 : sdc_expected_splits(m, k, 2 * L.nb);
+  L.srow = L.rs_row ? 1 : sdc_expected_splits(n, k, 2 * L.mb);
   auto al = [](int64_t x) { return (x + 63) / 64 * 64; };
   int64_t o = 0;
-  L.off_parts = o; o += al((3 * 2 * L.mb * L.kp + 1) / 2);
+  // x's block-sum parts: [3][2 mb][kp], or (register-streamed row GEMM) fragment order, whichever is larger
+  L.off_parts = o;
+  o += al(std::max((3 * 2 * L.mb * L.kp + 1) / 2, L.rs_row ? sdc_parts_fragments_bytes(2 * L.mb, k) / 4 : 0));
   L.off_stats = o; o += al(L.nkc * L.mb * NXS);
   L.off_xnp = o; o += al(L.nkc * 2 * m);
   L.off_xn = o; o += al(2 * m);
   L.off_rstat = o; o += al(L.mb * RST);
   L.off_erow = o; o += al(L.srow * 2 * L.mb * n);
   L.off_ecol = o; o += al(L.scol * 2 * L.nb * m);
+  // (the layer's parts in fragment order, made here when the caller passes none)
+  L.off_fcol = o; o += L.rs_col ? al(sdc_parts_fragments_bytes(2 * L.nb, k) / 4) : 0;
   L.total = o;
   return L;
 }
@@ -554,7 +582,7 @@ extern "C" int64_t sdc_linear_check_workspace(int64_t m, int64_t k, int64_t n) {
 
 extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const void* W, int64_t swn, const void* y,
                                 int64_t sym, const void* bias, int64_t m, int64_t k, int64_t n, const void* parts,
-                                int64_t spc, const float* block_consts, const float* w_norms, const float* sign_table,
+                                int64_t spc, const void* parts_frag, const float* block_consts, const float* w_norms, const float* sign_table,
                                 int64_t* state, int64_t* row_result, float z, float abs_floor, void* workspace,
                                 int64_t workspace_bytes, float* col_scores, float* row_scores, int flags,
                                 hipStream_t stream) {
@@ -581,11 +609,22 @@ extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const voi
   gc.m = m; gc.k = k; gc.N = 2 * L.nb; gc.splits = L.scol;
   gc.E = ws + L.off_ecol; gc.XN = nullptr; gc.et = 1;
   gc.prof_name = "col_gemm";
-  int rc = sdc_gemm_launch(SDC_BF16, gc, 1, side);
+  int rc = SDC_EUNSUPPORTED;
+  if (L.rs_col && (parts_frag ||
+                   sdc_parts_fragments(parts, spc, 2 * L.nb, k, ws + L.off_fcol, side) == SDC_OK)) {
+    GemmArgs gf = gc;
+    gf.B = parts_frag ? parts_frag : ws + L.off_fcol;
+    rc = sdc_rs_gemm_launch(SDC_BF16, gf, side);
+  }
+  if (rc == SDC_EUNSUPPORTED) rc = sdc_gemm_launch(SDC_BF16, gc, 1, side);   // (alignment: the staged GEMM)
   if (rc != SDC_OK) return rc;
 
-  // 1. the block sums of x (as three parts), their statistics and x's row norms
+  // 1. the block sums of x (as three parts, in fragment order when the row GEMM is the register-streamed one), their
+  //    statistics and x's row norms
+  const bool rs_row = L.rs_row && swn % 8 == 0 && (uintptr_t)W % 16 == 0;
   XStageArgs xa{};
+  xa.frag = rs_row ? 1 : 0;
+  xa.ncf = sdc_cdiv(2 * L.mb, 32);
   xa.x = (const uint16_t*)x; xa.sxm = sxm; xa.m = m; xa.k = k; xa.kp = L.kp; xa.mb = L.mb; xa.rem = L.rem_m;
   xa.nkc = L.nkc;
   xa.s_full = s_full; xa.s_last = L.rem_m ? sign_table + (L.rem_m - 1) * 128 : s_full;
@@ -612,7 +651,7 @@ extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const voi
   gr.m = n; gr.k = k; gr.N = 2 * L.mb; gr.splits = L.srow;
   gr.E = ws + L.off_erow; gr.XN = nullptr; gr.et = 1; gr.rows_per_xcd = 1;
   gr.prof_name = "row_gemm";
-  rc = sdc_gemm_launch(SDC_BF16, gr, 1, stream);
+  rc = rs_row ? sdc_rs_gemm_launch(SDC_BF16, gr, stream) : sdc_gemm_launch(SDC_BF16, gr, 1, stream);
   if (rc != SDC_OK) return rc;
   if ((rc = sdc_join(stream, fin)) != SDC_OK) return rc;     // (the side stream also holds the concurrent GEMM)
 
@@ -629,7 +668,10 @@ extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const voi
   ya.zt = z; ya.lim_a = 1e18f; ya.lim_big = 1e18f;
   ya.capk = (float)(1.02 + (double)k * 2.384185791015625e-07);
   SdcProf prof("ypass", stream);
-  hipLaunchKernelGGL(ypass_kernel<SDC_BF16>, dim3((unsigned)L.nb, (unsigned)L.mb), dim3(256), 0, stream, ya);
+  if (L.scol == 1 && gr.splits == 1)
+    hipLaunchKernelGGL((ypass_kernel<SDC_BF16, true>), dim3((unsigned)L.nb, (unsigned)L.mb), dim3(256), 0, stream, ya);
+  else
+    hipLaunchKernelGGL((ypass_kernel<SDC_BF16, false>), dim3((unsigned)L.nb, (unsigned)L.mb), dim3(256), 0, stream, ya);
   SDC_LAUNCH_CHECK();
   return SDC_OK;
 }

@@ -56,11 +56,12 @@ def check_linear_both(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torc
     if wn is None or wn.shape != (2, n):
         raise ValueError("the layer's checksums carry no row norms of W (LayerChecksums makes them)")
     L = _lib.lib()
+    frag = _fragments(P, 2 * cs.nb, k)
     nbytes = int(L.sdc_linear_check_workspace(m, k, n))
     ws = _lib.workspace(dev, nbytes)
     rc = L.sdc_linear_check(
         _lib.DT_BF16, x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0), y2.data_ptr(), y2.stride(0),
-        _lib.ptr(bias), m, k, n, P.data_ptr(), P.stride(1), packed.data_ptr(), wn.data_ptr(),
+        _lib.ptr(bias), m, k, n, P.data_ptr(), P.stride(1), _lib.ptr(frag), packed.data_ptr(), wn.data_ptr(),
         sign_table(dev).data_ptr(), state.data_ptr(), row_result.data_ptr(), float(z), float(abs_floor),
         ws.data_ptr(), ws.numel(), _lib.ptr(col_scores), _lib.ptr(row_scores), 1 if concurrent else 0,
         _lib.stream_of(y2))
@@ -70,6 +71,27 @@ def check_linear_both(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torc
         return state, row_result
     _lib.check(rc, "sdc_linear_check")
     return state, row_result
+
+
+def _fragments(P: torch.Tensor, ncols: int, k: int) -> Optional[torch.Tensor]:
+    """The layer's parts in the register-streamed GEMM's fragment order (sdc_parts_fragments), made once and kept on
+    the parts tensor (so they live as long as the constants they copy); None where that GEMM does not apply (depth
+    not a multiple of 256, part columns not 16-byte aligned)."""
+    if k % 256 or P.stride(1) % 8 or P.data_ptr() % 16:
+        return None
+    key = (P.data_ptr(), P._version, ncols, k)
+    hit = getattr(P, "_sdc_frag", None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    L = _lib.lib()
+    out = torch.empty(int(L.sdc_parts_fragments_bytes(ncols, k)) // 2, dtype=torch.int16, device=P.device)
+    _lib.check(L.sdc_parts_fragments(P.data_ptr(), P.stride(1), ncols, k, out.data_ptr(), _lib.stream_of(P)),
+               "sdc_parts_fragments")
+    try:
+        P._sdc_frag = (key, out)
+    except (AttributeError, RuntimeError):
+        pass
+    return out
 
 
 def _separately(x2, weight, bias, y2, cs, z, abs_floor, state, row_result, col_scores, row_scores) -> None:

@@ -59,7 +59,10 @@ def zmax(key) -> float:
 
 
 SHAPES = [(512, 640, 1000, True), (300, 256, 136, False), (129, 1032, 264, True), (1024, 4096, 1408, True),
-          (256, 4104, 512, False), (100, 1030, 264, True)]        # (the last: x rows not 16-byte aligned)
+          (256, 4104, 512, False), (100, 1030, 264, True),        # (x rows not 16-byte aligned)
+          # register-streamed GEMMs (depth a multiple of 512, 64 tiles or more): a ragged checksum-column count,
+          # then a ragged last row block and a row check narrower than its 64-column tile
+          (2048, 1024, 8200, True), (2000, 512, 8200, False)]
 
 
 @pytest.mark.parametrize("m,k,n,with_bias", SHAPES)
