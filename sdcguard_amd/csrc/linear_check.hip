@@ -40,7 +40,7 @@ namespace {
 
 constexpr int BS = 128;            // block width of both checks
 constexpr int RS_K = 256;          // depth multiple of the register-streamed GEMM (expected_gemm.hip)
-constexpr int XK = 256;            // depth per xstage workgroup
+constexpr int XK = 128;            // depth per xstage workgroup
 constexpr int NXS = 5;             // partial stats per (depth chunk, row block): sq0, sq1, max0, max1, max|x|
 constexpr int RST = 8;             // final stats per row block: the NXS above, then the sum of its sign pattern
 
@@ -51,6 +51,18 @@ __device__ __forceinline__ uint16_t bf16_rne(float f) {
   if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
   u += 0x7FFFu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
+}
+
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+// sum over the 16 lanes of a DPP row
+template <int DT>
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_xor1(v);
+  v += dpp_xor2(v);
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // half mirror
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));  // row mirror
+  return v;
 }
 
 // ---------------------------------------------------------------------------------------- 1. x block sums
@@ -68,68 +80,77 @@ struct XStageArgs {
   float* rstat;                    // [mb][RST]: sq0, sq1, max0, max1, max |x|, sum of the block's pattern
 };
 
-// One workgroup: one row block (128 rows) by 256 consecutive depths.  Thread t reads depths 8 (t % 32) .. +8 of
-// rows t / 32 + 8 i (i < 16): sixteen 16-byte loads, a wave covering two rows of 512 contiguous bytes each.  LDS
-// adds the eight row groups' depth sums; thread t then owns depth t: its two sums become three bf16 parts
-// (checksum._split3), stored k-contiguous per checksum column.  The same registers give each row's |x|_2^2 and
-// |x|_1 over the 256 depths (packed dot products; LDS adds the 32 lanes of a row), written per depth chunk for
-// xfinish_kernel to add up.
+// One workgroup: one row block (128 rows) by 128 consecutive depths (32 KB of x).  Thread t = 16 rg + dc reads
+// depths 8 dc .. 8 dc + 7 of rows rg + 16 i (i < 8): eight 16-byte loads, a wave covering four rows of 256
+// contiguous bytes each.  Per row, its |x|_2^2 and |x|_1 over the thread's 8 depths (packed dot products), added
+// over the row's 16 lanes (one DPP row) and written per depth chunk for xfinish_kernel.  Per depth, the plain and
+// signed sums over the thread's 8 rows by packed dot products that pick one half of each word (exact: +-1 times a
+// bf16 value); LDS adds the 16 row groups, and thread t < 128 owns depth t: its two sums become three bf16 parts
+// (checksum._split3), stored k-contiguous per checksum column or in the register-streamed GEMM's fragment order.
+// max |x| of the tile as the packed 16-bit maximum of the magnitudes' bits (NaN above infinity, read as infinity).
 __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
-  __shared__ float red[2][8][XK + 4];
-  __shared__ float nrm[2][BS][33];
+  __shared__ float red[2][16][XK + 4];
   __shared__ float wst[4][NXS];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int dc = t & 31, rg = t >> 5;
+  const int dc = t & 15, rg = t >> 4;
   const int64_t kc = blockIdx.x, ib = blockIdx.y;
   const int64_t k0 = kc * XK + 8 * dc;
   const int wid = (int)((ib == a.mb - 1 && a.rem > 0) ? a.rem : BS);
   const float* sp = (ib == a.mb - 1 && a.rem > 0) ? a.s_last : a.s_full;
   const uint16_t* base = a.x + (ib * BS) * a.sxm + k0;
-  constexpr uint32_t ONES = 0x3F803F80u;
-  float pl[8], sg[8], mx = 0.f, rsq[16], rab[16];
+  constexpr uint32_t ONES = 0x3F803F80u, HI1 = 0x3F800000u;
+  // (1, 0) as a bf16 pair, kept in a register: as an immediate the compiler encodes 0x00003F80 as the inline
+  // constant 1.0, which v_dot2c_f32_bf16 does not read as that pair
+  uint32_t LO1;
+  asm volatile("v_mov_b32 %0, 0x3f80" : "=v"(LO1));
+  float pl[8], sg[8], rsq[8], rab[8];
+  uint32_t mxb = 0;                                // packed max of the magnitudes' bits
 #pragma unroll
-  for (int e = 0; e < 8; ++e) pl[e] = sg[e] = 0.f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) rsq[i] = rab[i] = 0.f;
+  for (int e = 0; e < 8; ++e) pl[e] = sg[e] = rsq[e] = rab[e] = 0.f;
   if (k0 + 8 <= a.k) {
-    // a full block loads unconditionally (a guarded load would make the compiler wait for it inside the guard);
-    // rows past a narrower last block read row 0 of the block and are weighted 0
-    u32x4 v[16];
+    // loads unconditional (a guarded load makes the compiler wait for it inside the guard); rows past a narrower
+    // last block read row 0 of the block and are weighted 0
+    u32x4 v[8];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = rg + 8 * i;
-      v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + (r < wid ? r : 0) * a.sxm));
+    for (int i = 0; i < 8; ++i) {
+      const int r = rg + 16 * i;
+      v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + (int64_t)(r < wid ? r : 0) * a.sxm));
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = rg + 8 * i;
+    for (int i = 0; i < 8; ++i) {
+      const int r = rg + 16 * i;
       const float s = sp[r];                      // (0 past the pattern's width)
       if (r >= wid) v[i] = u32x4{0u, 0u, 0u, 0u};
+      const uint32_t sb = __float_as_uint(s) >> 16;                   // s as bf16 (+-1 or 0: exact)
+      const uint32_t slo = sb, shi = sb << 16;
       const uint32_t ww[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         rsq[i] = dot2<SDC_BF16>(ww[q], ww[q], rsq[i]);
-        rab[i] = dot2<SDC_BF16>(ww[q] & 0x7FFF7FFFu, ONES, rab[i]);
-        const float x0 = bf16_lo(ww[q]), x1 = bf16_hi(ww[q]);
-        pl[2 * q] += x0;
-        pl[2 * q + 1] += x1;
-        sg[2 * q] = fmaf(x0, s, sg[2 * q]);
-        sg[2 * q + 1] = fmaf(x1, s, sg[2 * q + 1]);
-        mx = fmaxf(mx, fmaxf(nan_abs(x0), nan_abs(x1)));
+        const uint32_t mag = ww[q] & 0x7FFF7FFFu;
+        rab[i] = dot2<SDC_BF16>(mag, ONES, rab[i]);
+        mxb = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, mxb),
+                                                                     __builtin_bit_cast(u16x2, mag)));
+        pl[2 * q] = dot2<SDC_BF16>(ww[q], LO1, pl[2 * q]);
+        pl[2 * q + 1] = dot2<SDC_BF16>(ww[q], HI1, pl[2 * q + 1]);
+        sg[2 * q] = dot2<SDC_BF16>(ww[q], slo, sg[2 * q]);
+        sg[2 * q + 1] = dot2<SDC_BF16>(ww[q], shi, sg[2 * q + 1]);
       }
     }
   } else if (k0 < a.k) {
     const int ne = (int)(a.k - k0);
 #pragma unroll 1
-    for (int i = 0; i < 16; ++i) {
-      const int r = rg + 8 * i;
+    for (int i = 0; i < 8; ++i) {
+      const int r = rg + 16 * i;
       if (r >= wid) continue;
       const float s = sp[r];
       for (int e = 0; e < ne; ++e) {
-        const float xv = bf16_lo(base[r * a.sxm + e]);
+        const uint16_t b = base[(int64_t)r * a.sxm + e];
+        const float xv = bf16_lo(b);
         pl[e] += xv;
         sg[e] = fmaf(xv, s, sg[e]);
-        mx = fmaxf(mx, nan_abs(xv));
+        const uint32_t mag = b & 0x7FFFu;
+        mxb = (mxb & 0xFFFFu) >= mag ? mxb : ((mxb & 0xFFFF0000u) | mag);
         rsq[i] = fmaf(xv, xv, rsq[i]);
         rab[i] += fabsf(xv);
       }
@@ -140,58 +161,71 @@ __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
     red[0][rg][8 * dc + e] = pl[e];
     red[1][rg][8 * dc + e] = sg[e];
   }
+  // the row's 16 lanes (a DPP row) add its norms in lane order; lane dc < 8 keeps row rg + 16 dc
+  {
+    float keep_sq = 0.f, keep_ab = 0.f;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    nrm[0][rg + 8 * i][dc] = rsq[i];
-    nrm[1][rg + 8 * i][dc] = rab[i];
+    for (int i = 0; i < 8; ++i) {
+      const float q = row16_sum<SDC_BF16>(rsq[i]), b = row16_sum<SDC_BF16>(rab[i]);
+      if (dc == i) {
+        keep_sq = q;
+        keep_ab = b;
+      }
+    }
+    const int r = rg + 16 * dc;
+    if (dc < 8 && r < wid) {
+      const int64_t row = ib * BS + r;
+      a.xnp[(kc * 2 + 0) * a.m + row] = keep_sq;
+      a.xnp[(kc * 2 + 1) * a.m + row] = keep_ab;
+    }
   }
+  // max |x|: the larger half, as a float (NaN's bits are above infinity's: read as infinity)
+  uint32_t mb16 = (mxb & 0xFFFFu) > (mxb >> 16) ? (mxb & 0xFFFFu) : (mxb >> 16);
+  float mx = mb16 > 0x7F80u ? __builtin_inff() : __uint_as_float(mb16 << 16);
 #pragma unroll
   for (int msk = 1; msk < 64; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
   __syncthreads();
-  float P = 0.f, S = 0.f;
+  float st[4] = {0.f, 0.f, 0.f, 0.f};
+  if (t < XK) {
+    float P = 0.f, S = 0.f;
 #pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    P += red[0][g][t];
-    S += red[1][g][t];
-  }
-  {
-    // this chunk's partial norm of row t / 2 (t % 2: squares, |values|), lanes in depth order
-    const int r = t >> 1, c = t & 1;
-    float acc = 0.f;
+    for (int g = 0; g < 16; ++g) {
+      P += red[0][g][t];
+      S += red[1][g][t];
+    }
+    const int64_t kk = kc * XK + t;
+    const bool mine = kk < a.k;
+    if (kk < a.kp) {
+      // three parts of each sum (hi + mid + lo reproduces it to ~2^-27); depths past k are zero
+      const float v2[2] = {mine ? P : 0.f, mine ? S : 0.f};
 #pragma unroll
-    for (int d = 0; d < 32; ++d) acc += nrm[c][r][d];
-    const int64_t row = ib * BS + r;
-    if (r < wid) a.xnp[(kc * 2 + c) * a.m + row] = acc;
-  }
-  const int64_t kk = kc * XK + t;
-  const bool mine = kk < a.k;
-  if (kk < a.kp) {
-    // three parts of each sum (hi + mid + lo reproduces it to ~2^-27); depths past k are zero
-    const float v2[2] = {mine ? P : 0.f, mine ? S : 0.f};
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const uint16_t h = bf16_rne(v2[c]);
-      const float r1 = v2[c] - bf16_lo(h);
-      const uint16_t md = bf16_rne(r1);
-      const uint16_t lo = bf16_rne(r1 - bf16_lo(md));
-      const int64_t col = 2 * ib + c;
-      if (a.frag) {
-        // element e of lane l of fragment (step s, part p, column fragment f): column 32 f + l % 32, depth
-        // 64 (s / 4) + 32 (l / 32) + 8 (s % 4) + e
-        const int64_t st = 4 * (kk >> 6) + ((kk & 31) >> 3);
-        const int64_t ln = (col & 31) + 32 * ((kk & 63) >> 5);
-        const int64_t base = (st * 3 * a.ncf + (col >> 5)) * 512 + ln * 8 + (kk & 7);
-        a.parts[base] = h;
-        a.parts[base + a.ncf * 512] = md;
-        a.parts[base + 2 * a.ncf * 512] = lo;
-      } else {
-        a.parts[(0 * 2 * a.mb + col) * a.kp + kk] = h;
-        a.parts[(1 * 2 * a.mb + col) * a.kp + kk] = md;
-        a.parts[(2 * 2 * a.mb + col) * a.kp + kk] = lo;
+      for (int c = 0; c < 2; ++c) {
+        const uint16_t h = bf16_rne(v2[c]);
+        const float r1 = v2[c] - bf16_lo(h);
+        const uint16_t md = bf16_rne(r1);
+        const uint16_t lo = bf16_rne(r1 - bf16_lo(md));
+        const int64_t col = 2 * ib + c;
+        if (a.frag) {
+          // element e of lane l of fragment (step s, part p, column fragment f): column 32 f + l % 32, depth
+          // 64 (s / 4) + 32 (l / 32) + 8 (s % 4) + e
+          const int64_t fs = 4 * (kk >> 6) + ((kk & 31) >> 3);
+          const int64_t ln = (col & 31) + 32 * ((kk & 63) >> 5);
+          const int64_t fb = (fs * 3 * a.ncf + (col >> 5)) * 512 + ln * 8 + (kk & 7);
+          a.parts[fb] = h;
+          a.parts[fb + a.ncf * 512] = md;
+          a.parts[fb + 2 * a.ncf * 512] = lo;
+        } else {
+          a.parts[(0 * 2 * a.mb + col) * a.kp + kk] = h;
+          a.parts[(1 * 2 * a.mb + col) * a.kp + kk] = md;
+          a.parts[(2 * 2 * a.mb + col) * a.kp + kk] = lo;
+        }
       }
     }
+    st[0] = mine ? P * P : 0.f;
+    st[1] = mine ? S * S : 0.f;
+    st[2] = mine ? nan_abs(P) : 0.f;
+    st[3] = mine ? nan_abs(S) : 0.f;
   }
-  float st[4] = {mine ? P * P : 0.f, mine ? S * S : 0.f, mine ? nan_abs(P) : 0.f, mine ? nan_abs(S) : 0.f};
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -276,14 +310,6 @@ struct YArgs {
   float u, h, abs_floor, l1c, zt, lim_a, lim_big, capk;
 };
 
-template <int DT>
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp_xor1(v);
-  v += dpp_xor2(v);
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // half mirror
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));  // row mirror
-  return v;
-}
 
 struct Best {
   int64_t key = 0, keyd = 0;
