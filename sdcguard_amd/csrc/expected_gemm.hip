@@ -562,7 +562,8 @@ constexpr int RS_KMULT = 64 * RS_WAVES;       // depth granularity of the regist
 constexpr int RS_RB = 4;                      // B's ring (steps); 8 measured no faster
 constexpr int RS_SEGB = 64 * 128;             // bytes of A per wave and segment (64 rows x 128 bytes)
 
-template <int DT, int RB>
+// ROLE only names the kernel apart (0: the column check's GEMM, 1: the row check's), for per-kernel profiles.
+template <int DT, int RB, int ROLE>
 __global__ __launch_bounds__(64 * RS_WAVES, 1) void rs_gemm_kernel(GemmArgs g) {
   constexpr int TRF = 2, TCF = 2, TR = 64, TC = 64, NG = TRF * TCF * 4;   // f32x4 groups of a wave's accumulators
   constexpr int SPB = RB / 4;                                   // segments per loop iteration (B's ring: RB steps)
@@ -761,9 +762,9 @@ __global__ __launch_bounds__(256) void parts_frag_kernel(const uint16_t* parts, 
 }  // namespace
 
 // The register-streamed GEMM applies to k-contiguous 16-bit A with depth a multiple of 256 and 16-byte rows, B in
-// fragment order (sdc_parts_fragments): one plane of E (transposed), 64 x 64 tiles.  Returns SDC_EUNSUPPORTED
-// otherwise.
-int sdc_rs_gemm_launch(int dtype, GemmArgs g, hipStream_t stream) {
+// fragment order (sdc_parts_fragments): one plane of E (transposed), 64 x 64 tiles; role 0 / 1 (column / row
+// check) only names the kernel.  Returns SDC_EUNSUPPORTED otherwise.
+int sdc_rs_gemm_launch(int dtype, GemmArgs g, int role, hipStream_t stream) {
   if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EUNSUPPORTED;
   if (g.sak != 1 || g.k % RS_KMULT || g.k < RS_KMULT || g.sam % 8 || ((uintptr_t)g.A | (uintptr_t)g.B) % 16 ||
       !g.et || g.goffs)
@@ -773,8 +774,13 @@ int sdc_rs_gemm_launch(int dtype, GemmArgs g, hipStream_t stream) {
   if (tiles > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
   SdcProf prof(g.prof_name ? g.prof_name : "expected_gemm", stream);
   const dim3 grid((unsigned)tiles), block(64 * RS_WAVES);
-  if (dtype == SDC_BF16) hipLaunchKernelGGL((rs_gemm_kernel<SDC_BF16, RS_RB>), grid, block, 0, stream, g);
-  else hipLaunchKernelGGL((rs_gemm_kernel<SDC_FP16, RS_RB>), grid, block, 0, stream, g);
+  if (role == 1) {
+    if (dtype == SDC_BF16) hipLaunchKernelGGL((rs_gemm_kernel<SDC_BF16, RS_RB, 1>), grid, block, 0, stream, g);
+    else hipLaunchKernelGGL((rs_gemm_kernel<SDC_FP16, RS_RB, 1>), grid, block, 0, stream, g);
+  } else {
+    if (dtype == SDC_BF16) hipLaunchKernelGGL((rs_gemm_kernel<SDC_BF16, RS_RB, 0>), grid, block, 0, stream, g);
+    else hipLaunchKernelGGL((rs_gemm_kernel<SDC_FP16, RS_RB, 0>), grid, block, 0, stream, g);
+  }
   SDC_LAUNCH_CHECK();
   return SDC_OK;
 }

@@ -9,6 +9,8 @@
 // One pass, 16 bytes per lane per load, grid-stride; each thread keeps its sums in registers, a wave adds
 // them with shuffles and one lane per wave adds them into the output with 64-bit atomics (wrapping addition,
 // so the result is exact whatever the order).
+#include <type_traits>
+
 #include "common.h"
 #include "profile.h"
 
@@ -164,7 +166,8 @@ unsigned grid_for(int64_t work_items) {
 // and the lane subtracts 128 times the sum of its positions' weights (made once, mod 2^64) from its sums.
 constexpr int KV_WPT = 16;                       // words per lane
 constexpr int KV_SLICE = 64 * KV_WPT;            // positions per wave slice
-constexpr int KV_UNROLL = 4;                     // blocks in flight per wave
+constexpr int KV_UNROLL = 4;                     // (grid sizing) blocks per wave and round
+constexpr int KV_BUF = 3;                        // blocks per register buffer (two buffers in flight)
 
 struct KvArgs {
   const uint8_t* cache;
@@ -226,17 +229,22 @@ __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
 constexpr int KV_WAVES = 4;                      // waves per workgroup: KV_WAVES slices of one block range
 
 template <int WB>
-__global__ __launch_bounds__(64 * KV_WAVES) void kv_fp3_kernel(KvArgs a) {
+__global__ __launch_bounds__(64 * KV_WAVES) void kv_fp3_kernel(KvArgs a, const int64_t* ids) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int64_t p0 = ((int64_t)blockIdx.x * KV_WAVES + w) * KV_SLICE + (int64_t)lane * KV_WPT;
-  // dg[j][c][d]: word pair j (positions p0 + 2j, 2j + 1), weight c, digit d, packed for the dot products
+  // the lane's words: two runs of KV_WPT / 2 at p0 and p0 + KV_SLICE / 2, so that each of a wave's two loads per
+  // block reads one contiguous run (2-byte words: 1 KB; whole lines per instruction)
+  const int64_t p0 = ((int64_t)blockIdx.x * KV_WAVES + w) * KV_SLICE + (int64_t)lane * (KV_WPT / 2);
+  auto pos_of = [&](int q) -> int64_t {                         // position of the lane's word q (0 .. KV_WPT - 1)
+    return p0 + (q < KV_WPT / 2 ? q : KV_SLICE / 2 + q - KV_WPT / 2);
+  };
+  // dg[j][c][d]: word pair j (the lane's words 2j, 2j + 1), weight c, digit d, packed for the dot products
   uint32_t dg[KV_WPT / 2][2][5];
 #pragma unroll
   for (int j = 0; j < KV_WPT / 2; ++j) {
     int32_t e0[2][5], e1[2][5];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const uint64_t z = fp3_z((uint64_t)(p0 + 2 * j + h));
+      const uint64_t z = fp3_z((uint64_t)pos_of(2 * j + h));
       weight_digits(z | 1ull, h ? e1[0] : e0[0]);
       weight_digits((z ^ (z >> 32)) | 1ull, h ? e1[1] : e0[1]);
     }
@@ -245,89 +253,143 @@ __global__ __launch_bounds__(64 * KV_WAVES) void kv_fp3_kernel(KvArgs a) {
 #pragma unroll
       for (int d = 0; d < 5; ++d) dg[j][c][d] = pack16(e0[c][d], e1[c][d]);
   }
-  const int nw = p0 >= a.words ? 0 : (a.words - p0 < KV_WPT ? (int)(a.words - p0) : KV_WPT);
+  // the lane's words that fall inside the block (bit q: word q)
+  uint32_t valid = 0;
+#pragma unroll
+  for (int q = 0; q < KV_WPT; ++q) valid |= (pos_of(q) < a.words ? 1u : 0u) << q;
+  const int nw = __builtin_popcount(valid);
   const bool full = a.vec && nw == KV_WPT;
   // 1-byte words: 128 x the sums of this lane's weights over its positions (the offset of u = v + 128)
   uint64_t corr[2] = {0ull, 0ull};
   if constexpr (WB == 1) {
-    for (int j = 0; j < nw; ++j) {
-      const uint64_t z = fp3_z((uint64_t)(p0 + j));
+    for (int q = 0; q < KV_WPT; ++q) {
+      if (pos_of(q) >= a.words) continue;
+      const uint64_t z = fp3_z((uint64_t)pos_of(q));
       corr[0] += (z | 1ull) << 7;
       corr[1] += ((z ^ (z >> 32)) | 1ull) << 7;
     }
   }
-  for (int64_t i0 = blockIdx.y; i0 < a.n; i0 += (int64_t)gridDim.y * KV_UNROLL) {
-    uint32_t b[KV_UNROLL][KV_WPT / 2];
-    bool live[KV_UNROLL];
+  const int64_t off1 = (int64_t)(KV_SLICE / 2) * WB;            // bytes from the lane's first run to its second
+  // fingerprint of block entry i from this lane's 8 word pairs b[0 .. 7]: the dot products, the wave's sums and
+  // three lanes' atomic additions
+  auto finish = [&](const uint32_t* bw, int64_t i, bool live_i) {
+    int s0 = 0, A[2][3] = {{0, 0, 0}, {0, 0, 0}}, H[2][2] = {{0, 0}, {0, 0}};
 #pragma unroll
-    for (int u = 0; u < KV_UNROLL; ++u) {
-      const int64_t i = i0 + (int64_t)u * gridDim.y;
-      const int64_t blk = i < a.n ? (a.ids ? a.ids[i] : i) : -1;
-      live[u] = blk >= 0 && blk < a.nblocks;
-      const uint8_t* src = a.cache + (live[u] ? blk : 0) * a.block_bytes + (nw ? p0 : 0) * WB;
-      if constexpr (WB == 2) {
-        if (full) {
-          const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-          const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16));
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            b[u][q] = v0[q];
-            b[u][4 + q] = v1[q];
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < KV_WPT / 2; ++j) {
-            const uint32_t lo = 2 * j < nw ? (uint32_t)(src[4 * j] | (src[4 * j + 1] << 8)) : 0u;
-            const uint32_t hi = 2 * j + 1 < nw ? (uint32_t)(src[4 * j + 2] | (src[4 * j + 3] << 8)) : 0u;
-            b[u][j] = lo | (hi << 16);
-          }
-        }
-      } else {
-        if (full) {
-          const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint32_t x = v0[q] ^ 0x80808080u;                 // u = v + 128 in every byte
-            b[u][2 * q] = __builtin_amdgcn_perm(0u, x, 0x0C010C00u);       // bytes 0, 1 -> two 16-bit lanes
-            b[u][2 * q + 1] = __builtin_amdgcn_perm(0u, x, 0x0C030C02u);   // bytes 2, 3
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < KV_WPT / 2; ++j) {
-            const uint32_t lo = 2 * j < nw ? (uint32_t)(src[2 * j] ^ 0x80u) : 0u;
-            const uint32_t hi = 2 * j + 1 < nw ? (uint32_t)(src[2 * j + 1] ^ 0x80u) : 0u;
-            b[u][j] = lo | (hi << 16);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < KV_UNROLL; ++u) {
-      int s0 = 0, A[2][3] = {{0, 0, 0}, {0, 0, 0}}, H[2][2] = {{0, 0}, {0, 0}};
-#pragma unroll
-      for (int j = 0; j < KV_WPT / 2; ++j) {
-        s0 = dot16(b[u][j], 0x00010001u, s0);
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-#pragma unroll
-          for (int d = 0; d < 3; ++d) A[c][d] = dot16(b[u][j], dg[j][c][d], A[c][d]);
-#pragma unroll
-          for (int d = 0; d < 2; ++d) H[c][d] = dot16(b[u][j], dg[j][c][3 + d], H[c][d]);
-        }
-      }
-      uint64_t v[3];
-      if constexpr (WB == 1) s0 -= 128 * nw;
-      v[0] = (uint64_t)(int64_t)wave_sum_i32(s0);
+    for (int j = 0; j < KV_WPT / 2; ++j) {
+      s0 = dot16(bw[j], 0x00010001u, s0);
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const int64_t low = (int64_t)A[c][0] + ((int64_t)A[c][1] << 12) + ((int64_t)A[c][2] << 24);
-        const uint32_t high = (uint32_t)H[c][0] + ((uint32_t)H[c][1] << 16);
-        v[1 + c] = wave_sum_u64((uint64_t)low + ((uint64_t)high << 32) - corr[c]);
+#pragma unroll
+        for (int d = 0; d < 3; ++d) A[c][d] = dot16(bw[j], dg[j][c][d], A[c][d]);
+#pragma unroll
+        for (int d = 0; d < 2; ++d) H[c][d] = dot16(bw[j], dg[j][c][3 + d], H[c][d]);
       }
-      const int64_t i = i0 + (int64_t)u * gridDim.y;
-      if (lane < 3 && live[u])
-        atomicAdd((unsigned long long*)(a.out + 3 * i + lane), (unsigned long long)v[lane == 0 ? 0 : (lane == 1 ? 1 : 2)]);
     }
+    uint64_t v[3];
+    if constexpr (WB == 1) s0 -= 128 * nw;
+    v[0] = (uint64_t)(int64_t)wave_sum_i32(s0);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int64_t low = (int64_t)A[c][0] + ((int64_t)A[c][1] << 12) + ((int64_t)A[c][2] << 24);
+      const uint32_t high = (uint32_t)H[c][0] + ((uint32_t)H[c][1] << 16);
+      v[1 + c] = wave_sum_u64((uint64_t)low + ((uint64_t)high << 32) - corr[c]);
+    }
+    if (lane < 3 && live_i)
+      atomicAdd((unsigned long long*)(a.out + 3 * i + lane), (unsigned long long)v[lane == 0 ? 0 : (lane == 1 ? 1 : 2)]);
+  };
+  // the block of entry i (or -1) and the address of this lane's first run in it
+  auto entry = [&](int64_t i, bool& live_i) {
+    int64_t blk = -1;
+    if (i < a.n) {
+      if (ids) {
+        // a scalar load (i is the same for the whole wave): counted by lgkmcnt, it does not wait behind the blocks'
+        // vector loads in flight
+        const int64_t* ip = ids + i;
+        asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(blk) : "s"(ip) : "memory");
+      } else {
+        blk = i;
+      }
+    }
+    live_i = blk >= 0 && blk < a.nblocks;
+    return a.cache + (live_i ? blk : 0) * a.block_bytes + (nw ? p0 : 0) * WB;
+  };
+  const int64_t G = gridDim.y;
+  // a wave whose every lane is full (the common case: blocks a multiple of the slice) streams blocks with two
+  // register buffers of KV_BUF entries: the next buffer's loads are issued before the current one's dot products
+  const bool wave_full = __builtin_amdgcn_ballot_w64(!full) == 0;
+  if (wave_full) {
+    using Raw = typename std::conditional<WB == 2, u32x4, u32x2>::type;
+    auto load = [&](int64_t i, Raw& r0, Raw& r1, bool& live_i) {
+      const uint8_t* src = entry(i, live_i);
+      r0 = __builtin_nontemporal_load(reinterpret_cast<const Raw*>(src));
+      r1 = __builtin_nontemporal_load(reinterpret_cast<const Raw*>(src + off1));
+    };
+    auto words_of = [&](const Raw& r0, const Raw& r1, uint32_t* bw) {
+      if constexpr (WB == 2) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          bw[q] = r0[q];
+          bw[4 + q] = r1[q];
+        }
+      } else {
+        const uint32_t xs[4] = {r0[0] ^ 0x80808080u, r0[1] ^ 0x80808080u,    // u = v + 128 in every byte
+                                r1[0] ^ 0x80808080u, r1[1] ^ 0x80808080u};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          bw[2 * q] = __builtin_amdgcn_perm(0u, xs[q], 0x0C010C00u);         // bytes 0, 1 -> two 16-bit lanes
+          bw[2 * q + 1] = __builtin_amdgcn_perm(0u, xs[q], 0x0C030C02u);     // bytes 2, 3
+        }
+      }
+    };
+    Raw xa0[KV_BUF], xa1[KV_BUF], xb0[KV_BUF], xb1[KV_BUF];
+    bool la[KV_BUF], lb[KV_BUF];
+    // entries i0 + u G (u < KV_BUF) per buffer; entries past n load entry 0's block again (live false)
+#pragma unroll
+    for (int u = 0; u < KV_BUF; ++u) load((int64_t)blockIdx.y + u * G, xa0[u], xa1[u], la[u]);
+    for (int64_t i0 = blockIdx.y; i0 < a.n; i0 += 2 * KV_BUF * G) {
+      const int64_t i1 = i0 + KV_BUF * G;
+#pragma unroll
+      for (int u = 0; u < KV_BUF; ++u) load(i1 + u * G, xb0[u], xb1[u], lb[u]);
+#pragma unroll
+      for (int u = 0; u < KV_BUF; ++u) {
+        uint32_t bw[KV_WPT / 2];
+        words_of(xa0[u], xa1[u], bw);
+        finish(bw, i0 + u * G, la[u]);
+      }
+      if (i1 >= a.n) break;
+#pragma unroll
+      for (int u = 0; u < KV_BUF; ++u) load(i1 + KV_BUF * G + u * G, xa0[u], xa1[u], la[u]);
+#pragma unroll
+      for (int u = 0; u < KV_BUF; ++u) {
+        uint32_t bw[KV_WPT / 2];
+        words_of(xb0[u], xb1[u], bw);
+        finish(bw, i1 + u * G, lb[u]);
+      }
+    }
+    return;
+  }
+  // otherwise (some of the wave's words fall past the block's end, or unaligned blocks): guarded loads
+  for (int64_t i0 = blockIdx.y; i0 < a.n; i0 += G) {
+    bool live_i;
+    const uint8_t* src = entry(i0, live_i);
+    uint32_t bw[KV_WPT / 2];
+#pragma unroll
+    for (int j = 0; j < KV_WPT / 2; ++j) {
+      uint32_t hv[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int q = 2 * j + e;
+        if constexpr (WB == 2) {
+          const uint8_t* wp = src + (q < KV_WPT / 2 ? 2 * q : off1 + 2 * (q - KV_WPT / 2));
+          hv[e] = (valid >> q) & 1u ? (uint32_t)(wp[0] | (wp[1] << 8)) : 0u;
+        } else {
+          const uint8_t* wp = src + (q < KV_WPT / 2 ? q : off1 + q - KV_WPT / 2);
+          hv[e] = (valid >> q) & 1u ? (uint32_t)(wp[0] ^ 0x80u) : 0u;
+        }
+      }
+      bw[j] = hv[0] | (hv[1] << 16);
+    }
+    finish(bw, i0, live_i);
   }
 }
 
@@ -391,9 +453,9 @@ extern "C" int sdc_kv_fingerprint(const void* cache, int64_t nblocks, int64_t bl
   if (gy > 65535) gy = 65535;
   SdcProf prof("kv_fingerprint", stream);
   if (word_bytes == 2)
-    hipLaunchKernelGGL(kv_fp3_kernel<2>, dim3((unsigned)gx, (unsigned)gy), dim3(64 * KV_WAVES), 0, stream, a);
+    hipLaunchKernelGGL(kv_fp3_kernel<2>, dim3((unsigned)gx, (unsigned)gy), dim3(64 * KV_WAVES), 0, stream, a, ids);
   else
-    hipLaunchKernelGGL(kv_fp3_kernel<1>, dim3((unsigned)gx, (unsigned)gy), dim3(64 * KV_WAVES), 0, stream, a);
+    hipLaunchKernelGGL(kv_fp3_kernel<1>, dim3((unsigned)gx, (unsigned)gy), dim3(64 * KV_WAVES), 0, stream, a, ids);
   SDC_LAUNCH_CHECK();
   return SDC_OK;
 }

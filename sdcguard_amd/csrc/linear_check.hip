@@ -32,7 +32,7 @@
 
 extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
 int sdc_gemm_launch(int dtype, GemmArgs g, int64_t batches, hipStream_t stream);
-int sdc_rs_gemm_launch(int dtype, GemmArgs g, hipStream_t stream);
+int sdc_rs_gemm_launch(int dtype, GemmArgs g, int role, hipStream_t stream);
 extern "C" int64_t sdc_parts_fragments_bytes(int64_t N, int64_t k);
 extern "C" int sdc_parts_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out, hipStream_t stream);
 
@@ -640,7 +640,7 @@ extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const voi
                    sdc_parts_fragments(parts, spc, 2 * L.nb, k, ws + L.off_fcol, side) == SDC_OK)) {
     GemmArgs gf = gc;
     gf.B = parts_frag ? parts_frag : ws + L.off_fcol;
-    rc = sdc_rs_gemm_launch(SDC_BF16, gf, side);
+    rc = sdc_rs_gemm_launch(SDC_BF16, gf, 0, side);
   }
   if (rc == SDC_EUNSUPPORTED) rc = sdc_gemm_launch(SDC_BF16, gc, 1, side);   // (alignment: the staged GEMM)
   if (rc != SDC_OK) return rc;
@@ -677,7 +677,7 @@ extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const voi
   gr.m = n; gr.k = k; gr.N = 2 * L.mb; gr.splits = L.srow;
   gr.E = ws + L.off_erow; gr.XN = nullptr; gr.et = 1; gr.rows_per_xcd = 1;
   gr.prof_name = "row_gemm";
-  rc = rs_row ? sdc_rs_gemm_launch(SDC_BF16, gr, stream) : sdc_gemm_launch(SDC_BF16, gr, 1, stream);
+  rc = rs_row ? sdc_rs_gemm_launch(SDC_BF16, gr, 1, stream) : sdc_gemm_launch(SDC_BF16, gr, 1, stream);
   if (rc != SDC_OK) return rc;
   if ((rc = sdc_join(stream, fin)) != SDC_OK) return rc;     // (the side stream also holds the concurrent GEMM)
 
