@@ -248,7 +248,9 @@ __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
 
 // The depth chunks' partials of one row block added up in chunk order (so the result is the same on every run):
 // the rows' |x|_2^2 and |x|_1 (thread t: row t / 2, t % 2 the statistic), the block sums' statistics (wave 1), the
-// sum of the block's sign pattern (wave 2).
+// sum of the block's sign pattern (wave 2).  Each thread has XF_BATCH chunks' loads in flight at once (its time is
+// the loads' latency, not their bytes).
+constexpr int XF_BATCH = 32;
 __global__ __launch_bounds__(256) void xfinish_kernel(XStageArgs a) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t ib = blockIdx.x;
@@ -258,12 +260,12 @@ __global__ __launch_bounds__(256) void xfinish_kernel(XStageArgs a) {
     const int r = t >> 1, c = t & 1;
     const int64_t row = ib * BS + (r < wid ? r : 0);
     float acc = 0.f;
-    for (int64_t q0 = 0; q0 < a.nkc; q0 += 8) {
-      float p[8];
+    for (int64_t q0 = 0; q0 < a.nkc; q0 += XF_BATCH) {
+      float p[XF_BATCH];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) p[j] = a.xnp[((q0 + j < a.nkc ? q0 + j : a.nkc - 1) * 2 + c) * a.m + row];
+      for (int j = 0; j < XF_BATCH; ++j) p[j] = a.xnp[((q0 + j < a.nkc ? q0 + j : a.nkc - 1) * 2 + c) * a.m + row];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < XF_BATCH; ++j)
         if (q0 + j < a.nkc) acc += p[j];
     }
     if (r < wid) a.xn[c * a.m + row] = acc;
@@ -271,12 +273,13 @@ __global__ __launch_bounds__(256) void xfinish_kernel(XStageArgs a) {
   if (w == 1) {
     const int i = lane < NXS ? lane : 0;
     float v = 0.f;
-    for (int64_t q0 = 0; q0 < a.nkc; q0 += 8) {
-      float p[8];
+    for (int64_t q0 = 0; q0 < a.nkc; q0 += XF_BATCH) {
+      float p[XF_BATCH];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) p[j] = a.stats[((q0 + j < a.nkc ? q0 + j : a.nkc - 1) * a.mb + ib) * NXS + i];
+      for (int j = 0; j < XF_BATCH; ++j)
+        p[j] = a.stats[((q0 + j < a.nkc ? q0 + j : a.nkc - 1) * a.mb + ib) * NXS + i];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < XF_BATCH; ++j)
         if (q0 + j < a.nkc) v = i < 2 ? v + p[j] : fmaxf(v, p[j]);
     }
     if (lane < NXS) a.rstat[ib * RST + lane] = v;
