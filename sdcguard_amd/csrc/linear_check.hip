@@ -343,7 +343,7 @@ __device__ __forceinline__ uint32_t pack_signs(float s0, float s1) {
 // ONE: both checks' E come as one plane each (the register-streamed GEMMs), else up to SDC_MAX_SPLITS planes to add
 template <int DT, bool ONE>
 __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
-  __shared__ f32x4 colp[BS][17];                // column partials [column][row group, rotated], padded
+  __shared__ f32x4 colw[4][2][64];              // each wave's column sums [wave][column parity][lane]
   __shared__ f32x4 rows[BS];                    // the tile's row sums
   __shared__ int64_t red_k[4], red_d[4];
   __shared__ int red_u[4];
@@ -455,10 +455,27 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
       cs[2 * q + 1][3] = dot2<DT>(phi & 0x7FFF7FFFu, ONES, cs[2 * q + 1][3]);
     }
   }
-  // column partials into LDS, the row-group slot rotated by the column group so the eight lanes of a write phase
-  // (columns 8 apart) fall in different banks; the reader adds all 16 slots
+  // the four row groups of the wave (lanes cg, cg + 16, cg + 32, cg + 48) add their column sums by lane swaps:
+  // permlane32_swap pairs lanes q and q + 2, permlane16_swap then q and q + 1; value i = 4 e + s of lane (q, cg)
+  // ends as the wave's sum of value i + 8 q, so lane (q, cg) holds the four sums of columns 8 cg + 2 q (u[0 .. 3])
+  // and 8 cg + 2 q + 1 (u[4 .. 7]).  Into LDS by lane (consecutive 16-byte slots); the reader adds the four waves.
+  {
+    float t1[16], u[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) colp[8 * cg + e][(rg + cg) & 15] = f32x4{cs[e][0], cs[e][1], cs[e][2], cs[e][3]};
+    for (int j = 0; j < 16; ++j) {
+      const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(cs[j / 4][j % 4]),
+                                                      __float_as_uint(cs[(j + 16) / 4][j % 4]), false, false);
+      t1[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(t1[j]), __float_as_uint(t1[j + 8]), false,
+                                                      false);
+      u[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    colw[w][0][lane] = f32x4{u[0], u[1], u[2], u[3]};
+    colw[w][1][lane] = f32x4{u[4], u[5], u[6], u[7]};
+  }
   // the 16 lanes of a row group add their row sums; lane cg < 8 keeps row 8 rg + cg
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -500,10 +517,12 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
     // row-block check of column J, row block ib (training flavour, y^T = W x^T + b)
     const int cc = 64 * (w - 2) + lane;
     if (cc < wc) {
+      // column cc = 8 cg + 2 q + parity sits at lane 16 q + cg of every wave's slot
+      const int cl = 16 * ((cc & 7) >> 1) + (cc >> 3), par = cc & 1;
       float pl = 0.f, sg = 0.f, sq = 0.f, ab = 0.f;
 #pragma unroll
-      for (int g = 0; g < 16; ++g) {
-        const f32x4 q = colp[cc][g];
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 q = colw[g][par][cl];
         pl += q.x; sg += q.y; sq += q.z; ab += q.w;
       }
       const float wf = (float)wr;
