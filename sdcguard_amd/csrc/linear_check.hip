@@ -85,11 +85,12 @@ struct XStageArgs {
 // contiguous bytes each.  Per row, its |x|_2^2 and |x|_1 over the thread's 8 depths (packed dot products), added
 // over the row's 16 lanes (one DPP row) and written per depth chunk for xfinish_kernel.  Per depth, the plain and
 // signed sums over the thread's 8 rows by packed dot products that pick one half of each word (exact: +-1 times a
-// bf16 value); LDS adds the 16 row groups, and thread t < 128 owns depth t: its two sums become three bf16 parts
+// bf16 value); lane swaps add the four row groups of a wave and LDS the four waves, and thread t < 128 owns depth
+// t: its two sums become three bf16 parts
 // (checksum._split3), stored k-contiguous per checksum column or in the register-streamed GEMM's fragment order.
 // max |x| of the tile as the packed 16-bit maximum of the magnitudes' bits (NaN above infinity, read as infinity).
 __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
-  __shared__ float red[2][16][XK + 4];
+  __shared__ f32x4 red[4][4][16];                 // each wave's depth sums [wave][lane / 16][lane % 16]
   __shared__ float wst[4][NXS];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int dc = t & 15, rg = t >> 4;
@@ -156,10 +157,24 @@ __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
       }
     }
   }
+  // the wave's four row groups (lanes dc, dc + 16, dc + 32, dc + 48) add their depth sums by lane swaps:
+  // permlane32_swap pairs lanes q and q + 2, permlane16_swap then q and q + 1; value i of lane (q, dc) (pl[0 .. 7],
+  // then sg[0 .. 7]) ends as the wave's sum of value i + 4 q, so lane (q, dc) holds depths 8 dc + 4 (q % 2) .. + 3
+  // of the plain (q < 2) or signed (q >= 2) sums
+  {
+    float t1[8], u[4];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    red[0][rg][8 * dc + e] = pl[e];
-    red[1][rg][8 * dc + e] = sg[e];
+    for (int j = 0; j < 8; ++j) {
+      const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(pl[j]), __float_as_uint(sg[j]), false, false);
+      t1[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(t1[j]), __float_as_uint(t1[j + 4]), false,
+                                                      false);
+      u[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    red[w][lane >> 4][lane & 15] = f32x4{u[0], u[1], u[2], u[3]};
   }
   // the row's 16 lanes (a DPP row) add its norms in lane order; lane dc < 8 keeps row rg + 16 dc
   {
@@ -187,11 +202,14 @@ __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
   __syncthreads();
   float st[4] = {0.f, 0.f, 0.f, 0.f};
   if (t < XK) {
+    // depth t = 8 dc + e: plain sums at slot (e / 4, dc), signed at (2 + e / 4, dc), element e % 4
+    const float* rf = reinterpret_cast<const float*>(&red[0][0][0]);
+    const int e4 = (t & 7) >> 2, dcr = t >> 3, ec = t & 3;
     float P = 0.f, S = 0.f;
 #pragma unroll
-    for (int g = 0; g < 16; ++g) {
-      P += red[0][g][t];
-      S += red[1][g][t];
+    for (int g = 0; g < 4; ++g) {
+      P += rf[((g * 4 + e4) * 16 + dcr) * 4 + ec];
+      S += rf[((g * 4 + 2 + e4) * 16 + dcr) * 4 + ec];
     }
     const int64_t kk = kc * XK + t;
     const bool mine = kk < a.k;
