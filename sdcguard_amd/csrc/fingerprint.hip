@@ -9,6 +9,8 @@
 // One pass, 16 bytes per lane per load, grid-stride; each thread keeps its sums in registers, a wave adds
 // them with shuffles and one lane per wave adds them into the output with 64-bit atomics (wrapping addition,
 // so the result is exact whatever the order).
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -393,6 +395,228 @@ __global__ __launch_bounds__(64 * KV_WAVES) void kv_fp3_kernel(KvArgs a, const i
   }
 }
 
+// ------------------------------------------------------------------------------------------- MFMA fingerprints
+// The weighted sums of 2-byte words as int8 matrix products: C[r][b] = sum over the bytes q of block b of
+// T[r][q] * D[q][b], on v_mfma_i32_32x32x32_i8.  D is the block's bytes (low bytes with their top bit flipped:
+// lo - 128, exact as int8; high bytes are the word's signed high half).  T (the weight table) holds, for weight c
+// (w1, w2) and digit d (each weight as eight balanced base-256 digits, sum dig_d 256^d = w mod 2^64), row
+// 8 c + d: dig_d(w_c(p)) at the low byte of word p and dig_{d-1}(w_c(p)) at its high byte, so that
+//   sum_p word_p w_c(p) = sum_d 256^d C[8 c + d] + 128 sum_p w_c(p)          (mod 2^64; 256^8 = 0)
+// and rows 16 / 17 (ones at the low / high bytes) give sum_p word_p = C[16] + 256 C[17] + 128 (number of words).
+// Every product is at most 2^14 in magnitude and a wave adds at most 2^15 of them per row: exact in int32.
+// T is the same for every block: a table in the MFMA's operand order, made once per device, with the prefix sums
+// of 128 w_c(p) (the low bytes' offset) per 16 words.
+constexpr int KVM_MAXW = 32768;                  // words per block the table covers
+constexpr int KVM_STEPS = KVM_MAXW * 2 / 32;     // 32-byte steps of a block (one MFMA each)
+constexpr int KVM_ENT = 64;                      // block entries per workgroup: two 32-column tiles per wave
+__device__ __attribute__((aligned(256))) uint8_t kvm_tab[KVM_STEPS * 1024];
+__device__ __attribute__((aligned(256))) uint64_t kvm_corr[2 * (KVM_STEPS + 1)];
+
+// balanced base-256 digit d of w (in [-128, 128))
+__device__ __forceinline__ int bdig8(uint64_t w, int d) {
+  uint64_t v = w;
+  int dig = 0;
+  for (int i = 0; i <= d; ++i) {
+    const int b = (int)(v & 0xFFu);
+    dig = b >= 128 ? b - 256 : b;
+    v = (v - (uint64_t)(int64_t)dig) >> 8;
+  }
+  return dig;
+}
+
+__device__ __forceinline__ uint64_t kvm_weight(uint64_t p, int c) {
+  const uint64_t z = fp3_z(p);
+  return c ? ((z ^ (z >> 32)) | 1ull) : (z | 1ull);
+}
+
+// table step s (bytes 32 s .. 32 s + 31), lane l: row l % 32, bytes 16 (l / 32) .. + 15 of the step: the A operand
+// of the step's MFMA, 1 KB per step with lane l's 16 bytes at 16 l
+__global__ __launch_bounds__(64) void kvm_fill_kernel(uint8_t* tab) {
+  const int s = blockIdx.x, l = threadIdx.x, r = l & 31, h = l >> 5;
+  uint32_t out[4] = {0u, 0u, 0u, 0u};
+  for (int j = 0; j < 16; ++j) {
+    const int64_t q = 32 * (int64_t)s + 16 * h + j;
+    const uint64_t p = (uint64_t)(q >> 1);
+    const int hb = (int)(q & 1);
+    int v = 0;
+    if (r < 16) {
+      const int c = r >> 3, d = r & 7;
+      const uint64_t wt = kvm_weight(p, c);
+      v = hb == 0 ? bdig8(wt, d) : (d > 0 ? bdig8(wt, d - 1) : 0);
+    } else if (r == 16) {
+      v = hb == 0 ? 1 : 0;
+    } else if (r == 17) {
+      v = hb == 1 ? 1 : 0;
+    }
+    out[j >> 2] |= ((uint32_t)v & 0xFFu) << (8 * (j & 3));
+  }
+  *reinterpret_cast<u32x4*>(tab + (int64_t)s * 1024 + 16 * l) = u32x4{out[0], out[1], out[2], out[3]};
+}
+
+// corr[c (KVM_STEPS + 1) + s] = sum over words p < 16 s of 128 w_c(p) (mod 2^64): one workgroup, thread t the
+// steps 8 t .. 8 t + 7, a serial scan of the 256 threads' totals
+__global__ __launch_bounds__(256) void kvm_corr_kernel(uint64_t* corr) {
+  __shared__ uint64_t tot[2][256];
+  const int t = threadIdx.x;
+  uint64_t st[2][8];
+  for (int c = 0; c < 2; ++c) {
+    uint64_t sum = 0;
+    for (int k = 0; k < 8; ++k) {
+      uint64_t v = 0;
+      for (int j = 0; j < 16; ++j) v += kvm_weight((uint64_t)(16 * (8 * t + k) + j), c);
+      st[c][k] = v << 7;
+      sum += st[c][k];
+    }
+    tot[c][t] = sum;
+  }
+  __syncthreads();
+  if (t < 2) {
+    uint64_t run = 0;
+    for (int i = 0; i < 256; ++i) {
+      const uint64_t v = tot[t][i];
+      tot[t][i] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  for (int c = 0; c < 2; ++c) {
+    uint64_t run = tot[c][t];
+    for (int k = 0; k < 8; ++k) {
+      corr[c * (KVM_STEPS + 1) + 8 * t + k] = run;
+      run += st[c][k];
+    }
+    if (t == 255) corr[c * (KVM_STEPS + 1) + KVM_STEPS] = run;
+  }
+}
+
+// Workgroup: entries e0 .. e0 + 63; wave w: the w-th quarter of each block's 128-byte chunks.  Per chunk, each lane
+// loads 8 pieces of 16 bytes (load i: entry 8 i + lane / 8, piece lane % 8: whole lines), flips the low bytes' top
+// bits and stores them to the wave's LDS tile (entry row of 128 bytes, piece j at slot j ^ (row % 8)); then per
+// 32-byte step s and column tile u, lane l reads row 32 u + l % 32, piece 2 s + l / 32 (the B operand) and the
+// MFMA takes the table's step (the A operand) against it.  Chunks alternate between two register sets, the next
+// one's loads issued before the current one is stored.
+__global__ __launch_bounds__(256) void kv_mfma_kernel(KvArgs a, const int64_t* ids, const uint8_t* tab,
+                                                      const uint64_t* corr) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[4][KVM_ENT * 128];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t e0 = (int64_t)blockIdx.x * KVM_ENT;
+  const int64_t chunks = a.words / 64;
+  const int64_t per = (chunks + 3) / 4;
+  const int64_t c0 = w * per < chunks ? w * per : chunks;
+  const int64_t c1 = c0 + per < chunks ? c0 + per : chunks;
+  const uint8_t* src[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t ent = e0 + 8 * i + (lane >> 3);
+    int64_t blk = -1;
+    if (ent < a.n) blk = ids ? ids[ent] : ent;
+    const bool live = blk >= 0 && blk < a.nblocks;
+    src[i] = a.cache + (live ? blk : 0) * a.block_bytes + 16 * (lane & 7);
+  }
+  uint8_t* const L = lds[w];
+  i32x16 acc[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[u][e] = 0;
+  auto load = [&](int64_t c, u32x4* d, i32x4* tf) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) d[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src[i] + 128 * c));
+#pragma unroll
+    for (int s = 0; s < 4; ++s) tf[s] = *reinterpret_cast<const i32x4*>(tab + (4 * c + s) * 1024 + 16 * lane);
+  };
+  const int wslot = (lane & 7) ^ (lane >> 3);                  // load i's piece lane % 8 of row 8 i + lane / 8
+  auto process = [&](const u32x4* d, const i32x4* tf) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const u32x4 x = d[i] ^ u32x4{0x00800080u, 0x00800080u, 0x00800080u, 0x00800080u};
+      *reinterpret_cast<u32x4*>(L + (8 * i + (lane >> 3)) * 128 + 16 * wslot) = x;
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int row = 32 * u + (lane & 31), piece = 2 * s + (lane >> 5);
+        const i32x4 b = *reinterpret_cast<const i32x4*>(L + row * 128 + 16 * (piece ^ (row & 7)));
+        acc[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(tf[s], b, acc[u], 0, 0, 0);
+      }
+  };
+  if (c0 < c1) {
+    u32x4 da[8], db[8];
+    i32x4 ta[4], tb[4];
+    load(c0, da, ta);
+    for (int64_t c = c0; c < c1; c += 2) {
+      if (c + 1 < c1) load(c + 1, db, tb);
+      process(da, ta);
+      if (c + 1 >= c1) break;
+      if (c + 2 < c1) load(c + 2, da, ta);
+      process(db, tb);
+    }
+  }
+  // lane l holds column (entry) 32 u + l % 32 of tile u, rows 8 (e / 4) + 4 (l / 32) + e % 4 of its 16 values
+  const int h = lane >> 5;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    uint64_t v1 = 0, v2 = 0, v0 = 0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int r = 8 * (e >> 2) + 4 * h + (e & 3);
+      const uint64_t x = (uint64_t)(int64_t)acc[u][e];
+      if (r < 8) v1 += x << (8 * r);
+      else if (r < 16) v2 += x << (8 * (r - 8));
+      else if (r == 16) v0 += x;
+      else if (r == 17) v0 += x << 8;
+    }
+    if (h == 0) {
+      v0 += (uint64_t)(128 * 64) * (uint64_t)(c1 - c0);
+      v1 += corr[4 * c1] - corr[4 * c0];
+      v2 += corr[(KVM_STEPS + 1) + 4 * c1] - corr[(KVM_STEPS + 1) + 4 * c0];
+    }
+    const int64_t ent = e0 + 32 * u + (lane & 31);
+    int64_t blk = -1;
+    if (ent < a.n) blk = ids ? ids[ent] : ent;
+    if (blk >= 0 && blk < a.nblocks && c0 < c1) {
+      int64_t* o = a.out + 3 * ent;
+      if (h == 0) atomicAdd((unsigned long long*)o, (unsigned long long)v0);
+      atomicAdd((unsigned long long*)(o + 1), (unsigned long long)v1);
+      atomicAdd((unsigned long long*)(o + 2), (unsigned long long)v2);
+    }
+  }
+}
+
+constexpr int KVM_MAXDEV = 64;
+std::atomic<const uint8_t*> g_kvm_tab[KVM_MAXDEV];
+std::atomic<const uint64_t*> g_kvm_corr[KVM_MAXDEV];
+std::mutex g_kvm_mu;
+
+// This device's weight table and corrections, made at the first call on the device (which waits for them); false
+// when they are not there and cannot be made now (the stream is being captured, or a HIP error)
+bool kvm_tables(hipStream_t stream, const uint8_t** tab, const uint64_t** corr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= KVM_MAXDEV) return false;
+  const uint8_t* tp = g_kvm_tab[dev].load(std::memory_order_acquire);
+  if (!tp) {
+    std::lock_guard<std::mutex> lk(g_kvm_mu);
+    tp = g_kvm_tab[dev].load(std::memory_order_relaxed);
+    if (!tp) {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+      void *pt = nullptr, *pc = nullptr;
+      if (hipGetSymbolAddress(&pt, HIP_SYMBOL(kvm_tab)) != hipSuccess || !pt) return false;
+      if (hipGetSymbolAddress(&pc, HIP_SYMBOL(kvm_corr)) != hipSuccess || !pc) return false;
+      hipLaunchKernelGGL(kvm_fill_kernel, dim3(KVM_STEPS), dim3(64), 0, stream, (uint8_t*)pt);
+      hipLaunchKernelGGL(kvm_corr_kernel, dim3(1), dim3(256), 0, stream, (uint64_t*)pc);
+      if (hipGetLastError() != hipSuccess || hipStreamSynchronize(stream) != hipSuccess) return false;
+      g_kvm_corr[dev].store((const uint64_t*)pc, std::memory_order_relaxed);
+      g_kvm_tab[dev].store((const uint8_t*)pt, std::memory_order_release);
+      tp = (const uint8_t*)pt;
+    }
+  }
+  *tab = tp;
+  *corr = g_kvm_corr[dev].load(std::memory_order_relaxed);
+  return true;
+}
+
 }  // namespace
 
 // out[3] (int64, zeroed by the caller) += fp3 of n words of word_bytes (2 or 1) bytes at bits, positions from start
@@ -451,6 +675,15 @@ extern "C" int sdc_kv_fingerprint(const void* cache, int64_t nblocks, int64_t bl
   int64_t gy = sdc_cdiv(2048, gx);
   if (gy > sdc_cdiv(n, KV_UNROLL)) gy = sdc_cdiv(n, KV_UNROLL);
   if (gy > 65535) gy = 65535;
+  // 2-byte words in whole 128-byte chunks, aligned, within the table: the MFMA kernel
+  const uint8_t* tab = nullptr;
+  const uint64_t* corr = nullptr;
+  if (word_bytes == 2 && a.vec && words % 64 == 0 && words <= KVM_MAXW && kvm_tables(stream, &tab, &corr)) {
+    SdcProf prof("kv_fingerprint", stream);
+    hipLaunchKernelGGL(kv_mfma_kernel, dim3((unsigned)sdc_cdiv(n, KVM_ENT)), dim3(256), 0, stream, a, ids, tab, corr);
+    SDC_LAUNCH_CHECK();
+    return SDC_OK;
+  }
   SdcProf prof("kv_fingerprint", stream);
   if (word_bytes == 2)
     hipLaunchKernelGGL(kv_fp3_kernel<2>, dim3((unsigned)gx, (unsigned)gy), dim3(64 * KV_WAVES), 0, stream, a, ids);

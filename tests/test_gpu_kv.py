@@ -49,6 +49,31 @@ def test_odd_sized_and_strided_blocks():
     assert np.array_equal(fp2, ref2)
 
 
+def test_whole_chunk_blocks_extremes_and_padding():
+    """Blocks of whole 64-word chunks, 16-byte aligned (the int8 matrix-core kernel): 320 words (five chunks, so a
+    workgroup's four waves take 2, 2, 1 and none), 64 and 32768 words (the table's limit), blocks of words at the
+    int16 extremes, entry counts that are not multiples of 64, dead and repeated entries, and blocks padded apart
+    in memory (2048 words at a stride of 3072)."""
+    from sdcguard_amd.kv import block_fingerprints
+    g = torch.Generator(device="cuda").manual_seed(4)
+    for words, nblk in ((320, 70), (64, 130), (32768, 67)):
+        raw = torch.randint(-32768, 32768, (nblk, words), generator=g, device="cuda", dtype=torch.int32)
+        raw = raw.to(torch.int16)
+        raw[0] = -32768
+        raw[1] = 32767
+        raw[2] = 0
+        ref = F.kv_block_fp3(raw.cpu().numpy())
+        assert np.array_equal(block_fingerprints(raw).cpu().numpy(), ref), words
+        ids = torch.tensor([nblk - 1, -1, 0, 1, nblk, 2, 0], device="cuda")
+        fi = block_fingerprints(raw, ids).cpu().numpy()
+        assert np.array_equal(fi[[0, 2, 3, 5, 6]], ref[[nblk - 1, 0, 1, 2, 0]]), words
+        assert not fi[[1, 4]].any()
+    base = torch.randn(9, 3, 1024, device="cuda", generator=g).bfloat16()
+    padded = base[:, :2]
+    ref = F.kv_block_fp3(padded.contiguous().view(torch.int16).cpu().numpy())
+    assert np.array_equal(block_fingerprints(padded).cpu().numpy(), ref)
+
+
 def test_ledger_catches_stale_blocks_and_bit_flips():
     from sdcguard_amd.kv import KVLedger
     cache = _cache(64, hkv=4, n=16, d=64, seed=2)
