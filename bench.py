@@ -579,7 +579,7 @@ def bench_kv(ctx: Ctx, kv) -> dict:
     ms = ctx.loop_ms(run, steps)
     km = ctx.kernel_ms(run, steps, ("kv_fingerprint",))
     alg = cache.numel() * 2
-    ent, roof = _roof(km, {"kv_fingerprint": ("hbm", alg, None)}, name, {"kv_fingerprint": r"kv_fp"}, steps)
+    ent, roof = _roof(km, {"kv_fingerprint": ("hbm", alg, None)}, name, {"kv_fingerprint": r"kv_mfma_kernel"}, steps)
     value = alg / (ms * 1e-3) / 1e9
     line = {"metric": "KV block fingerprint GB/s (% of HBM peak), 1 GPU", "value": round(value, 2), "unit": "GB/s",
             "ms_per_step": round(ms, 5), "dtype": "u16", "hbm_frac": round(value / HBM_PEAK_GBS, 4),
