@@ -399,7 +399,8 @@ def bench_quant(ctx: Ctx, kind: str, m: int, k: int, n: int, name: str, seed: in
     alg = ab + cb + pb + sc
     amounts = {gname: ("mfma", 2.0 * m * k * consts.parts.shape[0] * consts.parts.shape[1], kind),
                sname: ("hbm", cb, None)}
-    patterns = {gname: r"expected_gemm_kernel<" + ("3" if kind == "int8" else "2"), sname: r"quant_score"}
+    patterns = {gname: r"expected_gemm_kernel<" + ("3" if kind == "int8" else "2"),
+                sname: r"quant_(tile|score)_kernel<" + ("0" if kind == "int8" else "1")}
     ent, roof = _roof(km, amounts, name, patterns, a.steps)
     value = alg / (ms * 1e-3) / 1e9
     gemm_ms = None

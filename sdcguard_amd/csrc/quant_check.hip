@@ -263,7 +263,9 @@ __device__ __forceinline__ int64_t sum16_i64(int64_t v) {
   return v;
 }
 
-template <int KIND, int CT>
+// FEW: at most SDC_MAX_SPLITS depth splits (the launch picks the instance: each holds only its own way of adding
+// the splits, which measured faster than one kernel holding both)
+template <int KIND, int CT, bool FEW>
 __global__ __launch_bounds__(256) void quant_tile_kernel(QuantArgs a) {
   constexpr int ES = CT == C_BF16 ? 2 : 4;                  // bytes per C element
   constexpr int NL = 8 * ES / 16;                           // 16-byte loads per row piece (1 or 2)
@@ -300,23 +302,62 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(QuantArgs a) {
   double e0 = 0.0, e1 = 0.0;
   int64_t i0 = 0, i1 = 0;
   if (w == 0) {
+    // up to SDC_MAX_SPLITS splits: every split's loads issued at once (an index past a.splits reads split 0 and is
+    // not added), then added in split order; more splits (short fp8 GEMMs): four at a time
     if constexpr (KIND == 0) {
       const int32_t* E = reinterpret_cast<const int32_t*>(a.E);
+      if constexpr (FEW) {
+        int32_t hv[SDC_MAX_SPLITS][2], lv[SDC_MAX_SPLITS][2];
+#pragma unroll
+        for (int s = 0; s < SDC_MAX_SPLITS; ++s) {
+          const int64_t sc = s < a.splits ? s : 0;
+          const int32_t* hi = E + ((int64_t)(2 * sc) * a.ncols + 2 * jb) * a.m + rr;
+          const int32_t* lo = E + ((int64_t)(2 * sc + 1) * a.ncols + 2 * jb) * a.m + rr;
+          hv[s][0] = hi[0]; hv[s][1] = hi[a.m];
+          lv[s][0] = lo[0]; lv[s][1] = lo[a.m];
+        }
+#pragma unroll
+        for (int s = 0; s < SDC_MAX_SPLITS; ++s)
+          if (s < a.splits) {
+            i0 += 128 * (int64_t)hv[s][0] + (int64_t)lv[s][0];
+            i1 += 128 * (int64_t)hv[s][1] + (int64_t)lv[s][1];
+          }
+      } else {
 #pragma unroll 4
-      for (int s = 0; s < a.splits; ++s) {
-        const int32_t* hi = E + ((int64_t)(2 * s) * a.ncols + 2 * jb) * a.m + rr;
-        const int32_t* lo = E + ((int64_t)(2 * s + 1) * a.ncols + 2 * jb) * a.m + rr;
-        i0 += 128 * (int64_t)hi[0] + (int64_t)lo[0];
-        i1 += 128 * (int64_t)hi[a.m] + (int64_t)lo[a.m];
+        for (int s = 0; s < a.splits; ++s) {
+          const int32_t* hi = E + ((int64_t)(2 * s) * a.ncols + 2 * jb) * a.m + rr;
+          const int32_t* lo = E + ((int64_t)(2 * s + 1) * a.ncols + 2 * jb) * a.m + rr;
+          i0 += 128 * (int64_t)hi[0] + (int64_t)lo[0];
+          i1 += 128 * (int64_t)hi[a.m] + (int64_t)lo[a.m];
+        }
       }
     } else {
       double asq = 0.0;
+      if constexpr (FEW) {
+        float ev[SDC_MAX_SPLITS][3];
+#pragma unroll
+        for (int s = 0; s < SDC_MAX_SPLITS; ++s) {
+          const int64_t sc = s < a.splits ? s : 0;
+          const float* ep = a.E + ((int64_t)sc * a.ncols + 2 * jb) * a.m + rr;
+          ev[s][0] = ep[0];
+          ev[s][1] = ep[a.m];
+          ev[s][2] = a.XN[sc * 2 * a.m + rr];
+        }
+#pragma unroll
+        for (int s = 0; s < SDC_MAX_SPLITS; ++s)
+          if (s < a.splits) {
+            e0 += (double)ev[s][0];
+            e1 += (double)ev[s][1];
+            asq += (double)ev[s][2];
+          }
+      } else {
 #pragma unroll 4
-      for (int s = 0; s < a.splits; ++s) {
-        const float* ep = a.E + ((int64_t)s * a.ncols + 2 * jb) * a.m + rr;
-        e0 += (double)ep[0];
-        e1 += (double)ep[a.m];
-        asq += (double)a.XN[s * 2 * a.m + rr];
+        for (int s = 0; s < a.splits; ++s) {
+          const float* ep = a.E + ((int64_t)s * a.ncols + 2 * jb) * a.m + rr;
+          e0 += (double)ep[0];
+          e1 += (double)ep[a.m];
+          asq += (double)a.XN[s * 2 * a.m + rr];
+        }
       }
       const double sa = a.sa ? (double)a.sa[rr] : 1.0;
       e0 *= sa;
@@ -587,9 +628,14 @@ extern "C" int sdc_quant_check(int kind, const void* A, int64_t sam, const void*
   SdcProf prof(kind == 0 ? "quant_score_i8" : "quant_score_fp8", stream);
   if (tiles) {
     const dim3 grid((unsigned)L.nb, (unsigned)sdc_cdiv(m, 64));
-    if (kind == 0) hipLaunchKernelGGL((quant_tile_kernel<0, C_I32>), grid, dim3(256), 0, stream, qa);
-    else if (c_dtype == C_F32) hipLaunchKernelGGL((quant_tile_kernel<1, C_F32>), grid, dim3(256), 0, stream, qa);
-    else hipLaunchKernelGGL((quant_tile_kernel<1, C_BF16>), grid, dim3(256), 0, stream, qa);
+    const bool few = qa.splits <= SDC_MAX_SPLITS;
+    if (kind == 0 && few) hipLaunchKernelGGL((quant_tile_kernel<0, C_I32, true>), grid, dim3(256), 0, stream, qa);
+    else if (kind == 0) hipLaunchKernelGGL((quant_tile_kernel<0, C_I32, false>), grid, dim3(256), 0, stream, qa);
+    else if (c_dtype == C_F32 && few)
+      hipLaunchKernelGGL((quant_tile_kernel<1, C_F32, true>), grid, dim3(256), 0, stream, qa);
+    else if (c_dtype == C_F32) hipLaunchKernelGGL((quant_tile_kernel<1, C_F32, false>), grid, dim3(256), 0, stream, qa);
+    else if (few) hipLaunchKernelGGL((quant_tile_kernel<1, C_BF16, true>), grid, dim3(256), 0, stream, qa);
+    else hipLaunchKernelGGL((quant_tile_kernel<1, C_BF16, false>), grid, dim3(256), 0, stream, qa);
   } else {
     const int64_t groups = sdc_cdiv(qa.npairs, 4);
     const unsigned grid = (unsigned)(sdc_cdiv(groups, 4) < 2048 ? sdc_cdiv(groups, 4) : 2048);
