@@ -54,7 +54,8 @@ __device__ __forceinline__ void score_pair(const ScoreArgs& a, int64_t p, float 
   const int64_t r = (uint32_t)p / (uint32_t)a.nb, jb = (uint32_t)p - (uint32_t)r * (uint32_t)a.nb;
   const bool last = (jb == a.nb - 1) && (a.rem > 0);
   const float wf = (float)(last ? a.rem : a.bs);
-  // the GEMM's depth-split planes (at most SDC_MAX_SPLITS): every load issued before the first add
+  // the GEMM's depth-split planes (at most SDC_MAX_SPLITS): every load issued before the first add, unconditional
+  // (a split index past a.splits reads split 0 and is not added)
   const float* ep = a.E + r * a.ncols + 2 * jb;
   const float* xp = a.XN + r;
   const int64_t estep = a.m * a.ncols, xstep = 2 * a.m;
@@ -62,11 +63,10 @@ __device__ __forceinline__ void score_pair(const ScoreArgs& a, int64_t p, float 
   float xa[SDC_MAX_SPLITS], xb[SDC_MAX_SPLITS];
 #pragma unroll
   for (int s = 0; s < SDC_MAX_SPLITS; ++s) {
-    if (s < a.splits) {
-      ev[s] = *reinterpret_cast<const float2*>(ep + s * estep);
-      xa[s] = xp[s * xstep];
-      xb[s] = xp[s * xstep + a.m];
-    }
+    const int64_t sc = s < a.splits ? s : 0;
+    ev[s] = *reinterpret_cast<const float2*>(ep + sc * estep);
+    xa[s] = xp[sc * xstep];
+    xb[s] = xp[sc * xstep + a.m];
   }
   float e0 = ev[0].x, e1 = ev[0].y, asq = xa[0], asum = xb[0];
 #pragma unroll

@@ -321,14 +321,15 @@ __device__ __forceinline__ void train_pair(const TrainArgs& a, int64_t p, float 
   const int64_t estep = a.cv.m * a.ncols, xstep = 2 * a.cv.m;
   float2 ev[SDC_MAX_SPLITS];
   float xa[SDC_MAX_SPLITS], xb[SDC_MAX_SPLITS];
+  // loads unconditional, so all are in flight at once (a split index past a.splits reads split 0, not added)
 #pragma unroll
-  for (int s = 0; s < SDC_MAX_SPLITS; ++s)
-    if (s < a.splits) {
-      if (a.et) ev[s] = make_float2(ep[s * estep], ep[s * estep + a.cv.m]);
-      else ev[s] = *reinterpret_cast<const float2*>(ep + s * estep);
-      xa[s] = xp[s * xstep];
-      xb[s] = xp[s * xstep + a.cv.m];
-    }
+  for (int s = 0; s < SDC_MAX_SPLITS; ++s) {
+    const int64_t sc = s < a.splits ? s : 0;
+    if (a.et) ev[s] = make_float2(ep[sc * estep], ep[sc * estep + a.cv.m]);
+    else ev[s] = *reinterpret_cast<const float2*>(ep + sc * estep);
+    xa[s] = xp[sc * xstep];
+    xb[s] = xp[sc * xstep + a.cv.m];
+  }
   float e0 = ev[0].x, e1 = ev[0].y, asq = xa[0], asum = xb[0];
 #pragma unroll
   for (int s = 1; s < SDC_MAX_SPLITS; ++s)
