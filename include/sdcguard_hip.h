@@ -290,10 +290,10 @@ int sdc_fingerprint2(const void* bits, int64_t n, int kind, int64_t* out, hipStr
  * `words` words each, block b at cache + b * block_bytes; word_bytes 2: int16 words (16-bit and wider element
  * dtypes), 1: int8 words (1-byte element dtypes such as fp8 caches, recompute.py:86-87); ids == NULL: entry i is
  * block i (n = nblocks).  An entry whose id is negative or >= nblocks is left unchanged (a block-table walk passes
- * the table's rows).  2-byte words in whole 64-word chunks (words <= 32768, cache and block_bytes 16-byte
- * aligned) run on the int8 matrix cores against a 2 MB weight table held in static device memory: the first such
- * call on a device builds it and waits for it (a call made while the stream is captured, before that, takes the
- * vector kernel instead, with the same result). */
+ * the table's rows).  Blocks of whole 128-byte chunks (words * word_bytes a multiple of 128, at most 65536; cache
+ * and block_bytes 16-byte aligned) run on the int8 matrix cores against a 2 MB weight table per word size held in
+ * static device memory: the first such call on a device builds it and waits for it (a call made while the stream
+ * is captured, before that, takes the vector kernel instead, with the same result). */
 int sdc_kv_fingerprint(const void* cache, int64_t nblocks, int64_t block_bytes, int64_t words, int word_bytes,
                        const int64_t* ids, int64_t n, int64_t* out, hipStream_t stream);
 

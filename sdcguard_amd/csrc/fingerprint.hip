@@ -396,21 +396,25 @@ __global__ __launch_bounds__(64 * KV_WAVES) void kv_fp3_kernel(KvArgs a, const i
 }
 
 // ------------------------------------------------------------------------------------------- MFMA fingerprints
-// The weighted sums of 2-byte words as int8 matrix products: C[r][b] = sum over the bytes q of block b of
-// T[r][q] * D[q][b], on v_mfma_i32_32x32x32_i8.  D is the block's bytes (low bytes with their top bit flipped:
-// lo - 128, exact as int8; high bytes are the word's signed high half).  T (the weight table) holds, for weight c
-// (w1, w2) and digit d (each weight as eight balanced base-256 digits, sum dig_d 256^d = w mod 2^64), row
-// 8 c + d: dig_d(w_c(p)) at the low byte of word p and dig_{d-1}(w_c(p)) at its high byte, so that
-//   sum_p word_p w_c(p) = sum_d 256^d C[8 c + d] + 128 sum_p w_c(p)          (mod 2^64; 256^8 = 0)
-// and rows 16 / 17 (ones at the low / high bytes) give sum_p word_p = C[16] + 256 C[17] + 128 (number of words).
+// The weighted sums of a block's words as int8 matrix products: C[r][b] = sum over the bytes q of block b of
+// T[r][q] * D[q][b], on v_mfma_i32_32x32x32_i8.  T (the weight table) holds, for weight c (w1, w2) and digit d
+// (each weight as eight balanced base-256 digits, sum dig_d 256^d = w mod 2^64), row 8 c + d.
+//   2-byte words: D is the block's bytes, low bytes with their top bit flipped (lo - 128, exact as int8), high
+//   bytes the word's signed high half; row 8 c + d holds dig_d(w_c(p)) at the low byte of word p and
+//   dig_{d-1}(w_c(p)) at its high byte, so that
+//     sum_p word_p w_c(p) = sum_d 256^d C[8 c + d] + 128 sum_p w_c(p)          (mod 2^64; 256^8 = 0)
+//   and rows 16 / 17 (ones at the low / high bytes) give sum_p word_p = C[16] + 256 C[17] + 128 (words).
+//   1-byte words (int8, recompute.py:86-87): every byte is a word and D is the bytes as they are (signed int8);
+//   row 8 c + d holds dig_d(w_c(p)) at byte p and row 16 ones, so sum_p word_p w_c(p) = sum_d 256^d C[8 c + d]
+//   and sum_p word_p = C[16], with no offset.
 // Every product is at most 2^14 in magnitude and a wave adds at most 2^15 of them per row: exact in int32.
-// T is the same for every block: a table in the MFMA's operand order, made once per device, with the prefix sums
-// of 128 w_c(p) (the low bytes' offset) per 16 words.
-constexpr int KVM_MAXW = 32768;                  // words per block the table covers
-constexpr int KVM_STEPS = KVM_MAXW * 2 / 32;     // 32-byte steps of a block (one MFMA each)
+// T is the same for every block: a table in the MFMA's operand order per word size, made once per device, with
+// (2-byte words) the prefix sums of 128 w_c(p) (the low bytes' offset) per 32-byte step.
+constexpr int KVM_BYTES = 65536;                 // bytes per block the tables cover (32768 2-byte words)
+constexpr int KVM_STEPS = KVM_BYTES / 32;        // 32-byte steps of a block (one MFMA each)
 constexpr int KVM_ENT = 64;                      // block entries per workgroup: two 32-column tiles per wave
-__device__ __attribute__((aligned(256))) uint8_t kvm_tab[KVM_STEPS * 1024];
-__device__ __attribute__((aligned(256))) uint64_t kvm_corr[2 * (KVM_STEPS + 1)];
+__device__ __attribute__((aligned(256))) uint8_t kvm_tab[2][KVM_STEPS * 1024];            // [word bytes - 1]
+__device__ __attribute__((aligned(256))) uint64_t kvm_corr[2][2 * (KVM_STEPS + 1)];
 
 // balanced base-256 digit d of w (in [-128, 128))
 __device__ __forceinline__ int bdig8(uint64_t w, int d) {
@@ -431,13 +435,14 @@ __device__ __forceinline__ uint64_t kvm_weight(uint64_t p, int c) {
 
 // table step s (bytes 32 s .. 32 s + 31), lane l: row l % 32, bytes 16 (l / 32) .. + 15 of the step: the A operand
 // of the step's MFMA, 1 KB per step with lane l's 16 bytes at 16 l
+template <int WB>
 __global__ __launch_bounds__(64) void kvm_fill_kernel(uint8_t* tab) {
   const int s = blockIdx.x, l = threadIdx.x, r = l & 31, h = l >> 5;
   uint32_t out[4] = {0u, 0u, 0u, 0u};
   for (int j = 0; j < 16; ++j) {
     const int64_t q = 32 * (int64_t)s + 16 * h + j;
-    const uint64_t p = (uint64_t)(q >> 1);
-    const int hb = (int)(q & 1);
+    const uint64_t p = (uint64_t)(WB == 2 ? q >> 1 : q);
+    const int hb = WB == 2 ? (int)(q & 1) : 0;
     int v = 0;
     if (r < 16) {
       const int c = r >> 3, d = r & 7;
@@ -453,9 +458,10 @@ __global__ __launch_bounds__(64) void kvm_fill_kernel(uint8_t* tab) {
   *reinterpret_cast<u32x4*>(tab + (int64_t)s * 1024 + 16 * l) = u32x4{out[0], out[1], out[2], out[3]};
 }
 
-// corr[c (KVM_STEPS + 1) + s] = sum over words p < 16 s of 128 w_c(p) (mod 2^64): one workgroup, thread t the
-// steps 8 t .. 8 t + 7, a serial scan of the 256 threads' totals
+// (2-byte words) corr[c (KVM_STEPS + 1) + s] = sum over words p < 16 s of 128 w_c(p) (mod 2^64): one workgroup,
+// thread t the steps 8 t .. 8 t + 7, a serial scan of the 256 threads' totals
 __global__ __launch_bounds__(256) void kvm_corr_kernel(uint64_t* corr) {
+  constexpr int PPS = 16;                        // words per step
   __shared__ uint64_t tot[2][256];
   const int t = threadIdx.x;
   uint64_t st[2][8];
@@ -463,7 +469,7 @@ __global__ __launch_bounds__(256) void kvm_corr_kernel(uint64_t* corr) {
     uint64_t sum = 0;
     for (int k = 0; k < 8; ++k) {
       uint64_t v = 0;
-      for (int j = 0; j < 16; ++j) v += kvm_weight((uint64_t)(16 * (8 * t + k) + j), c);
+      for (int j = 0; j < PPS; ++j) v += kvm_weight((uint64_t)(PPS * (8 * t + k) + j), c);
       st[c][k] = v << 7;
       sum += st[c][k];
     }
@@ -495,12 +501,13 @@ __global__ __launch_bounds__(256) void kvm_corr_kernel(uint64_t* corr) {
 // 32-byte step s and column tile u, lane l reads row 32 u + l % 32, piece 2 s + l / 32 (the B operand) and the
 // MFMA takes the table's step (the A operand) against it.  Chunks alternate between two register sets, the next
 // one's loads issued before the current one is stored.
+template <int WB>
 __global__ __launch_bounds__(256) void kv_mfma_kernel(KvArgs a, const int64_t* ids, const uint8_t* tab,
                                                       const uint64_t* corr) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[4][KVM_ENT * 128];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t e0 = (int64_t)blockIdx.x * KVM_ENT;
-  const int64_t chunks = a.words / 64;
+  const int64_t chunks = a.words * WB / 128;
   const int64_t per = (chunks + 3) / 4;
   const int64_t c0 = w * per < chunks ? w * per : chunks;
   const int64_t c1 = c0 + per < chunks ? c0 + per : chunks;
@@ -529,7 +536,8 @@ __global__ __launch_bounds__(256) void kv_mfma_kernel(KvArgs a, const int64_t* i
   auto process = [&](const u32x4* d, const i32x4* tf) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const u32x4 x = d[i] ^ u32x4{0x00800080u, 0x00800080u, 0x00800080u, 0x00800080u};
+      // 2-byte words: the low bytes' top bits flipped (lo - 128); 1-byte words as they are
+      const u32x4 x = WB == 2 ? d[i] ^ u32x4{0x00800080u, 0x00800080u, 0x00800080u, 0x00800080u} : d[i];
       *reinterpret_cast<u32x4*>(L + (8 * i + (lane >> 3)) * 128 + 16 * wslot) = x;
     }
 #pragma unroll
@@ -567,7 +575,7 @@ __global__ __launch_bounds__(256) void kv_mfma_kernel(KvArgs a, const int64_t* i
       else if (r == 16) v0 += x;
       else if (r == 17) v0 += x << 8;
     }
-    if (h == 0) {
+    if (WB == 2 && h == 0) {
       v0 += (uint64_t)(128 * 64) * (uint64_t)(c1 - c0);
       v1 += corr[4 * c1] - corr[4 * c0];
       v2 += corr[(KVM_STEPS + 1) + 4 * c1] - corr[(KVM_STEPS + 1) + 4 * c0];
@@ -585,35 +593,42 @@ __global__ __launch_bounds__(256) void kv_mfma_kernel(KvArgs a, const int64_t* i
 }
 
 constexpr int KVM_MAXDEV = 64;
-std::atomic<const uint8_t*> g_kvm_tab[KVM_MAXDEV];
-std::atomic<const uint64_t*> g_kvm_corr[KVM_MAXDEV];
+std::atomic<const uint8_t*> g_kvm_tab[KVM_MAXDEV][2];
+std::atomic<const uint64_t*> g_kvm_corr[KVM_MAXDEV][2];
 std::mutex g_kvm_mu;
 
-// This device's weight table and corrections, made at the first call on the device (which waits for them); false
-// when they are not there and cannot be made now (the stream is being captured, or a HIP error)
-bool kvm_tables(hipStream_t stream, const uint8_t** tab, const uint64_t** corr) {
+// This device's weight table and corrections for words of wb bytes, made at the first such call on the device
+// (which waits for them); false when they are not there and cannot be made now (the stream is being captured, or a
+// HIP error)
+bool kvm_tables(hipStream_t stream, int wb, const uint8_t** tab, const uint64_t** corr) {
   int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= KVM_MAXDEV) return false;
-  const uint8_t* tp = g_kvm_tab[dev].load(std::memory_order_acquire);
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= KVM_MAXDEV || (wb != 1 && wb != 2)) return false;
+  const uint8_t* tp = g_kvm_tab[dev][wb - 1].load(std::memory_order_acquire);
   if (!tp) {
     std::lock_guard<std::mutex> lk(g_kvm_mu);
-    tp = g_kvm_tab[dev].load(std::memory_order_relaxed);
+    tp = g_kvm_tab[dev][wb - 1].load(std::memory_order_relaxed);
     if (!tp) {
       hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
       if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
       void *pt = nullptr, *pc = nullptr;
       if (hipGetSymbolAddress(&pt, HIP_SYMBOL(kvm_tab)) != hipSuccess || !pt) return false;
       if (hipGetSymbolAddress(&pc, HIP_SYMBOL(kvm_corr)) != hipSuccess || !pc) return false;
-      hipLaunchKernelGGL(kvm_fill_kernel, dim3(KVM_STEPS), dim3(64), 0, stream, (uint8_t*)pt);
-      hipLaunchKernelGGL(kvm_corr_kernel, dim3(1), dim3(256), 0, stream, (uint64_t*)pc);
+      uint8_t* t = (uint8_t*)pt + (int64_t)(wb - 1) * KVM_STEPS * 1024;
+      uint64_t* c = (uint64_t*)pc + (int64_t)(wb - 1) * 2 * (KVM_STEPS + 1);
+      if (wb == 2) {
+        hipLaunchKernelGGL(kvm_fill_kernel<2>, dim3(KVM_STEPS), dim3(64), 0, stream, t);
+        hipLaunchKernelGGL(kvm_corr_kernel, dim3(1), dim3(256), 0, stream, c);
+      } else {
+        hipLaunchKernelGGL(kvm_fill_kernel<1>, dim3(KVM_STEPS), dim3(64), 0, stream, t);   // (no offset to undo)
+      }
       if (hipGetLastError() != hipSuccess || hipStreamSynchronize(stream) != hipSuccess) return false;
-      g_kvm_corr[dev].store((const uint64_t*)pc, std::memory_order_relaxed);
-      g_kvm_tab[dev].store((const uint8_t*)pt, std::memory_order_release);
-      tp = (const uint8_t*)pt;
+      g_kvm_corr[dev][wb - 1].store(c, std::memory_order_relaxed);
+      g_kvm_tab[dev][wb - 1].store(t, std::memory_order_release);
+      tp = t;
     }
   }
   *tab = tp;
-  *corr = g_kvm_corr[dev].load(std::memory_order_relaxed);
+  *corr = g_kvm_corr[dev][wb - 1].load(std::memory_order_relaxed);
   return true;
 }
 
@@ -675,12 +690,15 @@ extern "C" int sdc_kv_fingerprint(const void* cache, int64_t nblocks, int64_t bl
   int64_t gy = sdc_cdiv(2048, gx);
   if (gy > sdc_cdiv(n, KV_UNROLL)) gy = sdc_cdiv(n, KV_UNROLL);
   if (gy > 65535) gy = 65535;
-  // 2-byte words in whole 128-byte chunks, aligned, within the table: the MFMA kernel
+  // words in whole 128-byte chunks, aligned, within the tables: the MFMA kernel
   const uint8_t* tab = nullptr;
   const uint64_t* corr = nullptr;
-  if (word_bytes == 2 && a.vec && words % 64 == 0 && words <= KVM_MAXW && kvm_tables(stream, &tab, &corr)) {
+  const int64_t wbytes = words * word_bytes;
+  if (a.vec && wbytes % 128 == 0 && wbytes <= KVM_BYTES && kvm_tables(stream, word_bytes, &tab, &corr)) {
     SdcProf prof("kv_fingerprint", stream);
-    hipLaunchKernelGGL(kv_mfma_kernel, dim3((unsigned)sdc_cdiv(n, KVM_ENT)), dim3(256), 0, stream, a, ids, tab, corr);
+    const dim3 grid((unsigned)sdc_cdiv(n, KVM_ENT));
+    if (word_bytes == 2) hipLaunchKernelGGL(kv_mfma_kernel<2>, grid, dim3(256), 0, stream, a, ids, tab, corr);
+    else hipLaunchKernelGGL(kv_mfma_kernel<1>, grid, dim3(256), 0, stream, a, ids, tab, corr);
     SDC_LAUNCH_CHECK();
     return SDC_OK;
   }

@@ -50,10 +50,10 @@ def test_odd_sized_and_strided_blocks():
 
 
 def test_whole_chunk_blocks_extremes_and_padding():
-    """Blocks of whole 64-word chunks, 16-byte aligned (the int8 matrix-core kernel): 320 words (five chunks, so a
+    """Blocks of whole 128-byte chunks, 16-byte aligned (the int8 matrix-core kernel): 320 words (five chunks, so a
     workgroup's four waves take 2, 2, 1 and none), 64 and 32768 words (the table's limit), blocks of words at the
-    int16 extremes, entry counts that are not multiples of 64, dead and repeated entries, and blocks padded apart
-    in memory (2048 words at a stride of 3072)."""
+    int16 extremes, entry counts that are not multiples of 64, dead and repeated entries, blocks padded apart in
+    memory (2048 words at a stride of 3072), and caches of 1-byte words at the int8 extremes."""
     from sdcguard_amd.kv import block_fingerprints
     g = torch.Generator(device="cuda").manual_seed(4)
     for words, nblk in ((320, 70), (64, 130), (32768, 67)):
@@ -72,6 +72,16 @@ def test_whole_chunk_blocks_extremes_and_padding():
     padded = base[:, :2]
     ref = F.kv_block_fp3(padded.contiguous().view(torch.int16).cpu().numpy())
     assert np.array_equal(block_fingerprints(padded).cpu().numpy(), ref)
+    # 1-byte words (int8): 128 (one chunk), 640 and 65536 (the table's limit) bytes a block, int8 extremes
+    for words, nblk in ((128, 70), (640, 66), (65536, 65)):
+        raw = torch.randint(-128, 128, (nblk, words), generator=g, device="cuda", dtype=torch.int32).to(torch.int8)
+        raw[0] = -128
+        raw[1] = 127
+        ref = F.kv_block_fp3(raw.cpu().numpy())
+        assert np.array_equal(block_fingerprints(raw).cpu().numpy(), ref), words
+        ids = torch.tensor([nblk - 1, -1, 1, 0], device="cuda")
+        fi = block_fingerprints(raw, ids).cpu().numpy()
+        assert np.array_equal(fi[[0, 2, 3]], ref[[nblk - 1, 1, 0]]) and not fi[1].any(), words
 
 
 def test_ledger_catches_stale_blocks_and_bit_flips():
