@@ -165,8 +165,10 @@ int sdc_fp8_quant_check(int dtype, const void* x, int64_t sxm, int64_t sxk, int6
  * dtype's unit roundoff, subnormal spacing and largest value); also count the known real rows whose expert ids are
  * all or partly -1.  Otherwise nothing is computed.
  *   x, out (m, H) row strides sx, so; gw (m, K) routing weights (gdtype 0 bf16, 1 fp16, 4 fp32); ids (m, K) int32;
- *   w13 (E, 2I, H) strides s13e, s13n; w2 (E, H, I) strides s2e, s2n; expert_map (global -> local expert) or null;
- *   act 0 SiLU, 1 GELU; routed_first: the routing weight multiplies the first matmul's result.  H <= 8192.
+ *   w13 (E, 2I, H) strides s13e, s13n; w2 (E, H, I) strides s2e, s2n; n_experts = E; expert_map (map_len entries,
+ *   global -> local expert, -1 for another GPU's) or null.  An id that is neither -1 nor in [0, map_len) (no map:
+ *   [0, E)), or a map entry outside [-1, E), is never read: its slot adds nothing to the recompute (whose output
+ *   then disagrees) and a known real row holding one counts with the rows missing experts.  act 0 SiLU, 1 GELU; routed_first: the routing weight multiplies the first matmul's result.  H <= 8192.
  *   state_row: the layer's 11 int64 (worst keys z << 32 | row, column, output bits, recompute bits, step; active
  *   calls; rows checked; unjudged outputs; real rows unrouted, partly routed; (step << 32) | last such row + 1).
  *   cap_meta (claimed, row, step, z bits), cap_x, cap_y (H floats), cap_ids (K int64), cap_g (K floats): the first
@@ -175,7 +177,8 @@ int sdc_fp8_quant_check(int dtype, const void* x, int64_t sxm, int64_t sxk, int6
 int64_t sdc_moe_check_workspace(int64_t H, int64_t I, int64_t K);
 int sdc_moe_check(int dtype, const void* x, int64_t sx, const void* out, int64_t so, const void* gw, int gdtype,
                   const int32_t* ids, const void* w13, int64_t s13e, int64_t s13n, const void* w2, int64_t s2e,
-                  int64_t s2n, const int32_t* expert_map, int64_t m, int64_t H, int64_t I, int64_t K, int act,
+                  int64_t s2n, const int32_t* expert_map, int64_t n_experts, int64_t map_len, int64_t m, int64_t H,
+                  int64_t I, int64_t K, int act,
                   int routed_first, const int64_t* stepbuf, int64_t nlayers, int64_t index, float u, float spacing,
                   float fmax, float line, int64_t* state_row, int32_t* cap_meta, float* cap_x, float* cap_y,
                   int64_t* cap_ids, float* cap_g, float* scores_out, void* workspace, int64_t workspace_bytes,

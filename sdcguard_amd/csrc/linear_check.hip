@@ -639,6 +639,12 @@ Layout layout(int64_t m, int64_t k, int64_t n) {
   return L;
 }
 
+int queue_both(const void* x, int64_t sxm, const void* W, int64_t swn, const void* y, int64_t sym, const void* bias,
+               int64_t m, int64_t k, int64_t n, const void* parts, int64_t spc, const void* parts_frag,
+               const float* block_consts, const float* w_norms, const float* sign_table, int64_t* state,
+               int64_t* row_result, float z, float abs_floor, float* ws, float* col_scores, float* row_scores,
+               const Layout& L, hipStream_t stream, hipStream_t side);
+
 }  // namespace
 
 extern "C" int64_t sdc_linear_check_workspace(int64_t m, int64_t k, int64_t n) {
@@ -663,12 +669,28 @@ extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const voi
   if (m * L.nb * 2 > 0xFFFFFFFFll || n * L.mb * 2 > 0xFFFFFFFFll) return SDC_EUNSUPPORTED;
   if (!workspace || workspace_bytes < L.total * (int64_t)sizeof(float) + 256) return SDC_EWORKSPACE;
   float* ws = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  hipStream_t side = stream;
+  if ((flags & 1) && !(side = sdc_fork(stream))) return SDC_ELAUNCH;
+  const int rc = queue_both(x, sxm, W, swn, y, sym, bias, m, k, n, parts, spc, parts_frag, block_consts, w_norms,
+                            sign_table, state, row_result, z, abs_floor, ws, col_scores, row_scores, L, stream, side);
+  // a call that fails after the fork still makes the caller's stream wait for the side stream, so nothing queued
+  // there can be reading the workspace when the caller reuses it
+  if (rc != SDC_OK && side != stream) sdc_join(stream, side);
+  return rc;
+}
+
+namespace {
+
+// The five launches of sdc_linear_check.  side: the stream of the column check's GEMM and of xfinish (the
+// caller's stream itself for the one-stream variant, in which every kernel runs on the caller's stream).
+int queue_both(const void* x, int64_t sxm, const void* W, int64_t swn, const void* y, int64_t sym, const void* bias,
+               int64_t m, int64_t k, int64_t n, const void* parts, int64_t spc, const void* parts_frag,
+               const float* block_consts, const float* w_norms, const float* sign_table, int64_t* state,
+               int64_t* row_result, float z, float abs_floor, float* ws, float* col_scores, float* row_scores,
+               const Layout& L, hipStream_t stream, hipStream_t side) {
   const float* s_full = sign_table + (BS - 1) * 128;
-  const bool concurrent = (flags & 1) != 0;
 
   // 3. (side stream when asked) the column check's GEMM: E_col = x @ B2 parts (x's row norms come from xstage)
-  hipStream_t side = stream;
-  if (concurrent && !(side = sdc_fork(stream))) return SDC_ELAUNCH;
   GemmArgs gc{};
   gc.A = (const uint16_t*)x; gc.sab = 0; gc.sam = sxm; gc.sak = 1;
   gc.B = parts; gc.sbb = 0; gc.sbc = spc;
@@ -701,9 +723,9 @@ extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const voi
     hipLaunchKernelGGL(xstage_kernel, dim3((unsigned)L.nkc, (unsigned)L.mb), dim3(256), 0, stream, xa);
     SDC_LAUNCH_CHECK();
   }
-  // 2. xfinish on the side stream, beside the row check's GEMM (whose 8-row-tile grid leaves CUs free)
-  hipStream_t fin = sdc_fork(stream);
-  if (!fin) return SDC_ELAUNCH;
+  // 2. xfinish on the side stream (when there is one), beside the row check's GEMM
+  hipStream_t fin = stream;
+  if (side != stream && !(fin = sdc_fork(stream))) return SDC_ELAUNCH;
   {
     SdcProf prof("xfinish", fin);
     hipLaunchKernelGGL(xfinish_kernel, dim3((unsigned)L.mb), dim3(256), 0, fin, xa);
@@ -719,7 +741,7 @@ extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const voi
   gr.prof_name = "row_gemm";
   rc = rs_row ? sdc_rs_gemm_launch(SDC_BF16, gr, 1, stream) : sdc_gemm_launch(SDC_BF16, gr, 1, stream);
   if (rc != SDC_OK) return rc;
-  if ((rc = sdc_join(stream, fin)) != SDC_OK) return rc;     // (the side stream also holds the concurrent GEMM)
+  if (fin != stream && (rc = sdc_join(stream, fin)) != SDC_OK) return rc;   // (the side stream also holds the GEMM)
 
   // 4. one pass over y: both checks
   YArgs ya{};
@@ -741,3 +763,5 @@ extern "C" int sdc_linear_check(int dtype, const void* x, int64_t sxm, const voi
   SDC_LAUNCH_CHECK();
   return SDC_OK;
 }
+
+}  // namespace

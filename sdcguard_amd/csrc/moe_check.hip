@@ -42,6 +42,7 @@ struct MoeArgs {
   const void* w2;                                // (E, H, I)
   int64_t s2e, s2n;
   const int32_t* emap;                           // expert map or null
+  int64_t E, maplen;                             // experts held (w13 / w2), entries of the expert map
   int64_t m, H, I, K;
   int act;                                       // 0 silu, 1 gelu
   int routed_first;
@@ -107,10 +108,24 @@ __device__ __forceinline__ int64_t sample_row(const Live& l, int j, int64_t nl) 
   return ((l.step / nl) * ROW_A + j * ROW_B) % (l.rows > 0 ? l.rows : 1);
 }
 
+// The local expert of slot k of a row: -1 for no expert (padding, or an expert the map puts on another GPU), -2 for
+// an id outside the router's range or a map entry outside the experts held.  Neither is read: a corrupted id must
+// not make the check itself read past the weights.
 __device__ __forceinline__ int64_t expert(const MoeArgs& a, int64_t row, int64_t k) {
   int64_t e = a.ids[row * a.K + k];
-  if (a.emap && e >= 0) e = a.emap[e];
+  if (e == -1) return -1;
+  if (e < 0 || e >= (a.emap ? a.maplen : a.E)) return -2;
+  if (a.emap) {
+    e = a.emap[e];
+    if (e == -1) return -1;
+    if (e < 0 || e >= a.E) return -2;
+  }
   return e;
+}
+
+// An id the router cannot have produced (not -1 and outside [0, experts or map entries))
+__device__ __forceinline__ bool bad_id(const MoeArgs& a, int64_t id) {
+  return id != -1 && (id < 0 || id >= (a.emap ? a.maplen : a.E));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -402,8 +417,11 @@ __global__ __launch_bounds__(256) void moe_compare_kernel(MoeArgs a) {
     int nn = 0, ns = 0;
     int64_t last = 0;
     for (int64_t rr = t; rr < l.rows; rr += 256) {
-      int neg = 0;
-      for (int64_t k = 0; k < a.K; ++k) neg += a.ids[rr * a.K + k] == -1;
+      int neg = 0;                               // slots with no expert, or with an id the router cannot produce
+      for (int64_t k = 0; k < a.K; ++k) {
+        const int64_t id = a.ids[rr * a.K + k];
+        neg += id == -1 || bad_id(a, id);
+      }
       const bool none = neg >= a.K, some = neg > 0 && neg < a.K;
       nn += none;
       ns += some;
@@ -466,7 +484,8 @@ extern "C" int64_t sdc_moe_check_workspace(int64_t H, int64_t I, int64_t K) {
 
 extern "C" int sdc_moe_check(int dtype, const void* x, int64_t sx, const void* out, int64_t so, const void* gw,
                              int gdtype, const int32_t* ids, const void* w13, int64_t s13e, int64_t s13n,
-                             const void* w2, int64_t s2e, int64_t s2n, const int32_t* expert_map, int64_t m,
+                             const void* w2, int64_t s2e, int64_t s2n, const int32_t* expert_map,
+                             int64_t n_experts, int64_t map_len, int64_t m,
                              int64_t H, int64_t I, int64_t K, int act, int routed_first, const int64_t* stepbuf,
                              int64_t nlayers, int64_t index, float u, float spacing, float fmax, float line,
                              int64_t* state_row, int32_t* cap_meta, float* cap_x, float* cap_y, int64_t* cap_ids,
@@ -479,6 +498,7 @@ extern "C" int sdc_moe_check(int dtype, const void* x, int64_t sx, const void* o
       !cap_ids || !cap_g)
     return SDC_EINVAL;
   if (m < 1 || H < 1 || I < 1 || K < 1 || nlayers < 1 || index < 0 || act < 0 || act > 1) return SDC_EINVAL;
+  if (n_experts < 1 || (expert_map && map_len < 1)) return SDC_EINVAL;
   if (H > 8192) return SDC_EUNSUPPORTED;         // the sampled row is staged in LDS
   const int64_t need = sdc_moe_check_workspace(H, I, K);
   if (!workspace || workspace_bytes < need) return SDC_EWORKSPACE;
@@ -487,6 +507,7 @@ extern "C" int sdc_moe_check(int dtype, const void* x, int64_t sx, const void* o
   MoeArgs a{};
   a.x = x; a.sx = sx; a.out = out; a.so = so; a.gw = gw; a.gdt = gdtype; a.ids = ids;
   a.w13 = w13; a.s13e = s13e; a.s13n = s13n; a.w2 = w2; a.s2e = s2e; a.s2n = s2n; a.emap = expert_map;
+  a.E = n_experts; a.maplen = expert_map ? map_len : 0;
   a.m = m; a.H = H; a.I = I; a.K = K; a.act = act; a.routed_first = routed_first; a.stepbuf = stepbuf;
   a.nl = nlayers; a.idx = index; a.u = u; a.spacing = spacing; a.fmax = fmax; a.line = line;
   a.A = (float*)ws;

@@ -299,7 +299,12 @@ extern "C" int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t s
       hipLaunchKernelGGL(serve_sums_kernel<SDC_BF16>, dim3(grid), dim3(256), 0, side, a, SUMS);
     else
       hipLaunchKernelGGL(serve_sums_kernel<SDC_FP16>, dim3(grid), dim3(256), 0, side, a, SUMS);
-    SDC_LAUNCH_CHECK();
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+      sdc_note_error(e);
+      if (kernel != 4) sdc_join(stream, side);    // (the caller's stream waits for the side stream even so)
+      return SDC_ELAUNCH;
+    }
   }
   int rc = sdc_expected_launch(dtype, x, sxm, sxk, parts, spk, spc, nparts, m, k, ncols, splits, E, XN, stream);
   if (kernel != 4) {

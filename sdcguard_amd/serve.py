@@ -154,30 +154,30 @@ def _parts3(x: torch.Tensor, dt: torch.dtype):
     return hi, mid, (r - mid).to(dt)
 
 
-_KMAJOR: dict = {}
-_KMAJOR_LOCK = threading.Lock()
-
-
 def _kmajor_parts(parts: torch.Tensor, scale: torch.Tensor, nb: int, dt: torch.dtype) -> torch.Tensor:
     """`parts` in the kernel's layout: three `dt` parts, k-contiguous.  A LayerChecksums made here already is;
-    constants made elsewhere (row-major parts, or fp32 block sums) are converted once and kept."""
+    constants made elsewhere (row-major parts, or fp32 block sums) are converted once and the copy is kept on the
+    parts tensor itself, so it lives exactly as long as the constants it copies (keyed by their version, and for
+    fp32 block sums by the scale they are divided by)."""
     if parts.shape[1] == 6 * nb and parts.dtype == dt and parts.stride(0) == 1:
         return parts
-    key = (parts.data_ptr(), parts._version, tuple(parts.shape), parts.dtype, str(parts.device))
-    hit = _KMAJOR.get(key)
-    if hit is not None:
-        return hit
+    fp32_sums = parts.shape[1] == 2 * nb
+    key = (parts._version, tuple(parts.shape), parts.dtype, dt,
+           (scale.data_ptr(), scale._version) if fp32_sums else None)
+    hit = getattr(parts, "_sdc_kmajor", None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
     with torch.no_grad():
         if parts.shape[1] == 6 * nb and parts.dtype == dt:
             out = parts.t().contiguous().t()
-        elif parts.shape[1] == 2 * nb:                       # plain fp32 B2: split it (scale applies to E after)
+        elif fp32_sums:                                      # plain fp32 B2: split it (scale applies to E after)
             out = _split3_kmajor(parts.float() / scale.reshape(1, 2 * nb), dt)
         else:
             raise ValueError(f"parts of shape {tuple(parts.shape)} don't fit {nb} blocks")
-    with _KMAJOR_LOCK:
-        if len(_KMAJOR) > 64:
-            _KMAJOR.clear()
-        _KMAJOR[key] = out
+    try:
+        parts._sdc_kmajor = (key, out)
+    except (AttributeError, RuntimeError):
+        pass
     return out
 
 

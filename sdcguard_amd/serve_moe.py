@@ -119,7 +119,8 @@ def moe_check(x: torch.Tensor, out: torch.Tensor, topk_w: torch.Tensor, topk_ids
     ws = _lib.workspace(x.device, ws_bytes)
     rc = L.sdc_moe_check(_code(out.dtype), x2.data_ptr(), x2.stride(0), y2.data_ptr(), y2.stride(0), gw.data_ptr(),
                          _code(gw.dtype), ids.data_ptr(), w13.data_ptr(), w13.stride(0), w13.stride(1), w2.data_ptr(),
-                         w2.stride(0), w2.stride(1), None if emap is None else emap.data_ptr(), m, hdim, w2.shape[2], k,
+                         w2.stride(0), w2.stride(1), None if emap is None else emap.data_ptr(), w13.shape[0],
+                         0 if emap is None else emap.numel(), m, hdim, w2.shape[2], k,
                          int(act), int(bool(routed_first)), stepbuf.data_ptr(), max(int(nlayers), 1), int(index),
                          float(u), float(sp), float(fm), float(line), state[slot].data_ptr(), cap_meta[slot].data_ptr(),
                          cap_x[slot].data_ptr(), cap_y[slot].data_ptr(), cap_ids[slot].data_ptr(),

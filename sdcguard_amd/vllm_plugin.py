@@ -72,17 +72,21 @@ class _Plugin:
 
     @staticmethod
     def _arm(layer, g, slot: int) -> None:
-        layer._sdcguard_args = (g.op_args(slot, with_bias=False), g.op_args(slot, with_bias=True))
+        # the guard and slot, not the op's arguments: a later layer can make the guard enlarge its device's state
+        # and capture tensors, and the arguments are read from the guard on every call so that no layer keeps
+        # writing into tensors the guard no longer polls
+        layer._sdcguard_ref = (g, slot)
         layer.__dict__.pop("_sdcguard_why", None)
 
     @staticmethod
     def after_apply(layer, x, y, bias) -> None:
         from .serve import _op, check_static_impl
-        args = getattr(layer, "_sdcguard_args", None)
-        if args is None or not isinstance(y, torch.Tensor):
+        ref = getattr(layer, "_sdcguard_ref", None)
+        if ref is None or not isinstance(y, torch.Tensor):
             return
+        g, slot = ref
         run = _op() if torch.compiler.is_compiling() else check_static_impl
-        run(x.reshape(-1, x.shape[-1]), y.reshape(-1, y.shape[-1]), *args[1 if bias is not None else 0])
+        run(x.reshape(-1, x.shape[-1]), y.reshape(-1, y.shape[-1]), *g.op_args(slot, with_bias=bias is not None))
 
     def poll(self, wait: bool = False) -> list:
         events = []

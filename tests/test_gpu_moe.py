@@ -106,6 +106,45 @@ def test_larger_layer_scores_against_oracle_and_faults(dt, act, rf):
                                           cap_ids=cap3["ids"], cap_g=cap3["g"])), what
 
 
+def test_out_of_range_expert_ids_are_counted_not_read():
+    """Expert ids a router cannot produce (past the experts held, past the expert map, below -1) are never used to
+    index the weights: a sampled row holding one disagrees with its output (its slot adds nothing), and every known
+    real row holding one is counted with the rows missing experts."""
+    g0 = torch.Generator().manual_seed(3)
+    E, H, I, K, M = 8, 256, 128, 2, 24
+    w13 = (torch.randn(E, 2 * I, H, generator=g0) * 0.05).bfloat16()
+    w2 = (torch.randn(E, H, I, generator=g0) * 0.05).bfloat16()
+    x = torch.randn(M, H, generator=g0).bfloat16()
+    gw, ids = torch.topk(torch.softmax(torch.randn(M, E, generator=g0), -1), K, -1)
+    ids = ids.to(torch.int32)
+    step, nl, idx = 5, 1, 0
+    raw = (20 << 32) | step
+    r0 = int(om.sample_rows(step, 20, nl)[0])
+    r_all, *_ = om.recompute(x.float().numpy(), ids.numpy(), gw.numpy(), w13.float().numpy(), w2.float().numpy(),
+                             None, 0, False, "bf16")
+    y = torch.from_numpy(r_all).bfloat16()
+    base = dict(name="oob", xw=x.view(torch.int16).numpy(), yw=y.view(torch.int16).numpy(),
+                w13w=w13.view(torch.int16).numpy(), w2w=w2.view(torch.int16).numpy(), g=gw.numpy(), act=0, rf=False,
+                raw=raw, nl=nl, idx=idx, dt="bf16", k=K)
+    bad = ids.clone()
+    bad[r0, 1] = 1 << 30                                  # the sampled row: an id far past the 8 experts
+    bad[(r0 + 3) % 20, 0] = E                             # another real row: the first id past the end
+    bad[21, 0] = -7                                       # a row past the real ones: not scanned
+    st, _ = _run_gpu(dict(base, ids=bad.numpy(), emap=None))
+    z = float(np.array([int(st[0]) >> 32], np.uint32).view(np.float32)[0])
+    print("no map:", z, st.tolist())
+    assert z > 6 and int(st[0]) & 0xFFFFFFFF == r0
+    assert st[om.C_PARTIAL] == 2 and st[om.C_UNROUTED] == 0 and st[om.C_BADROW] & 0xFFFFFFFF == max(r0, (r0 + 3) % 20) + 1
+    # with an expert map of 12 global ids (the last four on another GPU): 12 is out of range, 11 is not
+    emap = np.array(list(range(E)) + [-1, -1, -1, -1], np.int32)
+    ok = ids.clone()
+    ok[(r0 + 1) % 20, 0] = 11                             # another GPU's expert: a valid routing
+    ok[(r0 + 2) % 20, 1] = 12
+    st2, _ = _run_gpu(dict(base, ids=ok.numpy(), emap=emap))
+    print("map:", st2.tolist())
+    assert st2[om.C_PARTIAL] == 1 and st2[om.C_UNROUTED] == 0
+
+
 class _Act:
     value = "silu"
 

@@ -97,7 +97,7 @@ def test_patched_methods_check_every_product(monkeypatch, fake_vllm):
     layers = [_layer(384, 256, 0), _layer(256, 384, 1, bias=False)]
     for lay in layers:
         meth.process_weights_after_loading(lay)
-        assert lay.loaded == 1 and hasattr(lay, "_sdcguard_args")
+        assert lay.loaded == 1 and hasattr(lay, "_sdcguard_ref")
     x = torch.randn(48, 256, device="cuda").bfloat16()
     h = meth.apply(layers[0], x, layers[0].bias)
     meth.apply(layers[1], torch.nn.functional.gelu(h), None)
@@ -117,3 +117,36 @@ def test_patched_methods_check_every_product(monkeypatch, fake_vllm):
     assert vllm_plugin.poll(wait=True) == [] and len(g.layers) == 2
     vllm_plugin.unregister()
     assert not hasattr(M, "_sdcguard_originals")
+
+
+@pytest.mark.gpu
+def test_layers_armed_before_the_state_grows_still_report(monkeypatch, fake_vllm):
+    """A layer deeper than the first allocation (k > 8192) makes the guard enlarge its device's state and capture
+    tensors; a fault in a layer loaded before that is still reported, and both layers' checks are counted."""
+    from sdcguard_amd import vllm_plugin
+    monkeypatch.setenv("SDCGUARD", "1")
+    state = {"bad": False}
+
+    def corrupt(y):
+        if state["bad"] and y.shape[1] == 384:
+            y = y.clone()
+            y[5, 300] += 8.0
+        return y
+
+    M = fake_vllm(corrupt)
+    vllm_plugin.register()
+    meth = M()
+    first, deep = _layer(384, 256, 2), _layer(128, 9216, 3, bias=False)
+    meth.process_weights_after_loading(first)
+    g = vllm_plugin.plugin_state().guards[torch.device("cuda", 0)]
+    rows_before = g._rows[torch.device("cuda", 0)]
+    meth.process_weights_after_loading(deep)
+    assert g._rows[torch.device("cuda", 0)] is not rows_before       # the deep layer enlarged the device's rows
+    x = torch.randn(16, 256, device="cuda").bfloat16()
+    state["bad"] = True
+    meth.apply(first, x, first.bias)
+    meth.apply(deep, torch.randn(16, 9216, device="cuda").bfloat16(), None)
+    ev = vllm_plugin.poll(wait=True)
+    assert len(ev) == 1 and ev[0].layer == "model.layers.2.mlp" and (ev[0].row, ev[0].col_block) == (5, 2)
+    assert g.stats["checks_executed"] == 2
+    vllm_plugin.unregister()
