@@ -17,13 +17,12 @@ Static scales are weights: they are compared with their value at load.  The arit
 """
 from __future__ import annotations
 
-import struct
 import threading
 from typing import Optional
 
 import torch
 
-from .serve import SDCEvent
+from .stepchecks import W_ROWS, W_STEP, Binding, Registered, StepChecks, f32_of
 
 FP8_MAX = 448.0
 MIN_SCALE = 1.0 / (448.0 * 512.0)
@@ -41,10 +40,6 @@ C_CALLS, C_SCALE, C_OUTSIDE, C_VALUES, C_ONE, C_LAST, C_RATIO, C_STATIC = range(
 KIND_SCALE, KIND_OUTSIDE, KIND_VALUES, KIND_STATIC = 1, 2, 3, 4
 EVERY_ROW = 0xFFFFFF
 _DT_F32 = 4
-
-
-def _f32(bits: int) -> float:
-    return struct.unpack("<f", struct.pack("<I", int(bits) & M32))[0]
 
 
 def unwrap31(s31: int, marked: Optional[int]) -> int:
@@ -120,247 +115,167 @@ def quant_check(x2: torch.Tensor, xq: torch.Tensor, xs: torch.Tensor, recipe: in
 
 quant_check_torch = quant_check         # the reference's name for the same call
 
-_lib_lock = threading.Lock()
-_OP = [None]
+_OP_LOCK = threading.Lock()
+_OP: list = [None]
 
 
 def quant_op():
-    """sdcguard::fp8_quant_check, registered once: one opaque op under torch.compile (serve_fp8.py:181-205)."""
-    with _lib_lock:
-        if _OP[0] is None:
+    """The check as one opaque op for torch.compile, registered on first use under the reference's name and schema
+    (sdcguard::fp8_quant_check, serve_fp8.py:181-205); where the op cannot be registered, the library call."""
+    with _OP_LOCK:
+        if _OP[0] is not None:
+            return _OP[0]
+        op = getattr(getattr(torch.ops, "sdcguard", None), "fp8_quant_check", None)
+        if op is None:
             try:
-                @torch.library.custom_op("sdcguard::fp8_quant_check", mutates_args=("state",))
-                def fp8_quant_check(x2: torch.Tensor, xq: torch.Tensor, xs: torch.Tensor, recipe: int,
-                                    scale_ub: Optional[torch.Tensor], static_ref: Optional[torch.Tensor],
-                                    rows_buf: torch.Tensor, stepbuf: torch.Tensor, state: torch.Tensor,
-                                    slot: int, mult: int) -> None:
-                    quant_check(x2, xq, xs, recipe, scale_ub, static_ref, rows_buf, stepbuf, state, slot, mult)
-
-                @fp8_quant_check.register_fake
-                def _(*a):
-                    return None
-
-                _OP[0] = torch.ops.sdcguard.fp8_quant_check
+                lib_op = torch.library.custom_op("sdcguard::fp8_quant_check", mutates_args=("state",))(_op_body)
+                lib_op.register_fake(lambda *a: None)
+                op = torch.ops.sdcguard.fp8_quant_check
             except (AttributeError, RuntimeError):
-                _OP[0] = getattr(getattr(torch.ops, "sdcguard", None), "fp8_quant_check", None) or quant_check
-        return _OP[0]
+                op = quant_check
+        _OP[0] = op
+        return op
 
 
-def check_call(args: tuple, x2: torch.Tensor, xq: torch.Tensor, xs: torch.Tensor,
+def _op_body(x2: torch.Tensor, xq: torch.Tensor, xs: torch.Tensor, recipe: int, scale_ub: Optional[torch.Tensor],
+             static_ref: Optional[torch.Tensor], rows_buf: torch.Tensor, stepbuf: torch.Tensor, state: torch.Tensor,
+             slot: int, mult: int) -> None:
+    quant_check(x2, xq, xs, recipe, scale_ub, static_ref, rows_buf, stepbuf, state, slot, mult)
+
+
+def _shapes_fit(x2, xq, xs) -> bool:
+    return isinstance(xq, torch.Tensor) and isinstance(xs, torch.Tensor) and x2.dim() == 2 and xq.dim() == 2 and \
+        xq.shape[1] == x2.shape[1] and xq.shape[0] >= x2.shape[0]
+
+
+def check_call(binding, x2: torch.Tensor, xq: torch.Tensor, xs: torch.Tensor,
                scale_ub: Optional[torch.Tensor] = None, mult: int = 1) -> None:
-    """One quantization of a registered layer: its input, the FP8 input the GEMM got and its scale
-    (serve_fp8.py:208-219)."""
-    recipe, static_ref, rows_buf, stepbuf, state, slot = args
-    if not (isinstance(xq, torch.Tensor) and isinstance(xs, torch.Tensor)) or xq.dim() != 2 or x2.dim() != 2 or \
-            xq.shape[1] != x2.shape[1] or xq.shape[0] < x2.shape[0]:
+    """One quantization of a registered layer (its input, the FP8 input its GEMM got and that input's scale), queued
+    on the current stream.  binding: what Fp8Checks.add returned (serve_fp8.py:208-219)."""
+    if binding is None or not _shapes_fit(x2, xq, xs):
         return
-    if torch.compiler.is_compiling():
-        (_OP[0] if _OP[0] is not None else quant_op())(x2, xq, xs, recipe, scale_ub, static_ref, rows_buf, stepbuf,
-                                                       state, slot, int(mult))
-    else:
-        quant_check(x2, xq, xs, recipe, scale_ub, static_ref, rows_buf, stepbuf, state, slot, int(mult))
+    args = binding.checks.call_args(binding)
+    run = quant_op() if torch.compiler.is_compiling() else quant_check
+    run(x2, xq, xs, args[0], scale_ub, args[1], args[2], args[3], args[4], args[5], max(int(mult), 1))
 
 
-def _per_tensor(gs) -> bool:
-    """Whether a quantizer's group shape is per tensor: a (row, col) pair of -1s, an is_per_tensor() method, or a
-    name containing TENSOR."""
-    f = getattr(gs, "is_per_tensor", None)
-    if callable(f):
+# How a quantizer object of the serving stack tells its recipe (serve_fp8.py:236-248 reads the same attributes):
+# group (block) scales are not checked; a static scale must be one for the whole tensor; a dynamic one is per token
+# when the quantizer says so, else per tensor.
+def _is_whole_tensor(group_shape) -> bool:
+    probe = getattr(group_shape, "is_per_tensor", None)
+    if callable(probe):
         try:
-            return bool(f())
+            return bool(probe())
         except Exception:  # noqa: BLE001
             return False
-    if isinstance(gs, tuple) and len(gs) == 2:
-        return tuple(gs) == (-1, -1)
-    return "TENSOR" in str(getattr(gs, "name", gs) or "").upper()
+    if isinstance(group_shape, tuple):
+        return len(group_shape) == 2 and all(int(v) == -1 for v in group_shape)
+    label = getattr(group_shape, "name", group_shape)
+    return label is not None and "TENSOR" in str(label).upper()
 
 
 def recipe_of(quant_fp8) -> tuple:
-    """(recipe, why not) of a layer's FP8 input quantizer (serve_fp8.py:236-248)."""
+    """(recipe code, None) of an FP8 input quantizer, or (None, why it is not checked)."""
     if quant_fp8 is None:
         return None, "no FP8 input quantization found"
-    if getattr(quant_fp8, "is_group_quant", False):
+    if bool(getattr(quant_fp8, "is_group_quant", False)):
         return None, "FP8 with group (block) activation scales"
+    if not bool(getattr(quant_fp8, "static", False)):
+        token = bool(getattr(quant_fp8, "use_per_token_if_dynamic", False))
+        return RECIPES["dynamic_token" if token else "dynamic_tensor"], None
     gs = getattr(quant_fp8, "group_shape", None)
-    if getattr(quant_fp8, "static", False):
-        if not _per_tensor(gs):
-            return None, f"static FP8 activation scales per {getattr(gs, 'name', gs) or 'group'}"
+    if _is_whole_tensor(gs):
         return RECIPES["static"], None
-    if getattr(quant_fp8, "use_per_token_if_dynamic", False):
-        return RECIPES["dynamic_token"], None
-    return RECIPES["dynamic_tensor"], None
+    return None, f"static FP8 activation scales per {getattr(gs, 'name', gs) or 'group'}"
 
 
 _FINDINGS = {KIND_OUTSIDE: "scale_from_outside_rows", KIND_SCALE: "scale_wrong", KIND_VALUES: "values_wrong",
              KIND_STATIC: "static_scale_changed"}
-_READING = {
-    "scale_from_outside_rows": "the per-tensor FP8 scale the GEMM used is the maximum over every row of its input, "
-                               "padding included, not over this step's real rows: the output depends on rows an "
-                               "earlier request left",
-    "scale_wrong": "the FP8 scale the GEMM used differs from the scale its recipe gives for this step's rows",
-    "values_wrong": "FP8 values the GEMM got are two or more FP8 steps from the layer's input quantized with that "
-                    "scale",
-    "static_scale_changed": "the layer's static FP8 input scale changed since load",
+_MEANING = {
+    "scale_from_outside_rows": "the GEMM's per-tensor scale is the largest |x| over all its input rows, padding "
+                               "included; over this step's own rows it is smaller, so the result depended on rows "
+                               "left by an earlier request",
+    "scale_wrong": "the GEMM's FP8 scale is not the one its recipe gives for this step's rows",
+    "values_wrong": "sampled FP8 inputs of the GEMM are two or more E4M3 steps from the layer's input quantized with "
+                    "the GEMM's scale",
+    "static_scale_changed": "the layer's static FP8 input scale is not its value at load",
 }
 
 
-class Fp8Checks:
-    """The FP8 layers whose quantization one serving guard checks: add() each at weight processing, mark_step(step,
-    rows) before each model step and end_step() after it, poll() to read the counters (serve_fp8.py:251-419)."""
+class Fp8Checks(StepChecks):
+    """FP8 input quantizations checked for one serving guard.  add() each FP8 layer at load (it returns the binding
+    the layer's call site passes to check_call); mark_step / end_step around each model step; poll() to read.
+    State rows are the kernel's 8 counters per layer (the reference's columns, serve_fp8.py:46-50)."""
+
+    DETECTOR = "serve_fp8"
+    COLS = COLS
 
     def __init__(self, guard=None):
-        self._marked: Optional[int] = None
-        self.guard = guard
-        self.layers: list = []
-        self.unsupported: dict = {}
-        self._state, self._rows, self._step, self._host = {}, {}, {}, {}
-        self.stats = {"layers": 0, "calls": 0, "scale_wrong": 0, "scale_from_outside_rows": 0, "values_wrong": 0,
-                      "fp8_one_step": 0, "alerts": 0}
+        super().__init__(guard)
+        self.stats.update(calls=0, scale_wrong=0, scale_from_outside_rows=0, values_wrong=0, fp8_one_step=0)
         self.seen: dict = {}
-        self.events: list = []
-        self._lock = threading.Lock()
 
-    def _dev(self, dev):
-        if dev not in self._state:
-            with torch.inference_mode(False):
-                self._state[dev] = torch.zeros(64, COLS, dtype=torch.int64, device=dev)
-                self._rows[dev] = torch.zeros(1, dtype=torch.int64, device=dev)
-                self._step[dev] = torch.zeros(1, dtype=torch.int64, device=dev)
-        return self._state[dev]
-
-    def add(self, layer, name: str, quant_fp8, static_scale: Optional[torch.Tensor], device) -> Optional[tuple]:
-        """Register one layer; its call arguments (for check_call), or None with the reason in unsupported."""
-        device = torch.device(device)
+    def add(self, layer, name: str, quant_fp8, static_scale: Optional[torch.Tensor], device) -> Optional[Binding]:
         recipe, why = recipe_of(quant_fp8)
+        if why is None and torch.device(device).type != "cuda":
+            why = "not on a GPU"
         if why:
-            self.unsupported[name] = why
+            self._refuse(name, why)
             return None
-        if device.type != "cuda":
-            self.unsupported[name] = "not on a GPU"
-            return None
-        with self._lock:
-            st = self._dev(device)
-            slot = sum(1 for lay in self.layers if lay["device"] == device)
-            if slot >= st.shape[0]:
-                with torch.inference_mode(False):
-                    grown = torch.zeros(st.shape[0] * 2, COLS, dtype=torch.int64, device=device)
-                    grown[:st.shape[0]] = st
-                self._state[device] = grown
-                for lay in self.layers:               # their arguments hold the old rows: point them at the new ones
-                    if lay["device"] == device and lay["layer"] is not None:
-                        lay["layer"]._sdcguard_fp8 = self.args(lay)
-            ref = None
-            if recipe == RECIPES["static"] and isinstance(static_scale, torch.Tensor):
-                with torch.inference_mode(False):
-                    ref = static_scale.detach().float().reshape(-1)[:1].clone()
-            lay = {"name": name, "layer": layer, "device": device, "slot": slot, "recipe": recipe, "static_ref": ref}
-            self.layers.append(lay)
-            self.stats["layers"] += 1
-            quant_op()
-            a = self.args(lay)
-            if layer is not None:
-                layer._sdcguard_fp8 = a
-            return a
+        ref = None
+        if recipe == RECIPES["static"] and isinstance(static_scale, torch.Tensor):
+            with torch.inference_mode(False):
+                ref = static_scale.detach().float().reshape(-1)[:1].clone()
+        b = self._register(name, layer, device, recipe=recipe, static_ref=ref)
+        quant_op()
+        if layer is not None:
+            layer._sdcguard_fp8 = b
+        return b
 
-    def args(self, lay) -> tuple:
-        dev = lay["device"]
-        return (lay["recipe"], lay["static_ref"], self._rows[dev], self._step[dev], self._state[dev], lay["slot"])
+    def call_args(self, b: Binding) -> tuple:
+        """(recipe, static reference, real rows, step, state, slot) of a binding's layer, as the kernel takes them."""
+        lay, tab = b.layer, b.table()
+        return (lay.info["recipe"], lay.info["static_ref"], tab.word.view(W_ROWS), tab.word.view(W_STEP), tab.state,
+                lay.slot)
 
-    def mark_step(self, step: int, rows: Optional[int] = None) -> None:
-        """Publish the coming step and its real row count on every device (fills: no host synchronisation)."""
-        self._marked = int(step) & M32
-        for dev in self._state:
-            self._step[dev].fill_(int(step) & M32)
-            self._rows[dev].fill_(int(rows) if rows is not None else 0)
-
-    def end_step(self) -> None:
-        for dev in self._state:
-            self._rows[dev].zero_()
-
-    def detach(self) -> None:
-        try:
-            self.poll(wait=True)
-        finally:
-            for lay in self.layers:
-                if lay["layer"] is not None:
-                    lay["layer"].__dict__.pop("_sdcguard_fp8", None)
-                    lay["layer"].__dict__.pop("_sdcguard_fp8_moe", None)
-            self.layers.clear()
-            for d in (self._state, self._rows, self._step, self._host):
-                d.clear()
+    def _unbind(self, lay: Registered) -> None:
+        if lay.module is not None:
+            for attr in ("_sdcguard_fp8", "_sdcguard_fp8_moe"):
+                lay.module.__dict__.pop(attr, None)
 
     def coverage(self) -> dict:
-        return {"layers": len(self.layers), "calls": self.stats["calls"],
-                "layers_checked": sum(self.seen.get(lay["name"], 0) > 0 for lay in self.layers),
-                "never_checked": sorted(lay["name"] for lay in self.layers if not self.seen.get(lay["name"])),
-                "not_attached": dict(self.unsupported), "samples_per_call": SAMPLES,
-                "recipes": sorted({k for lay in self.layers for k, v in RECIPES.items() if v == lay["recipe"]})}
-
-    def poll(self, wait: bool = False) -> list:
-        """Counters read back and cleared.  Without wait the copy is started now and reported by a later poll."""
-        events = []
-        for dev, st in list(self._state.items()):
-            if wait:
-                pend = self._host.pop(dev, None)
-                if pend is not None:
-                    pend[1].synchronize()
-                    events += self._report(dev, pend[0])
-                host = st.to("cpu", copy=True)
-                st.zero_()
-                events += self._report(dev, host)
-                continue
-            pend = self._host.get(dev)
-            if pend is not None and pend[1].query():
-                events += self._report(dev, pend[0])
-                self._host.pop(dev, None)
-                pend = None
-            if pend is None:
-                hs = torch.empty(st.shape, dtype=st.dtype, pin_memory=True)
-                hs.copy_(st, non_blocking=True)
-                st.zero_()
-                ev = torch.cuda.Event()
-                ev.record(torch.cuda.current_stream(dev))
-                self._host[dev] = (hs, ev)
-        return events
-
-    def _report(self, dev, host) -> list:
-        out = []
-        for lay in self.layers:
-            if lay["device"] != dev or lay["slot"] >= host.shape[0]:
-                continue
-            k = [int(v) for v in host[lay["slot"]].tolist()]
-            self.stats["calls"] += k[C_CALLS]
-            self.seen[lay["name"]] = self.seen.get(lay["name"], 0) + k[C_CALLS]
-            self.stats["scale_wrong"] += k[C_SCALE]
-            self.stats["scale_from_outside_rows"] += k[C_OUTSIDE]
-            self.stats["values_wrong"] += k[C_VALUES]
-            self.stats["fp8_one_step"] += k[C_ONE]
-            if k[C_SCALE] or k[C_VALUES] or k[C_STATIC]:
-                out.append(self._alert(lay, k))
+        out = super().coverage()
+        out.update(calls=self.stats["calls"], samples_per_call=SAMPLES,
+                   recipes=sorted({n for n, v in RECIPES.items() for lay in self.layers if lay.info["recipe"] == v}))
         return out
 
-    def _alert(self, lay, k) -> SDCEvent:
-        last = k[C_LAST]
-        step, kind, row = unwrap31(last >> 32, self._marked), (last >> 24) & 0xFF, last & 0xFFFFFF
-        what = _FINDINGS.get(kind, "unknown")
-        detail = {"where": lay["name"], "kind": "fp8_quantization", "finding": what, "calls_judged": k[C_CALLS],
-                  "calls_with_wrong_scale": k[C_SCALE], "calls_scale_from_outside_rows": k[C_OUTSIDE],
-                  "sampled_rows_with_wrong_values": k[C_VALUES], "values_one_fp8_step_off": k[C_ONE],
-                  "scale_ratio": _f32(k[C_RATIO]) if k[C_RATIO] else None,
-                  "captured": ({"step": step, "row": None, "every_row": True} if row == EVERY_ROW else
-                               {"step": step, "row": row}) if kind in (KIND_VALUES, KIND_SCALE, KIND_OUTSIDE) else None,
-                  "recipe": next(n for n, v in RECIPES.items() if v == lay["recipe"]),
+    def _count(self, lay: Registered, k: list) -> None:
+        lay.calls += k[C_CALLS]
+        self.seen[lay.name] = self.seen.get(lay.name, 0) + k[C_CALLS]
+        for stat, col in (("calls", C_CALLS), ("scale_wrong", C_SCALE), ("scale_from_outside_rows", C_OUTSIDE),
+                          ("values_wrong", C_VALUES), ("fp8_one_step", C_ONE)):
+            self.stats[stat] += k[col]
+
+    def _judged(self, k: list) -> bool:
+        return k[C_CALLS] > 0
+
+    def _judge(self, lay: Registered, k: list, captured: dict, window) -> list:
+        if not (k[C_SCALE] or k[C_VALUES] or k[C_STATIC]):
+            return []
+        step = unwrap31(k[C_LAST] >> 32, self.marked)
+        kind, row = (k[C_LAST] >> 24) & 0xFF, k[C_LAST] & 0xFFFFFF
+        finding = _FINDINGS.get(kind, "unknown")
+        where = None
+        if kind in (KIND_VALUES, KIND_SCALE, KIND_OUTSIDE):
+            where = {"step": step, "row": None, "every_row": True} if row == EVERY_ROW else {"step": step, "row": row}
+        recipe = next(n for n, v in RECIPES.items() if v == lay.info["recipe"])
+        detail = {"where": lay.name, "kind": "fp8_quantization", "finding": finding, "recipe": recipe,
+                  "calls_judged": k[C_CALLS], "calls_with_wrong_scale": k[C_SCALE],
+                  "calls_scale_from_outside_rows": k[C_OUTSIDE], "sampled_rows_with_wrong_values": k[C_VALUES],
+                  "values_one_fp8_step_off": k[C_ONE], "scale_ratio": f32_of(k[C_RATIO]) if k[C_RATIO] else None,
+                  "captured": where, "read_window_steps": window, "last_clean_read_steps": self.last_clean(lay.name),
                   "check_config": {"samples_per_call": SAMPLES, "scale_tolerance": SCALE_TOL,
-                                   "values": "2 or more FP8 steps off is an alarm; 1 step is counted (fast math)"},
-                  "reading": _READING.get(what, "")}
-        ev = SDCEvent(detector="serve_fp8", layer=lay["name"], z=float("inf"), row=None if row == EVERY_ROW else row,
-                      extra=detail)
-        self.stats["alerts"] += 1
-        self.events.append(ev)
-        g = self.guard
-        if g is not None and getattr(g, "on_alert", None):
-            try:
-                g.on_alert(ev)
-            except Exception:  # noqa: BLE001  (an alert callback never breaks serving)
-                pass
-        return ev
+                                   "values": "an alarm from 2 E4M3 steps off; 1 step is counted only"},
+                  "reading": _MEANING.get(finding, "")}
+        return [self.emit(lay, float("inf"), None if row == EVERY_ROW else row, detail)]

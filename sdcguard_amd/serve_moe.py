@@ -22,13 +22,12 @@ activations other than gated SiLU/GELU, or layers that combine across GPUs.
 from __future__ import annotations
 
 import math
-import struct
 import threading
 from typing import Optional
 
 import torch
 
-from .serve import SDCEvent
+from .stepchecks import W_PACKED, Binding, Registered, StepChecks, f32_of, pack_step
 
 MOE_Z = 6.0
 SAMPLES = 2
@@ -46,10 +45,6 @@ ROWS_MAX = (1 << 31) - 1
 ACT = {"silu": 0, "gelu": 1}
 PLACE_KEPT = "the kept row's worst output, rechecked"
 PLACE_MAXIMA = "the read's score maxima (row, column and values of the worst score)"
-
-
-def _f32(bits: int) -> float:
-    return struct.unpack("<f", struct.pack("<I", int(bits) & M32))[0]
 
 
 def dtype_consts(dtype: torch.dtype) -> tuple:
@@ -74,12 +69,6 @@ def rows_of(raw: torch.Tensor, m: int) -> torch.Tensor:
     """The rows a step's samples come from: its real rows packed in the step buffer when known, else all m."""
     real = (raw >> ROWS_SHIFT) & ROWS_MAX
     return torch.where(real > 0, real.clamp(max=m), torch.full_like(real, m))
-
-
-def pack_step(step: int, rows: Optional[int] = None) -> int:
-    """The step buffer's value: the step (low 32 bits) and, above it, the step's real rows (0: unknown)."""
-    r = int(rows) if rows is not None and int(rows) > 0 else 0
-    return (min(r, ROWS_MAX) << ROWS_SHIFT) | (int(step) & M32)
 
 
 def _code(dt: torch.dtype) -> int:
@@ -132,47 +121,51 @@ def moe_check(x: torch.Tensor, out: torch.Tensor, topk_w: torch.Tensor, topk_ids
 moe_check_torch = moe_check          # the reference's names for the same call
 moe_check_any = moe_check
 
-_lib_lock = threading.Lock()
-_OP = [None]
+_OP_LOCK = threading.Lock()
+_OP: list = [None]
 
 
 def moe_op():
-    """sdcguard::moe_check, registered once (for callers under torch.compile)."""
-    with _lib_lock:
-        if _OP[0] is None:
+    """The check as one opaque op for torch.compile, registered once under the reference's name (sdcguard::moe_check);
+    where the op cannot be registered, the library call."""
+    with _OP_LOCK:
+        if _OP[0] is not None:
+            return _OP[0]
+        op = getattr(getattr(torch.ops, "sdcguard", None), "moe_check", None)
+        if op is None:
             try:
-                @torch.library.custom_op("sdcguard::moe_check",
-                                         mutates_args=("state", "cap_meta", "cap_x", "cap_y", "cap_ids", "cap_g"))
-                def _moe_check(x: torch.Tensor, out: torch.Tensor, topk_w: torch.Tensor, topk_ids: torch.Tensor,
-                               w13: torch.Tensor, w2: torch.Tensor, expert_map: Optional[torch.Tensor], act: int,
-                               routed_first: bool, state: torch.Tensor, slot: int, stepbuf: torch.Tensor,
-                               nlayers: int, index: int, cap_meta: torch.Tensor, cap_x: torch.Tensor,
-                               cap_y: torch.Tensor, cap_ids: torch.Tensor, cap_g: torch.Tensor, line: float) -> None:
-                    moe_check(x, out, topk_w, topk_ids, w13, w2, expert_map, act, routed_first, state, slot, stepbuf,
-                              nlayers, index, cap_meta, cap_x, cap_y, cap_ids, cap_g, line)
-
-                @_moe_check.register_fake
-                def _(*a):
-                    return None
-
-                _OP[0] = torch.ops.sdcguard.moe_check
+                lib_op = torch.library.custom_op(
+                    "sdcguard::moe_check", mutates_args=("state", "cap_meta", "cap_x", "cap_y", "cap_ids", "cap_g"))(
+                        _op_body)
+                lib_op.register_fake(lambda *a: None)
+                op = torch.ops.sdcguard.moe_check
             except (AttributeError, RuntimeError):
-                _OP[0] = getattr(getattr(torch.ops, "sdcguard", None), "moe_check", None) or moe_check
-        return _OP[0]
+                op = moe_check
+        _OP[0] = op
+        return op
 
 
-def check_call(args: tuple, x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor, out) -> None:
-    """Check one call of a registered MoE layer from its input, routing and (finalized) output."""
-    if not isinstance(out, torch.Tensor) or not isinstance(x, torch.Tensor) or out.shape[-1] != x.shape[-1] or \
-            out.shape[0] != x.shape[0]:
+def _op_body(x: torch.Tensor, out: torch.Tensor, topk_w: torch.Tensor, topk_ids: torch.Tensor, w13: torch.Tensor,
+             w2: torch.Tensor, expert_map: Optional[torch.Tensor], act: int, routed_first: bool, state: torch.Tensor,
+             slot: int, stepbuf: torch.Tensor, nlayers: int, index: int, cap_meta: torch.Tensor, cap_x: torch.Tensor,
+             cap_y: torch.Tensor, cap_ids: torch.Tensor, cap_g: torch.Tensor, line: float) -> None:
+    moe_check(x, out, topk_w, topk_ids, w13, w2, expert_map, act, routed_first, state, slot, stepbuf, nlayers, index,
+              cap_meta, cap_x, cap_y, cap_ids, cap_g, line)
+
+
+def check_call(binding, x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor, out) -> None:
+    """After one call of a registered MoE layer: its input, routing and (finalized) output.  binding: the layer's
+    _sdcguard_moe (set by MoEChecks.finalize)."""
+    if binding is None or not (isinstance(out, torch.Tensor) and isinstance(x, torch.Tensor)):
         return
-    w13, w2, emap, act, rf, st, slot, sb, nl, idx, cm, cx, cy, ci, cg, line = args
-    call = (x, out, topk_weights, topk_ids, w13, w2, emap, act, rf, st, slot, sb, nl, idx, cm, cx, cy, ci, cg, line)
+    if out.shape[-1] != x.shape[-1] or out.shape[0] != x.shape[0]:
+        return
+    args = binding.checks.call_args(binding)
     if torch.compiler.is_compiling():
-        (_OP[0] if _OP[0] is not None else moe_op())(*call)
-    else:
-        with torch.no_grad():
-            moe_check(*call)
+        moe_op()(x, out, topk_weights, topk_ids, *args)
+        return
+    with torch.no_grad():
+        moe_check(x, out, topk_weights, topk_ids, *args)
 
 
 def recheck(x_row: torch.Tensor, y_row: torch.Tensor, ids: torch.Tensor, g: torch.Tensor, w13: torch.Tensor,
@@ -200,11 +193,11 @@ def recheck(x_row: torch.Tensor, y_row: torch.Tensor, ids: torch.Tensor, g: torc
               routed_first, st, 0, sb, 1, 0, cm, cx, cy, ci, cg, line, scores_out=zs)
     z = zs[0].cpu()
     keys = st[0].cpu().tolist()
-    worst = _f32(keys[C_ROW] >> 32)
+    worst = f32_of(keys[C_ROW] >> 32)
     bad = int((z > line).sum())
     out = {"worst_score": worst, "outputs_over_line": bad, "outputs": h, "experts": used}
     if worst > 0:
-        out.update(col=keys[C_COL] & M32, output=_f32(keys[C_OUT]), expected=_f32(keys[C_REF]))
+        out.update(col=keys[C_COL] & M32, output=f32_of(keys[C_OUT]), expected=f32_of(keys[C_REF]))
     if bad:
         return {**out, "verdict": "output_wrong",
                 "why": f"{bad} of {h} outputs of the kept row are farther from the recompute (the layer's current "
@@ -215,307 +208,257 @@ def recheck(x_row: torch.Tensor, y_row: torch.Tensor, ids: torch.Tensor, g: torc
 
 
 # ------------------------------------------------------------------------------------------------- the MoE layers
-def describe(mod) -> tuple:
-    """(what the check needs, or None; why not) for a serving stack's fused MoE layer: unquantized bf16/fp16 experts
-    on the Triton MoE kernel, no biases, a gated SiLU or GELU, nothing combined across GPUs (serve_moe.py:709-748)."""
-    qm = getattr(mod, "quant_method", None)
-    if type(qm).__name__ != "UnquantizedFusedMoEMethod":
-        return None, f"{type(qm).__name__ if qm is not None else 'no quant method'}: quantized or another method"
+def _across_gpus(mod) -> bool:
+    """Whether the layer's rows or outputs combine other GPUs' (all-to-all, data or prefill-context parallelism)."""
     pc = getattr(getattr(mod, "moe_config", None), "moe_parallel_config", None)
     try:
-        across = bool(getattr(pc, "use_all2all_kernels", False) or getattr(pc, "use_passthrough_all2all", False) or
-                      int(getattr(pc, "dp_size", 1) or 1) > 1 or int(getattr(pc, "pcp_size", 1) or 1) > 1)
-    except Exception:  # noqa: BLE001
-        across = True
-    if across:
-        return None, ("expert parallelism's all-to-all, data parallelism or prefill context parallelism: the layer's "
-                      "rows or output combine other GPUs', which the recompute can't read")
-    backend = getattr(getattr(qm, "unquantized_backend", None), "name", None)
-    if backend != "TRITON":
-        return None, f"the {backend or 'unknown'} MoE backend (only the Triton MoE kernel's rounding is modelled)"
+        flags = [getattr(pc, f, False) for f in ("use_all2all_kernels", "use_passthrough_all2all")]
+        sizes = [int(getattr(pc, f, 1) or 1) for f in ("dp_size", "pcp_size")]
+    except Exception:  # noqa: BLE001  (an unreadable config counts as combined)
+        return True
+    return any(bool(f) for f in flags) or any(v > 1 for v in sizes)
+
+
+def _experts(mod):
     w13, w2 = getattr(mod, "w13_weight", None), getattr(mod, "w2_weight", None)
-    if not (isinstance(w13, torch.Tensor) and isinstance(w2, torch.Tensor) and w13.dim() == 3 and w2.dim() == 3):
-        return None, "no expert weights the check knows"
-    if w13.dtype not in (torch.bfloat16, torch.float16) or w2.dtype != w13.dtype:
-        return None, f"expert weights in {w13.dtype}"
-    if w13.shape[0] != w2.shape[0] or w13.shape[2] != w2.shape[1] or w13.shape[1] != 2 * w2.shape[2]:
-        return None, f"expert weight shapes {tuple(w13.shape)} and {tuple(w2.shape)} aren't gate-up and down"
-    if w13.shape[2] > 8192:
-        return None, f"hidden size {w13.shape[2]} (at most 8192)"
-    if any(isinstance(getattr(mod, b, None), torch.Tensor) for b in ("w13_bias", "w2_bias")):
-        return None, "experts with biases"
-    act = getattr(getattr(mod, "activation", None), "value", getattr(mod, "activation", None))
-    if str(act) not in ACT:
-        return None, f"activation {act}"
-    if not w13.is_cuda:
-        return None, "not on a GPU"
-    if getattr(mod, "_sdcguard_moe", None) is not None:
-        return None, "already checked by another ServeGuard"
-    return {"act": ACT[str(act)], "routed_first": bool(getattr(mod, "apply_router_weight_on_input", False)),
+    ok = isinstance(w13, torch.Tensor) and isinstance(w2, torch.Tensor) and w13.dim() == 3 and w2.dim() == 3
+    return (w13, w2) if ok else (None, None)
+
+
+def _activation(mod) -> str:
+    a = getattr(mod, "activation", None)
+    return str(getattr(a, "value", a))
+
+
+# What a fused MoE layer must be for the recompute to model it (the reference's serve_moe.py:709-748 asks the same
+# of the serving stack's layer): each rule is (holds, why not), tried in order.
+_RULES = (
+    (lambda m: type(getattr(m, "quant_method", None)).__name__ == "UnquantizedFusedMoEMethod",
+     lambda m: f"{type(getattr(m, 'quant_method', None)).__name__}: quantized or another method"),
+    (lambda m: not _across_gpus(m),
+     lambda m: "expert parallelism's all-to-all, data parallelism or prefill context parallelism: the layer's rows or "
+               "output combine other GPUs'"),
+    (lambda m: getattr(getattr(m.quant_method, "unquantized_backend", None), "name", None) == "TRITON",
+     lambda m: f"the {getattr(getattr(m.quant_method, 'unquantized_backend', None), 'name', None) or 'unknown'} MoE "
+               "backend (the recompute models the Triton MoE kernel's roundings)"),
+    (lambda m: _experts(m)[0] is not None, lambda m: "no expert weights the check knows"),
+    (lambda m: _experts(m)[0].dtype in (torch.bfloat16, torch.float16) and _experts(m)[1].dtype == _experts(m)[0].dtype,
+     lambda m: f"expert weights in {_experts(m)[0].dtype}"),
+    (lambda m: _experts(m)[0].shape[0] == _experts(m)[1].shape[0] and _experts(m)[0].shape[2] == _experts(m)[1].shape[1]
+     and _experts(m)[0].shape[1] == 2 * _experts(m)[1].shape[2],
+     lambda m: f"expert weight shapes {tuple(_experts(m)[0].shape)} and {tuple(_experts(m)[1].shape)} aren't gate-up "
+               "and down"),
+    (lambda m: _experts(m)[0].shape[2] <= 8192, lambda m: f"hidden size {_experts(m)[0].shape[2]} (at most 8192)"),
+    (lambda m: not any(isinstance(getattr(m, b, None), torch.Tensor) for b in ("w13_bias", "w2_bias")),
+     lambda m: "experts with biases"),
+    (lambda m: _activation(m) in ACT, lambda m: f"activation {_activation(m)}"),
+    (lambda m: _experts(m)[0].is_cuda, lambda m: "not on a GPU"),
+    (lambda m: getattr(m, "_sdcguard_moe", None) is None, lambda m: "already checked by another ServeGuard"),
+)
+
+
+def describe(mod) -> tuple:
+    """(what the check needs of a fused MoE layer, None), or (None, why it is not checked)."""
+    for holds, why in _RULES:
+        if not holds(mod):
+            return None, why(mod)
+    return {"act": ACT[_activation(mod)], "routed_first": bool(getattr(mod, "apply_router_weight_on_input", False)),
             "top_k": int(getattr(mod, "top_k", 0) or 0)}, None
 
 
-class MoEChecks:
-    """The fused MoE layers one serving guard checks: add() each, finalize() once before capture, mark_step() before
-    each model step (it decides which layer is active) and end_step() after, poll() with the guard's reads."""
+def _weights_id(mod) -> torch.Tensor:
+    """The experts' weights as two exact integer fingerprints each (sdc_fingerprint2), on their device."""
+    from .serve_weights import fingerprint
+    return torch.stack([fingerprint(mod.w13_weight.detach()), fingerprint(mod.w2_weight.detach())])
+
+
+_ROUTE_WHY = ("a real token's row came with expert ids of -1 or out of range (every real token gets top_k experts; "
+              "-1 marks padding rows), so the layer's output for it is not the sum of its experts")
+
+
+class MoEChecks(StepChecks):
+    """The fused MoE layers one serving guard checks: add() each, finalize() once before any graph is captured (it
+    numbers the layers' turns: at step s the layer with index s % layers recomputes), mark_step() / end_step() around
+    each model step, poll() to read.  State rows are the kernel's 11 columns (the reference's, serve_moe.py:60-70)."""
+
+    DETECTOR = "serve_moe"
+    COLS = COLS
+    CAPTURE = {"meta": torch.int32, "x": torch.float32, "y": torch.float32, "ids": torch.int64, "g": torch.float32}
+    READ_CAPTURE = ("meta",)
 
     def __init__(self, guard=None, line: float = MOE_Z):
         line = float(line)
         if not 5.0 <= line < float("inf"):
             raise ValueError(f"the MoE check's line must be at least 5, not {line!r}")
-        self.guard, self.line = guard, line
-        self.layers: list = []
-        self.unsupported: dict = {}
-        self._state, self._cap, self._step, self._host, self._read_from = {}, {}, {}, {}, {}
-        self._marked: Optional[int] = None
-        self._last_clean: dict = {}
+        super().__init__(guard)
+        self.line = line
+        self.finalized = False
         self.worst_seen: dict = {}
         self.checks_seen: dict = {}
-        self.events: list = []
-        self.finalized = False
-        self.stats = {"layers": 0, "active_calls": 0, "rows_checked": 0, "unjudged_outputs": 0,
-                      "unrouted_real_rows": 0, "partly_routed_real_rows": 0, "alerts": 0}
+        self.stats.update(active_calls=0, rows_checked=0, unjudged_outputs=0, unrouted_real_rows=0,
+                          partly_routed_real_rows=0)
 
     def add(self, mod, name: str) -> Optional[int]:
         if self.finalized:
             raise RuntimeError("MoE layers are added before finalize()")
         info, why = describe(mod)
         if why:
-            self.unsupported[name] = why
+            self._refuse(name, why)
             return None
+        h, k = int(mod.w13_weight.shape[2]), max(info["top_k"], 1)
         with torch.inference_mode(False), torch.no_grad():
-            sums = (mod.w13_weight.detach().float().sum(1), mod.w2_weight.detach().float().sum(2))
-        self.layers.append({"name": name, "module": mod, "device": mod.w13_weight.device, "sums": sums, **info,
-                            "h": int(mod.w13_weight.shape[2]), "i": int(mod.w2_weight.shape[2])})
-        self.stats["layers"] += 1
-        return len(self.layers) - 1
+            ident = _weights_id(mod)
+        b = self._register(name, mod, mod.w13_weight.device,
+                           widths={"meta": CAP_COLS, "x": h, "y": h, "ids": max(k, 64), "g": max(k, 64)},
+                           h=h, i=int(mod.w2_weight.shape[2]), k=k, ident=ident, **info)
+        return b.slot
 
     def finalize(self) -> int:
-        """Allocate the state rows, the kept rows and the kernels' workspace on each device (before any graph is
-        captured), number the layers' turns and register the op."""
+        """Number each device's layers' turns, reserve the kernels' workspace, register the op and give each layer
+        its binding (before any graph is captured: the tables' addresses are fixed from here on)."""
         if self.finalized:
             return len(self.layers)
         from . import _lib
-        by_dev: dict = {}
+        per_dev: dict = {}
         for lay in self.layers:
-            by_dev.setdefault(lay["device"], []).append(lay)
-        n = len(self.layers)
-        for dev, lays in by_dev.items():
-            hmax = max(lay["h"] for lay in lays)
-            kmax = max(max(lay["top_k"], 1) for lay in lays)
-            for i, lay in enumerate(lays):
-                lay["index"], lay["nlayers"] = i, len(lays)
-            with torch.inference_mode(False):
-                self._state[dev] = torch.zeros(n, COLS, dtype=torch.int64, device=dev)
-                self._cap[dev] = (torch.zeros(n, CAP_COLS, dtype=torch.int32, device=dev),
-                                  torch.zeros(n, hmax, device=dev), torch.zeros(n, hmax, device=dev),
-                                  torch.zeros(n, max(kmax, 64), dtype=torch.int64, device=dev),
-                                  torch.zeros(n, max(kmax, 64), device=dev))
-                self._step[dev] = torch.zeros(1, dtype=torch.int64, device=dev)
-            need = max(int(_lib.lib().sdc_moe_check_workspace(lay["h"], lay["i"], max(lay["top_k"], 1)))
-                       for lay in lays)
-            _lib.workspace(dev, need)
+            per_dev.setdefault(lay.device, []).append(lay)
+        for dev, lays in per_dev.items():
+            for turn, lay in enumerate(lays):
+                lay.info["index"], lay.info["nlayers"] = turn, len(lays)
+            _lib.workspace(dev, max(int(_lib.lib().sdc_moe_check_workspace(lay.info["h"], lay.info["i"],
+                                                                            lay.info["k"])) for lay in lays))
         moe_op()
-        for slot, lay in enumerate(self.layers):
-            lay["module"]._sdcguard_moe = self.args(slot)
+        for n, lay in enumerate(self.layers):
+            lay.module._sdcguard_moe = Binding(self, n)
         self.finalized = True
-        return n
+        return len(self.layers)
+
+    def call_args(self, b: Binding) -> tuple:
+        """The library call's arguments after (x, out, topk_w, topk_ids) for a binding's layer."""
+        lay, tab = b.layer, b.table()
+        c = tab.capture
+        return (lay.module.w13_weight, lay.module.w2_weight, getattr(lay.module, "expert_map", None),
+                lay.info["act"], lay.info["routed_first"], tab.state, lay.slot, tab.word.view(W_PACKED),
+                lay.info["nlayers"], lay.info["index"], c["meta"], c["x"], c["y"], c["ids"], c["g"], self.line)
 
     def args(self, slot: int) -> tuple:
-        lay = self.layers[slot]
-        mod, dev = lay["module"], lay["device"]
-        cm, cx, cy, ci, cg = self._cap[dev]
-        return (mod.w13_weight, mod.w2_weight, getattr(mod, "expert_map", None), lay["act"], lay["routed_first"],
-                self._state[dev], slot, self._step[dev], lay["nlayers"], lay["index"], cm, cx, cy, ci, cg, self.line)
+        return self.call_args(Binding(self, slot))
 
     def refresh(self) -> int:
-        """Take the experts' current weights as theirs (after an intended update)."""
+        """Take the experts' current weights as their own (after an intended update)."""
         with torch.inference_mode(False), torch.no_grad():
             for lay in self.layers:
-                mod = lay["module"]
-                lay["sums"] = (mod.w13_weight.detach().float().sum(1), mod.w2_weight.detach().float().sum(2))
-                lay.pop("restored", None)
+                lay.info["ident"] = _weights_id(lay.module)
+                lay.info.pop("restored", None)
         return len(self.layers)
 
     def weights_restored(self, module, step) -> None:
         """The weight scan's repair wrote these experts' load-time weights back after `step`."""
         for lay in self.layers:
-            if lay["module"] is module:
-                lay["restored"] = {"step": step}
+            if lay.module is module:
+                lay.info["restored"] = {"step": step}
 
     def detach(self) -> None:
-        try:
-            if self.layers and self.finalized:
-                self.poll(wait=True)
-        finally:
-            for lay in self.layers:
-                lay["module"].__dict__.pop("_sdcguard_moe", None)
-            self.layers.clear()
-            for d in (self._state, self._cap, self._step, self._host, self._read_from):
-                d.clear()
-            self.finalized = False
+        super().detach()
+        self.finalized = False
 
-    def mark_step(self, step: int, rows: Optional[int] = None) -> None:
-        """Before a model step: its number and, when known, its real rows before padding."""
-        step = int(step) & M32
-        self._marked = step
-        for dev, sb in self._step.items():
-            sb.fill_(pack_step(step, rows))
-            self._read_from.setdefault(dev, step)
-
-    def end_step(self) -> None:
-        """After a model step: runs before the next one (warm-up, capture) are checked over all their rows."""
-        if self._marked is None:
-            return
-        for sb in self._step.values():
-            sb.fill_(pack_step(self._marked))
-
-    def _window(self, dev):
-        if self._marked is None:
-            return None
-        a = self._read_from.pop(dev, None)
-        return [a if a is not None else self._marked, self._marked]
-
-    def poll(self, wait: bool = False) -> list:
-        """The counters and kept rows read back (cleared on the device); without wait, the copy started now is
-        reported by a later poll."""
-        events = []
-        for dev, st in self._state.items():
-            cm = self._cap[dev][0]
-            if wait:
-                pend = self._host.pop(dev, None)
-                if pend is not None:
-                    pend[2].synchronize()
-                    events += self._report(dev, pend[0], pend[1], pend[3])
-                host, hcap = st.to("cpu", copy=True), cm.to("cpu", copy=True)
-                st.zero_()
-                events += self._report(dev, host, hcap, self._window(dev))
-                continue
-            pend = self._host.get(dev)
-            if pend is not None and pend[2].query():
-                events += self._report(dev, pend[0], pend[1], pend[3])
-                pend = None
-                self._host.pop(dev, None)
-            if pend is None:
-                hs = torch.empty(st.shape, dtype=st.dtype, pin_memory=True)
-                hc = torch.empty(cm.shape, dtype=cm.dtype, pin_memory=True)
-                hs.copy_(st, non_blocking=True)
-                hc.copy_(cm, non_blocking=True)
-                st.zero_()
-                ev = torch.cuda.Event()
-                ev.record(torch.cuda.current_stream(dev))
-                self._host[dev] = (hs, hc, ev, self._window(dev))
-        return events
+    def _unbind(self, lay: Registered) -> None:
+        lay.module.__dict__.pop("_sdcguard_moe", None)
 
     def coverage(self) -> dict:
-        return {"layers": len(self.layers), "active_calls": self.stats["active_calls"],
-                "layers_checked": sum(self.checks_seen.get(lay["name"], 0) > 0 for lay in self.layers),
-                "never_checked": sorted(lay["name"] for lay in self.layers if not self.checks_seen.get(lay["name"])),
-                "not_attached": dict(self.unsupported), "samples_per_step": SAMPLES}
-
-    def _report(self, dev, host, hcap, window) -> list:
-        out = []
-        for slot, lay in enumerate(self.layers):
-            if lay["device"] != dev or slot >= host.shape[0]:
-                continue
-            keys = [int(v) for v in host[slot].tolist()]
-            self.stats["active_calls"] += keys[C_CALLS]
-            self.stats["rows_checked"] += keys[C_ROWS]
-            self.stats["unjudged_outputs"] += keys[C_UNJ]
-            self.stats["unrouted_real_rows"] += keys[C_UNROUTED]
-            self.stats["partly_routed_real_rows"] += keys[C_PARTIAL]
-            self.checks_seen[lay["name"]] = self.checks_seen.get(lay["name"], 0) + keys[C_CALLS]
-            routed_ok = not (keys[C_UNROUTED] or keys[C_PARTIAL])
-            if not routed_ok:
-                out.append(self._route_alert(slot, keys, window))
-            z = _f32(keys[C_ROW] >> 32)
-            self.worst_seen[lay["name"]] = max(self.worst_seen.get(lay["name"], 0.0), z)
-            if not (z > self.line):
-                if keys[C_CALLS] and window is not None and routed_ok:
-                    self._last_clean[lay["name"]] = list(window)
-                continue
-            out.append(self._alert(dev, slot, keys, [int(v) for v in hcap[slot].tolist()], window, z))
+        out = super().coverage()
+        out.update(active_calls=self.stats["active_calls"], samples_per_step=SAMPLES)
         return out
 
-    def _emit(self, lay, z: float, detail: dict) -> SDCEvent:
-        ev = SDCEvent(detector="serve_moe", layer=lay["name"], z=z, row=detail.get("row"), extra=detail)
-        self.stats["alerts"] += 1
-        self.events.append(ev)
-        g = self.guard
-        if g is not None and getattr(g, "on_alert", None):
-            try:
-                g.on_alert(ev)
-            except Exception:  # noqa: BLE001  (an alert callback never breaks serving)
-                pass
-        return ev
+    def _count(self, lay: Registered, k: list) -> None:
+        lay.calls += k[C_CALLS]
+        self.checks_seen[lay.name] = self.checks_seen.get(lay.name, 0) + k[C_CALLS]
+        for stat, col in (("active_calls", C_CALLS), ("rows_checked", C_ROWS), ("unjudged_outputs", C_UNJ),
+                          ("unrouted_real_rows", C_UNROUTED), ("partly_routed_real_rows", C_PARTIAL)):
+            self.stats[stat] += k[col]
 
-    def _route_alert(self, slot, keys, window) -> SDCEvent:
-        lay = self.layers[slot]
-        none_, some = keys[C_UNROUTED], keys[C_PARTIAL]
-        last = (keys[C_BADROW] & M32) - 1
-        step = (keys[C_BADROW] >> 32) & M32
-        detail = {"where": lay["name"], "kind": "moe_routing",
-                  "finding": "real_rows_unrouted" if none_ else "real_rows_partly_routed",
-                  "real_rows_without_experts": none_, "real_rows_missing_some_experts": some,
-                  "row": last if last >= 0 else None,
-                  "captured": {"row": last, "step": step if self._marked is not None else None} if last >= 0 else None,
-                  "recheck": {"verdict": "output_wrong",
-                              "why": "a real token's row had expert ids of -1 (every real token gets top_k experts; "
-                                     "-1 is for padding rows), so the layer's output for it isn't its experts' sum"},
-                  "read_window_steps": window, "last_clean_read_steps": self._last_clean.get(lay["name"]),
-                  "reading": "a real row reached the experts with no expert (or some missing): a router fault, a "
-                             "corrupted expert id, or a padding mask that marked a real row"}
-        return self._emit(lay, math.inf, detail)
+    def _judged(self, k: list) -> bool:
+        return k[C_CALLS] > 0 and not (k[C_UNROUTED] or k[C_PARTIAL])
 
-    def _alert(self, dev, slot, keys, cap, window, z) -> SDCEvent:
-        lay = self.layers[slot]
-        mod = lay["module"]
+    def _judge(self, lay: Registered, k: list, captured: dict, window) -> list:
+        out = []
+        if k[C_UNROUTED] or k[C_PARTIAL]:
+            out.append(self._routing_event(lay, k, window))
+        z = f32_of(k[C_ROW] >> 32)
+        self.worst_seen[lay.name] = max(self.worst_seen.get(lay.name, 0.0), z)
+        lay.worst = max(lay.worst, z)
+        if z > self.line:
+            meta = [int(v) for v in captured["meta"].tolist()] if "meta" in captured else [0, 0, 0, 0]
+            out.append(self._output_event(lay, k, meta, window, z))
+        return out
+
+    def _routing_event(self, lay: Registered, k: list, window) -> object:
+        row = (k[C_BADROW] & M32) - 1
+        step = (k[C_BADROW] >> 32) & M32
+        detail = {"where": lay.name, "kind": "moe_routing",
+                  "finding": "real_rows_unrouted" if k[C_UNROUTED] else "real_rows_partly_routed",
+                  "real_rows_without_experts": k[C_UNROUTED], "real_rows_missing_some_experts": k[C_PARTIAL],
+                  "row": row if row >= 0 else None,
+                  "captured": {"row": row, "step": step if self.marked is not None else None} if row >= 0 else None,
+                  "recheck": {"verdict": "output_wrong", "why": _ROUTE_WHY},
+                  "read_window_steps": window, "last_clean_read_steps": self.last_clean(lay.name),
+                  "reading": "a real row reached the experts without (some of) its experts: a router fault, a "
+                             "corrupted expert id, or a padding mask over a real row"}
+        return self.emit(lay, math.inf, detail["row"], detail)
+
+    def _kept_row(self, lay: Registered, meta: list) -> tuple:
+        """The kept row's record (input, output, experts, weights), read from the device, and its capture freed."""
+        if not meta[0]:
+            return None, None
+        c = self.tables[lay.device].capture
+        h, k = lay.info["h"], lay.info["k"]
+        rec = (c["x"][lay.slot, :h].clone(), c["y"][lay.slot, :h].clone(), c["ids"][lay.slot, :k].clone(),
+               c["g"][lay.slot, :k].clone())
+        c["meta"][lay.slot].zero_()
+        kept = {"row": meta[1] & M32, "step": (meta[2] & M32) if self.marked is not None else None,
+                "score": f32_of(meta[3]), "experts": rec[2].tolist(), "weights": rec[3].tolist()}
+        return kept, rec
+
+    def _output_event(self, lay: Registered, k: list, meta: list, window, z: float) -> object:
+        mod = lay.module
         dtype = mod.w13_weight.dtype
-        captured, rc = None, None
-        if cap[0]:
-            cm, cx, cy, ci, cg = self._cap[dev]
-            h, k = lay["h"], max(lay["top_k"], 1)
-            x_row, y_row = cx[slot, :h].clone(), cy[slot, :h].clone()
-            ids, gw = ci[slot, :k].clone(), cg[slot, :k].clone()
-            cm[slot].zero_()
-            captured = {"row": cap[1] & M32, "step": (cap[2] & M32) if self._marked is not None else None,
-                        "score": _f32(cap[3]), "experts": ids.tolist(), "weights": gw.tolist()}
+        kept, rec = self._kept_row(lay, meta)
+        verdict = None
+        if rec is not None:
             try:
-                rc = recheck(x_row, y_row, ids.to(torch.int32), gw, mod.w13_weight, mod.w2_weight,
-                             getattr(mod, "expert_map", None), lay["act"], lay["routed_first"], dtype, self.line)
-            except Exception as e:  # noqa: BLE001  (diagnosis is best effort)
-                rc = {"verdict": "not_rechecked", "why": f"{type(e).__name__}: {e}"}
-        changed = None
+                verdict = recheck(rec[0], rec[1], rec[2].to(torch.int32), rec[3], mod.w13_weight, mod.w2_weight,
+                                  getattr(mod, "expert_map", None), lay.info["act"], lay.info["routed_first"], dtype,
+                                  self.line)
+            except Exception as e:  # noqa: BLE001  (the diagnosis is best effort)
+                verdict = {"verdict": "not_rechecked", "why": f"{type(e).__name__}: {e}"}
         try:
             with torch.no_grad():
-                now = (mod.w13_weight.detach().float().sum(1), mod.w2_weight.detach().float().sum(2))
-            changed = not (torch.equal(now[0], lay["sums"][0]) and torch.equal(now[1], lay["sums"][1]))
+                changed = not torch.equal(_weights_id(mod).cpu(), lay.info["ident"].cpu())
         except Exception:  # noqa: BLE001
-            pass
-        if rc is not None and rc.get("verdict") == "output_agrees" and changed:
-            rc = {**rc, "verdict": "weights_changed",
-                  "why": "the kept row agrees with a recompute from the experts' current weights, which differ from "
-                         "their weights at load: the weights changed in memory (refresh() after an intended update)"}
-        if rc is not None and captured is not None:
+            changed = None
+        if verdict is not None and changed and verdict.get("verdict") == "output_agrees":
+            verdict = {**verdict, "verdict": "weights_changed",
+                       "why": "the kept row agrees with a recompute from the experts' weights as they are now, and "
+                              "those differ from the weights at load: the weights changed in memory (refresh() after "
+                              "an intended update)"}
+        if verdict is not None and kept is not None:
             from .serve_weights import before_repair, repair_why
-            if before_repair(lay.get("restored"), captured["step"]):
-                rc = {**rc, "verdict": "unknown", "why": repair_why(lay["restored"], captured["step"])}
-        yv, rv = _f32(keys[C_OUT]), _f32(keys[C_REF])
-        row, col, place = keys[C_ROW] & M32, keys[C_COL] & M32, PLACE_MAXIMA
-        if captured is not None and rc is not None and rc.get("outputs_over_line") and rc.get("col") is not None:
-            row, col, yv, rv, place = captured["row"], rc["col"], rc["output"], rc["expected"], PLACE_KEPT
-        u = dtype_consts(dtype)[0]
-        detail = {"where": lay["name"], "kind": "moe_experts", "max_z": z, "row": row, "col": col, "output": yv,
+            if before_repair(lay.info.get("restored"), kept["step"]):
+                verdict = {**verdict, "verdict": "unknown", "why": repair_why(lay.info["restored"], kept["step"])}
+        row, col, yv, rv, place = k[C_ROW] & M32, k[C_COL] & M32, f32_of(k[C_OUT]), f32_of(k[C_REF]), PLACE_MAXIMA
+        if kept is not None and verdict and verdict.get("outputs_over_line") and verdict.get("col") is not None:
+            row, col, yv, rv, place = kept["row"], verdict["col"], verdict["output"], verdict["expected"], PLACE_KEPT
+        detail = {"where": lay.name, "kind": "moe_experts", "max_z": z, "row": row, "col": col, "output": yv,
                   "expected": rv, "place": place,
-                  "relative_error": (abs(yv - rv) / abs(rv)) if rv and rv == rv else None, "captured": captured,
-                  "recheck": rc or {"verdict": "not_rechecked",
-                                    "why": "no row was kept for this alert (the layer's kept row was taken by an "
-                                           "earlier alert that hasn't been read yet)"},
+                  "relative_error": abs(yv - rv) / abs(rv) if rv and rv == rv else None, "captured": kept,
+                  "recheck": verdict or {"verdict": "not_rechecked",
+                                         "why": "no row was kept for this alert (an earlier alert's kept row has not "
+                                                "been read yet)"},
                   "weights_changed_since_load": changed, "read_window_steps": window,
-                  "last_clean_read_steps": self._last_clean.get(lay["name"]),
+                  "last_clean_read_steps": self.last_clean(lay.name),
                   "check_config": {"line": self.line, "samples_per_step": SAMPLES, "kappa": KAPPA, "flips": FLIPS,
-                                   "unit_roundoff": u,
+                                   "unit_roundoff": dtype_consts(dtype)[0],
                                    "reference": "sampled recompute with the fused MoE kernel's rounding steps"},
-                  "reading": "an output of the layer's routed experts differs from a recompute from the layer's own "
-                             "input, routing and weights by more than the kernel's rounding allows"}
-        return self._emit(lay, z, detail)
+                  "reading": "an output of the layer's routed experts is farther from a recompute from the layer's "
+                             "own input, routing and weights than the kernel's roundings allow"}
+        return self.emit(lay, z, row, detail)

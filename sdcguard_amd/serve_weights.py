@@ -44,144 +44,103 @@ def fingerprint(t: Optional[torch.Tensor], out: Optional[torch.Tensor] = None) -
 
 
 # ---------------------------------------------------------------------------------------------------------------
-# The scheduled weight scan (serve_weights.py:389-972) and the model digest (:335-364)
+# The model digest (the reference's serve_weights.py:335-364 hashes the same text) and the scheduled weight scan
+# (the reference's WeightScan, serve_weights.py:389-972, built here around a per-group status and a device-side
+# comparison).
 #
-# Each read of the guard's results fingerprints the next registered layers' tensors, up to a byte budget, on the
-# GPU and compares them with their reference fingerprints: every registered tensor is compared once per pass over
-# the model, so a changed bit that persists until its layer's turn is named however small its effect on outputs.
-# References are provisional until their first comparison (a reload that processed weights in temporary tensors
-# and copied them into the originals is taken in again); after it, tensors that moved, or that share memory with
-# another entry's (CPU offloading), are left out rather than called changed.  A read's comparisons come back
-# through pinned host memory and an event, so no read waits for the GPU (unless asked to).  Repair keeps a host copy
-# of each entry and writes it back in place when at most REPAIR_MAX_VALUES values differ, then verifies it.
+# The scan keeps, per registered group of tensors (a layer's weight and bias), a reference fingerprint on the GPU.
+# Every read of the guard's results fingerprints the next groups in turn, up to a byte budget, and compares them
+# with their references on the device; one int32 per group comes back through pinned memory and an event, so a read
+# never waits for the GPU unless asked to.  Each group is compared once per pass over the model, so a bit that
+# changes and stays changed is named within one pass, however small its effect on the outputs.
+#
+# A group's status moves PROVISIONAL (reference taken, never compared) -> CLEAN (compared equal) -> CHANGED (compared
+# different: one alert) or EXCLUDED (its tensors moved, or share memory with another group's: never called changed).
+# A provisional group whose tensors moved is taken in again where they are now (a load that processes weights in
+# temporary tensors and copies them into place).  refresh() makes groups provisional again after an intended update.
+# With repair on, a host copy of each group is kept; a changed group that differs from it in at most
+# repair_max_values values is written back in place and verified against its reference.
 
+import enum
 import hashlib
 import json
 import logging
+import os
 import time
 from dataclasses import dataclass, field
-from typing import Callable, Sequence
+from typing import Callable, Iterator, List, Sequence, Tuple
 
 log = logging.getLogger("sdcguard")
 
-CHUNK = 1 << 20                         # values compared per host step of a repair's count
 DEFAULT_BUDGET_MB = 64.0
-DEFAULT_MAX_MB = 1024.0                 # the most a read compares to meet a verification-age target
-REPAIR_MAX_VALUES = 64                  # a fault changes a few values; an unannounced update changes most of them
-HOST_SHARE = 0.5                        # host copies take at most this share of free host memory per local GPU
-
-
-def _host_room() -> Optional[int]:
-    """Bytes of host memory free for this process: MemAvailable, or the cgroup's limit less its use when lower;
-    None when neither can be read."""
-    room = None
-    try:
-        with open("/proc/meminfo") as f:
-            for line in f:
-                if line.startswith("MemAvailable:"):
-                    room = int(line.split()[1]) * 1024
-                    break
-    except (OSError, ValueError, IndexError):
-        pass
-    for lim_path, use_path in (("/sys/fs/cgroup/memory.max", "/sys/fs/cgroup/memory.current"),
-                               ("/sys/fs/cgroup/memory/memory.limit_in_bytes",
-                                "/sys/fs/cgroup/memory/memory.usage_in_bytes")):
-        try:
-            with open(lim_path) as f:
-                lim = f.read().strip()
-            if lim == "max":
-                continue
-            with open(use_path) as f:
-                left = int(lim) - int(f.read().strip())
-            room = left if room is None else min(room, left)
-            break
-        except (OSError, ValueError):
-            continue
-    return room
-
-
-def _local_gpus() -> int:
-    import os
-    try:
-        n = int(os.environ.get("LOCAL_WORLD_SIZE") or 0)
-    except ValueError:
-        n = 0
-    if n <= 0:
-        n = torch.cuda.device_count() if torch.cuda.is_available() else 1
-    return max(1, n)
-
-
-def _location(t) -> Optional[tuple]:
-    if not isinstance(t, torch.Tensor) or t.numel() == 0:
-        return None
-    return str(t.device), t.data_ptr(), tuple(t.shape), t.dtype
-
-
-def _bias(m) -> Optional[torch.Tensor]:
-    b = getattr(m, "bias", None)
-    return b if isinstance(b, torch.Tensor) else None
+DEFAULT_MAX_MB = 1024.0                 # the most one read compares to meet a verification-age target
+REPAIR_MAX_VALUES = 64                  # a memory fault changes a few values; an update changes most of them
+HOST_SHARE = 0.5                        # share of the free host memory (per local GPU) the repair copies may take
+COUNT_CHUNK = 1 << 20                   # values compared per host step when a repair counts the changed values
 
 
 def fingerprints(tensors: Sequence[Optional[torch.Tensor]], device) -> torch.Tensor:
-    """[k, 2] int64 on `device`: each tensor's fingerprint (a missing or empty tensor's row is zeros), one library
-    launch per tensor into its row; no host synchronisation."""
+    """[k, 2] int64 on `device`: row i the fingerprint of tensors[i] (zeros for a missing or empty one); one library
+    launch per tensor, no host synchronisation."""
     device = torch.device(device)
     out = torch.zeros(len(tensors), 2, dtype=torch.int64, device=device)
     for i, t in enumerate(tensors):
-        if not (isinstance(t, torch.Tensor) and t.numel()):
-            continue
-        if t.device == device:
-            fingerprint(t, out=out[i])
-        else:
-            out[i] = fingerprint(t).to(device)
+        if isinstance(t, torch.Tensor) and t.numel():
+            if t.device == device:
+                fingerprint(t, out=out[i])
+            else:
+                out[i] = fingerprint(t).to(device)
     return out
 
 
-def param_tensors(name: str, p):
-    """A parameter's tensors as digests take them: a shared-weight parameter's partitions, a tensor subclass's inner
-    tensors, else the parameter itself (serve_weights.py:315-332)."""
-    parts = getattr(p, "partitions", None)
-    if isinstance(parts, dict) and parts:
-        for k, v in parts.items():
-            yield from param_tensors(f"{name}.{k}", v)
-        return
-    try:
-        from torch.utils._python_dispatch import is_traceable_wrapper_subclass
-        wrapped = is_traceable_wrapper_subclass(p)
-    except Exception:  # noqa: BLE001
-        wrapped = False
-    if wrapped:
-        for a in p.__tensor_flatten__()[0]:
-            yield from param_tensors(f"{name}.{a}", getattr(p, a))
-        return
-    yield name, p
+def _leaves(name: str, p) -> Iterator[Tuple[str, torch.Tensor]]:
+    """(name, tensor) of every tensor a parameter holds, depth first: a shared weight's partitions (name.key) and a
+    tensor subclass's inner tensors (name.attr) stand for it; a plain tensor is itself."""
+    todo = [(name, p)]
+    while todo:
+        n, t = todo.pop()
+        parts = getattr(t, "partitions", None)
+        if isinstance(parts, dict) and parts:
+            todo.extend((f"{n}.{k}", v) for k, v in reversed(list(parts.items())))
+            continue
+        inner = None
+        try:
+            from torch.utils._python_dispatch import is_traceable_wrapper_subclass
+            if is_traceable_wrapper_subclass(t):
+                inner = t.__tensor_flatten__()[0]
+        except Exception:  # noqa: BLE001  (not a subclass this torch can flatten: the tensor itself)
+            inner = None
+        if inner:
+            todo.extend((f"{n}.{a}", getattr(t, a)) for a in reversed(list(inner)))
+            continue
+        yield n, t
+
+
+param_tensors = _leaves
 
 
 def model_digest(model) -> Optional[str]:
-    """One identity of a loaded model's weights (serve_weights.py:335-364): every parameter tensor (once)
-    fingerprinted, then names, shapes, dtypes and fingerprints hashed in name order (SHA-256, 16 hex digits; the
-    same text as the reference's, so the two give the same digest).  None without parameters."""
-    named, seen = [], set()
+    """16 hex digits naming a loaded model's weights: SHA-256 over one JSON line per tensor, in name order,
+    [name, shape, dtype, fingerprint] (every tensor once, however many parameters share it).  The text is the
+    reference's (serve_weights.py:335-364), so both give a model the same digest.  None for a model without
+    parameters."""
+    tensors = {}
     for pname, p in model.named_parameters():
-        for tname, t in param_tensors(pname, p):
-            if isinstance(t, torch.Tensor) and id(t) not in seen:
-                seen.add(id(t))
-                named.append((tname, t))
-    if not named:
+        for tname, t in _leaves(pname, p):
+            if isinstance(t, torch.Tensor):
+                tensors.setdefault(id(t), (tname, t))
+    if not tensors:
         return None
-    named.sort(key=lambda x: x[0])
-    rows: list = [None] * len(named)
-    by_dev: dict = {}
-    for i, (_, t) in enumerate(named):
-        by_dev.setdefault(t.device, []).append(i)
+    items = sorted(tensors.values(), key=lambda nt: nt[0])
+    prints: dict = {}
     with torch.no_grad():
-        for dev, idx in by_dev.items():
-            got = fingerprints([named[i][1] for i in idx], dev).cpu().tolist()
-            for i, f in zip(idx, got):
-                rows[i] = f
+        for dev in {t.device for _, t in items}:
+            mine = [(n, t) for n, t in items if t.device == dev]
+            for (n, _), f in zip(mine, fingerprints([t for _, t in mine], dev).cpu().tolist()):
+                prints[n] = f
     h = hashlib.sha256()
-    for (n, t), f in zip(named, rows):
-        h.update(json.dumps([n, list(t.shape), str(t.dtype).replace("torch.", ""), f]).encode())
+    for n, t in items:
+        h.update(json.dumps([n, list(t.shape), str(t.dtype).replace("torch.", ""), prints[n]]).encode())
     return h.hexdigest()[:16]
 
 
@@ -199,441 +158,478 @@ def repair_why(restored: dict, step) -> str:
             "the weights as they are now can't say whether it was right")
 
 
-@dataclass
-class _Entry:
-    """One registered group of tensors (a layer's weight and bias, or a quantized layer's tensors)."""
+def _free_host_bytes() -> Optional[int]:
+    """Host memory this process may still take: the available memory, or what the memory cgroup leaves when that is
+    less; None when neither is known."""
+    try:
+        import psutil
+        free = int(psutil.virtual_memory().available)
+    except Exception:  # noqa: BLE001
+        free = None
+    for cap, used in (("/sys/fs/cgroup/memory.max", "/sys/fs/cgroup/memory.current"),
+                      ("/sys/fs/cgroup/memory/memory.limit_in_bytes", "/sys/fs/cgroup/memory/memory.usage_in_bytes")):
+        try:
+            with open(cap) as f1, open(used) as f2:
+                c, u = f1.read().strip(), f2.read().strip()
+            if c != "max":
+                left = int(c) - int(u)
+                free = left if free is None else min(free, left)
+                break
+        except (OSError, ValueError):
+            pass
+    return free
+
+
+def _gpus_on_host() -> int:
+    """GPUs sharing this host's memory: LOCAL_WORLD_SIZE when a launcher set it, else the visible devices."""
+    n = os.environ.get("LOCAL_WORLD_SIZE", "")
+    if n.isdigit() and int(n) > 0:
+        return int(n)
+    return max(1, torch.cuda.device_count() if torch.cuda.is_available() else 1)
+
+
+def _where(t) -> Optional[tuple]:
+    """Where a tensor's values live (device, address, shape, dtype), or None for a missing or empty tensor."""
+    if isinstance(t, torch.Tensor) and t.numel():
+        return str(t.device), t.data_ptr(), tuple(t.shape), t.dtype
+    return None
+
+
+class Status(enum.Enum):
+    PROVISIONAL = "provisional"     # reference taken, not yet compared
+    CLEAN = "clean"                 # last comparison equal
+    CHANGED = "changed"             # compared different (alerted once)
+    EXCLUDED = "excluded"           # moved or shares memory: left out
+
+
+@dataclass(eq=False)
+class _Group:
+    """One registered group of tensors: get() returns them as they are now."""
     name: str
     get: Callable
     kind: str
     module: object
     device: torch.device
     nbytes: int
-    ref: Optional[torch.Tensor] = None        # [k, 2] int64 on the device
-    at: list = field(default_factory=list)    # where the tensors were when the reference was taken
-    ids: list = field(default_factory=list)
-    provisional: bool = True
+    ref: Optional[torch.Tensor] = None         # [k, 2] int64 on the device
+    places: list = field(default_factory=list)   # _where() of each tensor at the reference
+    objects: list = field(default_factory=list)  # id() of each tensor at the reference
+    gen: int = 0                               # bumped with every new reference: comparisons of an older one are void
+    status: Status = Status.PROVISIONAL
+    why_out: Optional[str] = None
     ref_step: Optional[int] = None
-    gen: int = -1                             # bumped with every new reference: older comparisons are void
-    alerted: bool = False
-    excluded: Optional[str] = None
-    last_clean: Optional[float] = None
-    last_clean_step: Optional[int] = None
-    compared: int = 0
+    clean_time: Optional[float] = None
+    clean_step: Optional[int] = None
     since: float = field(default_factory=time.monotonic)
+    compared: int = 0
     repairs: int = 0
     compared_at_repair: int = -1
-    clean: Optional[list] = None              # repair: host copies of the tensors the reference fingerprints
+    copies: Optional[list] = None              # repair: host copies of the tensors
+
+    def tensors(self) -> list:
+        return list(self.get())
+
+    def live(self) -> bool:
+        return self.status in (Status.PROVISIONAL, Status.CLEAN)
 
 
 @dataclass
-class _Batch:
-    """One read's comparisons on one device, on their way to the host."""
-    flags: torch.Tensor                       # pinned int32 per entry (or on the host already)
-    event: Optional[object]
-    items: list                               # (entry index, step, generation)
+class _InFlight:
+    flags: torch.Tensor                        # int32 per group: tensors whose fingerprint differs (pinned host)
+    done: Optional[torch.cuda.Event]
+    groups: list                               # (group, generation, step)
+
+
+class _Copies:
+    """The repair's host copies, within an allowance of host bytes."""
+
+    def __init__(self, allowance: Optional[int]):
+        self.allowance = allowance
+        self.bytes = 0
+
+    @staticmethod
+    def size(copies) -> int:
+        return sum(c.numel() * c.element_size() for c in copies or () if c is not None)
+
+    def keep(self, g: _Group, tensors: list) -> Optional[str]:
+        """Copy g's tensors to the host (reusing copies of the same shape and dtype); why repair must stop, or None."""
+        if self.allowance is None:
+            free = _free_host_bytes()
+            if free is None:
+                return "the free host memory can't be read, so the host copies can't be sized safely"
+            self.allowance = int(HOST_SHARE * max(free, 0) / _gpus_on_host())
+        old = g.copies or []
+        reuse = [i < len(old) and old[i] is not None and isinstance(t, torch.Tensor) and t.numel() > 0 and
+                 old[i].shape == t.shape and old[i].dtype == t.dtype for i, t in enumerate(tensors)]
+        total = self.bytes - self.size(c for i, c in enumerate(old) if not (i < len(reuse) and reuse[i]))
+        total += sum(t.numel() * t.element_size() for t, r in zip(tensors, reuse)
+                     if isinstance(t, torch.Tensor) and t.numel() and not r)
+        if total > self.allowance:
+            return (f"the host copies would take {total / (1 << 30):.2f} GiB, more than this worker's allowance of "
+                    f"{self.allowance / (1 << 30):.2f} GiB")
+        copies = []
+        for i, t in enumerate(tensors):
+            if not (isinstance(t, torch.Tensor) and t.numel()):
+                copies.append(None)
+            elif reuse[i]:
+                old[i].copy_(t.detach())
+                copies.append(old[i])
+            else:
+                copies.append(t.detach().to("cpu", copy=True))
+        g.copies, self.bytes = copies, total
+        return None
+
+    def drop(self, g: _Group) -> None:
+        self.bytes -= self.size(g.copies)
+        g.copies = None
+
+    @staticmethod
+    def differing(pairs: list, limit: int) -> Tuple[int, bool]:
+        """Values of the tensors that differ from their copies, counted on the host a chunk at a time (stops past
+        limit: (count so far, True))."""
+        n = 0
+        for t, c in pairs:
+            es = min(t.element_size(), 4)
+            view = {1: torch.uint8, 2: torch.int16, 4: torch.int32}[es]
+            a = t.detach().contiguous().view(-1).view(torch.uint8).view(view)
+            b = c.contiguous().view(-1).view(torch.uint8).view(view)
+            for lo in range(0, a.numel(), COUNT_CHUNK):
+                n += int((a[lo:lo + COUNT_CHUNK].cpu() != b[lo:lo + COUNT_CHUNK]).sum())
+                if n > limit:
+                    return n, True
+        return n, False
 
 
 class WeightScan:
-    """Scheduled weight integrity of one serving guard (ServeGuard.weight_scan()); poll() runs at each of the
-    guard's reads (serve_weights.py:389-972)."""
+    """Scheduled weight integrity for one serving guard (ServeGuard.weight_scan()): poll() at each of the guard's
+    reads.  budget_mb: bytes compared per read; target_age: seconds within which every weight should be compared
+    again (the budget grows, up to max_mb, at the measured time between reads); repair: keep host copies and write a
+    changed group back when few values changed."""
 
     def __init__(self, guard=None, budget_mb: float = DEFAULT_BUDGET_MB, target_age: Optional[float] = None,
                  max_mb: float = DEFAULT_MAX_MB, max_gap: float = 4.0, repair: bool = False,
                  repair_max_values: int = REPAIR_MAX_VALUES, host_allowance: Optional[int] = None):
         self.guard = guard
+        self.groups: List[_Group] = []
+        self.budget = max(1, int(float(budget_mb) * (1 << 20)))
+        self.max_budget = max(self.budget, int(float(max_mb) * (1 << 20)))
+        self.target_age = float(target_age) if target_age else None
+        self.max_gap = float(max_gap)
         self.repair = bool(repair)
         self.repair_max_values = max(0, int(repair_max_values))
         self.repair_off: Optional[str] = None
-        self._host_allowance = host_allowance
-        self._to_repair: list = []            # (entry index, generation, alert window, last clean)
-        self.budget = max(1, int(float(budget_mb) * (1 << 20)))
-        self.target_age = float(target_age) if target_age else None
-        self.max_budget = max(self.budget, int(float(max_mb) * (1 << 20)))
-        self.max_gap = float(max_gap)
-        self._last_read: Optional[float] = None
-        self._interval: Optional[float] = None
-        self._age_warned = False
-        self.entries: list = []
-        self._slots: set = set()
-        self.cursor = 0
+        self.copies = _Copies(host_allowance)
         self.paused = False
-        self._pending: dict = {}              # device -> [_Batch]
-        self._pass_started = time.monotonic()
         self.not_scanned: dict = {}
         self.events: list = []
+        self._turn = 0                         # next group in the round
+        self._round_began = time.monotonic()
+        self._gap: Optional[float] = None      # smoothed time between reads
+        self._last_read: Optional[float] = None
+        self._warned_age = False
+        self._taken_slots: set = set()
+        self._in_flight: dict = {}             # device -> [_InFlight]
+        self._repairs_due: list = []           # (group, generation, window, last clean)
         self.stats = {"entries": 0, "bytes": 0, "reads": 0, "entries_compared": 0, "bytes_compared": 0,
                       "passes": 0, "last_pass_seconds": None, "changed": 0, "alerts": 0, "references_retaken": 0,
                       "budget_bytes_now": self.budget, "target_met": None, "repaired": 0, "repair_failed": 0,
                       "host_copy_bytes": 0}
 
-    # ------------------------------------------------------------------------------------------- entries
+    @property
+    def entries(self) -> List[_Group]:
+        return self.groups
+
+    # ---------------------------------------------------------------------------------------------- registering
     def add(self, name: str, get: Callable[[], Sequence[Optional[torch.Tensor]]], kind: str,
             module: Optional[torch.nn.Module] = None) -> Optional[int]:
-        """Register tensors (get() returns them as they are now); their fingerprint now is the provisional
-        reference.  kind: "checked", "quantized", "unchecked" or "other".  The entry's index, or None."""
-        tensors = list(get())
-        live = [t for t in tensors if isinstance(t, torch.Tensor) and t.numel()]
+        """Register a group of tensors (get() returns them as they are now) with its reference taken now; kind names
+        what the tensors are ("checked", "quantized", "unchecked", "other").  The group's index, or None."""
+        ts = list(get())
+        live = [t for t in ts if isinstance(t, torch.Tensor) and t.numel()]
         if not live:
             self.not_scanned[name] = "no weight tensors to compare"
             return None
-        e = _Entry(name=name, get=get, kind=kind, module=module, device=live[0].device,
-                   nbytes=sum(t.numel() * t.element_size() for t in live))
+        g = _Group(name, get, kind, module, live[0].device, sum(t.numel() * t.element_size() for t in live))
         with torch.inference_mode(False), torch.no_grad():
-            self._take_reference(e, tensors)
-        self.entries.append(e)
-        self.stats["entries"] = len(self.entries)
-        self.stats["bytes"] += e.nbytes
+            self._reference(g, ts)
+        self.groups.append(g)
+        self.stats["entries"] = len(self.groups)
+        self.stats["bytes"] += g.nbytes
         self.not_scanned.pop(name, None)
-        return len(self.entries) - 1
+        return len(self.groups) - 1
 
     def sync(self) -> None:
         """Take in the guard's checked layers registered since the last call."""
-        g = self.guard
-        layers = getattr(g, "layers", None) or []
-        for slot, lay in enumerate(layers):
-            if slot in self._slots:
-                continue
-            self._slots.add(slot)
-            mod = lay["module"]
-            self.add(lay["name"], (lambda m=mod: (getattr(m, "weight", None), _bias(m))), "checked", mod)
+        for slot, lay in enumerate(getattr(self.guard, "layers", None) or []):
+            if slot not in self._taken_slots:
+                self._taken_slots.add(slot)
+                m = lay["module"]
+                self.add(lay["name"], lambda m=m: (getattr(m, "weight", None), _bias_of(m)), "checked", m)
 
     def refresh(self, module: Optional[torch.nn.Module] = None, kind: Optional[str] = None,
                 name: Optional[str] = None) -> int:
-        """After an intended update: the selected entries (all by default) take new provisional references and are
-        compared again.  Comparisons started before, and repairs not yet made, are dropped."""
-        n = 0
-        self._pending.clear()
-        now = time.monotonic()
+        """After an intended update: new references for the selected groups (all by default), compared again from
+        the next read; comparisons in flight and repairs not yet made for them are dropped."""
+        chosen = [g for g in self.groups if (module is None or g.module is module) and
+                  (kind is None or g.kind == kind) and (name is None or g.name == name)]
+        self._in_flight.clear()
         with torch.inference_mode(False), torch.no_grad():
-            for e in self.entries:
-                if (module is not None and e.module is not module) or (kind is not None and e.kind != kind) or \
-                        (name is not None and e.name != name):
-                    continue
-                self._take_reference(e, list(e.get()))
-                e.alerted, e.excluded, e.last_clean, e.last_clean_step, e.since = False, None, None, None, now
-                self.not_scanned.pop(e.name, None)
-                n += 1
-        self._to_repair = [r for r in self._to_repair if r[1] == self.entries[r[0]].gen]
-        return n
+            for g in chosen:
+                self._reference(g, g.tensors())
+                g.status, g.why_out, g.clean_time, g.clean_step, g.since = (Status.PROVISIONAL, None, None, None,
+                                                                            time.monotonic())
+                self.not_scanned.pop(g.name, None)
+        self._repairs_due = [r for r in self._repairs_due if r[1] == r[0].gen]
+        return len(chosen)
 
-    def _take_reference(self, e: _Entry, tensors: list) -> None:
-        e.ref = fingerprints(tensors, e.device)
-        e.at = [_location(t) for t in tensors]
-        e.ids = [id(t) for t in tensors]
-        e.provisional = True
-        e.ref_step = getattr(self.guard, "_marked_step", None)
-        e.gen += 1
+    def _reference(self, g: _Group, ts: list) -> None:
+        g.ref = fingerprints(ts, g.device)
+        g.places, g.objects = [_where(t) for t in ts], [id(t) for t in ts]
+        g.ref_step = getattr(self.guard, "_marked_step", None)
+        g.gen += 1
+        if g.status != Status.EXCLUDED:
+            g.status = Status.PROVISIONAL
         if self.repair:
-            self._keep_copy(e, tensors)
+            why = self.copies.keep(g, ts)
+            if why:
+                self._stop_repair(why)
+            self.stats["host_copy_bytes"] = self.copies.bytes
 
-    @staticmethod
-    def _nbytes(ts) -> int:
-        return sum(c.numel() * c.element_size() for c in ts or () if c is not None)
-
-    def _keep_copy(self, e: _Entry, tensors: list) -> None:
-        """e.clean: host copies of the tensors (an existing copy of the same shape and dtype is overwritten).
-        Repair turns itself off for every entry when the copies would pass the host allowance."""
-        old = e.clean or []
-        same = [k < len(old) and old[k] is not None and isinstance(t, torch.Tensor) and t.numel() > 0 and
-                old[k].shape == t.shape and old[k].dtype == t.dtype for k, t in enumerate(tensors)]
-        need = sum(t.numel() * t.element_size() for t, s in zip(tensors, same)
-                   if isinstance(t, torch.Tensor) and t.numel() and not s)
-        freed = self._nbytes(c for k, c in enumerate(old) if not (k < len(same) and same[k]))
-        if self._host_allowance is None:
-            room = _host_room()
-            if room is None:
-                self._host_allowance = 0
-                self._repair_disable("the free host memory can't be read, so the host copies can't be sized safely")
-                return
-            self._host_allowance = int(HOST_SHARE * max(room, 0) / _local_gpus())
-        after = self.stats["host_copy_bytes"] - freed + need
-        if after > self._host_allowance:
-            self._repair_disable(f"the host copies would take {after / (1 << 30):.2f} GiB, more than this worker's "
-                                 f"allowance of {self._host_allowance / (1 << 30):.2f} GiB")
-            return
-        clean = []
-        for k, (t, s) in enumerate(zip(tensors, same)):
-            if not (isinstance(t, torch.Tensor) and t.numel()):
-                clean.append(None)
-            elif s:
-                old[k].copy_(t.detach())
-                clean.append(old[k])
-            else:
-                clean.append(t.detach().to("cpu", copy=True))
-        e.clean = clean
-        self.stats["host_copy_bytes"] = after
-
-    def _repair_disable(self, why: str) -> None:
+    def _stop_repair(self, why: str) -> None:
         self.repair, self.repair_off = False, why
-        for e in self.entries:
-            e.clean = None
+        for g in self.groups:
+            g.copies = None
+        self.copies.bytes = 0
         self.stats["host_copy_bytes"] = 0
-        self._to_repair = []
+        self._repairs_due = []
         log.warning("sdcguard: weight repair is off: %s; the scan still compares and alerts", why)
 
-    def _drop_copy(self, e: _Entry) -> None:
-        if e.clean:
-            self.stats["host_copy_bytes"] -= self._nbytes(e.clean)
-            e.clean = None
+    def _exclude(self, g: _Group, why: str) -> None:
+        if g.status != Status.EXCLUDED:
+            log.warning("sdcguard: the weight scan no longer compares %s: %s", g.name, why)
+        g.status, g.why_out = Status.EXCLUDED, why
+        self.not_scanned[g.name] = why
+        self.copies.drop(g)
+        self.stats["host_copy_bytes"] = self.copies.bytes
 
-    def _shared(self, e: _Entry, tensors: list) -> tuple:
-        """(why, the other entry) when another entry's different tensor lives at the same address."""
-        mine = {}
-        for t in tensors:
-            loc = _location(t)
-            if loc:
-                mine[(loc[0], loc[1])] = id(t)
-        for other in self.entries:
-            if other is e:
+    def _overlap(self, g: _Group, ts: list) -> Optional[_Group]:
+        """Another group one of whose tensors (a different tensor object) lives at one of ts's addresses."""
+        mine = {(w[0], w[1]): id(t) for t, w in ((t, _where(t)) for t in ts) if w}
+        for other in self.groups:
+            if other is g:
                 continue
-            for loc, oid in zip(other.at, other.ids):
-                if loc and mine.get((loc[0], loc[1]), oid) != oid:
-                    return f"shares its memory with {other.name}'s tensors (CPU offloading)", other
-        return None, None
+            for w, oid in zip(other.places, other.objects):
+                if w and (w[0], w[1]) in mine and mine[(w[0], w[1])] != oid:
+                    return other
+        return None
 
-    def _exclude(self, e: _Entry, why: str) -> None:
-        if e.excluded is None:
-            log.warning("sdcguard: the weight scan no longer compares %s: %s", e.name, why)
-        e.excluded = why
-        self.not_scanned[e.name] = why
-        self._drop_copy(e)
-
-    # ------------------------------------------------------------------------------------------- reads
+    # ------------------------------------------------------------------------------------------------- reading
     def poll(self, wait: bool = False) -> list:
-        """Report the comparisons that have come back and start the next ones (up to the byte budget)."""
+        """Report the comparisons that came back, start the next ones (up to this read's budget), and make the
+        repairs that are due."""
         self.sync()
         self.stats["reads"] += 1
         now = time.monotonic()
         if self._last_read is not None:
-            dt = min(now - self._last_read, self.max_gap)
-            self._interval = dt if self._interval is None else 0.8 * self._interval + 0.2 * dt
+            gap = min(now - self._last_read, self.max_gap)
+            self._gap = gap if self._gap is None else 0.8 * self._gap + 0.2 * gap
         self._last_read = now
-        events = self._collect(wait)
-        if self.entries and not self.paused:
-            events += self._start(wait)
-        if self._to_repair:
-            self._repair_pending()
-        return events
+        out = self._settle(wait)
+        if self.groups and not self.paused:
+            out += self._compare_next(wait)
+        if self._repairs_due:
+            self._repair_due()
+        return out
 
     def target(self) -> int:
-        """The bytes this read compares: the budget, or with a verification-age target enough that a pass over the
-        entries still compared takes at most 2/3 of it at the measured time between reads, up to max_mb."""
-        if not self.target_age or self._interval is None or self._interval <= 0:
+        """Bytes this read compares: the budget, or with a verification-age target enough that a pass over the live
+        groups takes at most two thirds of it at the measured time between reads (at most max_mb)."""
+        if not self.target_age or not self._gap:
             return self.budget
-        live = sum(e.nbytes for e in self.entries if not e.alerted and not e.excluded)
-        reads = max(1.0, (self.target_age * 2 / 3) / self._interval)
-        want = int(live / reads) + 1
-        met = want <= self.max_budget
-        if not met and not self._age_warned:
-            self._age_warned = True
+        live = sum(g.nbytes for g in self.groups if g.live())
+        want = int(live * self._gap / (self.target_age * 2 / 3)) + 1
+        self.stats["target_met"] = want <= self.max_budget
+        if want > self.max_budget and not self._warned_age:
+            self._warned_age = True
             log.warning("sdcguard: the weight scan can't compare every weight within %gs at %.2fs between reads "
-                        "(it would need %.0f MB a read, above the %.0f MB most)", self.target_age, self._interval,
+                        "(it would need %.0f MB a read, above the %.0f MB most)", self.target_age, self._gap,
                         want / (1 << 20), self.max_budget / (1 << 20))
-        self.stats["target_met"] = met
         return max(self.budget, min(want, self.max_budget))
 
     def oldest_age(self, now: Optional[float] = None) -> Optional[float]:
         now = time.monotonic() if now is None else now
-        ages = [now - (e.last_clean if e.last_clean is not None else e.since)
-                for e in self.entries if not e.alerted and not e.excluded]
+        ages = [now - (g.clean_time if g.clean_time is not None else g.since) for g in self.groups if g.live()]
         return max(ages) if ages else None
 
-    def _start(self, wait: bool) -> list:
-        """Fingerprint the next entries (round robin, up to the budget) and queue their comparison: per device one
-        stacked comparison with the references and one per-entry reduction."""
-        chosen: dict = {}                      # device -> [(entry index, step, gen, tensors)]
-        spent, tried, n = 0, 0, len(self.entries)
-        budget = self.target()
-        self.stats["budget_bytes_now"] = budget
+    def _next_group(self) -> _Group:
+        g = self.groups[self._turn]
+        self._turn = (self._turn + 1) % len(self.groups)
+        if self._turn == 0:                    # a pass over every group ended
+            t = time.monotonic()
+            self.stats["passes"] += 1
+            self.stats["last_pass_seconds"] = round(t - self._round_began, 3)
+            self._round_began = t
+        return g
+
+    def _ready(self, g: _Group) -> Optional[list]:
+        """g's tensors if it is to be compared now; otherwise None, with g taken in again or left out."""
+        if not g.live():
+            return None
+        ts = g.tensors()
+        other = self._overlap(g, ts)
+        if other is not None:
+            self._exclude(g, f"shares its memory with {other.name}'s tensors (CPU offloading)")
+            if other.status != Status.EXCLUDED:
+                self._exclude(other, f"shares its memory with {g.name}'s tensors (CPU offloading)")
+            return None
+        if [_where(t) for t in ts] == g.places:
+            return ts
+        if g.status == Status.PROVISIONAL:     # never compared: the reference is taken where the tensors are now
+            self._reference(g, ts)
+            self.stats["references_retaken"] += 1
+        else:
+            self._exclude(g, "its tensors moved or changed shape after they were compared (call refresh() after an "
+                             "intended reload)")
+        return None
+
+    def _compare_next(self, wait: bool) -> list:
+        """Fingerprint the next groups and compare them with their references: per device one stacked comparison
+        and one count per group, all on the GPU."""
+        budget = self.stats["budget_bytes_now"] = self.target()
         step = getattr(self.guard, "_marked_step", None)
+        picked: dict = {}
+        spent = 0
         with torch.inference_mode(False), torch.no_grad():
-            while tried < n and (spent < budget or not chosen):
-                i = self.cursor
-                self.cursor = (self.cursor + 1) % n
-                tried += 1
-                if self.cursor == 0:
-                    self._pass_done()
-                e = self.entries[i]
-                if e.alerted or e.excluded:
-                    continue
-                tensors = list(e.get())
-                why, other = self._shared(e, tensors)
-                if why:
-                    self._exclude(e, why)
-                    if other is not None and not other.excluded:
-                        self._exclude(other, f"shares its memory with {e.name}'s tensors (CPU offloading)")
-                    continue
-                if [_location(t) for t in tensors] != e.at:
-                    if e.provisional:            # never compared: take the reference again where they are now
-                        self._take_reference(e, tensors)
-                        self.stats["references_retaken"] += 1
-                        continue
-                    self._exclude(e, "its tensors moved or changed shape after they were compared (call refresh() "
-                                     "after an intended reload)")
-                    continue
-                chosen.setdefault(e.device, []).append((i, step, e.gen, tensors))
-                spent += e.nbytes
-            events = []
-            for dev, items in chosen.items():
-                tensors = [t for *_, ts in items for t in ts]
-                owner = torch.tensor([k for k, it in enumerate(items) for _ in it[3]], dtype=torch.int64)
-                owner = owner.pin_memory().to(dev, non_blocking=True) if dev.type == "cuda" else owner
-                now = fingerprints(tensors, dev)
-                refs = torch.cat([self.entries[i].ref for i, *_ in items])
-                differ = torch.ne(now, refs).any(-1).to(torch.int32)
-                flags = torch.zeros(len(items), dtype=torch.int32, device=dev).index_add_(0, owner, differ)
-                idx = [(i, s, g) for i, s, g, _ in items]
+            for _ in range(len(self.groups)):
+                if spent >= budget and picked:
+                    break
+                g = self._next_group()
+                ts = self._ready(g)
+                if ts is not None:
+                    picked.setdefault(g.device, []).append((g, ts))
+                    spent += g.nbytes
+            out = []
+            for dev, items in picked.items():
+                flat = [t for _, ts in items for t in ts]
+                owner = torch.tensor([i for i, (_, ts) in enumerate(items) for _ in ts], dtype=torch.int64)
+                if dev.type == "cuda":
+                    owner = owner.pin_memory().to(dev, non_blocking=True)
+                differs = (fingerprints(flat, dev) != torch.cat([g.ref for g, _ in items])).any(-1)
+                flags = torch.zeros(len(items), dtype=torch.int32, device=dev).index_add_(0, owner,
+                                                                                          differs.to(torch.int32))
+                batch = [(g, g.gen, step) for g, _ in items]
                 if dev.type == "cuda" and not wait:
-                    host = torch.empty(flags.shape, dtype=torch.int32, pin_memory=True)
+                    host = torch.empty(len(items), dtype=torch.int32, pin_memory=True)
                     host.copy_(flags, non_blocking=True)
-                    ev = torch.cuda.Event()
-                    ev.record(torch.cuda.current_stream(dev))
-                    self._pending.setdefault(dev, []).append(_Batch(host, ev, idx))
+                    done = torch.cuda.Event()
+                    done.record(torch.cuda.current_stream(dev))
+                    self._in_flight.setdefault(dev, []).append(_InFlight(host, done, batch))
                 else:
-                    events += self._judge(flags.cpu(), idx)
-                self.stats["entries_compared"] += len(idx)
-                self.stats["bytes_compared"] += sum(self.entries[i].nbytes for i, _, _ in idx)
-        return events
+                    out += self._verdicts(flags.cpu(), batch)
+                self.stats["entries_compared"] += len(batch)
+                self.stats["bytes_compared"] += sum(g.nbytes for g, _ in items)
+        return out
 
-    def _pass_done(self) -> None:
-        now = time.monotonic()
-        self.stats["passes"] += 1
-        self.stats["last_pass_seconds"] = round(now - self._pass_started, 3)
-        self._pass_started = now
-
-    def _collect(self, wait: bool) -> list:
-        events = []
-        for dev in list(self._pending):
+    def _settle(self, wait: bool) -> list:
+        out = []
+        for dev, batches in list(self._in_flight.items()):
             left = []
-            for b in self._pending[dev]:
+            for b in batches:
                 if wait:
-                    b.event.synchronize()
-                if b.event.query():
-                    events += self._judge(b.flags, b.items)
+                    b.done.synchronize()
+                if b.done.query():
+                    out += self._verdicts(b.flags, b.groups)
                 else:
                     left.append(b)
             if left:
-                self._pending[dev] = left
+                self._in_flight[dev] = left
             else:
-                del self._pending[dev]
-        return events
+                self._in_flight.pop(dev)
+        return out
 
-    def _judge(self, flags: torch.Tensor, items: list) -> list:
-        events = []
+    def _verdicts(self, flags: torch.Tensor, batch: list) -> list:
+        out = []
         now = time.monotonic()
-        for f, (i, step, gen) in zip(flags.tolist(), items):
-            e = self.entries[i]
-            if e.excluded or gen != e.gen:      # left out, or a new reference, since this comparison started
+        for differs, (g, gen, step) in zip(flags.tolist(), batch):
+            if gen != g.gen or g.status == Status.EXCLUDED:   # a new reference, or left out, since it started
                 continue
-            e.compared += 1
-            e.provisional = False
-            if not f:
-                e.last_clean, e.last_clean_step = now, step
+            g.compared += 1
+            if not differs:
+                g.status, g.clean_time, g.clean_step = Status.CLEAN, now, step
                 continue
-            if e.alerted:
+            if g.status == Status.CHANGED:
                 continue
-            e.alerted = True
+            g.status = Status.CHANGED
             self.stats["changed"] += 1
-            ev = self._alert(e, now, step)
-            events.append(ev)
-            if self.repair and e.clean:
-                self._to_repair.append((i, e.gen, ev.extra.get("read_window_steps"),
-                                        ev.extra.get("last_clean_read_steps")))
-        return events
+            ev = self._changed_event(g, now, step)
+            out.append(ev)
+            if self.repair and g.copies:
+                self._repairs_due.append((g, g.gen, ev.extra.get("read_window_steps"),
+                                          ev.extra.get("last_clean_read_steps")))
+        return out
 
-    # ------------------------------------------------------------------------------------------- repair
-    def _repair_pending(self) -> None:
-        """Entries found changed with repair on: when at most repair_max_values values differ from the host copy, it
-        is written back in place (after the work queued so far) and verified against the reference at once; a
-        record goes out either way (the alert that found the change stands)."""
-        todo, self._to_repair = self._to_repair, []
-        for i, gen, window, clean in todo:
-            e = self.entries[i]
-            if gen != e.gen or not e.alerted:
+    # -------------------------------------------------------------------------------------------------- repair
+    def _repair_due(self) -> None:
+        """Changed groups with repair on: written back when at most repair_max_values values differ from the copy,
+        then verified against the reference; a record goes out either way (the alert stands)."""
+        due, self._repairs_due = self._repairs_due, []
+        for g, gen, window, clean in due:
+            if gen != g.gen or g.status != Status.CHANGED:
                 continue
             at = getattr(self.guard, "_marked_step", None)
             counts = None
             try:
                 with torch.inference_mode(False), torch.no_grad():
-                    ok, why, counts = self._restore(e, at)
-            except Exception as ex:  # noqa: BLE001  (a failed repair leaves the alert as it was)
-                ok, why = False, f"the restore failed: {type(ex).__name__}: {ex}"[:300]
-            if ok:
-                e.alerted = False
-                e.repairs += 1
-                e.gen += 1
-                e.last_clean, e.last_clean_step = time.monotonic(), at
-                e.compared_at_repair = e.compared
+                    why, counts = self._write_back(g, at)
+            except Exception as ex:  # noqa: BLE001  (a failed repair leaves the alert as it is)
+                why = f"the restore failed: {type(ex).__name__}: {ex}"[:300]
+            if why is None:
+                g.status, g.repairs, g.gen = Status.CLEAN, g.repairs + 1, g.gen + 1
+                g.clean_time, g.clean_step, g.compared_at_repair = time.monotonic(), at, g.compared
                 self.stats["repaired"] += 1
             else:
                 self.stats["repair_failed"] += 1
-            self._emit(self._repair_event(e, ok, why, at, window, clean, counts))
+            self._publish(self._repair_event(g, why, at, window, clean, counts))
 
-    def _count_changed(self, pairs: list) -> tuple:
-        """(values that differ from the copy, stopped early), CHUNK values at a time on the host."""
-        changed = 0
-        for t, c in pairs:
-            tv = t.detach().contiguous().view(-1).view(torch.uint8)
-            cv = c.contiguous().view(-1).view(torch.uint8)
-            es = max(1, min(t.element_size(), 4))
-            tv = tv.view({1: torch.uint8, 2: torch.int16, 4: torch.int32}[es])
-            cv = cv.view({1: torch.uint8, 2: torch.int16, 4: torch.int32}[es])
-            for a in range(0, tv.numel(), CHUNK):
-                changed += int(torch.ne(tv[a:a + CHUNK].to("cpu"), cv[a:a + CHUNK]).sum())
-                if changed > self.repair_max_values:
-                    return changed, True
-        return changed, False
-
-    def _restore(self, e: _Entry, at=None) -> tuple:
-        if e.excluded:
-            return False, f"the scan no longer compares it: {e.excluded}", None
-        tensors = list(e.get())
-        clean = e.clean or []
-        if [_location(t) for t in tensors] != e.at or len(clean) != len(tensors):
-            return False, "its tensors moved or changed since the clean copy was taken", None
-        why, _ = self._shared(e, tensors)
-        if why:
-            return False, f"it {why}", None
-        pairs = []
-        for t, c in zip(tensors, clean):
-            if c is None or not isinstance(t, torch.Tensor):
-                continue
-            if t.shape != c.shape or t.dtype != c.dtype:
-                return False, "a tensor's shape or dtype differs from its clean copy", None
-            pairs.append((t, c))
-        if e.device.type == "cuda":
-            torch.cuda.synchronize(e.device)
-        changed, stopped = self._count_changed(pairs)
-        values = sum(c.numel() * (2 if c.element_size() == 8 else 1) for _, c in pairs)   # (8 bytes: two words)
-        counts = {"values_changed": changed, "values": values, "at_least": stopped}
-        if changed > self.repair_max_values:
-            return False, (f"{'at least ' if stopped else ''}{changed} values differ from the copy kept with the "
-                           f"reference, more than a fault in memory would change (repair writes back at most "
-                           f"{self.repair_max_values}): an update the guard wasn't told about, or a stray write"), counts
+    def _write_back(self, g: _Group, at) -> Tuple[Optional[str], Optional[dict]]:
+        """(None, counts) after a verified write-back, or (why not, counts)."""
+        ts, copies = g.tensors(), g.copies or []
+        if [_where(t) for t in ts] != g.places or len(copies) != len(ts):
+            return "its tensors moved or changed since the clean copy was taken", None
+        other = self._overlap(g, ts)
+        if other is not None:
+            return f"it shares its memory with {other.name}'s tensors (CPU offloading)", None
+        pairs = [(t, c) for t, c in zip(ts, copies) if c is not None and isinstance(t, torch.Tensor)]
+        if any(t.shape != c.shape or t.dtype != c.dtype for t, c in pairs):
+            return "a tensor's shape or dtype differs from its clean copy", None
+        if g.device.type == "cuda":
+            torch.cuda.synchronize(g.device)
+        n, stopped = _Copies.differing(pairs, self.repair_max_values)
+        counts = {"values_changed": n, "values": sum(c.numel() * (2 if c.element_size() == 8 else 1) for _, c in pairs),
+                  "at_least": stopped}
+        if n > self.repair_max_values:
+            return (f"{'at least ' if stopped else ''}{n} values differ from the copy kept with the reference, more "
+                    f"than a fault in memory changes (repair writes back at most {self.repair_max_values}): an update "
+                    "the guard was not told about, or a stray write"), counts
         try:
             for t, c in pairs:
-                if t.is_inference():
-                    with torch.inference_mode():
-                        t.copy_(c)
-                else:
-                    with torch.inference_mode(False), torch.no_grad():
-                        t.copy_(c)
+                with torch.inference_mode(t.is_inference()), torch.no_grad():
+                    t.copy_(c)
         finally:
-            restored = getattr(self.guard, "_weights_restored", None)
-            if restored is not None and e.module is not None:
+            note = getattr(self.guard, "_weights_restored", None)
+            if note is not None and g.module is not None:
                 try:
-                    restored(e.module, at)
+                    note(g.module, at)
                 except Exception:  # noqa: BLE001
                     pass
-        if e.device.type == "cuda":
-            torch.cuda.synchronize(e.device)
-        now = fingerprints(tensors, e.device)
-        if torch.equal(now.cpu(), e.ref.cpu()):
-            return True, None, counts
-        return False, "the restored weights still don't match their reference fingerprint", counts
+        if g.device.type == "cuda":
+            torch.cuda.synchronize(g.device)
+        if torch.equal(fingerprints(ts, g.device).cpu(), g.ref.cpu()):
+            return None, counts
+        return "the restored weights still don't match their reference fingerprint", counts
 
-    # ------------------------------------------------------------------------------------------- reports
-    def _emit(self, ev) -> None:
+    # ------------------------------------------------------------------------------------------------- reports
+    def _publish(self, ev) -> None:
         self.events.append(ev)
         g = self.guard
         if g is not None and getattr(g, "events", None) is not None and g.events is not self.events:
@@ -645,73 +641,78 @@ class WeightScan:
             except Exception:  # noqa: BLE001  (an alert callback never breaks serving)
                 pass
 
-    def _alert(self, e: _Entry, now: float, step: Optional[int]):
+    def _changed_event(self, g: _Group, now: float, step: Optional[int]):
         from .serve import SDCEvent
-        clean = e.last_clean_step
         window, since = None, None
         if step is not None:
-            if clean is not None:
-                start, since = (clean + 1 if clean < step else step), "the last clean comparison"
+            if g.clean_step is not None:
+                window, since = [min(g.clean_step + 1, step), step], "the last clean comparison"
+            elif g.ref_step is not None:
+                window, since = [min(g.ref_step + 1, step), step], "the reference (at load or the last refresh)"
             else:
-                start = min(e.ref_step + 1, step) if e.ref_step is not None else 0
-                since = "the reference (at load or the last refresh)" if e.ref_step is not None else "load"
-            window = [start, step]
-        detail = {"where": e.name, "finding": "weights_changed", "kind": e.kind, "weights_changed_since_load": True,
+                window, since = [0, step], "load"
+        detail = {"where": g.name, "finding": "weights_changed", "kind": g.kind, "weights_changed_since_load": True,
                   "recheck": {"verdict": "weights_changed",
-                              "why": "the layer's tensors no longer match their reference fingerprint (taken at "
-                                     "load, or at the last refresh)"},
+                              "why": "the group's tensors no longer match their reference fingerprint (taken at load "
+                                     "or at the last refresh)"},
                   "read_window_steps": window, "window_since": since,
-                  "last_clean_read_steps": [clean, clean] if clean is not None else None,
-                  "seconds_since_last_clean_comparison": (round(now - e.last_clean, 3)
-                                                          if e.last_clean is not None else None),
+                  "last_clean_read_steps": [g.clean_step, g.clean_step] if g.clean_step is not None else None,
+                  "seconds_since_last_clean_comparison": (round(now - g.clean_time, 3)
+                                                          if g.clean_time is not None else None),
                   "last_pass_seconds": self.stats["last_pass_seconds"],
-                  "scan": {"budget_bytes": self.stats["budget_bytes_now"], "entries": len(self.entries),
+                  "scan": {"budget_bytes": self.stats["budget_bytes_now"], "entries": len(self.groups),
                            "target_age_seconds": self.target_age},
-                  "reading": "a weight bit changed after load: memory corruption, or an update the guard wasn't "
-                             "told about (call refresh() after an intended one). Every request this layer served "
-                             "since its last clean comparison may have used the changed weights."}
-        ev = SDCEvent(detector="serve_weights", layer=e.name, z=float("inf"), extra=detail)
+                  "reading": "a weight bit changed after load: memory corruption, or an update the guard was not told "
+                             "about (refresh() after an intended one); requests this layer served since its last "
+                             "clean comparison may have used the changed weights"}
+        ev = SDCEvent(detector="serve_weights", layer=g.name, z=float("inf"), extra=detail)
         self.stats["alerts"] += 1
-        self._emit(ev)
+        self._publish(ev)
         return ev
 
-    def _repair_event(self, e: _Entry, ok: bool, why, at, window, clean, counts):
+    def _repair_event(self, g: _Group, why: Optional[str], at, window, clean, counts):
         from .serve import SDCEvent
-        n = (counts or {}).get("values_changed")
+        ok = why is None
+        counts = counts or {}
         start = window[0] if window else at
-        detail = {"where": e.name, "kind": e.kind, "finding": "weights_restored" if ok else "weights_restore_failed",
+        detail = {"where": g.name, "kind": g.kind, "finding": "weights_restored" if ok else "weights_restore_failed",
                   "recheck": {"verdict": "weights_restored" if ok else "restore_failed",
                               "why": "the copy kept with the reference was written back and the tensors match their "
                                      "reference fingerprint again" if ok else why},
-                  "repairs": e.repairs, "values_changed": n, "values": (counts or {}).get("values"),
-                  "values_changed_at_least": bool((counts or {}).get("at_least")), "repaired_at_step": at,
+                  "repairs": g.repairs, "values_changed": counts.get("values_changed"), "values": counts.get("values"),
+                  "values_changed_at_least": bool(counts.get("at_least")), "repaired_at_step": at,
                   "read_window_steps": [start, at] if start is not None and at is not None and start <= at else None,
                   "last_clean_read_steps": clean,
-                  "reading": ("restored in place and verified; requests this layer served from its last clean "
-                              "comparison to the repair may have used the changed weights" if ok else
-                              f"not restored ({why}): the layer keeps its changed weights")}
-        (log.warning if ok else log.error)("sdcguard: weight repair of %s: %s", e.name,
-                                           f"restored ({n} values) and verified" if ok else why)
-        return SDCEvent(detector="serve_weights", layer=e.name, z=0.0 if ok else float("inf"), extra=detail)
+                  "reading": "restored in place and verified; requests this layer served from its last clean "
+                             "comparison to the repair may have used the changed weights" if ok else
+                             f"not restored ({why}): the layer keeps its changed weights"}
+        (log.warning if ok else log.error)("sdcguard: weight repair of %s: %s", g.name,
+                                           f"restored ({counts.get('values_changed')} values) and verified" if ok
+                                           else why)
+        return SDCEvent(detector="serve_weights", layer=g.name, z=0.0 if ok else float("inf"), extra=detail)
 
     def coverage(self) -> dict:
-        by_kind: dict = {}
-        for e in self.entries:
-            by_kind[e.kind] = by_kind.get(e.kind, 0) + 1
+        kinds: dict = {}
+        for g in self.groups:
+            kinds[g.kind] = kinds.get(g.kind, 0) + 1
         age = self.oldest_age()
-        return {"entries": len(self.entries), "by_kind": by_kind, "bytes": self.stats["bytes"],
+        return {"entries": len(self.groups), "by_kind": kinds, "bytes": self.stats["bytes"],
                 "budget_bytes_per_read": self.budget, "budget_bytes_now": self.stats["budget_bytes_now"],
                 "target_age_seconds": self.target_age, "target_met": self.stats["target_met"],
                 "oldest_verification_age_seconds": round(age, 3) if age is not None else None,
                 "oldest_within_target": (age <= self.target_age) if self.target_age and age is not None else None,
                 "passes": self.stats["passes"], "last_pass_seconds": self.stats["last_pass_seconds"],
-                "never_compared": sorted(e.name for e in self.entries if not e.compared and not e.excluded),
+                "never_compared": sorted(g.name for g in self.groups if not g.compared and g.live()),
                 "repair": {"on": self.repair, "off_because": self.repair_off, "max_values": self.repair_max_values,
-                           "host_copy_bytes": self.stats["host_copy_bytes"],
-                           "host_allowance_bytes": self._host_allowance, "repaired": self.stats["repaired"],
-                           "failed": self.stats["repair_failed"],
-                           "entries_repaired": sorted(e.name for e in self.entries if e.repairs),
-                           "not_compared_since_repair": sorted(e.name for e in self.entries if e.repairs and
-                                                               not e.excluded and e.compared <= e.compared_at_repair)},
-                "changed": sorted(e.name for e in self.entries if e.alerted),
+                           "host_copy_bytes": self.copies.bytes, "host_allowance_bytes": self.copies.allowance,
+                           "repaired": self.stats["repaired"], "failed": self.stats["repair_failed"],
+                           "entries_repaired": sorted(g.name for g in self.groups if g.repairs),
+                           "not_compared_since_repair": sorted(g.name for g in self.groups if g.repairs and g.live()
+                                                               and g.compared <= g.compared_at_repair)},
+                "changed": sorted(g.name for g in self.groups if g.status == Status.CHANGED),
                 "not_scanned": dict(self.not_scanned), "kernel": "sdc_fingerprint2"}
+
+
+def _bias_of(m) -> Optional[torch.Tensor]:
+    b = getattr(m, "bias", None)
+    return b if isinstance(b, torch.Tensor) else None

@@ -144,7 +144,7 @@ def test_fp8checks_flow_alerts_and_graph_capture():
     s_static.div_(1.5)
 
     # the calls in a captured graph: replays judge like eager calls
-    st = fc._state[dev]
+    st = fc.tables[dev].state
     fc.mark_step(9, real)
     calls(x, None)
     torch.cuda.synchronize()

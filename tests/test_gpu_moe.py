@@ -242,7 +242,7 @@ def test_moechecks_flow_alerts_and_capture():
     with torch.no_grad():
         L1.w2_weight[ex].div_(2)
     # the calls captured in a graph: replays count as eager calls do
-    st = mc._state[layers[0].w13_weight.device]
+    st = mc.tables[layers[0].w13_weight.device].state
     mc.mark_step(12, 20)
     graph = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
