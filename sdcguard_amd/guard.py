@@ -20,8 +20,13 @@ the fp32 accumulator before rounding it (fused.fused_mm_checked; fused_mm + zsco
 SDCGUARD_FUSED_FP64=1), so no fp32 product is written or read back; fused_inject(layer, pass, (m, n)) -> (row, col,
 value) or None adds a fault to one accumulator element (experiments).  A product the fused kernel refuses switches
 the guard to precise=True from then on (stats["fused_fallbacks"], fused_why).
-The reference's other routes (a dispatch mode over every operator, DTensor shards, recompute and replica checks)
-are not part of this path.
+SDCGuard(ops=True) adds the dispatch route (guard.py:1651-1805): on checked steps a TorchDispatchMode sees every
+aten matmul of the step -- mm, addmm, bmm, baddbmm and torch._grouped_mm (MoE experts), in the forward pass and,
+through the autograd engine's threads, the backward pass -- and queues its check with the same Group.  The MoE layout
+(tokens x experts' weights, offs on the device) is checked by one grouped launch with the group ends read on the GPU;
+the other grouped layouts are split per group on offs read on the host, as the reference splits them
+(guard.py:102-143).  The reference's other routes (DTensor shards, replica and evidence capture) are not part of
+this path.
 """
 from __future__ import annotations
 
@@ -36,7 +41,10 @@ from typing import Callable, Optional
 
 import torch
 
-from .checksum import ABS_FLOOR, UNIT_ROUNDOFF, CheckResult, _f32_of_bits, matmul_zscores, matmul_zscores_acc
+from torch.utils._python_dispatch import TorchDispatchMode
+
+from .checksum import (ABS_FLOOR, UNIT_ROUNDOFF, CheckResult, _f32_of_bits, grouped_checks, grouped_zscores,
+                       is_empty, matmul_zscores, matmul_zscores_acc, resolve_grouped)
 
 UNJUDGED = -1.0
 
@@ -210,6 +218,48 @@ class _PreciseLinear(torch.autograd.Function):
         return gx, gw, gb, None, None
 
 
+# ------------------------------------------------------------------------------------------ the dispatch route
+def _scales(args, kwargs) -> tuple:
+    """(alpha, beta) of an addmm / baddbmm call: beta scales the added input, alpha the product."""
+    beta = kwargs.get("beta", args[3] if len(args) > 3 else 1)
+    alpha = kwargs.get("alpha", args[4] if len(args) > 4 else 1)
+    return float(alpha), float(beta)
+
+
+# aten op -> its product C = beta * bias + alpha * (A @ B) as (A, B, C, bias, alpha, beta); the products the
+# reference's matmul_checks (guard.py:222-264) takes for these ops
+_OP_PRODUCTS = {
+    "mm": lambda a, kw, out: (a[0], a[1], out, None, 1.0, 1.0),
+    "bmm": lambda a, kw, out: (a[0], a[1], out, None, 1.0, 1.0),
+    "addmm": lambda a, kw, out: (a[1], a[2], out, a[0], *_scales(a, kw)),
+    "baddbmm": lambda a, kw, out: (a[1], a[2], out, a[0], *_scales(a, kw)),
+}
+
+
+def _grouped_args(args, kwargs) -> tuple:
+    """(a, b, offs, bias) of a torch._grouped_mm call."""
+    offs = kwargs.get("offs", args[2] if len(args) > 2 else None)
+    bias = kwargs.get("bias", args[3] if len(args) > 3 else None)
+    return args[0], args[1], offs, bias
+
+
+class _OpWatch(TorchDispatchMode):
+    """The guard's view of every aten operator while a checked step runs: matmul results are handed to the guard
+    after the operator ran (this mode is paused inside its own handler, so the checks' own operators pass by)."""
+
+    def __init__(self, guard: "SDCGuard"):
+        super().__init__()
+        self.guard = guard
+
+    def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        out = func(*args, **kwargs)
+        name = func.overloadpacket.__name__
+        if (name in _OP_PRODUCTS or name == "_grouped_mm") and self.guard._active:
+            self.guard._op_result(name, args, kwargs, out)
+        return out
+
+
 def _plain_linear(mod: torch.nn.Module) -> bool:
     return isinstance(mod, torch.nn.Linear) and type(mod).forward is torch.nn.Linear.forward and \
         "forward" not in mod.__dict__
@@ -230,15 +280,23 @@ class SDCGuard:
                  on_alert: Optional[Callable[[SDCEvent], None]] = None, raise_on_alert: bool = False,
                  abs_floor: Optional[float] = None, every: int = 10, max_pending: int = 4096,
                  fresh_signs: bool = True, seed: int = 0, precise=False, nfma: Optional[int] = 16,
-                 on_accumulator: Optional[Callable[[str, str, torch.Tensor], None]] = None, recompute: bool = False):
+                 on_accumulator: Optional[Callable[[str, str, torch.Tensor], None]] = None, recompute: bool = False,
+                 ops: bool = False):
         """precise: True or "fused", check the fp32 accumulators of the protected layers' products (see the module
         docstring); nfma: products per tensor-core accumulation step of those products (16: one 32x32x16 MFMA;
         None: none); recompute: also compare each activation-checkpointed block's recompute with its forward run
-        (recompute.RecomputeCheck, installed by protect() and flushed with the checks)."""
+        (recompute.RecomputeCheck, installed by protect() and flushed with the checks); ops: check every aten
+        matmul of a checked step (mm, addmm, bmm, baddbmm, torch._grouped_mm) through a dispatch mode instead of the
+        protected layers' hooks (protect() then only installs the recompute check)."""
         if not 0.0 <= sample_rate <= 1.0:
             raise ValueError("sample_rate is a share in [0, 1]")
         if precise not in (False, True, "fused"):
             raise ValueError(f"precise is False, True or 'fused', not {precise!r}")
+        if ops and precise:
+            raise ValueError("the dispatch route checks bf16 / fp16 results as they are (precise needs the layers' "
+                             "fp32 products)")
+        self.ops = bool(ops)
+        self.ops_seen: dict = {}            # aten matmul -> calls seen on checked steps (the dispatch route)
         self.sample_rate, self.block, self.z = float(sample_rate), int(block), float(z)
         self.on_alert, self.raise_on_alert = on_alert, raise_on_alert
         self.abs_floor = ABS_FLOOR if abs_floor is None else float(abs_floor)
@@ -279,6 +337,8 @@ class SDCGuard:
         """Check the forward product and both gradient products of every plain nn.Linear of `model`."""
         if self.recompute is not None:
             self.recompute.install(model)
+        if self.ops:                         # (the dispatch route sees every product itself)
+            return self
         for name, mod in model.named_modules():
             if not _plain_linear(mod) or mod in self._protected:
                 continue
@@ -350,7 +410,7 @@ class SDCGuard:
                 warnings.warn(f"the fused precise check refused a product, precise=True takes over: {self.fused_why}",
                               RuntimeWarning, stacklevel=2)
                 return None
-            self._pending.append((g, i, layer, where, self.step))
+            self._pending.append((g, i, layer, where, self.step, None))
             self.stats["checks"] += 1
             self.stats["checked_fused"] += 1
         return C
@@ -368,7 +428,7 @@ class SDCGuard:
                 g = self._groups[key] = Group(C32.device, A.dtype, self.block, self.abs_floor, self.z, self._epoch,
                                               precise=True, nfma=self.nfma)
             i = g.add(A, B, C32, bias, 1.0, 1.0)
-            self._pending.append((g, i, layer, where, self.step))
+            self._pending.append((g, i, layer, where, self.step, None))
             self.stats["checks"] += 1
 
     def _sampled(self) -> bool:
@@ -424,8 +484,10 @@ class SDCGuard:
             return None
         return hook
 
-    def _queue(self, layer: str, where: str, A, B, C, bias) -> None:
-        """Queue one check of C = A @ B (+ bias): its GPU work starts now; the result is read at the flush."""
+    def _queue(self, layer: str, where: str, A, B, C, bias, alpha: float = 1.0, beta: float = 1.0,
+               extra: Optional[dict] = None) -> None:
+        """Queue one check of C = beta * bias + alpha * (A @ B): its GPU work starts now; the result is read at the
+        flush."""
         if C.dtype not in UNIT_ROUNDOFF or not C.is_cuda:
             self.stats["skipped_dtype"] += 1
             return
@@ -436,9 +498,42 @@ class SDCGuard:
             g = self._groups.get(key)
             if g is None:
                 g = self._groups[key] = Group(C.device, C.dtype, self.block, self.abs_floor, self.z, self._epoch)
-            i = g.add(A, B, C, bias, 1.0, 1.0)
-            self._pending.append((g, i, layer, where, self.step))
+            i = g.add(A, B, C, bias, alpha, beta)
+            self._pending.append((g, i, layer, where, self.step, extra))
             self.stats["checks"] += 1
+
+    def _op_result(self, name: str, args, kwargs, out) -> None:
+        """The dispatch route: one aten matmul's result, seen on a checked step (forward or backward)."""
+        node = torch._C._current_autograd_node()
+        where = f"backward ({node.name()})" if node is not None else "forward"
+        label = f"aten.{name}"
+        with self._lock:
+            self.stats["matmuls_seen"] += 1
+            self.ops_seen[label] = self.ops_seen.get(label, 0) + 1
+        if not self._sampled():
+            return
+        if name != "_grouped_mm":
+            A, B, C, bias, alpha, beta = _OP_PRODUCTS[name](args, kwargs, out)
+            self._queue(label, where, A, B, C, bias, alpha, beta,
+                        extra={"op": label, "shape_A": tuple(A.shape), "shape_B": tuple(B.shape)})
+            return
+        a, b, offs, bias = _grouped_args(args, kwargs)
+        if not out.is_cuda or out.dtype not in UNIT_ROUNDOFF:
+            self.stats["skipped_dtype"] += 1
+            return
+        if a.dim() == 2 and b.dim() == 3 and offs is not None and (bias is None or bias.numel() == out.shape[-1]):
+            # tokens sorted by expert: one grouped launch, the group ends read on the GPU
+            st = grouped_zscores(a, b, out, offs, bias, block=self.block, abs_floor=self.abs_floor, z=self.z,
+                                 epoch=self._epoch)
+            with self._lock:
+                self._pending.append((None, st, label, where, self.step,
+                                      {"op": label, "shape_A": tuple(a.shape), "shape_B": tuple(b.shape)}))
+                self.stats["checks"] += 1
+            return
+        for gi, (A, B, C, bi, al, be) in enumerate(grouped_checks(a, b, out, offs, bias)):
+            if not is_empty(C):
+                self._queue(label, where, A, B, C, bi, al, be,
+                            extra={"op": label, "group": gi, "shape_A": tuple(A.shape), "shape_B": tuple(B.shape)})
 
     # ------------------------------------------------------------------------------------------- steps
     @contextlib.contextmanager
@@ -451,8 +546,10 @@ class SDCGuard:
         if self.fresh_signs:
             self._epoch = self.step + 1        # a new signed-checksum pattern every checked step
         self._active = True
+        watch = _OpWatch(self) if self.ops else contextlib.nullcontext()
         try:
-            yield self
+            with watch:
+                yield self
         finally:
             self._active = False
             for ctx in self._wctx.values():          # (a forward whose backward did not run this step)
@@ -473,7 +570,7 @@ class SDCGuard:
             self.recompute.flush()
         with self._lock:
             pending, self._pending = self._pending, []
-            groups = {id(g): g for g, *_ in pending}
+            groups = {id(g): g for g, *_ in pending if g is not None}
             self._groups = {}
         if not pending:
             return []
@@ -490,19 +587,38 @@ class SDCGuard:
                 rows[id(g)] = back[i:i + len(g)]
                 i += len(g)
         out, alerts = [], []
-        for g, i, layer, where, step in pending:
+
+        def judge(res, g, layer, where, step, info, batch=None, group=None):
+            out.append(res)
+            if res.ok:
+                return
+            extra = {"pass": where, **(info or {})}
+            if batch is not None:
+                extra["batch"] = batch
+            if group is not None:
+                extra["group"] = group
+            if g is not None and g.fused:
+                extra["dtype"] = f"float32 accumulator of {g.dtype} (fused)"
+            alerts.append(SDCEvent(detector="accumulator" if g is not None and g.precise else "checksum",
+                                   layer=layer, z=res.max_z, step=step, row=res.row, col_block=res.col_block,
+                                   noise=res.noise, nonfinite=res.nonfinite, extra=extra))
+
+        for g, i, layer, where, step, info in pending:
+            if g is None:                        # a grouped launch: one result per non-empty group, in group order
+                st, start, nonempty = i, 0, []
+                for gi, e in enumerate(int(v) for v in st.offs.tolist()):
+                    e = min(e, st.rows)
+                    if e > start:
+                        nonempty.append(gi)
+                    start = max(start, e)
+                for gi, res in zip(nonempty, resolve_grouped(st)):
+                    judge(res, None, layer, where, step, info, group=gi)
+                continue
             z, b_i, r_i, c_i, noise = g.row(i, rows[id(g)][i])
             finite = math.isfinite(z)
             res = CheckResult(ok=finite and z <= self.z, max_z=z, nonfinite=not finite, batch=None, row=r_i,
                               col_block=c_i, noise=noise)
-            out.append(res)
-            if not res.ok:
-                extra = {"pass": where}
-                if g.fused:
-                    extra["dtype"] = f"float32 accumulator of {g.dtype} (fused)"
-                ev = SDCEvent(detector="accumulator" if g.precise else "checksum", layer=layer, z=z, step=step,
-                              row=r_i, col_block=c_i, noise=noise, nonfinite=not finite, extra=extra)
-                alerts.append(ev)
+            judge(res, g, layer, where, step, info, batch=b_i if g.meta[i][2] else None)
         self.results.extend(out)
         for ev in alerts:
             self.events.append(ev)
