@@ -410,6 +410,7 @@ class ServeGuard:
         self._scan = None                      # the weight scan (weight_scan())
         self._fp8 = None                       # FP8 quantization checks (fp8_checks())
         self._moe = None                       # fused MoE checks (moe_checks())
+        self._attn = None                      # sampled attention recompute (attn_checks())
         self._marked_step: Optional[int] = None
         self.stats = {"layers": 0, "skipped_layers": 0, "polls": 0, "alerts": 0, "checks_executed": 0,
                       "unjudged_checksums": 0}
@@ -549,6 +550,8 @@ class ServeGuard:
             events += self._fp8.poll(wait)
         if self._moe is not None and self._moe.finalized:
             events += self._moe.poll(wait)
+        if self._attn is not None and self._attn.finalized:
+            events += self._attn.poll(wait)
         if self._scan is not None:
             events += self._scan.poll(wait)
         return events
@@ -569,12 +572,22 @@ class ServeGuard:
             self._moe = MoEChecks(self, MOE_Z if line is None else line)
         return self._moe
 
+    def attn_checks(self, line: Optional[float] = None):
+        """The sampled attention recompute of the serving stack's attention layers (serve_attn.AttnChecks), created
+        on first use: add() the layers, finalize() before capture; mark_step / end_step / poll reach it through the
+        guard."""
+        if self._attn is None:
+            from .serve_attn import ATTN_Z, AttnChecks
+            self._attn = AttnChecks(self, ATTN_Z if line is None else line)
+        return self._attn
+
+    def _step_checks(self) -> list:
+        return [c for c in (self._fp8, self._moe, self._attn) if c is not None]
+
     def end_step(self) -> None:
-        """After a model step's work is queued (the FP8 and MoE checks stop judging until the next mark_step)."""
-        if self._fp8 is not None:
-            self._fp8.end_step()
-        if self._moe is not None:
-            self._moe.end_step()
+        """After a model step's work is queued (the per-step checks stop judging until the next mark_step)."""
+        for c in self._step_checks():
+            c.end_step()
 
     def weight_scan(self, budget_mb: Optional[float] = None, **kw):
         """The scheduled weight scan of this guard's layers (serve_weights.WeightScan), created on the first call:
@@ -588,10 +601,8 @@ class ServeGuard:
     def mark_step(self, step: int, rows: Optional[int] = None) -> None:
         """Stamp the capture area with the serving step (kept rows carry it)."""
         self._marked_step = int(step)
-        if self._fp8 is not None:
-            self._fp8.mark_step(step, rows)
-        if self._moe is not None:
-            self._moe.mark_step(step, rows)
+        for c in self._step_checks():
+            c.mark_step(step, rows)
         step = int(step) & STEP_MASK
         for r in self._rows.values():
             r.cap_meta[1:2].fill_((r.epoch << EPOCH_SHIFT) | step)
@@ -649,10 +660,9 @@ class ServeGuard:
                     lay["hook"].remove()
                 for attr in ("_sdcguard_slot", "_sdcguard_name"):
                     lay["module"].__dict__.pop(attr, None)
-            for sub in (self._fp8, self._moe):
-                if sub is not None:
-                    sub.detach()
-            self._fp8 = self._moe = None
+            for sub in self._step_checks():
+                sub.detach()
+            self._fp8 = self._moe = self._attn = None
             self.layers.clear()
             self._rows.clear()
             self._scan = None

@@ -308,5 +308,334 @@ def decode_state(row) -> dict:
             "write_last": k[C_WLAST], "write_where": k[C_WWHERE]}
 
 
+# ------------------------------------------------------------------------------------------ the serving layers
+# Which attention layers the check models (the reference's why_not / call_issue, serve_attn.py:800-880, read the
+# same attributes of the serving stack's layer and backend): one ordered rule table per layer, and the per-call
+# conditions read from the call's tensors and metadata on the host.
+BACKENDS = ("FlashAttentionImpl", "TritonAttentionImpl")
+
+
+def _window_of(impl) -> tuple:
+    sw = getattr(impl, "sliding_window", (-1, -1))
+    return tuple(sw) if sw is not None else (-1, -1)
+
+
+def _heads(impl) -> tuple:
+    return tuple(getattr(impl, a, None) for a in ("head_size", "num_heads", "num_kv_heads"))
+
+
+_LAYER_RULES = (
+    (lambda layer, impl: type(layer).__name__ == "Attention",
+     lambda layer, impl: f"{type(layer).__name__}: only plain decoder attention layers are checked"),
+    (lambda layer, impl: type(impl).__name__ in BACKENDS,
+     lambda layer, impl: f"{type(impl).__name__}: only the FlashAttention and Triton backends' rounding is modelled"),
+    (lambda layer, impl: not (type(impl).__name__ == "FlashAttentionImpl" and
+                              getattr(impl, "vllm_flash_attn_version", None) not in (None, 2, 3)),
+     lambda layer, impl: f"FlashAttention {getattr(impl, 'vllm_flash_attn_version', None)} (the bound is written for "
+                         "versions 2 and 3)"),
+    (lambda layer, impl: str(getattr(impl, "attn_type", "decoder")).lower().endswith("decoder") and
+     "encoder" not in str(getattr(impl, "attn_type", "decoder")).lower(),
+     lambda layer, impl: f"attention type {getattr(impl, 'attn_type', None)}"),
+    (lambda layer, impl: getattr(impl, "alibi_slopes", None) is None and not getattr(impl, "use_alibi_sqrt", False),
+     lambda layer, impl: "ALiBi"),
+    (lambda layer, impl: getattr(impl, "sinks", None) is None, lambda layer, impl: "attention sinks"),
+    (lambda layer, impl: getattr(impl, "logits_soft_cap", 0) in (0, None, 0.0), lambda layer, impl: "a logit soft cap"),
+    (lambda layer, impl: _window_of(impl) == (-1, -1), lambda layer, impl: "a sliding window"),
+    (lambda layer, impl: getattr(impl, "chunk_lookback", -1) in (-1, None),
+     lambda layer, impl: "chunked local attention"),
+    (lambda layer, impl: (getattr(impl, "dcp_world_size", 1) or 1) <= 1,
+     lambda layer, impl: "decode context parallelism"),
+    (lambda layer, impl: str(getattr(impl, "kv_cache_dtype", "auto")) in ("auto", "bfloat16", "float16"),
+     lambda layer, impl: f"KV cache dtype {getattr(impl, 'kv_cache_dtype', None)}"),
+    (lambda layer, impl: all(isinstance(v, int) and v > 0 for v in _heads(impl)) and
+     _heads(impl)[1] % _heads(impl)[2] == 0,
+     lambda layer, impl: "head counts it can't read"),
+    (lambda layer, impl: _heads(impl)[0] <= 256, lambda layer, impl: f"head size {_heads(impl)[0]}"),
+    (lambda layer, impl: getattr(layer, "head_size_v", _heads(impl)[0]) == _heads(impl)[0],
+     lambda layer, impl: "values of another size than the keys"),
+)
+
+
+def why_not(layer, impl, model_dtype=None) -> Optional[str]:
+    """Why an attention layer of the serving stack is not checked, or None."""
+    for holds, why in _LAYER_RULES:
+        if not holds(layer, impl):
+            return why(layer, impl)
+    kvd = str(getattr(impl, "kv_cache_dtype", "auto"))
+    if model_dtype is not None and kvd != "auto" and kvd != str(model_dtype).replace("torch.", ""):
+        return f"KV cache dtype {kvd} differs from the model's"
+    return None
+
+
+def call_issue(impl, query, output, kv_cache, md, output_scale=None) -> Optional[str]:
+    """Why one call is not checked (shapes and the metadata's host fields), or None."""
+    if output_scale is not None:
+        return "fused output quantization"
+    if not all(isinstance(t, torch.Tensor) for t in (query, output, kv_cache)):
+        return "inputs it can't read"
+    if query.dim() != 3 or output.dim() != 3 or kv_cache.dim() != 4:
+        return "tensor layouts it doesn't know"
+    D = query.shape[2]
+    if output.shape != query.shape or output.dtype not in (torch.bfloat16, torch.float16) or \
+            query.dtype != output.dtype or output.stride(-1) != 1 or query.stride(-1) != 1:
+        return "outputs it can't compare"
+    if kv_cache.dtype != query.dtype or kv_cache.shape[1] != impl.num_kv_heads or kv_cache.shape[3] != 2 * D:
+        return "a KV cache layout it doesn't know"
+    if getattr(md, "causal", True) is not True:
+        return "attention that isn't causal for every request"
+    if any(getattr(md, f, None) is not None for f in ("mm_prefix_query_range_tensor", "mm_prefix_range_tensor",
+                                                      "rswa_prefix_lens")):
+        return "multimodal prefix ranges or R-SWA"
+    for f in ("query_start_loc", "seq_lens", "block_table"):
+        if not isinstance(getattr(md, f, None), torch.Tensor):
+            return f"metadata without {f}"
+    if md.block_table.dim() != 2 or md.query_start_loc.shape[0] != md.seq_lens.shape[0] + 1 or \
+            md.block_table.shape[0] < md.seq_lens.shape[0]:
+        return "metadata it can't read"
+    if md.seq_lens.shape[0] > MAX_REQUESTS:
+        return f"more than {MAX_REQUESTS:,} requests in a step"
+    return None
+
+
+from .stepchecks import W_STEP, Binding, Registered, StepChecks  # noqa: E402  (after the kernel wrappers)
+
+
+class AttnChecks(StepChecks):
+    """The attention layers one serving guard checks (ServeGuard.attn_checks()).  add() each layer, finalize() once
+    before any graph is captured (it numbers the layers' turns -- at step s the layer with index s % layers
+    recomputes its samples -- sizes the kept-keys buffer and gives each layer its binding, layer._sdcguard_attn),
+    check() after each call of a layer's backend, mark_step() / end_step() around each model step, poll() to read.
+    The state rows are the kernel's 18 columns (serve_attn.py:86-92)."""
+
+    DETECTOR = "serve_attn"
+    COLS = COLS
+    CAPTURE = {"meta": torch.int32, "q": torch.float32, "o": torch.float32}
+    READ_CAPTURE = ("meta",)
+
+    def __init__(self, guard=None, line: float = ATTN_Z):
+        line = float(line)
+        if not MIN_LINE <= line < float("inf"):
+            raise ValueError(f"the attention check's line must be at least {MIN_LINE} (a correct output scores at "
+                             f"most 1), not {line!r}")
+        super().__init__(guard)
+        self.line = line
+        self.finalized = False
+        self.shared: dict = {}                 # device -> {"capkv", "capkvm", "ws"}: one kept sample per device
+        self.cap_rows = 0
+        self.not_checked_calls: dict = {}      # why -> calls (seen on the host)
+        self.worst_seen: dict = {}
+        self.calls_seen: dict = {}
+        self.stats.update(calls_checked=0, samples=0, skipped=0, unjudged=0, keys=0, bad_blocks=0,
+                          writes_checked=0, writes_wrong=0, slots_wrong=0, graph_calls=0)
+        self._in_step = False                  # between mark_step and end_step (the host's view, for eager calls)
+
+    def add(self, layer, impl, name: str, device, model_dtype=None) -> Optional[int]:
+        if self.finalized:
+            raise RuntimeError("attention layers are added before finalize()")
+        why = why_not(layer, impl, model_dtype)
+        if why is None and getattr(layer, "_sdcguard_attn", None) is not None:
+            why = "already checked by another ServeGuard"
+        if why is None and torch.device(device).type != "cuda":
+            why = "not on a GPU"
+        if why:
+            self._refuse(name, why)
+            return None
+        D, Hq, Hkv = _heads(impl)
+        width = _pow2(D)
+        b = self._register(name, layer, device, widths={"meta": CAPM, "q": width, "o": width}, impl=impl,
+                           scale=float(impl.scale), left=int(_window_of(impl)[0]), D=D, Hq=Hq, Hkv=Hkv,
+                           write=getattr(impl, "kv_sharing_target_layer_name", None) is None,
+                           backend=type(impl).__name__)
+        return b.slot
+
+    def finalize(self, max_len: int = 32768, kv_dtype=torch.bfloat16) -> int:
+        """Number the layers' turns, allocate the per-device buffers (the kept sample's keys and values: up to
+        min(max_len, CAP_ROWS) rows) and bind the layers.  Before any graph is captured."""
+        if self.finalized:
+            return len(self.layers)
+        self.cap_rows = min(int(max_len), CAP_ROWS)
+        per_dev: dict = {}
+        for lay in self.layers:
+            per_dev.setdefault(lay.device, []).append(lay)
+        for dev, lays in per_dev.items():
+            for turn, lay in enumerate(lays):
+                lay.info["index"], lay.info["count"] = turn, len(lays)
+            width = max(_pow2(lay.info["D"]) for lay in lays)
+            ws = workspace_bytes(SAMPLES, 1 << 40, width)
+            with torch.inference_mode(False):
+                self.shared[dev] = {"capkv": torch.zeros(max(1, self.cap_rows), 2, width, dtype=kv_dtype,
+                                                         device=dev),
+                                    "capkvm": torch.zeros(4, dtype=torch.int32, device=dev),
+                                    "ws": torch.zeros(max(ws, 1), dtype=torch.uint8, device=dev)}
+        for n, lay in enumerate(self.layers):
+            lay.module._sdcguard_attn = Binding(self, n)
+        self.finalized = True
+        return len(self.layers)
+
+    def _skip(self, why: str) -> None:
+        self.not_checked_calls[why] = self.not_checked_calls.get(why, 0) + 1
+
+    def check(self, binding: Binding, impl, query, key, value, kv_cache, md, output, output_scale=None) -> None:
+        """After one call of a registered layer's backend.  Inside a graph capture the kernel is always queued (the
+        step's layer is chosen on the device from the step word); in eager calls during a marked step only the
+        step's layer queues it; outside marked steps (warm-up runs) every layer does, and the kernel returns at once
+        (it is compiled ahead of time: nothing is built during a capture)."""
+        lay = binding.layer
+        dev = lay.device
+        if torch.compiler.is_compiling():
+            return self._skip("traced by torch.compile")
+        capturing = torch.cuda.is_current_stream_capturing()
+        if capturing:
+            self.stats["graph_calls"] += 1
+        elif self._in_step and self.marked % lay.info["count"] != lay.info["index"]:
+            return None
+        why = call_issue(impl, query, output, kv_cache, md, output_scale)
+        if why:
+            return self._skip(why)
+        T = min(int(query.shape[0]), int(getattr(md, "num_actual_tokens", query.shape[0]) or query.shape[0]))
+        if T <= 0:
+            return None
+        has_write = bool(lay.info["write"]) and all(isinstance(t, torch.Tensor) for t in (key, value)) and \
+            isinstance(getattr(md, "slot_mapping", None), torch.Tensor) and key.dim() == 3 and value.dim() == 3 and \
+            key.dtype == kv_cache.dtype and value.dtype == kv_cache.dtype and key.stride(-1) == 1 and \
+            value.stride(-1) == 1 and key.shape[0] == query.shape[0] and value.shape[0] == query.shape[0]
+        tab, sh = self.tables[dev], self.shared[dev]
+        c = tab.capture
+        with torch.no_grad(), torch.autocast(device_type="cuda", enabled=False):
+            attn_check(query[:T], output[:T], kv_cache, key if has_write else None, value if has_write else None,
+                       md.query_start_loc, md.seq_lens, md.block_table, md.slot_mapping if has_write else None,
+                       tab.state, lay.slot, tab.word.view(W_STEP, 2), lay.info["count"], lay.info["index"],
+                       lay.info["scale"], lay.info["left"], self.line, c["meta"], c["q"], c["o"], sh["capkv"],
+                       sh["capkvm"], sh["ws"], has_write, self.cap_rows > 0)
+        lay.info["dtype"] = output.dtype
+
+    def mark_step(self, step: int, rows: Optional[int] = None) -> None:
+        super().mark_step(step, rows)
+        self._in_step = True
+
+    def end_step(self) -> None:
+        super().end_step()
+        self._in_step = False
+
+    def detach(self) -> None:
+        super().detach()
+        self.shared.clear()
+        self.finalized = False
+
+    def _unbind(self, lay: Registered) -> None:
+        lay.module.__dict__.pop("_sdcguard_attn", None)
+
+    def coverage(self) -> dict:
+        out = super().coverage()
+        out.update(calls_checked=self.stats["calls_checked"], samples_per_call=SAMPLES, one_layer_a_step=True,
+                   calls_not_checked=dict(self.not_checked_calls), samples=self.stats["samples"],
+                   keys_recomputed=self.stats["keys"], samples_without_a_token=self.stats["skipped"],
+                   samples_not_judged=self.stats["unjudged"], writes_checked=self.stats["writes_checked"])
+        return out
+
+    def _count(self, lay: Registered, k: list) -> None:
+        lay.calls += k[C_CALLS]
+        self.calls_seen[lay.name] = self.calls_seen.get(lay.name, 0) + k[C_CALLS]
+        for stat, col in (("calls_checked", C_CALLS), ("samples", C_SAMPLES), ("skipped", C_SKIP),
+                          ("unjudged", C_UNJ), ("keys", C_KEYS), ("bad_blocks", C_BADBLK),
+                          ("writes_checked", C_WN), ("writes_wrong", C_WBAD), ("slots_wrong", C_WSLOT)):
+            self.stats[stat] += k[col]
+
+    def _judged(self, k: list) -> bool:
+        return k[C_CALLS] > 0
+
+    def _judge(self, lay: Registered, k: list, captured: dict, window) -> list:
+        out = []
+        z = f32_of_bits(k[C_ZT] >> 32)
+        self.worst_seen[lay.name] = max(self.worst_seen.get(lay.name, 0.0), z)
+        lay.worst = max(lay.worst, z)
+        if z > self.line:
+            meta = [int(v) for v in captured["meta"].tolist()] if "meta" in captured else [0] * CAPM
+            out.append(self._output_event(lay, k, meta, window, z))
+        if k[C_WBAD] or k[C_WSLOT]:
+            out.append(self._write_event(lay, k, window))
+        if k[C_BADBLK]:
+            out.append(self.emit(lay, float("inf"), None, {
+                "where": lay.name, "kind": "attention", "finding": "block_table_out_of_range",
+                "samples": k[C_BADBLK], "read_window_steps": window,
+                "reading": "a sampled request's block table named KV-cache blocks outside the cache: the attention "
+                           "kernel read memory that is not part of the KV cache"}))
+        return out
+
+    def _kept_sample(self, lay: Registered, meta: list) -> tuple:
+        """(what the kept record says, the float64 recheck of it or None) -- the kept keys and values are read from
+        the device and its claim released."""
+        if not meta[CM_CLAIM]:
+            return None, None
+        tab, sh = self.tables[lay.device], self.shared[lay.device]
+        D = lay.info["D"]
+        q_row, o_row = tab.capture["q"][lay.slot, :D].cpu(), tab.capture["o"][lay.slot, :D].cpu()
+        kvm = [int(v) for v in sh["capkvm"].tolist()]
+        kept = bool(meta[CM_KEPT]) and kvm[0] == 1 and kvm[1] == lay.slot and kvm[3] == meta[CM_STEP]
+        rec = {"row": meta[CM_ROW] & M32, "head": meta[CM_HEAD], "kv_head": meta[CM_HK],
+               "request_index": meta[CM_REQ], "position": meta[CM_POS], "seq_len": meta[CM_SL],
+               "first_key": meta[CM_LO], "step": (meta[CM_STEP] & M32) if self.marked is not None else None,
+               "score": f32_of_bits(meta[CM_Z]), "keys_kept": kept}
+        verdict = None
+        if kept:
+            rows = sh["capkv"][:kvm[2]].cpu()
+            verdict = recheck(q_row, o_row, rows[:, 0, :D], rows[:, 1, :D], lay.info["scale"],
+                              lay.info.get("dtype", torch.bfloat16), self.line)
+            sh["capkvm"].zero_()
+        else:
+            verdict = {"verdict": "not_rechecked",
+                       "why": "the keys and values it attended were not kept (another layer's alert took the "
+                              "buffer, or there were more than it holds)"}
+        tab.capture["meta"][lay.slot].zero_()
+        return rec, verdict
+
+    def _output_event(self, lay: Registered, k: list, meta: list, window, z: float) -> object:
+        rec, verdict = self._kept_sample(lay, meta)
+        place = {"row": k[C_ZT] & M32, "head": k[C_ZH] & M32, "dim": k[C_ZD] & M32, "position": k[C_ZP] & M32,
+                 "step": (k[C_ZS] & M32) if self.marked is not None else None, "output": f32_of_bits(k[C_ZO]),
+                 "expected": f32_of_bits(k[C_ZR]), "place": "the read's score maxima"}
+        if rec is not None and verdict and verdict.get("outputs_over_line") and verdict.get("dim") is not None:
+            place = {"row": rec["row"], "head": rec["head"], "dim": verdict["dim"], "position": rec["position"],
+                     "step": rec["step"], "output": verdict["output"], "expected": verdict["expected"],
+                     "place": "the kept sample's worst output, rechecked"}
+        dtype = lay.info.get("dtype", torch.bfloat16)
+        detail = {"where": lay.name, "kind": "attention", "backend": lay.info["backend"],
+                  "finding": "output_wrong_or_misread", "max_z": z, **place, "captured": rec,
+                  "recheck": verdict or {"verdict": "not_rechecked",
+                                         "why": "no sample was kept for this alert (an earlier alert's kept sample "
+                                                "has not been read yet)"},
+                  "read_window_steps": window, "last_clean_read_steps": self.last_clean(lay.name),
+                  "check_config": {"line": self.line, "unit_roundoff": dtype_consts(dtype)[0], "samples": SAMPLES},
+                  "reading": "an attention output is farther from attention recomputed from the request's own keys "
+                             "and values in the KV cache than a correct backend's rounding allows: wrong arithmetic "
+                             "in the attention kernel, or it read other keys than the metadata names"}
+        return self.emit(lay, z, place["row"], detail)
+
+    def _write_event(self, lay: Registered, k: list, window) -> object:
+        last, wh = k[C_WLAST], k[C_WWHERE]
+        kind, info = (wh >> 28) & 0xF, wh & 0x0FFFFFFF
+        from .serve_fp8 import unwrap31
+        latest = {"step": unwrap31(last >> 32, self.marked) if self.marked is not None else None, "row": last & M32}
+        wrong = {"content_wrong": bool(kind & W_CONTENT), "slot_wrong": bool(kind & W_SLOT)}
+        if kind & W_CONTENT:
+            wrong.update({"kv_head": info >> 12, "dim": (info >> 1) & 0x7FF, "part": "value" if info & 1 else "key"})
+        detail = {"where": lay.name, "kind": "attention", "backend": lay.info["backend"], "finding": "kv_write_wrong",
+                  "writes_checked": k[C_WN], "writes_with_wrong_content": k[C_WBAD],
+                  "writes_to_another_slot": k[C_WSLOT], "latest": latest, "a_wrong_write": wrong,
+                  "captured": {"row": latest["row"], "step": latest["step"]}, "read_window_steps": window,
+                  "last_clean_read_steps": self.last_clean(lay.name),
+                  "reading": "a sampled token's KV-cache slot does not hold the key and value the layer computed for "
+                             "it, or they went to another slot than its position's block names: attention reads "
+                             "wrong state for that position from now on"}
+        return self.emit(lay, float("inf"), latest["row"], detail)
+
+
+def check_call(binding, impl, query, key, value, kv_cache, md, output, output_scale=None) -> None:
+    """After a backend call of a registered layer (binding: layer._sdcguard_attn)."""
+    if binding is not None:
+        binding.checks.check(binding, impl, query, key, value, kv_cache, md, output, output_scale)
+
+
 __all__ = ["ATTN_Z", "SAMPLES", "COLS", "CAPM", "bound_consts", "sample_python", "buffers", "attn_check",
-           "attn_check_triton", "run_case", "make_case", "recheck", "decode_state", "workspace_bytes"]
+           "attn_check_triton", "run_case", "make_case", "recheck", "decode_state", "workspace_bytes", "AttnChecks",
+           "why_not", "call_issue", "check_call"]

@@ -5,10 +5,11 @@ Each of them has kernels that fold what they find into one int64 state row per c
 packed keys, counters) and, for some, a kept record of the first sample over the alert line.  Around those rows the
 host needs the same four things, which this module provides once:
 
-  StepWord      the device word the kernels read to know which model step they run in: [step, real rows,
-                step | rows << 32, armed].  mark_step() writes it with one asynchronous copy from a fresh pinned
-                buffer (the caching host allocator keeps the buffer until the copy has run), so a guarded step never
-                waits for the device; a graph captured once reads each replay's step from it.
+  StepWord      the device word the kernels read to know which model step they run in: [step, armed, real rows,
+                step | rows << 32] (the first two are the attention check's control pair).  mark_step() writes it
+                with one asynchronous copy from a fresh pinned buffer (the caching host allocator keeps the buffer
+                until the copy has run), so a guarded step never waits for the device; a graph captured once reads
+                each replay's step from it.
   DeviceTable   per device, the state rows [rows, COLS] and the named capture tensors [rows, width], grown by
                 doubling while layers are added (never after a graph has captured them: layers are added at load).
   Binding       what a layer's call site holds: the checks object and the layer's slot.  The tensors are looked up
@@ -34,7 +35,7 @@ ROWS_SHIFT = 32
 ROWS_MAX = (1 << 31) - 1
 
 # the step word: what mark_step publishes on every device
-W_STEP, W_ROWS, W_PACKED, W_ARMED = range(4)
+W_STEP, W_ARMED, W_ROWS, W_PACKED = range(4)
 
 
 def f32_of(bits: int) -> float:
@@ -49,21 +50,21 @@ def pack_step(step: int, rows: Optional[int] = None) -> int:
 
 
 class StepWord:
-    """int64[4] on one device: [step, real rows (0 unknown), step | rows << 32, armed (1 inside a marked step)]."""
+    """int64[4] on one device: [step, armed (1 inside a marked step), real rows (0 unknown), step | rows << 32]."""
 
     def __init__(self, device: torch.device):
         with torch.inference_mode(False):
             self.t = torch.zeros(4, dtype=torch.int64, device=device)
 
     def write(self, step: int, rows: Optional[int], armed: bool) -> None:
-        vals = [int(step) & M32, int(rows) if rows else 0, pack_step(step, rows), int(bool(armed))]
+        vals = [int(step) & M32, int(bool(armed)), int(rows) if rows else 0, pack_step(step, rows)]
         host = torch.tensor(vals, dtype=torch.int64)
         if self.t.is_cuda:
             host = host.pin_memory()
         self.t.copy_(host, non_blocking=self.t.is_cuda)
 
-    def view(self, i: int) -> torch.Tensor:
-        return self.t[i:i + 1]
+    def view(self, i: int, n: int = 1) -> torch.Tensor:
+        return self.t[i:i + n]
 
 
 class DeviceTable:

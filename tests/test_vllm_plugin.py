@@ -150,3 +150,144 @@ def test_layers_armed_before_the_state_grows_still_report(monkeypatch, fake_vllm
     assert len(ev) == 1 and ev[0].layer == "model.layers.2.mlp" and (ev[0].row, ev[0].col_block) == (5, 2)
     assert g.stats["checks_executed"] == 2
     vllm_plugin.unregister()
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Attention through register(): stand-ins of vLLM's FlashAttention backend (a correct paged-attention forward in
+# PyTorch, KV cache [blocks, kv heads, block size, 2 x head size]), its Attention layer and its model runner
+# (load_model, execute_model running one decode step of every layer).
+
+D_, HQ, HKV, NBLK, BS, REQ = 64, 4, 2, 64, 16, 4
+
+
+def _fake_vllm_runner(fault: dict):
+    import types as _t
+
+    class FlashAttentionImpl:
+        def __init__(self):
+            self.num_heads, self.head_size, self.num_kv_heads, self.scale = HQ, D_, HKV, D_ ** -0.5
+            self.sliding_window, self.kv_cache_dtype, self.attn_type = (-1, -1), "auto", "decoder"
+            self.alibi_slopes, self.logits_soft_cap, self.sinks = None, 0, None
+
+        def forward(self, layer, query, key, value, kv_cache, md, output=None, output_scale=None):
+            T = md.num_actual_tokens
+            slots = md.slot_mapping[:T]
+            blk, off = slots // BS, slots % BS
+            k_new = key[:T].clone()
+            if fault.get("write"):                              # a wrong KV write: one bit of every new key
+                k_new.view(torch.int16)[:, :, 3] ^= 1 << 9
+            kv_cache[blk, :, off, :D_] = k_new
+            kv_cache[blk, :, off, D_:] = value[:T]
+            qsl, sls, bt = md.query_start_loc.tolist(), md.seq_lens.tolist(), md.block_table
+            for r in range(len(sls)):
+                i, L = qsl[r], sls[r]
+                t = torch.arange(L, device=kv_cache.device)
+                rows = kv_cache[bt[r, t // BS].long(), :, t % BS].float()       # [L, Hkv, 2D]
+                if fault.get("read"):                           # the kernel read a changed value of the first key
+                    rows = rows.clone()
+                    rows[0, :, D_:] += 8.0
+                for hq in range(HQ):
+                    hk = hq // (HQ // HKV)
+                    p = torch.softmax(rows[:, hk, :D_] @ query[i, hq].float() * self.scale, 0)
+                    output[i, hq] = (p @ rows[:, hk, D_:]).to(output.dtype)
+            return output
+
+    class Attention(torch.nn.Module):
+        def __init__(self, name):
+            super().__init__()
+            self.impl, self.layer_name = FlashAttentionImpl(), name
+
+    class GPUModelRunner:
+        def __init__(self):
+            self.device = torch.device("cuda", 0)
+            self.model_config = _t.SimpleNamespace(dtype=torch.bfloat16, max_model_len=4096)
+            g = torch.Generator(device="cpu").manual_seed(3)
+            self.gen = g
+            self.caches = [(torch.randn(NBLK, HKV, BS, 2 * D_, generator=g) * 0.7).bfloat16().cuda()
+                           for _ in range(2)]
+            self.bt = torch.randperm(NBLK, generator=g)[:REQ * 8].view(REQ, 8).to(torch.int32).cuda()
+            self.lens = [40, 57, 71, 90]
+
+        def load_model(self):
+            self.model = torch.nn.ModuleDict({"l0": Attention("model.layers.0.attn"),
+                                              "l1": Attention("model.layers.1.attn")})
+
+        def get_model(self):
+            return self.model
+
+        def execute_model(self, scheduler_output):
+            self.lens = [n + 1 for n in self.lens]               # one new token per request
+            T = REQ
+            dev = self.device
+            md = _t.SimpleNamespace(
+                num_actual_tokens=T, causal=True,
+                query_start_loc=torch.arange(T + 1, dtype=torch.int32, device=dev),
+                seq_lens=torch.tensor(self.lens, dtype=torch.int32, device=dev), block_table=self.bt,
+                slot_mapping=torch.tensor([int(self.bt[r, (L - 1) // BS]) * BS + (L - 1) % BS
+                                           for r, L in enumerate(self.lens)], dtype=torch.int64, device=dev))
+            for li, lay in enumerate(self.model.values()):
+                q = (torch.randn(T, HQ, D_, generator=self.gen) * 0.5).bfloat16().to(dev)
+                k = (torch.randn(T, HKV, D_, generator=self.gen) * 0.7).bfloat16().to(dev)
+                v = (torch.randn(T, HKV, D_, generator=self.gen) * 0.7).bfloat16().to(dev)
+                out = torch.empty(T, HQ, D_, dtype=torch.bfloat16, device=dev)
+                lay.impl.forward(lay, q, k, v, self.caches[li], md, output=out)
+            return None
+
+    mods = {n: types.ModuleType(n) for n in ("vllm", "vllm.v1", "vllm.v1.attention", "vllm.v1.attention.backends",
+                                             "vllm.v1.attention.backends.flash_attn", "vllm.v1.worker",
+                                             "vllm.v1.worker.gpu_model_runner")}
+    mods["vllm.v1.attention.backends.flash_attn"].FlashAttentionImpl = FlashAttentionImpl
+    mods["vllm.v1.worker.gpu_model_runner"].GPUModelRunner = GPUModelRunner
+    base, _ = _fake_vllm()
+    for k in ("vllm.model_executor", "vllm.model_executor.layers", "vllm.model_executor.layers.linear"):
+        mods[k] = base[k]
+    return mods, GPUModelRunner
+
+
+def _serve_steps(monkeypatch, fault: dict, steps: int = 6) -> list:
+    from sdcguard_amd import vllm_plugin
+    monkeypatch.setenv("SDCGUARD", "1")
+    monkeypatch.setenv("SDCGUARD_POLL_EVERY", "1000")
+    mods, Runner = _fake_vllm_runner(fault)
+    for k, v in mods.items():
+        monkeypatch.setitem(sys.modules, k, v)
+    vllm_plugin.register()
+    try:
+        runner = Runner()
+        runner.load_model()
+        p = vllm_plugin.plugin_state()
+        assert p.attn_report["checked"] == 2, p.attn_report
+        for _ in range(steps):
+            runner.execute_model(None)
+        ev = vllm_plugin.poll(wait=True)
+        g = p.guards[torch.device("cuda", 0)]
+        print(p.errors, g._attn.stats, [(e.layer, e.extra.get("finding"), e.z) for e in ev], flush=True)
+        assert not p.errors
+        assert g._attn.stats["calls_checked"] == steps and g._attn.stats["samples"] > 0
+        return ev
+    finally:
+        vllm_plugin.unregister()
+
+
+@pytest.mark.gpu
+def test_attention_checked_through_register_clean(monkeypatch):
+    ev = _serve_steps(monkeypatch, {})
+    assert ev == []
+
+
+@pytest.mark.gpu
+def test_attention_read_of_a_changed_value_is_flagged_through_register(monkeypatch):
+    ev = _serve_steps(monkeypatch, {"read": True})
+    found = {(e.layer, e.extra["finding"]) for e in ev}
+    assert found == {("model.layers.0.attn", "output_wrong_or_misread"),
+                     ("model.layers.1.attn", "output_wrong_or_misread")}, found
+    assert all(e.z > 4 and e.extra["recheck"]["verdict"] in ("output_wrong", "not_rechecked") for e in ev)
+
+
+@pytest.mark.gpu
+def test_wrong_kv_write_is_flagged_through_register(monkeypatch):
+    ev = _serve_steps(monkeypatch, {"write": True})
+    found = {(e.layer, e.extra["finding"]) for e in ev}
+    assert ("model.layers.0.attn", "kv_write_wrong") in found and ("model.layers.1.attn", "kv_write_wrong") in found
+    w = next(e for e in ev if e.extra["finding"] == "kv_write_wrong")
+    assert w.extra["a_wrong_write"]["content_wrong"] and w.extra["a_wrong_write"]["part"] == "key"
