@@ -184,6 +184,34 @@ int sdc_moe_check(int dtype, const void* x, int64_t sx, const void* out, int64_t
                   int64_t* cap_ids, float* cap_g, float* scores_out, void* workspace, int64_t workspace_bytes,
                   hipStream_t stream);
 
+/* ---- the MoE router check -------------------------------------------------------------------------------------
+ * Replaces serve_route.route_check_torch / route_check_triton (serve_route.py:141-184, the Triton kernel
+ * _route_kernel :216-353, its launcher :359-373): when the step in stepbuf[0] (low 32 bits) modulo nlayers is this
+ * router's index and rows_buf[0] (the step's real rows, clamped to m) is positive, recompute the routing policy in
+ * fp32 for SAMPLES = 2 rows ((step / nlayers * 7919 + j * 104729) % real rows) and judge the router's choice as
+ * serve_route.judge does (:91-138): each chosen expert's choice score (softmax, or sigmoid, scores plus the
+ * correction bias when there is one) at least the k-th best of the groups surely chosen less the tolerance
+ * 1e-6 max(|v|, 1) + 4u |v|, and with groups (DeepSeek's grouped top-k; a group scores its two best choice scores
+ * with a bias, its best without; groups within twice the tolerance of the cut may be in or out) also the k-th best of
+ * its group and of the groups that may be chosen; the k ids distinct and in [0, E); the weights the chosen experts'
+ * scores, renormalized over them when renormalize is set, times scale, to 2e-5 + (1e-4 + 6u) |weight|.  A row whose
+ * ids are all -1 is padding and isn't judged.  Otherwise nothing is computed.
+ *   logits (m, E) row stride sl, ldt 0 fp32 / 1 bf16 / 2 fp16; weights (m, K) row stride sw, wdt likewise; ids
+ *   (m, K) row stride si, idt 0 int32 / 1 int64; bias (E) fp32 or null; groups 0 (plain top-k) or a divisor of E up
+ *   to 64 with 0 < topk_group <= groups and topk_group * E / groups >= K; u: 0 for fp32 logits, half the epsilon of
+ *   16-bit ones.  E <= 2048, K <= 32.
+ *   state_row: the router's 6 int64 (calls judged; rows with a wrong expert set; rows with a wrong weight; the
+ *   largest (step & 0x7FFFFFFF) << 32 | kind << 24 | row of a wrong row, kind 2 experts, 1 weights; the worst weight
+ *   difference's float bits; rows judged), added to.  cap_meta (taken, row, step, kind, E, ldt), cap_lg (E floats),
+ *   cap_ids (K int64), cap_w (K floats): the first wrong row while cap_meta[0] is 0.  No host synchronisation, no
+ *   memory set: the call can be captured in a graph. */
+int sdc_route_check(const void* logits, int64_t sl, int ldt, const void* weights, int64_t sw, int wdt,
+                    const void* ids, int64_t si, int idt, const float* bias, int64_t m, int64_t E, int64_t K,
+                    int scoring, int renormalize, int groups, int topk_group, float scale, float u,
+                    const int64_t* rows_buf, const int64_t* stepbuf, int64_t nlayers, int64_t index,
+                    int64_t* state_row, int64_t* cap_meta, float* cap_lg, int64_t* cap_ids, float* cap_w,
+                    hipStream_t stream);
+
 /* ---- both block checksums of one linear layer, one pass over y (no counterpart function in the reference) --------
  * y = x @ W^T (+ bias): the column-block check of sdc_check_static (the serving check, serve.py:301-396) and the
  * row-block check of sdc_matmul_check on the transposed views (W, x^T, y^T, bias[:, None]; checksum.py:435-530),
@@ -358,7 +386,7 @@ int sdc_attn_check_noalloc(int dtype, const void* q, int64_t sqt, int64_t sqh, c
  * "quant_score_i8", "quant_score_fp8", "fingerprint3", "fingerprint2", "kv_fingerprint", "attn_check", "acc_bsums",
  * "acc_finish", "acc_anorm", "acc_gemm", "acc_score" (sdc_matmul_check_acc, sdc_matmul_check_acc_stats),
  * "fused_pack", "fused_side", "fused_mm", "fused_mm_checked" (sdc_fused_mm, sdc_fused_mm_checked), "fp8q_amax",
- * "fp8q_judge" (sdc_fp8_quant_check), "moe_up", "moe_act", "moe_down", "moe_compare" (sdc_moe_check). */
+ * "fp8q_judge" (sdc_fp8_quant_check), "moe_up", "moe_act", "moe_down", "moe_compare" (sdc_moe_check), "route_check" (sdc_route_check). */
 int sdc_profile_enable(int on);
 int sdc_profile_reset(void);
 int sdc_profile_read(const char* name, double* total_ms, int64_t* launches);

@@ -49,6 +49,8 @@ SIGNATURES = {
     "sdc_moe_check_workspace": (I64, [I64, I64, I64]),
     "sdc_moe_check": (I32, [I32, P, I64, P, I64, P, I32, P, P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, I64, I64,
                             I32, I32, P, I64, I64, F32, F32, F32, F32, P, P, P, P, P, P, P, P, I64, P]),
+    "sdc_route_check": (I32, [P, I64, I32, P, I64, I32, P, I64, I32, P, I64, I64, I64, I32, I32, I32, I32, F32, F32,
+                              P, P, I64, I64, P, P, P, P, P, P]),
     "sdc_expected_splits": (I64, [I64, I64, I64]),
     "sdc_linear_check_workspace": (I64, [I64, I64, I64]),
     "sdc_linear_check": (I32, [I32, P, I64, P, I64, P, I64, P, I64, I64, I64, P, I64, P, P, P, P, P, P, F32, F32,

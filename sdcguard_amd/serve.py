@@ -411,6 +411,7 @@ class ServeGuard:
         self._fp8 = None                       # FP8 quantization checks (fp8_checks())
         self._moe = None                       # fused MoE checks (moe_checks())
         self._attn = None                      # sampled attention recompute (attn_checks())
+        self._route = None                     # MoE router checks (route_checks())
         self._marked_step: Optional[int] = None
         self.stats = {"layers": 0, "skipped_layers": 0, "polls": 0, "alerts": 0, "checks_executed": 0,
                       "unjudged_checksums": 0}
@@ -552,6 +553,8 @@ class ServeGuard:
             events += self._moe.poll(wait)
         if self._attn is not None and self._attn.finalized:
             events += self._attn.poll(wait)
+        if self._route is not None and self._route.finalized:
+            events += self._route.poll(wait)
         if self._scan is not None:
             events += self._scan.poll(wait)
         return events
@@ -581,8 +584,16 @@ class ServeGuard:
             self._attn = AttnChecks(self, ATTN_Z if line is None else line)
         return self._attn
 
+    def route_checks(self):
+        """The MoE router checks (serve_route.RouteChecks), created on first use: add() the routers, finalize()
+        before capture; mark_step / end_step / poll reach them through the guard."""
+        if self._route is None:
+            from .serve_route import RouteChecks
+            self._route = RouteChecks(self)
+        return self._route
+
     def _step_checks(self) -> list:
-        return [c for c in (self._fp8, self._moe, self._attn) if c is not None]
+        return [c for c in (self._fp8, self._moe, self._attn, self._route) if c is not None]
 
     def end_step(self) -> None:
         """After a model step's work is queued (the per-step checks stop judging until the next mark_step)."""
@@ -662,7 +673,7 @@ class ServeGuard:
                     lay["module"].__dict__.pop(attr, None)
             for sub in self._step_checks():
                 sub.detach()
-            self._fp8 = self._moe = self._attn = None
+            self._fp8 = self._moe = self._attn = self._route = None
             self.layers.clear()
             self._rows.clear()
             self._scan = None

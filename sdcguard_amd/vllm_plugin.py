@@ -15,9 +15,13 @@ register() is what vLLM's general-plugin loader calls in every process.  With SD
                                          the backend's attention, then the sampled recompute of a registered layer
                                          (serve_attn.AttnChecks: one layer a step, from the paged KV cache) and the
                                          check of the step's own KV writes
+  FusedMoERouter
+    select_experts(hidden, logits, ...)  the router's experts and weights, then the check of a registered router's
+                                         result against its policy recomputed from its logits (serve_route: one
+                                         router a step, 2 rows)
   GPUModelRunner
-    load_model()                         after vLLM's own, the model's attention layers are registered (before any
-                                         graph is captured)
+    load_model()                         after vLLM's own, the model's attention layers and MoE routers are
+                                         registered (before any graph is captured)
     execute_model(...)                   each model step is marked on the device before its work is queued and
                                          closed after it; results are read every SDCGUARD_POLL_EVERY steps (16)
                                          without waiting, and after SDCGUARD_POLL_SECONDS (2) with a wait
@@ -47,6 +51,7 @@ class RequirementNotMet(RuntimeError):
 ATTN_BACKENDS = (("vllm.v1.attention.backends.flash_attn", "FlashAttentionImpl"),
                  ("vllm.v1.attention.backends.triton_attn", "TritonAttentionImpl"))
 RUNNERS = ("vllm.v1.worker.gpu_model_runner", "vllm.v1.worker.gpu.model_runner")
+ROUTER = ("vllm.model_executor.layers.fused_moe.router.fused_moe_router", "FusedMoERouter")
 
 
 class _Plugin:
@@ -63,6 +68,8 @@ class _Plugin:
         self.last_poll = time.monotonic()
         self.attn_registered = False
         self.attn_report: dict = {}
+        self.routers_registered = False
+        self.route_report: dict = {}
         self.errors: dict = {}           # what failed in a hook -> times (the server keeps running)
         self.wrapped: list = []          # (class, attribute, original) to put back
 
@@ -165,6 +172,46 @@ class _Plugin:
         log.info("sdcguard: checking %d of %d attention layers (one a step)", len(ac.layers), len(found))
         return self.attn_report
 
+    # ------------------------------------------------------------------------------------------------ routers
+    def after_route(self, router, logits, weights, ids) -> None:
+        from .serve_route import check_call
+        b = getattr(router, "_sdcguard_route", None)
+        if b is None:
+            return
+        try:
+            check_call(b, logits, weights, ids)
+        except Exception as e:  # noqa: BLE001  (never break serving: the router goes unchecked from now on)
+            router.__dict__.pop("_sdcguard_route", None)
+            self._failed("a routing check", e)
+
+    def register_routers(self, runner) -> dict:
+        """After the model is loaded and before graphs are captured: its MoE routers (the `router` of a module,
+        with select_experts) go to the device's guard, which numbers their turns."""
+        if self.routers_registered:
+            return self.route_report
+        self.routers_registered = True
+        get = getattr(runner, "get_model", None)
+        model = get() if callable(get) else getattr(runner, "model", None)
+        found = []
+        for name, m in (model.named_modules() if model is not None else []):
+            r = getattr(m, "router", None)
+            if r is not None and callable(getattr(r, "select_experts", None)) and \
+                    getattr(r, "_sdcguard_route", None) is None:
+                found.append((f"{name or type(m).__name__}.router", r))
+        if not found:
+            self.route_report = {"checked": 0, "not_checked": {}, "why": "no MoE routers found"}
+            return self.route_report
+        dev = getattr(runner, "device", None)
+        if not isinstance(dev, torch.device):
+            dev = next((p.device for p in model.parameters()), torch.device("cuda", torch.cuda.current_device()))
+        rc = self.guard(dev).route_checks()
+        for name, r in found:
+            rc.add(r, name, dev)
+        rc.finalize()
+        self.route_report = {"checked": len(rc.layers), "not_checked": dict(rc.unsupported)}
+        log.info("sdcguard: checking the routing of %d of %d MoE routers (one a step)", len(rc.layers), len(found))
+        return self.route_report
+
     # ------------------------------------------------------------------------------------------------ steps
     def before_step(self, rows: Optional[int]) -> None:
         for g in self.guards.values():
@@ -232,8 +279,30 @@ def _wrap_attention(plugin: "_Plugin") -> list:
     return done
 
 
+def _wrap_router(plugin: "_Plugin") -> list:
+    """Follow vLLM's MoE routers' select_experts with the routing check.  Returns the class wrapped."""
+    module, cname = ROUTER
+    try:
+        cls = getattr(importlib.import_module(module), cname)
+        orig = cls.__dict__["select_experts"]
+    except Exception as e:  # noqa: BLE001  (a vLLM build without this router: no routing to check)
+        log.info("sdcguard: vLLM's %s not found (%s); MoE routing is not checked", cname, e)
+        return []
+
+    def select_experts(self, hidden_states, router_logits, *args, _orig=orig, **kwargs):
+        out = _orig(self, hidden_states, router_logits, *args, **kwargs)
+        if isinstance(out, tuple) and len(out) == 2:
+            plugin.after_route(self, router_logits, out[0], out[1])
+        return out
+
+    cls.select_experts = select_experts
+    plugin.wrapped.append((cls, "select_experts", orig))
+    return [cname]
+
+
 def _wrap_runner(plugin: "_Plugin") -> list:
-    """Register the attention layers after load_model; mark, close and read each model step around execute_model."""
+    """Register the attention layers and MoE routers after load_model; mark, close and read each model step around
+    execute_model."""
     done = []
     for module in RUNNERS:
         try:
@@ -248,6 +317,10 @@ def _wrap_runner(plugin: "_Plugin") -> list:
                     plugin.register_attention(self)
                 except Exception as e:  # noqa: BLE001  (never break loading: attention goes unchecked)
                     plugin._failed("registering the attention layers", e)
+                try:
+                    plugin.register_routers(self)
+                except Exception as e:  # noqa: BLE001  (never break loading: routing goes unchecked)
+                    plugin._failed("registering the MoE routers", e)
                 return out
             GM.load_model = load_model
             plugin.wrapped.append((GM, "load_model", orig_load))
@@ -309,6 +382,7 @@ def register() -> None:
     M.apply = apply
     M._sdcguard_originals = (orig_load, orig_apply)
     plugin.attn_backends = _wrap_attention(plugin)
+    plugin.routers = _wrap_router(plugin)
     plugin.runners = _wrap_runner(plugin)
 
 

@@ -22,6 +22,11 @@ cases, the inputs and the reference's answers:
   * weights.npz    serve_weights.model_digest and fingerprint of a small model with 1, 2, 4 and 8-byte parameters;
   * moe.npz        serve_moe.moe_check_torch (the sampled fused-MoE recompute): the state row and the kept row after
                    one call on the reference's verification scenarios and a larger routed-first case;
+  * route.npz      serve_route.route_check_torch (the MoE router check) and serve_route.judge on every row: the
+                   softmax, sigmoid, biased and grouped (DeepSeek) policies, fp32 / bf16 / fp16 logits, routing as
+                   the policy gives it, a moved expert, a repeated expert, weights off, an id out of range, a
+                   padding row, tied scores, an inactive step and a step without real rows: the state row, the kept
+                   row and every row's (wrong set, wrong weight, weight differences);
   * attn.npz       serve_attn.attn_check_torch on make_case calls (shapes, request mixes, a sliding window, wrong
                    outputs, wrong KV writes and slots, block ids outside the cache, non-finite values, padding)
                    over several steps: every sample's per-dimension scores, the 18-column state row and the
@@ -615,6 +620,97 @@ def make_moe(sm):
     return len(names)
 
 
+ROUTE_POLICIES = {
+    # name: (E, k, scoring (0 softmax, 1 sigmoid), renormalize, bias, groups, topk_group, scale)
+    "softmax_top4": (64, 4, 0, True, False, 0, 0, 1.0),
+    "sigmoid_top6": (64, 6, 1, False, False, 0, 0, 1.0),
+    "biased_top4": (64, 4, 1, True, True, 0, 0, 1.5),
+    "deepseek_grouped": (256, 8, 1, True, True, 8, 4, 2.5),
+    "grouped_softmax": (64, 6, 0, False, False, 4, 2, 1.0),
+    "grouped_small_groups": (96, 4, 1, True, True, 12, 3, 1.0),
+}
+
+
+def make_route(sr):
+    """serve_route.route_check_torch on seeded router calls (8 rows; state, kept row) and serve_route.judge on every
+    row of the same call (fp32 logits as the check computes them)."""
+    st_ = _Store()
+    out = st_.out
+    names = []
+    for pname, (E, k, scoring, renorm, has_bias, groups, tg, scale) in ROUTE_POLICIES.items():
+        for dtype in (torch.float32, torch.bfloat16, torch.float16):
+            gen = torch.Generator().manual_seed(len(names) + 7)
+            M = 8
+            bias = (torch.randn(E, generator=gen) * 0.03) if has_bias else None
+            lg = (torch.randn(M, E, generator=gen) * 2.0).to(dtype)
+            w, ids = sr._reference_route(lg.float(), k, scoring, renorm, bias, groups, tg, scale)
+            cases = ["clean", "moved_expert", "repeated_expert", "weights_off", "weights_within", "id_out_of_range",
+                     "padding", "inactive", "no_rows"]
+            if dtype == torch.float32 and not groups:
+                cases.append("ties")
+            for case in cases:
+                lg_c, w_c, ids_c = lg.clone(), w.clone(), ids.clone()
+                step, real = 5, M
+                if case == "moved_expert":
+                    ids_c[:, -1] = lg.float().argmin(-1).to(ids_c.dtype)
+                elif case == "repeated_expert":
+                    ids_c[:, 1] = ids_c[:, 0]
+                elif case == "weights_off":
+                    w_c[:, 0] *= 1.02
+                elif case == "weights_within":
+                    w_c = w_c * (1 + 3e-6)
+                elif case == "id_out_of_range":
+                    ids_c[:, 0] = E + 3
+                elif case == "padding":
+                    ids_c[:] = -1
+                elif case == "inactive":
+                    step = 6
+                elif case == "no_rows":
+                    real = 0
+                elif case == "ties":
+                    lg_c = torch.zeros(M, E)
+                    lg_c[:, 0] = 3.0
+                    w_c, ids_c = sr._reference_route(lg_c, k, scoring, renorm, bias, groups, tg, scale)
+                    ids_c[:, 1] = (ids_c[:, 1] + 7) % E                 # another of the tied experts
+                    ids_c[:, 1] = torch.where(ids_c[:, 1] == 0, torch.ones_like(ids_c[:, 1]), ids_c[:, 1])
+                    s_ = torch.softmax(lg_c, -1) if scoring == 0 else torch.sigmoid(lg_c)
+                    ww = s_.gather(1, ids_c.long())
+                    w_c = ((ww / ww.sum(-1, keepdim=True)) if renorm else ww) * scale
+                state = torch.zeros(1, sr.COLS, dtype=torch.int64)
+                caps = sr.new_caps("cpu", 1, E)
+                rb = torch.full((1,), real, dtype=torch.int64)
+                sb = torch.full((1,), step, dtype=torch.int64)
+                sr.route_check_torch(lg_c, w_c, ids_c, k, scoring, renorm, bias, groups, tg, scale, rb, sb, state, 0,
+                                     2, 1, *caps)
+                u = sr.unit_roundoff(lg_c.dtype)
+                sb_all, wb_all, diff_all = sr.judge(lg_c.float(), ids_c.long(), w_c.float(), k, scoring, renorm,
+                                                    bias, groups, tg, scale, u)
+                i = len(names)
+                names.append(f"{pname}_{str(dtype).replace('torch.', '')}_{case}")
+                p = f"c{i}_"
+                if dtype == torch.float32:
+                    out[p + "logits"] = lg_c.numpy()
+                else:
+                    out[p + "logits_bits"] = _bits(lg_c)
+                out[p + "ids"] = ids_c.numpy().astype(np.int32)
+                out[p + "w"] = w_c.float().numpy()
+                out[p + "bias"] = bias.numpy() if bias is not None else np.zeros(0, np.float32)
+                out[p + "meta"] = np.array([E, k, scoring, int(renorm), groups, tg, {torch.float32: 0,
+                                            torch.bfloat16: 1, torch.float16: 2}[dtype], step, real, 2, 1], np.int64)
+                out[p + "scale"] = np.float32(scale)
+                out[p + "state"] = state[0].numpy()
+                out[p + "cap_meta"] = caps[0][0].numpy()
+                out[p + "cap_lg"] = caps[1][0].numpy()
+                out[p + "cap_ids"] = caps[2][0, :k].numpy()
+                out[p + "cap_w"] = caps[3][0, :k].numpy()
+                out[p + "set_bad"] = sb_all.numpy()
+                out[p + "w_bad"] = wb_all.numpy()
+                out[p + "diff"] = diff_all.float().numpy()
+    out["names"] = np.array(names)
+    np.savez_compressed(os.path.join(OUT, "route.npz"), **out)
+    return len(names)
+
+
 def _serve_cases():
     g = torch.Generator().manual_seed(11)
     shapes = [(64, 256, 300, True), (1, 256, 1000, False), (200, 96, 40, True), (33, 130, 129, True),
@@ -884,7 +980,11 @@ def main():
     from sdcguard import serve as sv
     cs.USE_FAST = False
     torch.set_num_threads(4)
-    which = sys.argv[1:] or ["signs", "train", "acc", "serve", "quant", "attn", "fused", "fp8", "weights", "moe"]
+    which = sys.argv[1:] or ["signs", "train", "acc", "serve", "quant", "attn", "fused", "fp8", "weights", "moe",
+                             "route"]
+    if "route" in which:
+        from sdcguard import serve_route as sr
+        print("route.npz:", make_route(sr), "cases")
     if "moe" in which:
         from sdcguard import serve_moe as sm
         print("moe.npz:", make_moe(sm), "cases")

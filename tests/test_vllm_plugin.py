@@ -291,3 +291,125 @@ def test_wrong_kv_write_is_flagged_through_register(monkeypatch):
     assert ("model.layers.0.attn", "kv_write_wrong") in found and ("model.layers.1.attn", "kv_write_wrong") in found
     w = next(e for e in ev if e.extra["finding"] == "kv_write_wrong")
     assert w.extra["a_wrong_write"]["content_wrong"] and w.extra["a_wrong_write"]["part"] == "key"
+
+
+# ------------------------------------------------------------------------------------------------- MoE routers
+MOE_E, MOE_K, MOE_T = 64, 6, 96
+
+
+def _fake_moe_runner(fault: dict):
+    """vLLM's router layout (FusedMoERouter.select_experts, subclassed by the routers) and a runner whose model has
+    two MoE blocks with a router each: a DeepSeek-style grouped router and a softmax top-k one.  fault["route"]: the
+    routers' kernel puts a wrong expert in every row's last slot."""
+    import types as _t
+
+    class FusedMoERouter:
+        def select_experts(self, hidden_states, router_logits, topk_indices_dtype=None, *, input_ids=None):
+            s = torch.softmax(router_logits.float(), -1) if self.scoring_func == "softmax" else \
+                torch.sigmoid(router_logits.float())
+            ch = s + self.e_score_correction_bias if self.e_score_correction_bias is not None else s
+            groups = getattr(self, "num_expert_group", 0) or 0
+            if groups:
+                m = ch.shape[0]
+                g = ch.view(m, groups, -1)
+                gs = g.topk(2, -1).values.sum(-1) if self.e_score_correction_bias is not None else g.amax(-1)
+                keep = torch.zeros(m, groups, dtype=torch.bool, device=ch.device)
+                keep.scatter_(1, gs.topk(self.topk_group, -1).indices, True)
+                ch = ch.masked_fill(~keep.repeat_interleave(MOE_E // groups, 1), float("-inf"))
+            ids = ch.topk(self.top_k, -1).indices
+            if fault.get("route"):
+                ids[:, -1] = router_logits.float().argmin(-1)
+            w = s.gather(1, ids)
+            if self.renormalize:
+                w = w / w.sum(-1, keepdim=True)
+            scale = getattr(self, "routed_scaling_factor", 1.0) if type(self).__name__ != "FusedTopKRouter" else 1.0
+            return (w * scale).float(), ids.to(torch.int32)
+
+    class GroupedTopKRouter(FusedMoERouter):
+        def __init__(self, bias):
+            self.top_k, self.global_num_experts, self.scoring_func, self.renormalize = MOE_K, MOE_E, "sigmoid", True
+            self.e_score_correction_bias, self.routed_scaling_factor = bias, 2.5
+            self.num_expert_group, self.topk_group = 8, 3
+
+    class FusedTopKRouter(FusedMoERouter):
+        def __init__(self):
+            self.top_k, self.global_num_experts, self.scoring_func, self.renormalize = MOE_K, MOE_E, "softmax", True
+            self.e_score_correction_bias = None
+
+    class MoEBlock(torch.nn.Module):
+        def __init__(self, router):
+            super().__init__()
+            self.router = router
+
+    class GPUModelRunner:
+        def __init__(self):
+            self.device = torch.device("cuda", 0)
+            self.gen = torch.Generator(device="cpu").manual_seed(9)
+
+        def load_model(self):
+            bias = (torch.randn(MOE_E, generator=self.gen) * 0.03).cuda()
+            self.model = torch.nn.ModuleDict({"moe0": MoEBlock(GroupedTopKRouter(bias)),
+                                              "moe1": MoEBlock(FusedTopKRouter())})
+
+        def get_model(self):
+            return self.model
+
+        def execute_model(self, scheduler_output):
+            for blk in self.model.values():
+                logits = (torch.randn(MOE_T + 8, MOE_E, generator=self.gen) * 2).bfloat16().cuda()   # 8 padding
+                hidden = torch.zeros(MOE_T + 8, 16, device="cuda")
+                blk.router.select_experts(hidden, logits)
+            return None
+
+    names = ("vllm", "vllm.v1", "vllm.v1.worker", "vllm.v1.worker.gpu_model_runner", "vllm.model_executor.layers",
+             "vllm.model_executor.layers.fused_moe", "vllm.model_executor.layers.fused_moe.router",
+             "vllm.model_executor.layers.fused_moe.router.fused_moe_router")
+    mods = {n: types.ModuleType(n) for n in names}
+    mods["vllm.v1.worker.gpu_model_runner"].GPUModelRunner = GPUModelRunner
+    mods["vllm.model_executor.layers.fused_moe.router.fused_moe_router"].FusedMoERouter = FusedMoERouter
+    base, _ = _fake_vllm()
+    for k in ("vllm.model_executor", "vllm.model_executor.layers.linear"):
+        mods[k] = base[k]
+    mods["vllm.model_executor.layers"].linear = base["vllm.model_executor.layers.linear"]
+    return mods, GPUModelRunner, FusedMoERouter, _t.SimpleNamespace(total_num_scheduled_tokens=MOE_T)
+
+
+def _route_steps(monkeypatch, fault: dict, steps: int = 6) -> list:
+    from sdcguard_amd import vllm_plugin
+    monkeypatch.setenv("SDCGUARD", "1")
+    monkeypatch.setenv("SDCGUARD_POLL_EVERY", "1000")
+    mods, Runner, Router, sched = _fake_moe_runner(fault)
+    for k, v in mods.items():
+        monkeypatch.setitem(sys.modules, k, v)
+    orig = Router.__dict__["select_experts"]
+    vllm_plugin.register()
+    try:
+        assert Router.__dict__["select_experts"] is not orig
+        runner = Runner()
+        runner.load_model()
+        p = vllm_plugin.plugin_state()
+        assert p.route_report["checked"] == 2, p.route_report
+        for _ in range(steps):
+            runner.execute_model(sched)
+        ev = vllm_plugin.poll(wait=True)
+        rc = p.guards[torch.device("cuda", 0)]._route
+        print(p.errors, rc.stats, [(e.layer, e.extra.get("finding"), e.extra.get("captured")) for e in ev], flush=True)
+        assert not p.errors
+        assert rc.stats["calls"] == steps and rc.stats["rows"] == 2 * steps
+        return ev
+    finally:
+        vllm_plugin.unregister()
+        assert Router.__dict__["select_experts"] is orig
+
+
+@pytest.mark.gpu
+def test_routing_checked_through_register_clean(monkeypatch):
+    assert _route_steps(monkeypatch, {}) == []
+
+
+@pytest.mark.gpu
+def test_wrong_expert_from_a_router_is_flagged_through_register(monkeypatch):
+    ev = _route_steps(monkeypatch, {"route": True})
+    found = {(e.layer, e.extra["finding"]) for e in ev}
+    assert found == {("moe0.router", "wrong_experts"), ("moe1.router", "wrong_experts")}, found
+    assert all(e.extra["recheck"]["verdict"] == "output_wrong" and e.extra["captured"]["row"] < MOE_T for e in ev)
