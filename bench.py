@@ -17,10 +17,15 @@ y^T = W x^T, one pass over y for both).  Inputs are resident in HBM; the timed l
                 workload at full size, median of >= 5 runs
 
 "more" holds one line per other workload, each with its own value, roofline and cpu_baseline:
+  serve_bf16_4096x4096x14336  the serving check alone (column-block, ServeGuard.check) of the headline's layer
+  fused_bf16_4096x4096x14336  the layer's GEMM with both checksums scored in its epilogue, against hipBLASLt's GEMM
   fp8_mlp_4096x4096x14336   fp8 e4m3 linear layer with per-token / per-channel scales, bf16 output, column check
   int8_2048x7168x4096       int8 W8A8 GEMM, exact int32 check
   fp8_2048x7168x4096        fp8 e4m3 GEMM with scales 10^U(-3,-1), bf16 output
   moe_4096x8of64_2048x1408  MoE grouped GEMM: 4096 tokens, top-8 of 64 experts (Zipf 1.1), bf16
+  moe_recompute_4096x8of64_2048x1408  the sampled fused-MoE recompute (two rows, their experts' weights)
+  fp8_quant_check_4096x4096  the FP8 input-quantization check of a serving layer (per-tensor and per-token scales)
+  route_check_8192x256_grouped  the MoE router check of a DeepSeek-V3 router (microseconds per call)
   kv_fingerprint_28x4096    fingerprints of every block of a 28-layer x 4096-block paged KV cache (7.52 GB)
   attn_recompute_28x64      sampled attention recompute: one decode step of 64 sequences over 28 layers, 16
                             sampled (row, head) pairs a layer
@@ -345,6 +350,133 @@ def cpu_linear(x, W, y, alg: int, seconds: float) -> dict:
                       "made in the call as the reference's CPU path makes them; GB/s over the same 273.94 MB"}
 
 
+def bench_serve_bf16(ctx: Ctx) -> dict:
+    """The column-block check alone, as serving runs it (ServeGuard.check -> sdc_check_static: what register()
+    queues after every checked linear layer), on the same layer as the headline."""
+    torch, a = ctx.torch, ctx.a
+    from sdcguard_amd.serve import ServeGuard, decode_counts, decode_state
+    M, K, N = 4096, 4096, 14336
+    name = "serve_bf16_4096x4096x14336"
+    g = torch.Generator(device=ctx.dev).manual_seed(0)
+    W = (torch.randn(N, K, device=ctx.dev, generator=g) * 0.02).bfloat16()
+    xs = [torch.randn(M, K, device=ctx.dev, generator=g).bfloat16() for _ in range(a.copies)]
+    ys = [torch.nn.functional.linear(x, W) for x in xs]
+    guard = ServeGuard()
+    layer = torch.nn.Module()
+    slot = guard.add_layer(layer, "mlp.gate_up_proj", weight=W)
+    nb = guard.layers[slot]["cs"].nb
+
+    def check(i):
+        guard.check(slot, xs[i % a.copies], ys[i % a.copies], with_bias=False)
+
+    for i in range(a.warmup):
+        check(i)
+    torch.cuda.synchronize()
+    st = guard.state(ctx.dev)[slot:slot + 1].cpu()
+    z = decode_state(st)[0][0]
+    checks = decode_counts(st)[0][0]
+    if checks != a.warmup or not z < guard.z:
+        raise RuntimeError(f"{name}: {checks} checks counted of {a.warmup}, clean max z {z}")
+    ctx.settle(check)
+    ms = ctx.loop_ms(check, a.steps)
+    km = ctx.kernel_ms(check, a.steps, ("expected_gemm", "serve_fused"))
+    xb, yb, pb = M * K * 2, M * N * 2, K * 6 * nb * 2
+    alg = xb + yb + pb
+    amounts = {"expected_gemm": ("mfma", 2.0 * M * K * 6 * nb, "bf16"), "serve_fused": ("hbm", yb, None)}
+    patterns = {"expected_gemm": r"expected_gemm_kernel<0", "serve_fused": r"serve_fused_kernel"}
+    ent, roof = _roof(km, amounts, name, patterns, a.steps)
+
+    def gemm(i):
+        torch.mm(xs[i % a.copies], W.t(), out=ys[i % a.copies])
+
+    for i in range(3):
+        gemm(i)
+    gemm_ms = ctx.loop_ms(gemm, a.steps)
+    both_ms = ctx.loop_ms(lambda i: (gemm(i), check(i)), a.steps)
+    value = alg / (ms * 1e-3) / 1e9
+    line = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "ms_per_step": round(ms, 5), "dtype": "bf16",
+            "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+            "config": {"workload": "the serving check alone (column-block checksums against the layer's block sums, "
+                                   "ServeGuard.check as the vLLM plugin queues it) of the bf16 Llama-MLP linear "
+                                   "layer, x 4096x4096 N(0,1), W 14336x4096 N(0,0.02), y = x W^T bf16, block 128",
+                       "name": name, "m": M, "k": K, "n": N, "algorithmic_bytes": alg},
+            "roofline": roof, "kernels": ent, "clean_max_z": round(z, 4),
+            "guarded_gemm_ms": round(gemm_ms, 5),
+            "overhead_pct_warm": round(100.0 * (both_ms - gemm_ms) / gemm_ms, 2),
+            "overhead_pct_cold": round(100.0 * ms / gemm_ms, 2)}
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_serve(xs[0], W, ys[0], alg, a.cpu_seconds)
+    return line
+
+
+def cpu_serve(x, W, y, alg: int, seconds: float) -> dict:
+    """The torch restatement of the column-block check (oracle.torch_check.zscores) on the whole layer."""
+    from oracle import torch_check
+    cores = _cpu_threads()
+    xc, Wt, yc = x.cpu(), W.cpu().t(), y.cpu()
+    med, runs = _cpu_median(lambda: torch_check.zscores(xc, Wt, yc), seconds)
+    return {"value": round(alg / med / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "median_s": round(med, 4), "runs": runs, **_cpu_info(),
+            "sample": "oracle.torch_check.zscores (the reference's checksum._zscores in torch, fp32, on the CPU) over "
+                      "the whole 4096x4096x14336 layer, block sums of W made in the call; GB/s over the same bytes"}
+
+
+def bench_fused(ctx: Ctx) -> dict:
+    """The GEMM with the check in its epilogue (fused_mm_checked: the product and both checksums' scores from one
+    fp32 accumulator, nothing read back) against hipBLASLt's GEMM alone, on the headline's layer."""
+    torch, a = ctx.torch, ctx.a
+    from sdcguard_amd import checksum as csm
+    from sdcguard_amd.fused import fused_mm_checked
+    M, K, N = 4096, 4096, 14336
+    name = "fused_bf16_4096x4096x14336"
+    g = torch.Generator(device=ctx.dev).manual_seed(0)
+    W = (torch.randn(N, K, device=ctx.dev, generator=g) * 0.02).bfloat16()
+    Wt = W.t()
+    xs = [torch.randn(M, K, device=ctx.dev, generator=g).bfloat16() for _ in range(a.copies)]
+    ys = [torch.empty(M, N, dtype=torch.bfloat16, device=ctx.dev) for _ in range(a.copies)]
+    res = torch.zeros(3, dtype=torch.int64, device=ctx.dev)
+
+    def fused(i):
+        fused_mm_checked(xs[i % a.copies], Wt, out=res)
+
+    for i in range(a.warmup):
+        fused(i)
+    torch.cuda.synchronize()
+    st = csm.resolve([csm.CheckStat(result=res, m=M, nb=N // 128, batched=False, z=6.0)], 6.0)[0]
+    if not st.ok:
+        raise RuntimeError(f"{name}: the clean product raised (max z {st.max_z})")
+    ctx.settle(fused)
+    ms = ctx.loop_ms(fused, a.steps)
+    km = ctx.kernel_ms(fused, a.steps, ("fused_mm_checked", "fused_pack"))
+
+    def gemm(i):
+        torch.mm(xs[i % a.copies], Wt, out=ys[i % a.copies])
+
+    for i in range(3):
+        gemm(i)
+    gemm_ms = ctx.loop_ms(gemm, a.steps)
+    nb = N // 128
+    flops = 2.0 * M * K * N + 2.0 * M * K * 12 * nb       # the product and the expected side (2 sums x 3 parts x 2)
+    amounts = {"fused_mm_checked": ("mfma", flops, "bf16")}
+    ent, roof = _roof({"fused_mm_checked": km["fused_mm_checked"]}, amounts, name,
+                      {"fused_mm_checked": r"fused_(mm|gemm).*kernel"}, a.steps)
+    alg = M * K * 2 + N * K * 2 + M * N * 2
+    value = alg / (ms * 1e-3) / 1e9
+    return {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "ms_per_step": round(ms, 5), "dtype": "bf16",
+            "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+            "config": {"workload": "the product y = x W^T of the bf16 Llama-MLP linear layer (x 4096x4096, W "
+                                   "14336x4096) from the library's MFMA GEMM with both checksums scored in its "
+                                   "epilogue (fused_mm_checked), against the same product from hipBLASLt (torch.mm)",
+                       "name": name, "m": M, "k": K, "n": N, "algorithmic_bytes": alg},
+            "roofline": roof, "kernels": ent, "clean_max_z": round(st.max_z, 4),
+            "fused_pack_us": round(km["fused_pack"][0] * 1e3, 2) if km["fused_pack"][1] else 0.0,
+            "guarded_gemm_ms": round(gemm_ms, 5),
+            "overhead_pct_vs_hipblaslt": round(100.0 * (ms - gemm_ms) / gemm_ms, 2),
+            "cpu_baseline": {"value": None, "unit": "GB/s", "cores": 0, "kind": "port",
+                             "sample": "none: the fused line is the GEMM itself; the CPU check of this layer is the "
+                                       "headline's and the serving line's baseline"}}
+
+
 def _fp8_problem(ctx, seed, m, k, n, copies):
     torch = ctx.torch
     g = torch.Generator(device=ctx.dev).manual_seed(seed)
@@ -554,6 +686,243 @@ def cpu_moe(A, Bw, out, sizes, alg, seconds) -> dict:
             "sample": "oracle.torch_check.zscores per expert over the whole grouped product (64 experts)"}
 
 
+def bench_fp8_quant(ctx: Ctx) -> dict:
+    """The FP8 input-quantization check of a serving layer (sdc_fp8_quant_check) on the headline layer's input:
+    per-tensor dynamic scales (the scale against max |x| over the step's 4096 real rows: one read of x, the
+    line's value), and per-token scales (two sampled rows: a latency figure)."""
+    torch, a = ctx.torch, ctx.a
+    from sdcguard_amd import serve_fp8 as sf
+    M, K = 4096, 4096
+    name = "fp8_quant_check_4096x4096"
+    g = torch.Generator(device=ctx.dev).manual_seed(31)
+    xs = [torch.randn(M, K, device=ctx.dev, generator=g).bfloat16() for _ in range(a.copies)]
+    qt, st_, qk, sk = [], [], [], []
+    for x in xs:
+        s_t = (x.float().abs().amax() / 448.0).reshape(1)
+        qt.append((x.float() * (1.0 / s_t)).clamp(-448, 448).to(torch.float8_e4m3fn))
+        st_.append(s_t)
+        s_k = (x.float().abs().amax(1) / 448.0).clamp(min=1.0 / (448 * 512))
+        qk.append((x.float() / s_k[:, None]).clamp(-448, 448).to(torch.float8_e4m3fn))
+        sk.append(s_k.reshape(-1, 1))
+    rows = torch.tensor([M], dtype=torch.int64, device=ctx.dev)
+    step = torch.zeros(1, dtype=torch.int64, device=ctx.dev)
+    state = torch.zeros(2, sf.COLS, dtype=torch.int64, device=ctx.dev)
+
+    def tensor_check(i):
+        sf.quant_check(xs[i % a.copies], qt[i % a.copies], st_[i % a.copies], sf.RECIPES["dynamic_tensor"], None,
+                       None, rows, step, state, 0)
+
+    def token_check(i):
+        sf.quant_check(xs[i % a.copies], qk[i % a.copies], sk[i % a.copies], sf.RECIPES["dynamic_token"], None,
+                       None, rows, step, state, 1)
+
+    for i in range(a.warmup):
+        tensor_check(i)
+        token_check(i)
+    torch.cuda.synchronize()
+    k = state.cpu().tolist()
+    if k[0][sf.C_CALLS] != a.warmup or k[1][sf.C_CALLS] != a.warmup or any(
+            r[c] for r in k for c in (sf.C_SCALE, sf.C_OUTSIDE, sf.C_VALUES, sf.C_STATIC)):
+        raise RuntimeError(f"{name}: the clean quantization raised or was not judged: {k}")
+    ctx.settle(tensor_check)
+    ms = ctx.loop_ms(tensor_check, a.steps)
+    km = ctx.kernel_ms(tensor_check, a.steps, ("fp8q_amax", "fp8q_judge"))
+    ms_tok = ctx.loop_ms(token_check, a.steps)
+    km_tok = ctx.kernel_ms(token_check, a.steps, ("fp8q_judge",))
+    xb = M * K * 2
+    alg = xb + 2 * K * 3 + 4
+    ent, roof = _roof(km, {"fp8q_amax": ("hbm", xb, None)}, name, {"fp8q_amax": r"amax"}, a.steps)
+    ent["fp8q_judge"] = {"avg_us": round(km["fp8q_judge"][0] * 1e3, 2), "bound": "latency"}
+    value = alg / (ms * 1e-3) / 1e9
+    return {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "ms_per_step": round(ms, 5), "dtype": "bf16",
+            "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+            "config": {"workload": "the FP8 input-quantization check of one serving layer: x 4096x4096 bf16 N(0,1) "
+                                   "quantized to e4m3 with a per-tensor dynamic scale (max |x| over the 4096 real "
+                                   "rows / 448, against the scale the GEMM got; two sampled rows' codes); also the "
+                                   "per-token recipe (two sampled rows' scales and codes)",
+                       "name": name, "m": M, "k": K, "algorithmic_bytes": alg},
+            "roofline": roof, "kernels": ent,
+            "per_token_us_per_call": round(ms_tok * 1e3, 2),
+            "per_token_judge_us": round(km_tok["fp8q_judge"][0] * 1e3, 2),
+            "cpu_baseline": cpu_fp8_quant(xs[0], qt[0], st_[0], alg, a.cpu_seconds) if not a.no_cpu else None}
+
+
+def cpu_fp8_quant(x, xq, s, alg, seconds) -> dict:
+    """The oracle's quantization check (numpy) of the per-tensor call."""
+    import numpy as np
+    import torch
+
+    from oracle import serve_fp8 as of8
+    cores = _cpu_threads()
+    xf = x.float().cpu().numpy()
+    q = xq.view(torch.uint8).cpu().numpy()
+    sc = s.float().cpu().numpy()
+    fn = lambda: of8.quant_check(xf, q, sc, 1, None, None, x.shape[0], 0)    # noqa: E731
+    med, runs = _cpu_median(fn, seconds)
+    del np
+    return {"value": round(alg / med / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "median_s": round(med, 4), "runs": runs, **_cpu_info(),
+            "sample": "oracle.serve_fp8.quant_check (numpy, one thread: the amax is one pass) of the whole "
+                      "per-tensor call, 4096 rows"}
+
+
+def _moe_outputs(torch, x, w13, w2, ids, gw):
+    """The fused MoE kernel's output with its roundings: per expert, x W13^T in fp32 rounded, SiLU(gate) rounded,
+    times up rounded, (.) W2^T in fp32 times the routing weight rounded, the experts' terms added in fp32."""
+    T, H = x.shape
+    I = w2.shape[2]
+    acc = torch.zeros(T, H, dtype=torch.float32, device=x.device)
+    for e in range(w13.shape[0]):
+        r, slot = (ids == e).nonzero(as_tuple=True)
+        if r.numel() == 0:
+            continue
+        h = (x[r].float() @ w13[e].float().t()).bfloat16()
+        act = torch.nn.functional.silu(h[:, :I].float()).bfloat16()
+        p = (act.float() * h[:, I:].float()).bfloat16()
+        o = ((p.float() @ w2[e].float().t()) * gw[r, slot].float()[:, None]).bfloat16()
+        acc.index_add_(0, r, o.float())
+    return acc.bfloat16()
+
+
+def bench_moe_recompute(ctx: Ctx) -> dict:
+    """The sampled recompute of a fused MoE layer (sdc_moe_check) at the grouped workload's shape: 4096 tokens, top-8
+    of 64 experts, H 2048, I 1408; every call is the active one (one layer), two rows recomputed."""
+    torch, a = ctx.torch, ctx.a
+    from sdcguard_amd import serve_moe as sm
+    name = "moe_recompute_4096x8of64_2048x1408"
+    T, E, TOPK, H, I = 4096, 64, 8, 2048, 1408
+    g = torch.Generator(device=ctx.dev).manual_seed(41)
+    x = torch.randn(T, H, device=ctx.dev, generator=g).bfloat16()
+    w13 = (torch.randn(E, 2 * I, H, device=ctx.dev, generator=g) * 0.02).bfloat16()
+    w2 = (torch.randn(E, H, I, device=ctx.dev, generator=g) * 0.02).bfloat16()
+    gw, ids = torch.topk(torch.softmax(torch.randn(T, E, device=ctx.dev, generator=g), -1), TOPK, -1)
+    gw = (gw / gw.sum(-1, keepdim=True)).float()
+    ids = ids.to(torch.int32)
+    out = _moe_outputs(torch, x, w13, w2, ids, gw)
+    state = torch.zeros(1, sm.COLS, dtype=torch.int64, device=ctx.dev)
+    cap = (torch.zeros(1, sm.CAP_COLS, dtype=torch.int32, device=ctx.dev), torch.zeros(1, H, device=ctx.dev),
+           torch.zeros(1, H, device=ctx.dev), torch.zeros(1, 64, dtype=torch.int64, device=ctx.dev),
+           torch.zeros(1, 64, device=ctx.dev))
+    words = torch.tensor([(T << 32) | (1000 + i) for i in range(64)], dtype=torch.int64, device=ctx.dev)
+
+    def check(i):
+        sm.moe_check(x, out, gw, ids, w13, w2, None, 0, False, state, 0, words[i % 64:i % 64 + 1], 1, 0, *cap,
+                     sm.MOE_Z)
+
+    for i in range(a.warmup):
+        check(i)
+    torch.cuda.synchronize()
+    k = state[0].cpu().tolist()
+    z = struct_f32(k[sm.C_ROW] >> 32)
+    if k[sm.C_CALLS] != a.warmup or not z < sm.MOE_Z:
+        raise RuntimeError(f"{name}: clean calls counted {k[sm.C_CALLS]} of {a.warmup}, max z {z}")
+    ctx.settle(check)
+    ms = ctx.loop_ms(check, a.steps)
+    names = ("moe_up", "moe_act", "moe_down", "moe_compare")
+    km = ctx.kernel_ms(check, a.steps, names)
+    # bytes: the distinct experts of the two sampled rows (their W13 and W2), the rows' x and outputs
+    idc = ids.cpu()
+    per_expert = (2 * I * H + H * I) * 2
+    tot = 0
+    for i in range(a.steps):
+        rows = sm.sample_rows(torch.tensor(1000 + i % 64), T, "cpu").tolist()
+        tot += len({int(e) for r in rows for e in idc[r].tolist()}) * per_expert + 2 * 2 * H * 2
+    alg = tot / a.steps
+    up_bytes = alg * (2 * I * H) / (3 * I * H)
+    amounts = {"moe_up": ("hbm", up_bytes, None), "moe_down": ("hbm", alg - up_bytes, None)}
+    ent, roof = _roof(km, amounts, name, {"moe_up": r"moe_up", "moe_down": r"moe_down"}, a.steps)
+    for nm in ("moe_act", "moe_compare"):
+        ent[nm] = {"avg_us": round(km[nm][0] * 1e3, 2), "bound": "latency"}
+    value = alg / (ms * 1e-3) / 1e9
+    return {"metric": "sampled MoE recompute GB/s of the sampled rows' expert weights, 1 GPU",
+            "value": round(value, 2), "unit": "GB/s", "ms_per_step": round(ms, 5), "us_per_call": round(ms * 1e3, 2),
+            "dtype": "bf16", "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+            "config": {"workload": "one active call of the sampled fused-MoE recompute: 4096 tokens, top-8 of 64 "
+                                   "experts (softmax routing), H 2048, I 1408 (gate-up 2816x2048, down 2048x1408 "
+                                   "bf16), SiLU; two rows recomputed with the fused kernel's roundings",
+                       "name": name, "tokens": T, "experts": E, "top_k": TOPK, "hidden": H, "inter": I,
+                       "algorithmic_bytes_per_call": int(alg)},
+            "roofline": roof, "kernels": ent, "clean_max_z": round(z, 4),
+            "cpu_baseline": cpu_moe_recompute(x, out, gw, ids, w13, w2, alg, a.cpu_seconds) if not a.no_cpu else None}
+
+
+def struct_f32(bits: int) -> float:
+    import struct
+    return struct.unpack("<f", struct.pack("<I", int(bits) & 0xFFFFFFFF))[0]
+
+
+def cpu_moe_recompute(x, out, gw, ids, w13, w2, alg, seconds) -> dict:
+    """The oracle's recompute (numpy) of one call's two sampled rows, on the experts they use."""
+    import numpy as np
+
+    from oracle import serve_moe as om
+    cores = _cpu_threads()
+    rows = om.sample_rows(1000, x.shape[0], 1)
+    used = sorted({int(e) for r in rows for e in ids[r].tolist()})
+    remap = {e: i for i, e in enumerate(used)}
+    xs = x[rows].float().cpu().numpy()
+    ids_c = np.array([[remap[int(e)] for e in ids[r].tolist()] for r in rows], np.int32)
+    g_c = gw[rows].cpu().numpy()
+    w13_c = w13[used].float().cpu().numpy()
+    w2_c = w2[used].float().cpu().numpy()
+    fn = lambda: om.recompute(xs, ids_c, g_c, w13_c, w2_c, None, 0, False, "bf16")   # noqa: E731
+    med, runs = _cpu_median(fn, seconds)
+    nbytes = len(used) * (w13_c[0].size + w2_c[0].size) * 2 + 2 * 2 * x.shape[1] * 2
+    return {"value": round(nbytes / med / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "median_s": round(med, 4), "runs": runs, **_cpu_info(),
+            "sample": f"oracle.serve_moe.recompute (numpy BLAS) of one call's two sampled rows over their "
+                      f"{len(used)} experts"}
+
+
+def bench_route(ctx: Ctx) -> dict:
+    """The MoE router check (sdc_route_check) of a DeepSeek-V3 router: 8192 tokens, sigmoid scores with a correction
+    bias, top-8 of 256 experts within the best 4 of 8 groups, scaled by 2.5; every call is the active one."""
+    torch, a = ctx.torch, ctx.a
+    from sdcguard_amd import serve_route as sr
+    name = "route_check_8192x256_grouped"
+    T, E, TOPK, G, TG = 8192, 256, 8, 8, 4
+    g = torch.Generator(device=ctx.dev).manual_seed(43)
+    lg = (torch.randn(T, E, device=ctx.dev, generator=g) * 2).bfloat16()
+    bias = torch.randn(E, device=ctx.dev, generator=g) * 0.03
+    s = torch.sigmoid(lg.float())
+    ch = (s + bias).view(T, G, E // G)
+    keep = torch.zeros(T, G, dtype=torch.bool, device=ctx.dev)
+    keep.scatter_(1, ch.topk(2, -1).values.sum(-1).topk(TG, -1).indices, True)
+    ids = (s + bias).masked_fill(~keep.repeat_interleave(E // G, 1), float("-inf")).topk(TOPK, -1).indices
+    w = s.gather(1, ids)
+    w = (w / w.sum(-1, keepdim=True) * 2.5).float()
+    ids = ids.to(torch.int32)
+    st = torch.zeros(1, sr.COLS, dtype=torch.int64, device=ctx.dev)
+    cap = (torch.zeros(1, sr.CAP_COLS, dtype=torch.int64, device=ctx.dev), torch.zeros(1, E, device=ctx.dev),
+           torch.zeros(1, TOPK, dtype=torch.int64, device=ctx.dev), torch.zeros(1, TOPK, device=ctx.dev))
+    real = torch.tensor([T], dtype=torch.int64, device=ctx.dev)
+    steps_t = torch.arange(64, dtype=torch.int64, device=ctx.dev) + 1000
+
+    def check(i):
+        sr.route_check(lg, w, ids, TOPK, 1, True, bias, G, TG, 2.5, real, steps_t[i % 64:i % 64 + 1], st, 0, 1, 0,
+                       *cap)
+
+    for i in range(a.warmup):
+        check(i)
+    torch.cuda.synchronize()
+    k = st[0].cpu().tolist()
+    if k[sr.C_CALLS] != a.warmup or k[sr.C_SET] or k[sr.C_WEIGHT]:
+        raise RuntimeError(f"{name}: the clean routing raised or was not judged: {k}")
+    ctx.settle(check)
+    ms = ctx.loop_ms(check, a.steps)
+    km = ctx.kernel_ms(check, a.steps, ("route_check",))
+    alg = 2 * (E * 2 + TOPK * 4 + TOPK * 4)
+    ent, roof = _roof(km, {"route_check": ("hbm", alg, None)}, name, {"route_check": r"route_kernel"}, a.steps)
+    return {"metric": "MoE router check microseconds per router call, 1 GPU", "value": round(ms * 1e3, 2),
+            "unit": "us", "higher_is_better": False, "ms_per_step": round(ms, 5), "dtype": "f32",
+            "config": {"workload": "one active call of the MoE router check: DeepSeek-V3 routing (8192 tokens, bf16 "
+                                   "logits, sigmoid + correction bias, top-8 of 256 experts in the best 4 of 8 groups, "
+                                   "renormalized, x2.5); two rows' policy recomputed and judged",
+                       "name": name, "tokens": T, "experts": E, "top_k": TOPK, "algorithmic_bytes": alg},
+            "roofline": roof, "kernels": ent,
+            "note": "latency-bound: a call reads two rows (about 1.1 KB); the figure is the launch's duration"}
+
+
 def _kv_cache(ctx, layers=28, nblk=4096):
     torch = ctx.torch
     g = torch.Generator(device=ctx.dev).manual_seed(55)
@@ -717,20 +1086,42 @@ def cpu_attn(kv, q, outs, keys, vals, qsl, lens, bt, slots, L_, samples, alg_ste
     f = lambda t: t.float().cpu().numpy()                                   # noqa: E731
     args = (f(q[layer]), f(outs[layer]), kv_c, f(keys[layer]), f(vals[layer]), qsl.cpu().numpy(), lens.numpy(),
             bt_c, sl_c)
-    med, runs = _cpu_median(lambda: OA.check(*args, step=1000, scale=128 ** -0.5, samples=samples), seconds)
-    return {"value": round(alg_step / L_ / med / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+    from concurrent.futures import ThreadPoolExecutor
+
+    from threadpoolctl import threadpool_limits
+
+    def one(_):
+        OA.check(*args, step=1000, scale=128 ** -0.5, samples=samples)
+
+    # one layer call per host thread at a time (numpy's kernels release the GIL; BLAS kept to one thread each)
+    with threadpool_limits(limits=1), ThreadPoolExecutor(cores) as ex:
+        med, runs = _cpu_median(lambda: list(ex.map(one, range(cores))), seconds)
+    return {"value": round(cores * alg_step / L_ / med / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
             "median_s": round(med, 4), "runs": runs, **_cpu_info(),
-            "sample": "oracle.attn.check (numpy) of one layer's call (16 samples) over the blocks the step's "
-                      "sequences hold; GB/s over a layer's average sampled K/V bytes"}
+            "sample": f"oracle.attn.check (numpy) of a layer's call (16 samples) over the blocks the step's sequences "
+                      f"hold, {cores} calls at once on {cores} threads; GB/s over a layer's average sampled K/V bytes "
+                      f"times the calls"}
 
 
-WORKLOADS = ("bf16_mlp_4096x4096x14336", "fp8_mlp_4096x4096x14336", "int8_2048x7168x4096", "fp8_2048x7168x4096",
-             "moe_4096x8of64_2048x1408", "kv_fingerprint_28x4096", "attn_recompute_28x64")
+WORKLOADS = ("bf16_mlp_4096x4096x14336", "serve_bf16_4096x4096x14336", "fused_bf16_4096x4096x14336",
+             "fp8_mlp_4096x4096x14336", "int8_2048x7168x4096", "fp8_2048x7168x4096", "moe_4096x8of64_2048x1408",
+             "moe_recompute_4096x8of64_2048x1408", "fp8_quant_check_4096x4096", "route_check_8192x256_grouped",
+             "kv_fingerprint_28x4096", "attn_recompute_28x64")
 
 
 def run(ctx: Ctx, name: str, kv_holder: dict) -> dict:
     if name == "bf16_mlp_4096x4096x14336":
         return bench_bf16_mlp(ctx)
+    if name == "serve_bf16_4096x4096x14336":
+        return bench_serve_bf16(ctx)
+    if name == "fused_bf16_4096x4096x14336":
+        return bench_fused(ctx)
+    if name == "moe_recompute_4096x8of64_2048x1408":
+        return bench_moe_recompute(ctx)
+    if name == "fp8_quant_check_4096x4096":
+        return bench_fp8_quant(ctx)
+    if name == "route_check_8192x256_grouped":
+        return bench_route(ctx)
     if name == "fp8_mlp_4096x4096x14336":
         return bench_quant(ctx, "fp8", 4096, 4096, 14336, name, seed=21)
     if name == "int8_2048x7168x4096":

@@ -13,9 +13,10 @@
 //                  range
 //   weights        the chosen experts' scores, renormalized over them when the policy does, times the scale, to
 //                  2e-5 + (1e-4 + 6 u) |weight|
-// One workgroup per sample: the row's choice scores live in LDS; the k-th bests come from k rounds of a
-// workgroup (or, within a group, a wave) maximum with the winner taken out, so equal scores count each, as top-k
-// does.  The router's state row gets its counts and the packed last finding by atomics, and the first wrong row
+// One workgroup per sample: the row's choice scores live in LDS, and the k-th bests come from places: an expert's
+// place in its group is the number of its group's experts that come before it (larger, or equal at a smaller
+// index, as top-k orders them), so the expert at place k - 1 holds the k-th best, equal scores counted each; the
+// groups are placed the same way, and the k best of the groups surely in are placed among the k best of each.  The router's state row gets its counts and the packed last finding by atomics, and the first wrong row
 // since the last read is kept (logits, ids, weights) behind a compare-and-swap on its flag.  No host
 // synchronisation, no memory set: the call can be captured in a graph.
 #include <math.h>
@@ -73,57 +74,60 @@ __device__ __forceinline__ float tol_of(float v, float u) {
   return TIE * fmaxf(a, 1.f) + U_CHOICE * u * a;
 }
 
-// the larger of two (value, index) pairs; equal values: the smaller index (the first occurrence)
-__device__ __forceinline__ void better(float& v, int& i, float ov, int oi) {
-  if (ov > v || (ov == v && oi < i)) {
-    v = ov;
-    i = oi;
-  }
+// Wave reductions on DPP lane moves (quad swaps, then the half-row and row mirrors: every lane of a row of 16 holds
+// the row's result) and four lane reads: no LDS round trips.  The whole wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float rows_of_wave(float v, bool is_max) {
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return is_max ? fmaxf(fmaxf(a, b), fmaxf(c, d)) : (a + b) + (c + d);
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  return rows_of_wave(v, true);
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  return rows_of_wave(v, false);
 }
 
-__device__ __forceinline__ void wave_best(float& v, int& i) {
-#pragma unroll
-  for (int msk = 1; msk < 64; msk <<= 1) better(v, i, __shfl_xor(v, msk, 64), __shfl_xor(i, msk, 64));
+// Whether value a (at index ia) comes before value b (at index ib) in top-k order: larger first, equal values by
+// index, as the reference's sorts and top-k take them.  (Branch-free: a short-circuit form compiles to a branch per
+// comparison.)
+__device__ __forceinline__ int before(float a, int ia, float b, int ib) {
+  return (int)(a > b) | ((int)(a == b) & (int)(ia < ib));
 }
 
-// the smaller (value, index); equal values: the smaller index
-__device__ __forceinline__ void wave_least(float& v, int& i) {
-#pragma unroll
-  for (int msk = 1; msk < 64; msk <<= 1) {
-    const float ov = __shfl_xor(v, msk, 64);
-    const int oi = __shfl_xor(i, msk, 64);
-    if (ov < v || (ov == v && oi < i)) {
-      v = ov;
-      i = oi;
-    }
-  }
-}
-
-// The k-th largest of the n values vals[base + p * step] (p < n <= 64 * 32) held by one wave, counting equal values
-// each: k rounds of the wave maximum, its first occurrence taken out (lane p % 64, bit p / 64 of its mask).
-__device__ float wave_kth(const float* vals, int base, int step, int n, int k, int lane) {
-  uint32_t gone = 0;
-  float last = -__builtin_inff();
-  for (int round = 0; round < k; ++round) {
-    float v = -__builtin_inff();
-    int i = 0x7FFFFFFF;
-    for (int q = 0; lane + 64 * q < n; ++q)
-      if (!(gone >> q & 1u)) better(v, i, vals[base + (lane + 64 * q) * step], lane + 64 * q);
-    wave_best(v, i);
-    last = v;
-    if (i != 0x7FFFFFFF && i % 64 == lane) gone |= 1u << (i / 64);
-  }
-  return last;
+// The same order as one unsigned 64-bit key: the float's bits made monotonic (-0 counted as +0) above the index
+// complemented, so a key above another comes before it.
+__device__ __forceinline__ unsigned long long order_key(float v, int i) {
+  const uint32_t u = __float_as_uint(v + 0.f);
+  const uint32_t m = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)m << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
 }
 
 __global__ __launch_bounds__(NT) void route_kernel(RouteArgs a) {
-  __shared__ float sc[MAXE], ch[MAXE];          // the row's scores and choice scores
-  __shared__ float redv[NW];
-  __shared__ int redi[NW];
-  __shared__ float gsc[MAXG], kwg[MAXG];        // per group: its score, its k-th best choice score
+  __shared__ __attribute__((aligned(16))) float sc[MAXE], ch[MAXE];   // the row's scores and choice scores
+  __shared__ unsigned long long key[MAXE];      // the choice scores' order keys
+  __shared__ unsigned short grank[MAXE];        // each expert's place within its group (0: the group's best)
+  __shared__ unsigned long long ck[MAXE];       // per group and place < k: that expert's key
+  __shared__ float red[NW];
+  __shared__ float top1[MAXG], top2[MAXG], gsc[MAXG], kwg[MAXG];   // per group: its two best, score, k-th best
   __shared__ int gin[MAXG];                     // per group: bit 0 surely in, bit 1 may be in
-  __shared__ float s_low, s_kth;
+  __shared__ float s_gth, s_gnext, s_low, s_kth, s_w[MAXK], s_d[MAXK];
   __shared__ int s_won;
+  __shared__ long long s_id[MAXK];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t step = a.stepbuf[0] & M32;
   int64_t real = a.rows_buf[0];
@@ -132,7 +136,17 @@ __global__ __launch_bounds__(NT) void route_kernel(RouteArgs a) {
   const int j = blockIdx.x;
   const int64_t row = ((step / a.nl) * ROW_A + j * ROW_B) % real;
   const int E = (int)a.E, K = (int)a.K, G = a.groups, TG = a.topk_group;
-  const float NEG = -__builtin_inff();
+  const int gsz = G ? E / G : E, NG = G ? G : 1;
+  const float NEG = -__builtin_inff(), POS = __builtin_inff();
+
+  // the router's choice for the row (wave 0, one chosen expert a lane), loaded now: it is judged at the end
+  int64_t id = -1;
+  float kw = 0.f;
+  if (w == 0 && lane < K) {
+    id = a.idt == 0 ? (int64_t)reinterpret_cast<const int32_t*>(a.ids)[row * a.si + lane]
+                    : reinterpret_cast<const int64_t*>(a.ids)[row * a.si + lane];
+    kw = load_val(a.w, a.wdt, row * a.sw + lane);
+  }
 
   // ---- scores and choice scores
   float lgv[EPT];
@@ -143,23 +157,32 @@ __global__ __launch_bounds__(NT) void route_kernel(RouteArgs a) {
     lgv[q] = e < E ? load_val(a.logits, a.ldt, row * a.sl + e) : NEG;
     mx = fmaxf(mx, lgv[q]);
   }
+  if (t < MAXG) {
+    top1[t] = NEG;
+    top2[t] = NEG;
+    kwg[t] = NEG;                               // (a group of fewer than k experts has no k-th best)
+  }
+  if (t == 0) {
+    s_gth = NEG;
+    s_gnext = NEG;
+    s_low = POS;
+    s_kth = NEG;
+  }
   float den = 1.f;
   if (a.scoring == 0) {
-#pragma unroll
-    for (int msk = 1; msk < 64; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
-    if (lane == 0) redv[w] = mx;
+    mx = wave_max(mx);
+    if (lane == 0) red[w] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(redv[0], redv[1]), fmaxf(redv[2], redv[3]));
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float sum = 0.f;
 #pragma unroll
     for (int q = 0; q < EPT; ++q)
       if (t + NT * q < E) sum += expf(lgv[q] - mx);
-#pragma unroll
-    for (int msk = 1; msk < 64; msk <<= 1) sum += __shfl_xor(sum, msk, 64);
+    sum = wave_sum(sum);
     __syncthreads();
-    if (lane == 0) redv[w] = sum;
+    if (lane == 0) red[w] = sum;
     __syncthreads();
-    den = (redv[0] + redv[1]) + (redv[2] + redv[3]);
+    den = (red[0] + red[1]) + (red[2] + red[3]);
   }
 #pragma unroll
   for (int q = 0; q < EPT; ++q) {
@@ -167,117 +190,92 @@ __global__ __launch_bounds__(NT) void route_kernel(RouteArgs a) {
     if (e < E) {
       const float s = a.scoring == 0 ? expf(lgv[q] - mx) / den : 1.f / (1.f + expf(-lgv[q]));
       sc[e] = s;
-      ch[e] = a.bias ? s + a.bias[e] : s;
+      const float c = a.bias ? s + a.bias[e] : s;
+      ch[e] = c;
+      key[e] = order_key(c, e);
     }
   }
   __syncthreads();
 
-  // ---- groups: scores, the k-th best within each, which are in
-  const int gsz = G ? E / G : E;
+  // ---- each expert's place within its group (the whole row without groups): the experts of its group that come
+  //      before it.  Its group's best, second best and k-th best are the experts at places 0, 1 and k - 1.
+#pragma unroll
+  for (int q = 0; q < EPT; ++q) {
+    const int e = t + NT * q;
+    if (e < E) {
+      const float v = ch[e];
+      const unsigned long long kv = key[e];
+      const int g = e / gsz, b0 = g * gsz;
+      int place = 0;
+#pragma unroll 8
+      for (int p = 0; p < gsz; ++p) place += (int)(key[b0 + p] > kv);
+      grank[e] = (unsigned short)place;
+      if (place == 0) top1[g] = v;
+      if (place == 1) top2[g] = v;
+      if (place == K - 1) kwg[g] = v;
+      if (G && place < K) ck[g * K + place] = kv;
+    }
+  }
+  __syncthreads();
+
   if (G) {
-    for (int g = w; g < G; g += NW) {
-      float m1 = NEG, m2 = NEG;
-      int i1 = 0x7FFFFFFF, i2 = 0x7FFFFFFF;
-      for (int p = lane; p < gsz; p += 64) better(m1, i1, ch[g * gsz + p], p);
-      wave_best(m1, i1);
-      float score = m1;
-      if (a.bias) {
-        for (int p = lane; p < gsz; p += 64)
-          if (p != i1) better(m2, i2, ch[g * gsz + p], p);
-        wave_best(m2, i2);
-        score = m1 + m2;
-      }
-      const float kg = gsz >= K ? wave_kth(ch, g * gsz, 1, gsz, K, lane) : NEG;
-      if (lane == 0) {
-        gsc[g] = score;
-        kwg[g] = kg;
-      }
+    // ---- groups: a group's score (its two best with a bias, its best without); the cut (the topk_group-th best
+    //      score) and the next; which groups are surely in and which may be
+    if (t < G) gsc[t] = a.bias ? top1[t] + top2[t] : top1[t];
+    __syncthreads();
+    if (t < G) {
+      const float v = gsc[t];
+      int place = 0;
+      for (int h = 0; h < G; ++h) place += before(gsc[h], h, v, t);
+      if (place == TG - 1) s_gth = v;
+      if (place == TG) s_gnext = v;
     }
     __syncthreads();
-    if (w == 0) {
-      // the topk_group-th best group score (the cut) and the next one, by rounds of the maximum over the groups
-      const float gv = lane < G ? gsc[lane] : NEG;
-      uint32_t out = 0;
-      float gth = NEG, gnext = NEG;
-      for (int round = 0; round <= TG; ++round) {
-        float v = out ? NEG : gv;
-        int i = lane < G && !out ? lane : 0x7FFFFFFF;
-        wave_best(v, i);
-        if (round < TG) {
-          gth = v;
-          if (i == lane) out = 1;
-        } else {
-          gnext = TG < G ? v : NEG;
-        }
-      }
+    if (t < G) {
+      const float gth = s_gth, v = gsc[t];
       const float tolg = 2.f * tol_of(gth, a.u);
-      const bool amb = gnext >= gth - tolg;
-      const bool clear = lane < G && gv >= gth;
-      const bool sure = amb ? (lane < G && gv > gth + tolg) : clear;
-      const bool may = amb ? (lane < G && gv >= gth - tolg) : clear;
-      if (lane < G) gin[lane] = (sure ? 1 : 0) | (may ? 2 : 0);
-      // the topk_group-th smallest k-th best over the groups that may be in
-      float kv = (lane < G && may) ? kwg[lane] : __builtin_inff();
-      uint32_t used = 0;
-      float low = __builtin_inff();
-      for (int round = 0; round < TG; ++round) {
-        float v = used ? __builtin_inff() : kv;
-        int i = lane < G && !used ? lane : 0x7FFFFFFF;
-        wave_least(v, i);
-        low = v;
-        if (i == lane) used = 1;
-      }
-      if (lane == 0) s_low = low;
+      const bool amb = s_gnext >= gth - tolg;
+      const bool clear = v >= gth;
+      const bool sure = amb ? v > gth + tolg : clear;
+      const bool may = amb ? v >= gth - tolg : clear;
+      gin[t] = (sure ? 1 : 0) | (may ? 2 : 0);
     }
     __syncthreads();
+    // the topk_group-th smallest k-th best over the groups that may be in
+    if (t < G && (gin[t] & 2)) {
+      const float v = kwg[t];
+      int place = 0;
+      for (int h = 0; h < G; ++h)
+        if (gin[h] & 2) place += (int)(kwg[h] < v) | ((int)(kwg[h] == v) & (int)(h < t));
+      if (place == TG - 1) s_low = v;
+    }
   }
 
-  // ---- the k-th best choice score over the experts of the groups surely in: k workgroup rounds
-  {
-    float cv[EPT];
-#pragma unroll
-    for (int q = 0; q < EPT; ++q) {
-      const int e = t + NT * q;
-      cv[q] = (e < E && (!G || (gin[e / gsz] & 1))) ? ch[e] : NEG;
-    }
-    float kth = NEG;
-    for (int round = 0; round < K; ++round) {
-      float v = NEG;
-      int i = 0x7FFFFFFF;
-#pragma unroll
-      for (int q = 0; q < EPT; ++q) better(v, i, cv[q], t + NT * q);
-      wave_best(v, i);
-      if (lane == 0) {
-        redv[w] = v;
-        redi[w] = i;
+  // ---- the k-th best choice score over the experts of the groups surely in: only an expert among the k best of
+  //      its group can be among the k best of several groups, so those candidates (held by group and place) are
+  //      placed among themselves
+  if (!G) {
+    if (t == 0) s_kth = kwg[0];
+  } else {
+    const int per = gsz < K ? gsz : K;
+    for (int c = t; c < G * K; c += NT) {
+      const int g = c / K;
+      if ((c % K) < per && (gin[g] & 1)) {
+        const unsigned long long kv = ck[c];
+        int place = 0;
+        for (int h = 0; h < G; ++h)
+          if (gin[h] & 1)
+            for (int q = 0; q < per; ++q) place += (int)(ck[h * K + q] > kv);
+        if (place == K - 1) s_kth = ch[0xFFFFFFFFu - (uint32_t)kv];
       }
-      __syncthreads();
-      v = redv[0];
-      i = redi[0];
-#pragma unroll
-      for (int q = 1; q < NW; ++q) better(v, i, redv[q], redi[q]);
-      kth = v;
-      if (i != 0x7FFFFFFF && i % NT == t) {
-#pragma unroll
-        for (int q = 0; q < EPT; ++q)
-          if (q == i / NT) cv[q] = NEG;
-      }
-      __syncthreads();
     }
-    if (t == 0) s_kth = kth;
   }
   __syncthreads();
 
   // ---- the router's choices (wave 0, one chosen expert a lane)
   if (w == 0) {
     const bool km = lane < K;
-    int64_t id = -1;
-    float kw = 0.f;
-    if (km) {
-      id = a.idt == 0 ? (int64_t)reinterpret_cast<const int32_t*>(a.ids)[row * a.si + lane]
-                      : reinterpret_cast<const int64_t*>(a.ids)[row * a.si + lane];
-      kw = load_val(a.w, a.wdt, row * a.sw + lane);
-    }
+    if (km) s_id[lane] = (long long)id;
     const bool valid = km && id >= 0 && id < E;
     const int kc = (int)(id < 0 ? 0 : (id >= E ? E - 1 : id));
     float bnd = s_kth;
@@ -288,30 +286,33 @@ __global__ __launch_bounds__(NT) void route_kernel(RouteArgs a) {
       bnd = fmaxf(fmaxf(bnd, s_low), kwg[gk]);
     }
     const bool ok = valid && alk && ch[kc] >= bnd - tol_of(bnd, a.u);
-    // a repeated id among the K
+    const float sk = valid ? sc[kc] : 0.f;
+    if (km) s_w[lane] = sk;
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    // a repeated id among the k, and the chosen experts' scores added in order
     bool dup = false;
-    for (int q = 0; q < MAXK; ++q) {
-      const int64_t o = __shfl((long long)id, q, 64);
-      if (q < K && q < lane && km && o == id) dup = true;
+    float ssum = 0.f;
+    for (int q = 0; q < K; ++q) {
+      dup = dup || (km && q < lane && s_id[q] == (long long)id);
+      ssum += s_w[q];
     }
     const bool set_bad = __any((km && !ok) || dup);
     const bool pad = __all(!km || id == -1);
-    const float sk = valid ? sc[kc] : 0.f;
-    float ssum = km ? sk : 0.f;
-#pragma unroll
-    for (int msk = 1; msk < 64; msk <<= 1) ssum += __shfl_xor(ssum, msk, 64);
     float ref = a.renorm ? sk / (ssum + 1e-20f) : sk;
     ref = ref * a.scale;
     const float diff = valid ? fabsf(kw - ref) : 0.f;
     const float wrel = (float)((double)W_REL + (double)U_WEIGHT * (double)a.u);   // (summed in double, as stated)
     const bool wrong_w = valid && !(diff <= W_ABS + wrel * fabsf(ref));
     const bool w_bad = __any(wrong_w) && !set_bad;
-    float worst = diff;
-#pragma unroll
-    for (int msk = 1; msk < 64; msk <<= 1) worst = fmaxf(worst, __shfl_xor(worst, msk, 64));
+    if (km) s_d[lane] = diff;
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
     unsigned long long* st = reinterpret_cast<unsigned long long*>(a.state);
     int won = 0;
     if (lane == 0) {
+      float worst = 0.f;
+      for (int q = 0; q < K; ++q) worst = fmaxf(worst, s_d[q]);
       if (j == 0) atomicAdd(st + C_CALLS, 1ull);
       if (!pad) {
         atomicAdd(st + C_ROWS, 1ull);
@@ -333,7 +334,7 @@ __global__ __launch_bounds__(NT) void route_kernel(RouteArgs a) {
       }
       s_won = won;
     }
-    if (__shfl(won, 0, 64) && km) {
+    if (__builtin_amdgcn_readfirstlane(won) && km) {
       a.cap_ids[lane] = id;
       a.cap_w[lane] = kw;
     }
