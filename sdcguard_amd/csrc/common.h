@@ -103,6 +103,82 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   return v;
 }
 
+// Wave reductions on DPP lane moves: xor 1 and xor 2 (quad swaps), the half-row and row mirrors (every lane of a
+// row of 16 then holds its row's result), then the four rows read through lanes 0, 16, 32 and 48.  No LDS round
+// trips, unlike the shuffles above; every lane of the wave must be active.  (Integer maxima and sums: any order
+// gives the same result.)
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));
+  v = max(v, dpp_u32<0x4E>(v));
+  v = max(v, dpp_u32<0x141>(v));
+  v = max(v, dpp_u32<0x140>(v));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ int wave_sum_i32_dpp(int v) {
+  v += (int)dpp_u32<0xB1>((uint32_t)v);
+  v += (int)dpp_u32<0x4E>((uint32_t)v);
+  v += (int)dpp_u32<0x141>((uint32_t)v);
+  v += (int)dpp_u32<0x140>((uint32_t)v);
+  return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+         (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
+}
+// (Float sums: the order is the lanes' pairs, then quads, eights and rows, then the rows in pairs.)
+__device__ __forceinline__ float wave_sum_f32_dpp(float v) {
+  v += __uint_as_float(dpp_u32<0xB1>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<0x4E>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<0x141>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<0x140>(__float_as_uint(v)));
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (a + b) + (c + d);
+}
+__device__ __forceinline__ float wave_max_f32_dpp(float v) {
+  v = fmaxf(v, __uint_as_float(dpp_u32<0xB1>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x4E>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x141>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x140>(__float_as_uint(v))));
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+template <int CTRL>
+__device__ __forceinline__ int64_t dpp_i64(int64_t v) {
+  const uint32_t lo = dpp_u32<CTRL>((uint32_t)(uint64_t)v), hi = dpp_u32<CTRL>((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ int64_t readlane_i64(int64_t v, int l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(uint64_t)v, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ int64_t wave_max_i64_dpp(int64_t v) {
+  int64_t o = dpp_i64<0xB1>(v);
+  v = o > v ? o : v;
+  o = dpp_i64<0x4E>(v);
+  v = o > v ? o : v;
+  o = dpp_i64<0x141>(v);
+  v = o > v ? o : v;
+  o = dpp_i64<0x140>(v);
+  v = o > v ? o : v;
+  int64_t r = readlane_i64(v, 0);
+#pragma unroll
+  for (int l = 16; l < 64; l += 16) {
+    const int64_t q = readlane_i64(v, l);
+    r = q > r ? q : r;
+  }
+  return r;
+}
+
 // bits of a float as an int64 holding the unsigned 32-bit pattern
 __device__ __forceinline__ int64_t fbits64(float f) { return (int64_t)(uint32_t)__float_as_uint(f); }
 

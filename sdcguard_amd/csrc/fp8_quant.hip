@@ -117,8 +117,8 @@ __global__ __launch_bounds__(256) void fp8q_amax_kernel(Fp8Args a) {
     ma = rm > ma ? rm : ma;
     if (row < real) mi = rm > mi ? rm : mi;
   }
-  mi = wave_max_u32(mi);
-  ma = wave_max_u32(ma);
+  mi = wave_max_u32_dpp(mi);
+  ma = wave_max_u32_dpp(ma);
   if (lane == 0) {
     red[w][0] = mi;
     red[w][1] = ma;
@@ -167,30 +167,71 @@ __global__ __launch_bounds__(256) void fp8q_judge_kernel(Fp8Args a) {
   // the sampled rows: their max |x| and their values against the GEMM's codes
   uint32_t am[SAMPLES];
   int nbad[SAMPLES], none = 0;
+  float inv[SAMPLES];
 #pragma unroll
   for (int j = 0; j < SAMPLES; ++j) {
     am[j] = 0;
     nbad[j] = 0;
-    const float inv = 1.0f / use[j];
-    for (int64_t kk = t; kk < a.k; kk += 256) {
-      const float x = load_x<DT>(a.x, rows[j] * a.sxm + kk * a.sxk);
-      const uint32_t xb = abs_bits(x);
-      am[j] = xb > am[j] ? xb : am[j];
-      float v = divide ? x / use[j] : x * inv;
-      v = v != v ? v : fminf(fmaxf(v, -FP8_MAX), FP8_MAX);
-      const int d = abs(fp8_order(to_e4m3(v)) - fp8_order(a.xq[rows[j] * a.sqm + kk * a.sqk]));
-      nbad[j] += d >= 2;
-      none += d == 1;
-    }
+    inv[j] = 1.0f / use[j];
   }
-  mi = wave_max_u32(mi);
-  ma = wave_max_u32(ma);
+  // one value of sampled row j against the GEMM's code for it
+  auto judge_one = [&](int j, float x, uint32_t code) {
+    const uint32_t xb = abs_bits(x);
+    am[j] = xb > am[j] ? xb : am[j];
+    float v = divide ? x / use[j] : x * inv[j];
+    v = v != v ? v : fminf(fmaxf(v, -FP8_MAX), FP8_MAX);
+    const int d = abs(fp8_order(to_e4m3(v)) - fp8_order(code));
+    nbad[j] += d >= 2;
+    none += d == 1;
+  };
+  const bool vec = DT != DT_F32 && a.sxk == 1 && a.sqk == 1 && a.k % 8 == 0 && a.sxm % 8 == 0 && a.sqm % 8 == 0 &&
+                   ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.xq & 7) == 0;
+  if (vec) {
+    // 8 values a load (16 bytes of x, 8 of codes); both rows' loads of U chunks issued before any is used
+    constexpr int U = 2;
+    const int64_t nch = a.k / 8;
+    for (int64_t c0 = t; c0 < nch; c0 += 256 * U) {
+      uint4 xv[SAMPLES][U];
+      uint2 qv[SAMPLES][U];
+#pragma unroll
+      for (int j = 0; j < SAMPLES; ++j)
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t c = c0 + 256 * u;
+          if (c < nch) {
+            xv[j][u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + rows[j] * a.sxm + 8 * c);
+            qv[j][u] = *reinterpret_cast<const uint2*>(a.xq + rows[j] * a.sqm + 8 * c);
+          }
+        }
+#pragma unroll
+      for (int j = 0; j < SAMPLES; ++j)
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (c0 + 256 * u >= nch) continue;
+          const uint32_t ws[4] = {xv[j][u].x, xv[j][u].y, xv[j][u].z, xv[j][u].w};
+          const uint32_t qs[2] = {qv[j][u].x, qv[j][u].y};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t qw = qs[e / 2] >> (16 * (e & 1));
+            judge_one(j, lo_of<DT>(ws[e]), qw & 0xFFu);
+            judge_one(j, hi_of<DT>(ws[e]), (qw >> 8) & 0xFFu);
+          }
+        }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < SAMPLES; ++j)
+      for (int64_t kk = t; kk < a.k; kk += 256)
+        judge_one(j, load_x<DT>(a.x, rows[j] * a.sxm + kk * a.sxk), a.xq[rows[j] * a.sqm + kk * a.sqk]);
+  }
+  mi = wave_max_u32_dpp(mi);
+  ma = wave_max_u32_dpp(ma);
 #pragma unroll
   for (int j = 0; j < SAMPLES; ++j) {
-    am[j] = wave_max_u32(am[j]);
-    nbad[j] = wave_sum_i32(nbad[j]);
+    am[j] = wave_max_u32_dpp(am[j]);
+    nbad[j] = wave_sum_i32_dpp(nbad[j]);
   }
-  none = wave_sum_i32(none);
+  none = wave_sum_i32_dpp(none);
   if (lane == 0) {
     ru[w][0] = mi;
     ru[w][1] = ma;

@@ -15,8 +15,8 @@
 // the device: no host synchronisation, graph-safe): moe_up (one wave per row of W13: 16-byte loads of the expert's
 // weights against the sampled input row, wave reduction), moe_act (h and its rounding sensitivity s per sampled
 // (row, expert) into scratch), moe_down (one wave per output row of W2: the sum, the sum of squares and the worst
-// |w| s), moe_compare (one workgroup per sampled row: experts summed, scored, keys, capture; workgroup 0 also scans
-// the real rows' expert ids).
+// |w| s), moe_compare (one workgroup per sampled row: experts summed, scored, keys, capture; NSCAN more scan the
+// real rows' expert ids).
 #include "common.h"
 #include "profile.h"
 
@@ -28,6 +28,7 @@ constexpr int64_t M32 = 0xFFFFFFFFll;
 enum { C_ROW, C_COL, C_OUT, C_REF, C_STEP, C_CALLS, C_ROWS, C_UNJ, C_UNROUTED, C_PARTIAL, C_BADROW, COLS };
 constexpr int WPB = 4;                           // waves per workgroup (256 threads)
 constexpr int RPW = 4;                           // matrix rows per wave
+constexpr int NSCAN = 8;                         // workgroups of moe_compare scanning the real rows' expert ids
 
 struct MoeArgs {
   const void* x;                                 // (m, H) layer input
@@ -128,16 +129,8 @@ __device__ __forceinline__ bool bad_id(const MoeArgs& a, int64_t id) {
   return id != -1 && (id < 0 || id >= (a.emap ? a.maplen : a.E));
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m, SDC_WAVE);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, SDC_WAVE));
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return wave_sum_f32_dpp(v); }
+__device__ __forceinline__ float wave_max(float v) { return wave_max_f32_dpp(v); }
 
 // dots of RPW weight rows (n 16-bit values each, rows w[r], null past the matrix) with a float vector v, the rows
 // read together so each chunk of v (and of sens) is read once for all of them; each lane takes 8 consecutive values
@@ -304,7 +297,8 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
 __device__ __forceinline__ int64_t fb(float f) { return (int64_t)(uint32_t)__float_as_uint(f); }
 
 // 4. one workgroup per sampled row: the experts summed and every output scored; the worst into the keys; the first
-// row over the line kept; workgroup 0 also counts the call and scans every known real row's expert ids
+// row over the line kept; workgroup 0 also counts the call.  Workgroups SAMPLES .. SAMPLES + NSCAN - 1 scan every
+// known real row's expert ids.
 template <int DT>
 __global__ __launch_bounds__(256) void moe_compare_kernel(MoeArgs a) {
   __shared__ float rz[4];
@@ -315,11 +309,61 @@ __global__ __launch_bounds__(256) void moe_compare_kernel(MoeArgs a) {
   const Live l = live_of(a);
   if (!l.live) return;
   const int j = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+  unsigned long long* s = reinterpret_cast<unsigned long long*>(a.state);
+  if (j >= SAMPLES) {
+    // the routing's validity: every known real row's expert ids, NSCAN workgroups striding over the rows, four
+    // rows a thread at a time (their ids' loads in flight together)
+    if (((a.stepbuf[0] >> 32) & 0x7FFFFFFFll) == 0) return;
+    int nn = 0, ns = 0;
+    int64_t last = 0;
+    const int64_t stride = (int64_t)NSCAN * 256;
+    for (int64_t r0 = (int64_t)(j - SAMPLES) * 256 + t; r0 < l.rows; r0 += 4 * stride) {
+      int neg[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t rr = r0 + q * stride;
+        if (rr < l.rows) {
+#pragma unroll 8
+          for (int64_t k = 0; k < a.K; ++k) {     // slots with no expert, or with an id the router cannot produce
+            const int64_t id = a.ids[rr * a.K + k];
+            neg[q] += id == -1 || bad_id(a, id);
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t rr = r0 + q * stride;
+        const bool none = rr < l.rows && neg[q] >= a.K, some = rr < l.rows && neg[q] > 0 && neg[q] < a.K;
+        nn += none;
+        ns += some;
+        if (none || some) last = rr + 1 > last ? rr + 1 : last;
+      }
+    }
+    nn = wave_sum_i32_dpp(nn);
+    ns = wave_sum_i32_dpp(ns);
+    last = wave_max_i64_dpp(last);
+    if (lane == 0) {
+      rnone[w] = nn;
+      rsome[w] = ns;
+      rlast[w] = last;
+    }
+    __syncthreads();
+    if (t == 0) {
+      const int tn = rnone[0] + rnone[1] + rnone[2] + rnone[3];
+      const int ts = rsome[0] + rsome[1] + rsome[2] + rsome[3];
+      int64_t lr = rlast[0];
+      for (int i = 1; i < 4; ++i) lr = rlast[i] > lr ? rlast[i] : lr;
+      if (tn > 0) atomicAdd(s + C_UNROUTED, (unsigned long long)tn);
+      if (ts > 0) atomicAdd(s + C_PARTIAL, (unsigned long long)ts);
+      if (lr > 0) atomicMax(s + C_BADROW, (unsigned long long)((l.step << 32) | lr));
+    }
+    return;
+  }
   const int64_t row = sample_row(l, j, a.nl);
   int nneg = 0;
+#pragma unroll 8
   for (int64_t k = 0; k < a.K; ++k) nneg += a.ids[row * a.K + k] == -1;
   const bool routed = nneg < a.K;                // a padding row (no experts) is neither judged nor counted
-  const bool known = ((a.stepbuf[0] >> 32) & 0x7FFFFFFFll) > 0;
   float best = 0.f;
   int64_t bcol = 0;
   int unj = 0;
@@ -328,6 +372,8 @@ __global__ __launch_bounds__(256) void moe_compare_kernel(MoeArgs a) {
   if (routed) {
     for (int64_t o = t; o < a.H; o += 256) {
       float r = 0.f, cmax = 0.f, sq = 0.f, mx = 0.f;
+      // (unrolled: the loads of eight experts' terms are in flight together)
+#pragma unroll 8
       for (int64_t k = 0; k < a.K; ++k) {
         const float* cr = a.C + ((int64_t)j * a.K + k) * 3 * a.H;
         const float cv = cr[o];
@@ -350,16 +396,13 @@ __global__ __launch_bounds__(256) void moe_compare_kernel(MoeArgs a) {
       }
     }
   }
-  // the row's worst (ties: the smallest column), the unjudged count
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const float oz = __shfl_xor(best, m, SDC_WAVE);
-    const int64_t oc = __shfl_xor(bcol, m, SDC_WAVE);
-    if (oz > best || (oz == best && oc < bcol)) {
-      best = oz;
-      bcol = oc;
-    }
-    unj += __shfl_xor(unj, m, SDC_WAVE);
+  // the row's worst (ties: the smallest column) as one key, z's bits (non-negative) above the column complemented;
+  // the unjudged count
+  {
+    const int64_t key = wave_max_i64_dpp((fb(best) << 32) | (int64_t)(0xFFFFFFFFu - (uint32_t)bcol));
+    best = __uint_as_float((uint32_t)((uint64_t)key >> 32));
+    bcol = (int64_t)(0xFFFFFFFFu - (uint32_t)(uint64_t)key);
+    unj = wave_sum_i32_dpp(unj);
   }
   if (lane == 0) {
     rz[w] = best;
@@ -367,7 +410,6 @@ __global__ __launch_bounds__(256) void moe_compare_kernel(MoeArgs a) {
     ru[w] = unj;
   }
   __syncthreads();
-  unsigned long long* s = reinterpret_cast<unsigned long long*>(a.state);
   if (t == 0) {
     for (int i = 1; i < 4; ++i)
       if (rz[i] > best || (rz[i] == best && rc[i] < bcol)) {
@@ -378,6 +420,7 @@ __global__ __launch_bounds__(256) void moe_compare_kernel(MoeArgs a) {
     if (best > 0.f) {
       const float y = ld<DT>(a.out, row * a.so + bcol);
       float r = 0.f;
+#pragma unroll 8
       for (int64_t k = 0; k < a.K; ++k) r += a.C[((int64_t)j * a.K + k) * 3 * a.H + bcol];
       const int64_t zb = fb(best) << 32;
       const int64_t cur = (int64_t)__atomic_load_n(s + C_ROW, __ATOMIC_RELAXED);
@@ -412,40 +455,6 @@ __global__ __launch_bounds__(256) void moe_compare_kernel(MoeArgs a) {
       a.capg[k] = gweight(a, row * a.K + k);
     }
   }
-  // the routing's validity: every known real row's expert ids
-  if (j == 0 && known) {
-    int nn = 0, ns = 0;
-    int64_t last = 0;
-    for (int64_t rr = t; rr < l.rows; rr += 256) {
-      int neg = 0;                               // slots with no expert, or with an id the router cannot produce
-      for (int64_t k = 0; k < a.K; ++k) {
-        const int64_t id = a.ids[rr * a.K + k];
-        neg += id == -1 || bad_id(a, id);
-      }
-      const bool none = neg >= a.K, some = neg > 0 && neg < a.K;
-      nn += none;
-      ns += some;
-      if (none || some) last = rr + 1 > last ? rr + 1 : last;
-    }
-    nn = wave_sum_i32(nn);
-    ns = wave_sum_i32(ns);
-    last = wave_max_i64(last);
-    if (lane == 0) {
-      rnone[w] = nn;
-      rsome[w] = ns;
-      rlast[w] = last;
-    }
-    __syncthreads();
-    if (t == 0) {
-      const int tn = rnone[0] + rnone[1] + rnone[2] + rnone[3];
-      const int ts = rsome[0] + rsome[1] + rsome[2] + rsome[3];
-      int64_t lr = rlast[0];
-      for (int i = 1; i < 4; ++i) lr = rlast[i] > lr ? rlast[i] : lr;
-      if (tn > 0) atomicAdd(s + C_UNROUTED, (unsigned long long)tn);
-      if (ts > 0) atomicAdd(s + C_PARTIAL, (unsigned long long)ts);
-      if (lr > 0) atomicMax(s + C_BADROW, (unsigned long long)((l.step << 32) | lr));
-    }
-  }
 }
 
 template <int DT>
@@ -468,7 +477,7 @@ int run(MoeArgs a, hipStream_t stream) {
   }
   {
     SdcProf prof("moe_compare", stream);
-    hipLaunchKernelGGL(moe_compare_kernel<DT>, dim3(SAMPLES), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(moe_compare_kernel<DT>, dim3(SAMPLES + NSCAN), dim3(256), 0, stream, a);
     SDC_LAUNCH_CHECK();
   }
   return SDC_OK;
