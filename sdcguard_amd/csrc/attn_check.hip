@@ -34,6 +34,7 @@ enum { CM_CLAIM, CM_ROW, CM_HEAD, CM_REQ, CM_POS, CM_SL, CM_LO, CM_STEP, CM_Z, C
 constexpr float TWO22 = 2.384185791015625e-07f;   // 2^-22
 constexpr float TWO21 = 4.76837158203125e-07f;    // 2^-21
 constexpr float NEG_INF = -__builtin_inff();
+constexpr int BTCAP = 256;                        // block-table entries a workgroup holds in LDS
 
 struct AttnArgs {
   const uint16_t* q; const uint16_t* o; const uint16_t* kv; const uint16_t* key; const uint16_t* val;
@@ -46,6 +47,7 @@ struct AttnArgs {
   int64_t slot, nl, idx, left, caprows, capw;
   float scale, g_qk, u, sig_o, hsig_p, line;
   int nsplit, has_write, keep_kv, nshift;     // nshift: log2(N) when N is a power of two, else -1
+  int nsamp;                                  // samples (workgroups past nsamp * nsplit check the KV writes)
 };
 
 struct Sample {
@@ -159,6 +161,10 @@ __device__ __forceinline__ int64_t key_of(float z, int64_t low) {
   return ((int64_t)(uint32_t)__float_as_uint(z) << 32) | (low & 0xFFFFFFFFll);
 }
 
+// A split record's value stored, and read back, at the device's coherence point (agent-scope atomics).
+__device__ __forceinline__ void publish(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ float coherent_load(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -175,7 +181,73 @@ struct Lds {
   int mk[4], mv[4], fk[4], fv[4];
   float py, pr;
   int last, claim, keep;
+  int bt[BTCAP];              // the block-table entries of the workgroup's keys, when they fit
 };
+
+// The sampled token's own KV write (serve_attn.py:533-569): the cache slot its K and V went to, against the slot
+// its position maps to, and their values against the step's keys and values.  Run by one workgroup of the sample
+// (the last split's), before its keys, so it overlaps the other splits' work.
+template <int DT, int DP>
+__device__ void check_write(const AttnArgs& a, const Sample& s, Lds<DP>& sh, int64_t* sb, int64_t step, int D,
+                            const int32_t* btr) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  if (a.has_write && s.i < a.SN) {
+    const int64_t si = a.slots[s.i];
+    if (si >= 0 && si < a.NB * a.N) {
+      const int64_t want = (int64_t)btr[s.pos / a.N] * a.N + s.pos % a.N;
+      const int64_t cblk = si / a.N, coff = si % a.N;
+      const int64_t total = a.Hkv * D;
+      int nbk = 0, nbv = 0, fk = 0x7FFFFFFF, fv = 0x7FFFFFFF;
+#pragma unroll 4
+      for (int64_t e = tid; e < total; e += 256) {       // (unrolled: several elements' loads in flight)
+        const int64_t hh = e / D, dd = e % D;
+        const uint16_t* cp = a.kv + cblk * a.skb + hh * a.skh + coff * a.skn;
+        const bool bk = cp[dd * a.skd] != a.key[s.i * a.skt + hh * a.skh2 + dd];
+        const bool bv = cp[(D + dd) * a.skd] != a.val[s.i * a.svt + hh * a.svh + dd];
+        nbk += bk;
+        nbv += bv;
+        if (bk && e < fk) fk = (int)e;
+        if (bv && e < fv) fv = (int)e;
+      }
+      nbk = wave_sum_i32_dpp(nbk);
+      nbv = wave_sum_i32_dpp(nbv);
+      fk = (int)(0x7FFFFFFFu - wave_max_u32_dpp(0x7FFFFFFFu - (uint32_t)fk));   // the first (smallest) element
+      fv = (int)(0x7FFFFFFFu - wave_max_u32_dpp(0x7FFFFFFFu - (uint32_t)fv));
+      if (lane == 0) {
+        sh.mk[w] = nbk;
+        sh.mv[w] = nbv;
+        sh.fk[w] = fk;
+        sh.fv[w] = fv;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        int tk = 0, tv = 0, FK = 0x7FFFFFFF, FV = 0x7FFFFFFF;
+        for (int ww = 0; ww < 4; ++ww) {
+          tk += sh.mk[ww];
+          tv += sh.mv[ww];
+          FK = min(FK, sh.fk[ww]);
+          FV = min(FV, sh.fv[ww]);
+        }
+        atomicAdd((unsigned long long*)(sb + C_WN), 1ull);
+        const bool badc = tk + tv > 0, bads = si != want;
+        if (badc || bads) {
+          const int64_t big = total;
+          const int64_t fk64 = FK == 0x7FFFFFFF ? big : FK, fv64 = FV == 0x7FFFFFFF ? big : FV;
+          const bool isv = fk64 >= big;
+          const int64_t first = isv ? fv64 : fk64;
+          int64_t wh = ((first / D) << 12) | ((first % D) << 1) | (isv ? 1 : 0);
+          const int64_t kind = (badc ? 1 : 0) | (bads ? 2 : 0);
+          wh = badc ? wh : 0;
+          if (badc) atomicAdd((unsigned long long*)(sb + C_WBAD), 1ull);
+          if (bads) atomicAdd((unsigned long long*)(sb + C_WSLOT), 1ull);
+          const int64_t s31 = (step & 0x7FFFFFFFll) << 32;
+          atomicMax((unsigned long long*)(sb + C_WLAST), (unsigned long long)(s31 | s.i));
+          atomicMax((unsigned long long*)(sb + C_WWHERE), (unsigned long long)(s31 | (kind << 28) | wh));
+        }
+      }
+    }
+  }
+}
 
 template <int DT, int DP, bool VEC>
 __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
@@ -185,11 +257,18 @@ __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
   constexpr int TOK = G * U;                // keys per wave per tile
   __shared__ Lds<DP> sh;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t sj = blockIdx.x / a.nsplit, c = blockIdx.x - sj * a.nsplit;
   const int64_t step = a.ctrl[0] & 0xFFFFFFFFll;
   const bool live = a.ctrl[1] != 0 && (step % a.nl) == a.idx;
   if (!live) return;
   int64_t* sb = a.state + a.slot * NCOLS;
+  if ((int64_t)blockIdx.x >= (int64_t)a.nsamp * a.nsplit) {
+    // a workgroup of its own per sample checks the sampled token's KV write, beside the splits' keys
+    const int64_t sw = (int64_t)blockIdx.x - (int64_t)a.nsamp * a.nsplit;
+    const Sample s = pick_sample(a, step, sw);
+    if (s.valid) check_write<DT, DP>(a, s, sh, sb, step, (int)a.D, a.bt + s.r * a.sbt);
+    return;
+  }
+  const int64_t sj = blockIdx.x / a.nsplit, c = blockIdx.x - sj * a.nsplit;
   if (blockIdx.x == 0 && tid == 0) atomicAdd((unsigned long long*)(sb + C_CALLS), 1ull);
   const Sample s = pick_sample(a, step, sj);
   if (!s.valid) {
@@ -206,12 +285,20 @@ __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
   const int cl = lane % LPT, g = lane / LPT, d0 = 8 * cl;
   const int32_t* btr = a.bt + s.r * a.sbt;
   const uint16_t* kvh = a.kv + hk * a.skh;
+  auto block_of = [&](int64_t t) { return a.nshift >= 0 ? (t >> a.nshift) : t / a.N; };
+  // the block-table entries of keys t0 .. t1 - 1 into LDS with one round trip (when they fit)
+  const int64_t b_first = t1 > t0 ? block_of(t0) : 0;
+  const int64_t nbt = t1 > t0 ? block_of(t1 - 1) - b_first + 1 : 0;
+  const bool bt_lds = nbt <= BTCAP;
+  if (bt_lds)
+    for (int64_t i = tid; i < nbt; i += 256) sh.bt[i] = btr[b_first + i];
 
   float q8[8], qa8[8];
   load8<DT, false>(a.q + s.i * a.sqt + s.hq * a.sqh, 1, d0, D, q8);
 #pragma unroll
   for (int e = 0; e < 8; ++e) qa8[e] = fabsf(q8[e]);
   const float sc = a.scale, gq = a.g_qk * a.scale;
+  __syncthreads();
 
   float m = NEG_INF, lsum = 0.f, le = 0.f;
   float acc[8], aa[8], ae[8], v1[8];
@@ -219,18 +306,17 @@ __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
   for (int e = 0; e < 8; ++e) acc[e] = aa[e] = ae[e] = v1[e] = 0.f;
   int bad = 0;
 
-  for (int64_t tb = t0 + (int64_t)w * TOK; tb < t1; tb += 4 * TOK) {
-    u32x4 kw[U], vw[U];
-    bool in[U];
+  // a tile: U keys of each lane group (G groups a wave): their K and V rows through the block table
+  auto fetch = [&](int64_t tb, u32x4* kw, u32x4* vw, bool* in) {
 #pragma unroll
     for (int uu = 0; uu < U; ++uu) {
       const int64_t t = tb + uu * G + g;
       in[uu] = t < t1;
       int64_t blk = 0, off = 0;
       if (in[uu]) {
-        const int64_t bi = a.nshift >= 0 ? (t >> a.nshift) : t / a.N;
+        const int64_t bi = block_of(t);
         off = t - bi * a.N;
-        blk = btr[bi];
+        blk = bt_lds ? sh.bt[bi - b_first] : btr[bi];
         const bool ok = blk >= 0 && blk < a.NB;
         bad |= !ok;
         blk = ok ? blk : 0;
@@ -239,6 +325,9 @@ __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
       kw[uu] = in[uu] ? raw8<DT, VEC>(p, a.skd, d0, D) : u32x4{0u, 0u, 0u, 0u};
       vw[uu] = in[uu] ? raw8<DT, VEC>(p + (int64_t)D * a.skd, a.skd, d0, D) : u32x4{0u, 0u, 0u, 0u};
     }
+  };
+  // the online softmax over a fetched tile
+  auto consume = [&](const u32x4* kw, const u32x4* vw, const bool* in) {
     float s_[U], sa_[U];
     float mt = NEG_INF;
 #pragma unroll
@@ -288,6 +377,23 @@ __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
         ae[e] = fmaf(pe, va, ae[e]);
         v1[e] += va;
       }
+    }
+  };
+  // two tiles' buffers: the next tile's loads are in flight while this one is consumed
+  {
+    u32x4 ka[U], va[U], kb[U], vb[U];
+    bool ia[U], ib[U];
+    int64_t tb = t0 + (int64_t)w * TOK;
+    const int64_t stride = 4 * TOK;
+    if (tb < t1) fetch(tb, ka, va, ia);
+    while (tb < t1) {
+      if (tb + stride < t1) fetch(tb + stride, kb, vb, ib);
+      consume(ka, va, ia);
+      tb += stride;
+      if (tb >= t1) break;
+      if (tb + stride < t1) fetch(tb + stride, ka, va, ia);
+      consume(kb, vb, ib);
+      tb += stride;
     }
   }
   // the lane groups of the wave into group 0
@@ -343,35 +449,40 @@ __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
     }
   }
   if (a.nsplit > 1) {
+    // Publish the record at the device's coherence point (agent-scope stores go past this XCD's L2), wait until
+    // every store of the workgroup has completed, then count the split in.  The last split to count reads the
+    // records back from the coherence point.  No L2 write-back or invalidation is needed: nothing here goes
+    // through the non-coherent L2 lines another XCD may hold.
     const int64_t PW = 4 + 4 * (int64_t)DP;
     float* rec = a.ws + (sj * a.nsplit + c) * PW;
     if (d < DP) {
-      rec[4 + d] = RA;
-      rec[4 + DP + d] = RAA;
-      rec[4 + 2 * DP + d] = RAE;
-      rec[4 + 3 * DP + d] = RV;
+      publish(rec + 4 + d, RA);
+      publish(rec + 4 + DP + d, RAA);
+      publish(rec + 4 + 2 * DP + d, RAE);
+      publish(rec + 4 + 3 * DP + d, RV);
     }
     if (tid == 0) {
-      rec[0] = M;
-      rec[1] = L;
-      rec[2] = LE;
-      rec[3] = (float)BAD;
+      publish(rec, M);
+      publish(rec + 1, L);
+      publish(rec + 2, LE);
+      publish(rec + 3, (float)BAD);
     }
-    __threadfence();
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
-      const int prev = atomicAdd(a.cnt + sj, 1);
+      const int prev = __hip_atomic_fetch_add(a.cnt + sj, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       sh.last = prev == a.nsplit - 1;
-      if (sh.last) a.cnt[sj] = 0;           // ready for the next call
+      if (sh.last) __hip_atomic_store(a.cnt + sj, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next call
     }
     __syncthreads();
     if (!sh.last) return;
-    __threadfence();
     const float* base = a.ws + sj * a.nsplit * PW;
     M = NEG_INF;
+#pragma unroll 8
     for (int cc = 0; cc < a.nsplit; ++cc) M = fmaxf(M, coherent_load(base + cc * PW));
     L = LE = RA = RAA = RAE = RV = 0.f;
     BAD = 0;
+#pragma unroll 4
     for (int cc = 0; cc < a.nsplit; ++cc) {
       const float* r = base + cc * PW;
       const float mc = coherent_load(r);
@@ -496,64 +607,6 @@ __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
       }
     }
   }
-  // ---- the sampled token's own KV write (serve_attn.py:533-569)
-  if (a.has_write && s.i < a.SN) {
-    const int64_t si = a.slots[s.i];
-    if (si >= 0 && si < a.NB * a.N) {
-      const int64_t want = (int64_t)btr[s.pos / a.N] * a.N + s.pos % a.N;
-      const int64_t cblk = si / a.N, coff = si % a.N;
-      const int64_t total = a.Hkv * D;
-      int nbk = 0, nbv = 0, fk = 0x7FFFFFFF, fv = 0x7FFFFFFF;
-      for (int64_t e = tid; e < total; e += 256) {
-        const int64_t hh = e / D, dd = e % D;
-        const uint16_t* cp = a.kv + cblk * a.skb + hh * a.skh + coff * a.skn;
-        const bool bk = cp[dd * a.skd] != a.key[s.i * a.skt + hh * a.skh2 + dd];
-        const bool bv = cp[(D + dd) * a.skd] != a.val[s.i * a.svt + hh * a.svh + dd];
-        nbk += bk;
-        nbv += bv;
-        if (bk && e < fk) fk = (int)e;
-        if (bv && e < fv) fv = (int)e;
-      }
-      nbk = wave_sum_i32(nbk);
-      nbv = wave_sum_i32(nbv);
-      for (int off = 32; off > 0; off >>= 1) {
-        fk = min(fk, __shfl_xor(fk, off, 64));
-        fv = min(fv, __shfl_xor(fv, off, 64));
-      }
-      if (lane == 0) {
-        sh.mk[w] = nbk;
-        sh.mv[w] = nbv;
-        sh.fk[w] = fk;
-        sh.fv[w] = fv;
-      }
-      __syncthreads();
-      if (tid == 0) {
-        int tk = 0, tv = 0, FK = 0x7FFFFFFF, FV = 0x7FFFFFFF;
-        for (int ww = 0; ww < 4; ++ww) {
-          tk += sh.mk[ww];
-          tv += sh.mv[ww];
-          FK = min(FK, sh.fk[ww]);
-          FV = min(FV, sh.fv[ww]);
-        }
-        atomicAdd((unsigned long long*)(sb + C_WN), 1ull);
-        const bool badc = tk + tv > 0, bads = si != want;
-        if (badc || bads) {
-          const int64_t big = total;
-          const int64_t fk64 = FK == 0x7FFFFFFF ? big : FK, fv64 = FV == 0x7FFFFFFF ? big : FV;
-          const bool isv = fk64 >= big;
-          const int64_t first = isv ? fv64 : fk64;
-          int64_t wh = ((first / D) << 12) | ((first % D) << 1) | (isv ? 1 : 0);
-          const int64_t kind = (badc ? 1 : 0) | (bads ? 2 : 0);
-          wh = badc ? wh : 0;
-          if (badc) atomicAdd((unsigned long long*)(sb + C_WBAD), 1ull);
-          if (bads) atomicAdd((unsigned long long*)(sb + C_WSLOT), 1ull);
-          const int64_t s31 = (step & 0x7FFFFFFFll) << 32;
-          atomicMax((unsigned long long*)(sb + C_WLAST), (unsigned long long)(s31 | s.i));
-          atomicMax((unsigned long long*)(sb + C_WWHERE), (unsigned long long)(s31 | (kind << 28) | wh));
-        }
-      }
-    }
-  }
 }
 
 template <int DT, int DP>
@@ -581,12 +634,12 @@ int64_t pad_dim(int64_t D) { return D <= 64 ? 64 : D <= 128 ? 128 : 256; }
 constexpr int64_t MAX_SAMPLES = 1024;
 constexpr int64_t COUNTER_BYTES = MAX_SAMPLES * (int64_t)sizeof(int32_t);
 
-// Workgroups per sample: enough that a long context spreads over the chip (about 256 keys each), at most 64, and
-// at most 1024 workgroups in all.
+// Workgroups per sample: enough that a long context spreads over the chip (about 128 keys each: two tiles a wave),
+// at most 64, and at most 1024 workgroups in all.
 extern "C" int64_t sdc_attn_splits(int64_t samples, int64_t max_keys) {
   if (samples <= 0 || max_keys <= 0) return 1;
   const int64_t cap = std::max<int64_t>(1, 1024 / samples);
-  const int64_t s = std::min<int64_t>(sdc_cdiv(max_keys, 256), cap);
+  const int64_t s = std::min<int64_t>(sdc_cdiv(max_keys, 128), cap);
   return std::max<int64_t>(1, std::min<int64_t>(s, 64));
 }
 
@@ -653,7 +706,8 @@ static int attn_check_impl(SDC_ATTN_PARAMS, void* workspace, int64_t workspace_b
   a.nshift = (N & (N - 1)) == 0 ? __builtin_ctzll((unsigned long long)N) : -1;
   const int vec = skd == 1 && D % 8 == 0 && skb % 8 == 0 && skh % 8 == 0 && skn % 8 == 0 &&
                   ((uintptr_t)kv % 16) == 0;
-  const unsigned grid = (unsigned)(samples * nsplit);
+  a.nsamp = samples;
+  const unsigned grid = (unsigned)(samples * nsplit + (has_write ? samples : 0));
   SdcProf prof("attn_check", stream);
   if (dtype == SDC_BF16)
     launch_dt<SDC_BF16>(a, (int)dp, vec, grid, stream);
