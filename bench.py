@@ -308,7 +308,7 @@ def bench_bf16_mlp(ctx: Ctx) -> dict:
     amounts = {"xstage": ("hbm", xb, None), "row_gemm": ("hbm", wb, None),
                "col_gemm": ("mfma", 2.0 * M * K * 6 * nb, "bf16"), "ypass": ("hbm", yb, None)}
     patterns = {"xstage": r"xstage_kernel", "ypass": r"ypass_kernel",
-                "row_gemm": r"rs_gemm_kernel<0, 4, 1>", "col_gemm": r"rs_gemm_kernel<0, 4, 0>"}
+                "row_gemm": r"rs_gemm(_tall)?_kernel<0, (4, )?1>", "col_gemm": r"rs_gemm(_tall)?_kernel<0, (4, )?0>"}
     ent, roof = _roof(km, amounts, name, patterns, a.steps)
     ent["xfinish"] = {"avg_us": round(km["xfinish"][0] * 1e3, 2), "launches_per_step": km["xfinish"][1] / a.steps,
                       "bound": "latency"}

@@ -741,6 +741,219 @@ __global__ __launch_bounds__(64 * RS_WAVES, 1) void rs_gemm_kernel(GemmArgs g) {
   }
 }
 
+// ------------------------------------------------------------------------- register-streamed GEMM, tall tiles
+// The same loop with 128 rows of A per wave: each B fragment loaded from L2 meets twice the rows, so a workgroup
+// moves 36% fewer bytes through the vector memory path per MFMA (1.25 MB instead of 2 MB for the same 64 x 64 x
+// 4096 worth of products).  The workgroup tile is 128 x 64 over half the depth; the two halves are separate
+// workgroups, each writing its own plane of E (plane h = depth half h), which the scoring pass adds in half order.
+// A's ring per wave is two 16 KB segments (128 rows x 128 bytes; 128 KB for the 4 waves), the next segment loading
+// while the current one is read.  Per step a wave issues 4 of the next segment's 16 A instructions, then the B
+// fragments RB steps ahead.  So at a step's wait, the loads issued after B(st) are (RB - 1) (4 + 6) and, at the
+// first step of a segment, those after the segment's last A piece are the 6 B loads of one step: the wait is
+// vmcnt(30) inside a segment and vmcnt(6) at its first step.
+// XCD order: XCDs 0-3 take depth half 0 and 4-7 half 1 (each XCD's L2 holds its half of B), row tiles in order.
+#ifndef SDC_TALL_TRF
+#define SDC_TALL_TRF 4
+#endif
+
+template <int DT, int ROLE, int TRF>
+__global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_kernel(GemmArgs g) {
+  constexpr int TCF = 2, TR = 32 * TRF, TC = 64, NG = TRF * TCF * 4, RB = 4, NAI = TR / 8, APS = NAI / 4;
+  constexpr int RT_SEGB = TR * 128;             // bytes of A per wave and segment (TR rows x 128 bytes)
+  __shared__ __attribute__((aligned(16))) uint8_t smem[RS_WAVES * 2 * RT_SEGB];
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int r = lane & 31, h = lane >> 5;
+  const int64_t N = g.N, m = g.m;
+  const int64_t nct = sdc_cdiv(N, TC), ncf = sdc_cdiv(N, 32);
+  const int64_t tiles = sdc_cdiv(m, TR) * nct;
+  const int64_t G = (int64_t)gridDim.x, b = blockIdx.x;
+  const int64_t wid = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+  const int64_t half = wid / tiles, tile = wid % tiles;
+  const int64_t ct = tile % nct, rt = tile / nct;
+  const int64_t r0 = rt * TR, c0 = ct * TC;
+  const int per = (int)(g.k / 64) / (RS_WAVES * (int)g.splits);   // segments per wave
+  const int seg0 = (int)half * per * RS_WAVES + w * per;
+  uint8_t* const abuf = smem + w * 2 * RT_SEGB;
+  int ard[TRF][4];
+#pragma unroll
+  for (int i = 0; i < TRF; ++i)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int R = 32 * i + r, rr = R & 7;
+      ard[i][jj] = (R >> 3) * 1024 + 16 * (8 * rr + ((4 * h + jj) ^ rr));
+    }
+  const uint16_t* bq = (const uint16_t*)g.B + (int64_t)(4 * seg0) * 3 * ncf * 512 + 8 * lane;
+  int bf[TCF];
+#pragma unroll
+  for (int n = 0; n < TCF; ++n) {
+    const int64_t f = c0 / 32 + n;
+    bf[n] = (int)((f < ncf ? f : ncf - 1) * 512);
+  }
+  const int64_t bstep = 3 * ncf * 512;
+  const int lastseg = per - 1;
+  const int last = 4 * per - 1;
+  // A's instruction I (0 .. 15) of a segment, lane L: row 8 I + L / 8 (clamped to m - 1), piece (L % 8) ^ (L / 8);
+  // rows as 32-bit element offsets from the tile's first row
+  const uint8_t* abase = (const uint8_t*)g.A + (64 * (int64_t)seg0) * 2 + 16 * ((lane & 7) ^ (lane >> 3));
+  int64_t arow[NAI];
+#pragma unroll
+  for (int I = 0; I < NAI; ++I) {
+    const int64_t row = r0 + 8 * I + (lane >> 3);
+    arow[I] = (row < m ? row : m - 1) * g.sam * 2;
+  }
+  u32x4 rb[RB][3][TCF];
+  auto issue_a4 = [&](int sg, int I0) {
+    const int s2 = sg < lastseg ? sg : lastseg;
+    uint8_t* dst = abuf + (sg & 1) * RT_SEGB;
+#pragma unroll
+    for (int I = I0; I < I0 + APS; ++I)
+      sdc_pipe::lds_load16(abase + arow[I] + 128 * (int64_t)s2, (uint16_t*)(dst + 1024 * I));
+  };
+  auto issue_b = [&](int slot, int st) {
+    const uint16_t* q = bq + (int64_t)(st < last ? st : last) * bstep;
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+      for (int n = 0; n < TCF; ++n)
+        asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(rb[slot][p][n]) : "v"(q + p * ncf * 512 + bf[n]));
+  };
+  // part p of B(st) into slot `slot`
+  auto issue_bp = [&](int slot, int st, int p) {
+    const uint16_t* q = bq + (int64_t)(st < last ? st : last) * bstep + p * ncf * 512;
+#pragma unroll
+    for (int n = 0; n < TCF; ++n)
+      asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(rb[slot][p][n]) : "v"(q + bf[n]));
+  };
+  const uint32_t lds0 = (uint32_t)(uintptr_t)abuf;
+  f32x16 acc[TRF][TCF];
+#pragma unroll
+  for (int i = 0; i < TRF; ++i)
+#pragma unroll
+    for (int n = 0; n < TCF; ++n)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][n][e] = 0.f;
+#pragma unroll
+  for (int q = 0; q < RB; ++q)
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+      for (int n = 0; n < TCF; ++n) rb[q][p][n] = u32x4{0u, 0u, 0u, 0u};
+  if (per > 0) {
+    // prologue: the four steps before the first would issue segment 0's A (a quarter each) and B(0 .. 3)
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      issue_a4(0, APS * q);
+      issue_b(q, q);
+    }
+    // Each step's 24 MFMAs go in three groups (one part each); the loads are issued between the groups: after the
+    // first, the next segment's A pieces and this slot's B fragments of part 0 for RB steps ahead (the MFMAs that
+    // read them are issued), then part 1's, then part 2's.  The next step's A fragments are read from LDS in the
+    // middle of the second group (inside a segment; the first step of a segment reads its own after the wait).
+    u32x4 fr[2][TRF];
+    for (int sg = 0; sg < per; ++sg) {
+      const uint32_t L = lds0 + (uint32_t)((sg & 1) * RT_SEGB);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        static_assert(RB == 4, "the wait counts below assume B four steps ahead");
+        const int st = 4 * sg + jj, cur = jj & 1;
+        if (jj == 0) {
+          asm volatile("s_waitcnt vmcnt(6)"
+                       : "+v"(rb[0][0][0]), "+v"(rb[0][0][1]), "+v"(rb[0][1][0]), "+v"(rb[0][1][1]),
+                         "+v"(rb[0][2][0]), "+v"(rb[0][2][1]));
+#pragma unroll
+          for (int i = 0; i < TRF; ++i)
+            asm volatile("ds_read_b128 %0, %1" : "=v"(fr[0][i]) : "v"(L + (uint32_t)ard[i][0]));
+        } else {
+          asm volatile("s_waitcnt vmcnt(%6)"
+                       : "+v"(rb[jj][0][0]), "+v"(rb[jj][0][1]), "+v"(rb[jj][1][0]), "+v"(rb[jj][1][1]),
+                         "+v"(rb[jj][2][0]), "+v"(rb[jj][2][1])
+                       : "n"((RB - 1) * (APS + 6)));
+        }
+        if constexpr (TRF == 4)
+          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fr[cur][0]), "+v"(fr[cur][1]), "+v"(fr[cur][2]), "+v"(fr[cur][3]));
+        else
+          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fr[cur][0]), "+v"(fr[cur][1]));
+#pragma unroll
+        for (int i = 0; i < TRF; ++i)
+#pragma unroll
+          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<DT>(fr[cur][i], rb[jj][0][n], acc[i][n]);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_a4(sg + 1, APS * jj);
+        issue_bp(jj, st + RB, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < TRF / 2; ++i)
+#pragma unroll
+          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<DT>(fr[cur][i], rb[jj][1][n], acc[i][n]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (jj < 3) {
+#pragma unroll
+          for (int i = 0; i < TRF; ++i)
+            asm volatile("ds_read_b128 %0, %1" : "=v"(fr[cur ^ 1][i]) : "v"(L + (uint32_t)ard[i][jj + 1]));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = TRF / 2; i < TRF; ++i)
+#pragma unroll
+          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<DT>(fr[cur][i], rb[jj][1][n], acc[i][n]);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_bp(jj, st + RB, 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < TRF; ++i)
+#pragma unroll
+          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<DT>(fr[cur][i], rb[jj][2][n], acc[i][n]);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_bp(jj, st + RB, 2);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(rb[0][0][0]), "+v"(rb[0][0][1]), "+v"(rb[0][1][0]), "+v"(rb[0][1][1]), "+v"(rb[0][2][0]),
+                   "+v"(rb[0][2][1]));
+#pragma unroll
+    for (int q = 1; q < RB; ++q)
+      asm volatile("" : "+v"(rb[q][0][0]), "+v"(rb[q][0][1]), "+v"(rb[q][1][0]), "+v"(rb[q][1][1]), "+v"(rb[q][2][0]),
+                   "+v"(rb[q][2][1]));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __syncthreads();
+  f32x4* red = reinterpret_cast<f32x4*>(smem);                  // [RS_WAVES][NG][64]: 128 KB
+  static_assert(RS_WAVES * NG * 64 * 16 <= (int)sizeof(smem), "the reduction fits the ring");
+#pragma unroll
+  for (int i = 0; i < TRF; ++i)
+#pragma unroll
+    for (int n = 0; n < TCF; ++n)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        red[(w * NG + (i * TCF + n) * 4 + r4) * 64 + lane] =
+            f32x4{acc[i][n][4 * r4], acc[i][n][4 * r4 + 1], acc[i][n][4 * r4 + 2], acc[i][n][4 * r4 + 3]};
+  __syncthreads();
+  const int64_t me = g.m;
+  float* const Eh = g.E + half * N * me;
+#pragma unroll
+  for (int gq = 0; gq < NG / RS_WAVES; ++gq) {
+    const int gi = w * (NG / RS_WAVES) + gq;
+    f32x4 v = red[gi * 64 + lane];
+#pragma unroll
+    for (int q = 1; q < RS_WAVES; ++q) v += red[(q * NG + gi) * 64 + lane];
+    const int i = gi / (4 * TCF), n = (gi / 4) % TCF, r4 = gi % 4;
+    const int64_t row = r0 + 32 * i + 8 * r4 + 4 * h;
+    const int64_t col = c0 + 32 * n + r;
+    if (col < N) {
+      float* Ec = Eh + col * me;
+      if (row + 4 <= m && (me % 4) == 0) {
+        *reinterpret_cast<f32x4*>(Ec + row) = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (row + e < m) Ec[row + e] = v[e];
+      }
+    }
+  }
+}
+
 // Parts [3][N][kp] (k-contiguous per column, column stride spc) -> fragment order for rs_gemm_kernel: element e of
 // lane l of fragment (step s, part p, column fragment f) is part p, column 32 f + l % 32 (zero past N), depth
 // 64 (s / 4) + 32 (l / 32) + 8 (s % 4) + e.  One thread per 16-byte piece.
@@ -780,6 +993,29 @@ int sdc_rs_gemm_launch(int dtype, GemmArgs g, int role, hipStream_t stream) {
   } else {
     if (dtype == SDC_BF16) hipLaunchKernelGGL((rs_gemm_kernel<SDC_BF16, RS_RB, 0>), grid, block, 0, stream, g);
     else hipLaunchKernelGGL((rs_gemm_kernel<SDC_FP16, RS_RB, 0>), grid, block, 0, stream, g);
+  }
+  SDC_LAUNCH_CHECK();
+  return SDC_OK;
+}
+
+// The tall-tile variant: 128 x 64 tiles over depth halves, two planes of E (g.splits must be 2, the depth a
+// multiple of 512).  Returns SDC_EUNSUPPORTED where it does not apply.
+int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream) {
+  if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EUNSUPPORTED;
+  if (g.splits != 2 || g.sak != 1 || g.k % (2 * RS_KMULT) || g.sam % 8 || ((uintptr_t)g.A | (uintptr_t)g.B) % 16 ||
+      !g.et || g.goffs)
+    return SDC_EUNSUPPORTED;
+  if (g.m < 1 || g.N < 1) return SDC_EINVAL;
+  const int64_t blocks = 2 * sdc_cdiv(g.m, 32 * SDC_TALL_TRF) * sdc_cdiv(g.N, 64);
+  if (blocks > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
+  SdcProf prof(g.prof_name ? g.prof_name : "expected_gemm", stream);
+  const dim3 grid((unsigned)blocks), block(64 * RS_WAVES);
+  if (role == 1) {
+    if (dtype == SDC_BF16) hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 1, SDC_TALL_TRF>), grid, block, 0, stream, g);
+    else hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_FP16, 1, SDC_TALL_TRF>), grid, block, 0, stream, g);
+  } else {
+    if (dtype == SDC_BF16) hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 0, SDC_TALL_TRF>), grid, block, 0, stream, g);
+    else hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_FP16, 0, SDC_TALL_TRF>), grid, block, 0, stream, g);
   }
   SDC_LAUNCH_CHECK();
   return SDC_OK;

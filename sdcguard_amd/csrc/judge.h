@@ -114,3 +114,77 @@ __device__ __forceinline__ float judge_one(float expected, float actual, float n
   return z;
 }
 
+
+// The same two scores where every input is finite and the pair is not "impossible" (the common case): ok tells
+// whether that held; where it did, the result is judge_serve's (the same expressions, without its non-finite
+// selects), else the caller takes judge_serve.
+template <class A>
+__device__ __forceinline__ PairScore judge_serve_clean(float plain, float sgn, float sq, float l1, float xn,
+                                                       float asum, float e0, float e1, float sc0, float sc1,
+                                                       float bs0, float bs1, float bmaxv, float bmbv, float b2n0,
+                                                       float b2n1, float b2m0, float b2m1, float wf, const A& a,
+                                                       bool& ok) {
+  const float inf = __builtin_inff();
+  const float exp0 = e0 * sc0 + bs0;
+  const float exp1 = e1 * sc1 + bs1;
+  const float bound = asum * bmaxv + bmbv;
+  const float rsq = fsqrt(sq);
+  const float noise = rsq * a.u;
+  float fl0 = xn * b2n0 * 1e-5f;
+  float fl1 = xn * b2n1 * 1e-5f;
+  const float hl0 = asum * b2m0 * a.l1c;
+  const float hl1 = asum * b2m1 * a.l1c;
+  fl0 = fminf(fabsf(fl0) < inf ? fl0 : inf, fabsf(hl0) < inf ? hl0 : inf);
+  fl1 = fminf(fabsf(fl1) < inf ? fl1 : inf, fabsf(hl1) < inf ? hl1 : inf);
+  const float bigfl = bound * (float)(1e-5 * 128.0);
+  fl0 = fl0 < inf ? fl0 : bigfl;
+  fl1 = fl1 < inf ? fl1 : bigfl;
+  const float swf = fsqrt(wf);
+  const float tail = a.abs_floor + swf * a.h;
+  const float den0 = (noise + fl0) + tail;
+  const float den1 = (noise + fl1) + tail;
+  const float d0 = fabsf(exp0 - plain);
+  const float d1 = fabsf(exp1 - sgn);
+  float z0 = fdiv(d0, den0);
+  const float z1 = fdiv(d1, den1);
+  const float worst = (l1 * (1.25f * a.u) + (1.25f * a.h * wf)) + fl0 + a.abs_floor;
+  const float zw = fdiv(d0, worst) * a.zt;
+  const float lim = bound * 1.01f;
+  const float cap = bound * a.capk + 2.0f * a.h;
+  // d finite <=> expected and actual finite; noise finite; no NaN score; not "impossible"
+  ok = (d0 < inf) && (d1 < inf) && (noise < inf) && (z0 == z0) && (zw == zw) && (z1 == z1) &&
+       !((lim < a.lim_big) && (rsq > cap * swf));
+  z0 = fminf(z0, zw);
+  PairScore r;
+  r.z0 = z0;
+  r.z1 = z1;
+  r.sec = z1 > z0;
+  r.zc = r.sec ? z1 : z0;
+  r.dc = r.sec ? den1 : den0;
+  r.unk = 0;
+  return r;
+}
+
+// judge_one where the checksum's inputs are finite and it is not "impossible": ok tells whether that held; where it
+// did, the score is judge_one's.
+template <class A>
+__device__ __forceinline__ float judge_one_clean(float expected, float actual, float noise, float cn, float fl,
+                                                 float bound, float wf, float l1, bool plain, const A& a, float& den,
+                                                 bool& ok) {
+  const float inf = __builtin_inff();
+  const float swf = fsqrt(wf);
+  den = (noise + fl) + (a.abs_floor + swf * a.h);
+  const float diff = fabsf(expected - actual);
+  float z = fdiv(diff, den);
+  bool fin = z == z;
+  if (plain) {
+    const float worst = ((l1 * (1.25f * a.u) + 1.25f * wf * a.h) + fl) + a.abs_floor;
+    const float zw = fdiv(diff, worst) * a.zt;
+    fin = fin && (zw == zw);
+    z = fminf(z, zw);
+  }
+  const float lim = bound * 1.01f;
+  const float cap = bound * a.capk + 2.f * a.h;
+  ok = (diff < inf) && (noise < inf) && fin && !((lim < 1e18f) && (cn > cap * swf));
+  return z;
+}

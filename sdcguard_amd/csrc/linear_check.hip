@@ -33,6 +33,7 @@
 extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
 int sdc_gemm_launch(int dtype, GemmArgs g, int64_t batches, hipStream_t stream);
 int sdc_rs_gemm_launch(int dtype, GemmArgs g, int role, hipStream_t stream);
+int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream);
 extern "C" int64_t sdc_parts_fragments_bytes(int64_t N, int64_t k);
 extern "C" int sdc_parts_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out, hipStream_t stream);
 
@@ -43,6 +44,10 @@ constexpr int RS_K = 256;          // depth multiple of the register-streamed GE
 constexpr int XK = 128;            // depth per xstage workgroup
 constexpr int NXS = 5;             // partial stats per (depth chunk, row block): sq0, sq1, max0, max1, max|x|
 constexpr int RST = 8;             // final stats per row block: the NXS above, then the sum of its sign pattern
+#ifndef SDC_YTPW
+#define SDC_YTPW 1
+#endif
+constexpr int YTPW = SDC_YTPW;     // column blocks per y-pass workgroup
 
 __device__ __forceinline__ float nan_abs(float v) { return v == v ? fabsf(v) : __builtin_inff(); }
 
@@ -353,13 +358,16 @@ __device__ __forceinline__ uint32_t pack_signs(float s0, float s1) {
 }
 
 
-// The tile of one workgroup: 128 rows (one row block) x 128 columns (one column block).  Thread t = 16 rg + cg owns
-// rows 8 rg .. 8 rg + 7 and columns 8 cg .. 8 cg + 7 (each load instruction of a wave reads 4 rows x 256
-// contiguous bytes).  Waves 0 and 1 score the tile's 128 column-block pairs (one row each), waves 2 and 3 its 128
-// row-block pairs (one column each); what that scoring needs is loaded at the start, so its latency passes under
-// the arithmetic.
-// ONE: both checks' E come as one plane each (the register-streamed GEMMs), else up to SDC_MAX_SPLITS planes to add
-template <int DT, bool ONE>
+// A workgroup takes TPW tiles of one row block: 128 rows x 128 columns each (one column block), column blocks
+// TPW bx .. TPW bx + TPW - 1.  Every tile's loads (y and what its scoring reads) are issued first, so the later
+// tiles' reads stream in while the first tile is summed and scored.  Per tile, thread t = 16 rg + cg owns rows
+// 8 rg .. 8 rg + 7 and columns 8 cg .. 8 cg + 7 (each load instruction of a wave reads 4 rows x 256 contiguous
+// bytes).  Waves 0 and 1 score the tile's 128 column-block pairs (one row each), waves 2 and 3 its 128 row-block
+// pairs (one column each).  Each wave keeps its worst keys over the tiles; one atomic maximum per check and
+// workgroup at the end.
+// NS: the most planes of E either check has (1 or 2: the register-streamed GEMMs; else up to SDC_MAX_SPLITS), added
+// in plane order
+template <int DT, int NS, int TPW>
 __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
   __shared__ f32x4 colw[4][2][64];              // each wave's column sums [wave][column parity][lane]
   __shared__ f32x4 rows[BS];                    // the tile's row sums
@@ -367,212 +375,231 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
   __shared__ int red_u[4];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int rg = t >> 4, cg = t & 15;
-  const int jb = blockIdx.x, ib = blockIdx.y;
-  const int r0 = ib * BS, c0 = jb * BS;
-  const int wr = (int)((ib == a.mb - 1 && a.rem_m > 0) ? a.rem_m : BS);     // rows in this tile
-  const int wc = (int)((jb == a.nb - 1 && a.rem_n > 0) ? a.rem_n : BS);     // columns in this tile
+  const int ib = blockIdx.y, jb0 = blockIdx.x * TPW;
+  const int r0 = ib * BS;
+  const int wr = (int)((ib == a.mb - 1 && a.rem_m > 0) ? a.rem_m : BS);     // rows in this row block
   const int m = (int)a.m, n = (int)a.n;
-
-  // ---- loads: y (eight 16-byte pieces, unconditional on a full tile), then what this lane's scoring needs
-  u32x4 v[8];
-  if (wr == BS && wc == BS) {
-    const uint16_t* p0 = a.y + (int64_t)(r0 + 8 * rg) * a.sym + c0 + 8 * cg;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p0 + i * a.sym));
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = 8 * rg + i;
-      v[i] = (r < wr && 8 * cg < wc)
-          ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.y + (int64_t)(r0 + r) * a.sym + c0 + 8 * cg))
-          : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-  // waves 0, 1: column-block pair of row R; waves 2, 3: row-block pair of column J
   const bool colside = w < 2;
-  const int R = r0 + 64 * w + lane, J = c0 + 64 * (w - 2) + lane;
-  const float* ebase;
-  const float* nbase;
-  int64_t estride, pstride, nstride, splits;
-  if (colside) {
-    const int Rc = R < m ? R : m - 1;
-    ebase = a.Ecol + (int64_t)(2 * jb) * a.m + Rc; estride = a.m; pstride = 2 * a.nb * a.m;
-    nbase = a.xn + Rc; nstride = a.m; splits = a.scol;
-  } else {
-    const int Jc = J < n ? J : n - 1;
-    ebase = a.Erow + (int64_t)(2 * ib) * a.n + Jc; estride = a.n; pstride = 2 * a.mb * a.n;
-    nbase = a.wn + Jc; nstride = a.n; splits = a.srow;
+  const int R = r0 + 64 * w + lane;                                          // (column side) this lane's row
+  constexpr uint32_t ONES = DT == SDC_BF16 ? 0x3F803F80u : 0x3C003C00u;
+
+  // ---- what every tile shares: the row block's pattern (this thread's 8 rows), statistics, the rows' norms
+  uint32_t srow2[4];
+  {
+    const float* spr = a.sign_table + (wr - 1) * 128;
+    const f32x4 ra = *reinterpret_cast<const f32x4*>(spr + 8 * rg);
+    const f32x4 rb = *reinterpret_cast<const f32x4*>(spr + 8 * rg + 4);
+    srow2[0] = pack_signs<DT>(ra.x, ra.y); srow2[1] = pack_signs<DT>(ra.z, ra.w);
+    srow2[2] = pack_signs<DT>(rb.x, rb.y); srow2[3] = pack_signs<DT>(rb.z, rb.w);
   }
-  constexpr int NSPL = ONE ? 1 : SDC_MAX_SPLITS;
-  float ev[NSPL][2];
-#pragma unroll
-  for (int s = 0; s < NSPL; ++s) {
-    const int64_t sc = s < splits ? s : 0;
-    ev[s][0] = ebase[sc * pstride];
-    ev[s][1] = ebase[sc * pstride + estride];
-  }
-  const float asq = nbase[0], asum = nbase[nstride];
-  const float bj = (!colside && a.bias) ? half_to_f32<DT>(a.bias[J < n ? J : n - 1]) : 0.f;
-  // the row block's statistics (complete: xstage's last chunk added them up) and the sum of its pattern
   const f32x4 rst0 = *reinterpret_cast<const f32x4*>(a.rstat + (int64_t)ib * RST);
   const f32x4 rst1 = *reinterpret_cast<const f32x4*>(a.rstat + (int64_t)ib * RST + 4);
   const float rstat[NXS] = {rst0.x, rst0.y, rst0.z, rst0.w, rst1.x};
   const float rsign = rst1.y;
+  const int Rc = R < m ? R : m - 1;
+  const float xsq = colside ? a.xn[Rc] : 0.f, xsum = colside ? a.xn[a.m + Rc] : 0.f;
 
-  // ---- signs: this thread's 8 columns of the column block's pattern, its 8 rows of the row block's pattern
-  const float* spc = a.sign_table + (wc - 1) * 128;
-  const float* spr = a.sign_table + (wr - 1) * 128;
-  uint32_t scol2[4], srow2[4];
-  {
-    const f32x4 ca = *reinterpret_cast<const f32x4*>(spc + 8 * cg);
-    const f32x4 cb = *reinterpret_cast<const f32x4*>(spc + 8 * cg + 4);
-    const f32x4 ra = *reinterpret_cast<const f32x4*>(spr + 8 * rg);
-    const f32x4 rb = *reinterpret_cast<const f32x4*>(spr + 8 * rg + 4);
-    scol2[0] = pack_signs<DT>(ca.x, ca.y); scol2[1] = pack_signs<DT>(ca.z, ca.w);
-    scol2[2] = pack_signs<DT>(cb.x, cb.y); scol2[3] = pack_signs<DT>(cb.z, cb.w);
-    srow2[0] = pack_signs<DT>(ra.x, ra.y); srow2[1] = pack_signs<DT>(ra.z, ra.w);
-    srow2[2] = pack_signs<DT>(rb.x, rb.y); srow2[3] = pack_signs<DT>(rb.z, rb.w);
-  }
-  constexpr uint32_t ONES = DT == SDC_BF16 ? 0x3F803F80u : 0x3C003C00u;
-
-  // ---- row direction: four sums of each of the eight rows over this thread's eight columns
-  float rs[8][4];
+  // ---- every tile's loads: y (eight 16-byte pieces, unconditional on a full tile), its column block's pattern,
+  //      E, and (row side) W's row norms and the bias
+  u32x4 v[TPW][8];
+  float ev[TPW][NS][2], wsq[TPW], wsum[TPW], bjv[TPW];
+  uint32_t scol2[TPW][4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t ww[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-    float pl = 0.f, sg = 0.f, sq = 0.f, ab = 0.f;
+  for (int tt = 0; tt < TPW; ++tt) {
+    const int jbt = jb0 + tt < a.nb ? jb0 + tt : (int)a.nb - 1;   // (a tile past the last is skipped below)
+    const int c0 = jbt * BS;
+    const int wc = (int)((jbt == a.nb - 1 && a.rem_n > 0) ? a.rem_n : BS);
+    if (wr == BS && wc == BS) {
+      const uint16_t* p0 = a.y + (int64_t)(r0 + 8 * rg) * a.sym + c0 + 8 * cg;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      pl = dot2<DT>(ww[q], ONES, pl);
-      sg = dot2<DT>(ww[q], scol2[q], sg);
-      sq = dot2<DT>(ww[q], ww[q], sq);
-      ab = dot2<DT>(ww[q] & 0x7FFF7FFFu, ONES, ab);
-    }
-    rs[i][0] = pl; rs[i][1] = sg; rs[i][2] = sq; rs[i][3] = ab;
-  }
-  // ---- column direction: two rows' values of one column packed into one operand
-  float cs[8][4];
+      for (int i = 0; i < 8; ++i)
+        v[tt][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p0 + i * a.sym));
+    } else {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) cs[e][0] = cs[e][1] = cs[e][2] = cs[e][3] = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; i += 2) {
-    const uint32_t w0[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-    const uint32_t w1[4] = {v[i + 1].x, v[i + 1].y, v[i + 1].z, v[i + 1].w};
-    const uint32_t sr = srow2[i / 2];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t plo = __builtin_amdgcn_perm(w1[q], w0[q], 0x05040100u);     // column 2q of rows i, i + 1
-      const uint32_t phi = __builtin_amdgcn_perm(w1[q], w0[q], 0x07060302u);     // column 2q + 1
-      cs[2 * q][0] = dot2<DT>(plo, ONES, cs[2 * q][0]);
-      cs[2 * q][1] = dot2<DT>(plo, sr, cs[2 * q][1]);
-      cs[2 * q][2] = dot2<DT>(plo, plo, cs[2 * q][2]);
-      cs[2 * q][3] = dot2<DT>(plo & 0x7FFF7FFFu, ONES, cs[2 * q][3]);
-      cs[2 * q + 1][0] = dot2<DT>(phi, ONES, cs[2 * q + 1][0]);
-      cs[2 * q + 1][1] = dot2<DT>(phi, sr, cs[2 * q + 1][1]);
-      cs[2 * q + 1][2] = dot2<DT>(phi, phi, cs[2 * q + 1][2]);
-      cs[2 * q + 1][3] = dot2<DT>(phi & 0x7FFF7FFFu, ONES, cs[2 * q + 1][3]);
-    }
-  }
-  // the four row groups of the wave (lanes cg, cg + 16, cg + 32, cg + 48) add their column sums by lane swaps:
-  // permlane32_swap pairs lanes q and q + 2, permlane16_swap then q and q + 1; value i = 4 e + s of lane (q, cg)
-  // ends as the wave's sum of value i + 8 q, so lane (q, cg) holds the four sums of columns 8 cg + 2 q (u[0 .. 3])
-  // and 8 cg + 2 q + 1 (u[4 .. 7]).  Into LDS by lane (consecutive 16-byte slots); the reader adds the four waves.
-  {
-    float t1[16], u[8];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(cs[j / 4][j % 4]),
-                                                      __float_as_uint(cs[(j + 16) / 4][j % 4]), false, false);
-      t1[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(t1[j]), __float_as_uint(t1[j + 8]), false,
-                                                      false);
-      u[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
-    }
-    colw[w][0][lane] = f32x4{u[0], u[1], u[2], u[3]};
-    colw[w][1][lane] = f32x4{u[4], u[5], u[6], u[7]};
-  }
-  // the 16 lanes of a row group add their row sums; lane cg < 8 keeps row 8 rg + cg
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    f32x4 r;
-    r.x = row16_sum<DT>(rs[i][0]);
-    r.y = row16_sum<DT>(rs[i][1]);
-    r.z = row16_sum<DT>(rs[i][2]);
-    r.w = row16_sum<DT>(rs[i][3]);
-    if (cg == i) rows[8 * rg + i] = r;
-  }
-  __syncthreads();
-
-  // ---- scoring
-  float e0 = ev[0][0], e1 = ev[0][1];
-#pragma unroll
-  for (int s = 1; s < NSPL; ++s)
-    if (s < splits) {
-      e0 += ev[s][0];
-      e1 += ev[s][1];
-    }
-  Best best;
-  if (colside) {
-    // column-block check of row R, block jb (serving flavour)
-    const int rr = 64 * w + lane;
-    if (rr < wr) {
-      const f32x4 s4 = rows[rr];
-      const f32x4 q0 = a.consts[3 * jb], q1 = a.consts[3 * jb + 1], q2 = a.consts[3 * jb + 2];
-      const PairScore ps = judge_serve(s4.x, s4.y, s4.z, s4.w, fsqrt(asq), asum, e0, e1, q0.x, q0.y, q0.z, q0.w,
-                                       q2.x, q2.y, q1.x, q1.y, q1.z, q1.w, (float)wc, a);
-      const int64_t p = (int64_t)R * a.nb + jb;
-      if (a.zcol) {
-        a.zcol[2 * p] = ps.z0;
-        a.zcol[2 * p + 1] = ps.z1;
+      for (int i = 0; i < 8; ++i) {
+        const int r = 8 * rg + i;
+        v[tt][i] = (r < wr && 8 * cg < wc) ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+                                                 a.y + (int64_t)(r0 + r) * a.sym + c0 + 8 * cg))
+                                           : u32x4{0u, 0u, 0u, 0u};
       }
-      keep_best(best, ps.zc, ps.sec, ps.dc, p);
-      best.unk += ps.unk;
     }
-  } else {
-    // row-block check of column J, row block ib (training flavour, y^T = W x^T + b)
-    const int cc = 64 * (w - 2) + lane;
-    if (cc < wc) {
-      // column cc = 8 cg + 2 q + parity sits at lane 16 q + cg of every wave's slot
-      const int cl = 16 * ((cc & 7) >> 1) + (cc >> 3), par = cc & 1;
+    {
+      const float* spc = a.sign_table + (wc - 1) * 128;
+      const f32x4 ca = *reinterpret_cast<const f32x4*>(spc + 8 * cg);
+      const f32x4 cb = *reinterpret_cast<const f32x4*>(spc + 8 * cg + 4);
+      scol2[tt][0] = pack_signs<DT>(ca.x, ca.y); scol2[tt][1] = pack_signs<DT>(ca.z, ca.w);
+      scol2[tt][2] = pack_signs<DT>(cb.x, cb.y); scol2[tt][3] = pack_signs<DT>(cb.z, cb.w);
+    }
+    const float* ebase;
+    int64_t estride, pstride, splits;
+    if (colside) {
+      ebase = a.Ecol + (int64_t)(2 * jbt) * a.m + Rc; estride = a.m; pstride = 2 * a.nb * a.m; splits = a.scol;
+      wsq[tt] = wsum[tt] = bjv[tt] = 0.f;
+    } else {
+      const int J = c0 + 64 * (w - 2) + lane, Jc = J < n ? J : n - 1;
+      ebase = a.Erow + (int64_t)(2 * ib) * a.n + Jc; estride = a.n; pstride = 2 * a.mb * a.n; splits = a.srow;
+      wsq[tt] = a.wn[Jc];
+      wsum[tt] = a.wn[a.n + Jc];
+      bjv[tt] = a.bias ? half_to_f32<DT>(a.bias[Jc]) : 0.f;
+    }
+#pragma unroll
+    for (int sp = 0; sp < NS; ++sp) {
+      const int64_t sc = sp < splits ? sp : 0;
+      ev[tt][sp][0] = ebase[sc * pstride];
+      ev[tt][sp][1] = ebase[sc * pstride + estride];
+    }
+  }
+
+  Best best;
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) {
+    const int jb = jb0 + tt;
+    if (jb >= a.nb) break;                                       // (uniform over the workgroup)
+    if (tt > 0) __syncthreads();                                 // the previous tile's LDS reads are done
+    const int c0 = jb * BS;
+    const int wc = (int)((jb == a.nb - 1 && a.rem_n > 0) ? a.rem_n : BS);
+    // ---- column direction: two rows' values of one column packed into one operand
+    float cs[8][4];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) cs[e][0] = cs[e][1] = cs[e][2] = cs[e][3] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const uint32_t w0[4] = {v[tt][i].x, v[tt][i].y, v[tt][i].z, v[tt][i].w};
+      const uint32_t w1[4] = {v[tt][i + 1].x, v[tt][i + 1].y, v[tt][i + 1].z, v[tt][i + 1].w};
+      const uint32_t sr = srow2[i / 2];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t plo = __builtin_amdgcn_perm(w1[q], w0[q], 0x05040100u);     // column 2q of rows i, i + 1
+        const uint32_t phi = __builtin_amdgcn_perm(w1[q], w0[q], 0x07060302u);     // column 2q + 1
+        cs[2 * q][0] = dot2<DT>(plo, ONES, cs[2 * q][0]);
+        cs[2 * q][1] = dot2<DT>(plo, sr, cs[2 * q][1]);
+        cs[2 * q][2] = dot2<DT>(plo, plo, cs[2 * q][2]);
+        cs[2 * q][3] = dot2<DT>(plo & 0x7FFF7FFFu, ONES, cs[2 * q][3]);
+        cs[2 * q + 1][0] = dot2<DT>(phi, ONES, cs[2 * q + 1][0]);
+        cs[2 * q + 1][1] = dot2<DT>(phi, sr, cs[2 * q + 1][1]);
+        cs[2 * q + 1][2] = dot2<DT>(phi, phi, cs[2 * q + 1][2]);
+        cs[2 * q + 1][3] = dot2<DT>(phi & 0x7FFF7FFFu, ONES, cs[2 * q + 1][3]);
+      }
+    }
+    // the four row groups of the wave (lanes cg, cg + 16, cg + 32, cg + 48) add their column sums by lane swaps:
+    // permlane32_swap pairs lanes q and q + 2, permlane16_swap then q and q + 1; value i = 4 e + s of lane (q, cg)
+    // ends as the wave's sum of value i + 8 q, so lane (q, cg) holds the four sums of columns 8 cg + 2 q (u[0 .. 3])
+    // and 8 cg + 2 q + 1 (u[4 .. 7]).  Into LDS by lane (consecutive 16-byte slots); the reader adds the four waves.
+    {
+      float t1[16], u[8];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(cs[j / 4][j % 4]),
+                                                        __float_as_uint(cs[(j + 16) / 4][j % 4]), false, false);
+        t1[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(t1[j]), __float_as_uint(t1[j + 8]), false,
+                                                        false);
+        u[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+      }
+      colw[w][0][lane] = f32x4{u[0], u[1], u[2], u[3]};
+      colw[w][1][lane] = f32x4{u[4], u[5], u[6], u[7]};
+    }
+    // ---- row direction: four sums of each of the eight rows over this thread's eight columns, each row's added
+    //      over the 16 lanes of its row group at once (lane cg < 8 keeps row 8 rg + cg)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t ww[4] = {v[tt][i].x, v[tt][i].y, v[tt][i].z, v[tt][i].w};
       float pl = 0.f, sg = 0.f, sq = 0.f, ab = 0.f;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 q = colw[g][par][cl];
-        pl += q.x; sg += q.y; sq += q.z; ab += q.w;
+      for (int q = 0; q < 4; ++q) {
+        pl = dot2<DT>(ww[q], ONES, pl);
+        sg = dot2<DT>(ww[q], scol2[tt][q], sg);
+        sq = dot2<DT>(ww[q], ww[q], sq);
+        ab = dot2<DT>(ww[q] & 0x7FFF7FFFu, ONES, ab);
       }
-      const float wf = (float)wr;
-      float bound = asum * rstat[4];
-      if (a.bias) {
-        // a bias constant along the block: w copies of b_j, whose sums w b_j and (sum of signs) b_j are exact
-        e0 = e0 + bj * wf;
-        e1 = e1 + bj * rsign;
-        bound = bound + nan_abs(bj);
-      }
-      const float cn = fsqrt(sq), noise = cn * a.u, xn = fsqrt(asq);
-      const float inf = __builtin_inff();
-      const float nrm[2] = {fsqrt(rstat[0]), fsqrt(rstat[1])};
-      float fl[2];
+      f32x4 r;
+      r.x = row16_sum<DT>(pl);
+      r.y = row16_sum<DT>(sg);
+      r.z = row16_sum<DT>(sq);
+      r.w = row16_sum<DT>(ab);
+      if (cg == i) rows[8 * rg + i] = r;
+    }
+    __syncthreads();
+
+    // ---- scoring
+    float e0 = ev[tt][0][0], e1 = ev[tt][0][1];
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const float f_l2 = (xn * nrm[c]) * 1e-5f;
-        const float f_l1 = (asum * rstat[2 + c]) * a.l1c;
-        const float f = fminf(fabsf(f_l2) < inf ? f_l2 : inf, fabsf(f_l1) < inf ? f_l1 : inf);
-        fl[c] = f < inf ? f : bound * (float)(1e-5 * 128.0);
+    for (int sp = 1; sp < NS; ++sp)
+      if (sp < (colside ? a.scol : a.srow)) {
+        e0 += ev[tt][sp][0];
+        e1 += ev[tt][sp][1];
       }
-      float d0, d1;
-      const float z0 = judge_one(e0, pl, noise, cn, fl[0], bound, wf, ab, true, a, d0);
-      const float z1 = judge_one(e1, sg, noise, cn, fl[1], bound, wf, ab, false, a, d1);
-      const int64_t p = (int64_t)J * a.mb + ib;
-      if (a.zrow) {
-        a.zrow[2 * p] = z0;
-        a.zrow[2 * p + 1] = z1;
+    if (colside) {
+      // column-block check of row R, block jb (serving flavour)
+      const int rr = 64 * w + lane;
+      if (rr < wr) {
+        const f32x4 s4 = rows[rr];
+        const f32x4 q0 = a.consts[3 * jb], q1 = a.consts[3 * jb + 1], q2 = a.consts[3 * jb + 2];
+        bool ok;
+        PairScore ps = judge_serve_clean(s4.x, s4.y, s4.z, s4.w, fsqrt(xsq), xsum, e0, e1, q0.x, q0.y, q0.z, q0.w,
+                                         q2.x, q2.y, q1.x, q1.y, q1.z, q1.w, (float)wc, a, ok);
+        if (!ok)                                 // (non-finite inputs or an "impossible" pair: the full rules)
+          ps = judge_serve(s4.x, s4.y, s4.z, s4.w, fsqrt(xsq), xsum, e0, e1, q0.x, q0.y, q0.z, q0.w, q2.x, q2.y,
+                           q1.x, q1.y, q1.z, q1.w, (float)wc, a);
+        const int64_t p = (int64_t)R * a.nb + jb;
+        if (a.zcol) {
+          a.zcol[2 * p] = ps.z0;
+          a.zcol[2 * p + 1] = ps.z1;
+        }
+        keep_best(best, ps.zc, ps.sec, ps.dc, p);
+        best.unk += ps.unk;
       }
-      best.unk += (z0 < 0.f) + (z1 < 0.f);
-      const bool sec = z1 > z0;
-      keep_best(best, sec ? z1 : z0, sec, sec ? d1 : d0, p);
+    } else {
+      // row-block check of column J, row block ib (training flavour, y^T = W x^T + b)
+      const int cc = 64 * (w - 2) + lane, J = c0 + cc;
+      if (cc < wc) {
+        // column cc = 8 cg + 2 q + parity sits at lane 16 q + cg of every wave's slot
+        const int cl = 16 * ((cc & 7) >> 1) + (cc >> 3), par = cc & 1;
+        float pl = 0.f, sg = 0.f, sq = 0.f, ab = 0.f;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 q = colw[g][par][cl];
+          pl += q.x; sg += q.y; sq += q.z; ab += q.w;
+        }
+        const float wf = (float)wr, asum = wsum[tt], bj = bjv[tt];
+        float bound = asum * rstat[4];
+        if (a.bias) {
+          // a bias constant along the block: w copies of b_j, whose sums w b_j and (sum of signs) b_j are exact
+          e0 = e0 + bj * wf;
+          e1 = e1 + bj * rsign;
+          bound = bound + nan_abs(bj);
+        }
+        const float cn = fsqrt(sq), noise = cn * a.u, xn = fsqrt(wsq[tt]);
+        const float inf = __builtin_inff();
+        const float nrm[2] = {fsqrt(rstat[0]), fsqrt(rstat[1])};
+        float fl[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const float f_l2 = (xn * nrm[c]) * 1e-5f;
+          const float f_l1 = (asum * rstat[2 + c]) * a.l1c;
+          const float f = fminf(fabsf(f_l2) < inf ? f_l2 : inf, fabsf(f_l1) < inf ? f_l1 : inf);
+          fl[c] = f < inf ? f : bound * (float)(1e-5 * 128.0);
+        }
+        float d0, d1;
+        bool ok0, ok1;
+        float z0 = judge_one_clean(e0, pl, noise, cn, fl[0], bound, wf, ab, true, a, d0, ok0);
+        float z1 = judge_one_clean(e1, sg, noise, cn, fl[1], bound, wf, ab, false, a, d1, ok1);
+        if (!(ok0 && ok1)) {                     // (non-finite inputs or an "impossible" checksum: the full rules)
+          z0 = judge_one(e0, pl, noise, cn, fl[0], bound, wf, ab, true, a, d0);
+          z1 = judge_one(e1, sg, noise, cn, fl[1], bound, wf, ab, false, a, d1);
+        }
+        const int64_t p = (int64_t)J * a.mb + ib;
+        if (a.zrow) {
+          a.zrow[2 * p] = z0;
+          a.zrow[2 * p + 1] = z1;
+        }
+        best.unk += (z0 < 0.f) + (z1 < 0.f);
+        const bool sec = z1 > z0;
+        keep_best(best, sec ? z1 : z0, sec, sec ? d1 : d0, p);
+      }
     }
   }
   const int64_t key = wave_max_i64(best.key), keyd = wave_max_i64(best.keyd);
@@ -604,7 +631,7 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
 
 struct Layout {
   int64_t nb, mb, rem_n, rem_m, nkc, kp, scol, srow;
-  bool rs_col, rs_row;
+  bool rs_col, rs_row, tall_col, tall_row;
   int64_t off_parts, off_stats, off_xnp, off_xn, off_rstat, off_erow, off_ecol, off_fcol, total;   // in floats
 };
 
@@ -620,8 +647,11 @@ Layout layout(int64_t m, int64_t k, int64_t n) {
   // at least), else depth splits of the staged GEMM
   L.rs_col = k % RS_K == 0 && sdc_cdiv(m, 64) * sdc_cdiv(2 * L.nb, 64) >= 64;
   L.rs_row = k % RS_K == 0 && sdc_cdiv(n, 64) * sdc_cdiv(2 * L.mb, 64) >= 64;
-  L.scol = L.rs_col ? 1 : sdc_expected_splits(m, k, 2 * L.nb);
-  L.srow = L.rs_row ? 1 : sdc_expected_splits(n, k, 2 * L.mb);
+  // the tall-tile variant (128-row tiles over depth halves, two planes) where its workgroups still fill the GPU
+  L.tall_col = L.rs_col && k % (2 * RS_K) == 0 && 2 * sdc_cdiv(m, 128) * sdc_cdiv(2 * L.nb, 64) >= 192;
+  L.tall_row = L.rs_row && k % (2 * RS_K) == 0 && 2 * sdc_cdiv(n, 128) * sdc_cdiv(2 * L.mb, 64) >= 192;
+  L.scol = L.rs_col ? (L.tall_col ? 2 : 1) : sdc_expected_splits(m, k, 2 * L.nb);
+  L.srow = L.rs_row ? (L.tall_row ? 2 : 1) : sdc_expected_splits(n, k, 2 * L.mb);
   auto al = [](int64_t x) { return (x + 63) / 64 * 64; };
   int64_t o = 0;
   // x's block-sum parts: [3][2 mb][kp], or (register-streamed row GEMM) fragment order, whichever is larger
@@ -702,7 +732,7 @@ int queue_both(const void* x, int64_t sxm, const void* W, int64_t swn, const voi
                    sdc_parts_fragments(parts, spc, 2 * L.nb, k, ws + L.off_fcol, side) == SDC_OK)) {
     GemmArgs gf = gc;
     gf.B = parts_frag ? parts_frag : ws + L.off_fcol;
-    rc = sdc_rs_gemm_launch(SDC_BF16, gf, 0, side);
+    rc = L.tall_col ? sdc_rs_gemm_tall_launch(SDC_BF16, gf, 0, side) : sdc_rs_gemm_launch(SDC_BF16, gf, 0, side);
   }
   if (rc == SDC_EUNSUPPORTED) rc = sdc_gemm_launch(SDC_BF16, gc, 1, side);   // (alignment: the staged GEMM)
   if (rc != SDC_OK) return rc;
@@ -739,7 +769,11 @@ int queue_both(const void* x, int64_t sxm, const void* W, int64_t swn, const voi
   gr.m = n; gr.k = k; gr.N = 2 * L.mb; gr.splits = L.srow;
   gr.E = ws + L.off_erow; gr.XN = nullptr; gr.et = 1; gr.rows_per_xcd = 1;
   gr.prof_name = "row_gemm";
-  rc = rs_row ? sdc_rs_gemm_launch(SDC_BF16, gr, 1, stream) : sdc_gemm_launch(SDC_BF16, gr, 1, stream);
+  if (!rs_row) {
+    rc = sdc_gemm_launch(SDC_BF16, gr, 1, stream);              // (W not 16-byte aligned: the staged GEMM)
+  } else {
+    rc = L.tall_row ? sdc_rs_gemm_tall_launch(SDC_BF16, gr, 1, stream) : sdc_rs_gemm_launch(SDC_BF16, gr, 1, stream);
+  }
   if (rc != SDC_OK) return rc;
   if (fin != stream && (rc = sdc_join(stream, fin)) != SDC_OK) return rc;   // (the side stream also holds the GEMM)
 
@@ -756,10 +790,11 @@ int queue_both(const void* x, int64_t sxm, const void* W, int64_t swn, const voi
   ya.zt = z; ya.lim_a = 1e18f; ya.lim_big = 1e18f;
   ya.capk = (float)(1.02 + (double)k * 2.384185791015625e-07);
   SdcProf prof("ypass", stream);
-  if (L.scol == 1 && gr.splits == 1)
-    hipLaunchKernelGGL((ypass_kernel<SDC_BF16, true>), dim3((unsigned)L.nb, (unsigned)L.mb), dim3(256), 0, stream, ya);
-  else
-    hipLaunchKernelGGL((ypass_kernel<SDC_BF16, false>), dim3((unsigned)L.nb, (unsigned)L.mb), dim3(256), 0, stream, ya);
+  const int64_t ns = std::max(L.scol, gr.splits);
+  const dim3 yg((unsigned)sdc_cdiv(L.nb, YTPW), (unsigned)L.mb);
+  if (ns == 1) hipLaunchKernelGGL((ypass_kernel<SDC_BF16, 1, YTPW>), yg, dim3(256), 0, stream, ya);
+  else if (ns == 2) hipLaunchKernelGGL((ypass_kernel<SDC_BF16, 2, YTPW>), yg, dim3(256), 0, stream, ya);
+  else hipLaunchKernelGGL((ypass_kernel<SDC_BF16, SDC_MAX_SPLITS, YTPW>), yg, dim3(256), 0, stream, ya);
   SDC_LAUNCH_CHECK();
   return SDC_OK;
 }

@@ -62,7 +62,9 @@ SHAPES = [(512, 640, 1000, True), (300, 256, 136, False), (129, 1032, 264, True)
           (256, 4104, 512, False), (100, 1030, 264, True),        # (x rows not 16-byte aligned)
           # register-streamed GEMMs (depth a multiple of 512, 64 tiles or more): a ragged checksum-column count,
           # then a ragged last row block and a row check narrower than its 64-column tile
-          (2048, 1024, 8200, True), (2000, 512, 8200, False)]
+          (2048, 1024, 8200, True), (2000, 512, 8200, False),
+          # its tall-tile variant (128-row tiles over two depth halves) for both GEMMs, ragged last row tile
+          (3000, 512, 12800, True)]
 
 
 @pytest.mark.parametrize("m,k,n,with_bias", SHAPES)
@@ -138,3 +140,33 @@ def test_full_size_layer_single_bit_flips():
     print(f"16 single-bit flips x 2 checks: {agree} verdicts agree, {band} in the band, {flagged} flagged; "
           f"max |dz| at the flipped blocks {worst_dz:.2e}")
     assert band <= 2
+
+
+@pytest.mark.parametrize("m,k,n,with_bias", [(512, 512, 1024, True), (3000, 512, 12800, False)])
+def test_non_finite_and_impossible_outputs(m, k, n, with_bias):
+    """NaN, +Inf, -Inf and a huge finite value (an "impossible" checksum) in y: every score of both checks equals the
+    separate checks' and the oracle's (special scores exactly), so the y pass's full non-finite rules agree with the
+    fast scoring of clean pairs beside them; the unjudged counts match."""
+    from sdcguard_amd.checksum import linear_rows_operands
+    from sdcguard_amd.serve import LayerChecksums
+    x, W, b, y = make(m, k, n, with_bias, seed=m + n + 7)
+    y[3, 5] = float("nan")
+    y[m // 2, n - 3] = float("inf")
+    y[m - 1, n // 3] = float("-inf")
+    y[m // 4, n // 5] = 1e30
+    cs = LayerChecksums(W, b, 128)
+    zc, zr, st, rr = fused(x, W, b, y, cs)
+    zc2, zr2, st2, rr2 = separate(x, W, b, y, cs)
+    assert z_close(zc.reshape(-1), zc2.reshape(-1)).all()
+    assert z_close(zr.reshape(-1), zr2.reshape(-1)).all()
+    assert st[3] == st2[3] and rr[2] == rr2[2]
+    f = lambda t: t.float().cpu().numpy()                                    # noqa: E731
+    c = serve_check.layer_constants(f(W), None if b is None else f(b), 128, "bf16", seed=1)
+    o = serve_check.check_static(f(x), f(y), c, dtype="bf16", seed=1)
+    assert z_close(zc.reshape(-1), o.z.reshape(-1), gemm_slack(o.csb, o.den).reshape(-1)).all()
+    A, B, C, bias = linear_rows_operands(x, W, b, y)
+    orow = abft.zscores(f(A), f(B), f(C), None if bias is None else f(bias), dtype="bf16", seed=1)
+    assert z_close(zr.reshape(-1), orow.z.reshape(-1), gemm_slack(orow.csb, orow.den).reshape(-1)).all()
+    nb = -(-n // 128)
+    assert np.isinf(zc[m // 4, (n // 5) // 128]).any() and np.isinf(zc[m // 2, (n - 3) // 128]).any()
+    assert zmax(st[0]) > 6 and zmax(rr[0]) > 6 and nb > 0
