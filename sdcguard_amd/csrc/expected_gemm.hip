@@ -760,7 +760,9 @@ template <int DT, int ROLE, int TRF>
 __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_kernel(GemmArgs g) {
   constexpr int TCF = 2, TR = 32 * TRF, TC = 64, NG = TRF * TCF * 4, RB = 4, NAI = TR / 8, APS = NAI / 4;
   constexpr int RT_SEGB = TR * 128;             // bytes of A per wave and segment (TR rows x 128 bytes)
-  __shared__ __attribute__((aligned(16))) uint8_t smem[RS_WAVES * 2 * RT_SEGB];
+  constexpr int RED_BYTES = RS_WAVES * TC * (TR + 4) * 4;       // the epilogue's reduction (below)
+  __shared__ __attribute__((aligned(16)))
+  uint8_t smem[RS_WAVES * 2 * RT_SEGB > RED_BYTES ? RS_WAVES * 2 * RT_SEGB : RED_BYTES];
   const int t = threadIdx.x, lane = t & 63;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int r = lane & 31, h = lane >> 5;
@@ -919,28 +921,34 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
     __builtin_amdgcn_sched_barrier(0);
   }
   __syncthreads();
-  f32x4* red = reinterpret_cast<f32x4*>(smem);                  // [RS_WAVES][NG][64]: 128 KB
-  static_assert(RS_WAVES * NG * 64 * 16 <= (int)sizeof(smem), "the reduction fits the ring");
+  // The waves' accumulators meet in LDS column by column ([wave][column][row], rows padded to TR + 4 floats so a
+  // wave's 16-byte writes spread over the banks) and are added in wave (depth) order; each store instruction then
+  // writes two whole columns of the tile (2 x TR floats, contiguous in the transposed plane).
+  constexpr int RP = TR + 4;
+  float* red = reinterpret_cast<float*>(smem);                  // [RS_WAVES][TC][RP]
+  static_assert(RS_WAVES * TC * RP * 4 <= (int)sizeof(smem), "the reduction fits the shared memory");
 #pragma unroll
   for (int i = 0; i < TRF; ++i)
 #pragma unroll
     for (int n = 0; n < TCF; ++n)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4)
-        red[(w * NG + (i * TCF + n) * 4 + r4) * 64 + lane] =
+        *reinterpret_cast<f32x4*>(red + (w * TC + 32 * n + r) * RP + 32 * i + 8 * r4 + 4 * h) =
             f32x4{acc[i][n][4 * r4], acc[i][n][4 * r4 + 1], acc[i][n][4 * r4 + 2], acc[i][n][4 * r4 + 3]};
   __syncthreads();
   const int64_t me = g.m;
   float* const Eh = g.E + half * N * me;
+  constexpr int LPC = TR / 4;                                   // lanes per column (4 rows each)
+  constexpr int CPI = 64 / LPC;                                 // columns per store instruction
+  const int lr = lane % LPC, lc = lane / LPC;
 #pragma unroll
-  for (int gq = 0; gq < NG / RS_WAVES; ++gq) {
-    const int gi = w * (NG / RS_WAVES) + gq;
-    f32x4 v = red[gi * 64 + lane];
+  for (int gq = 0; gq < TC / (RS_WAVES * CPI); ++gq) {
+    const int cl = (w * (TC / (RS_WAVES * CPI)) + gq) * CPI + lc;   // the tile's column
+    f32x4 v = *reinterpret_cast<const f32x4*>(red + cl * RP + 4 * lr);
 #pragma unroll
-    for (int q = 1; q < RS_WAVES; ++q) v += red[(q * NG + gi) * 64 + lane];
-    const int i = gi / (4 * TCF), n = (gi / 4) % TCF, r4 = gi % 4;
-    const int64_t row = r0 + 32 * i + 8 * r4 + 4 * h;
-    const int64_t col = c0 + 32 * n + r;
+    for (int q = 1; q < RS_WAVES; ++q) v += *reinterpret_cast<const f32x4*>(red + (q * TC + cl) * RP + 4 * lr);
+    const int64_t row = r0 + 4 * lr;
+    const int64_t col = c0 + cl;
     if (col < N) {
       float* Ec = Eh + col * me;
       if (row + 4 <= m && (me % 4) == 0) {

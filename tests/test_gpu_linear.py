@@ -108,14 +108,29 @@ def _flip(y: torch.Tensor, flat: int, bit: int) -> None:
 
 
 def test_full_size_layer_single_bit_flips():
-    """x 4096x4096 N(0,1), W 14336x4096 N(0,0.02), y = x W^T in bf16: clean, then 16 trials each flipping one random
-    bit (exponent or mantissa) of one random element of y.  Both verdicts agree with the separate checks outside the
-    band |z - 6| < 0.3; a flagged flip is located at the same place."""
+    """x 4096x4096 N(0,1), W 14336x4096 N(0,0.02), y = x W^T in bf16: every clean score of both checks against the
+    oracle (the serving check on y, the training check on y^T = W x^T); then 16 trials each flipping one random bit
+    (exponent or mantissa) of one random element of y: the flipped row's column-block scores and the flipped column's
+    row-block scores against the oracle's for that row and column, every other score as clean, and the verdicts
+    against the separate checks' outside the band |z - 6| < 0.3; a flagged flip is located at the same place.
+    Prints the largest |dz| against the oracle and the band count."""
+    from sdcguard_amd.checksum import linear_rows_operands
     from sdcguard_amd.serve import LayerChecksums
     x, W, b, y = make(4096, 4096, 14336, False, seed=3)
     cs = LayerChecksums(W, None, 128)
     zc, zr, st, rr = fused(x, W, None, y, cs)
     assert zmax(st[0]) < 6 and zmax(rr[0]) < 6, (zmax(st[0]), zmax(rr[0]))
+    f = lambda t: t.float().cpu().numpy()                                    # noqa: E731
+    xf, Wf, yf = f(x), f(W), f(y)
+    c = serve_check.layer_constants(Wf, None, 128, "bf16", seed=1)
+    o = serve_check.check_static(xf, yf, c, dtype="bf16", seed=1)
+    ok = z_close(zc.reshape(-1), o.z.reshape(-1), gemm_slack(o.csb, o.den).reshape(-1))
+    assert ok.all(), (np.nonzero(~ok)[0][:5], zc.reshape(-1)[~ok][:5], o.z.reshape(-1)[~ok][:5])
+    xt = np.ascontiguousarray(xf.T)
+    orow = abft.zscores(Wf, xt, np.ascontiguousarray(yf.T), None, dtype="bf16", seed=1)
+    ok = z_close(zr.reshape(-1), orow.z.reshape(-1), gemm_slack(orow.csb, orow.den).reshape(-1))
+    assert ok.all(), (np.nonzero(~ok)[0][:5], zr.reshape(-1)[~ok][:5], orow.z.reshape(-1)[~ok][:5])
+    dz_clean = max(float(np.abs(zc - o.z.reshape(zc.shape)).max()), float(np.abs(zr - orow.z.reshape(zr.shape)).max()))
     rng = random.Random(11)
     band = agree = flagged = 0
     worst_dz = 0.0
@@ -123,11 +138,27 @@ def test_full_size_layer_single_bit_flips():
         i, j, bit = rng.randrange(4096), rng.randrange(14336), rng.randrange(0, 15)
         y2 = y.clone()
         _flip(y2, i * 14336 + j, bit)
-        zc, zr, st, rr = fused(x, W, None, y2, cs)
-        zc2, zr2, st2, rr2 = separate(x, W, None, y2, cs)
-        worst_dz = max(worst_dz, float(np.abs(zc[i, j // 128] - zc2[i, j // 128]).max()),
-                       float(np.abs(zr[j, i // 128] - zr2[j, i // 128]).max()))
-        for got, want, loc in ((st, st2, (i * 112 + j // 128)), (rr, rr2, (j * 32 + i // 128))):
+        zc2, zr2, st2, rr2 = fused(x, W, None, y2, cs)
+        zs, zrs, sts, rrs = separate(x, W, None, y2, cs)
+        # every other row / column scores as clean
+        keep_r = np.ones(4096, bool)
+        keep_r[i] = False
+        keep_c = np.ones(14336, bool)
+        keep_c[j] = False
+        assert np.array_equal(zc2[keep_r], zc[keep_r]) and np.array_equal(zr2[keep_c], zr[keep_c]), trial
+        # the flipped row and column against the oracle
+        y2f = y2[i:i + 1].float().cpu().numpy()
+        orr = serve_check.check_static(xf[i:i + 1], y2f, c, dtype="bf16", seed=1)
+        okr = z_close(zc2[i].reshape(-1), orr.z.reshape(-1), gemm_slack(orr.csb, orr.den).reshape(-1))
+        assert okr.all(), (trial, bit, zc2[i].reshape(-1)[~okr][:4], orr.z.reshape(-1)[~okr][:4])
+        ycol = y2[:, j:j + 1].float().cpu().numpy().T
+        occ = abft.zscores(Wf[j:j + 1], xt, np.ascontiguousarray(ycol), None, dtype="bf16", seed=1)
+        okc = z_close(zr2[j].reshape(-1), occ.z.reshape(-1), gemm_slack(occ.csb, occ.den).reshape(-1))
+        assert okc.all(), (trial, bit, zr2[j].reshape(-1)[~okc][:4], occ.z.reshape(-1)[~okc][:4])
+        fin_r, fin_c = np.isfinite(orr.z), np.isfinite(occ.z)
+        worst_dz = max(worst_dz, float(np.abs(zc2[i].reshape(-1) - orr.z.reshape(-1))[fin_r.reshape(-1)].max()),
+                       float(np.abs(zr2[j].reshape(-1) - occ.z.reshape(-1))[fin_c.reshape(-1)].max()))
+        for got, want, loc in ((st2, sts, (i * 112 + j // 128)), (rr2, rrs, (j * 32 + i // 128))):
             zg, zw = zmax(got[0]), zmax(want[0])
             if abs(zw - 6.0) < 0.3 or abs(zg - 6.0) < 0.3:
                 band += 1
@@ -137,8 +168,9 @@ def test_full_size_layer_single_bit_flips():
             if zg > 6:
                 flagged += 1
                 assert (int(got[0]) & 0xFFFFFFFF) // 2 == loc, (trial, bit)
-    print(f"16 single-bit flips x 2 checks: {agree} verdicts agree, {band} in the band, {flagged} flagged; "
-          f"max |dz| at the flipped blocks {worst_dz:.2e}")
+    print(f"clean: max |dz| against the oracle {dz_clean:.2e}; 16 single-bit flips x 2 checks: {agree} verdicts "
+          f"agree, {band} in the band, {flagged} flagged; max |dz| of the flipped row and column against the oracle "
+          f"{worst_dz:.2e}")
     assert band <= 2
 
 
