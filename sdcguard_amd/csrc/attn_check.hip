@@ -35,6 +35,7 @@ constexpr float TWO22 = 2.384185791015625e-07f;   // 2^-22
 constexpr float TWO21 = 4.76837158203125e-07f;    // 2^-21
 constexpr float NEG_INF = -__builtin_inff();
 constexpr int BTCAP = 256;                        // block-table entries a workgroup holds in LDS
+constexpr int QCAP = 1025;                        // query start locations a workgroup holds in LDS (1024 requests)
 
 struct AttnArgs {
   const uint16_t* q; const uint16_t* o; const uint16_t* kv; const uint16_t* key; const uint16_t* val;
@@ -57,7 +58,7 @@ struct Sample {
 
 // The smallest k in [0, n] with arr[k] >= x (arr non-decreasing with n + 1 entries; n when none of arr[0..n-1]
 // is): serve_attn.py:292-304.
-__device__ int64_t lower_bound(const int32_t* arr, int64_t n, int64_t x) {
+__device__ __forceinline__ int64_t lower_bound(const int32_t* arr, int64_t n, int64_t x) {
   int64_t lo = 0, hi = n;
   while (lo < hi) {
     const int64_t mid = (lo + hi) >> 1;
@@ -68,9 +69,10 @@ __device__ int64_t lower_bound(const int32_t* arr, int64_t n, int64_t x) {
 
 // Sample j of the layer at a step: serve_attn.py:306-327 (even j: a token of the step; odd j: the newest token
 // of a request; one number picks the token or request and the head together).
-__device__ Sample pick_sample(const AttnArgs& a, int64_t step, int64_t j) {
+// qsl: the query start locations (R + 1 entries), read from LDS when the workgroup holds them.
+__device__ __forceinline__ Sample pick_sample(const AttnArgs& a, int64_t step, int64_t j, const int32_t* qsl) {
   Sample s;
-  const int64_t ntok = min((int64_t)a.qsl[a.R], a.T);
+  const int64_t ntok = min((int64_t)qsl[a.R], a.T);
   const int64_t h = (step / a.nl) * 1000003ll + j * 7919ll + a.idx * 104729ll;
   const bool odd = (j & 1) != 0;
   int64_t i, pk;
@@ -80,15 +82,15 @@ __device__ Sample pick_sample(const AttnArgs& a, int64_t step, int64_t j) {
     i = pk / a.Hq;
     have = ntok > 0;
   } else {
-    const int64_t rreal = lower_bound(a.qsl, a.R, ntok);
+    const int64_t rreal = lower_bound(qsl, a.R, ntok);
     pk = h % max(rreal * a.Hq, (int64_t)1);
     const int64_t rq = min(pk / a.Hq, a.R - 1);
-    i = (int64_t)a.qsl[rq + 1] - 1;
+    i = (int64_t)qsl[rq + 1] - 1;
     have = ntok > 0 && rreal > 0;
   }
   i = min(max(i, (int64_t)0), a.T - 1);
-  const int64_t r = min(max(lower_bound(a.qsl, a.R, i + 1) - 1, (int64_t)0), a.R - 1);
-  const int64_t q0 = a.qsl[r], q1 = a.qsl[r + 1], sl = a.seqlens[r];
+  const int64_t r = min(max(lower_bound(qsl, a.R, i + 1) - 1, (int64_t)0), a.R - 1);
+  const int64_t q0 = qsl[r], q1 = qsl[r + 1], sl = a.seqlens[r];
   const int64_t qlen = q1 - q0, pos = sl - qlen + (i - q0);
   s.valid = have && qlen > 0 && sl > 0 && pos >= 0 && pos < sl && sl <= a.W * a.N;
   s.i = i;
@@ -182,6 +184,8 @@ struct Lds {
   float py, pr;
   int last, claim, keep;
   int bt[BTCAP];              // the block-table entries of the workgroup's keys, when they fit
+  int qs[QCAP];               // the query start locations, when they fit
+  float cw[64];               // (the combine) each split record's weight exp(m_c - M)
 };
 
 // The sampled token's own KV write (serve_attn.py:533-569): the cache slot its K and V went to, against the slot
@@ -257,20 +261,36 @@ __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
   constexpr int TOK = G * U;                // keys per wave per tile
   __shared__ Lds<DP> sh;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // the query start locations into LDS with one round trip (the sample's binary searches then read LDS); their
+  // loads go out beside the control word's
+  const bool qs_lds = a.R + 1 <= QCAP;
+  int32_t qv[(QCAP + 255) / 256];
+#pragma unroll
+  for (int u = 0; u < (QCAP + 255) / 256; ++u) {
+    const int64_t i = tid + 256 * u;
+    qv[u] = (qs_lds && i <= a.R) ? a.qsl[i] : 0;
+  }
   const int64_t step = a.ctrl[0] & 0xFFFFFFFFll;
   const bool live = a.ctrl[1] != 0 && (step % a.nl) == a.idx;
   if (!live) return;
+#pragma unroll
+  for (int u = 0; u < (QCAP + 255) / 256; ++u) {
+    const int64_t i = tid + 256 * u;
+    if (qs_lds && i <= a.R) sh.qs[i] = qv[u];
+  }
+  __syncthreads();
+  auto pick = [&](int64_t j) { return qs_lds ? pick_sample(a, step, j, sh.qs) : pick_sample(a, step, j, a.qsl); };
   int64_t* sb = a.state + a.slot * NCOLS;
   if ((int64_t)blockIdx.x >= (int64_t)a.nsamp * a.nsplit) {
     // a workgroup of its own per sample checks the sampled token's KV write, beside the splits' keys
     const int64_t sw = (int64_t)blockIdx.x - (int64_t)a.nsamp * a.nsplit;
-    const Sample s = pick_sample(a, step, sw);
+    const Sample s = pick(sw);
     if (s.valid) check_write<DT, DP>(a, s, sh, sb, step, (int)a.D, a.bt + s.r * a.sbt);
     return;
   }
   const int64_t sj = blockIdx.x / a.nsplit, c = blockIdx.x - sj * a.nsplit;
   if (blockIdx.x == 0 && tid == 0) atomicAdd((unsigned long long*)(sb + C_CALLS), 1ull);
-  const Sample s = pick_sample(a, step, sj);
+  const Sample s = pick(sj);
   if (!s.valid) {
     if (c == 0 && tid == 0) atomicAdd((unsigned long long*)(sb + C_SKIP), 1ull);
     return;
@@ -293,6 +313,8 @@ __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
   if (bt_lds)
     for (int64_t i = tid; i < nbt; i += 256) sh.bt[i] = btr[b_first + i];
 
+  // the sampled row's output (what the judging workgroup compares), loaded beside q
+  const float ov = tid < D ? half_to_f32<DT>(a.o[s.i * a.sot + s.hq * a.soh + tid]) : 0.f;
   float q8[8], qa8[8];
   load8<DT, false>(a.q + s.i * a.sqt + s.hq * a.sqh, 1, d0, D, q8);
 #pragma unroll
@@ -477,24 +499,79 @@ __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
     __syncthreads();
     if (!sh.last) return;
     const float* base = a.ws + sj * a.nsplit * PW;
+    // Every record's values in flight at once: thread t < nsplit reads record t's scalars; the 256 / DP threads
+    // of dimension d (t % DP == d) read its four values of their share of the records, 32 records' loads at a
+    // time.  Then the maximum, the weights exp(m_c - M) and the sums, records added in order.
+    constexpr int TPD = 256 / DP;                               // threads per dimension (1, 2 or 4)
+    constexpr int CH = 32;                                      // records a thread has in flight
+    float sm = NEG_INF, sl = 0.f, sle = 0.f, sbad = 0.f;
+    if (tid < a.nsplit) {
+      const float* r = base + tid * PW;
+      sm = coherent_load(r);
+      sl = coherent_load(r + 1);
+      sle = coherent_load(r + 2);
+      sbad = coherent_load(r + 3);
+    }
+    const int dd = tid % DP, part = tid / DP;
+    const int per = (a.nsplit + TPD - 1) / TPD;
+    const int c_lo = part * per, c_hi = min(a.nsplit, c_lo + per);
+    float va[CH][4];
+    auto load_chunk = [&](int cb) {
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const bool in = cb + u < c_hi;
+        const float* r = base + (in ? cb + u : 0) * PW + 4 + dd;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) va[u][q] = in ? coherent_load(r + q * DP) : 0.f;
+      }
+    };
+    load_chunk(c_lo);
+    if (tid < a.nsplit) {
+      sh.cw[tid] = sm;
+      sh.vec[0][0][tid] = sl;
+      sh.vec[0][1][tid] = sle;
+      sh.vec[0][2][tid] = sbad;
+    }
+    __syncthreads();
     M = NEG_INF;
-#pragma unroll 8
-    for (int cc = 0; cc < a.nsplit; ++cc) M = fmaxf(M, coherent_load(base + cc * PW));
-    L = LE = RA = RAA = RAE = RV = 0.f;
+    for (int cc = 0; cc < a.nsplit; ++cc) M = fmaxf(M, sh.cw[cc]);
+    L = LE = 0.f;
     BAD = 0;
-#pragma unroll 4
     for (int cc = 0; cc < a.nsplit; ++cc) {
-      const float* r = base + cc * PW;
-      const float mc = coherent_load(r);
+      const float mc = sh.cw[cc];
       const float cw = mc > NEG_INF ? __expf(mc - M) : 0.f;
-      L += cw * coherent_load(r + 1);
-      LE += cw * coherent_load(r + 2);
-      BAD += coherent_load(r + 3) > 0.f ? 1 : 0;
-      if (d < DP) {
-        RA += cw * coherent_load(r + 4 + d);
-        RAA += cw * coherent_load(r + 4 + DP + d);
-        RAE += cw * coherent_load(r + 4 + 2 * DP + d);
-        RV += coherent_load(r + 4 + 3 * DP + d);
+      L += cw * sh.vec[0][0][cc];
+      LE += cw * sh.vec[0][1][cc];
+      BAD += sh.vec[0][2][cc] > 0.f ? 1 : 0;
+    }
+    float pa = 0.f, paa = 0.f, pae = 0.f, pv = 0.f;
+    for (int cb = c_lo; cb < c_hi; cb += CH) {
+      if (cb > c_lo) load_chunk(cb);
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        if (cb + u >= c_hi) break;
+        const float mc = sh.cw[cb + u];
+        const float cw = mc > NEG_INF ? __expf(mc - M) : 0.f;
+        pa += cw * va[u][0];
+        paa += cw * va[u][1];
+        pae += cw * va[u][2];
+        pv += va[u][3];
+      }
+    }
+    __syncthreads();                                            // (sh.vec is reused for the parts' sums)
+    sh.vec[part][0][dd] = pa;
+    sh.vec[part][1][dd] = paa;
+    sh.vec[part][2][dd] = pae;
+    sh.vec[part][3][dd] = pv;
+    __syncthreads();
+    RA = RAA = RAE = RV = 0.f;
+    if (d < DP) {
+#pragma unroll
+      for (int pp = 0; pp < TPD; ++pp) {
+        RA += sh.vec[pp][0][d];
+        RAA += sh.vec[pp][1][d];
+        RAE += sh.vec[pp][2][d];
+        RV += sh.vec[pp][3][d];
       }
     }
   }
@@ -504,8 +581,6 @@ __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
   const float ref = RA / L, ra = fabsf(ref);
   const float gam = ((float)nkeys / 16.0f + 32.0f) * TWO22 + TWO22 * fabsf(M);
   const float bound = (2.0f * a.u + gam) * (RAA / L + ra) + (RAE + ra * LE) / L + a.hsig_p * RV / L + a.sig_o;
-  float ov = 0.f;
-  if (d < D) ov = half_to_f32<DT>(a.o[s.i * a.sot + s.hq * a.soh + d]);
   float z = fabsf(ov - ref) / bound;
   z = z == z ? z : inf;
   z = d < D ? z : 0.f;
@@ -548,17 +623,14 @@ __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
       atomicAdd((unsigned long long*)(sb + C_SAMPLES), 1ull);
       atomicAdd((unsigned long long*)(sb + C_KEYS), (unsigned long long)nkeys);
       if (pz > 0.f) {
-        const int64_t zb = (int64_t)(uint32_t)__float_as_uint(pz) << 32;
-        const int64_t cur = __atomic_load_n(sb, __ATOMIC_RELAXED);
-        if (zb >= (cur & (int64_t)0xFFFFFFFF00000000ll)) {   // (ties too: the same columns in any order)
-          atomicMax((unsigned long long*)(sb + C_ZT), (unsigned long long)key_of(pz, s.i));
-          atomicMax((unsigned long long*)(sb + C_ZH), (unsigned long long)key_of(pz, s.hq));
-          atomicMax((unsigned long long*)(sb + C_ZD), (unsigned long long)key_of(pz, pd));
-          atomicMax((unsigned long long*)(sb + C_ZO), (unsigned long long)key_of(pz, __float_as_uint(sh.py)));
-          atomicMax((unsigned long long*)(sb + C_ZR), (unsigned long long)key_of(pz, __float_as_uint(sh.pr)));
-          atomicMax((unsigned long long*)(sb + C_ZS), (unsigned long long)key_of(pz, step));
-          atomicMax((unsigned long long*)(sb + C_ZP), (unsigned long long)key_of(pz, s.pos));
-        }
+        // (each column keeps the key of the largest score; no read of the row first, so no round trip)
+        atomicMax((unsigned long long*)(sb + C_ZT), (unsigned long long)key_of(pz, s.i));
+        atomicMax((unsigned long long*)(sb + C_ZH), (unsigned long long)key_of(pz, s.hq));
+        atomicMax((unsigned long long*)(sb + C_ZD), (unsigned long long)key_of(pz, pd));
+        atomicMax((unsigned long long*)(sb + C_ZO), (unsigned long long)key_of(pz, __float_as_uint(sh.py)));
+        atomicMax((unsigned long long*)(sb + C_ZR), (unsigned long long)key_of(pz, __float_as_uint(sh.pr)));
+        atomicMax((unsigned long long*)(sb + C_ZS), (unsigned long long)key_of(pz, step));
+        atomicMax((unsigned long long*)(sb + C_ZP), (unsigned long long)key_of(pz, s.pos));
       }
       if (pz > a.line && a.capm) {
         int32_t* cb = a.capm + a.slot * NCAPM;
@@ -634,12 +706,12 @@ int64_t pad_dim(int64_t D) { return D <= 64 ? 64 : D <= 128 ? 128 : 256; }
 constexpr int64_t MAX_SAMPLES = 1024;
 constexpr int64_t COUNTER_BYTES = MAX_SAMPLES * (int64_t)sizeof(int32_t);
 
-// Workgroups per sample: enough that a long context spreads over the chip (about 128 keys each: two tiles a wave),
+// Workgroups per sample: enough that a long context spreads over the chip (about 64 keys each: one tile a wave),
 // at most 64, and at most 1024 workgroups in all.
 extern "C" int64_t sdc_attn_splits(int64_t samples, int64_t max_keys) {
   if (samples <= 0 || max_keys <= 0) return 1;
   const int64_t cap = std::max<int64_t>(1, 1024 / samples);
-  const int64_t s = std::min<int64_t>(sdc_cdiv(max_keys, 128), cap);
+  const int64_t s = std::min<int64_t>(sdc_cdiv(max_keys, 64), cap);
   return std::max<int64_t>(1, std::min<int64_t>(s, 64));
 }
 
