@@ -260,6 +260,29 @@ int sdc_grouped_check(int dtype, const void* A, int64_t sam, int64_t sak, const 
                       float abs_floor, const float* sign_table, int64_t* results, void* workspace,
                       int64_t workspace_bytes, float* scores_out, hipStream_t stream);
 
+/* ---- the grouped check's serving form ------------------------------------------------------------------------
+ * No counterpart in the reference (its grouped check, guard._grouped_checks, makes every expert's block sums in
+ * every call): for served MoE layers, whose expert weights do not change between calls, the B-side constants are
+ * made once per layer and each call runs only the expected-side GEMM and the pass over out.
+ *   sdc_grouped_constants: from B (groups, k, n; strides sbg, sbk, sbn) and an optional shared bias (n values at
+ *     stride sbias), into consts (sdc_grouped_constants_bytes bytes, 256-byte aligned): per expert its block sums'
+ *     column norms, maxima and power-of-two scales, each block's largest |B|, the bias's block sums, and the three
+ *     16-bit parts of the scaled block sums.  workspace: sdc_grouped_constants_workspace bytes of scratch.
+ *   sdc_grouped_check_consts: sdc_grouped_check against those constants (has_bias: whether they hold a bias);
+ *     the same results and scores.  workspace: sdc_grouped_check_consts_workspace bytes. */
+int64_t sdc_grouped_constants_bytes(int64_t groups, int64_t k, int64_t n, int64_t bs);
+int64_t sdc_grouped_constants_workspace(int64_t groups, int64_t k, int64_t n, int64_t bs);
+int sdc_grouped_constants(int dtype, const void* B, int64_t sbg, int64_t sbk, int64_t sbn, int64_t groups, int64_t k,
+                          int64_t n, int64_t bs, const void* bias, int64_t sbias, const float* sign_table,
+                          void* consts, int64_t consts_bytes, void* workspace, int64_t workspace_bytes,
+                          hipStream_t stream);
+int64_t sdc_grouped_check_consts_workspace(int64_t groups, int64_t rows, int64_t k, int64_t n, int64_t bs);
+int sdc_grouped_check_consts(int dtype, const void* A, int64_t sam, int64_t sak, const void* consts, int64_t groups,
+                             const void* C, int64_t scm, int64_t scn, int64_t rows, int64_t k, int64_t n, int64_t bs,
+                             const int64_t* offs, int has_bias, float z, float abs_floor, const float* sign_table,
+                             int64_t* results, void* workspace, int64_t workspace_bytes, float* scores_out,
+                             hipStream_t stream);
+
 /* ---- per-layer constants of the serving check -------------------------------------------------------------
  * Replaces LayerChecksums._initialize (serve.py:149-211): built on the device from W (n x k, row stride swn, rows
  * k-contiguous) and an optional bias (n values at stride sbias, NULL: none), blocks of bs <= 128 output rows.

@@ -58,6 +58,12 @@ SIGNATURES = {
     "sdc_parts_fragments_bytes": (I64, [I64, I64]),
     "sdc_parts_fragments": (I32, [P, I64, I64, I64, P, P]),
     "sdc_grouped_check_workspace": (I64, [I64, I64, I64, I64, I64]),
+    "sdc_grouped_constants_bytes": (I64, [I64, I64, I64, I64]),
+    "sdc_grouped_constants_workspace": (I64, [I64, I64, I64, I64]),
+    "sdc_grouped_constants": (I32, [I32, P, I64, I64, I64, I64, I64, I64, I64, P, I64, P, P, I64, P, I64, P]),
+    "sdc_grouped_check_consts_workspace": (I64, [I64, I64, I64, I64, I64]),
+    "sdc_grouped_check_consts": (I32, [I32, P, I64, I64, P, I64, P, I64, I64, I64, I64, I64, I64, P, I32, F32, F32, P,
+                                       P, P, I64, P, P]),
     "sdc_grouped_check": (I32, [I32, P, I64, I64, P, I64, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, P, P, I64,
                                 F32, F32, P, P, P, I64, P, P]),
     "sdc_layer_constants_workspace": (I64, [I64, I64, I64]),

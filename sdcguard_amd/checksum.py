@@ -400,14 +400,18 @@ class GroupedStat:
     z: float
 
 
-def grouped_zscores(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, offs: torch.Tensor,
+def grouped_zscores(a: torch.Tensor, b: Optional[torch.Tensor], out: torch.Tensor, offs: torch.Tensor,
                     bias: Optional[torch.Tensor] = None, *, block: int = 128, abs_floor: float = ABS_FLOOR,
-                    z: float = 6.0, epoch: int = 0, scores_out: Optional[torch.Tensor] = None) -> GroupedStat:
+                    z: float = 6.0, epoch: int = 0, scores_out: Optional[torch.Tensor] = None,
+                    checksums: Optional["GroupedChecksums"] = None) -> GroupedStat:
     """Queue the check of a MoE grouped product out = a @ b[g] for the rows of group g (a: (T, k) tokens sorted by
     expert, b: (G, k, n), out: (T, n), offs: (G,) cumulative row ends, int32 or int64, on the device) without
     reading offs on the host: every group's rows are checked against that group's B, as
-    check_matmul(a[start:end], b[g], out[start:end]) checks them (guard._grouped_checks + checksum._zscores)."""
+    check_matmul(a[start:end], b[g], out[start:end]) checks them (guard._grouped_checks + checksum._zscores).
+    checksums: the layer's GroupedChecksums (b and bias may then be None; block and epoch are theirs)."""
     from . import _lib
+    if checksums is not None:
+        return _grouped_with(a, checksums, out, offs, abs_floor, z, scores_out)
     if a.dim() != 2 or b.dim() != 3 or out.dim() != 2:
         raise ValueError("grouped_zscores covers the (T, k) x (G, k, n) -> (T, n) layout")
     _lib.require_gpu(a, b, out, offs, bias)
@@ -425,10 +429,9 @@ def grouped_zscores(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, offs: t
         if bias.numel() != n:
             raise ValueError("grouped_zscores: a shared bias of n values")
         bias = bias if bias.dtype == dt else bias.to(dt)
-    # the ends as both kernels read them: clamped to the rows and made non-decreasing (a running maximum), so the
-    # GEMM's tile walk and the scoring pass's row-to-group search agree whatever offs holds; a private copy, so a
-    # routing buffer reused before resolve_grouped does not change how the results decode
-    offs64 = torch.cummax(offs.reshape(-1).to(torch.int64).clamp(0, T), 0).values.contiguous()
+    # (a private copy of the ends, so a routing buffer reused before resolve_grouped does not change how the results
+    # decode)
+    offs64 = _clamped_ends(offs, T)
     L = _lib.lib()
     nb = -(-n // block)
     results = torch.zeros(G, 3, dtype=torch.int64, device=out.device)
@@ -441,6 +444,78 @@ def grouped_zscores(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, offs: t
                              None if scores_out is None else scores_out.data_ptr(), _lib.stream_of(out))
     _lib.check(rc, "sdc_grouped_check")
     return GroupedStat(results, offs64, T, nb, z)
+
+
+class GroupedChecksums:
+    """A served MoE layer's grouped-check constants, made once on the device from its expert weights (groups, k, n)
+    and optional shared bias (n,): every expert's block sums, their norms, maxima and scales, and the three 16-bit
+    parts of the scaled sums (sdc_grouped_constants).  grouped_zscores(..., checksums=this) then runs only the
+    expected-side GEMM and the pass over the output, with the same results as a call that makes them (this
+    library's serving form; the reference makes every expert's block sums in every call).  The constants follow the
+    weights they were made from: make them again after the weights change."""
+
+    def __init__(self, b: torch.Tensor, bias: Optional[torch.Tensor] = None, *, block: int = 128, epoch: int = 0):
+        from . import _lib
+        if b.dim() != 3:
+            raise ValueError("GroupedChecksums takes expert weights (groups, k, n)")
+        _lib.require_gpu(b, bias)
+        if b.dtype not in UNIT_ROUNDOFF:
+            raise ValueError(f"unsupported dtype {b.dtype}")
+        G, k, n = b.shape
+        self.groups, self.k, self.n, self.block, self.epoch, self.dtype = G, k, n, block, epoch, b.dtype
+        if bias is not None:
+            bias = bias.reshape(-1)
+            if bias.numel() != n:
+                raise ValueError("GroupedChecksums: a shared bias of n values")
+            bias = bias if bias.dtype == b.dtype else bias.to(b.dtype)
+        self.has_bias = bias is not None
+        L = _lib.lib()
+        nbytes = int(L.sdc_grouped_constants_bytes(G, k, n, block))
+        if nbytes <= 0:
+            raise ValueError(f"GroupedChecksums: unsupported shape {tuple(b.shape)} or block {block}")
+        self.consts = torch.empty(nbytes // 4 + 64, dtype=torch.float32, device=b.device)
+        off = (-self.consts.data_ptr()) % 256 // 4          # 256-byte aligned start
+        self._ptr = self.consts.data_ptr() + 4 * off
+        ws = _lib.workspace(b.device, int(L.sdc_grouped_constants_workspace(G, k, n, block)))
+        rc = L.sdc_grouped_constants(_lib.dtype_code(b.dtype), b.data_ptr(), b.stride(0), b.stride(1), b.stride(2),
+                                     G, k, n, block, None if bias is None else bias.data_ptr(),
+                                     0 if bias is None else bias.stride(0), sign_table(b.device, epoch).data_ptr(),
+                                     self._ptr, nbytes, ws.data_ptr(), ws.numel(), _lib.stream_of(b))
+        _lib.check(rc, "sdc_grouped_constants")
+
+
+def _clamped_ends(offs: torch.Tensor, T: int) -> torch.Tensor:
+    # the ends as both kernels read them: clamped to the rows and made non-decreasing (a running maximum), so the
+    # GEMM's tile walk and the scoring pass's row-to-group search agree whatever offs holds; a private copy
+    return torch.cummax(offs.reshape(-1).to(torch.int64).clamp(0, T), 0).values.contiguous()
+
+
+def _grouped_with(a, cs: "GroupedChecksums", out, offs, abs_floor, z, scores_out) -> GroupedStat:
+    from . import _lib
+    if a.dim() != 2 or out.dim() != 2:
+        raise ValueError("grouped_zscores covers the (T, k) x (G, k, n) -> (T, n) layout")
+    _lib.require_gpu(a, out, offs, cs.consts)
+    dt = out.dtype
+    if dt != cs.dtype:
+        raise ValueError(f"the output's dtype {dt} is not the checksums' {cs.dtype}")
+    T, k = a.shape
+    G, n = cs.groups, cs.n
+    if k != cs.k or out.shape != (T, n) or offs.numel() != G:
+        raise ValueError(f"shape mismatch: a{tuple(a.shape)} out{tuple(out.shape)} offs {offs.numel()} for "
+                         f"checksums of ({G}, {cs.k}, {n})")
+    a = a if a.dtype == dt else a.to(dt)
+    offs64 = _clamped_ends(offs, T)
+    L = _lib.lib()
+    results = torch.zeros(G, 3, dtype=torch.int64, device=out.device)
+    ws = _lib.workspace(out.device, int(L.sdc_grouped_check_consts_workspace(G, T, k, n, cs.block)))
+    rc = L.sdc_grouped_check_consts(_lib.dtype_code(dt), a.data_ptr(), a.stride(0), a.stride(1), cs._ptr, G,
+                                    out.data_ptr(), out.stride(0), out.stride(1), T, k, n, cs.block, offs64.data_ptr(),
+                                    1 if cs.has_bias else 0, float(z), float(abs_floor),
+                                    sign_table(out.device, cs.epoch).data_ptr(), results.data_ptr(), ws.data_ptr(),
+                                    ws.numel(), None if scores_out is None else scores_out.data_ptr(),
+                                    _lib.stream_of(out))
+    _lib.check(rc, "sdc_grouped_check_consts")
+    return GroupedStat(results, offs64, T, -(-n // cs.block), z)
 
 
 def resolve_grouped(st: GroupedStat) -> list:

@@ -629,26 +629,24 @@ extern "C" int64_t sdc_matmul_check_workspace(int64_t batch_a, int64_t batch_b, 
 
 namespace {
 
-// The check of sdc_matmul_check, or (goffs set) of sdc_grouped_check: batch_b groups of B over one tall A / C.
-int run_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, int64_t batch_a, const void* B,
-              int64_t sbb, int64_t sbk, int64_t sbn, int64_t batch_b, const void* C, int64_t scb, int64_t scm,
-              int64_t scn, int64_t batch_c, int64_t m, int64_t k, int64_t n, int64_t bs, const void* bias,
-              int bias_kind, int64_t sbias_b, int64_t sbias_m, int64_t sbias_n, float alpha, float beta, float z,
-              float abs_floor, const float* sign_table, int64_t* result, void* workspace, int64_t workspace_bytes,
-              float* scores_out, const int64_t* goffs, hipStream_t stream) {
-  const bool grouped = goffs != nullptr;
-  const int64_t nbt = grouped ? 1 : (batch_a > batch_b ? batch_a : batch_b);
-  const Layout L = layout(batch_a, batch_b, m, k, n, bs, grouped);
-  if (batch_c * m * L.nb * 2 > 0xFFFFFFFFll) return SDC_EUNSUPPORTED;     // flat index in 32 bits
-  if (!workspace || workspace_bytes < L.total * (int64_t)sizeof(float) + 256) return SDC_EWORKSPACE;
-  float* ws = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
-  const float* s_full = sign_table + (bs - 1) * 128;
-  const float* s_last = L.rem ? sign_table + (L.rem - 1) * 128 : s_full;
+// Where a check's B-side constants live: in the call's workspace (the training checks), or in a per-layer buffer
+// made once (the grouped check's serving form, sdc_grouped_constants).
+struct BConsts {
+  float* colstat;                  // [bB][2nb][3]
+  float* bmaxf;                    // [bB][nb]
+  float* bias3;                    // [nb][3]
+  uint16_t* parts;                 // [bB][3 * 2nb][kp]
+};
 
+// The B side: block sums of B and their statistics (b_stage, b_finish), the bias's block sums, and the three parts
+// of the block sums (split).  b2t and part are scratch of layout()'s sizes.
+int stage_b(int dtype, const void* B, int64_t sbb, int64_t sbk, int64_t sbn, int64_t batch_b, int64_t k, int64_t n,
+            int64_t bs, const Layout& L, const void* bias, int bias_kind, int64_t sbias_n, const float* s_full,
+            const float* s_last, float* b2t, float* part, const BConsts& bc, hipStream_t stream) {
   BStageArgs ba{};
   ba.B = (const uint16_t*)B; ba.sbb = sbb; ba.sbk = sbk; ba.sbn = sbn;
   ba.k = k; ba.n = n; ba.nb = L.nb; ba.bs = bs; ba.rem = L.rem; ba.nkc = L.nkc;
-  ba.s_full = s_full; ba.s_last = s_last; ba.B2T = ws + L.off_b2t; ba.part = ws + L.off_part;
+  ba.s_full = s_full; ba.s_last = s_last; ba.B2T = b2t; ba.part = part;
   // B with k-contiguous rows (W.t(), x^T) is read down its columns by b_stage_t_kernel; otherwise across rows
   const bool b_t = sbk == 1 && sbn != 1;
   if (b_t) ba.vec = (sbn % 8 == 0) && (sbb % 8 == 0) && ((uintptr_t)B % 16 == 0);
@@ -667,10 +665,10 @@ int run_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, i
     SDC_LAUNCH_CHECK();
   }
   BFinishArgs fa{};
-  fa.part = ws + L.off_part; fa.nkc = L.nkc; fa.nb = L.nb; fa.bs = bs; fa.rem = L.rem; fa.fp16 = dtype == SDC_FP16;
-  fa.colstat = ws + L.off_col; fa.bmaxf = ws + L.off_bmax;
+  fa.part = part; fa.nkc = L.nkc; fa.nb = L.nb; fa.bs = bs; fa.rem = L.rem; fa.fp16 = dtype == SDC_FP16;
+  fa.colstat = bc.colstat; fa.bmaxf = bc.bmaxf;
   fa.bias = bias_kind == 1 ? (const uint16_t*)bias : nullptr; fa.sbias = sbias_n;
-  fa.s_full = s_full; fa.s_last = s_last; fa.bias_out = ws + L.off_bias;
+  fa.s_full = s_full; fa.s_last = s_last; fa.bias_out = bc.bias3;
   {
     SdcProf prof("b_finish", stream);
     dim3 grid((unsigned)L.nb, (unsigned)batch_b);
@@ -679,20 +677,58 @@ int run_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, i
     SDC_LAUNCH_CHECK();
   }
   // the three parts of B2 / scale (scale: every third float of colstat, stride 3 per column)
-  uint16_t* parts = (uint16_t*)(ws + L.off_parts);
-  int rc = sdc_split_launch(dtype, ws + L.off_b2t, ws + L.off_col + 2, L.ncols * 3, 3, L.ncols, k, L.kp, batch_b,
-                            parts, stream);
+  return sdc_split_launch(dtype, b2t, bc.colstat + 2, L.ncols * 3, 3, L.ncols, k, L.kp, batch_b, bc.parts, stream);
+}
+
+int check_with(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, int64_t batch_a, int64_t batch_b,
+               const void* C, int64_t scb, int64_t scm, int64_t scn, int64_t batch_c, int64_t m, int64_t k, int64_t bs,
+               const Layout& L, const BConsts& bc, const void* bias, int bias_kind, int64_t sbias_b, int64_t sbias_m,
+               int64_t sbias_n, float alpha, float beta, float z, float abs_floor, const float* s_full,
+               const float* s_last, int64_t* result, float* E, float* XN, float* scores_out, const int64_t* goffs,
+               hipStream_t stream);
+
+// The check of sdc_matmul_check, or (goffs set) of sdc_grouped_check: batch_b groups of B over one tall A / C.
+int run_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, int64_t batch_a, const void* B,
+              int64_t sbb, int64_t sbk, int64_t sbn, int64_t batch_b, const void* C, int64_t scb, int64_t scm,
+              int64_t scn, int64_t batch_c, int64_t m, int64_t k, int64_t n, int64_t bs, const void* bias,
+              int bias_kind, int64_t sbias_b, int64_t sbias_m, int64_t sbias_n, float alpha, float beta, float z,
+              float abs_floor, const float* sign_table, int64_t* result, void* workspace, int64_t workspace_bytes,
+              float* scores_out, const int64_t* goffs, hipStream_t stream) {
+  const bool grouped = goffs != nullptr;
+  const Layout L = layout(batch_a, batch_b, m, k, n, bs, grouped);
+  if (batch_c * m * L.nb * 2 > 0xFFFFFFFFll) return SDC_EUNSUPPORTED;     // flat index in 32 bits
+  if (!workspace || workspace_bytes < L.total * (int64_t)sizeof(float) + 256) return SDC_EWORKSPACE;
+  float* ws = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  const float* s_full = sign_table + (bs - 1) * 128;
+  const float* s_last = L.rem ? sign_table + (L.rem - 1) * 128 : s_full;
+  const BConsts bc{ws + L.off_col, ws + L.off_bmax, ws + L.off_bias, (uint16_t*)(ws + L.off_parts)};
+  int rc = stage_b(dtype, B, sbb, sbk, sbn, batch_b, k, n, bs, L, bias, bias_kind, sbias_n, s_full, s_last,
+                   ws + L.off_b2t, ws + L.off_part, bc, stream);
   if (rc != SDC_OK) return rc;
+  return check_with(dtype, A, sab, sam, sak, batch_a, batch_b, C, scb, scm, scn, batch_c, m, k, bs, L, bc, bias,
+                    bias_kind, sbias_b, sbias_m, sbias_n, alpha, beta, z, abs_floor, s_full, s_last, result,
+                    ws + L.off_e, ws + L.off_xn, scores_out, goffs, stream);
+}
+
+// The expected-side GEMM and the scoring pass of a check whose B-side constants are made (bc).
+int check_with(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, int64_t batch_a, int64_t batch_b,
+               const void* C, int64_t scb, int64_t scm, int64_t scn, int64_t batch_c, int64_t m, int64_t k, int64_t bs,
+               const Layout& L, const BConsts& bc, const void* bias, int bias_kind, int64_t sbias_b, int64_t sbias_m,
+               int64_t sbias_n, float alpha, float beta, float z, float abs_floor, const float* s_full,
+               const float* s_last, int64_t* result, float* E, float* XN, float* scores_out, const int64_t* goffs,
+               hipStream_t stream) {
+  const bool grouped = goffs != nullptr;
+  const int64_t nbt = grouped ? 1 : (batch_a > batch_b ? batch_a : batch_b);
   GemmArgs g{};
   g.A = (const uint16_t*)A; g.sab = batch_a > 1 ? sab : 0; g.sam = sam; g.sak = sak;
-  g.B = parts; g.sbb = batch_b > 1 ? 3 * L.ncols * L.kp : 0; g.sbc = L.kp;
+  g.B = bc.parts; g.sbb = batch_b > 1 ? 3 * L.ncols * L.kp : 0; g.sbc = L.kp;
   g.m = m; g.k = k; g.N = L.ncols; g.splits = L.splits;
-  g.E = ws + L.off_e; g.XN = ws + L.off_xn;
+  g.E = E; g.XN = XN;
   const bool c_t = !grouped && scm == 1 && scn != 1 && L.nb < 65536 && batch_c < 65536;   // C read down columns
   g.et = c_t;
   g.prof_name = "train_gemm";
   g.goffs = goffs; g.ngroups = grouped ? batch_b : 0;
-  rc = sdc_gemm_launch(dtype, g, nbt, stream);
+  int rc = sdc_gemm_launch(dtype, g, nbt, stream);
   if (rc != SDC_OK) return rc;
 
   TrainArgs ta{};
@@ -701,8 +737,8 @@ int run_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, i
   ta.cv.vec = scn == 1 && (scm % 8 == 0) && (scb % 8 == 0) && (bs % 8 == 0) && ((uintptr_t)C % 16 == 0);
   ta.k = k; ta.splits = L.splits; ta.nbt = nbt; ta.ncols = L.ncols;
   ta.b_batched = batch_b > 1; ta.e_batched = nbt > 1;
-  ta.E = ws + L.off_e; ta.XN = ws + L.off_xn; ta.colstat = ws + L.off_col; ta.bmaxf = ws + L.off_bmax;
-  ta.bias_kind = bias_kind; ta.bias_vec = ws + L.off_bias; ta.bias_mat = (const uint16_t*)bias;
+  ta.E = E; ta.XN = XN; ta.colstat = bc.colstat; ta.bmaxf = bc.bmaxf;
+  ta.bias_kind = bias_kind; ta.bias_vec = bc.bias3; ta.bias_mat = (const uint16_t*)bias;
   ta.sbias_b = sbias_b; ta.sbias_m = sbias_m; ta.sbias_n = sbias_n;
   ta.alpha = alpha; ta.beta = beta;
   ta.u = dtype == SDC_BF16 ? 1.f / 256.f : 1.f / 2048.f;
@@ -763,6 +799,100 @@ extern "C" int sdc_matmul_check(int dtype, const void* A, int64_t sab, int64_t s
 extern "C" int64_t sdc_grouped_check_workspace(int64_t groups, int64_t rows, int64_t k, int64_t n, int64_t bs) {
   if (groups <= 0 || rows <= 0 || n <= 0 || k <= 0 || bs <= 0) return 0;
   return layout(1, groups, rows, k, n, bs, true).total * (int64_t)sizeof(float) + 256;
+}
+
+// ---- the grouped check's serving form: the experts' constants made once per layer, the per-call check without
+// a B-side stage.  Constants buffer: colstat [groups][2nb][3] | bmaxf [groups][nb] | bias [nb][3] | parts
+// [groups][3 * 2nb][kp] (16-bit), each section 256-byte aligned.
+namespace {
+struct ConstsLayout {
+  int64_t off_col, off_bmax, off_bias, off_parts, total;          // bytes
+};
+ConstsLayout consts_layout(int64_t groups, int64_t k, int64_t n, int64_t bs) {
+  const Layout L = layout(1, groups, 1, k, n, bs, true);
+  auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
+  ConstsLayout c{};
+  int64_t o = 0;
+  c.off_col = o; o += al(groups * L.ncols * 3 * 4);
+  c.off_bmax = o; o += al(groups * L.nb * 4);
+  c.off_bias = o; o += al(3 * L.nb * 4);
+  c.off_parts = o; o += al(groups * 3 * L.ncols * L.kp * 2);
+  c.total = o;
+  return c;
+}
+BConsts consts_at(void* consts, const ConstsLayout& c) {
+  uint8_t* p = (uint8_t*)consts;
+  return BConsts{(float*)(p + c.off_col), (float*)(p + c.off_bmax), (float*)(p + c.off_bias),
+                 (uint16_t*)(p + c.off_parts)};
+}
+}  // namespace
+
+extern "C" int64_t sdc_grouped_constants_bytes(int64_t groups, int64_t k, int64_t n, int64_t bs) {
+  if (groups <= 0 || n <= 0 || k <= 0 || bs <= 0 || bs > 128) return 0;
+  return consts_layout(groups, k, n, bs).total;
+}
+
+// Scratch of the constants' build (the block sums before their split, per-slice statistics).
+extern "C" int64_t sdc_grouped_constants_workspace(int64_t groups, int64_t k, int64_t n, int64_t bs) {
+  if (groups <= 0 || n <= 0 || k <= 0 || bs <= 0) return 0;
+  const Layout L = layout(1, groups, 1, k, n, bs, true);
+  return (L.off_col - L.off_b2t) * (int64_t)sizeof(float) + 512;
+}
+
+extern "C" int sdc_grouped_constants(int dtype, const void* B, int64_t sbg, int64_t sbk, int64_t sbn, int64_t groups,
+                                     int64_t k, int64_t n, int64_t bs, const void* bias, int64_t sbias,
+                                     const float* sign_table, void* consts, int64_t consts_bytes, void* workspace,
+                                     int64_t workspace_bytes, hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
+  if (n < 1 || k < 1 || groups < 1) return SDC_EINVAL;
+  if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EINVAL;
+  if (bs < 1 || bs > 128) return SDC_EUNSUPPORTED;
+  if (!B || !sign_table || !consts) return SDC_EINVAL;
+  if ((uintptr_t)consts % 256) return SDC_EINVAL;
+  const ConstsLayout c = consts_layout(groups, k, n, bs);
+  if (consts_bytes < c.total) return SDC_EWORKSPACE;
+  if (!workspace || workspace_bytes < sdc_grouped_constants_workspace(groups, k, n, bs)) return SDC_EWORKSPACE;
+  const Layout L = layout(1, groups, 1, k, n, bs, true);
+  float* ws = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  const float* s_full = sign_table + (bs - 1) * 128;
+  const float* s_last = L.rem ? sign_table + (L.rem - 1) * 128 : s_full;
+  return stage_b(dtype, B, sbg, sbk, sbn, groups, k, n, bs, L, bias, bias ? 1 : 0, sbias, s_full, s_last, ws,
+                 ws + (L.off_part - L.off_b2t), consts_at(consts, c), stream);
+}
+
+extern "C" int64_t sdc_grouped_check_consts_workspace(int64_t groups, int64_t rows, int64_t k, int64_t n,
+                                                      int64_t bs) {
+  if (groups <= 0 || rows <= 0 || n <= 0 || k <= 0 || bs <= 0) return 0;
+  const Layout L = layout(1, groups, rows, k, n, bs, true);
+  return (L.total - L.off_e) * (int64_t)sizeof(float) + 256;
+}
+
+extern "C" int sdc_grouped_check_consts(int dtype, const void* A, int64_t sam, int64_t sak, const void* consts,
+                                        int64_t groups, const void* C, int64_t scm, int64_t scn, int64_t rows,
+                                        int64_t k, int64_t n, int64_t bs, const int64_t* offs, int has_bias,
+                                        float z, float abs_floor, const float* sign_table, int64_t* results,
+                                        void* workspace, int64_t workspace_bytes, float* scores_out,
+                                        hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
+  if (rows < 1 || n < 1 || k < 1 || groups < 1) return SDC_EINVAL;
+  if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EINVAL;
+  if (bs < 1 || bs > 128) return SDC_EUNSUPPORTED;
+  if (!A || !consts || !C || !offs || !sign_table || !results) return SDC_EINVAL;
+  if ((uintptr_t)consts % 256) return SDC_EINVAL;
+  if (scn != 1 && scm == 1) return SDC_EUNSUPPORTED;
+  const Layout L = layout(1, groups, rows, k, n, bs, true);
+  if (rows * L.nb * 2 > 0xFFFFFFFFll) return SDC_EUNSUPPORTED;
+  if (!workspace || workspace_bytes < sdc_grouped_check_consts_workspace(groups, rows, k, n, bs))
+    return SDC_EWORKSPACE;
+  float* ws = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  const float* s_full = sign_table + (bs - 1) * 128;
+  const float* s_last = L.rem ? sign_table + (L.rem - 1) * 128 : s_full;
+  const ConstsLayout c = consts_layout(groups, k, n, bs);
+  const BConsts bc = consts_at(const_cast<void*>(consts), c);
+  // (the bias's block sums are part of the constants; has_bias says whether the layer has one)
+  return check_with(dtype, A, 0, sam, sak, 1, groups, C, 0, scm, scn, 1, rows, k, bs, L, bc, nullptr, has_bias ? 1 : 0,
+                    0, 0, 0, 1.f, 1.f, z, abs_floor, s_full, s_last, results, ws, ws + (L.off_xn - L.off_e),
+                    scores_out, offs, stream);
 }
 
 extern "C" int sdc_grouped_check(int dtype, const void* A, int64_t sam, int64_t sak, const void* B, int64_t sbg,

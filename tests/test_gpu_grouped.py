@@ -148,3 +148,34 @@ def test_offsets_out_of_order_and_past_the_rows_decode_consistently():
     torch.cuda.synchronize()
     r2 = check_grouped_mm(a, b, out, torch.tensor([40, 70, 120], device="cuda"), epoch=3)
     assert len(r2) == 3
+
+
+@pytest.mark.parametrize("sizes,k,n,dtype,with_bias", [([0, 37, 130, 1, 200], 256, 300, torch.bfloat16, False),
+                                                       ([513, 0, 0, 700], 512, 128, torch.float16, True),
+                                                       ([5] * 20, 96, 40, torch.bfloat16, True)])
+def test_serving_form_equals_the_per_call_check(sizes, k, n, dtype, with_bias):
+    """GroupedChecksums (the experts' constants made once) and grouped_zscores(..., checksums=): the same result
+    rows and every score as the call that makes the constants itself, clean and with a corrupted tile, over two
+    calls in a row on one set of constants, with and without a shared bias (bias added to the outputs)."""
+    from sdcguard_amd.checksum import GroupedChecksums, grouped_zscores, resolve_grouped
+    a, b, out, offs = _grouped(sizes, k, n, dtype=dtype, seed=len(sizes) + 5)
+    bias = None
+    if with_bias:
+        bias = (torch.randn(n, generator=torch.Generator().manual_seed(2)) * 0.3).to(dtype).cuda()
+        out = (out.float() + bias.float()).to(dtype)
+    cs = GroupedChecksums(b, bias)
+    nb = -(-n // min(128, n))
+    bad = out.clone()
+    r0 = sizes[0] + min(sizes[1], 3) if sizes[0] == 0 else 3
+    bad[r0, : min(n, 9)] += 2.0
+    for y in (out, bad, out):
+        z1 = torch.full((sum(sizes), nb, 2), -7.0, device="cuda")
+        z2 = torch.full((sum(sizes), nb, 2), -7.0, device="cuda")
+        s1 = grouped_zscores(a, b, y, offs, bias, scores_out=z1)
+        s2 = grouped_zscores(a, None, y, offs, scores_out=z2, checksums=cs)
+        torch.cuda.synchronize()
+        assert torch.equal(s1.results, s2.results)
+        assert torch.equal(z1, z2)
+        r1, r2 = resolve_grouped(s1), resolve_grouped(s2)
+        assert [(r.ok, r.row, r.col_block) for r in r1] == [(r.ok, r.row, r.col_block) for r in r2]
+    assert not all(r.ok for r in resolve_grouped(grouped_zscores(a, None, bad, offs, checksums=cs)))
