@@ -305,40 +305,54 @@ struct TrainBest {
   int unk = 0;
 };
 
-template <int DT>
-__device__ __forceinline__ void train_pair(const TrainArgs& a, int64_t p, float pl, float sg, float sq, float l1,
-                                           TrainBest& best, int64_t grp = -1) {
-  if (p >= a.cv.npairs) return;
-  int64_t bc, r, jb;
-  pair_index(a.cv, p, bc, r, jb);
-  const bool last = (jb == a.cv.nb - 1) && (a.cv.rem > 0);
-  const float wf = (float)(last ? a.cv.rem : a.cv.bs);
-  const int64_t eb = (a.e_batched && grp < 0) ? bc : 0, bbi = grp >= 0 ? grp : (a.b_batched ? bc : 0);
+// A pair's expected sums and its row's norms, the GEMM's split planes added in split order.  eb: the E / XN batch.
+struct PairE {
+  float e0, e1, asq, asum;
+};
+
+template <int NS = SDC_MAX_SPLITS>
+__device__ __forceinline__ PairE pair_expected(const TrainArgs& a, int64_t eb, int64_t r, int64_t jb) {
   // E planes row-major ([m][ncols]: plain and signed adjacent) or transposed ([ncols][m]: adjacent rows)
   const float* ep = a.et ? a.E + ((eb * a.splits) * a.ncols + 2 * jb) * a.cv.m + r
                          : a.E + ((eb * a.splits) * a.cv.m + r) * a.ncols + 2 * jb;
   const float* xp = a.XN + (eb * a.splits) * 2 * a.cv.m + r;
   const int64_t estep = a.cv.m * a.ncols, xstep = 2 * a.cv.m;
-  float2 ev[SDC_MAX_SPLITS];
-  float xa[SDC_MAX_SPLITS], xb[SDC_MAX_SPLITS];
+  float2 ev[NS];
+  float xa[NS], xb[NS];
   // loads unconditional, so all are in flight at once (a split index past a.splits reads split 0, not added)
 #pragma unroll
-  for (int s = 0; s < SDC_MAX_SPLITS; ++s) {
+  for (int s = 0; s < NS; ++s) {
     const int64_t sc = s < a.splits ? s : 0;
     if (a.et) ev[s] = make_float2(ep[sc * estep], ep[sc * estep + a.cv.m]);
     else ev[s] = *reinterpret_cast<const float2*>(ep + sc * estep);
     xa[s] = xp[sc * xstep];
     xb[s] = xp[sc * xstep + a.cv.m];
   }
-  float e0 = ev[0].x, e1 = ev[0].y, asq = xa[0], asum = xb[0];
+  PairE pe{ev[0].x, ev[0].y, xa[0], xb[0]};
 #pragma unroll
-  for (int s = 1; s < SDC_MAX_SPLITS; ++s)
+  for (int s = 1; s < NS; ++s)
     if (s < a.splits) {
-      e0 += ev[s].x;
-      e1 += ev[s].y;
-      asq += xa[s];
-      asum += xb[s];
+      pe.e0 += ev[s].x;
+      pe.e1 += ev[s].y;
+      pe.asq += xa[s];
+      pe.asum += xb[s];
     }
+  return pe;
+}
+
+// pe: the pair's expected sums when the caller has them (loaded ahead of C), else null
+template <int DT>
+__device__ __forceinline__ void train_pair(const TrainArgs& a, int64_t p, float pl, float sg, float sq, float l1,
+                                           TrainBest& best, int64_t grp = -1, const PairE* pe = nullptr) {
+  if (p >= a.cv.npairs) return;
+  int64_t bc, r, jb;
+  pair_index(a.cv, p, bc, r, jb);
+  const bool last = (jb == a.cv.nb - 1) && (a.cv.rem > 0);
+  const float wf = (float)(last ? a.cv.rem : a.cv.bs);
+  const int64_t eb = (a.e_batched && grp < 0) ? bc : 0, bbi = grp >= 0 ? grp : (a.b_batched ? bc : 0);
+  const PairE ex = pe ? *pe : pair_expected(a, eb, r, jb);
+  float e0 = ex.e0, e1 = ex.e1;
+  const float asq = ex.asq, asum = ex.asum;
   const float* cs = a.colstat + (bbi * a.ncols + 2 * jb) * 3;
   e0 *= cs[2];                                   // the parts were made from B2 / scale
   e1 *= cs[5];
@@ -549,43 +563,86 @@ __device__ __forceinline__ int64_t group_of(const int64_t* offs, int64_t ng, int
 }
 
 __device__ __forceinline__ void flush_group(int64_t* res, const TrainBest& b) {
-  if (b.key > __atomic_load_n(res, __ATOMIC_RELAXED)) atomicMax((unsigned long long*)res, (unsigned long long)b.key);
-  if (b.keyd > __atomic_load_n(res + 1, __ATOMIC_RELAXED))
-    atomicMax((unsigned long long*)(res + 1), (unsigned long long)b.keyd);
+  if (b.key) atomicMax((unsigned long long*)res, (unsigned long long)b.key);
+  if (b.keyd) atomicMax((unsigned long long*)(res + 1), (unsigned long long)b.keyd);
   if (b.unk > 0) atomicAdd((unsigned long long*)(res + 2), (unsigned long long)b.unk);
 }
 
-template <int DT>
+constexpr int GCAP = 1024;                        // group ends a workgroup holds in LDS
+constexpr int GSLOT = 64;                         // groups a workgroup gathers its results for in LDS
+
+// One tile of 64 consecutive pairs per wave, the workgroup's four tiles consecutive (no loop: every wave's loads go
+// out at once).  The group ends go to LDS first (up to GCAP groups; the row-to-group searches then read LDS), each
+// pair's expected sums are loaded before its C.  The waves gather their worst keys and counts per group in LDS (the
+// workgroup's rows span few groups), then one thread per group it touched updates that group's result row: device
+// atomics on one row serialize, so they are made per workgroup, not per wave.  NS: the most split planes added.
+template <int DT, int NS>
 __global__ __launch_bounds__(256) void grouped_score_kernel(TrainArgs a) {
+  __shared__ int64_t offs_s[GCAP];
+  __shared__ unsigned long long s_key[GSLOT], s_keyd[GSLOT];
+  __shared__ int s_unk[GSLOT];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, q = lane & 3;
+  const bool gl = a.ngroups <= GCAP;
+  if (gl)
+    for (int64_t i = t; i < a.ngroups; i += 256) offs_s[i] = a.goffs[i];
+  if (t < GSLOT) {
+    s_key[t] = s_keyd[t] = 0ull;
+    s_unk[t] = 0;
+  }
   uint32_t sg2[16];
   lane_signs<DT>(a.cv, q, sg2);
+  __syncthreads();
+  const int64_t* offs = gl ? offs_s : a.goffs;
   const int64_t tiles = (a.cv.npairs + 63) / 64;
-  for (int64_t tile = (int64_t)blockIdx.x * 4 + w; tile < tiles; tile += (int64_t)gridDim.x * 4) {
+  const int64_t tile = (int64_t)blockIdx.x * 4 + w;
+  // the group of the workgroup's first row: its pairs' groups are that one and the next few
+  const int64_t gfirst = group_of(offs, a.ngroups, ((int64_t)blockIdx.x * 256) / a.cv.nb);
+  TrainBest tb;
+  int64_t grp = -1, g0 = -1, g1 = -1;
+  if (tile < tiles) {
     const int64_t base = tile * 64;
-    float pl, sg, sq, ab;
-    pair_sums<DT>(a.cv, base, lane, sg2, pl, sg, sq, ab);
     const int64_t p = base + q * 16 + (lane >> 2);
     const int64_t pc = p < a.cv.npairs ? p : a.cv.npairs - 1;
-    const int64_t grp = group_of(a.goffs, a.ngroups, pc / a.cv.nb);
-    TrainBest tb;
-    if (grp >= 0) train_pair<DT>(a, p, pl, sg, sq, ab, tb, grp);
+    int64_t bc, r, jb;
+    pair_index(a.cv, pc, bc, r, jb);
+    const PairE pe = pair_expected<NS>(a, 0, r, jb);
+    float pl, sg, sq, ab;
+    pair_sums<DT>(a.cv, base, lane, sg2, pl, sg, sq, ab);
+    grp = group_of(offs, a.ngroups, r);
+    if (grp >= 0) train_pair<DT>(a, p, pl, sg, sq, ab, tb, grp, &pe);
     const int64_t last = base + 63 < a.cv.npairs ? base + 63 : a.cv.npairs - 1;
-    const int64_t g0 = group_of(a.goffs, a.ngroups, base / a.cv.nb);
-    const int64_t g1 = group_of(a.goffs, a.ngroups, last / a.cv.nb);
-    if (g0 == g1) {
-      if (g0 >= 0) {
-        const int64_t key = wave_max_i64(tb.key), keyd = wave_max_i64(tb.keyd);
-        const int unk = wave_sum_i32(tb.unk);
-        if (lane == 0) {
-          TrainBest w1;
-          w1.key = key; w1.keyd = keyd; w1.unk = unk;
-          flush_group(a.result + 3 * g0, w1);
-        }
-      }
-    } else if (grp >= 0) {
-      flush_group(a.result + 3 * grp, tb);
+    g0 = group_of(offs, a.ngroups, base / a.cv.nb);
+    g1 = group_of(offs, a.ngroups, last / a.cv.nb);
+  }
+  // into the workgroup's slots (a group past the slots, or rows before the first group: straight to its row)
+  auto gather = [&](int64_t g, const TrainBest& b) {
+    const int64_t sl = gfirst >= 0 ? g - gfirst : -1;
+    if (sl >= 0 && sl < GSLOT) {
+      if (b.key) atomicMax(&s_key[sl], (unsigned long long)b.key);
+      if (b.keyd) atomicMax(&s_keyd[sl], (unsigned long long)b.keyd);
+      if (b.unk) atomicAdd(&s_unk[sl], b.unk);
+    } else {
+      flush_group(a.result + 3 * g, b);
     }
+  };
+  if (g0 == g1) {
+    if (g0 >= 0) {
+      const int64_t key = wave_max_i64(tb.key), keyd = wave_max_i64(tb.keyd);
+      const int unk = wave_sum_i32(tb.unk);
+      if (lane == 0) {
+        TrainBest w1;
+        w1.key = key; w1.keyd = keyd; w1.unk = unk;
+        gather(g0, w1);
+      }
+    }
+  } else if (grp >= 0) {
+    gather(grp, tb);
+  }
+  __syncthreads();
+  if (t < GSLOT && gfirst >= 0 && gfirst + t < a.ngroups && (s_key[t] | s_keyd[t] | (unsigned long long)s_unk[t])) {
+    TrainBest b;
+    b.key = (int64_t)s_key[t]; b.keyd = (int64_t)s_keyd[t]; b.unk = s_unk[t];
+    flush_group(a.result + 3 * (gfirst + t), b);
   }
 }
 
@@ -754,9 +811,17 @@ int check_with(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, 
   ta.et = c_t;
   if (grouped) {
     const int64_t tiles = sdc_cdiv(ta.cv.npairs, 64);
-    const unsigned grid = (unsigned)(sdc_cdiv(tiles, 4) < 1024 ? sdc_cdiv(tiles, 4) : 1024);
-    if (dtype == SDC_BF16) hipLaunchKernelGGL(grouped_score_kernel<SDC_BF16>, dim3(grid), dim3(256), 0, stream, ta);
-    else hipLaunchKernelGGL(grouped_score_kernel<SDC_FP16>, dim3(grid), dim3(256), 0, stream, ta);
+    if (sdc_cdiv(tiles, 4) > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
+    const unsigned grid = (unsigned)sdc_cdiv(tiles, 4);                // one tile per wave
+    if (ta.splits <= 4) {
+      if (dtype == SDC_BF16) hipLaunchKernelGGL((grouped_score_kernel<SDC_BF16, 4>), dim3(grid), dim3(256), 0, stream, ta);
+      else hipLaunchKernelGGL((grouped_score_kernel<SDC_FP16, 4>), dim3(grid), dim3(256), 0, stream, ta);
+    } else {
+      if (dtype == SDC_BF16)
+        hipLaunchKernelGGL((grouped_score_kernel<SDC_BF16, SDC_MAX_SPLITS>), dim3(grid), dim3(256), 0, stream, ta);
+      else
+        hipLaunchKernelGGL((grouped_score_kernel<SDC_FP16, SDC_MAX_SPLITS>), dim3(grid), dim3(256), 0, stream, ta);
+    }
   } else if (c_t) {
     // C with adjacent rows (y^T): read 512 rows at a time down each column
     ta.cv.vec = (scn % 8 == 0) && (scb % 8 == 0) && ((uintptr_t)C % 16 == 0);

@@ -32,7 +32,9 @@ def _grouped(sizes, k, n, dtype=torch.bfloat16, seed=0, w_scale=None):
 
 
 @pytest.mark.parametrize("sizes,k,n", [([0, 37, 130, 1, 200], 256, 300), ([513, 0, 0, 700], 512, 128),
-                                       ([5] * 20, 96, 40)])
+                                       ([5] * 20, 96, 40),
+                                       # more groups than a workgroup gathers in LDS (one-row groups)
+                                       ([1] * 100 + [0, 300], 64, 40)])
 def test_grouped_scores_match_oracle_per_group(sizes, k, n):
     from sdcguard_amd.checksum import grouped_zscores, resolve_grouped
     a, b, out, offs = _grouped(sizes, k, n, seed=len(sizes))
