@@ -319,9 +319,12 @@ int sdc_layer_constants(int dtype, const void* W, int64_t swn, int64_t n, int64_
  *     (1, m)).  sign_table: as sdc_check_static (epoch 0).
  *   result: int64[4], zeroed by the caller: the worst block's key (bits of z << 32 | row * nb + block), the key with
  *     its noise, the number of wrong blocks (z > z; int8: any differing sum), blocks with a non-finite sum.
+ *   parts_frag (fp8): the parts in sdc_parts_fragments' order (made once with the weight's constants), or NULL: an
+ *     fp8 GEMM whose tiles fill the GPU takes them (the library makes them in the workspace when NULL).
  *   workspace: at least sdc_quant_check_workspace(kind, m, k, n, bs) bytes; scores_out: (m, nb) z or NULL. */
 int64_t sdc_quant_check_workspace(int kind, int64_t m, int64_t k, int64_t n, int64_t bs);
-int sdc_quant_check(int kind, const void* A, int64_t sam, const void* parts, int64_t spc, const float* sa,
+int sdc_quant_check(int kind, const void* A, int64_t sam, const void* parts, int64_t spc,
+                    const void* parts_frag, const float* sa,
                     const void* C, int64_t scm, int64_t scn, int c_dtype, int64_t m, int64_t k, int64_t n, int64_t bs,
                     const float* sign_table, const float* bfrob, const float* bcol, float unit, float nfma, float z,
                     int64_t* result, void* workspace, int64_t workspace_bytes, float* scores_out, hipStream_t stream);

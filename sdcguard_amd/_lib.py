@@ -69,7 +69,7 @@ SIGNATURES = {
     "sdc_layer_constants_workspace": (I64, [I64, I64, I64]),
     "sdc_layer_constants": (I32, [I32, P, I64, I64, I64, I64, P, I64, P, P, I64, P, P, P, P, I64, P]),
     "sdc_quant_check_workspace": (I64, [I32, I64, I64, I64, I64]),
-    "sdc_quant_check": (I32, [I32, P, I64, P, I64, P, P, I64, I64, I32, I64, I64, I64, I64, P, P, P, F32, F32, F32,
+    "sdc_quant_check": (I32, [I32, P, I64, P, I64, P, P, P, I64, I64, I32, I64, I64, I64, I64, P, P, P, F32, F32, F32,
                               P, P, I64, P, P]),
     "sdc_fingerprint3": (I32, [P, I64, I32, I64, P, P]),
     "sdc_fingerprint2": (I32, [P, I64, I32, P, P]),

@@ -9,6 +9,8 @@
 // checksum._matmul_fp32 scales).  The same pass over A adds |a_row|_2^2 and |a_row|_1 (the noise model's row
 // norms), in the workgroups of the first column tile.  Depth is split over workgroups when the tiles alone cannot
 // fill the 256 CUs: each split writes its own plane of E and the scoring kernels add the planes.
+#include <type_traits>
+
 #include "common.h"
 #include "gemm.h"
 #include "mfma_pipe.h"
@@ -46,6 +48,15 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16(u32x2 v) {
     o[2 * w + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[w], 1.0f, true));
   }
   return o;
+}
+
+// a . b + c over the two 16-bit halves of a and b (fp32 accumulation)
+template <int DT>
+__device__ __forceinline__ float pk_dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (DT == SDC_BF16)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
 }
 
 // 8 consecutive (in depth) 16-bit elements at p[kk * sk], or zeros past `lim`
@@ -747,22 +758,31 @@ __global__ __launch_bounds__(64 * RS_WAVES, 1) void rs_gemm_kernel(GemmArgs g) {
 // 4096 worth of products).  The workgroup tile is 128 x 64 over half the depth; the two halves are separate
 // workgroups, each writing its own plane of E (plane h = depth half h), which the scoring pass adds in half order.
 // A's ring per wave is two 16 KB segments (128 rows x 128 bytes; 128 KB for the 4 waves), the next segment loading
-// while the current one is read.  Per step a wave issues 4 of the next segment's 16 A instructions, then the B
-// fragments RB steps ahead.  So at a step's wait, the loads issued after B(st) are (RB - 1) (4 + 6) and, at the
-// first step of a segment, those after the segment's last A piece are the 6 B loads of one step: the wait is
-// vmcnt(30) inside a segment and vmcnt(6) at its first step.
+// while the current one is read.  A segment is 64 depths of a 16-bit A, or 128 of an fp8 A (AT = 1: one byte per
+// element, widened exactly to bf16 after the LDS read; the MFMAs are bf16), so 4 or 8 steps of 16 depths.  Per step
+// a wave issues its share of the next segment's 16 A instructions (APS = 16 / steps), then the B fragments RB
+// steps ahead.  So at a step's wait, the loads issued after B(st) are (RB - 1) (APS + 6) and, at the first step of
+// a segment, those after the segment's last A piece are the 6 B loads of one step: the wait is
+// vmcnt((RB - 1) (APS + 6)) inside a segment and vmcnt(6) at its first step.
+// XN: the workgroups of the first column tile also add up |a_row|_2^2 and |a_row|_1 of their rows (from the A
+// fragments, over their depth half) into plane `half` of g.XN ([half][2][m]).
 // XCD order: XCDs 0-3 take depth half 0 and 4-7 half 1 (each XCD's L2 holds its half of B), row tiles in order.
 #ifndef SDC_TALL_TRF
 #define SDC_TALL_TRF 4
 #endif
 
-template <int DT, int ROLE, int TRF>
+template <int DT, int ROLE, int TRF, int AT, bool XNORM>
 __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_kernel(GemmArgs g) {
-  constexpr int TCF = 2, TR = 32 * TRF, TC = 64, NG = TRF * TCF * 4, RB = 4, NAI = TR / 8, APS = NAI / 4;
+  constexpr int MDT = AT ? SDC_BF16 : DT;       // the MFMAs' type
+  constexpr int SPS = AT ? 8 : 4;               // steps per segment
+  constexpr int SD = 16 * SPS;                  // depths per segment
+  constexpr int ES = AT ? 1 : 2;                // bytes per A element
+  constexpr int TCF = 2, TR = 32 * TRF, TC = 64, RB = 4, NAI = TR / 8, APS = NAI / SPS;
   constexpr int RT_SEGB = TR * 128;             // bytes of A per wave and segment (TR rows x 128 bytes)
   constexpr int RED_BYTES = RS_WAVES * TC * (TR + 4) * 4;       // the epilogue's reduction (below)
   __shared__ __attribute__((aligned(16)))
   uint8_t smem[RS_WAVES * 2 * RT_SEGB > RED_BYTES ? RS_WAVES * 2 * RT_SEGB : RED_BYTES];
+  __shared__ float xred[XNORM ? RS_WAVES : 1][XNORM ? TR : 1][2];
   const int t = threadIdx.x, lane = t & 63;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int r = lane & 31, h = lane >> 5;
@@ -774,18 +794,26 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
   const int64_t half = wid / tiles, tile = wid % tiles;
   const int64_t ct = tile % nct, rt = tile / nct;
   const int64_t r0 = rt * TR, c0 = ct * TC;
-  const int per = (int)(g.k / 64) / (RS_WAVES * (int)g.splits);   // segments per wave
+  const bool do_xn = XNORM && ct == 0;
+  const int per = (int)(g.k / SD) / (RS_WAVES * (int)g.splits);   // segments per wave
   const int seg0 = (int)half * per * RS_WAVES + w * per;
   uint8_t* const abuf = smem + w * 2 * RT_SEGB;
-  int ard[TRF][4];
+  // LDS address of fragment i (rows 32 i + r) at step jj of a segment: the 16-bit depth piece 4 h + jj, or the
+  // fp8 byte offset 64 (jj / 4) + 32 h + 8 (jj % 4) (its 16-byte chunk c, swizzled by the row, and half of it)
+  int ard[TRF][SPS];
 #pragma unroll
   for (int i = 0; i < TRF; ++i)
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
+    for (int jj = 0; jj < SPS; ++jj) {
       const int R = 32 * i + r, rr = R & 7;
-      ard[i][jj] = (R >> 3) * 1024 + 16 * (8 * rr + ((4 * h + jj) ^ rr));
+      if constexpr (AT) {
+        const int o = 64 * (jj / 4) + 32 * h + 8 * (jj % 4);
+        ard[i][jj] = (R >> 3) * 1024 + 16 * (8 * rr + ((o >> 4) ^ rr)) + (o & 15);
+      } else {
+        ard[i][jj] = (R >> 3) * 1024 + 16 * (8 * rr + ((4 * h + jj) ^ rr));
+      }
     }
-  const uint16_t* bq = (const uint16_t*)g.B + (int64_t)(4 * seg0) * 3 * ncf * 512 + 8 * lane;
+  const uint16_t* bq = (const uint16_t*)g.B + (int64_t)(SPS * seg0) * 3 * ncf * 512 + 8 * lane;
   int bf[TCF];
 #pragma unroll
   for (int n = 0; n < TCF; ++n) {
@@ -794,15 +822,15 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
   }
   const int64_t bstep = 3 * ncf * 512;
   const int lastseg = per - 1;
-  const int last = 4 * per - 1;
-  // A's instruction I (0 .. 15) of a segment, lane L: row 8 I + L / 8 (clamped to m - 1), piece (L % 8) ^ (L / 8);
-  // rows as 32-bit element offsets from the tile's first row
-  const uint8_t* abase = (const uint8_t*)g.A + (64 * (int64_t)seg0) * 2 + 16 * ((lane & 7) ^ (lane >> 3));
+  const int last = SPS * per - 1;
+  // A's instruction I (0 .. 15) of a segment, lane L: row 8 I + L / 8 (clamped to m - 1), 16-byte piece
+  // (L % 8) ^ (L / 8) of the row's 128 bytes
+  const uint8_t* abase = (const uint8_t*)g.A + (SD * (int64_t)seg0) * ES + 16 * ((lane & 7) ^ (lane >> 3));
   int64_t arow[NAI];
 #pragma unroll
   for (int I = 0; I < NAI; ++I) {
     const int64_t row = r0 + 8 * I + (lane >> 3);
-    arow[I] = (row < m ? row : m - 1) * g.sam * 2;
+    arow[I] = (row < m ? row : m - 1) * g.sam * ES;
   }
   u32x4 rb[RB][3][TCF];
   auto issue_a4 = [&](int sg, int I0) {
@@ -827,6 +855,17 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
     for (int n = 0; n < TCF; ++n)
       asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(rb[slot][p][n]) : "v"(q + bf[n]));
   };
+  // fragment reads of step jj into fr (fp8: 8 bytes each, widened after the wait).  Each read lands in the very
+  // registers the wait names ("=v" then "+v"): a copy out of an asm read's result before its wait would copy data
+  // that has not arrived.
+  using FragT = typename std::conditional<AT != 0, u32x2, u32x4>::type;
+  auto read_frags = [&](uint32_t L, int jj, FragT* fr) {
+#pragma unroll
+    for (int i = 0; i < TRF; ++i) {
+      if constexpr (AT) asm volatile("ds_read_b64 %0, %1" : "=v"(fr[i]) : "v"(L + (uint32_t)ard[i][jj]));
+      else asm volatile("ds_read_b128 %0, %1" : "=v"(fr[i]) : "v"(L + (uint32_t)ard[i][jj]));
+    }
+  };
   const uint32_t lds0 = (uint32_t)(uintptr_t)abuf;
   f32x16 acc[TRF][TCF];
 #pragma unroll
@@ -835,6 +874,9 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
     for (int n = 0; n < TCF; ++n)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][n][e] = 0.f;
+  float xsq[TRF], xab[TRF];
+#pragma unroll
+  for (int i = 0; i < TRF; ++i) xsq[i] = xab[i] = 0.f;
 #pragma unroll
   for (int q = 0; q < RB; ++q)
 #pragma unroll
@@ -842,72 +884,88 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
 #pragma unroll
       for (int n = 0; n < TCF; ++n) rb[q][p][n] = u32x4{0u, 0u, 0u, 0u};
   if (per > 0) {
-    // prologue: the four steps before the first would issue segment 0's A (a quarter each) and B(0 .. 3)
+    // prologue: segment 0's A and B(0 .. 3) as the steps before the first would issue them (its A shares of those
+    // steps; with 8 steps a segment, the shares of steps 0 .. 3 go out first)
+#pragma unroll
+    for (int q = 0; q < SPS - RB; ++q) issue_a4(0, APS * q);
 #pragma unroll
     for (int q = 0; q < RB; ++q) {
-      issue_a4(0, APS * q);
+      issue_a4(0, APS * (q + (SPS - RB)));
       issue_b(q, q);
     }
     // Each step's 24 MFMAs go in three groups (one part each); the loads are issued between the groups: after the
     // first, the next segment's A pieces and this slot's B fragments of part 0 for RB steps ahead (the MFMAs that
     // read them are issued), then part 1's, then part 2's.  The next step's A fragments are read from LDS in the
     // middle of the second group (inside a segment; the first step of a segment reads its own after the wait).
-    u32x4 fr[2][TRF];
+    FragT fr[2][TRF];
     for (int sg = 0; sg < per; ++sg) {
       const uint32_t L = lds0 + (uint32_t)((sg & 1) * RT_SEGB);
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
+      for (int jj = 0; jj < SPS; ++jj) {
         static_assert(RB == 4, "the wait counts below assume B four steps ahead");
-        const int st = 4 * sg + jj, cur = jj & 1;
+        const int st = SPS * sg + jj, cur = jj & 1, sl = jj & 3;
         if (jj == 0) {
           asm volatile("s_waitcnt vmcnt(6)"
                        : "+v"(rb[0][0][0]), "+v"(rb[0][0][1]), "+v"(rb[0][1][0]), "+v"(rb[0][1][1]),
                          "+v"(rb[0][2][0]), "+v"(rb[0][2][1]));
-#pragma unroll
-          for (int i = 0; i < TRF; ++i)
-            asm volatile("ds_read_b128 %0, %1" : "=v"(fr[0][i]) : "v"(L + (uint32_t)ard[i][0]));
+          read_frags(L, 0, fr[0]);
         } else {
           asm volatile("s_waitcnt vmcnt(%6)"
-                       : "+v"(rb[jj][0][0]), "+v"(rb[jj][0][1]), "+v"(rb[jj][1][0]), "+v"(rb[jj][1][1]),
-                         "+v"(rb[jj][2][0]), "+v"(rb[jj][2][1])
+                       : "+v"(rb[sl][0][0]), "+v"(rb[sl][0][1]), "+v"(rb[sl][1][0]), "+v"(rb[sl][1][1]),
+                         "+v"(rb[sl][2][0]), "+v"(rb[sl][2][1])
                        : "n"((RB - 1) * (APS + 6)));
         }
         if constexpr (TRF == 4)
           asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fr[cur][0]), "+v"(fr[cur][1]), "+v"(fr[cur][2]), "+v"(fr[cur][3]));
         else
           asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fr[cur][0]), "+v"(fr[cur][1]));
+        u32x4 a[TRF];
+#pragma unroll
+        for (int i = 0; i < TRF; ++i) {
+          if constexpr (AT) a[i] = fp8x8_to_bf16(fr[cur][i]);
+          else a[i] = fr[cur][i];
+        }
 #pragma unroll
         for (int i = 0; i < TRF; ++i)
 #pragma unroll
-          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<DT>(fr[cur][i], rb[jj][0][n], acc[i][n]);
+          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<MDT>(a[i], rb[sl][0][n], acc[i][n]);
         __builtin_amdgcn_sched_barrier(0);
         issue_a4(sg + 1, APS * jj);
-        issue_bp(jj, st + RB, 0);
+        issue_bp(sl, st + RB, 0);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < TRF / 2; ++i)
 #pragma unroll
-          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<DT>(fr[cur][i], rb[jj][1][n], acc[i][n]);
+          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<MDT>(a[i], rb[sl][1][n], acc[i][n]);
         __builtin_amdgcn_sched_barrier(0);
-        if (jj < 3) {
-#pragma unroll
-          for (int i = 0; i < TRF; ++i)
-            asm volatile("ds_read_b128 %0, %1" : "=v"(fr[cur ^ 1][i]) : "v"(L + (uint32_t)ard[i][jj + 1]));
-        }
+        if (jj < SPS - 1) read_frags(L, jj + 1, fr[cur ^ 1]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = TRF / 2; i < TRF; ++i)
 #pragma unroll
-          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<DT>(fr[cur][i], rb[jj][1][n], acc[i][n]);
+          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<MDT>(a[i], rb[sl][1][n], acc[i][n]);
         __builtin_amdgcn_sched_barrier(0);
-        issue_bp(jj, st + RB, 1);
+        issue_bp(sl, st + RB, 1);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < TRF; ++i)
 #pragma unroll
-          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<DT>(fr[cur][i], rb[jj][2][n], acc[i][n]);
+          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<MDT>(a[i], rb[sl][2][n], acc[i][n]);
         __builtin_amdgcn_sched_barrier(0);
-        issue_bp(jj, st + RB, 2);
+        issue_bp(sl, st + RB, 2);
+        if (do_xn) {
+          // the rows' norms over this step's 8 depths of each fragment (packed dot products)
+          constexpr uint32_t ONES = MDT == SDC_BF16 ? 0x3F803F80u : 0x3C003C00u;
+#pragma unroll
+          for (int i = 0; i < TRF; ++i) {
+            const uint32_t ww[4] = {a[i].x, a[i].y, a[i].z, a[i].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              xsq[i] = pk_dot2<MDT>(ww[q], ww[q], xsq[i]);
+              xab[i] = pk_dot2<MDT>(ww[q] & 0x7FFF7FFFu, ONES, xab[i]);
+            }
+          }
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -920,7 +978,36 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
                    "+v"(rb[q][2][1]));
     __builtin_amdgcn_sched_barrier(0);
   }
+  if constexpr (XNORM) {
+    if (do_xn) {
+      // the two depth halves of a row (lanes r, r + 32), then the four waves' depth quarters in LDS, in wave order
+#pragma unroll
+      for (int i = 0; i < TRF; ++i) {
+        xsq[i] += __shfl_xor(xsq[i], 32, 64);
+        xab[i] += __shfl_xor(xab[i], 32, 64);
+        if (h == 0) {
+          xred[w][32 * i + r][0] = xsq[i];
+          xred[w][32 * i + r][1] = xab[i];
+        }
+      }
+    }
+  }
   __syncthreads();
+  if constexpr (XNORM) {
+    if (do_xn && t < TR) {
+      float sq = xred[0][t][0], ab = xred[0][t][1];
+#pragma unroll
+      for (int q = 1; q < RS_WAVES; ++q) {
+        sq += xred[q][t][0];
+        ab += xred[q][t][1];
+      }
+      const int64_t row = r0 + t;
+      if (row < m) {
+        g.XN[half * 2 * m + row] = sq;
+        g.XN[half * 2 * m + m + row] = ab;
+      }
+    }
+  }
   // The waves' accumulators meet in LDS column by column ([wave][column][row], rows padded to TR + 4 floats so a
   // wave's 16-byte writes spread over the banks) and are added in wave (depth) order; each store instruction then
   // writes two whole columns of the tile (2 x TR floats, contiguous in the transposed plane).
@@ -1006,11 +1093,13 @@ int sdc_rs_gemm_launch(int dtype, GemmArgs g, int role, hipStream_t stream) {
   return SDC_OK;
 }
 
-// The tall-tile variant: 128 x 64 tiles over depth halves, two planes of E (g.splits must be 2, the depth a
-// multiple of 512).  Returns SDC_EUNSUPPORTED where it does not apply.
+// The tall-tile variant: 128 x 64 tiles over depth halves, two planes of E (g.splits must be 2; the depth a multiple
+// of 512, of 1024 for an fp8 A; A's rows 16-byte aligned); with g.XN set, also A's row norms, one plane per half.
+// dtype SDC_FP8: an fp8 e4m3 A widened to bf16 (B's parts bf16).  Returns SDC_EUNSUPPORTED where it does not apply.
 int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream) {
-  if (dtype != SDC_BF16 && dtype != SDC_FP16) return SDC_EUNSUPPORTED;
-  if (g.splits != 2 || g.sak != 1 || g.k % (2 * RS_KMULT) || g.sam % 8 || ((uintptr_t)g.A | (uintptr_t)g.B) % 16 ||
+  if (dtype != SDC_BF16 && dtype != SDC_FP16 && dtype != SDC_FP8) return SDC_EUNSUPPORTED;
+  const int64_t es = dtype == SDC_FP8 ? 1 : 2, kmul = dtype == SDC_FP8 ? 2 * RS_WAVES * 128 : 2 * RS_KMULT;
+  if (g.splits != 2 || g.sak != 1 || g.k % kmul || (g.sam * es) % 16 || ((uintptr_t)g.A | (uintptr_t)g.B) % 16 ||
       !g.et || g.goffs)
     return SDC_EUNSUPPORTED;
   if (g.m < 1 || g.N < 1) return SDC_EINVAL;
@@ -1018,12 +1107,16 @@ int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream)
   if (blocks > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
   SdcProf prof(g.prof_name ? g.prof_name : "expected_gemm", stream);
   const dim3 grid((unsigned)blocks), block(64 * RS_WAVES);
-  if (role == 1) {
-    if (dtype == SDC_BF16) hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 1, SDC_TALL_TRF>), grid, block, 0, stream, g);
-    else hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_FP16, 1, SDC_TALL_TRF>), grid, block, 0, stream, g);
+  constexpr int T = SDC_TALL_TRF;
+  if (dtype == SDC_FP8) {
+    if (g.XN) hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 3, T, 1, true>), grid, block, 0, stream, g);
+    else hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 3, T, 1, false>), grid, block, 0, stream, g);
+  } else if (role == 1) {
+    if (dtype == SDC_BF16) hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 1, T, 0, false>), grid, block, 0, stream, g);
+    else hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_FP16, 1, T, 0, false>), grid, block, 0, stream, g);
   } else {
-    if (dtype == SDC_BF16) hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 0, SDC_TALL_TRF>), grid, block, 0, stream, g);
-    else hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_FP16, 0, SDC_TALL_TRF>), grid, block, 0, stream, g);
+    if (dtype == SDC_BF16) hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 0, T, 0, false>), grid, block, 0, stream, g);
+    else hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_FP16, 0, T, 0, false>), grid, block, 0, stream, g);
   }
   SDC_LAUNCH_CHECK();
   return SDC_OK;

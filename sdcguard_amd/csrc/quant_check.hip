@@ -16,6 +16,9 @@
 #include "profile.h"
 
 extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
+int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream);
+extern "C" int64_t sdc_parts_fragments_bytes(int64_t N, int64_t k);
+extern "C" int sdc_parts_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out, hipStream_t stream);
 
 namespace {
 
@@ -265,7 +268,8 @@ __device__ __forceinline__ int64_t sum16_i64(int64_t v) {
 
 // FEW: at most SDC_MAX_SPLITS depth splits (the launch picks the instance: each holds only its own way of adding
 // the splits, which measured faster than one kernel holding both)
-template <int KIND, int CT, bool FEW>
+// NS: the most planes the instance adds with all loads in flight (2: the tall-tile GEMM's pair)
+template <int KIND, int CT, bool FEW, int NS = SDC_MAX_SPLITS>
 __global__ __launch_bounds__(256) void quant_tile_kernel(QuantArgs a) {
   constexpr int ES = CT == C_BF16 ? 2 : 4;                  // bytes per C element
   constexpr int NL = 8 * ES / 16;                           // 16-byte loads per row piece (1 or 2)
@@ -307,9 +311,9 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(QuantArgs a) {
     if constexpr (KIND == 0) {
       const int32_t* E = reinterpret_cast<const int32_t*>(a.E);
       if constexpr (FEW) {
-        int32_t hv[SDC_MAX_SPLITS][2], lv[SDC_MAX_SPLITS][2];
+        int32_t hv[NS][2], lv[NS][2];
 #pragma unroll
-        for (int s = 0; s < SDC_MAX_SPLITS; ++s) {
+        for (int s = 0; s < NS; ++s) {
           const int64_t sc = s < a.splits ? s : 0;
           const int32_t* hi = E + ((int64_t)(2 * sc) * a.ncols + 2 * jb) * a.m + rr;
           const int32_t* lo = E + ((int64_t)(2 * sc + 1) * a.ncols + 2 * jb) * a.m + rr;
@@ -317,7 +321,7 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(QuantArgs a) {
           lv[s][0] = lo[0]; lv[s][1] = lo[a.m];
         }
 #pragma unroll
-        for (int s = 0; s < SDC_MAX_SPLITS; ++s)
+        for (int s = 0; s < NS; ++s)
           if (s < a.splits) {
             i0 += 128 * (int64_t)hv[s][0] + (int64_t)lv[s][0];
             i1 += 128 * (int64_t)hv[s][1] + (int64_t)lv[s][1];
@@ -334,9 +338,9 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(QuantArgs a) {
     } else {
       double asq = 0.0;
       if constexpr (FEW) {
-        float ev[SDC_MAX_SPLITS][3];
+        float ev[NS][3];
 #pragma unroll
-        for (int s = 0; s < SDC_MAX_SPLITS; ++s) {
+        for (int s = 0; s < NS; ++s) {
           const int64_t sc = s < a.splits ? s : 0;
           const float* ep = a.E + ((int64_t)sc * a.ncols + 2 * jb) * a.m + rr;
           ev[s][0] = ep[0];
@@ -344,7 +348,7 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(QuantArgs a) {
           ev[s][2] = a.XN[sc * 2 * a.m + rr];
         }
 #pragma unroll
-        for (int s = 0; s < SDC_MAX_SPLITS; ++s)
+        for (int s = 0; s < NS; ++s)
           if (s < a.splits) {
             e0 += (double)ev[s][0];
             e1 += (double)ev[s][1];
@@ -504,7 +508,8 @@ int64_t quant_splits(int kind, int64_t m, int64_t k, int64_t ncols) {
 }
 
 struct QLayout {
-  int64_t nb, rem, ncols, splits, nacc, kpad, off_e, off_xn, off_apad, off_ppad, total;   // offsets in floats
+  int64_t nb, rem, ncols, splits, nacc, kpad, off_e, off_xn, off_apad, off_ppad, off_frag, total;   // in floats
+  bool tall;                       // fp8: the tall-tile register-streamed GEMM (two planes) where the shape allows
 };
 
 QLayout qlayout(int kind, int64_t m, int64_t k, int64_t n, int64_t bs) {
@@ -514,13 +519,18 @@ QLayout qlayout(int kind, int64_t m, int64_t k, int64_t n, int64_t bs) {
   L.ncols = 2 * L.nb;
   L.nacc = kind == 0 ? 2 : 1;
   L.splits = quant_splits(kind, m, kind == 0 ? (k + 1) / 2 : k, L.ncols);
+  // an fp8 GEMM whose 128 x 64 tiles over two depth halves fill the GPU (192 workgroups or more; depth a multiple
+  // of 1024): one pair of E planes, the parts in fragment order
+  L.tall = kind == 1 && k % 1024 == 0 && 2 * sdc_cdiv(m, 128) * sdc_cdiv(L.ncols, 64) >= 192;
+  const int64_t esplits = L.tall && L.splits < 2 ? 2 : L.splits;
   L.kpad = kind == 0 ? (k + 63) / 64 * 64 : 0;           // int8: depth of the zero-padded copies (bytes)
   auto al = [](int64_t x) { return (x + 63) / 64 * 64; };
   int64_t o = 0;
-  L.off_e = o; o += al(L.splits * L.nacc * m * L.ncols);
-  L.off_xn = o; o += al(L.splits * 2 * m);
+  L.off_e = o; o += al(esplits * L.nacc * m * L.ncols);
+  L.off_xn = o; o += al(esplits * 2 * m);
   L.off_apad = o; o += al(sdc_cdiv(m * L.kpad, 4));
   L.off_ppad = o; o += al(sdc_cdiv(2 * L.ncols * L.kpad, 4));
+  L.off_frag = o; o += L.tall ? al(sdc_parts_fragments_bytes(L.ncols, k) / 4) : 0;
   L.total = o;
   return L;
 }
@@ -563,7 +573,8 @@ extern "C" int64_t sdc_quant_check_workspace(int kind, int64_t m, int64_t k, int
   return qlayout(kind, m, k, n, bs).total * (int64_t)sizeof(float) + 256;
 }
 
-extern "C" int sdc_quant_check(int kind, const void* A, int64_t sam, const void* parts, int64_t spc, const float* sa,
+extern "C" int sdc_quant_check(int kind, const void* A, int64_t sam, const void* parts, int64_t spc,
+                               const void* parts_frag, const float* sa,
                                const void* C, int64_t scm, int64_t scn, int c_dtype, int64_t m, int64_t k, int64_t n,
                                int64_t bs, const float* sign_table, const float* bfrob, const float* bcol, float unit,
                                float nfma, float z, int64_t* result, void* workspace, int64_t workspace_bytes,
@@ -610,7 +621,25 @@ extern "C" int sdc_quant_check(int kind, const void* A, int64_t sam, const void*
   g.m = m; g.k = kg; g.N = L.ncols; g.splits = L.splits;
   g.E = ws + L.off_e; g.XN = ws + L.off_xn;
   g.prof_name = kind == 0 ? "quant_gemm_i8" : "quant_gemm_fp8";
-  int rc = sdc_gemm_launch(kind == 0 ? SDC_I8 : SDC_FP8, g, 1, stream);
+  int rc = SDC_EUNSUPPORTED;
+  int64_t splits = L.splits;
+  if (L.tall && tiles && sam % 16 == 0 && (uintptr_t)A % 16 == 0 && spc % 8 == 0 && spc >= k &&
+      (uintptr_t)parts % 16 == 0) {
+    // the parts in fragment order (given, or made here), then the tall-tile GEMM with the row norms
+    const void* frag = parts_frag;
+    if (!frag) {
+      frag = ws + L.off_frag;
+      rc = sdc_parts_fragments(parts, spc, L.ncols, k, ws + L.off_frag, stream);
+      if (rc != SDC_OK) return rc;
+    }
+    GemmArgs gt = g;
+    gt.B = frag;
+    gt.splits = 2;
+    gt.et = 1;
+    rc = sdc_rs_gemm_tall_launch(SDC_FP8, gt, 0, stream);
+    if (rc == SDC_OK) splits = 2;
+  }
+  if (rc == SDC_EUNSUPPORTED) rc = sdc_gemm_launch(kind == 0 ? SDC_I8 : SDC_FP8, g, 1, stream);
   if (rc != SDC_OK) return rc;
 
   QuantArgs qa{};
@@ -618,7 +647,7 @@ extern "C" int sdc_quant_check(int kind, const void* A, int64_t sam, const void*
   qa.m = m; qa.n = n; qa.nb = L.nb; qa.bs = bs; qa.rem = L.rem; qa.npairs = m * L.nb;
   qa.vec = vec;
   qa.s_full = s_full; qa.s_last = s_last;
-  qa.E = ws + L.off_e; qa.XN = ws + L.off_xn; qa.splits = L.splits; qa.ncols = L.ncols;
+  qa.E = ws + L.off_e; qa.XN = ws + L.off_xn; qa.splits = splits; qa.ncols = L.ncols;
   qa.sa = sa; qa.bfrob = bfrob; qa.bcol = bcol;
   qa.unit = unit;
   qa.per_out = (float)(sqrt((double)k) + (nfma > 0.f ? (double)k / (double)nfma : 0.0));
@@ -631,6 +660,9 @@ extern "C" int sdc_quant_check(int kind, const void* A, int64_t sam, const void*
     const bool few = qa.splits <= SDC_MAX_SPLITS;
     if (kind == 0 && few) hipLaunchKernelGGL((quant_tile_kernel<0, C_I32, true>), grid, dim3(256), 0, stream, qa);
     else if (kind == 0) hipLaunchKernelGGL((quant_tile_kernel<0, C_I32, false>), grid, dim3(256), 0, stream, qa);
+    else if (c_dtype == C_F32 && qa.splits <= 2)
+      hipLaunchKernelGGL((quant_tile_kernel<1, C_F32, true, 2>), grid, dim3(256), 0, stream, qa);
+    else if (qa.splits <= 2) hipLaunchKernelGGL((quant_tile_kernel<1, C_BF16, true, 2>), grid, dim3(256), 0, stream, qa);
     else if (c_dtype == C_F32 && few)
       hipLaunchKernelGGL((quant_tile_kernel<1, C_F32, true>), grid, dim3(256), 0, stream, qa);
     else if (c_dtype == C_F32) hipLaunchKernelGGL((quant_tile_kernel<1, C_F32, false>), grid, dim3(256), 0, stream, qa);

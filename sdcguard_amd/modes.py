@@ -104,6 +104,15 @@ class QuantStat:
     scores: Optional[torch.Tensor] = None
 
 
+def _fp8_fragments(P: torch.Tensor, ncols: int, k: int) -> Optional[torch.Tensor]:
+    """The fp8 weight's parts in the register-streamed GEMM's fragment order, made once and kept on the parts tensor
+    (the GEMM whose tiles fill the GPU reads them; None where it cannot: depth not a multiple of 1024)."""
+    if k % 1024 or P.stride(1) % 8 or P.data_ptr() % 16:
+        return None
+    from .linear import _fragments
+    return _fragments(P, ncols, k)
+
+
 def quant_zscores(A: torch.Tensor, consts: QuantChecksums, C: torch.Tensor, *, sa: Optional[torch.Tensor] = None,
                   unit: float = UNIT_FP8, nfma: Optional[int] = NFMA_FP8, z: float = ALARM,
                   scores_out: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
@@ -133,8 +142,10 @@ def quant_zscores(A: torch.Tensor, consts: QuantChecksums, C: torch.Tensor, *, s
     tab = sign_table(C.device)
     P = consts.parts
     Av = A.view(torch.uint8) if kind == 1 else A
+    frag = _fp8_fragments(P, 2 * nb, k) if kind == 1 else None
     rc = L.sdc_quant_check(
-        kind, Av.data_ptr(), Av.stride(0), P.data_ptr(), P.stride(1), None if sa is None else sa.data_ptr(),
+        kind, Av.data_ptr(), Av.stride(0), P.data_ptr(), P.stride(1), None if frag is None else frag.data_ptr(),
+        None if sa is None else sa.data_ptr(),
         C.data_ptr(), C.stride(0), C.stride(1), _C_DTYPES[C.dtype], m, k, consts.n, consts.block, tab.data_ptr(),
         None if consts.bfrob is None else consts.bfrob.data_ptr(), None if consts.bcol is None else consts.bcol.data_ptr(),
         float(unit), float(nfma or 0), float(z), out.data_ptr(), ws.data_ptr(), ws.numel(),

@@ -102,6 +102,43 @@ def test_fp8_scaled_matches_oracle(shape, out):
     assert np.allclose(zg, o["z"], rtol=1e-3, atol=2e-3), np.abs(zg - o["z"]).max()
 
 
+@pytest.mark.parametrize("out", [torch.bfloat16, torch.float32])
+def test_fp8_tall_gemm_matches_oracle(out):
+    """An fp8 layer whose tiles fill the GPU (4096 x 2048 x 14336): the expected side on the tall-tile GEMM (fp8 A
+    widened to bf16 in registers, two depth-half planes, the row norms in the same pass) scores every block as the
+    oracle does, and faults (a dequantized output 4 RMS off, a flipped exponent bit) are located."""
+    from sdcguard_amd import modes
+    m, k, n = 4096, 2048, 14336
+    Aq, Bq, sa, sb, C = _scaled_problem(71, m, k, n, out=out)
+    consts = modes.QuantChecksums.make(Bq, sb)
+    zs = torch.full((m, n // 128), -7.0, device="cuda")
+    res = modes.resolve(modes.quant_zscores(Aq, consts, C, sa=sa, scores_out=zs))
+    assert res["wrong_blocks"] == 0 and res["worst_z"] < 1.0, res
+    vals = quant.fp8_e4m3_values()
+    A = vals[Aq.view(torch.uint8).cpu().numpy()]
+    B = vals[Bq.view(torch.uint8).cpu().numpy()]
+    o = quant.fp8_judge(A, B, sa.double().cpu().numpy(), sb.double().cpu().numpy(), C.double().cpu().numpy(),
+                        quant.patterns(1), c_bf16=out == torch.bfloat16)
+    zg = zs.cpu().numpy()
+    assert np.allclose(zg, o["z"], rtol=1e-3, atol=2e-3), np.abs(zg - o["z"]).max()
+    print(f"fp8 {m}x{k}x{n} ({out}): max |dz| against the oracle {float(np.abs(zg - o['z']).max()):.2e}")
+    rng = np.random.default_rng(9)
+    for t in range(4):
+        i, j = int(rng.integers(m)), int(rng.integers(n))
+        c = C.clone()
+        blk = c[i, (j // 128) * 128:(j // 128 + 1) * 128].float()
+        if t % 2:
+            c[i, j] = (c[i, j].float() + 4 * blk.pow(2).mean().sqrt()).to(out)
+        elif out == torch.float32:
+            v = c[i:i + 1, j].view(torch.int32)
+            v ^= (1 << 30)
+        else:
+            v = c[i:i + 1, j].view(torch.int16)
+            v ^= (1 << 14)
+        res = modes.resolve(modes.quant_zscores(Aq, consts, c, sa=sa))
+        assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (i, j // 128), (t, i, j, res)
+
+
 def test_fp8_scaled_faults_located():
     from sdcguard_amd import modes
     Aq, Bq, sa, sb, C = _scaled_problem(9, 64, 512, 512)
