@@ -771,7 +771,9 @@ __global__ __launch_bounds__(64 * RS_WAVES, 1) void rs_gemm_kernel(GemmArgs g) {
 #define SDC_TALL_TRF 4
 #endif
 
-template <int DT, int ROLE, int TRF, int AT, bool XNORM>
+constexpr int GSCAN = 1024;                       // groups the grouped tall GEMM takes
+
+template <int DT, int ROLE, int TRF, int AT, bool XNORM, bool GROUPED = false>
 __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_kernel(GemmArgs g) {
   constexpr int MDT = AT ? SDC_BF16 : DT;       // the MFMAs' type
   constexpr int SPS = AT ? 8 : 4;               // steps per segment
@@ -788,12 +790,50 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
   const int r = lane & 31, h = lane >> 5;
   const int64_t N = g.N, m = g.m;
   const int64_t nct = sdc_cdiv(N, TC), ncf = sdc_cdiv(N, 32);
-  const int64_t tiles = sdc_cdiv(m, TR) * nct;
   const int64_t G = (int64_t)gridDim.x, b = blockIdx.x;
   const int64_t wid = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
-  const int64_t half = wid / tiles, tile = wid % tiles;
-  const int64_t ct = tile % nct, rt = tile / nct;
-  const int64_t r0 = rt * TR, c0 = ct * TC;
+  int64_t tiles, half, r0, rend, grp = 0;
+  if constexpr (GROUPED) {
+    // grouped rows (g.goffs: the groups' cumulative ends): a row tile never crosses a group, so group q has
+    // ceil(rows_q / TR) row tiles; their running count comes from the ends in LDS (a scan over the groups), and
+    // the grid covers (ceil(m / TR) + groups) row tiles per column tile and half -- workgroups past the last exit
+    __shared__ int64_t gend[GSCAN], gtile[GSCAN];
+    const int ng = (int)g.ngroups;
+    for (int q = t; q < ng; q += 64 * RS_WAVES) {
+      const int64_t e = min(max(g.goffs[q], (int64_t)0), m), s0 = q ? min(max(g.goffs[q - 1], (int64_t)0), m) : 0;
+      gend[q] = e;
+      gtile[q] = e > s0 ? sdc_cdiv(e - s0, TR) : 0;
+    }
+    __syncthreads();
+    if (t == 0)
+      for (int q = 1; q < ng; ++q) gtile[q] += gtile[q - 1];    // (inclusive running count, 1024 groups at most)
+    __syncthreads();
+    const int64_t rtiles = sdc_cdiv(m, TR) + g.ngroups;
+    tiles = rtiles * nct;
+    half = wid / tiles;
+    const int64_t tile = wid % tiles, rt = tile / nct;
+    if (rt >= gtile[ng - 1] || half >= g.splits) return;
+    int lo = 0, hi = ng - 1;                                     // first group whose running count exceeds rt
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (gtile[mid] > rt) hi = mid;
+      else lo = mid + 1;
+    }
+    grp = lo;
+    const int64_t gs = grp ? gend[grp - 1] : 0, lt = rt - (grp ? gtile[grp - 1] : 0);
+    r0 = gs + lt * TR;
+    rend = gend[grp];
+    tiles = tile;                                                // (reused below as this tile's index)
+  } else {
+    tiles = sdc_cdiv(m, TR) * nct;
+    half = wid / tiles;
+    const int64_t rt = (wid % tiles) / nct;
+    r0 = rt * TR;
+    rend = m;
+    tiles = wid % tiles;
+  }
+  const int64_t ct = tiles % nct;
+  const int64_t c0 = ct * TC;
   const bool do_xn = XNORM && ct == 0;
   const int per = (int)(g.k / SD) / (RS_WAVES * (int)g.splits);   // segments per wave
   const int seg0 = (int)half * per * RS_WAVES + w * per;
@@ -813,7 +853,7 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
         ard[i][jj] = (R >> 3) * 1024 + 16 * (8 * rr + ((4 * h + jj) ^ rr));
       }
     }
-  const uint16_t* bq = (const uint16_t*)g.B + (int64_t)(SPS * seg0) * 3 * ncf * 512 + 8 * lane;
+  const uint16_t* bq = (const uint16_t*)g.B + grp * g.sbb + (int64_t)(SPS * seg0) * 3 * ncf * 512 + 8 * lane;
   int bf[TCF];
 #pragma unroll
   for (int n = 0; n < TCF; ++n) {
@@ -830,7 +870,7 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
 #pragma unroll
   for (int I = 0; I < NAI; ++I) {
     const int64_t row = r0 + 8 * I + (lane >> 3);
-    arow[I] = (row < m ? row : m - 1) * g.sam * ES;
+    arow[I] = (row < rend ? row : rend - 1) * g.sam * ES;
   }
   u32x4 rb[RB][3][TCF];
   auto issue_a4 = [&](int sg, int I0) {
@@ -1002,7 +1042,7 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
         ab += xred[q][t][1];
       }
       const int64_t row = r0 + t;
-      if (row < m) {
+      if (row < rend) {
         g.XN[half * 2 * m + row] = sq;
         g.XN[half * 2 * m + m + row] = ab;
       }
@@ -1038,12 +1078,12 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
     const int64_t col = c0 + cl;
     if (col < N) {
       float* Ec = Eh + col * me;
-      if (row + 4 <= m && (me % 4) == 0) {
+      if (row + 4 <= rend && (me % 4) == 0 && (row % 4) == 0) {
         *reinterpret_cast<f32x4*>(Ec + row) = v;
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (row + e < m) Ec[row + e] = v[e];
+          if (row + e < rend) Ec[row + e] = v[e];
       }
     }
   }
@@ -1053,9 +1093,11 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
 // lane l of fragment (step s, part p, column fragment f) is part p, column 32 f + l % 32 (zero past N), depth
 // 64 (s / 4) + 32 (l / 32) + 8 (s % 4) + e.  One thread per 16-byte piece.
 __global__ __launch_bounds__(256) void parts_frag_kernel(const uint16_t* parts, int64_t spc, int64_t N, int64_t k,
-                                                         uint16_t* out) {
+                                                         uint16_t* out, int64_t sgp) {
   const int64_t ncf = sdc_cdiv(N, 32), nst = k / 16;
   const int64_t total = nst * 3 * ncf * 64;
+  parts += blockIdx.y * sgp;                      // group blockIdx.y: its parts, and its fragments after the last's
+  out += blockIdx.y * total * 8;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
     const int lane = (int)(i % 64);
     const int64_t fr = i / 64, f = fr % ncf, p = (fr / ncf) % 3, s = fr / (3 * ncf);
@@ -1093,22 +1135,32 @@ int sdc_rs_gemm_launch(int dtype, GemmArgs g, int role, hipStream_t stream) {
   return SDC_OK;
 }
 
-// The tall-tile variant: 128 x 64 tiles over depth halves, two planes of E (g.splits must be 2; the depth a multiple
-// of 512, of 1024 for an fp8 A; A's rows 16-byte aligned); with g.XN set, also A's row norms, one plane per half.
-// dtype SDC_FP8: an fp8 e4m3 A widened to bf16 (B's parts bf16).  Returns SDC_EUNSUPPORTED where it does not apply.
+// The tall-tile variant: 128 x 64 tiles over g.splits (1 or 2) depth parts, one plane of E per part (the depth a
+// multiple of 256 splits, of 512 splits for an fp8 A; A's rows 16-byte aligned); with g.XN set, also A's row norms,
+// one plane per part.  dtype SDC_FP8: an fp8 e4m3 A widened to bf16 (B's parts bf16).  With g.goffs (16-bit A
+// only): rows grouped by the groups' cumulative ends, group q's fragments at g.B + q g.sbb, row norms always.
+// Returns SDC_EUNSUPPORTED where it does not apply.
 int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream) {
   if (dtype != SDC_BF16 && dtype != SDC_FP16 && dtype != SDC_FP8) return SDC_EUNSUPPORTED;
-  const int64_t es = dtype == SDC_FP8 ? 1 : 2, kmul = dtype == SDC_FP8 ? 2 * RS_WAVES * 128 : 2 * RS_KMULT;
-  if (g.splits != 2 || g.sak != 1 || g.k % kmul || (g.sam * es) % 16 || ((uintptr_t)g.A | (uintptr_t)g.B) % 16 ||
-      !g.et || g.goffs)
+  const int64_t es = dtype == SDC_FP8 ? 1 : 2, kmul = (dtype == SDC_FP8 ? RS_WAVES * 128 : RS_KMULT) * g.splits;
+  if ((g.splits != 1 && g.splits != 2) || g.sak != 1 || g.k % kmul || (g.sam * es) % 16 ||
+      ((uintptr_t)g.A | (uintptr_t)g.B) % 16 || !g.et)
     return SDC_EUNSUPPORTED;
+  if (g.goffs && (dtype == SDC_FP8 || g.ngroups < 1 || g.ngroups > GSCAN || g.sbb % 8)) return SDC_EUNSUPPORTED;
   if (g.m < 1 || g.N < 1) return SDC_EINVAL;
-  const int64_t blocks = 2 * sdc_cdiv(g.m, 32 * SDC_TALL_TRF) * sdc_cdiv(g.N, 64);
+  const int64_t rtiles = sdc_cdiv(g.m, 32 * SDC_TALL_TRF) + (g.goffs ? g.ngroups : 0);
+  const int64_t blocks = g.splits * rtiles * sdc_cdiv(g.N, 64);
   if (blocks > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
   SdcProf prof(g.prof_name ? g.prof_name : "expected_gemm", stream);
   const dim3 grid((unsigned)blocks), block(64 * RS_WAVES);
   constexpr int T = SDC_TALL_TRF;
-  if (dtype == SDC_FP8) {
+  if (g.goffs) {
+    // (grouped: 16-bit A with its row norms)
+    if (dtype == SDC_BF16)
+      hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 4, T, 0, true, true>), grid, block, 0, stream, g);
+    else
+      hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_FP16, 4, T, 0, true, true>), grid, block, 0, stream, g);
+  } else if (dtype == SDC_FP8) {
     if (g.XN) hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 3, T, 1, true>), grid, block, 0, stream, g);
     else hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 3, T, 1, false>), grid, block, 0, stream, g);
   } else if (role == 1) {
@@ -1128,19 +1180,27 @@ extern "C" int64_t sdc_parts_fragments_bytes(int64_t N, int64_t k) {
   return 3 * sdc_cdiv(N, 32) * 32 * k * 2;
 }
 
-// 3 x N parts [3][N][spc] (16-bit, k-contiguous per column) -> fragment order for the register-streamed GEMM.
-extern "C" int sdc_parts_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out,
-                                   hipStream_t stream) {
-  SDC_CLEAR_ERRORS();
-  if (!parts || !out || N < 1 || k < 64 || k % 64 || spc % 8 || spc < k || ((uintptr_t)parts | (uintptr_t)out) % 16)
+// `groups` sets of 3 x N parts (set q at parts + q sgp elements, each [3][N][spc]: 16-bit, k-contiguous per column)
+// -> fragment order for the register-streamed GEMM, set q's fragments at out + q sdc_parts_fragments_bytes(N, k).
+int sdc_parts_fragments_sets(const void* parts, int64_t spc, int64_t sgp, int64_t groups, int64_t N, int64_t k,
+                             void* out, hipStream_t stream) {
+  if (!parts || !out || N < 1 || k < 64 || k % 64 || spc % 8 || spc < k || sgp % 8 || groups < 1 ||
+      groups > 65535 || ((uintptr_t)parts | (uintptr_t)out) % 16)
     return SDC_EINVAL;
   const int64_t total = (k / 16) * 3 * sdc_cdiv(N, 32) * 64;
   const int64_t blocks = sdc_cdiv(total, 256) < 4096 ? sdc_cdiv(total, 256) : 4096;
   SdcProf prof("parts_frag", stream);
-  hipLaunchKernelGGL(parts_frag_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint16_t*)parts, spc, N, k,
-                     (uint16_t*)out);
+  hipLaunchKernelGGL(parts_frag_kernel, dim3((unsigned)blocks, (unsigned)groups), dim3(256), 0, stream,
+                     (const uint16_t*)parts, spc, N, k, (uint16_t*)out, sgp);
   SDC_LAUNCH_CHECK();
   return SDC_OK;
+}
+
+// 3 x N parts [3][N][spc] (16-bit, k-contiguous per column) -> fragment order for the register-streamed GEMM.
+extern "C" int sdc_parts_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out,
+                                   hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
+  return sdc_parts_fragments_sets(parts, spc, 0, 1, N, k, out, stream);
 }
 
 // Split of the depth so that tiles x splits fill the GPU (one workgroup per CU), in multiples of the stage depth.

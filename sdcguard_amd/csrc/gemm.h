@@ -28,6 +28,17 @@ struct GemmArgs {
 // E and XN for `batches` batches.
 int sdc_gemm_launch(int dtype, GemmArgs g, int64_t batches, hipStream_t stream);
 
+// Register-streamed GEMMs over 16-bit parts in fragment order (E transposed): 64 x 64 tiles, one plane of E; and
+// 128 x 64 tiles over g.splits depth parts (fp8 or 16-bit A, optional row norms, grouped rows).  Both return
+// SDC_EUNSUPPORTED, launching nothing, where their shape or alignment rules do not hold.
+int sdc_rs_gemm_launch(int dtype, GemmArgs g, int role, hipStream_t stream);
+int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream);
+extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
+extern "C" int64_t sdc_parts_fragments_bytes(int64_t N, int64_t k);
+extern "C" int sdc_parts_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out, hipStream_t stream);
+int sdc_parts_fragments_sets(const void* parts, int64_t spc, int64_t sgp, int64_t groups, int64_t N, int64_t k,
+                             void* out, hipStream_t stream);
+
 // parts[batch][3 * ncols][kp] from B2T[batch][ncols][k] (fp32), each column divided by
 // scale[batch * sscb + col * scale_stride] first (null: 1); depth kp >= k padded with zeros.
 int sdc_split_launch(int dtype, const float* B2T, const float* scale, int64_t sscb, int64_t scale_stride,

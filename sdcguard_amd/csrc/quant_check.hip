@@ -15,10 +15,6 @@
 #include "gemm.h"
 #include "profile.h"
 
-extern "C" int64_t sdc_expected_splits(int64_t m, int64_t k, int64_t ncols);
-int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream);
-extern "C" int64_t sdc_parts_fragments_bytes(int64_t N, int64_t k);
-extern "C" int sdc_parts_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out, hipStream_t stream);
 
 namespace {
 

@@ -649,8 +649,16 @@ __global__ __launch_bounds__(256) void grouped_score_kernel(TrainArgs a) {
 struct Layout {
   int64_t nb, rem, ncols, nkc, splits, nbt;
   int64_t kp;                      // depth pitch of the parts (k rounded up to 8: 16-byte aligned columns)
-  int64_t off_b2t, off_part, off_col, off_bmax, off_bias, off_parts, off_e, off_xn, total;
+  int64_t esplits;                 // E and XN planes the workspace holds (the grouped tall GEMM's two at least)
+  int64_t fragb;                   // bytes of one group's parts in fragment order (grouped, depth a multiple of 512)
+  int64_t off_b2t, off_part, off_col, off_bmax, off_bias, off_parts, off_frag, off_e, off_xn, total;
 };
+
+// The grouped check's expected side runs on the tall-tile GEMM (over 1 or 2 depth parts) where the depth allows it.
+constexpr int64_t TALL_K = 512;
+#ifndef SDC_GROUPED_TALL_SPLITS
+#define SDC_GROUPED_TALL_SPLITS 2
+#endif
 
 // grouped: B has batch_b groups but A, C, E and XN are one tall matrix (rows grouped by offsets)
 Layout layout(int64_t batch_a, int64_t batch_b, int64_t m, int64_t k, int64_t n, int64_t bs, bool grouped = false) {
@@ -670,8 +678,11 @@ Layout layout(int64_t batch_a, int64_t batch_b, int64_t m, int64_t k, int64_t n,
   L.off_bmax = o; o += al(batch_b * L.nb);
   L.off_bias = o; o += al(3 * L.nb);
   L.off_parts = o; o += al((batch_b * 3 * L.ncols * L.kp + 1) / 2);      // 16-bit parts, two per float
-  L.off_e = o; o += al(L.nbt * L.splits * m * L.ncols);
-  L.off_xn = o; o += al(L.nbt * L.splits * 2 * m);
+  L.fragb = grouped && k % TALL_K == 0 ? sdc_parts_fragments_bytes(L.ncols, k) : 0;
+  L.off_frag = o; o += al(batch_b * L.fragb / 4);
+  L.esplits = L.fragb ? std::max<int64_t>(L.splits, 2) : L.splits;
+  L.off_e = o; o += al(L.nbt * L.esplits * m * L.ncols);
+  L.off_xn = o; o += al(L.nbt * L.esplits * 2 * m);
   L.total = o;
   return L;
 }
@@ -693,6 +704,7 @@ struct BConsts {
   float* bmaxf;                    // [bB][nb]
   float* bias3;                    // [nb][3]
   uint16_t* parts;                 // [bB][3 * 2nb][kp]
+  uint16_t* frag;                  // the parts in fragment order, [bB][fragb / 2] (grouped), or null
 };
 
 // The B side: block sums of B and their statistics (b_stage, b_finish), the bias's block sums, and the three parts
@@ -734,7 +746,10 @@ int stage_b(int dtype, const void* B, int64_t sbb, int64_t sbk, int64_t sbn, int
     SDC_LAUNCH_CHECK();
   }
   // the three parts of B2 / scale (scale: every third float of colstat, stride 3 per column)
-  return sdc_split_launch(dtype, b2t, bc.colstat + 2, L.ncols * 3, 3, L.ncols, k, L.kp, batch_b, bc.parts, stream);
+  int rc = sdc_split_launch(dtype, b2t, bc.colstat + 2, L.ncols * 3, 3, L.ncols, k, L.kp, batch_b, bc.parts, stream);
+  if (rc != SDC_OK || !bc.frag) return rc;
+  // and, for the tall-tile GEMM, in its fragment order (one set per group)
+  return sdc_parts_fragments_sets(bc.parts, L.kp, 3 * L.ncols * L.kp, batch_b, L.ncols, k, bc.frag, stream);
 }
 
 int check_with(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, int64_t batch_a, int64_t batch_b,
@@ -758,7 +773,8 @@ int run_check(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, i
   float* ws = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
   const float* s_full = sign_table + (bs - 1) * 128;
   const float* s_last = L.rem ? sign_table + (L.rem - 1) * 128 : s_full;
-  const BConsts bc{ws + L.off_col, ws + L.off_bmax, ws + L.off_bias, (uint16_t*)(ws + L.off_parts)};
+  const BConsts bc{ws + L.off_col, ws + L.off_bmax, ws + L.off_bias, (uint16_t*)(ws + L.off_parts),
+                   L.fragb ? (uint16_t*)(ws + L.off_frag) : nullptr};
   int rc = stage_b(dtype, B, sbb, sbk, sbn, batch_b, k, n, bs, L, bias, bias_kind, sbias_n, s_full, s_last,
                    ws + L.off_b2t, ws + L.off_part, bc, stream);
   if (rc != SDC_OK) return rc;
@@ -785,14 +801,28 @@ int check_with(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, 
   g.et = c_t;
   g.prof_name = "train_gemm";
   g.goffs = goffs; g.ngroups = grouped ? batch_b : 0;
-  int rc = sdc_gemm_launch(dtype, g, nbt, stream);
+  int rc = SDC_EUNSUPPORTED;
+  int64_t splits = L.splits;
+  bool e_t = c_t;
+  if (grouped && bc.frag) {
+    // the tall-tile GEMM over two depth halves: E transposed, the groups' fragments L.fragb bytes apart
+    GemmArgs gt = g;
+    gt.B = bc.frag; gt.sbb = L.fragb / 2; gt.sbc = 0;
+    gt.splits = SDC_GROUPED_TALL_SPLITS; gt.et = 1;
+    rc = sdc_rs_gemm_tall_launch(dtype, gt, 0, stream);
+    if (rc == SDC_OK) {
+      splits = gt.splits;
+      e_t = true;
+    }
+  }
+  if (rc == SDC_EUNSUPPORTED) rc = sdc_gemm_launch(dtype, g, nbt, stream);
   if (rc != SDC_OK) return rc;
 
   TrainArgs ta{};
   ta.cv.y = (const uint16_t*)C; ta.cv.sb = scb; ta.cv.sm = scm; ta.cv.sn = scn; ta.cv.m = m; ta.cv.nb = L.nb;
   ta.cv.bs = bs; ta.cv.rem = L.rem; ta.cv.npairs = batch_c * m * L.nb; ta.cv.s_full = s_full; ta.cv.s_last = s_last;
   ta.cv.vec = scn == 1 && (scm % 8 == 0) && (scb % 8 == 0) && (bs % 8 == 0) && ((uintptr_t)C % 16 == 0);
-  ta.k = k; ta.splits = L.splits; ta.nbt = nbt; ta.ncols = L.ncols;
+  ta.k = k; ta.splits = splits; ta.nbt = nbt; ta.ncols = L.ncols;
   ta.b_batched = batch_b > 1; ta.e_batched = nbt > 1;
   ta.E = E; ta.XN = XN; ta.colstat = bc.colstat; ta.bmaxf = bc.bmaxf;
   ta.bias_kind = bias_kind; ta.bias_vec = bc.bias3; ta.bias_mat = (const uint16_t*)bias;
@@ -808,7 +838,7 @@ int check_with(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, 
   ta.result = result; ta.zdump = scores_out;
   ta.goffs = goffs; ta.ngroups = grouped ? batch_b : 0;
   SdcProf prof("train_score", stream);
-  ta.et = c_t;
+  ta.et = e_t;
   if (grouped) {
     const int64_t tiles = sdc_cdiv(ta.cv.npairs, 64);
     if (sdc_cdiv(tiles, 4) > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
@@ -871,7 +901,7 @@ extern "C" int64_t sdc_grouped_check_workspace(int64_t groups, int64_t rows, int
 // [groups][3 * 2nb][kp] (16-bit), each section 256-byte aligned.
 namespace {
 struct ConstsLayout {
-  int64_t off_col, off_bmax, off_bias, off_parts, total;          // bytes
+  int64_t off_col, off_bmax, off_bias, off_parts, off_frag, total;          // bytes
 };
 ConstsLayout consts_layout(int64_t groups, int64_t k, int64_t n, int64_t bs) {
   const Layout L = layout(1, groups, 1, k, n, bs, true);
@@ -882,13 +912,14 @@ ConstsLayout consts_layout(int64_t groups, int64_t k, int64_t n, int64_t bs) {
   c.off_bmax = o; o += al(groups * L.nb * 4);
   c.off_bias = o; o += al(3 * L.nb * 4);
   c.off_parts = o; o += al(groups * 3 * L.ncols * L.kp * 2);
+  c.off_frag = o; o += al(groups * L.fragb);                      // (none where the depth is not a multiple of 512)
   c.total = o;
   return c;
 }
 BConsts consts_at(void* consts, const ConstsLayout& c) {
   uint8_t* p = (uint8_t*)consts;
   return BConsts{(float*)(p + c.off_col), (float*)(p + c.off_bmax), (float*)(p + c.off_bias),
-                 (uint16_t*)(p + c.off_parts)};
+                 (uint16_t*)(p + c.off_parts), c.total > c.off_frag ? (uint16_t*)(p + c.off_frag) : nullptr};
 }
 }  // namespace
 
