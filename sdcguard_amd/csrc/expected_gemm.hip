@@ -790,7 +790,11 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
   const int r = lane & 31, h = lane >> 5;
   const int64_t N = g.N, m = g.m;
   const int64_t nct = sdc_cdiv(N, TC), ncf = sdc_cdiv(N, 32);
-  const int64_t G = (int64_t)gridDim.x, b = blockIdx.x;
+  const int64_t G = (int64_t)gridDim.x - g.xf_blocks, b = blockIdx.x;
+  if (b >= G) {
+    xfinish_block(g.xf, b - G, t);                // (a spare workgroup: the x pass's finishing step)
+    return;
+  }
   const int64_t wid = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
   int64_t tiles, half, r0, rend, grp = 0;
   if constexpr (GROUPED) {
@@ -1149,7 +1153,8 @@ int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream)
   if (g.goffs && (dtype == SDC_FP8 || g.ngroups < 1 || g.ngroups > GSCAN || g.sbb % 8)) return SDC_EUNSUPPORTED;
   if (g.m < 1 || g.N < 1) return SDC_EINVAL;
   const int64_t rtiles = sdc_cdiv(g.m, 32 * SDC_TALL_TRF) + (g.goffs ? g.ngroups : 0);
-  const int64_t blocks = g.splits * rtiles * sdc_cdiv(g.N, 64);
+  if (g.xf_blocks < 0 || (g.xf_blocks && (g.goffs || dtype == SDC_FP8))) return SDC_EINVAL;
+  const int64_t blocks = g.splits * rtiles * sdc_cdiv(g.N, 64) + g.xf_blocks;
   if (blocks > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
   SdcProf prof(g.prof_name ? g.prof_name : "expected_gemm", stream);
   const dim3 grid((unsigned)blocks), block(64 * RS_WAVES);

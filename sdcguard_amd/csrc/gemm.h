@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "xfinish.h"
+
 struct GemmArgs {
   const uint16_t* A;            // bf16/fp16 rows; element (batch, row, kk) at A[batch * sab + row * sam + kk * sak]
   int64_t sab, sam, sak;
@@ -23,6 +25,11 @@ struct GemmArgs {
   // takes every depth slice of some row tiles (its rows' 128-byte lines stay in its L2 between the two stages that
   // read their halves: for a tall A read once, whose parts fit one L2 whole)
   int rows_per_xcd;
+  // (the tall-tile kernel) the grid's last xf_blocks workgroups run the x pass's finishing step for row blocks
+  // 0 .. xf_blocks - 1 instead of tiles: sdc_linear_check's row GEMM leaves CUs idle, and xfinish has no other use
+  // for them
+  XStageArgs xf;
+  int xf_blocks;
 };
 
 // E and XN for `batches` batches.

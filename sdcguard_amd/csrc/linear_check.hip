@@ -29,6 +29,7 @@
 #include "judge.h"
 #include "profile.h"
 #include "streams.h"
+#include "xfinish.h"
 
 
 namespace {
@@ -36,8 +37,6 @@ namespace {
 constexpr int BS = 128;            // block width of both checks
 constexpr int RS_K = 256;          // depth multiple of the register-streamed GEMM (expected_gemm.hip)
 constexpr int XK = 128;            // depth per xstage workgroup
-constexpr int NXS = 5;             // partial stats per (depth chunk, row block): sq0, sq1, max0, max1, max|x|
-constexpr int RST = 8;             // final stats per row block: the NXS above, then the sum of its sign pattern
 #ifndef SDC_YTPW
 #define SDC_YTPW 1
 #endif
@@ -65,19 +64,6 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 // ---------------------------------------------------------------------------------------- 1. x block sums
-struct XStageArgs {
-  const uint16_t* x;
-  int64_t sxm, m, k, kp, mb, rem, nkc;
-  int frag;                        // parts in the register-streamed GEMM's fragment order (else [3][2 mb][kp])
-  int64_t ncf;                     // (fragment order) 32-column fragments of the 2 mb checksum columns
-  const float* s_full;             // sign pattern of a full row block (128), and of the last (rem) one
-  const float* s_last;
-  uint16_t* parts;                 // [3][2 mb][kp] bf16: hi, mid, lo of (plain, signed) per row block
-  float* stats;                    // [nkc][mb][NXS] partial statistics of the sums, per depth chunk
-  float* xnp;                      // [nkc][2][m] partial |x_i|_2^2, |x_i|_1 per depth chunk
-  float* xn;                       // [2][m] |x_i|_2^2, |x_i|_1 (the column check's A norms)
-  float* rstat;                    // [mb][RST]: sq0, sq1, max0, max1, max |x|, sum of the block's pattern
-};
 
 // One workgroup: one row block (128 rows) by 128 consecutive depths (32 KB of x).  Thread t = 16 rg + dc reads
 // depths 8 dc .. 8 dc + 7 of rows rg + 16 i (i < 8): eight 16-byte loads, a wave covering four rows of 256
@@ -263,48 +249,9 @@ __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
   }
 }
 
-// The depth chunks' partials of one row block added up in chunk order (so the result is the same on every run):
-// the rows' |x|_2^2 and |x|_1 (thread t: row t / 2, t % 2 the statistic), the block sums' statistics (wave 1), the
-// sum of the block's sign pattern (wave 2).  Each thread has XF_BATCH chunks' loads in flight at once (its time is
-// the loads' latency, not their bytes).
-constexpr int XF_BATCH = 32;
-__global__ __launch_bounds__(256) void xfinish_kernel(XStageArgs a) {
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int64_t ib = blockIdx.x;
-  const int wid = (int)((ib == a.mb - 1 && a.rem > 0) ? a.rem : BS);
-  const float* sp = (ib == a.mb - 1 && a.rem > 0) ? a.s_last : a.s_full;
-  {
-    const int r = t >> 1, c = t & 1;
-    const int64_t row = ib * BS + (r < wid ? r : 0);
-    float acc = 0.f;
-    for (int64_t q0 = 0; q0 < a.nkc; q0 += XF_BATCH) {
-      float p[XF_BATCH];
-#pragma unroll
-      for (int j = 0; j < XF_BATCH; ++j) p[j] = a.xnp[((q0 + j < a.nkc ? q0 + j : a.nkc - 1) * 2 + c) * a.m + row];
-#pragma unroll
-      for (int j = 0; j < XF_BATCH; ++j)
-        if (q0 + j < a.nkc) acc += p[j];
-    }
-    if (r < wid) a.xn[c * a.m + row] = acc;
-  }
-  if (w == 1) {
-    const int i = lane < NXS ? lane : 0;
-    float v = 0.f;
-    for (int64_t q0 = 0; q0 < a.nkc; q0 += XF_BATCH) {
-      float p[XF_BATCH];
-#pragma unroll
-      for (int j = 0; j < XF_BATCH; ++j)
-        p[j] = a.stats[((q0 + j < a.nkc ? q0 + j : a.nkc - 1) * a.mb + ib) * NXS + i];
-#pragma unroll
-      for (int j = 0; j < XF_BATCH; ++j)
-        if (q0 + j < a.nkc) v = i < 2 ? v + p[j] : fmaxf(v, p[j]);
-    }
-    if (lane < NXS) a.rstat[ib * RST + lane] = v;
-  } else if (w == 2) {
-    const float ss = wave_sum_f32((lane < wid ? sp[lane] : 0.f) + (lane + 64 < wid ? sp[lane + 64] : 0.f));
-    if (lane == 0) a.rstat[ib * RST + NXS] = ss;
-  }
-}
+
+// The finishing step as its own launch (where the row check's GEMM has no spare workgroups to run it).
+__global__ __launch_bounds__(256) void xfinish_kernel(XStageArgs a) { xfinish_block(a, blockIdx.x, threadIdx.x); }
 
 // --------------------------------------------------------------------------------------------- 4. the y pass
 struct YArgs {
@@ -747,29 +694,38 @@ int queue_both(const void* x, int64_t sxm, const void* W, int64_t swn, const voi
     hipLaunchKernelGGL(xstage_kernel, dim3((unsigned)L.nkc, (unsigned)L.mb), dim3(256), 0, stream, xa);
     SDC_LAUNCH_CHECK();
   }
-  // 2. xfinish on the side stream (when there is one), beside the row check's GEMM
-  hipStream_t fin = stream;
-  if (side != stream && !(fin = sdc_fork(stream))) return SDC_ELAUNCH;
-  {
-    SdcProf prof("xfinish", fin);
-    hipLaunchKernelGGL(xfinish_kernel, dim3((unsigned)L.mb), dim3(256), 0, fin, xa);
-    SDC_LAUNCH_CHECK();
-  }
-  // 3. the row check's GEMM: E_row = W @ (x block sums), each XCD taking every depth slice of its rows (W's row
-  //    norms are the layer's, made once)
+  // 2, 3. the row check's GEMM: E_row = W @ (x block sums), each XCD taking every depth slice of its rows (W's row
+  //    norms are the layer's, made once); the tall-tile GEMM runs xfinish in spare workgroups of its grid (one per
+  //    row block), else xfinish is a launch of its own (on the side stream when there is one)
   GemmArgs gr{};
   gr.A = (const uint16_t*)W; gr.sab = 0; gr.sam = swn; gr.sak = 1;
   gr.B = ws + L.off_parts; gr.sbb = 0; gr.sbc = L.kp;
   gr.m = n; gr.k = k; gr.N = 2 * L.mb; gr.splits = L.srow;
   gr.E = ws + L.off_erow; gr.XN = nullptr; gr.et = 1; gr.rows_per_xcd = 1;
   gr.prof_name = "row_gemm";
-  if (!rs_row) {
-    rc = sdc_gemm_launch(SDC_BF16, gr, 1, stream);              // (W not 16-byte aligned: the staged GEMM)
-  } else {
-    rc = L.tall_row ? sdc_rs_gemm_tall_launch(SDC_BF16, gr, 1, stream) : sdc_rs_gemm_launch(SDC_BF16, gr, 1, stream);
+  rc = SDC_EUNSUPPORTED;
+  bool finished = false;
+  if (rs_row && L.tall_row && side == stream) {
+    GemmArgs gx = gr;
+    gx.xf = xa;
+    gx.xf_blocks = (int)L.mb;
+    rc = sdc_rs_gemm_tall_launch(SDC_BF16, gx, 1, stream);
+    finished = rc == SDC_OK;
+  }
+  hipStream_t fin = stream;
+  if (!finished) {
+    if (side != stream && !(fin = sdc_fork(stream))) return SDC_ELAUNCH;
+    SdcProf prof("xfinish", fin);
+    hipLaunchKernelGGL(xfinish_kernel, dim3((unsigned)L.mb), dim3(256), 0, fin, xa);
+    SDC_LAUNCH_CHECK();
+  }
+  if (rc == SDC_EUNSUPPORTED) {
+    if (!rs_row) rc = sdc_gemm_launch(SDC_BF16, gr, 1, stream);     // (W not 16-byte aligned: the staged GEMM)
+    else if (L.tall_row) rc = sdc_rs_gemm_tall_launch(SDC_BF16, gr, 1, stream);
+    else rc = sdc_rs_gemm_launch(SDC_BF16, gr, 1, stream);
   }
   if (rc != SDC_OK) return rc;
-  if (fin != stream && (rc = sdc_join(stream, fin)) != SDC_OK) return rc;   // (the side stream also holds the GEMM)
+  if (side != stream && (rc = sdc_join(stream, side)) != SDC_OK) return rc;   // (the column GEMM, and xfinish)
 
   // 4. one pass over y: both checks
   YArgs ya{};

@@ -23,14 +23,16 @@ BLOCK = 128
 def check_linear_both(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], y: torch.Tensor,
                       cs: LayerChecksums, *, z: float = 6.0, abs_floor: float = ABS_FLOOR,
                       state: Optional[torch.Tensor] = None, row_result: Optional[torch.Tensor] = None,
-                      concurrent: bool = True, col_scores: Optional[torch.Tensor] = None,
+                      concurrent: bool = False, col_scores: Optional[torch.Tensor] = None,
                       row_scores: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Queue both checks of y = linear(x, weight, bias) on the current stream (no host sync).  cs: the layer's
     LayerChecksums (block 128).  Returns (state, row_result): the column check's int64[4] state row (worst key, key
     with noise, checks, unjudged) and the row check's int64[3] result row (worst key, key with noise, unjudged);
-    pass zeroed ones to fold several calls into one.  concurrent: run the column check's GEMM on a side stream
-    beside the x pass and the row check's GEMM (the default: 104 us against 111 us on one stream for the 4096 x
-    4096 x 14336 layer on MI355X); False keeps every kernel on the current stream."""
+    pass zeroed ones to fold several calls into one.  concurrent: run the column check's GEMM and the x pass's
+    finishing step on a side stream beside the x pass and the row check's GEMM; the default (False) keeps every
+    kernel on the current stream, where the row check's GEMM runs that finishing step in its spare workgroups (on
+    MI355X for the 4096 x 4096 x 14336 layer the one-stream form is the faster: the column GEMM fills every CU, so
+    the side stream only adds the cost of its fork and join)."""
     _lib.require_gpu(x, weight, y)
     if y.dtype != torch.bfloat16 or x.dtype != y.dtype or weight.dtype != y.dtype:
         raise _lib.HipLibraryError("check_linear_both takes bf16 layers (fp16: check_static_impl and "
