@@ -1139,20 +1139,21 @@ int sdc_rs_gemm_launch(int dtype, GemmArgs g, int role, hipStream_t stream) {
   return SDC_OK;
 }
 
-// The tall-tile variant: 128 x 64 tiles over g.splits (1 or 2) depth parts, one plane of E per part (the depth a
-// multiple of 256 splits, of 512 splits for an fp8 A; A's rows 16-byte aligned); with g.XN set, also A's row norms,
-// one plane per part.  dtype SDC_FP8: an fp8 e4m3 A widened to bf16 (B's parts bf16).  With g.goffs (16-bit A
+// The tall-tile variant: 128 x 64 tiles (64 x 64 with g.short_rows, fp8 only) over g.splits (1 .. SDC_MAX_SPLITS)
+// depth parts, one plane of E per part (the depth a multiple of 256 splits, of 512 splits for an fp8 A; A's rows
+// 16-byte aligned); with g.XN set, also A's row norms, one plane per part.  dtype SDC_FP8: an fp8 e4m3 A widened to bf16 (B's parts bf16).  With g.goffs (16-bit A
 // only): rows grouped by the groups' cumulative ends, group q's fragments at g.B + q g.sbb, row norms always.
 // Returns SDC_EUNSUPPORTED where it does not apply.
 int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream) {
   if (dtype != SDC_BF16 && dtype != SDC_FP16 && dtype != SDC_FP8) return SDC_EUNSUPPORTED;
   const int64_t es = dtype == SDC_FP8 ? 1 : 2, kmul = (dtype == SDC_FP8 ? RS_WAVES * 128 : RS_KMULT) * g.splits;
-  if ((g.splits != 1 && g.splits != 2) || g.sak != 1 || g.k % kmul || (g.sam * es) % 16 ||
+  if (g.splits < 1 || g.splits > SDC_MAX_SPLITS || g.sak != 1 || g.k % kmul || (g.sam * es) % 16 ||
       ((uintptr_t)g.A | (uintptr_t)g.B) % 16 || !g.et)
     return SDC_EUNSUPPORTED;
   if (g.goffs && (dtype == SDC_FP8 || g.ngroups < 1 || g.ngroups > GSCAN || g.sbb % 8)) return SDC_EUNSUPPORTED;
   if (g.m < 1 || g.N < 1) return SDC_EINVAL;
-  const int64_t rtiles = sdc_cdiv(g.m, 32 * SDC_TALL_TRF) + (g.goffs ? g.ngroups : 0);
+  if (g.short_rows && (dtype != SDC_FP8 || g.goffs || g.xf_blocks)) return SDC_EUNSUPPORTED;
+  const int64_t rtiles = sdc_cdiv(g.m, g.short_rows ? 64 : 32 * SDC_TALL_TRF) + (g.goffs ? g.ngroups : 0);
   if (g.xf_blocks < 0 || (g.xf_blocks && (g.goffs || dtype == SDC_FP8))) return SDC_EINVAL;
   const int64_t blocks = g.splits * rtiles * sdc_cdiv(g.N, 64) + g.xf_blocks;
   if (blocks > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
@@ -1165,6 +1166,9 @@ int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream)
       hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 4, T, 0, true, true>), grid, block, 0, stream, g);
     else
       hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_FP16, 4, T, 0, true, true>), grid, block, 0, stream, g);
+  } else if (dtype == SDC_FP8 && g.short_rows) {
+    if (g.XN) hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 3, 2, 1, true>), grid, block, 0, stream, g);
+    else hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 3, 2, 1, false>), grid, block, 0, stream, g);
   } else if (dtype == SDC_FP8) {
     if (g.XN) hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 3, T, 1, true>), grid, block, 0, stream, g);
     else hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 3, T, 1, false>), grid, block, 0, stream, g);

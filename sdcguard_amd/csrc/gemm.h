@@ -30,6 +30,9 @@ struct GemmArgs {
   // for them
   XStageArgs xf;
   int xf_blocks;
+  // (the tall-tile kernel, an fp8 A) 64-row tiles instead of 128, for a short A whose 128-row tiles would leave
+  // most CUs idle
+  int short_rows;
 };
 
 // E and XN for `batches` batches.

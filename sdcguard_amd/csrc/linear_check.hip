@@ -323,6 +323,15 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
   const bool colside = w < 2;
   const int R = r0 + 64 * w + lane;                                          // (column side) this lane's row
   constexpr uint32_t ONES = DT == SDC_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  // the result rows' worst keys as they stand now (thread 0: the column check's, thread 64: the row check's), read
+  // first so the read's latency hides under the tile's: at the end a key at or below them needs no atomic (keys
+  // only grow, so a stale value only lets an unneeded atomic through)
+  int64_t seen0 = 0, seen1 = 0;
+  if (t == 0 || t == 64) {
+    const int64_t* res = t == 0 ? a.state : a.result;
+    seen0 = __atomic_load_n(res, __ATOMIC_RELAXED);
+    seen1 = __atomic_load_n(res + 1, __ATOMIC_RELAXED);
+  }
 
   // ---- what every tile shares: the row block's pattern (this thread's 8 rows), statistics, the rows' norms
   uint32_t srow2[4];
@@ -558,9 +567,8 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
     const int64_t d0 = red_d[w0] > red_d[w0 + 1] ? red_d[w0] : red_d[w0 + 1];
     const int un = red_u[w0] + red_u[w0 + 1];
     int64_t* res = t == 0 ? a.state : a.result;
-    if (k0 > __atomic_load_n(res, __ATOMIC_RELAXED)) atomicMax((unsigned long long*)res, (unsigned long long)k0);
-    if (d0 > __atomic_load_n(res + 1, __ATOMIC_RELAXED))
-      atomicMax((unsigned long long*)(res + 1), (unsigned long long)d0);
+    if (k0 > seen0) atomicMax((unsigned long long*)res, (unsigned long long)k0);
+    if (d0 > seen1) atomicMax((unsigned long long*)(res + 1), (unsigned long long)d0);
     if (t == 0) {
       if (blockIdx.x == 0 && blockIdx.y == 0) atomicAdd((unsigned long long*)(res + 2), 1ull);
       if (un > 0) atomicAdd((unsigned long long*)(res + 3), (unsigned long long)un);

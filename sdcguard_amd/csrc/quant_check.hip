@@ -279,6 +279,13 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(QuantArgs a) {
   const int rg = t >> 4, cg = t & 15;
   const int64_t jb = blockIdx.x, r0 = (int64_t)blockIdx.y * 64;
   const int64_t c0 = jb * 128 + 8 * cg;
+  // the result row's worst keys as they stand now, read first so the read's latency hides under the tile's (a key
+  // at or below them needs no atomic at the end; keys only grow, so a stale value only lets an unneeded one through)
+  int64_t seen0 = 0, seen1 = 0;
+  if (t == 0) {
+    seen0 = __atomic_load_n(a.result, __ATOMIC_RELAXED);
+    seen1 = __atomic_load_n(a.result + 1, __ATOMIC_RELAXED);
+  }
   // C: 4 rows x 8 columns, clamped to row m - 1 (rows past m are never judged); the last block's columns past n
   // are masked at use
   u32x4 v[4][NL];
@@ -479,9 +486,8 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(QuantArgs a) {
     const int wr = wave_sum_i32(best.wrong), nf = wave_sum_i32(best.nonfin);
     if (lane == 0) {
       int64_t* res = a.result;
-      if (key > __atomic_load_n(res, __ATOMIC_RELAXED)) atomicMax((unsigned long long*)res, (unsigned long long)key);
-      if (keyd > __atomic_load_n(res + 1, __ATOMIC_RELAXED))
-        atomicMax((unsigned long long*)(res + 1), (unsigned long long)keyd);
+      if (key > seen0) atomicMax((unsigned long long*)res, (unsigned long long)key);
+      if (keyd > seen1) atomicMax((unsigned long long*)(res + 1), (unsigned long long)keyd);
       if (wr > 0) atomicAdd((unsigned long long*)(res + 2), (unsigned long long)wr);
       if (nf > 0) atomicAdd((unsigned long long*)(res + 3), (unsigned long long)nf);
     }
@@ -505,7 +511,9 @@ int64_t quant_splits(int kind, int64_t m, int64_t k, int64_t ncols) {
 
 struct QLayout {
   int64_t nb, rem, ncols, splits, nacc, kpad, off_e, off_xn, off_apad, off_ppad, off_frag, total;   // in floats
-  bool tall;                       // fp8: the tall-tile register-streamed GEMM (two planes) where the shape allows
+  bool tall;                       // fp8: the tall-tile register-streamed GEMM where the shape allows
+  bool short_rows;                 // (its 64-row tiles, for a short A)
+  int64_t tsplits;                 // (its depth parts: planes of E)
 };
 
 QLayout qlayout(int kind, int64_t m, int64_t k, int64_t n, int64_t bs) {
@@ -515,10 +523,24 @@ QLayout qlayout(int kind, int64_t m, int64_t k, int64_t n, int64_t bs) {
   L.ncols = 2 * L.nb;
   L.nacc = kind == 0 ? 2 : 1;
   L.splits = quant_splits(kind, m, kind == 0 ? (k + 1) / 2 : k, L.ncols);
-  // an fp8 GEMM whose 128 x 64 tiles over two depth halves fill the GPU (192 workgroups or more; depth a multiple
-  // of 1024): one pair of E planes, the parts in fragment order
-  L.tall = kind == 1 && k % 1024 == 0 && 2 * sdc_cdiv(m, 128) * sdc_cdiv(L.ncols, 64) >= 192;
-  const int64_t esplits = L.tall && L.splits < 2 ? 2 : L.splits;
+  // an fp8 GEMM on the register-streamed tall-tile kernel (depth a multiple of 1024, the parts in fragment order):
+  // 128 x 64 tiles over two depth halves where they fill the GPU (192 workgroups or more), else (a short A) 64 x 64
+  // tiles over as many depth parts, up to SDC_MAX_SPLITS, as keep within two workgroups a CU
+  const int64_t nct = sdc_cdiv(L.ncols, 64);
+  if (kind == 1 && k % 1024 == 0) {
+    if (2 * sdc_cdiv(m, 128) * nct >= 192) {
+      L.tall = true;
+      L.tsplits = 2;
+    } else {
+      for (int64_t s = SDC_MAX_SPLITS; s >= 2; --s)
+        if (k % (512 * s) == 0 && s * sdc_cdiv(m, 64) * nct <= 512) {
+          L.tall = L.short_rows = true;
+          L.tsplits = s;
+          break;
+        }
+    }
+  }
+  const int64_t esplits = L.tall && L.splits < L.tsplits ? L.tsplits : L.splits;
   L.kpad = kind == 0 ? (k + 63) / 64 * 64 : 0;           // int8: depth of the zero-padded copies (bytes)
   auto al = [](int64_t x) { return (x + 63) / 64 * 64; };
   int64_t o = 0;
@@ -630,10 +652,11 @@ extern "C" int sdc_quant_check(int kind, const void* A, int64_t sam, const void*
     }
     GemmArgs gt = g;
     gt.B = frag;
-    gt.splits = 2;
+    gt.splits = L.tsplits;
+    gt.short_rows = L.short_rows ? 1 : 0;
     gt.et = 1;
     rc = sdc_rs_gemm_tall_launch(SDC_FP8, gt, 0, stream);
-    if (rc == SDC_OK) splits = 2;
+    if (rc == SDC_OK) splits = L.tsplits;
   }
   if (rc == SDC_EUNSUPPORTED) rc = sdc_gemm_launch(kind == 0 ? SDC_I8 : SDC_FP8, g, 1, stream);
   if (rc != SDC_OK) return rc;

@@ -102,13 +102,14 @@ def test_fp8_scaled_matches_oracle(shape, out):
     assert np.allclose(zg, o["z"], rtol=1e-3, atol=2e-3), np.abs(zg - o["z"]).max()
 
 
+@pytest.mark.parametrize("m,k,n", [(4096, 2048, 14336), (2048, 7168, 4096), (1000, 3072, 2048)])
 @pytest.mark.parametrize("out", [torch.bfloat16, torch.float32])
-def test_fp8_tall_gemm_matches_oracle(out):
-    """An fp8 layer whose tiles fill the GPU (4096 x 2048 x 14336): the expected side on the tall-tile GEMM (fp8 A
-    widened to bf16 in registers, two depth-half planes, the row norms in the same pass) scores every block as the
-    oracle does, and faults (a dequantized output 4 RMS off, a flipped exponent bit) are located."""
+def test_fp8_tall_gemm_matches_oracle(out, m, k, n):
+    """The expected side on the tall-tile GEMM (fp8 A widened to bf16 in registers, the row norms in the same pass):
+    128-row tiles over two depth halves where they fill the GPU (4096 x 2048 x 14336), else 64-row tiles over up to
+    8 depth parts (2048 x 7168 x 4096: seven; 1000 x 3072 x 2048: six, a ragged last row tile).  Every block scores
+    as the oracle scores it, and faults (a dequantized output 4 RMS off, a flipped exponent bit) are located."""
     from sdcguard_amd import modes
-    m, k, n = 4096, 2048, 14336
     Aq, Bq, sa, sb, C = _scaled_problem(71, m, k, n, out=out)
     consts = modes.QuantChecksums.make(Bq, sb)
     zs = torch.full((m, n // 128), -7.0, device="cuda")
@@ -135,8 +136,17 @@ def test_fp8_tall_gemm_matches_oracle(out):
         else:
             v = c[i:i + 1, j].view(torch.int16)
             v ^= (1 << 14)
-        res = modes.resolve(modes.quant_zscores(Aq, consts, c, sa=sa))
-        assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (i, j // 128), (t, i, j, res)
+        zf = torch.full((m, n // 128), -7.0, device="cuda")
+        res = modes.resolve(modes.quant_zscores(Aq, consts, c, sa=sa, scores_out=zf))
+        of = quant.fp8_judge(A, B, sa.double().cpu().numpy(), sb.double().cpu().numpy(), c.double().cpu().numpy(),
+                             quant.patterns(1), c_bf16=out == torch.bfloat16)
+        # the faulty block scores as the oracle scores it, and the verdicts agree
+        zfb, ofb = float(zf[i, j // 128]), float(of["z"][i, j // 128])
+        assert (zfb == ofb) or abs(zfb - ofb) <= 1e-3 * max(1.0, abs(ofb)), (t, i, j, zfb, ofb)
+        assert res["wrong_blocks"] == of["wrong_blocks"] and res["nonfinite_blocks"] == of.get(
+            "nonfinite_blocks", res["nonfinite_blocks"]), (t, i, j, res, of["wrong_blocks"])
+        if of["wrong_blocks"]:
+            assert (res["row"], res["block"]) == (i, j // 128), (t, i, j, res)
 
 
 def test_fp8_scaled_faults_located():
