@@ -538,7 +538,8 @@ def bench_quant(ctx: Ctx, kind: str, m: int, k: int, n: int, name: str, seed: in
     alg = ab + cb + pb + sc
     amounts = {gname: ("mfma", 2.0 * m * k * consts.parts.shape[0] * consts.parts.shape[1], kind),
                sname: ("hbm", cb, None)}
-    patterns = {gname: r"expected_gemm_kernel<" + ("3" if kind == "int8" else "2"),
+    # (int8: the staged GEMM, expected_gemm_kernel<3, ..>; fp8: the tall-tile GEMM, rs_gemm_tall_kernel<0, 3, ..>)
+    patterns = {gname: r"expected_gemm_kernel<3" if kind == "int8" else r"rs_gemm_tall_kernel<0, 3,",
                 sname: r"quant_(tile|score)_kernel<" + ("0" if kind == "int8" else "1")}
     ent, roof = _roof(km, amounts, name, patterns, a.steps)
     value = alg / (ms * 1e-3) / 1e9
@@ -652,7 +653,7 @@ def bench_moe(ctx: Ctx) -> dict:
     ab, cb, b2 = T * K * 2, T * N * 2, E * K * 2 * nb * 4
     alg = ab + cb + b2
     amounts = {"train_gemm": ("mfma", 2.0 * T * K * 6 * nb, "bf16"), "train_score": ("hbm", cb, None)}
-    patterns = {"train_gemm": r"expected_gemm_kernel<0", "train_score": r"score"}
+    patterns = {"train_gemm": r"rs_gemm_tall_kernel<0, 4,", "train_score": r"grouped_score_kernel"}
     ent, roof = _roof(km, amounts, name, patterns, a.steps)
     value = alg / (ms * 1e-3) / 1e9
     gemm_ms = None
