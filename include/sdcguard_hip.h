@@ -266,8 +266,9 @@ int sdc_grouped_check(int dtype, const void* A, int64_t sam, int64_t sak, const 
  * made once per layer and each call runs only the expected-side GEMM and the pass over out.
  *   sdc_grouped_constants: from B (groups, k, n; strides sbg, sbk, sbn) and an optional shared bias (n values at
  *     stride sbias), into consts (sdc_grouped_constants_bytes bytes, 256-byte aligned): per expert its block sums'
- *     column norms, maxima and power-of-two scales, each block's largest |B|, the bias's block sums, and the three
- *     16-bit parts of the scaled block sums.  workspace: sdc_grouped_constants_workspace bytes of scratch.
+ *     column norms, maxima and power-of-two scales, each block's largest |B|, the bias's block sums, the three
+ *     16-bit parts of the scaled block sums and (depth a multiple of 512) the same parts in the register-streamed
+ *     GEMM's fragment order, one set per expert.  workspace: sdc_grouped_constants_workspace bytes of scratch.
  *   sdc_grouped_check_consts: sdc_grouped_check against those constants (has_bias: whether they hold a bias);
  *     the same results and scores.  workspace: sdc_grouped_check_consts_workspace bytes. */
 int64_t sdc_grouped_constants_bytes(int64_t groups, int64_t k, int64_t n, int64_t bs);
