@@ -538,8 +538,8 @@ def bench_quant(ctx: Ctx, kind: str, m: int, k: int, n: int, name: str, seed: in
     alg = ab + cb + pb + sc
     amounts = {gname: ("mfma", 2.0 * m * k * consts.parts.shape[0] * consts.parts.shape[1], kind),
                sname: ("hbm", cb, None)}
-    # (int8: the staged GEMM, expected_gemm_kernel<3, ..>; fp8: the tall-tile GEMM, rs_gemm_tall_kernel<0, 3, ..>)
-    patterns = {gname: r"expected_gemm_kernel<3" if kind == "int8" else r"rs_gemm_tall_kernel<0, 3,",
+    # (the tall-tile GEMM: rs_gemm_tall_kernel<0, 5, ..> for int8, <0, 3, ..> for fp8)
+    patterns = {gname: r"rs_gemm_tall_kernel<0, 5," if kind == "int8" else r"rs_gemm_tall_kernel<0, 3,",
                 sname: r"quant_(tile|score)_kernel<" + ("0" if kind == "int8" else "1")}
     ent, roof = _roof(km, amounts, name, patterns, a.steps)
     value = alg / (ms * 1e-3) / 1e9

@@ -236,6 +236,13 @@ int64_t sdc_linear_check_workspace(int64_t m, int64_t k, int64_t n);
  * multiple of 64; out: sdc_parts_fragments_bytes(N, k) bytes, 16-byte aligned. */
 int64_t sdc_parts_fragments_bytes(int64_t N, int64_t k);
 int sdc_parts_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out, hipStream_t stream);
+/* The int8 check's two base-128 digit planes of the block sums (QuantChecksums.parts: [2][N][spc] int8,
+ * k-contiguous per column) in the int8 fragment order of the tall-tile GEMM (8 bytes a lane: digit p, column 32 f +
+ * l % 32, the same permuted depths as the 16-bit fragments), made once per layer and passed to sdc_quant_check as
+ * parts_frag for kind 0.  No counterpart in the reference (its int8 check multiplies unsplit block sums).
+ * k a multiple of 64; out: sdc_digit_fragments_bytes(N, k) bytes, 8-byte aligned. */
+int64_t sdc_digit_fragments_bytes(int64_t N, int64_t k);
+int sdc_digit_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out, hipStream_t stream);
 int sdc_linear_check(int dtype, const void* x, int64_t sxm, const void* W, int64_t swn, const void* y, int64_t sym,
                      const void* bias, int64_t m, int64_t k, int64_t n, const void* parts, int64_t spc,
                      const void* parts_frag, const float* block_consts, const float* w_norms, const float* sign_table, int64_t* state,
@@ -320,8 +327,9 @@ int sdc_layer_constants(int dtype, const void* W, int64_t swn, int64_t n, int64_
  *     (1, m)).  sign_table: as sdc_check_static (epoch 0).
  *   result: int64[4], zeroed by the caller: the worst block's key (bits of z << 32 | row * nb + block), the key with
  *     its noise, the number of wrong blocks (z > z; int8: any differing sum), blocks with a non-finite sum.
- *   parts_frag (fp8): the parts in sdc_parts_fragments' order (made once with the weight's constants), or NULL: an
- *     fp8 GEMM whose tiles fill the GPU takes them (the library makes them in the workspace when NULL).
+ *   parts_frag: the parts in the tall-tile GEMM's order -- fp8: sdc_parts_fragments', int8: sdc_digit_fragments'
+ *     -- made once with the weight's constants, or NULL (the library makes them in the workspace when the GEMM
+ *     takes them: depth a multiple of 1024).
  *   workspace: at least sdc_quant_check_workspace(kind, m, k, n, bs) bytes; scores_out: (m, nb) z or NULL. */
 int64_t sdc_quant_check_workspace(int kind, int64_t m, int64_t k, int64_t n, int64_t bs);
 int sdc_quant_check(int kind, const void* A, int64_t sam, const void* parts, int64_t spc,

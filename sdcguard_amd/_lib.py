@@ -57,6 +57,8 @@ SIGNATURES = {
                                P, I64, P, P, I32, P]),
     "sdc_parts_fragments_bytes": (I64, [I64, I64]),
     "sdc_parts_fragments": (I32, [P, I64, I64, I64, P, P]),
+    "sdc_digit_fragments_bytes": (I64, [I64, I64]),
+    "sdc_digit_fragments": (I32, [P, I64, I64, I64, P, P]),
     "sdc_grouped_check_workspace": (I64, [I64, I64, I64, I64, I64]),
     "sdc_grouped_constants_bytes": (I64, [I64, I64, I64, I64]),
     "sdc_grouped_constants_workspace": (I64, [I64, I64, I64, I64]),

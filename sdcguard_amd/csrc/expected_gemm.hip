@@ -775,10 +775,14 @@ constexpr int GSCAN = 1024;                       // groups the grouped tall GEM
 
 template <int DT, int ROLE, int TRF, int AT, bool XNORM, bool GROUPED = false>
 __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_kernel(GemmArgs g) {
-  constexpr int MDT = AT ? SDC_BF16 : DT;       // the MFMAs' type
+  constexpr int MDT = AT ? SDC_BF16 : DT;       // the MFMAs' type (AT 2: int8)
   constexpr int SPS = AT ? 8 : 4;               // steps per segment
   constexpr int SD = 16 * SPS;                  // depths per segment
   constexpr int ES = AT ? 1 : 2;                // bytes per A element
+  constexpr int NP = AT == 2 ? 2 : 3;           // B parts (int8: the block sums' two base-128 digits)
+  constexpr int NACC = AT == 2 ? 2 : 1;         // accumulator sets (int8: one per digit, exact int32)
+  constexpr int FRAG = AT == 2 ? 256 : 512;     // 16-bit units per B fragment (int8: 8 bytes a lane)
+  static_assert(AT != 2 || (TRF == 2 && !XNORM && !GROUPED), "int8: 64-row tiles, no row norms");
   constexpr int TCF = 2, TR = 32 * TRF, TC = 64, RB = 4, NAI = TR / 8, APS = NAI / SPS;
   constexpr int RT_SEGB = TR * 128;             // bytes of A per wave and segment (TR rows x 128 bytes)
   constexpr int RED_BYTES = RS_WAVES * TC * (TR + 4) * 4;       // the epilogue's reduction (below)
@@ -857,14 +861,15 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
         ard[i][jj] = (R >> 3) * 1024 + 16 * (8 * rr + ((4 * h + jj) ^ rr));
       }
     }
-  const uint16_t* bq = (const uint16_t*)g.B + grp * g.sbb + (int64_t)(SPS * seg0) * 3 * ncf * 512 + 8 * lane;
+  const uint16_t* bq =
+      (const uint16_t*)g.B + grp * g.sbb + (int64_t)(SPS * seg0) * NP * ncf * FRAG + (FRAG / 64) * lane;
   int bf[TCF];
 #pragma unroll
   for (int n = 0; n < TCF; ++n) {
     const int64_t f = c0 / 32 + n;
-    bf[n] = (int)((f < ncf ? f : ncf - 1) * 512);
+    bf[n] = (int)((f < ncf ? f : ncf - 1) * FRAG);
   }
-  const int64_t bstep = 3 * ncf * 512;
+  const int64_t bstep = NP * ncf * FRAG;
   const int lastseg = per - 1;
   const int last = SPS * per - 1;
   // A's instruction I (0 .. 15) of a segment, lane L: row 8 I + L / 8 (clamped to m - 1), 16-byte piece
@@ -876,7 +881,8 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
     const int64_t row = r0 + 8 * I + (lane >> 3);
     arow[I] = (row < rend ? row : rend - 1) * g.sam * ES;
   }
-  u32x4 rb[RB][3][TCF];
+  using BT = typename std::conditional<AT == 2, u32x2, u32x4>::type;
+  BT rb[RB][NP][TCF];
   auto issue_a4 = [&](int sg, int I0) {
     const int s2 = sg < lastseg ? sg : lastseg;
     uint8_t* dst = abuf + (sg & 1) * RT_SEGB;
@@ -884,25 +890,45 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
     for (int I = I0; I < I0 + APS; ++I)
       sdc_pipe::lds_load16(abase + arow[I] + 128 * (int64_t)s2, (uint16_t*)(dst + 1024 * I));
   };
-  auto issue_b = [&](int slot, int st) {
-    const uint16_t* q = bq + (int64_t)(st < last ? st : last) * bstep;
-#pragma unroll
-    for (int p = 0; p < 3; ++p)
-#pragma unroll
-      for (int n = 0; n < TCF; ++n)
-        asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(rb[slot][p][n]) : "v"(q + p * ncf * 512 + bf[n]));
-  };
   // part p of B(st) into slot `slot`
   auto issue_bp = [&](int slot, int st, int p) {
-    const uint16_t* q = bq + (int64_t)(st < last ? st : last) * bstep + p * ncf * 512;
+    const uint16_t* q = bq + (int64_t)(st < last ? st : last) * bstep + p * ncf * FRAG;
 #pragma unroll
-    for (int n = 0; n < TCF; ++n)
-      asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(rb[slot][p][n]) : "v"(q + bf[n]));
+    for (int n = 0; n < TCF; ++n) {
+      if constexpr (AT == 2) asm volatile("global_load_dwordx2 %0, %1, off" : "+v"(rb[slot][p][n]) : "v"(q + bf[n]));
+      else asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(rb[slot][p][n]) : "v"(q + bf[n]));
+    }
+  };
+  auto issue_b = [&](int slot, int st) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) issue_bp(slot, st, p);
   };
   // fragment reads of step jj into fr (fp8: 8 bytes each, widened after the wait).  Each read lands in the very
   // registers the wait names ("=v" then "+v"): a copy out of an asm read's result before its wait would copy data
   // that has not arrived.
   using FragT = typename std::conditional<AT != 0, u32x2, u32x4>::type;
+  // s_waitcnt vmcnt(C) naming B slot `slot`'s registers (so nothing reads them before the wait), and a no-op that
+  // names a slot's registers (so the loads into them count as used)
+#define SDC_TALL_WAIT_B(C, slot)                                                                                   \
+  do {                                                                                                            \
+    if constexpr (NP == 3)                                                                                        \
+      asm volatile("s_waitcnt vmcnt(%6)"                                                                          \
+                   : "+v"(rb[slot][0][0]), "+v"(rb[slot][0][1]), "+v"(rb[slot][1][0]), "+v"(rb[slot][1][1]),      \
+                     "+v"(rb[slot][2 % NP][0]), "+v"(rb[slot][2 % NP][1])                                         \
+                   : "n"(C));                                                                                     \
+    else                                                                                                          \
+      asm volatile("s_waitcnt vmcnt(%4)"                                                                          \
+                   : "+v"(rb[slot][0][0]), "+v"(rb[slot][0][1]), "+v"(rb[slot][1][0]), "+v"(rb[slot][1][1])       \
+                   : "n"(C));                                                                                     \
+  } while (0)
+#define SDC_TALL_NAME_B(slot)                                                                                      \
+  do {                                                                                                            \
+    if constexpr (NP == 3)                                                                                        \
+      asm volatile("" : "+v"(rb[slot][0][0]), "+v"(rb[slot][0][1]), "+v"(rb[slot][1][0]), "+v"(rb[slot][1][1]),   \
+                   "+v"(rb[slot][2 % NP][0]), "+v"(rb[slot][2 % NP][1]));                                          \
+    else                                                                                                          \
+      asm volatile("" : "+v"(rb[slot][0][0]), "+v"(rb[slot][0][1]), "+v"(rb[slot][1][0]), "+v"(rb[slot][1][1]));  \
+  } while (0)
   auto read_frags = [&](uint32_t L, int jj, FragT* fr) {
 #pragma unroll
     for (int i = 0; i < TRF; ++i) {
@@ -911,22 +937,24 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
     }
   };
   const uint32_t lds0 = (uint32_t)(uintptr_t)abuf;
-  f32x16 acc[TRF][TCF];
+  f32x16 acc[NACC][TRF][TCF];                   // (int8: the int32 sums' bits)
 #pragma unroll
-  for (int i = 0; i < TRF; ++i)
+  for (int pa = 0; pa < NACC; ++pa)
 #pragma unroll
-    for (int n = 0; n < TCF; ++n)
+    for (int i = 0; i < TRF; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][n][e] = 0.f;
+      for (int n = 0; n < TCF; ++n)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[pa][i][n][e] = 0.f;
   float xsq[TRF], xab[TRF];
 #pragma unroll
   for (int i = 0; i < TRF; ++i) xsq[i] = xab[i] = 0.f;
 #pragma unroll
   for (int q = 0; q < RB; ++q)
 #pragma unroll
-    for (int p = 0; p < 3; ++p)
+    for (int p = 0; p < NP; ++p)
 #pragma unroll
-      for (int n = 0; n < TCF; ++n) rb[q][p][n] = u32x4{0u, 0u, 0u, 0u};
+      for (int n = 0; n < TCF; ++n) rb[q][p][n] = BT{};
   if (per > 0) {
     // prologue: segment 0's A and B(0 .. 3) as the steps before the first would issue them (its A shares of those
     // steps; with 8 steps a segment, the shares of steps 0 .. 3 go out first)
@@ -942,6 +970,7 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
     // read them are issued), then part 1's, then part 2's.  The next step's A fragments are read from LDS in the
     // middle of the second group (inside a segment; the first step of a segment reads its own after the wait).
     FragT fr[2][TRF];
+    using AOpT = typename std::conditional<AT == 2, u32x2, u32x4>::type;
     for (int sg = 0; sg < per; ++sg) {
       const uint32_t L = lds0 + (uint32_t)((sg & 1) * RT_SEGB);
 #pragma unroll
@@ -949,30 +978,34 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
         static_assert(RB == 4, "the wait counts below assume B four steps ahead");
         const int st = SPS * sg + jj, cur = jj & 1, sl = jj & 3;
         if (jj == 0) {
-          asm volatile("s_waitcnt vmcnt(6)"
-                       : "+v"(rb[0][0][0]), "+v"(rb[0][0][1]), "+v"(rb[0][1][0]), "+v"(rb[0][1][1]),
-                         "+v"(rb[0][2][0]), "+v"(rb[0][2][1]));
+          SDC_TALL_WAIT_B(NP * TCF, 0);
           read_frags(L, 0, fr[0]);
         } else {
-          asm volatile("s_waitcnt vmcnt(%6)"
-                       : "+v"(rb[sl][0][0]), "+v"(rb[sl][0][1]), "+v"(rb[sl][1][0]), "+v"(rb[sl][1][1]),
-                         "+v"(rb[sl][2][0]), "+v"(rb[sl][2][1])
-                       : "n"((RB - 1) * (APS + 6)));
+          SDC_TALL_WAIT_B((RB - 1) * (APS + NP * TCF), sl);
         }
         if constexpr (TRF == 4)
           asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fr[cur][0]), "+v"(fr[cur][1]), "+v"(fr[cur][2]), "+v"(fr[cur][3]));
         else
           asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fr[cur][0]), "+v"(fr[cur][1]));
-        u32x4 a[TRF];
+        AOpT a[TRF];
 #pragma unroll
         for (int i = 0; i < TRF; ++i) {
-          if constexpr (AT) a[i] = fp8x8_to_bf16(fr[cur][i]);
+          if constexpr (AT == 1) a[i] = fp8x8_to_bf16(fr[cur][i]);
           else a[i] = fr[cur][i];
         }
+        auto mma = [&](int i, int n, int p) {
+          if constexpr (AT == 2)
+            acc[p][i][n] = __builtin_bit_cast(
+                f32x16, __builtin_amdgcn_mfma_i32_32x32x16_i8(__builtin_bit_cast(long, a[i]),
+                                                               __builtin_bit_cast(long, rb[sl][p][n]),
+                                                               __builtin_bit_cast(i32x16, acc[p][i][n]), 0, 0, 0));
+          else
+            acc[0][i][n] = sdc_pipe::mfma32<MDT>(a[i], rb[sl][p][n], acc[0][i][n]);
+        };
 #pragma unroll
         for (int i = 0; i < TRF; ++i)
 #pragma unroll
-          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<MDT>(a[i], rb[sl][0][n], acc[i][n]);
+          for (int n = 0; n < TCF; ++n) mma(i, n, 0);
         __builtin_amdgcn_sched_barrier(0);
         issue_a4(sg + 1, APS * jj);
         issue_bp(sl, st + RB, 0);
@@ -980,29 +1013,32 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
 #pragma unroll
         for (int i = 0; i < TRF / 2; ++i)
 #pragma unroll
-          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<MDT>(a[i], rb[sl][1][n], acc[i][n]);
+          for (int n = 0; n < TCF; ++n) mma(i, n, 1);
         __builtin_amdgcn_sched_barrier(0);
         if (jj < SPS - 1) read_frags(L, jj + 1, fr[cur ^ 1]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = TRF / 2; i < TRF; ++i)
 #pragma unroll
-          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<MDT>(a[i], rb[sl][1][n], acc[i][n]);
+          for (int n = 0; n < TCF; ++n) mma(i, n, 1);
         __builtin_amdgcn_sched_barrier(0);
         issue_bp(sl, st + RB, 1);
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (NP == 3) {
 #pragma unroll
-        for (int i = 0; i < TRF; ++i)
+          for (int i = 0; i < TRF; ++i)
 #pragma unroll
-          for (int n = 0; n < TCF; ++n) acc[i][n] = sdc_pipe::mfma32<MDT>(a[i], rb[sl][2][n], acc[i][n]);
-        __builtin_amdgcn_sched_barrier(0);
-        issue_bp(sl, st + RB, 2);
-        if (do_xn) {
+            for (int n = 0; n < TCF; ++n) mma(i, n, 2);
+          __builtin_amdgcn_sched_barrier(0);
+          issue_bp(sl, st + RB, 2);
+        }
+        if constexpr (XNORM) {
+          if (do_xn) {
           // the rows' norms over this step's 8 depths of each fragment (packed dot products)
           constexpr uint32_t ONES = MDT == SDC_BF16 ? 0x3F803F80u : 0x3C003C00u;
 #pragma unroll
           for (int i = 0; i < TRF; ++i) {
-            const uint32_t ww[4] = {a[i].x, a[i].y, a[i].z, a[i].w};
+            const uint32_t* ww = reinterpret_cast<const uint32_t*>(&a[i]);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
               xsq[i] = pk_dot2<MDT>(ww[q], ww[q], xsq[i]);
@@ -1010,16 +1046,13 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
             }
           }
         }
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    asm volatile("s_waitcnt vmcnt(0)"
-                 : "+v"(rb[0][0][0]), "+v"(rb[0][0][1]), "+v"(rb[0][1][0]), "+v"(rb[0][1][1]), "+v"(rb[0][2][0]),
-                   "+v"(rb[0][2][1]));
+    SDC_TALL_WAIT_B(0, 0);
 #pragma unroll
-    for (int q = 1; q < RB; ++q)
-      asm volatile("" : "+v"(rb[q][0][0]), "+v"(rb[q][0][1]), "+v"(rb[q][1][0]), "+v"(rb[q][1][1]), "+v"(rb[q][2][0]),
-                   "+v"(rb[q][2][1]));
+    for (int q = 1; q < RB; ++q) SDC_TALL_NAME_B(q);
     __builtin_amdgcn_sched_barrier(0);
   }
   if constexpr (XNORM) {
@@ -1058,40 +1091,55 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
   constexpr int RP = TR + 4;
   float* red = reinterpret_cast<float*>(smem);                  // [RS_WAVES][TC][RP]
   static_assert(RS_WAVES * TC * RP * 4 <= (int)sizeof(smem), "the reduction fits the shared memory");
-#pragma unroll
-  for (int i = 0; i < TRF; ++i)
-#pragma unroll
-    for (int n = 0; n < TCF; ++n)
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4)
-        *reinterpret_cast<f32x4*>(red + (w * TC + 32 * n + r) * RP + 32 * i + 8 * r4 + 4 * h) =
-            f32x4{acc[i][n][4 * r4], acc[i][n][4 * r4 + 1], acc[i][n][4 * r4 + 2], acc[i][n][4 * r4 + 3]};
-  __syncthreads();
   const int64_t me = g.m;
-  float* const Eh = g.E + half * N * me;
   constexpr int LPC = TR / 4;                                   // lanes per column (4 rows each)
   constexpr int CPI = 64 / LPC;                                 // columns per store instruction
   const int lr = lane % LPC, lc = lane / LPC;
+  // (int8: one round per digit, its plane after the other's; the wave partials are int32 and added as integers)
 #pragma unroll
-  for (int gq = 0; gq < TC / (RS_WAVES * CPI); ++gq) {
-    const int cl = (w * (TC / (RS_WAVES * CPI)) + gq) * CPI + lc;   // the tile's column
-    f32x4 v = *reinterpret_cast<const f32x4*>(red + cl * RP + 4 * lr);
+  for (int pa = 0; pa < NACC; ++pa) {
+    if (pa > 0) __syncthreads();                                // (the previous round's reads are done)
 #pragma unroll
-    for (int q = 1; q < RS_WAVES; ++q) v += *reinterpret_cast<const f32x4*>(red + (q * TC + cl) * RP + 4 * lr);
-    const int64_t row = r0 + 4 * lr;
-    const int64_t col = c0 + cl;
-    if (col < N) {
-      float* Ec = Eh + col * me;
-      if (row + 4 <= rend && (me % 4) == 0 && (row % 4) == 0) {
-        *reinterpret_cast<f32x4*>(Ec + row) = v;
-      } else {
+    for (int i = 0; i < TRF; ++i)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (row + e < rend) Ec[row + e] = v[e];
+      for (int n = 0; n < TCF; ++n)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          *reinterpret_cast<f32x4*>(red + (w * TC + 32 * n + r) * RP + 32 * i + 8 * r4 + 4 * h) =
+              f32x4{acc[pa][i][n][4 * r4], acc[pa][i][n][4 * r4 + 1], acc[pa][i][n][4 * r4 + 2],
+                    acc[pa][i][n][4 * r4 + 3]};
+    __syncthreads();
+    float* const Eh = g.E + (half * NACC + pa) * N * me;
+#pragma unroll
+    for (int gq = 0; gq < TC / (RS_WAVES * CPI); ++gq) {
+      const int cl = (w * (TC / (RS_WAVES * CPI)) + gq) * CPI + lc;   // the tile's column
+      f32x4 v = *reinterpret_cast<const f32x4*>(red + cl * RP + 4 * lr);
+#pragma unroll
+      for (int q = 1; q < RS_WAVES; ++q) {
+        const f32x4 u = *reinterpret_cast<const f32x4*>(red + (q * TC + cl) * RP + 4 * lr);
+        if constexpr (AT == 2)
+          v = __builtin_bit_cast(f32x4, __builtin_bit_cast(i32x4, v) + __builtin_bit_cast(i32x4, u));
+        else
+          v += u;
+      }
+      const int64_t row = r0 + 4 * lr;
+      const int64_t col = c0 + cl;
+      if (col < N) {
+        float* Ec = Eh + col * me;
+        if (row + 4 <= rend && (me % 4) == 0 && (row % 4) == 0) {
+          *reinterpret_cast<f32x4*>(Ec + row) = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (row + e < rend) Ec[row + e] = v[e];
+        }
       }
     }
   }
 }
+
+#undef SDC_TALL_WAIT_B
+#undef SDC_TALL_NAME_B
 
 // Parts [3][N][kp] (k-contiguous per column, column stride spc) -> fragment order for rs_gemm_kernel: element e of
 // lane l of fragment (step s, part p, column fragment f) is part p, column 32 f + l % 32 (zero past N), depth
@@ -1110,6 +1158,24 @@ __global__ __launch_bounds__(256) void parts_frag_kernel(const uint16_t* parts, 
     u32x4 v = {0u, 0u, 0u, 0u};
     if (col < N) v = *reinterpret_cast<const u32x4*>(parts + (p * N + col) * spc + kk);
     *reinterpret_cast<u32x4*>(out + i * 8) = v;
+  }
+}
+
+// int8 digits [2][N][spc] (bytes, k-contiguous per column) -> the tall GEMM's int8 fragment order: byte e of lane l
+// of fragment (step s, digit p, column fragment f) is digit p, column 32 f + l % 32 (zero past N), depth
+// 64 (s / 4) + 32 (l / 32) + 8 (s % 4) + e -- the depths the A fragment of that lane reads.  One thread per 8 bytes.
+__global__ __launch_bounds__(256) void digit_frag_kernel(const uint8_t* parts, int64_t spc, int64_t N, int64_t k,
+                                                         uint8_t* out) {
+  const int64_t ncf = sdc_cdiv(N, 32), nst = k / 16;
+  const int64_t total = nst * 2 * ncf * 64;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int lane = (int)(i % 64);
+    const int64_t fr = i / 64, f = fr % ncf, p = (fr / ncf) % 2, s = fr / (2 * ncf);
+    const int64_t col = 32 * f + lane % 32;
+    const int64_t kk = 64 * (s / 4) + 32 * (lane / 32) + 8 * (s % 4);
+    u32x2 v = {0u, 0u};
+    if (col < N) v = *reinterpret_cast<const u32x2*>(parts + (p * N + col) * spc + kk);
+    *reinterpret_cast<u32x2*>(out + i * 8) = v;
   }
 }
 
@@ -1145,14 +1211,17 @@ int sdc_rs_gemm_launch(int dtype, GemmArgs g, int role, hipStream_t stream) {
 // only): rows grouped by the groups' cumulative ends, group q's fragments at g.B + q g.sbb, row norms always.
 // Returns SDC_EUNSUPPORTED where it does not apply.
 int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream) {
-  if (dtype != SDC_BF16 && dtype != SDC_FP16 && dtype != SDC_FP8) return SDC_EUNSUPPORTED;
-  const int64_t es = dtype == SDC_FP8 ? 1 : 2, kmul = (dtype == SDC_FP8 ? RS_WAVES * 128 : RS_KMULT) * g.splits;
+  if (dtype != SDC_BF16 && dtype != SDC_FP16 && dtype != SDC_FP8 && dtype != SDC_I8) return SDC_EUNSUPPORTED;
+  const bool byte_a = dtype == SDC_FP8 || dtype == SDC_I8;
+  const int64_t es = byte_a ? 1 : 2, kmul = (byte_a ? RS_WAVES * 128 : RS_KMULT) * g.splits;
   if (g.splits < 1 || g.splits > SDC_MAX_SPLITS || g.sak != 1 || g.k % kmul || (g.sam * es) % 16 ||
       ((uintptr_t)g.A | (uintptr_t)g.B) % 16 || !g.et)
     return SDC_EUNSUPPORTED;
   if (g.goffs && (dtype == SDC_FP8 || g.ngroups < 1 || g.ngroups > GSCAN || g.sbb % 8)) return SDC_EUNSUPPORTED;
   if (g.m < 1 || g.N < 1) return SDC_EINVAL;
-  if (g.short_rows && (dtype != SDC_FP8 || g.goffs || g.xf_blocks)) return SDC_EUNSUPPORTED;
+  if ((g.short_rows || dtype == SDC_I8) && (!byte_a || g.goffs || g.xf_blocks || (dtype == SDC_I8 && g.XN)))
+    return SDC_EUNSUPPORTED;
+  if (dtype == SDC_I8) g.short_rows = 1;                        // (int8: 64-row tiles only)
   const int64_t rtiles = sdc_cdiv(g.m, g.short_rows ? 64 : 32 * SDC_TALL_TRF) + (g.goffs ? g.ngroups : 0);
   if (g.xf_blocks < 0 || (g.xf_blocks && (g.goffs || dtype == SDC_FP8))) return SDC_EINVAL;
   const int64_t blocks = g.splits * rtiles * sdc_cdiv(g.N, 64) + g.xf_blocks;
@@ -1166,6 +1235,8 @@ int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream)
       hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 4, T, 0, true, true>), grid, block, 0, stream, g);
     else
       hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_FP16, 4, T, 0, true, true>), grid, block, 0, stream, g);
+  } else if (dtype == SDC_I8) {
+    hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 5, 2, 2, false>), grid, block, 0, stream, g);
   } else if (dtype == SDC_FP8 && g.short_rows) {
     if (g.XN) hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 3, 2, 1, true>), grid, block, 0, stream, g);
     else hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 3, 2, 1, false>), grid, block, 0, stream, g);
@@ -1210,6 +1281,27 @@ extern "C" int sdc_parts_fragments(const void* parts, int64_t spc, int64_t N, in
                                    hipStream_t stream) {
   SDC_CLEAR_ERRORS();
   return sdc_parts_fragments_sets(parts, spc, 0, 1, N, k, out, stream);
+}
+
+// Bytes of the int8 digits [2][N][k] in the tall GEMM's int8 fragment order (k a multiple of 64).
+extern "C" int64_t sdc_digit_fragments_bytes(int64_t N, int64_t k) {
+  if (N < 1 || k < 64 || k % 64) return 0;
+  return 2 * sdc_cdiv(N, 32) * 32 * k;
+}
+
+// int8 digits [2][N][spc] (k-contiguous per column) -> the int8 fragment order of the tall GEMM.
+extern "C" int sdc_digit_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out,
+                                   hipStream_t stream) {
+  SDC_CLEAR_ERRORS();
+  if (!parts || !out || N < 1 || k < 64 || k % 64 || spc % 8 || spc < k || ((uintptr_t)parts | (uintptr_t)out) % 8)
+    return SDC_EINVAL;
+  const int64_t total = (k / 16) * 2 * sdc_cdiv(N, 32) * 64;
+  const int64_t blocks = sdc_cdiv(total, 256) < 4096 ? sdc_cdiv(total, 256) : 4096;
+  SdcProf prof("digit_frag", stream);
+  hipLaunchKernelGGL(digit_frag_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint8_t*)parts, spc, N,
+                     k, (uint8_t*)out);
+  SDC_LAUNCH_CHECK();
+  return SDC_OK;
 }
 
 // Split of the depth so that tiles x splits fill the GPU (one workgroup per CU), in multiples of the stage depth.

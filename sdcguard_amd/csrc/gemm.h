@@ -48,6 +48,8 @@ extern "C" int64_t sdc_parts_fragments_bytes(int64_t N, int64_t k);
 extern "C" int sdc_parts_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out, hipStream_t stream);
 int sdc_parts_fragments_sets(const void* parts, int64_t spc, int64_t sgp, int64_t groups, int64_t N, int64_t k,
                              void* out, hipStream_t stream);
+extern "C" int64_t sdc_digit_fragments_bytes(int64_t N, int64_t k);
+extern "C" int sdc_digit_fragments(const void* parts, int64_t spc, int64_t N, int64_t k, void* out, hipStream_t stream);
 
 // parts[batch][3 * ncols][kp] from B2T[batch][ncols][k] (fp32), each column divided by
 // scale[batch * sscb + col * scale_stride] first (null: 1); depth kp >= k padded with zeros.

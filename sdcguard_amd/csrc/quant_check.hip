@@ -527,8 +527,9 @@ QLayout qlayout(int kind, int64_t m, int64_t k, int64_t n, int64_t bs) {
   // 128 x 64 tiles over two depth halves where they fill the GPU (192 workgroups or more), else (a short A) 64 x 64
   // tiles over as many depth parts, up to SDC_MAX_SPLITS, as keep within two workgroups a CU
   const int64_t nct = sdc_cdiv(L.ncols, 64);
-  if (kind == 1 && k % 1024 == 0) {
-    if (2 * sdc_cdiv(m, 128) * nct >= 192) {
+  if (k % 1024 == 0) {
+    // (int8: always 64-row tiles, two int32 digit planes a part)
+    if (kind == 1 && 2 * sdc_cdiv(m, 128) * nct >= 192) {
       L.tall = true;
       L.tsplits = 2;
     } else {
@@ -548,7 +549,8 @@ QLayout qlayout(int kind, int64_t m, int64_t k, int64_t n, int64_t bs) {
   L.off_xn = o; o += al(esplits * 2 * m);
   L.off_apad = o; o += al(sdc_cdiv(m * L.kpad, 4));
   L.off_ppad = o; o += al(sdc_cdiv(2 * L.ncols * L.kpad, 4));
-  L.off_frag = o; o += L.tall ? al(sdc_parts_fragments_bytes(L.ncols, k) / 4) : 0;
+  L.off_frag = o;
+  o += L.tall ? al((kind == 0 ? sdc_digit_fragments_bytes(L.ncols, k) : sdc_parts_fragments_bytes(L.ncols, k)) / 4) : 0;
   L.total = o;
   return L;
 }
@@ -643,11 +645,13 @@ extern "C" int sdc_quant_check(int kind, const void* A, int64_t sam, const void*
   int64_t splits = L.splits;
   if (L.tall && tiles && sam % 16 == 0 && (uintptr_t)A % 16 == 0 && spc % 8 == 0 && spc >= k &&
       (uintptr_t)parts % 16 == 0) {
-    // the parts in fragment order (given, or made here), then the tall-tile GEMM with the row norms
+    // the parts in fragment order (given, or made here), then the tall-tile GEMM (fp8: with the row norms; int8:
+    // on bytes, both digits)
     const void* frag = parts_frag;
     if (!frag) {
       frag = ws + L.off_frag;
-      rc = sdc_parts_fragments(parts, spc, L.ncols, k, ws + L.off_frag, stream);
+      rc = kind == 0 ? sdc_digit_fragments(parts, spc, L.ncols, k, ws + L.off_frag, stream)
+                     : sdc_parts_fragments(parts, spc, L.ncols, k, ws + L.off_frag, stream);
       if (rc != SDC_OK) return rc;
     }
     GemmArgs gt = g;
@@ -655,7 +659,10 @@ extern "C" int sdc_quant_check(int kind, const void* A, int64_t sam, const void*
     gt.splits = L.tsplits;
     gt.short_rows = L.short_rows ? 1 : 0;
     gt.et = 1;
-    rc = sdc_rs_gemm_tall_launch(SDC_FP8, gt, 0, stream);
+    if (kind == 0) {
+      gt.sam = sam; gt.k = k; gt.XN = nullptr;                 // (bytes, not the staged GEMM's pairs)
+    }
+    rc = sdc_rs_gemm_tall_launch(kind == 0 ? SDC_I8 : SDC_FP8, gt, 0, stream);
     if (rc == SDC_OK) splits = L.tsplits;
   }
   if (rc == SDC_EUNSUPPORTED) rc = sdc_gemm_launch(kind == 0 ? SDC_I8 : SDC_FP8, g, 1, stream);

@@ -113,6 +113,27 @@ def _fp8_fragments(P: torch.Tensor, ncols: int, k: int) -> Optional[torch.Tensor
     return _fragments(P, ncols, k)
 
 
+def _i8_fragments(P: torch.Tensor, ncols: int, k: int) -> Optional[torch.Tensor]:
+    """The int8 weight's two digit planes in the tall-tile GEMM's int8 fragment order (sdc_digit_fragments), made
+    once and kept on the parts tensor; None where that GEMM does not apply (depth not a multiple of 1024)."""
+    from . import _lib
+    if k % 1024 or P.stride(1) % 8 or P.data_ptr() % 16:
+        return None
+    key = (P.data_ptr(), P._version, ncols, k)
+    hit = getattr(P, "_sdc_frag8", None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    L = _lib.lib()
+    out = torch.empty(int(L.sdc_digit_fragments_bytes(ncols, k)), dtype=torch.uint8, device=P.device)
+    _lib.check(L.sdc_digit_fragments(P.data_ptr(), P.stride(1), ncols, k, out.data_ptr(), _lib.stream_of(P)),
+               "sdc_digit_fragments")
+    try:
+        P._sdc_frag8 = (key, out)
+    except (AttributeError, RuntimeError):
+        pass
+    return out
+
+
 def quant_zscores(A: torch.Tensor, consts: QuantChecksums, C: torch.Tensor, *, sa: Optional[torch.Tensor] = None,
                   unit: float = UNIT_FP8, nfma: Optional[int] = NFMA_FP8, z: float = ALARM,
                   scores_out: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
@@ -142,7 +163,7 @@ def quant_zscores(A: torch.Tensor, consts: QuantChecksums, C: torch.Tensor, *, s
     tab = sign_table(C.device)
     P = consts.parts
     Av = A.view(torch.uint8) if kind == 1 else A
-    frag = _fp8_fragments(P, 2 * nb, k) if kind == 1 else None
+    frag = _fp8_fragments(P, 2 * nb, k) if kind == 1 else _i8_fragments(P, 2 * nb, k)
     rc = L.sdc_quant_check(
         kind, Av.data_ptr(), Av.stride(0), P.data_ptr(), P.stride(1), None if frag is None else frag.data_ptr(),
         None if sa is None else sa.data_ptr(),

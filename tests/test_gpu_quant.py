@@ -149,6 +149,27 @@ def test_fp8_tall_gemm_matches_oracle(out, m, k, n):
             assert (res["row"], res["block"]) == (i, j // 128), (t, i, j, res)
 
 
+def test_fp8_bf16_output_term_worst_case():
+    """Outputs rounded to bf16 the same way by the most the format allows (tests/test_oracle_quant.py builds them):
+    the HIP check scores every block as the oracle does -- 5.4 < z <= 5.66 for 2^-9 of the value, about 11 for 2^-8 --
+    and flags the same blocks."""
+    from sdcguard_amd import modes
+    from tests.test_oracle_quant import worst_rounding_problem
+    A, B, sa, sb, exact, c16 = worst_rounding_problem()
+    Aq = torch.from_numpy(A).float().to(torch.float8_e4m3fn).cuda()
+    Bq = torch.from_numpy(B).float().to(torch.float8_e4m3fn).cuda()
+    consts = modes.QuantChecksums.make(Bq, torch.from_numpy(sb).float().cuda())
+    C = torch.from_numpy(c16).bfloat16().cuda()
+    zs = torch.full((C.shape[0], C.shape[1] // 128), -7.0, device="cuda")
+    res = modes.resolve(modes.quant_zscores(Aq, consts, C, sa=torch.from_numpy(sa).float().cuda(), scores_out=zs))
+    o = quant.fp8_judge(A, B, sa, sb, c16, quant.patterns(1), c_bf16=True)
+    zg = zs.cpu().numpy()
+    assert np.allclose(zg, o["z"], rtol=1e-3, atol=1e-3), (zg, o["z"])
+    assert (5.4 < zg[:2]).all() and (zg[:2] <= np.sqrt(128) / 2 + 1e-3).all(), zg
+    assert res["wrong_blocks"] == o["wrong_blocks"] == 2, res
+    print(f"worst-case bf16 rounding: z {zg[:, 0]} (oracle {o['z'][:, 0]})")
+
+
 def test_fp8_scaled_faults_located():
     from sdcguard_amd import modes
     Aq, Bq, sa, sb, C = _scaled_problem(9, 64, 512, 512)
@@ -162,6 +183,32 @@ def test_fp8_scaled_faults_located():
             c[r, j] = {"nan": float("nan"), "huge": 1e30, "inf": float("inf")}[kind]
         res = modes.resolve(modes.quant_zscores(Aq, consts, c, sa=sa))
         assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (r, j // 128), (kind, res)
+
+
+@pytest.mark.parametrize("m,k,n", [(1000, 3072, 2048), (64, 1024, 4096), (300, 2048, 1000)])
+def test_int8_tall_gemm_matches_oracle(m, k, n):
+    """An int8 check whose depth is a multiple of 1024 runs its expected side on the tall-tile GEMM (int8 MFMA on
+    64-row tiles over up to 8 depth parts, one int32 plane per digit and part): every block's two exact sums equal
+    the oracle's (1000 x 3072 x 2048: six parts, a ragged last row tile; 64 x 1024 x 4096: two; 300 x 2048 x 1000: a
+    ragged last block), int8 values at both ends included, and a +1 in one output is that block alone."""
+    from sdcguard_amd import modes
+    g = torch.Generator(device="cuda").manual_seed(m + k + n)
+    A = torch.randint(-128, 128, (m, k), device="cuda", generator=g, dtype=torch.int32).to(torch.int8)
+    B = torch.randint(-127, 128, (k, n), device="cuda", generator=g, dtype=torch.int32).to(torch.int8)
+    A[0, :] = -128
+    A[1, :] = 127
+    C = (A.double() @ B.double()).to(torch.int32)
+    consts = modes.QuantChecksums.make(B)
+    res = modes.resolve(modes.quant_zscores(A, consts, C))
+    o = quant.int8_judge(A.cpu().numpy().astype(np.int64), B.cpu().numpy().astype(np.int64),
+                         C.cpu().numpy().astype(np.int64), quant.patterns(1))
+    assert res["wrong_blocks"] == o["wrong_blocks"] == 0, res
+    i, j = m - 1, n - 1
+    C[i, j] += 1
+    zs = torch.full((m, -(-n // 128)), -7.0, device="cuda")
+    res = modes.resolve(modes.quant_zscores(A, consts, C, scores_out=zs))
+    assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (i, j // 128), res
+    assert int((zs > 6).sum()) == 1 and float(zs[i, j // 128]) > 6
 
 
 def test_int8_known_answer_at_the_largest_values():

@@ -143,11 +143,45 @@ def test_fp8_scaled_faults():
 
 
 def test_fp8_bf16_output_adds_its_rounding():
-    """A bf16 result: its rounding (at most 2^-9 per output) is priced by the added 2^-8 |C_blk| term -- the unit
-    the reference's serving check gives bf16 outputs -- and lowers every z."""
+    """A bf16 result: its rounding (half a unit in the last place: between 2^-9 and 2^-8 of the output, by where it
+    sits in its binade) is priced by the added 2^-8 |C_blk| term -- the unit the reference's serving check gives
+    bf16 outputs -- and lowers every z."""
     A, B, sa, sb, C = _fp8_problem(4)
     c16 = torch.from_numpy(C).bfloat16().float().numpy().astype(np.float64)
     W = quant.patterns(1)
     z0 = quant.fp8_judge(A, B, sa, sb, c16, W)["z"]
     res = quant.fp8_judge(A, B, sa, sb, c16, W, c_bf16=True)
     assert res["wrong_blocks"] == 0 and res["worst_z"] < 1.0 and (res["z"] < z0).all()
+
+
+def worst_rounding_problem():
+    """Rows whose 128 outputs of a block all round the same way by the most bf16 allows: C = sa_i (1 x 1 fp8 ones),
+    sa_i chosen so the exact output sits just below / above a rounding midpoint.  Row 0: just below 2 - 2^-8 (rounds
+    down by 2^-8 - 2^-20: 2^-9 of the value), row 1: just above it (rounds up to 2: 2^-9), row 2: just below
+    1 + 2^-8 (rounds down to 1: 2^-8 of the value), row 3: 1.5 (exact).  Returns fp8 values, scales, the exact C and
+    its bf16 rounding (float64)."""
+    m, n = 4, 256
+    v = np.array([2 - 2.0 ** -8 - 2.0 ** -20, 2 - 2.0 ** -8 + 2.0 ** -20, 1 + 2.0 ** -8 - 2.0 ** -20, 1.5])
+    A, B = np.ones((m, 1)), np.ones((1, n))
+    sa, sb = v.astype(np.float32).astype(np.float64), np.ones(n)
+    exact = np.repeat(sa[:, None], n, axis=1)
+    c16 = torch.from_numpy(exact).bfloat16().double().numpy()
+    return A, B, sa, sb, exact, c16
+
+
+def test_fp8_bf16_output_term_worst_case():
+    """The bf16-output term against its worst case: every output of a block rounded the same way by 2^-9 of its
+    value scores sqrt(128) / 2 = 5.66 units less the other noise terms' share and the rounded output's larger norm
+    (here 3% at most): in (5.4, 5.66], below the threshold.  By 2^-8 of the value (just above a power of two) the same construction scores about 11: the term
+    is a unit-roundoff noise model, as the reference's u = 2^-8 for bf16 outputs, not a worst-case bound.  A term of
+    2^-9, or none, would score the first rows 11.2 and about 90; one of 2^-7 would score them 2.8."""
+    A, B, sa, sb, exact, c16 = worst_rounding_problem()
+    W = quant.patterns(1)
+    res = quant.fp8_judge(A, B, sa, sb, c16, W, c_bf16=True)
+    z = res["z"]
+    assert (5.4 < z[0]).all() and (z[0] <= np.sqrt(128) / 2).all(), z[0]
+    assert (5.4 < z[1]).all() and (z[1] <= np.sqrt(128) / 2).all(), z[1]
+    assert (z[2] > 10.5).all() and (z[2] < np.sqrt(128)).all(), z[2]
+    assert (z[3] == 0).all()
+    # the exact outputs score (near) zero: what the rows score is their rounding alone
+    assert quant.fp8_judge(A, B, sa, sb, exact, W, c_bf16=True)["worst_z"] < 1e-3
