@@ -306,6 +306,10 @@ __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
   const int32_t* btr = a.bt + s.r * a.sbt;
   const uint16_t* kvh = a.kv + hk * a.skh;
   auto block_of = [&](int64_t t) { return a.nshift >= 0 ? (t >> a.nshift) : t / a.N; };
+  // the sampled row's output (what the judging workgroup compares) and q, loaded beside the block-table entries
+  const float ov = tid < D ? half_to_f32<DT>(a.o[s.i * a.sot + s.hq * a.soh + tid]) : 0.f;
+  float q8[8], qa8[8];
+  load8<DT, false>(a.q + s.i * a.sqt + s.hq * a.sqh, 1, d0, D, q8);
   // the block-table entries of keys t0 .. t1 - 1 into LDS with one round trip (when they fit)
   const int64_t b_first = t1 > t0 ? block_of(t0) : 0;
   const int64_t nbt = t1 > t0 ? block_of(t1 - 1) - b_first + 1 : 0;
@@ -313,10 +317,6 @@ __global__ __launch_bounds__(256) void attn_check_kernel(AttnArgs a) {
   if (bt_lds)
     for (int64_t i = tid; i < nbt; i += 256) sh.bt[i] = btr[b_first + i];
 
-  // the sampled row's output (what the judging workgroup compares), loaded beside q
-  const float ov = tid < D ? half_to_f32<DT>(a.o[s.i * a.sot + s.hq * a.soh + tid]) : 0.f;
-  float q8[8], qa8[8];
-  load8<DT, false>(a.q + s.i * a.sqt + s.hq * a.sqh, 1, d0, D, q8);
 #pragma unroll
   for (int e = 0; e < 8; ++e) qa8[e] = fabsf(q8[e]);
   const float sc = a.scale, gq = a.g_qk * a.scale;
