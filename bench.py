@@ -390,7 +390,7 @@ def bench_serve_bf16(ctx: Ctx) -> dict:
     xb, yb, pb = M * K * 2, M * N * 2, K * 6 * nb * 2
     alg = xb + yb + pb
     amounts = {"expected_gemm": ("mfma", 2.0 * M * K * 6 * nb, "bf16"), "serve_fused": ("hbm", yb, None)}
-    patterns = {"expected_gemm": r"expected_gemm_kernel<0", "serve_fused": r"serve_fused_kernel"}
+    patterns = {"expected_gemm": r"expected_gemm_kernel<0|rs_gemm_tall_kernel<0, 2,", "serve_fused": r"serve_fused_kernel"}
     ent, roof = _roof(km, amounts, name, patterns, a.steps)
 
     def gemm(i):

@@ -41,7 +41,10 @@ extern "C" {
  *     GEMM, then a scoring pass (the reference's SDCGUARD_SERVE_KERNEL=v1|v3 switch); 4 = v3 on `stream` alone.
  *   block_consts (may be NULL): the same per-block constants packed as (nb, 12) fp32, 16-byte aligned, per block
  *     [scale0, scale1, bsum0, bsum1, b2n0, b2n1, b2max0, b2max1, bmax, bmax_bias, 0, 0]: three 16-byte loads
- *     per block instead of ten scattered ones; the separate arrays are still required. */
+ *     per block instead of ten scattered ones; the separate arrays are still required.
+ *   parts_frag (may be NULL; no counterpart in the reference): the parts in sdc_parts_fragments' order, 16-byte
+ *     aligned, made once per layer: with them (k-contiguous 16-bit x, depth a multiple of 512) the expected side
+ *     runs on the register-streamed tall-tile GEMM (two planes of E) instead of the staged one. */
 int64_t sdc_check_static_workspace(int64_t m, int64_t k, int64_t n, int64_t bs);
 int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t sxk, const void* y, int64_t sym, int64_t syn,
                      int64_t m, int64_t k, int64_t n, int64_t bs, const void* parts, int64_t spk, int64_t spc,
@@ -50,7 +53,7 @@ int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t sxk, const v
                      int64_t* state, int counts, int64_t slot, float z, float abs_floor, int64_t* cap_meta,
                      float* cap_data, int64_t cap_stride, int64_t cap_w, int64_t cap_tag, int64_t cap_flags,
                      int64_t cap_slots, void* workspace, int64_t workspace_bytes, float* scores_out, int kernel,
-                     const float* block_consts, hipStream_t stream);
+                     const float* block_consts, const void* parts_frag, hipStream_t stream);
 
 /* ---- check of one matmul (training / one-off) -------------------------------------------------------------
  * Replaces checksum.matmul_zscores (checksum.py:400-432, `_zscores` :435-530) and the Triton group it routes to

@@ -29,7 +29,7 @@ P, I64, I32, F32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
 SIGNATURES = {
     "sdc_check_static_workspace": (I64, [I64, I64, I64, I64]),
     "sdc_check_static": (I32, [I32, P, I64, I64, P, I64, I64, I64, I64, I64, I64, P, I64, I64, I32, P, P, P, P, P,
-                               P, P, P, I32, I64, F32, F32, P, P, I64, I64, I64, I64, I64, P, I64, P, I32, P, P]),
+                               P, P, P, I32, I64, F32, F32, P, P, I64, I64, I64, I64, I64, P, I64, P, I32, P, P, P]),
     "sdc_matmul_check_workspace": (I64, [I64, I64, I64, I64, I64, I64]),
     "sdc_matmul_check": (I32, [I32, P, I64, I64, I64, I64, P, I64, I64, I64, I64, P, I64, I64, I64, I64, I64, I64, I64,
                                I64, P, I32, I64, I64, I64, F32, F32, F32, F32, P, P, P, I64, P, P]),

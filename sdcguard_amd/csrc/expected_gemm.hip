@@ -1110,6 +1110,40 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
                     acc[pa][i][n][4 * r4 + 3]};
     __syncthreads();
     float* const Eh = g.E + (half * NACC + pa) * N * me;
+    if (!g.et) {
+      // a row-major plane ([m][N]): each store instruction writes 4 rows x 64 columns, lane l row 4 gq + l / 16
+      // of the wave's quarter of the tile's rows, columns 4 (l % 16) .. + 3 (the four waves' partials added in
+      // wave order, as below)
+      const int c4 = 4 * (lane & 15);
+#pragma unroll
+      for (int gq = 0; gq < TR / 16; ++gq) {
+        const int rl = w * (TR / 4) + 4 * gq + (lane >> 4);
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = red[(c4 + e) * RP + rl];
+#pragma unroll
+          for (int q = 1; q < RS_WAVES; ++q) {
+            const float u = red[(q * TC + c4 + e) * RP + rl];
+            if constexpr (AT == 2) x = __int_as_float(__float_as_int(x) + __float_as_int(u));
+            else x += u;
+          }
+          v[e] = x;
+        }
+        const int64_t row = r0 + rl, col = c0 + c4;
+        if (row < rend) {
+          float* Er = Eh + row * N;
+          if (col + 4 <= N && (N % 4) == 0) {
+            *reinterpret_cast<f32x4*>(Er + col) = v;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (col + e < N) Er[col + e] = v[e];
+          }
+        }
+      }
+      continue;
+    }
 #pragma unroll
     for (int gq = 0; gq < TC / (RS_WAVES * CPI); ++gq) {
       const int cl = (w * (TC / (RS_WAVES * CPI)) + gq) * CPI + lc;   // the tile's column
@@ -1215,7 +1249,7 @@ int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream)
   const bool byte_a = dtype == SDC_FP8 || dtype == SDC_I8;
   const int64_t es = byte_a ? 1 : 2, kmul = (byte_a ? RS_WAVES * 128 : RS_KMULT) * g.splits;
   if (g.splits < 1 || g.splits > SDC_MAX_SPLITS || g.sak != 1 || g.k % kmul || (g.sam * es) % 16 ||
-      ((uintptr_t)g.A | (uintptr_t)g.B) % 16 || !g.et)
+      ((uintptr_t)g.A | (uintptr_t)g.B) % 16 || (!g.et && (g.goffs || ((uintptr_t)g.E % 16))))
     return SDC_EUNSUPPORTED;
   if (g.goffs && (dtype == SDC_FP8 || g.ngroups < 1 || g.ngroups > GSCAN || g.sbb % 8)) return SDC_EUNSUPPORTED;
   if (g.m < 1 || g.N < 1) return SDC_EINVAL;
@@ -1246,6 +1280,10 @@ int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream)
   } else if (role == 1) {
     if (dtype == SDC_BF16) hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 1, T, 0, false>), grid, block, 0, stream, g);
     else hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_FP16, 1, T, 0, false>), grid, block, 0, stream, g);
+  } else if (g.XN) {
+    // (the serving check: its x row norms in the same pass)
+    if (dtype == SDC_BF16) hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 2, T, 0, true>), grid, block, 0, stream, g);
+    else hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_FP16, 2, T, 0, true>), grid, block, 0, stream, g);
   } else {
     if (dtype == SDC_BF16) hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 0, T, 0, false>), grid, block, 0, stream, g);
     else hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_FP16, 0, T, 0, false>), grid, block, 0, stream, g);

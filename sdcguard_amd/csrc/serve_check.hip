@@ -11,6 +11,7 @@
 //      state row with one integer atomic maximum (only when it raises the row), counts with atomic adds.
 #include "blocksums.h"
 #include "judge.h"
+#include "gemm.h"
 #include "profile.h"
 #include "streams.h"
 
@@ -230,7 +231,7 @@ extern "C" int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t s
                                 float abs_floor, int64_t* cap_meta, float* cap_data, int64_t cap_stride,
                                 int64_t cap_w, int64_t cap_tag, int64_t cap_flags, int64_t cap_slots,
                                 void* workspace, int64_t workspace_bytes, float* scores_out, int kernel,
-                                const float* block_consts, hipStream_t stream) {
+                                const float* block_consts, const void* parts_frag, hipStream_t stream) {
   SDC_CLEAR_ERRORS();
   if (m < 0 || n < 0 || k < 0) return SDC_EINVAL;
   if (m == 0 || n == 0) return SDC_OK;                     // nothing to check, not counted (serve.py:435)
@@ -275,11 +276,29 @@ extern "C" int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t s
   a.vec = (syn == 1) && (sym % 8 == 0) && (bs % 8 == 0) && ((uintptr_t)y % 16 == 0);
   a.yv.vec = a.vec;
   if (cap_meta && (!cap_data || cap_w < bs)) return SDC_EINVAL;
+  // The expected side: the register-streamed tall-tile GEMM (two depth halves, row-major planes, x's row norms in
+  // the same pass) where the parts come in fragment order and the shape suits it, else the staged GEMM
+  auto expected = [&]() -> int {
+    if (parts_frag && nparts == 3 && spk == 1 && sxk == 1 && splits >= 2 && k % 512 == 0 &&
+        2 * sdc_cdiv(m, 128) * sdc_cdiv(ncols, 64) >= 192) {
+      GemmArgs g{};
+      g.A = (const uint16_t*)x; g.sam = sxm; g.sak = 1;
+      g.B = parts_frag; g.m = m; g.k = k; g.N = ncols; g.splits = 2;
+      g.E = E; g.XN = XN; g.et = 0;
+      g.prof_name = "expected_gemm";
+      const int rc = sdc_rs_gemm_tall_launch(dtype, g, 0, stream);
+      if (rc != SDC_EUNSUPPORTED) {
+        a.splits = 2;
+        return rc;
+      }
+    }
+    return sdc_expected_launch(dtype, x, sxm, sxk, parts, spk, spc, nparts, m, k, ncols, splits, E, XN, stream);
+  };
   // persistent grids: about four workgroups per CU (256 CUs), fewer for small batches
   const int64_t tiles = sdc_cdiv(m * nb, 64);
   const unsigned grid = (unsigned)(sdc_cdiv(tiles, 4) < 1024 ? sdc_cdiv(tiles, 4) : 1024);
   if (!split_design) {
-    int rc = sdc_expected_launch(dtype, x, sxm, sxk, parts, spk, spc, nparts, m, k, ncols, splits, E, XN, stream);
+    int rc = expected();
     if (rc != SDC_OK) return rc;
     SdcProf prof("serve_fused", stream);
     if (dtype == SDC_BF16)
@@ -306,7 +325,7 @@ extern "C" int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t s
       return SDC_ELAUNCH;
     }
   }
-  int rc = sdc_expected_launch(dtype, x, sxm, sxk, parts, spk, spc, nparts, m, k, ncols, splits, E, XN, stream);
+  int rc = expected();
   if (kernel != 4) {
     const int jc = sdc_join(stream, side);
     if (rc == SDC_OK) rc = jc;

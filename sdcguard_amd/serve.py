@@ -215,6 +215,11 @@ def check_static_impl(x2: torch.Tensor, y2: torch.Tensor, parts: torch.Tensor, p
         if t.dtype != torch.float32 or not t.is_contiguous():
             raise ValueError("layer constants must be contiguous fp32 tensors")
     L = _lib.lib()
+    # the parts in fragment order for the tall-tile GEMM (made once, kept on the parts tensor), where it applies
+    frag = None
+    if k % 512 == 0 and x2.stride(1) == 1 and x2.data_ptr() % 16 == 0 and (x2.stride(0) * x2.element_size()) % 16 == 0:
+        from .linear import _fragments
+        frag = _fragments(P, 2 * nb, k)
     ws_bytes = int(L.sdc_check_static_workspace(m, k, n, bs))
     ws = _lib.workspace(y2.device, ws_bytes)
     row = state.data_ptr() + slot * state.stride(0) * state.element_size()
@@ -227,7 +232,7 @@ def check_static_impl(x2: torch.Tensor, y2: torch.Tensor, parts: torch.Tensor, p
         cap_data.stride(0) if capture else 0, int(cap_w), int(cap_tag), CAP_FLAGS, CAPTURE_SLOTS,
         ws.data_ptr(), ws_bytes, None if scores_out is None else scores_out.data_ptr(),
         kernel_mode() if kernel is None else {"v1": 1, "v3": 3, "v3-serial": 4}[kernel],
-        _packed_consts(scale, b2n, b2max, bmax, bmax_bias, bsum).data_ptr(), _lib.stream_of(y2))
+        _packed_consts(scale, b2n, b2max, bmax, bmax_bias, bsum).data_ptr(), _lib.ptr(frag), _lib.stream_of(y2))
     _lib.check(rc, "sdc_check_static")
 
 
