@@ -404,8 +404,13 @@ __device__ __forceinline__ void train_pair(const TrainArgs& a, int64_t p, float 
     fl[c] = f < inf ? f : bound * (float)(1e-5 * 128.0);
   }
   float d0, d1;
-  const float z0 = judge_one(e0, pl, noise, cn, fl[0], bound, wf, l1, true, a, d0);
-  const float z1 = judge_one(e1, sg, noise, cn, fl[1], bound, wf, l1, false, a, d1);
+  bool ok0, ok1;
+  float z0 = judge_one_clean(e0, pl, noise, cn, fl[0], bound, wf, l1, true, a, d0, ok0);
+  float z1 = judge_one_clean(e1, sg, noise, cn, fl[1], bound, wf, l1, false, a, d1, ok1);
+  if (!(ok0 && ok1)) {                           // (non-finite inputs or an "impossible" checksum: the full rules)
+    z0 = judge_one(e0, pl, noise, cn, fl[0], bound, wf, l1, true, a, d0);
+    z1 = judge_one(e1, sg, noise, cn, fl[1], bound, wf, l1, false, a, d1);
+  }
   if (a.zdump) {
     a.zdump[2 * p] = z0;
     a.zdump[2 * p + 1] = z1;
