@@ -511,7 +511,7 @@ int64_t quant_splits(int kind, int64_t m, int64_t k, int64_t ncols) {
 
 struct QLayout {
   int64_t nb, rem, ncols, splits, nacc, kpad, off_e, off_xn, off_apad, off_ppad, off_frag, total;   // in floats
-  bool tall;                       // fp8: the tall-tile register-streamed GEMM where the shape allows
+  bool tall;                       // the tall-tile register-streamed GEMM where the shape allows
   bool short_rows;                 // (its 64-row tiles, for a short A)
   int64_t tsplits;                 // (its depth parts: planes of E)
 };
@@ -523,12 +523,13 @@ QLayout qlayout(int kind, int64_t m, int64_t k, int64_t n, int64_t bs) {
   L.ncols = 2 * L.nb;
   L.nacc = kind == 0 ? 2 : 1;
   L.splits = quant_splits(kind, m, kind == 0 ? (k + 1) / 2 : k, L.ncols);
-  // an fp8 GEMM on the register-streamed tall-tile kernel (depth a multiple of 1024, the parts in fragment order):
-  // 128 x 64 tiles over two depth halves where they fill the GPU (192 workgroups or more), else (a short A) 64 x 64
-  // tiles over as many depth parts, up to SDC_MAX_SPLITS, as keep within two workgroups a CU
+  // the GEMM on the register-streamed tall-tile kernel (depth a multiple of 1024, the parts in fragment order):
+  // fp8 takes 128 x 64 tiles over two depth halves where they fill the GPU (192 workgroups or more), else (a short
+  // A, and int8 always) 64 x 64 tiles over as many depth parts, up to SDC_MAX_SPLITS, as keep within two workgroups
+  // a CU
   const int64_t nct = sdc_cdiv(L.ncols, 64);
   if (k % 1024 == 0) {
-    // (int8: always 64-row tiles, two int32 digit planes a part)
+    // (int8: two int32 digit planes a part)
     if (kind == 1 && 2 * sdc_cdiv(m, 128) * nct >= 192) {
       L.tall = true;
       L.tsplits = 2;
