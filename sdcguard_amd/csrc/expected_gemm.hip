@@ -883,21 +883,25 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
   }
   using BT = typename std::conditional<AT == 2, u32x2, u32x4>::type;
   BT rb[RB][NP][TCF];
-  auto issue_a4 = [&](int sg, int I0) {
+  // A instruction I of segment sg into its half of the ring (past the last segment: the last again)
+  auto issue_a1 = [&](int sg, int I) {
     const int s2 = sg < lastseg ? sg : lastseg;
     uint8_t* dst = abuf + (sg & 1) * RT_SEGB;
-#pragma unroll
-    for (int I = I0; I < I0 + APS; ++I)
-      sdc_pipe::lds_load16(abase + arow[I] + 128 * (int64_t)s2, (uint16_t*)(dst + 1024 * I));
+    sdc_pipe::lds_load16(abase + arow[I] + 128 * (int64_t)s2, (uint16_t*)(dst + 1024 * I));
   };
-  // part p of B(st) into slot `slot`
-  auto issue_bp = [&](int slot, int st, int p) {
-    const uint16_t* q = bq + (int64_t)(st < last ? st : last) * bstep + p * ncf * FRAG;
+  auto issue_a4 = [&](int sg, int I0) {
 #pragma unroll
-    for (int n = 0; n < TCF; ++n) {
-      if constexpr (AT == 2) asm volatile("global_load_dwordx2 %0, %1, off" : "+v"(rb[slot][p][n]) : "v"(q + bf[n]));
-      else asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(rb[slot][p][n]) : "v"(q + bf[n]));
-    }
+    for (int I = I0; I < I0 + APS; ++I) issue_a1(sg, I);
+  };
+  // column fragment n of part p of B(st) into slot `slot`
+  auto issue_b1 = [&](int slot, int st, int p, int n) {
+    const uint16_t* q = bq + (int64_t)(st < last ? st : last) * bstep + p * ncf * FRAG;
+    if constexpr (AT == 2) asm volatile("global_load_dwordx2 %0, %1, off" : "+v"(rb[slot][p][n]) : "v"(q + bf[n]));
+    else asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(rb[slot][p][n]) : "v"(q + bf[n]));
+  };
+  auto issue_bp = [&](int slot, int st, int p) {
+#pragma unroll
+    for (int n = 0; n < TCF; ++n) issue_b1(slot, st, p, n);
   };
   auto issue_b = [&](int slot, int st) {
 #pragma unroll
@@ -929,12 +933,13 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
     else                                                                                                          \
       asm volatile("" : "+v"(rb[slot][0][0]), "+v"(rb[slot][0][1]), "+v"(rb[slot][1][0]), "+v"(rb[slot][1][1]));  \
   } while (0)
+  auto read_frag1 = [&](uint32_t L, int jj, FragT* fr, int i) {
+    if constexpr (AT) asm volatile("ds_read_b64 %0, %1" : "=v"(fr[i]) : "v"(L + (uint32_t)ard[i][jj]));
+    else asm volatile("ds_read_b128 %0, %1" : "=v"(fr[i]) : "v"(L + (uint32_t)ard[i][jj]));
+  };
   auto read_frags = [&](uint32_t L, int jj, FragT* fr) {
 #pragma unroll
-    for (int i = 0; i < TRF; ++i) {
-      if constexpr (AT) asm volatile("ds_read_b64 %0, %1" : "=v"(fr[i]) : "v"(L + (uint32_t)ard[i][jj]));
-      else asm volatile("ds_read_b128 %0, %1" : "=v"(fr[i]) : "v"(L + (uint32_t)ard[i][jj]));
-    }
+    for (int i = 0; i < TRF; ++i) read_frag1(L, jj, fr, i);
   };
   const uint32_t lds0 = (uint32_t)(uintptr_t)abuf;
   f32x16 acc[NACC][TRF][TCF];                   // (int8: the int32 sums' bits)
@@ -965,10 +970,13 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
       issue_a4(0, APS * (q + (SPS - RB)));
       issue_b(q, q);
     }
-    // Each step's 24 MFMAs go in three groups (one part each); the loads are issued between the groups: after the
-    // first, the next segment's A pieces and this slot's B fragments of part 0 for RB steps ahead (the MFMAs that
-    // read them are issued), then part 1's, then part 2's.  The next step's A fragments are read from LDS in the
-    // middle of the second group (inside a segment; the first step of a segment reads its own after the wait).
+    // A step issues its MFMAs part by part, each part column by column, and after each MFMA at most one load, so
+    // that the load's issue (which stalls the wave while the CU's memory pipeline is busy) overlaps the MFMA just
+    // issued instead of leaving the matrix core idle: in part 0 the step's share of the next segment's A (a piece
+    // after each of the first APS MFMAs), and in every part each column's B fragment for RB steps ahead, right
+    // after the last MFMA that reads that column's registers (in part 0, after the A pieces).  So the loads still
+    // go out in the order A, B part 0, 1, 2 that the wait counts assume.  The next step's A fragments are read from
+    // LDS during part 1 (inside a segment; the first step of a segment reads its own after the wait).
     FragT fr[2][TRF];
     using AOpT = typename std::conditional<AT == 2, u32x2, u32x4>::type;
     for (int sg = 0; sg < per; ++sg) {
@@ -1003,35 +1011,23 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
             acc[0][i][n] = sdc_pipe::mfma32<MDT>(a[i], rb[sl][p][n], acc[0][i][n]);
         };
 #pragma unroll
-        for (int i = 0; i < TRF; ++i)
+        for (int p = 0; p < NP; ++p)
 #pragma unroll
-          for (int n = 0; n < TCF; ++n) mma(i, n, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        issue_a4(sg + 1, APS * jj);
-        issue_bp(sl, st + RB, 0);
-        __builtin_amdgcn_sched_barrier(0);
+          for (int n = 0; n < TCF; ++n)
 #pragma unroll
-        for (int i = 0; i < TRF / 2; ++i)
+            for (int i = 0; i < TRF; ++i) {
+              const int q = n * TRF + i;                          // the MFMA's place in its part
+              mma(i, n, p);
+              __builtin_amdgcn_sched_barrier(0);
+              if (p == 0 && q < APS) issue_a1(sg + 1, APS * jj + q);
+              if (p == 1 && n == 0 && jj < SPS - 1) read_frag1(L, jj + 1, fr[cur ^ 1], i);
 #pragma unroll
-          for (int n = 0; n < TCF; ++n) mma(i, n, 1);
-        __builtin_amdgcn_sched_barrier(0);
-        if (jj < SPS - 1) read_frags(L, jj + 1, fr[cur ^ 1]);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = TRF / 2; i < TRF; ++i)
-#pragma unroll
-          for (int n = 0; n < TCF; ++n) mma(i, n, 1);
-        __builtin_amdgcn_sched_barrier(0);
-        issue_bp(sl, st + RB, 1);
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (NP == 3) {
-#pragma unroll
-          for (int i = 0; i < TRF; ++i)
-#pragma unroll
-            for (int n = 0; n < TCF; ++n) mma(i, n, 2);
-          __builtin_amdgcn_sched_barrier(0);
-          issue_bp(sl, st + RB, 2);
-        }
+              for (int c = 0; c < TCF; ++c) {                     // column c's B load: after its last reader (and
+                const int qc = c * TRF + TRF - 1;                 // in part 0 after the A pieces)
+                if (q == (p == 0 && qc < APS ? APS : qc)) issue_b1(sl, st + RB, p, c);
+              }
+              __builtin_amdgcn_sched_barrier(0);
+            }
         if constexpr (XNORM) {
           if (do_xn) {
           // the rows' norms over this step's 8 depths of each fragment (packed dot products)

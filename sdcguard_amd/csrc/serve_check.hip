@@ -47,43 +47,61 @@ struct LaneBest {
   int unk = 0;
 };
 
-// Scores pair p (skipped when p >= npairs) from its four sums into the lane's running worst.
-template <int DT>
-__device__ __forceinline__ void score_pair(const ScoreArgs& a, int64_t p, float pl, float sg, float sq, float ab,
-                                           LaneBest& best) {
+// Pair p's expected sums and x row norms over the GEMM's NS depth-split planes (NS at most SDC_MAX_SPLITS), all
+// loads issued before any is used and unconditional: a split index past a.splits reads split 0 (added nowhere), a
+// pair past the last reads the last pair's (scored nowhere).
+template <int NS>
+struct PairE {
+  float2 ev[NS];
+  float xa[NS], xb[NS];
+};
+
+template <int NS>
+__device__ __forceinline__ PairE<NS> load_pair_e(const ScoreArgs& a, int64_t p) {
+  const int64_t pc = p < a.npairs ? p : a.npairs - 1;
+  const int64_t r = (uint32_t)pc / (uint32_t)a.nb, jb = (uint32_t)pc - (uint32_t)r * (uint32_t)a.nb;
+  const float* ep = a.E + r * a.ncols + 2 * jb;
+  const float* xp = a.XN + r;
+  const int64_t estep = a.m * a.ncols, xstep = 2 * a.m;
+  PairE<NS> e;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int64_t sc = s < a.splits ? s : 0;
+    e.ev[s] = *reinterpret_cast<const float2*>(ep + sc * estep);
+    e.xa[s] = xp[sc * xstep];
+    e.xb[s] = xp[sc * xstep + a.m];
+  }
+  return e;
+}
+
+// Scores pair p (skipped when p >= npairs) from its four sums and its loaded planes into the lane's running worst.
+template <int DT, int NS>
+__device__ __forceinline__ void score_pair_e(const ScoreArgs& a, int64_t p, float pl, float sg, float sq, float ab,
+                                             const PairE<NS>& pe, LaneBest& best) {
   if (p >= a.npairs) return;
   const int64_t r = (uint32_t)p / (uint32_t)a.nb, jb = (uint32_t)p - (uint32_t)r * (uint32_t)a.nb;
   const bool last = (jb == a.nb - 1) && (a.rem > 0);
   const float wf = (float)(last ? a.rem : a.bs);
-  // the GEMM's depth-split planes (at most SDC_MAX_SPLITS): every load issued before the first add, unconditional
-  // (a split index past a.splits reads split 0 and is not added)
-  const float* ep = a.E + r * a.ncols + 2 * jb;
-  const float* xp = a.XN + r;
-  const int64_t estep = a.m * a.ncols, xstep = 2 * a.m;
-  float2 ev[SDC_MAX_SPLITS];
-  float xa[SDC_MAX_SPLITS], xb[SDC_MAX_SPLITS];
+  // the planes added in split order
+  float e0 = pe.ev[0].x, e1 = pe.ev[0].y, asq = pe.xa[0], asum = pe.xb[0];
 #pragma unroll
-  for (int s = 0; s < SDC_MAX_SPLITS; ++s) {
-    const int64_t sc = s < a.splits ? s : 0;
-    ev[s] = *reinterpret_cast<const float2*>(ep + sc * estep);
-    xa[s] = xp[sc * xstep];
-    xb[s] = xp[sc * xstep + a.m];
-  }
-  float e0 = ev[0].x, e1 = ev[0].y, asq = xa[0], asum = xb[0];
-#pragma unroll
-  for (int s = 1; s < SDC_MAX_SPLITS; ++s) {
+  for (int s = 1; s < NS; ++s) {
     if (s < a.splits) {
-      e0 += ev[s].x;
-      e1 += ev[s].y;
-      asq += xa[s];
-      asum += xb[s];
+      e0 += pe.ev[s].x;
+      e1 += pe.ev[s].y;
+      asq += pe.xa[s];
+      asum += pe.xb[s];
     }
   }
   PairScore ps;
   if (a.packed) {
     const f32x4 c0 = a.packed[3 * jb], c1 = a.packed[3 * jb + 1], c2 = a.packed[3 * jb + 2];
-    ps = judge_serve(pl, sg, sq, ab, fsqrt(asq), asum, e0, e1, c0.x, c0.y, c0.z, c0.w, c2.x, c2.y, c1.x, c1.y,
-                     c1.z, c1.w, wf, a);
+    bool ok;
+    ps = judge_serve_clean(pl, sg, sq, ab, fsqrt(asq), asum, e0, e1, c0.x, c0.y, c0.z, c0.w, c2.x, c2.y, c1.x, c1.y,
+                           c1.z, c1.w, wf, a, ok);
+    if (!ok)                                   // (non-finite inputs or an "impossible" pair: the full rules)
+      ps = judge_serve(pl, sg, sq, ab, fsqrt(asq), asum, e0, e1, c0.x, c0.y, c0.z, c0.w, c2.x, c2.y, c1.x, c1.y,
+                       c1.z, c1.w, wf, a);
   } else {
     ps = judge_serve(pl, sg, sq, ab, fsqrt(asq), asum, e0, e1, a.scale[2 * jb], a.scale[2 * jb + 1],
                      a.bsum[2 * jb], a.bsum[2 * jb + 1], a.bmax[jb], a.bmb[jb], a.b2n[2 * jb], a.b2n[2 * jb + 1],
@@ -100,6 +118,14 @@ __device__ __forceinline__ void score_pair(const ScoreArgs& a, int64_t p, float 
   best.key = k1 > best.key ? k1 : best.key;
   best.keyd = d1 > best.keyd ? d1 : best.keyd;
   best.unk += ps.unk;
+}
+
+// The same with the planes loaded here.
+template <int DT>
+__device__ __forceinline__ void score_pair(const ScoreArgs& a, int64_t p, float pl, float sg, float sq, float ab,
+                                           LaneBest& best) {
+  if (p >= a.npairs) return;
+  score_pair_e<DT, SDC_MAX_SPLITS>(a, p, pl, sg, sq, ab, load_pair_e<SDC_MAX_SPLITS>(a, p), best);
 }
 
 // The workgroup's worst key into the layer's state row (one atomic maximum, only when it raises the row), the
@@ -165,8 +191,9 @@ __device__ __forceinline__ void report_wg(const ScoreArgs& a, LaneBest best) {
 }
 
 // v1 (one launch after the GEMM): sums and scores in the same pass over y.  Each wave walks tiles of 64 pairs
-// with a grid stride and keeps its worst key; the workgroup reports once at the end.
-template <int DT>
+// with a grid stride and keeps its worst key; the workgroup reports once at the end.  A tile's expected sums (NS
+// planes: 2 from the tall-tile GEMM) are loaded before its outputs, so both arrive in one round trip.
+template <int DT, int NS>
 __global__ __launch_bounds__(256) void serve_fused_kernel(ScoreArgs a) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, q = lane & 3;
   uint32_t sg2[16];
@@ -174,10 +201,11 @@ __global__ __launch_bounds__(256) void serve_fused_kernel(ScoreArgs a) {
   LaneBest best;
   const int64_t tiles = (a.npairs + 63) / 64;
   for (int64_t tile = (int64_t)blockIdx.x * 4 + w; tile < tiles; tile += (int64_t)gridDim.x * 4) {
-    const int64_t base = tile * 64;
+    const int64_t base = tile * 64, p = base + q * 16 + (lane >> 2);
+    const PairE<NS> pe = load_pair_e<NS>(a, p);
     float pl, sg, sq, ab;
     pair_sums<DT>(a.yv, base, lane, sg2, pl, sg, sq, ab);
-    score_pair<DT>(a, base + q * 16 + (lane >> 2), pl, sg, sq, ab, best);
+    score_pair_e<DT, NS>(a, p, pl, sg, sq, ab, pe, best);
   }
   report_wg<DT>(a, best);
 }
@@ -301,10 +329,15 @@ extern "C" int sdc_check_static(int dtype, const void* x, int64_t sxm, int64_t s
     int rc = expected();
     if (rc != SDC_OK) return rc;
     SdcProf prof("serve_fused", stream);
-    if (dtype == SDC_BF16)
-      hipLaunchKernelGGL(serve_fused_kernel<SDC_BF16>, dim3(grid), dim3(256), 0, stream, a);
+    constexpr int MS = SDC_MAX_SPLITS;
+    if (dtype == SDC_BF16 && a.splits <= 2)
+      hipLaunchKernelGGL((serve_fused_kernel<SDC_BF16, 2>), dim3(grid), dim3(256), 0, stream, a);
+    else if (dtype == SDC_BF16)
+      hipLaunchKernelGGL((serve_fused_kernel<SDC_BF16, MS>), dim3(grid), dim3(256), 0, stream, a);
+    else if (a.splits <= 2)
+      hipLaunchKernelGGL((serve_fused_kernel<SDC_FP16, 2>), dim3(grid), dim3(256), 0, stream, a);
     else
-      hipLaunchKernelGGL(serve_fused_kernel<SDC_FP16>, dim3(grid), dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((serve_fused_kernel<SDC_FP16, MS>), dim3(grid), dim3(256), 0, stream, a);
     SDC_LAUNCH_CHECK();
     return SDC_OK;
   }
