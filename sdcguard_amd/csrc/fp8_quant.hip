@@ -27,7 +27,8 @@ constexpr int64_t ROW_A = 7919, ROW_B = 104729;   // their positions: (step * RO
 constexpr int64_t M32 = 0xFFFFFFFFll, S31 = 0x7FFFFFFFll, EVERY_ROW = 0xFFFFFF;
 enum { C_CALLS, C_SCALE, C_OUTSIDE, C_VALUES, C_ONE, C_LAST, C_RATIO, C_STATIC };
 enum { KIND_SCALE = 1, KIND_OUTSIDE = 2, KIND_VALUES = 3, KIND_STATIC = 4 };
-constexpr int AMAX_BLOCKS = 512;                  // workgroups of fp8q_amax (at most)
+constexpr int AMAX_BLOCKS = 1024;                 // workgroups of fp8q_amax (at most)
+constexpr int AMAX_ROWS = 4;                      // rows a workgroup of fp8q_amax has in flight
 
 template <int DT>
 __device__ __forceinline__ float load_x(const void* p, int64_t i) {
@@ -94,28 +95,52 @@ __global__ __launch_bounds__(256) void fp8q_amax_kernel(Fp8Args a) {
   const int64_t real = real_rows(a);
   uint32_t mi = 0, ma = 0;
   const bool vec = DT != DT_F32 && a.sxk == 1 && a.k % 8 == 0 && a.sxm % 8 == 0 && ((uintptr_t)a.x & 15) == 0;
-  for (int64_t row = blockIdx.x; row < a.m; row += gridDim.x) {
-    uint32_t rm = 0;
+  // AMAX_ROWS rows a workgroup at a time, every 16-byte load of a thread's share of them (two pieces a row) issued
+  // before any is used
+  for (int64_t r0 = (int64_t)blockIdx.x * AMAX_ROWS; r0 < a.m; r0 += (int64_t)gridDim.x * AMAX_ROWS) {
     if (vec) {
-      const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + row * a.sxm);
-      for (int64_t c = t; c < a.k / 8; c += 256) {
-        const uint4 q = p[c];
-        const uint32_t ws[4] = {q.x, q.y, q.z, q.w};
+      const int64_t cpr = a.k / 8;                                  // 16-byte pieces a row
+      for (int64_t c0 = t; c0 < cpr; c0 += 512) {
+        uint4 q[AMAX_ROWS][2];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t lo = abs_bits(lo_of<DT>(ws[e])), hi = abs_bits(hi_of<DT>(ws[e]));
-          rm = lo > rm ? lo : rm;
-          rm = hi > rm ? hi : rm;
+        for (int i = 0; i < AMAX_ROWS; ++i)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int64_t row = r0 + i, c = c0 + 256 * h;
+            q[i][h] = row < a.m && c < cpr ? reinterpret_cast<const uint4*>(
+                                                 reinterpret_cast<const uint16_t*>(a.x) + row * a.sxm)[c]
+                                           : uint4{0u, 0u, 0u, 0u};
+          }
+#pragma unroll
+        for (int i = 0; i < AMAX_ROWS; ++i) {
+          uint32_t rm = 0;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t ws[4] = {q[i][h].x, q[i][h].y, q[i][h].z, q[i][h].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t lo = abs_bits(lo_of<DT>(ws[e])), hi = abs_bits(hi_of<DT>(ws[e]));
+              rm = lo > rm ? lo : rm;
+              rm = hi > rm ? hi : rm;
+            }
+          }
+          ma = rm > ma ? rm : ma;
+          if (r0 + i < real) mi = rm > mi ? rm : mi;
         }
       }
     } else {
-      for (int64_t kk = t; kk < a.k; kk += 256) {
-        const uint32_t v = abs_bits(load_x<DT>(a.x, row * a.sxm + kk * a.sxk));
-        rm = v > rm ? v : rm;
+      for (int i = 0; i < AMAX_ROWS; ++i) {
+        const int64_t row = r0 + i;
+        if (row >= a.m) break;
+        uint32_t rm = 0;
+        for (int64_t kk = t; kk < a.k; kk += 256) {
+          const uint32_t v = abs_bits(load_x<DT>(a.x, row * a.sxm + kk * a.sxk));
+          rm = v > rm ? v : rm;
+        }
+        ma = rm > ma ? rm : ma;
+        if (row < real) mi = rm > mi ? rm : mi;
       }
     }
-    ma = rm > ma ? rm : ma;
-    if (row < real) mi = rm > mi ? rm : mi;
   }
   mi = wave_max_u32_dpp(mi);
   ma = wave_max_u32_dpp(ma);
@@ -344,7 +369,10 @@ int run(Fp8Args a, hipStream_t stream) {
   return SDC_OK;
 }
 
-int64_t amax_blocks(int64_t m) { return m < AMAX_BLOCKS ? (m > 0 ? m : 1) : AMAX_BLOCKS; }
+int64_t amax_blocks(int64_t m) {
+  const int64_t b = (m + AMAX_ROWS - 1) / AMAX_ROWS;
+  return b < 1 ? 1 : (b < AMAX_BLOCKS ? b : AMAX_BLOCKS);
+}
 
 }  // namespace
 

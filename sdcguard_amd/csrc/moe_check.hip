@@ -132,39 +132,69 @@ __device__ __forceinline__ bool bad_id(const MoeArgs& a, int64_t id) {
 __device__ __forceinline__ float wave_sum(float v) { return wave_sum_f32_dpp(v); }
 __device__ __forceinline__ float wave_max(float v) { return wave_max_f32_dpp(v); }
 
+// The vector path reads the rows in chunks of NCH 16-byte pieces a lane and row (chunk cb: pieces at values
+// cb + 8 lane + 512 u, u < NCH), every load of a chunk issued before any is used.
+constexpr int NCH = 4;
+using RowChunk = uint4[RPW][NCH];
+
+__device__ __forceinline__ void rows_load(const uint16_t* const (&w)[RPW], int64_t n, int lane, int64_t cb,
+                                          RowChunk& q) {
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) {
+      const int64_t c = cb + lane * 8 + 512 * u;
+      q[r][u] = (w[r] && c < n) ? *reinterpret_cast<const uint4*>(w[r] + c) : uint4{0u, 0u, 0u, 0u};
+    }
+}
+
 // dots of RPW weight rows (n 16-bit values each, rows w[r], null past the matrix) with a float vector v, the rows
 // read together so each chunk of v (and of sens) is read once for all of them; each lane takes 8 consecutive values
 // at a time when the rows are 16-byte aligned, else one.  With SQ also the sums of squares of the products and the
-// largest |w| sens.
-template <int DT, bool SQ>
+// largest |w| sens.  With PRE, `pre` holds the vector path's first chunk, already loaded by the caller.
+template <int DT, bool SQ, bool PRE = false>
 __device__ __forceinline__ void rows_dot(const uint16_t* const (&w)[RPW], const float* v, int64_t n, int lane,
                                          bool vec, const float* sens, float (&acc)[RPW], float (&sq)[RPW],
-                                         float (&mx)[RPW]) {
+                                         float (&mx)[RPW], const RowChunk& pre = RowChunk{}) {
 #pragma unroll
   for (int r = 0; r < RPW; ++r) acc[r] = sq[r] = mx[r] = 0.f;
   if (vec) {
-    for (int64_t c = lane * 8; c < n; c += 64 * 8) {
-      float vv[8], ss[8];
+    for (int64_t cb = 0; cb < n; cb += 512 * NCH) {
+      RowChunk qc;
+      if (PRE && cb == 0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        vv[e] = v[c + e];
-        if constexpr (SQ) ss[e] = sens[c + e];
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+          for (int u = 0; u < NCH; ++u) qc[r][u] = pre[r][u];
+      } else {
+        rows_load(w, n, lane, cb, qc);
       }
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) {
-        if (!w[r]) continue;
-        const uint4 q = *reinterpret_cast<const uint4*>(w[r] + c);
-        const uint32_t ws[4] = {q.x, q.y, q.z, q.w};
+      for (int u = 0; u < NCH; ++u) {
+        const int64_t c = cb + lane * 8 + 512 * u;
+        if (c >= n) break;
+        float vv[8], ss[8];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float w0 = lo_of<DT>(ws[e]), w1 = hi_of<DT>(ws[e]);
-          const float p0 = w0 * vv[2 * e], p1 = w1 * vv[2 * e + 1];
-          acc[r] += p0;
-          acc[r] += p1;
-          if constexpr (SQ) {
-            sq[r] += p0 * p0;
-            sq[r] += p1 * p1;
-            mx[r] = fmaxf(mx[r], fmaxf(fabsf(w0) * ss[2 * e], fabsf(w1) * ss[2 * e + 1]));
+        for (int e = 0; e < 8; ++e) {
+          vv[e] = v[c + e];
+          if constexpr (SQ) ss[e] = sens[c + e];
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+          if (!w[r]) continue;
+          const uint4 q = qc[r][u];
+          const uint32_t ws[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float w0 = lo_of<DT>(ws[e]), w1 = hi_of<DT>(ws[e]);
+            const float p0 = w0 * vv[2 * e], p1 = w1 * vv[2 * e + 1];
+            acc[r] += p0;
+            acc[r] += p1;
+            if constexpr (SQ) {
+              sq[r] += p0 * p0;
+              sq[r] += p1 * p1;
+              mx[r] = fmaxf(mx[r], fmaxf(fabsf(w0) * ss[2 * e], fabsf(w1) * ss[2 * e + 1]));
+            }
           }
         }
       }
@@ -205,10 +235,7 @@ __global__ __launch_bounds__(256) void moe_up_kernel(MoeArgs a) {
   const int jk = blockIdx.x, j = jk / (int)a.K, k = jk % (int)a.K;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t row = sample_row(l, j, a.nl), e = expert(a, row, k);
-  for (int64_t h = t; h < a.H; h += 256) xs[h] = ld<DT>(a.x, row * a.sx + h);
-  __syncthreads();
   const int64_t n2 = 2 * a.I;
-  const float g = gweight(a, row * a.K + k);
   const bool vec = (a.H % 8 == 0) && (a.s13n % 8 == 0) && (a.s13e % 8 == 0) && (((uintptr_t)a.w13 & 15) == 0);
   const int64_t n0 = ((int64_t)blockIdx.y * WPB + w) * RPW;
   const uint16_t* wr[RPW];
@@ -216,8 +243,14 @@ __global__ __launch_bounds__(256) void moe_up_kernel(MoeArgs a) {
   for (int r = 0; r < RPW; ++r)
     wr[r] = (e >= 0 && n0 + r < n2) ? reinterpret_cast<const uint16_t*>(a.w13) + e * a.s13e + (n0 + r) * a.s13n
                                     : nullptr;
+  // the rows' first chunk goes out before the sampled row is staged in LDS: both arrive in one round trip
+  RowChunk pre = {};
+  if (vec) rows_load(wr, a.H, lane, 0, pre);
+  for (int64_t h = t; h < a.H; h += 256) xs[h] = ld<DT>(a.x, row * a.sx + h);
+  __syncthreads();
+  const float g = gweight(a, row * a.K + k);
   float acc[RPW], sq[RPW], mx[RPW];
-  rows_dot<DT, false>(wr, xs, a.H, lane, vec, nullptr, acc, sq, mx);
+  rows_dot<DT, false, true>(wr, xs, a.H, lane, vec, nullptr, acc, sq, mx, pre);
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
     if (n0 + r >= n2) break;
