@@ -58,8 +58,8 @@ template <int DT>
 __device__ __forceinline__ float row16_sum(float v) {
   v += dpp_xor1(v);
   v += dpp_xor2(v);
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // half mirror
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));  // row mirror
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, true));   // half mirror
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, true));   // row mirror
   return v;
 }
 
@@ -453,7 +453,11 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
       colw[w][1][lane] = f32x4{u[4], u[5], u[6], u[7]};
     }
     // ---- row direction: four sums of each of the eight rows over this thread's eight columns, each row's added
-    //      over the 16 lanes of its row group at once (lane cg < 8 keeps row 8 rg + cg)
+    //      over the 16 lanes of its row group at once; lane cg < 8 keeps row 8 rg + cg (selected, not stored under
+    //      a branch, so every DPP step folds into its add) and stores it once.  The empty asm pins each row's
+    //      reduction before the select: the DPP steps read other lanes, so they must not be moved under the
+    //      `cg == i` mask (where the lanes they read are off).
+    f32x4 kept = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t ww[4] = {v[tt][i].x, v[tt][i].y, v[tt][i].z, v[tt][i].w};
@@ -465,13 +469,15 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
         sq = dot2<DT>(ww[q], ww[q], sq);
         ab = dot2<DT>(ww[q] & 0x7FFF7FFFu, ONES, ab);
       }
-      f32x4 r;
-      r.x = row16_sum<DT>(pl);
-      r.y = row16_sum<DT>(sg);
-      r.z = row16_sum<DT>(sq);
-      r.w = row16_sum<DT>(ab);
-      if (cg == i) rows[8 * rg + i] = r;
+      float r0 = row16_sum<DT>(pl), r1 = row16_sum<DT>(sg), r2 = row16_sum<DT>(sq), r3 = row16_sum<DT>(ab);
+      asm volatile("" : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3));
+      const bool mine = cg == i;
+      kept.x = mine ? r0 : kept.x;
+      kept.y = mine ? r1 : kept.y;
+      kept.z = mine ? r2 : kept.z;
+      kept.w = mine ? r3 : kept.w;
     }
+    if (cg < 8) rows[8 * rg + cg] = kept;
     __syncthreads();
 
     // ---- scoring
