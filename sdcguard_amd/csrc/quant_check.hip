@@ -444,6 +444,8 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(QuantArgs a) {
       fi += dpp_xor2(fi);
       fi += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(fi), 0x141, 0xF, 0xF, false));
       fi += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(fi), 0x140, 0xF, 0xF, false));
+      // (the sums finish here, with every lane on: their last DPP steps must not move under the store's mask)
+      asm volatile("" : "+v"(pl), "+v"(sg), "+v"(sq), "+v"(fi));
       if (cg == 0) {
         srow[RPT * rg + i][0] = pl;
         srow[RPT * rg + i][1] = sg;
