@@ -44,6 +44,16 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   }
 }
 
+// a . b + 0, the first term of a sum: the three-operand form takes the zero as an inline constant, where the
+// accumulating form (what the compiler picks for dot2(a, b, 0)) needs a register cleared first
+template <int DT>
+__device__ __forceinline__ float dot2_first(uint32_t a, uint32_t b) {
+  float r;
+  if constexpr (DT == SDC_BF16) asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  else asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 template <int DT>
 __device__ __forceinline__ void acc8(u32x4 v, const uint32_t* sg2, float& pl, float& sg, float& sq, float& ab) {
   constexpr uint32_t ONES = DT == SDC_BF16 ? 0x3F803F80u : 0x3C003C00u;

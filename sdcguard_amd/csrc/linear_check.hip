@@ -63,6 +63,20 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// One reduce-scatter step over the lanes of a DPP row: the lane holds NV values (v[0 .. NV)), its partner under
+// the DPP pattern CTRL the same ones; `low` lanes keep the first half, the others the second (moved to the front),
+// each adding the partner's copy of what it keeps (which the partner sends: the half it does not keep).  Every lane
+// active.
+template <int CTRL, int NV>
+__device__ __forceinline__ void row_scatter(float* v, bool low) {
+  constexpr int H = NV / 2;
+#pragma unroll
+  for (int j = 0; j < H; ++j) {
+    const float keep = low ? v[j] : v[H + j], send = low ? v[H + j] : v[j];
+    v[j] = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), CTRL, 0xF, 0xF, true));
+  }
+}
+
 // ---------------------------------------------------------------------------------------- 1. x block sums
 
 // One workgroup: one row block (128 rows) by 128 consecutive depths (32 KB of x).  Thread t = 16 rg + dc reads
@@ -409,9 +423,8 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
     const int c0 = jb * BS;
     const int wc = (int)((jb == a.nb - 1 && a.rem_n > 0) ? a.rem_n : BS);
     // ---- column direction: two rows' values of one column packed into one operand
+    // (the first row pair starts each sum with the three-operand dot2: no cleared accumulators)
     float cs[8][4];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) cs[e][0] = cs[e][1] = cs[e][2] = cs[e][3] = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; i += 2) {
       const uint32_t w0[4] = {v[tt][i].x, v[tt][i].y, v[tt][i].z, v[tt][i].w};
@@ -421,14 +434,23 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
       for (int q = 0; q < 4; ++q) {
         const uint32_t plo = __builtin_amdgcn_perm(w1[q], w0[q], 0x05040100u);     // column 2q of rows i, i + 1
         const uint32_t phi = __builtin_amdgcn_perm(w1[q], w0[q], 0x07060302u);     // column 2q + 1
-        cs[2 * q][0] = dot2<DT>(plo, ONES, cs[2 * q][0]);
-        cs[2 * q][1] = dot2<DT>(plo, sr, cs[2 * q][1]);
-        cs[2 * q][2] = dot2<DT>(plo, plo, cs[2 * q][2]);
-        cs[2 * q][3] = dot2<DT>(plo & 0x7FFF7FFFu, ONES, cs[2 * q][3]);
-        cs[2 * q + 1][0] = dot2<DT>(phi, ONES, cs[2 * q + 1][0]);
-        cs[2 * q + 1][1] = dot2<DT>(phi, sr, cs[2 * q + 1][1]);
-        cs[2 * q + 1][2] = dot2<DT>(phi, phi, cs[2 * q + 1][2]);
-        cs[2 * q + 1][3] = dot2<DT>(phi & 0x7FFF7FFFu, ONES, cs[2 * q + 1][3]);
+        const uint32_t op[2] = {plo, phi};
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const uint32_t pv = op[hh], pa = pv & 0x7FFF7FFFu;
+          float* c = cs[2 * q + hh];
+          if (i == 0) {
+            c[0] = dot2_first<DT>(pv, ONES);
+            c[1] = dot2_first<DT>(pv, sr);
+            c[2] = dot2_first<DT>(pv, pv);
+            c[3] = dot2_first<DT>(pa, ONES);
+          } else {
+            c[0] = dot2<DT>(pv, ONES, c[0]);
+            c[1] = dot2<DT>(pv, sr, c[1]);
+            c[2] = dot2<DT>(pv, pv, c[2]);
+            c[3] = dot2<DT>(pa, ONES, c[3]);
+          }
+        }
       }
     }
     // the four row groups of the wave (lanes cg, cg + 16, cg + 32, cg + 48) add their column sums by lane swaps:
@@ -452,32 +474,32 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
       colw[w][0][lane] = f32x4{u[0], u[1], u[2], u[3]};
       colw[w][1][lane] = f32x4{u[4], u[5], u[6], u[7]};
     }
-    // ---- row direction: four sums of each of the eight rows over this thread's eight columns, each row's added
-    //      over the 16 lanes of its row group at once; lane cg < 8 keeps row 8 rg + cg (selected, not stored under
-    //      a branch, so every DPP step folds into its add) and stores it once.  The empty asm pins each row's
-    //      reduction before the select: the DPP steps read other lanes, so they must not be moved under the
-    //      `cg == i` mask (where the lanes they read are off).
-    f32x4 kept = {0.f, 0.f, 0.f, 0.f};
+    // ---- row direction: four sums of each of the eight rows over this thread's eight columns (32 values a lane,
+    //      value 4 i + kind), added over the 16 lanes of the row group by a reduce-scatter: at each of four DPP
+    //      steps a lane and its partner (lane xor 8, 7, 3, 1: the same values held, one bit of the lane apart) keep
+    //      opposite halves, each adding the partner's copy of its half.  Lane cg ends with values 2 cg, 2 cg + 1:
+    //      row cg / 2, kinds 2 (cg & 1) and 2 (cg & 1) + 1, stored as one pair.
+    float rv[32];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t ww[4] = {v[tt][i].x, v[tt][i].y, v[tt][i].z, v[tt][i].w};
-      float pl = 0.f, sg = 0.f, sq = 0.f, ab = 0.f;
+      float pl = dot2_first<DT>(ww[0], ONES), sg = dot2_first<DT>(ww[0], scol2[tt][0]);
+      float sq = dot2_first<DT>(ww[0], ww[0]), ab = dot2_first<DT>(ww[0] & 0x7FFF7FFFu, ONES);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 1; q < 4; ++q) {
         pl = dot2<DT>(ww[q], ONES, pl);
         sg = dot2<DT>(ww[q], scol2[tt][q], sg);
         sq = dot2<DT>(ww[q], ww[q], sq);
         ab = dot2<DT>(ww[q] & 0x7FFF7FFFu, ONES, ab);
       }
-      float r0 = row16_sum<DT>(pl), r1 = row16_sum<DT>(sg), r2 = row16_sum<DT>(sq), r3 = row16_sum<DT>(ab);
-      asm volatile("" : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3));
-      const bool mine = cg == i;
-      kept.x = mine ? r0 : kept.x;
-      kept.y = mine ? r1 : kept.y;
-      kept.z = mine ? r2 : kept.z;
-      kept.w = mine ? r3 : kept.w;
+      rv[4 * i] = pl; rv[4 * i + 1] = sg; rv[4 * i + 2] = sq; rv[4 * i + 3] = ab;
     }
-    if (cg < 8) rows[8 * rg + cg] = kept;
+    row_scatter<0x128, 32>(rv, (cg & 8) == 0);        // row_ror:8 (lane xor 8)
+    row_scatter<0x141, 16>(rv, (cg & 4) == 0);        // row_half_mirror (lane xor 7)
+    row_scatter<0x1B, 8>(rv, (cg & 2) == 0);          // quad_perm [3, 2, 1, 0] (lane xor 3)
+    row_scatter<0xB1, 4>(rv, (cg & 1) == 0);          // quad_perm [1, 0, 3, 2] (lane xor 1)
+    *reinterpret_cast<float2*>(reinterpret_cast<float*>(&rows[8 * rg + (cg >> 1)]) + 2 * (cg & 1)) =
+        float2{rv[0], rv[1]};
     __syncthreads();
 
     // ---- scoring
