@@ -773,7 +773,8 @@ __global__ __launch_bounds__(64 * RS_WAVES, 1) void rs_gemm_kernel(GemmArgs g) {
 
 constexpr int GSCAN = 1024;                       // groups the grouped tall GEMM takes
 
-template <int DT, int ROLE, int TRF, int AT, bool XNORM, bool GROUPED = false>
+// TCF: 32-column fragments a tile (2; 1 for outputs of at most 32 columns, whose second fragment would be empty)
+template <int DT, int ROLE, int TRF, int AT, bool XNORM, bool GROUPED = false, int TCF = 2>
 __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_kernel(GemmArgs g) {
   constexpr int MDT = AT ? SDC_BF16 : DT;       // the MFMAs' type (AT 2: int8)
   constexpr int SPS = AT ? 8 : 4;               // steps per segment
@@ -783,7 +784,8 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
   constexpr int NACC = AT == 2 ? 2 : 1;         // accumulator sets (int8: one per digit, exact int32)
   constexpr int FRAG = AT == 2 ? 256 : 512;     // 16-bit units per B fragment (int8: 8 bytes a lane)
   static_assert(AT != 2 || (TRF == 2 && !XNORM && !GROUPED), "int8: 64-row tiles, no row norms");
-  constexpr int TCF = 2, TR = 32 * TRF, TC = 64, RB = 4, NAI = TR / 8, APS = NAI / SPS;
+  static_assert(TCF == 1 || TCF == 2, "one or two column fragments a tile");
+  constexpr int TR = 32 * TRF, TC = 32 * TCF, RB = 4, NAI = TR / 8, APS = NAI / SPS;
   constexpr int RT_SEGB = TR * 128;             // bytes of A per wave and segment (TR rows x 128 bytes)
   constexpr int RED_BYTES = RS_WAVES * TC * (TR + 4) * 4;       // the epilogue's reduction (below)
   __shared__ __attribute__((aligned(16)))
@@ -915,23 +917,35 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
   // names a slot's registers (so the loads into them count as used)
 #define SDC_TALL_WAIT_B(C, slot)                                                                                   \
   do {                                                                                                            \
-    if constexpr (NP == 3)                                                                                        \
+    if constexpr (NP == 3 && TCF == 2)                                                                            \
       asm volatile("s_waitcnt vmcnt(%6)"                                                                          \
-                   : "+v"(rb[slot][0][0]), "+v"(rb[slot][0][1]), "+v"(rb[slot][1][0]), "+v"(rb[slot][1][1]),      \
-                     "+v"(rb[slot][2 % NP][0]), "+v"(rb[slot][2 % NP][1])                                         \
+                   : "+v"(rb[slot][0][0]), "+v"(rb[slot][0][TCF - 1]), "+v"(rb[slot][1][0]),                      \
+                     "+v"(rb[slot][1][TCF - 1]), "+v"(rb[slot][NP - 1][0]), "+v"(rb[slot][NP - 1][TCF - 1])       \
+                   : "n"(C));                                                                                     \
+    else if constexpr (TCF == 2)                                                                                  \
+      asm volatile("s_waitcnt vmcnt(%4)"                                                                          \
+                   : "+v"(rb[slot][0][0]), "+v"(rb[slot][0][TCF - 1]), "+v"(rb[slot][NP - 1][0]),                 \
+                     "+v"(rb[slot][NP - 1][TCF - 1])                                                              \
+                   : "n"(C));                                                                                     \
+    else if constexpr (NP == 3)                                                                                   \
+      asm volatile("s_waitcnt vmcnt(%3)"                                                                          \
+                   : "+v"(rb[slot][0][0]), "+v"(rb[slot][1][0]), "+v"(rb[slot][NP - 1][0])                        \
                    : "n"(C));                                                                                     \
     else                                                                                                          \
-      asm volatile("s_waitcnt vmcnt(%4)"                                                                          \
-                   : "+v"(rb[slot][0][0]), "+v"(rb[slot][0][1]), "+v"(rb[slot][1][0]), "+v"(rb[slot][1][1])       \
-                   : "n"(C));                                                                                     \
+      asm volatile("s_waitcnt vmcnt(%2)" : "+v"(rb[slot][0][0]), "+v"(rb[slot][NP - 1][0]) : "n"(C));             \
   } while (0)
 #define SDC_TALL_NAME_B(slot)                                                                                      \
   do {                                                                                                            \
-    if constexpr (NP == 3)                                                                                        \
-      asm volatile("" : "+v"(rb[slot][0][0]), "+v"(rb[slot][0][1]), "+v"(rb[slot][1][0]), "+v"(rb[slot][1][1]),   \
-                   "+v"(rb[slot][2 % NP][0]), "+v"(rb[slot][2 % NP][1]));                                          \
+    if constexpr (NP == 3 && TCF == 2)                                                                            \
+      asm volatile("" : "+v"(rb[slot][0][0]), "+v"(rb[slot][0][TCF - 1]), "+v"(rb[slot][1][0]),                   \
+                   "+v"(rb[slot][1][TCF - 1]), "+v"(rb[slot][NP - 1][0]), "+v"(rb[slot][NP - 1][TCF - 1]));        \
+    else if constexpr (TCF == 2)                                                                                  \
+      asm volatile("" : "+v"(rb[slot][0][0]), "+v"(rb[slot][0][TCF - 1]), "+v"(rb[slot][NP - 1][0]),              \
+                   "+v"(rb[slot][NP - 1][TCF - 1]));                                                              \
+    else if constexpr (NP == 3)                                                                                   \
+      asm volatile("" : "+v"(rb[slot][0][0]), "+v"(rb[slot][1][0]), "+v"(rb[slot][NP - 1][0]));                   \
     else                                                                                                          \
-      asm volatile("" : "+v"(rb[slot][0][0]), "+v"(rb[slot][0][1]), "+v"(rb[slot][1][0]), "+v"(rb[slot][1][1]));  \
+      asm volatile("" : "+v"(rb[slot][0][0]), "+v"(rb[slot][NP - 1][0]));                                         \
   } while (0)
   auto read_frag1 = [&](uint32_t L, int jj, FragT* fr, int i) {
     if constexpr (AT) asm volatile("ds_read_b64 %0, %1" : "=v"(fr[i]) : "v"(L + (uint32_t)ard[i][jj]));
@@ -1023,8 +1037,9 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
               if (p == 1 && n == 0 && jj < SPS - 1) read_frag1(L, jj + 1, fr[cur ^ 1], i);
 #pragma unroll
               for (int c = 0; c < TCF; ++c) {                     // column c's B load: after its last reader (and
-                const int qc = c * TRF + TRF - 1;                 // in part 0 after the A pieces)
-                if (q == (p == 0 && qc < APS ? APS : qc)) issue_b1(sl, st + RB, p, c);
+                const int qc = c * TRF + TRF - 1;                 // in part 0 after the A pieces, at the part's
+                const int qs = p == 0 && qc < APS ? APS : qc;     // last MFMA at the latest)
+                if (q == (qs < TRF * TCF ? qs : TRF * TCF - 1)) issue_b1(sl, st + RB, p, c);
               }
               __builtin_amdgcn_sched_barrier(0);
             }
@@ -1106,7 +1121,8 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
                     acc[pa][i][n][4 * r4 + 3]};
     __syncthreads();
     float* const Eh = g.E + (half * NACC + pa) * N * me;
-    if (!g.et) {
+    if constexpr (TCF == 2) {                                   // (row-major planes: 64-column tiles only;
+    if (!g.et) {                                                //  the launcher asks transposed ones otherwise)
       // a row-major plane ([m][N]): each store instruction writes 4 rows x 64 columns, lane l row 4 gq + l / 16
       // of the wave's quarter of the tile's rows, columns 4 (l % 16) .. + 3 (the four waves' partials added in
       // wave order, as below)
@@ -1139,6 +1155,7 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
         }
       }
       continue;
+    }
     }
 #pragma unroll
     for (int gq = 0; gq < TC / (RS_WAVES * CPI); ++gq) {
@@ -1254,14 +1271,20 @@ int sdc_rs_gemm_tall_launch(int dtype, GemmArgs g, int role, hipStream_t stream)
   if (dtype == SDC_I8) g.short_rows = 1;                        // (int8: 64-row tiles only)
   const int64_t rtiles = sdc_cdiv(g.m, g.short_rows ? 64 : 32 * SDC_TALL_TRF) + (g.goffs ? g.ngroups : 0);
   if (g.xf_blocks < 0 || (g.xf_blocks && (g.goffs || dtype == SDC_FP8))) return SDC_EINVAL;
-  const int64_t blocks = g.splits * rtiles * sdc_cdiv(g.N, 64) + g.xf_blocks;
+  // (grouped outputs of at most 32 columns: one-fragment tiles, whose grid counts 32-column tiles)
+  const bool narrow = g.goffs && g.N <= 32;
+  const int64_t blocks = g.splits * rtiles * sdc_cdiv(g.N, narrow ? 32 : 64) + g.xf_blocks;
   if (blocks > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
   SdcProf prof(g.prof_name ? g.prof_name : "expected_gemm", stream);
   const dim3 grid((unsigned)blocks), block(64 * RS_WAVES);
   constexpr int T = SDC_TALL_TRF;
   if (g.goffs) {
     // (grouped: 16-bit A with its row norms)
-    if (dtype == SDC_BF16)
+    if (narrow && dtype == SDC_BF16)
+      hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 4, T, 0, true, true, 1>), grid, block, 0, stream, g);
+    else if (narrow)
+      hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_FP16, 4, T, 0, true, true, 1>), grid, block, 0, stream, g);
+    else if (dtype == SDC_BF16)
       hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_BF16, 4, T, 0, true, true>), grid, block, 0, stream, g);
     else
       hipLaunchKernelGGL((rs_gemm_tall_kernel<SDC_FP16, 4, T, 0, true, true>), grid, block, 0, stream, g);
