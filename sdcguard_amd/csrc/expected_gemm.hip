@@ -815,8 +815,23 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
       gtile[q] = e > s0 ? sdc_cdiv(e - s0, TR) : 0;
     }
     __syncthreads();
-    if (t == 0)
-      for (int q = 1; q < ng; ++q) gtile[q] += gtile[q - 1];    // (inclusive running count, 1024 groups at most)
+    if (w == 0) {
+      // the inclusive running count (1024 groups at most), 64 groups at a time: a shuffle scan across the wave,
+      // plus the running total of the chunks before
+      int64_t carry = 0;
+      for (int q0 = 0; q0 < ng; q0 += 64) {
+        const int q = q0 + lane;
+        int64_t c = q < ng ? gtile[q] : 0;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const int64_t u = __shfl_up(c, d, 64);
+          c += lane >= d ? u : 0;
+        }
+        c += carry;
+        if (q < ng) gtile[q] = c;
+        carry = __shfl(c, 63, 64);
+      }
+    }
     __syncthreads();
     const int64_t rtiles = sdc_cdiv(m, TR) + g.ngroups;
     tiles = rtiles * nct;
