@@ -795,14 +795,17 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int r = lane & 31, h = lane >> 5;
   const int64_t N = g.N, m = g.m;
-  const int64_t nct = sdc_cdiv(N, TC), ncf = sdc_cdiv(N, 32);
-  const int64_t G = (int64_t)gridDim.x - g.xf_blocks, b = blockIdx.x;
+  // (tile indices in 32 bits, their divisions by run-time divisors the short unsigned ones: the launcher keeps the
+  // grid, and so every tile count, below 2^31)
+  const uint32_t nct = ((uint32_t)N + TC - 1) / TC, ncf = ((uint32_t)N + 31) / 32;
+  const uint32_t G = gridDim.x - (uint32_t)g.xf_blocks, b = blockIdx.x;
   if (b >= G) {
-    xfinish_block(g.xf, b - G, t);                // (a spare workgroup: the x pass's finishing step)
+    xfinish_block(g.xf, (int64_t)(b - G), t);     // (a spare workgroup: the x pass's finishing step)
     return;
   }
-  const int64_t wid = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
-  int64_t tiles, half, r0, rend, grp = 0;
+  const uint32_t wid = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+  uint32_t tile, half;
+  int64_t r0, rend, grp = 0;
   if constexpr (GROUPED) {
     // grouped rows (g.goffs: the groups' cumulative ends): a row tile never crosses a group, so group q has
     // ceil(rows_q / TR) row tiles; their running count comes from the ends in LDS (a scan over the groups), and
@@ -833,11 +836,11 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
       }
     }
     __syncthreads();
-    const int64_t rtiles = sdc_cdiv(m, TR) + g.ngroups;
-    tiles = rtiles * nct;
+    const uint32_t tiles = ((uint32_t)((m + TR - 1) / TR) + (uint32_t)ng) * nct;
     half = wid / tiles;
-    const int64_t tile = wid % tiles, rt = tile / nct;
-    if (rt >= gtile[ng - 1] || half >= g.splits) return;
+    tile = wid - half * tiles;
+    const int64_t rt = tile / nct;
+    if (rt >= gtile[ng - 1] || (int64_t)half >= g.splits) return;
     int lo = 0, hi = ng - 1;                                     // first group whose running count exceeds rt
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
@@ -848,19 +851,17 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
     const int64_t gs = grp ? gend[grp - 1] : 0, lt = rt - (grp ? gtile[grp - 1] : 0);
     r0 = gs + lt * TR;
     rend = gend[grp];
-    tiles = tile;                                                // (reused below as this tile's index)
   } else {
-    tiles = sdc_cdiv(m, TR) * nct;
+    const uint32_t tiles = (uint32_t)((m + TR - 1) / TR) * nct;
     half = wid / tiles;
-    const int64_t rt = (wid % tiles) / nct;
-    r0 = rt * TR;
+    tile = wid - half * tiles;
+    r0 = (int64_t)(tile / nct) * TR;
     rend = m;
-    tiles = wid % tiles;
   }
-  const int64_t ct = tiles % nct;
-  const int64_t c0 = ct * TC;
+  const uint32_t ct = tile % nct;
+  const int64_t c0 = (int64_t)ct * TC;
   const bool do_xn = XNORM && ct == 0;
-  const int per = (int)(g.k / SD) / (RS_WAVES * (int)g.splits);   // segments per wave
+  const int per = (int)((uint32_t)(g.k / SD) / (uint32_t)(RS_WAVES * g.splits));   // segments per wave
   const int seg0 = (int)half * per * RS_WAVES + w * per;
   uint8_t* const abuf = smem + w * 2 * RT_SEGB;
   // LDS address of fragment i (rows 32 i + r) at step jj of a segment: the 16-bit depth piece 4 h + jj, or the
@@ -879,14 +880,14 @@ __global__ __launch_bounds__(64 * RS_WAVES, TRF == 4 ? 1 : 2) void rs_gemm_tall_
       }
     }
   const uint16_t* bq =
-      (const uint16_t*)g.B + grp * g.sbb + (int64_t)(SPS * seg0) * NP * ncf * FRAG + (FRAG / 64) * lane;
+      (const uint16_t*)g.B + grp * g.sbb + (int64_t)(SPS * seg0) * NP * (int64_t)ncf * FRAG + (FRAG / 64) * lane;
   int bf[TCF];
 #pragma unroll
   for (int n = 0; n < TCF; ++n) {
-    const int64_t f = c0 / 32 + n;
+    const uint32_t f = (uint32_t)(c0 / 32) + n;
     bf[n] = (int)((f < ncf ? f : ncf - 1) * FRAG);
   }
-  const int64_t bstep = NP * ncf * FRAG;
+  const int64_t bstep = NP * (int64_t)ncf * FRAG;
   const int lastseg = per - 1;
   const int last = SPS * per - 1;
   // A's instruction I (0 .. 15) of a segment, lane L: row 8 I + L / 8 (clamped to m - 1), 16-byte piece
@@ -1252,6 +1253,7 @@ int sdc_rs_gemm_launch(int dtype, GemmArgs g, int role, hipStream_t stream) {
       !g.et || g.goffs)
     return SDC_EUNSUPPORTED;
   if (g.m < 1 || g.N < 1) return SDC_EINVAL;
+  if (g.N > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
   const int64_t tiles = sdc_cdiv(g.m, 64) * sdc_cdiv(g.N, 64);
   if (tiles > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
   SdcProf prof(g.prof_name ? g.prof_name : "expected_gemm", stream);
