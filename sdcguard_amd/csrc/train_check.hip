@@ -848,7 +848,10 @@ int check_with(int dtype, const void* A, int64_t sab, int64_t sam, int64_t sak, 
     const int64_t tiles = sdc_cdiv(ta.cv.npairs, 64);
     if (sdc_cdiv(tiles, 4) > 0x7FFFFFFF) return SDC_EUNSUPPORTED;
     const unsigned grid = (unsigned)sdc_cdiv(tiles, 4);                // one tile per wave
-    if (ta.splits <= 4) {
+    if (ta.splits <= 2) {                                              // (the tall grouped GEMM's two planes)
+      if (dtype == SDC_BF16) hipLaunchKernelGGL((grouped_score_kernel<SDC_BF16, 2>), dim3(grid), dim3(256), 0, stream, ta);
+      else hipLaunchKernelGGL((grouped_score_kernel<SDC_FP16, 2>), dim3(grid), dim3(256), 0, stream, ta);
+    } else if (ta.splits <= 4) {
       if (dtype == SDC_BF16) hipLaunchKernelGGL((grouped_score_kernel<SDC_BF16, 4>), dim3(grid), dim3(256), 0, stream, ta);
       else hipLaunchKernelGGL((grouped_score_kernel<SDC_FP16, 4>), dim3(grid), dim3(256), 0, stream, ta);
     } else {
