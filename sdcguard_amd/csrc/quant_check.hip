@@ -256,6 +256,15 @@ __device__ __forceinline__ float sum16(float v) {
   return v;
 }
 
+// int32 sum over the 16 lanes of a DPP row (every lane holding it)
+__device__ __forceinline__ int sum16_i32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true);    // xor 1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, true);    // xor 2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, true);   // half mirror
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, true);   // row mirror
+  return v;
+}
+
 __device__ __forceinline__ int64_t sum16_i64(int64_t v) {
 #pragma unroll
   for (int msk = 1; msk < 16; msk <<= 1) v += shfl_xor_i64(v, msk);
@@ -380,25 +389,38 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(QuantArgs a) {
   }
   __syncthreads();
   if constexpr (KIND == 0) {
+    // Exact sums of 128 int32 values without 64-bit lane traffic: each value split as x = hi 2^16 + lo (lo in
+    // [0, 2^16), hi signed), the halves summed in int32 (|sum| < 2^23 over a block) and over the 16 lanes by DPP
+    // adds, then put back together in int64
+    int sgi[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sgi[e] = sgn[e] > 0.f ? 1 : (sgn[e] < 0.f ? -1 : 0);
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
-      int64_t pl = 0, sg = 0;
+      int pl_lo = 0, pl_hi = 0, sg_lo = 0, sg_hi = 0;
       if (on) {
 #pragma unroll
         for (int l = 0; l < NL; ++l)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const int e = 4 * l + q;
-            const int64_t x = (int64_t)(int32_t)v[i][l][q];
-            pl += x;
-            sg += sgn[e] > 0.f ? x : (sgn[e] < 0.f ? -x : 0);
+            const int x = (int)v[i][l][q];
+            const int lo = x & 0xFFFF, hi = x >> 16;
+            pl_lo += lo;
+            pl_hi += hi;
+            sg_lo += sgi[e] * lo;
+            sg_hi += sgi[e] * hi;
           }
       }
-      pl = sum16_i64(pl);
-      sg = sum16_i64(sg);
+      pl_lo = sum16_i32(pl_lo);
+      pl_hi = sum16_i32(pl_hi);
+      sg_lo = sum16_i32(sg_lo);
+      sg_hi = sum16_i32(sg_hi);
+      // (the sums finish here, with every lane on: their DPP steps must not move under the store's mask)
+      asm volatile("" : "+v"(pl_lo), "+v"(pl_hi), "+v"(sg_lo), "+v"(sg_hi));
       if (cg == 0) {
-        irow[RPT * rg + i][0] = pl;
-        irow[RPT * rg + i][1] = sg;
+        irow[RPT * rg + i][0] = (int64_t)pl_hi * 65536 + pl_lo;
+        irow[RPT * rg + i][1] = (int64_t)sg_hi * 65536 + sg_lo;
       }
     }
   } else {
