@@ -580,8 +580,9 @@ __global__ __launch_bounds__(256) void ypass_kernel(YArgs a) {
       }
     }
   }
-  const int64_t key = wave_max_i64(best.key), keyd = wave_max_i64(best.keyd);
-  const int unk = wave_sum_i32(best.unk);
+  // (every lane of the wave active here: the reductions by DPP moves, no LDS round trips)
+  const int64_t key = wave_max_i64_dpp(best.key), keyd = wave_max_i64_dpp(best.keyd);
+  const int unk = wave_sum_i32_dpp(best.unk);
   if (lane == 0) {
     red_k[w] = key;
     red_d[w] = keyd;

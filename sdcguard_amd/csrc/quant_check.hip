@@ -509,9 +509,9 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(QuantArgs a) {
       best.keyd = (zb << 32) | (int64_t)__float_as_uint((float)noise);
     }
   }
-  if (scorer) {
-    const int64_t key = wave_max_i64(best.key), keyd = wave_max_i64(best.keyd);
-    const int wr = wave_sum_i32(best.wrong), nf = wave_sum_i32(best.nonfin);
+  if (scorer) {                                              // (a whole wave: the reductions by DPP moves)
+    const int64_t key = wave_max_i64_dpp(best.key), keyd = wave_max_i64_dpp(best.keyd);
+    const int wr = wave_sum_i32_dpp(best.wrong), nf = wave_sum_i32_dpp(best.nonfin);
     if (lane == 0) {
       int64_t* res = a.result;
       if (key > seen0) atomicMax((unsigned long long*)res, (unsigned long long)key);
