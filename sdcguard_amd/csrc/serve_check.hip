@@ -136,9 +136,9 @@ __device__ __forceinline__ void report_wg(const ScoreArgs& a, LaneBest best) {
   __shared__ int red_u[4];
   __shared__ int64_t cap_slot;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  int64_t key = wave_max_i64(best.key);
-  int64_t keyd = wave_max_i64(best.keyd);
-  int unk = wave_sum_i32(best.unk);
+  int64_t key = wave_max_i64_dpp(best.key);        // (every lane of the wave calls this: DPP reductions)
+  int64_t keyd = wave_max_i64_dpp(best.keyd);
+  int unk = wave_sum_i32_dpp(best.unk);
   if (lane == 0) { red_k[w] = key; red_d[w] = keyd; red_u[w] = unk; }
   __syncthreads();
   int64_t* st = a.state;

@@ -441,8 +441,8 @@ __global__ __launch_bounds__(256) void train_score_kernel(TrainArgs a) {
     pair_sums<DT>(a.cv, base, lane, sg2, pl, sg, sq, ab);
     train_pair<DT>(a, base + q * 16 + (lane >> 2), pl, sg, sq, ab, best);
   }
-  int64_t key = wave_max_i64(best.key), keyd = wave_max_i64(best.keyd);
-  int unk = wave_sum_i32(best.unk);
+  int64_t key = wave_max_i64_dpp(best.key), keyd = wave_max_i64_dpp(best.keyd);   // (every lane active)
+  int unk = wave_sum_i32_dpp(best.unk);
   if (lane == 0) { red_k[w] = key; red_d[w] = keyd; red_u[w] = unk; }
   __syncthreads();
   if (t == 0) {
@@ -533,8 +533,8 @@ __global__ __launch_bounds__(256) void train_score_t_kernel(TrainArgs a) {
       train_pair<DT>(a, (bc * m + r) * a.cv.nb + jb, s4[0], s4[1], s4[2], s4[3], best);
     }
   }
-  int64_t key = wave_max_i64(best.key), keyd = wave_max_i64(best.keyd);
-  int unk = wave_sum_i32(best.unk);
+  int64_t key = wave_max_i64_dpp(best.key), keyd = wave_max_i64_dpp(best.keyd);   // (every lane active)
+  int unk = wave_sum_i32_dpp(best.unk);
   if (lane == 0) { red_k[w] = key; red_d[w] = keyd; red_u[w] = unk; }
   __syncthreads();
   if (t == 0) {
@@ -632,8 +632,9 @@ __global__ __launch_bounds__(256) void grouped_score_kernel(TrainArgs a) {
   };
   if (g0 == g1) {
     if (g0 >= 0) {
-      const int64_t key = wave_max_i64(tb.key), keyd = wave_max_i64(tb.keyd);
-      const int unk = wave_sum_i32(tb.unk);
+      // (g0 and g1 are the wave's: the whole wave is here, so the reductions can use DPP moves)
+      const int64_t key = wave_max_i64_dpp(tb.key), keyd = wave_max_i64_dpp(tb.keyd);
+      const int unk = wave_sum_i32_dpp(tb.unk);
       if (lane == 0) {
         TrainBest w1;
         w1.key = key; w1.keyd = keyd; w1.unk = unk;
