@@ -196,8 +196,7 @@ __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
   // max |x|: the larger half, as a float (NaN's bits are above infinity's: read as infinity)
   uint32_t mb16 = (mxb & 0xFFFFu) > (mxb >> 16) ? (mxb & 0xFFFFu) : (mxb >> 16);
   float mx = mb16 > 0x7F80u ? __builtin_inff() : __uint_as_float(mb16 << 16);
-#pragma unroll
-  for (int msk = 1; msk < 64; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+  mx = wave_max_f32_dpp(mx);                      // (every lane active: DPP moves, no LDS round trips)
   __syncthreads();
   float st[4] = {0.f, 0.f, 0.f, 0.f};
   if (t < XK) {
@@ -243,13 +242,10 @@ __global__ __launch_bounds__(256) void xstage_kernel(XStageArgs a) {
     st[2] = mine ? nan_abs(P) : 0.f;
     st[3] = mine ? nan_abs(S) : 0.f;
   }
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int msk = 1; msk < 64; msk <<= 1) {
-      const float o = __shfl_xor(st[i], msk, 64);
-      st[i] = i < 2 ? st[i] + o : fmaxf(st[i], o);
-    }
+  st[0] = wave_sum_f32_dpp(st[0]);
+  st[1] = wave_sum_f32_dpp(st[1]);
+  st[2] = wave_max_f32_dpp(st[2]);
+  st[3] = wave_max_f32_dpp(st[3]);
   if (lane == 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) wst[w][i] = st[i];
