@@ -225,6 +225,32 @@ def test_int8_known_answer_at_the_largest_values():
     assert res["wrong_blocks"] == 1 and (res["row"], res["block"]) == (5, 1)
 
 
+def test_int8_extreme_outputs_match_oracle():
+    """The tile pass adds each int32 output as its two 16-bit halves: outputs at both ends of int32 (INT32_MIN,
+    INT32_MAX, -1 in single outputs, and a block whose 128 outputs are all INT32_MAX) give exactly the oracle's
+    per-block verdicts, which flag those blocks and no other."""
+    from sdcguard_amd import modes
+    m, k, n = 128, 1024, 512
+    g = torch.Generator(device="cuda").manual_seed(31)
+    A = torch.randint(-127, 128, (m, k), device="cuda", generator=g, dtype=torch.int32).to(torch.int8)
+    B = torch.randint(-127, 128, (k, n), device="cuda", generator=g, dtype=torch.int32).to(torch.int8)
+    C = (A.double() @ B.double()).to(torch.int32)
+    j9 = 256 + int((C[9, 256:384] != -1).nonzero()[0])            # (an output of block 2 whose value is not -1)
+    C[3, 5] = -2 ** 31
+    C[7, 130] = 2 ** 31 - 1
+    C[9, j9] = -1
+    C[20, 384:512] = 2 ** 31 - 1
+    consts = modes.QuantChecksums.make(B)
+    zs = torch.full((m, n // 128), -7.0, device="cuda")
+    res = modes.resolve(modes.quant_zscores(A, consts, C, scores_out=zs))
+    o = quant.int8_judge(A.cpu().numpy().astype(np.int64), B.cpu().numpy().astype(np.int64),
+                         C.cpu().numpy().astype(np.int64), quant.patterns(1))
+    assert res["wrong_blocks"] == o["wrong_blocks"] == 4, (res, o["wrong_blocks"])
+    flagged = (zs > 6).cpu().numpy()
+    assert np.array_equal(flagged, o["bad"]), np.argwhere(flagged != o["bad"])
+    assert {tuple(x) for x in np.argwhere(flagged)} == {(3, 0), (7, 1), (9, 2), (20, 3)}
+
+
 def test_int8_2048x7168x4096_accumulator_bit_flips():
     """The quantized config at full size: A, B uniform on [-127, 127], C the exact int32 product; clean is exact;
     a flip of any one bit (0-30) of one int32 accumulator is exactly one wrong block, located; 8 trials."""
